@@ -1,0 +1,166 @@
+"""Benchmark of the hip_native hot path on one MI355X.
+
+Workload: one ResNet18(output_dim=2) training step with Adam through the
+Variable/Graph API, every convolution, the stem max-pool and the fc Linear on libmfhip; batch 64,
+input 3x120x160 ~ N(0, 1), targets ~ U(-1, 1), MSE loss, Kaiming weights from seed 0 (synthetic
+data, random-init weights of the reference architecture). ``value`` is images per second over the
+timed steps.
+
+``roofline`` is the FP32 MFMA GEMM engine on the 4096^3 GEMM of BASELINE config 2 (the metric's
+"GEMM TFLOP/s vs FP32 peak"): algorithmic 2*M*N*K flop per launch divided by the average launch
+time measured with HIP events on the launch stream, against the 157.3 TFLOP/s FP32 matrix peak.
+``cpu_baseline`` is the NumPy restatement of the reference CPU path (oracle/resnet.py) timed on this
+host on a bounded sample: full forward + backward + Adam steps of ResNet18 at batch 2 (config 1).
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+# The CPU baseline uses as many BLAS threads as this process may run on (capped by OMP_NUM_THREADS
+# when the host sets it); fix that before NumPy loads its BLAS.
+_CORES = len(os.sched_getaffinity(0))
+if os.environ.get("OMP_NUM_THREADS", "").isdigit():
+    _CORES = min(_CORES, int(os.environ["OMP_NUM_THREADS"]))
+os.environ.setdefault("OPENBLAS_NUM_THREADS", str(_CORES))
+
+import numpy as np  # noqa: E402
+import torch  # noqa: E402
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+import myflows_amd as mf  # noqa: E402
+from myflows_amd import native  # noqa: E402
+
+FP32_MFMA_PEAK_TFLOPS = 157.3
+HBM_PEAK_GBS = 8000.0
+METRIC = "ResNet18 FP32 train images/s (bs64, 3×120×160); GEMM TFLOP/s vs FP32 peak"
+# Algorithmic work of one bs64 training step: 3x the forward conv + fc MACs minus the skipped stem
+# dX, 4.138 GFLOP per image.
+STEP_GFLOP = 264.85
+
+
+def build_step(batch, height, width, seed=0):
+    model = mf.ResNet18(output_dim=2, initializer=mf.make_initializer(seed=seed), conv_backend="hip_native")
+    rng = np.random.default_rng(seed)
+    x_np = rng.standard_normal((batch, 3, height, width)).astype(np.float32)
+    t_np = rng.uniform(-1, 1, (batch, 2)).astype(np.float32)
+    x = mf.Variable(torch.as_tensor(x_np, device="cuda"), requires_grad=False, name="images")
+    t = mf.Variable(torch.as_tensor(t_np, device="cuda"), requires_grad=False, name="targets")
+    loss = mf.MSELoss(model(x), t)
+    graph = mf.Graph(loss)
+    return mf.Adam(graph, learning_rate=1e-3), loss
+
+
+def time_steps(opt, steps, warmup):
+    for _ in range(warmup):
+        opt.one_step()
+        opt.update()
+    torch.cuda.synchronize()
+    start = time.perf_counter()
+    for _ in range(steps):
+        opt.one_step()
+        opt.update()
+    torch.cuda.synchronize()
+    return time.perf_counter() - start
+
+
+def gemm_roofline(m=4096, n=4096, k=4096, reps=20):
+    """Average launch time of the MFMA GEMM on C = A B (A, B ~ N(0, 1) seed 0), from HIP events on
+    the stream the kernels are launched on."""
+    g = torch.Generator().manual_seed(0)
+    a = torch.randn((m, k), generator=g).cuda()
+    b = torch.randn((k, n), generator=g).cuda()
+    out = torch.empty((m, n), device="cuda")
+    stream = torch.cuda.current_stream()
+    for _ in range(3):
+        native.gemm(a, b, out=out)
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    start.record(stream)
+    for _ in range(reps):
+        native.gemm(a, b, out=out)
+    end.record(stream)
+    end.synchronize()
+    ms = start.elapsed_time(end) / reps
+    achieved = 2.0 * m * n * k / (ms * 1e-3) / 1e12
+    tile, slices = native.gemm_plan(m, n, k)
+    return {"bound": "mfma", "achieved": round(achieved, 2), "peak": FP32_MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
+            "frac": round(achieved / FP32_MFMA_PEAK_TFLOPS, 4), "traffic": None,
+            "kernel": f"gemm_mfma_kernel NN {m}x{n}x{k} tile {tile} slices {slices}",
+            "avg_launch_ms": round(ms, 4), "algorithmic_flop_per_launch": 2 * m * n * k}
+
+
+def cpu_baseline(min_seconds=10.0, batch=2):
+    """The NumPy reference-path ResNet18 step (forward + backward + Adam) on this host."""
+    from oracle import resnet as oracle_resnet
+
+    params, running = oracle_resnet.init_params(seed=0)
+    x, target = oracle_resnet.synthetic_batch(batch, seed=0)
+    state = {}
+    _, grads, _ = oracle_resnet.forward_backward(params, running, x, target)  # warm-up
+    oracle_resnet.adam_step(params, grads, state, 1)
+    steps, start = 0, time.perf_counter()
+    while True:
+        _, grads, _ = oracle_resnet.forward_backward(params, running, x, target)
+        oracle_resnet.adam_step(params, grads, state, steps + 2)
+        steps += 1
+        elapsed = time.perf_counter() - start
+        if elapsed >= min_seconds and steps >= 2:
+            break
+    blas = "unknown"
+    try:
+        info = np.show_config(mode="dicts")
+        blas = info.get("Build Dependencies", {}).get("blas", {}).get("name", "unknown")
+    except Exception:  # noqa: BLE001 - only a label
+        pass
+    return {"value": round(batch * steps / elapsed, 3), "unit": "images/s", "cores": _CORES, "kind": "port",
+            "sample": f"{steps} ResNet18 train steps (fwd+bwd+Adam) at batch {batch}, 3x120x160, NumPy "
+                      f"{np.__version__} ({blas}, {_CORES} threads), {elapsed:.1f} s"}
+
+
+def main():
+    parser = argparse.ArgumentParser()
+    parser.add_argument("--gpus", type=int, default=1)
+    parser.add_argument("--steps", type=int, default=20)
+    parser.add_argument("--warmup", type=int, default=3)
+    parser.add_argument("--batch", type=int, default=64)
+    parser.add_argument("--no-cpu-baseline", action="store_true")
+    args = parser.parse_args()
+    if args.gpus != 1:
+        print("bench.py measures one GPU: this build runs no multi-GPU path (use --gpus 1)", file=sys.stderr)
+        return 2
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU", file=sys.stderr)
+        return 2
+    torch.cuda.set_device(0)
+    native._library()
+    opt, _ = build_step(args.batch, 120, 160)
+    seconds = time_steps(opt, args.steps, args.warmup)
+    ms_per_step = seconds * 1e3 / args.steps
+    images_per_s = args.batch * args.steps / seconds
+    roofline = gemm_roofline()
+    result = {
+        "metric": METRIC, "value": round(images_per_s, 2), "unit": "images/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(ms_per_step, 3), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "f32", "data": "synthetic",
+        "config": {"workload": "ResNet18(output_dim=2) train step (fwd+bwd+Adam), hip_native backend",
+                   "global_batch": args.batch, "input": [3, 120, 160], "loss": "MSE"},
+        "step_tflops": round(STEP_GFLOP * args.batch / 64 / (ms_per_step * 1e-3) / 1e3, 2),
+        "roofline": roofline,
+    }
+    if not args.no_cpu_baseline:
+        result["cpu_baseline"] = cpu_baseline()
+    print(json.dumps(result), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,128 @@
+/*
+ * libmfhip: the MI355X (gfx950) native library behind MyFlows' convolution / GEMM / max-pool hot
+ * path. It replaces the NVRTC + cuBLAS scheduler of the reference (`ops/cuda_native/native_cublas.cpp`)
+ * behind the same calling conventions:
+ *
+ *   - every device buffer is a `uint64_t` device address owned by the caller (PyTorch here, CuPy in
+ *     the reference); the library never allocates device memory;
+ *   - a null optional pointer means "not requested";
+ *   - dimensions are `int`, the stream is a `uint64_t` hipStream_t handle (0 = null stream);
+ *   - launches are asynchronous on that stream; nothing synchronises unless debug sync is on
+ *     (`mfh_set_debug_sync(1)` or `MFHIP_SYNC=1`);
+ *   - every entry point returns a status: 0 OK, 1 initialisation failed, 2 invalid argument,
+ *     3 HIP runtime error, 5 called on another device than mfh_init's (4 is unused; it was the
+ *     cuBLAS status of the reference). The detail is this thread's `mfh_last_error()`, of the form
+ *     "<file>:<line>: <reason>".
+ *
+ * Kernels index buffers with int32 offsets; entry points reject problems whose buffers exceed
+ * 2^31 - 1 elements.
+ *
+ * GEMM engine codes (`engine` arguments): 1 = the FP32 MFMA engine with its automatic tile and
+ * split-K plan; 16 + tile * 128 + (slices - 1) = an explicit plan (tile index of
+ * mfh_gemm_tile_info, 1..128 K slices). The reference's engine 0 (cuBLAS) does not exist here.
+ */
+#ifndef MFHIP_H
+#define MFHIP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define MFH_API __attribute__((visibility("default")))
+
+/* One-time initialisation on the current HIP device: checks that the device is gfx950, that the
+ * embedded code objects load, reads the CU count and the MFHIP_SYNC flag.
+ * Replaces mf_init(cublas_path, nvrtc_path, cache_dir), ops/cuda_native/native_cublas.cpp:1425-1427
+ * (no library paths and no kernel cache: code objects are compiled ahead of time). */
+MFH_API int mfh_init(void);
+
+/* Replaces mf_last_error, native_cublas.cpp:1413-1415. */
+MFH_API const char* mfh_last_error(void);
+
+/* JSON build/device facts: device_arch, device_name, cu_count, binary, load_ms.
+ * Replaces mf_info, native_cublas.cpp:1417-1419. */
+MFH_API const char* mfh_info(void);
+
+/* Synchronise the stream after every launch so asynchronous faults name their kernel.
+ * Replaces mf_set_debug_sync, native_cublas.cpp:1421-1423. */
+MFH_API void mfh_set_debug_sync(int enabled);
+
+/* cols (N*OH*OW, CI*KH*KW) = im2col(x), zero outside the padded input.
+ * Replaces mf_conv_im2col, native_cublas.cpp:1430-1438. */
+MFH_API int mfh_conv_im2col(uint64_t x, uint64_t cols, int N, int CI, int H, int W, int CO, int KH, int KW, int OH,
+                            int OW, int SH, int SW, int PH, int PW, uint64_t stream);
+
+/* y (N,CO,OH,OW) = act(conv(x, weight) + bias) through cols = im2col(x), rows = cols weight^T
+ * (GEMM engine `engine`), then the NCHW epilogue. activation: 0 none, 1 ReLU, 2 LeakyReLU(alpha > 0).
+ * bias may be 0. workspace (workspace_floats floats, may be 0) enables split-K.
+ * Replaces mf_conv_forward, native_cublas.cpp:1441-1461. */
+MFH_API int mfh_conv_forward(uint64_t x, uint64_t weight, uint64_t bias, uint64_t cols, uint64_t rows, uint64_t y,
+                             int N, int CI, int H, int W, int CO, int KH, int KW, int OH, int OW, int SH, int SW,
+                             int PH, int PW, int activation, float alpha, int engine, uint64_t workspace,
+                             int64_t workspace_floats, uint64_t stream);
+
+/* Backward of mfh_conv_forward. dyT (N*OH*OW, CO) = gate(dy) transposed, with per-block FP64 bias
+ * partials in `partial` (N * grid_x * CO doubles, grid_x in [1, ceil(OH*OW / 64)]); db = in-order
+ * FP64 sum of the partials; dw (CO, CI*KH*KW) = dyT^T cols on dw_engine; grad_cols = dyT weight on
+ * dx_engine; dx = col2im(grad_cols). dx/grad_cols and partial/db are given together or not at all;
+ * dw needs cols and dyT. With dx as the only output the gated NCHW dy is read directly per image.
+ * Replaces mf_conv_backward_plans / mf_conv_backward, native_cublas.cpp:1465-1532. */
+MFH_API int mfh_conv_backward(uint64_t weight, uint64_t dy, uint64_t y, uint64_t cols, uint64_t dyT, uint64_t dw,
+                              uint64_t grad_cols, uint64_t dx, uint64_t partial, uint64_t db, int N, int CI, int H,
+                              int W, int CO, int KH, int KW, int OH, int OW, int SH, int SW, int PH, int PW,
+                              int grid_x, int activation, float alpha, int dw_engine, int dx_engine,
+                              uint64_t workspace, int64_t workspace_floats, uint64_t stream);
+
+/* Max-pool without padding (the caller pads with -inf): y = window max in (kh, kw) order with the
+ * first maximum winning ties and NaN taking over; argmax (int32) = flat index into x.
+ * Replaces mf_pool_forward, native_cublas.cpp:1534-1547. */
+MFH_API int mfh_pool_forward(uint64_t x, uint64_t y, uint64_t argmax, int N, int C, int H, int W, int OH, int OW,
+                             int KH, int KW, int SH, int SW, uint64_t stream);
+
+/* dx[i] = sum of dy over the windows whose argmax is i, in (oh, ow) order.
+ * Replaces mf_pool_backward, native_cublas.cpp:1549-1562. */
+MFH_API int mfh_pool_backward(uint64_t dy, uint64_t argmax, uint64_t dx, int N, int C, int H, int W, int OH, int OW,
+                              int KH, int KW, int SH, int SW, uint64_t stream);
+
+/* C(M,N) = A(M,K) B(K,N) [+ bias(N)], row-major, with a lecture kernel. variant: 0 basic, 1 tiled,
+ * 2 shared, 4 register (3, cuBLAS in the reference, is rejected); tile 16/32 for variants 1-2;
+ * accumulate: 0 fp32, 1 Kahan-grouped, 2 Dot2. variant 4 with accumulate 0 runs the MFMA engine.
+ * Replaces mf_matmul, native_cublas.cpp:1567-1613. */
+MFH_API int mfh_matmul(int variant, int tile, int accumulate, uint64_t a, uint64_t b, uint64_t bias, uint64_t c, int M,
+                       int N, int K, uint64_t stream);
+
+/* Number of GEMM tiles and their geometry: values[0..4] = BM, BN, WM, WN, BK (block tile, wave
+ * tile, LDS stage depth). Replaces mf_gemm_tile_count / mf_gemm_tile_info, native_cublas.cpp:1617-1624
+ * (values[2..3] are the wave tile where the reference reports the thread tile). */
+MFH_API int mfh_gemm_tile_count(void);
+MFH_API int mfh_gemm_tile_info(int index, int* values);
+
+/* Automatic tile and split-K slice count for C(M,N) over K.
+ * Replaces mf_gemm_plan, native_cublas.cpp:1635-1643. */
+MFH_API int mfh_gemm_plan(int M, int N, int K, int* tile, int* slices);
+
+/* Workspace floats the automatic plan uses (0 when it does not split), -1 on error.
+ * Replaces mf_gemm_workspace, native_cublas.cpp:1659-1666. */
+MFH_API int64_t mfh_gemm_workspace(int M, int N, int K);
+
+/* C = (float) FP64 sum of slices x M x N contiguous partials in slice order (the split-K
+ * reduction); `reference` is accepted for interface parity and selects the same kernel.
+ * Replaces mf_split_reduce, native_cublas.cpp:1647-1655. */
+MFH_API int mfh_split_reduce(uint64_t partial, uint64_t c, int slices, int M, int N, int ldc, int reference,
+                             uint64_t stream);
+
+/* C(M,N) = op(A) op(B) [+ bias(N)], row-major with leading dimensions lda/ldb/ldc. op(A) = A^T when
+ * trans_a (A stored K x M), op(B) = B^T when trans_b (B stored N x K); not both. workspace may be
+ * 0; with the plan's slices * M * N floats the engine splits K. bias needs ldc == N.
+ * Replaces mf_gemm, native_cublas.cpp:1672-1692. */
+MFH_API int mfh_gemm(int engine, int trans_a, int trans_b, uint64_t a, uint64_t b, uint64_t bias, uint64_t c, int M,
+                     int N, int K, int lda, int ldb, int ldc, uint64_t workspace, int64_t workspace_floats,
+                     uint64_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MFHIP_H */

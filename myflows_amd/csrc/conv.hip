@@ -1,0 +1,295 @@
+// Bandwidth-bound kernels of the convolution and pooling path: im2col, col2im (gather), the NCHW
+// epilogue (bias + activation), the transposed/gated dy with FP64 bias partials, the in-order FP64
+// partial reduction, the GEMM bias epilogue and max-pool forward/backward.
+//
+// Layouts (row-major, NCHW): cols[(n*OH + oh)*OW + ow][(ci*KH + kh)*KW + kw] is the im2col matrix
+// (M = N*OH*OW rows, K = CI*KH*KW features); rows[(n*OHW + p)][co] is the GEMM output before the
+// epilogue. Every reduction sums in a fixed order, so each kernel is bitwise reproducible.
+#include "common.h"
+#include "fastdiv.h"
+
+namespace mfh {
+namespace {
+
+// One thread per cols element. The index decomposition uses FastDiv; the x reads of neighbouring
+// threads (consecutive kw, then kh/ci) hit the same cache lines, the writes are fully coalesced.
+__global__ __launch_bounds__(256) void im2col_kernel(const float* __restrict__ x, float* __restrict__ cols, int total,
+                                                     FastDiv div_k, FastDiv div_kw, FastDiv div_kh, FastDiv div_ow,
+                                                     FastDiv div_oh, int CI, int H, int W, int SH, int SW, int PH,
+                                                     int PW) {
+    const int idx = blockIdx.x * 256 + threadIdx.x;
+    if (idx >= total) return;
+    int feature, kw, kh, ow, oh;
+    const int row = div_k.divmod(idx, feature);
+    const int t = div_kw.divmod(feature, kw);
+    const int ci = div_kh.divmod(t, kh);
+    const int t2 = div_ow.divmod(row, ow);
+    const int n = div_oh.divmod(t2, oh);
+    const int ih = oh * SH - PH + kh;
+    const int iw = ow * SW - PW + kw;
+    float v = 0.0f;
+    if (ih >= 0 && ih < H && iw >= 0 && iw < W) v = x[((n * CI + ci) * H + ih) * W + iw];
+    cols[idx] = v;
+}
+
+// dx[n, ci, ih, iw] = sum of grad_cols over every window position that reads (ih, iw), visited in
+// increasing (oh, ow) order; no atomics, so the result is deterministic.
+__global__ __launch_bounds__(256) void col2im_kernel(const float* __restrict__ grad_cols, float* __restrict__ dx,
+                                                     int total, FastDiv div_w, FastDiv div_h, FastDiv div_ci, int CI,
+                                                     int KH, int KW, int OH, int OW, int SH, int SW, int PH, int PW) {
+    const int idx = blockIdx.x * 256 + threadIdx.x;
+    if (idx >= total) return;
+    int iw, ih, ci;
+    const int t = div_w.divmod(idx, iw);
+    const int t2 = div_h.divmod(t, ih);
+    const int n = div_ci.divmod(t2, ci);
+    const int hp = ih + PH, wp = iw + PW;  // coordinates in the zero-padded input
+    // Windows oh with oh*SH <= hp <= oh*SH + KH - 1.
+    const int oh_lo = hp >= KH ? (hp - KH) / SH + 1 : 0;
+    const int oh_hi = min(OH - 1, hp / SH);
+    const int ow_lo = wp >= KW ? (wp - KW) / SW + 1 : 0;
+    const int ow_hi = min(OW - 1, wp / SW);
+    const int features = CI * KH * KW;
+    float sum = 0.0f;
+    for (int oh = oh_lo; oh <= oh_hi; ++oh) {
+        const int kh = hp - oh * SH;
+        const float* base = grad_cols + ((n * OH + oh) * OW) * features + (ci * KH + kh) * KW;
+        for (int ow = ow_lo; ow <= ow_hi; ++ow) {
+            const int kw = wp - ow * SW;
+            sum += base[ow * features + kw];
+        }
+    }
+    dx[idx] = sum;
+}
+
+constexpr int TILE = 64;   // pixels x channels per transpose tile (one wave64 per row of the tile)
+constexpr int TROWS = 4;   // waves per block; each thread covers TILE / TROWS tile rows
+
+// rows (N*OHW, CO) -> y (N, CO, OHW), y = act(rows + bias). The transpose goes through a padded
+// LDS tile so that the read (along CO) and the write (along OHW) are both coalesced. LeakyReLU is
+// only fused for alpha > 0, so y > 0 exactly when the pre-activation is > 0 (the backward gate).
+__global__ __launch_bounds__(TILE* TROWS) void conv_epilogue_kernel(const float* __restrict__ rows,
+                                                                    const float* __restrict__ bias,
+                                                                    float* __restrict__ y, int OHW, int CO, int act,
+                                                                    float alpha) {
+    __shared__ float tile[TILE][TILE + 1];
+    const int n = blockIdx.z, p0 = blockIdx.x * TILE, c0 = blockIdx.y * TILE;
+    const int tx = threadIdx.x, ty = threadIdx.y;
+    const float* src = rows + static_cast<long long>(n) * OHW * CO;
+    float* dst = y + static_cast<long long>(n) * CO * OHW;
+#pragma unroll
+    for (int j = ty; j < TILE; j += TROWS) {
+        const int p = p0 + j, c = c0 + tx;
+        if (p < OHW && c < CO) tile[tx][j] = src[p * CO + c];
+    }
+    __syncthreads();
+#pragma unroll
+    for (int j = ty; j < TILE; j += TROWS) {
+        const int c = c0 + j, p = p0 + tx;
+        if (p < OHW && c < CO) {
+            float v = tile[j][tx];
+            if (bias) v += bias[c];
+            if (act == ACT_RELU) v = v < 0.0f ? 0.0f : v;  // NaN stays NaN, like max(0, v) in NumPy
+            else if (act == ACT_LEAKY_RELU) v = v > 0.0f ? v : alpha * v;
+            dst[c * OHW + p] = v;
+        }
+    }
+}
+
+// dy (N, CO, OHW) -> dyT (N*OHW, CO), gated by the fused activation through the forward output y,
+// plus per-channel FP64 sums of the gated dy. Block (bx, by, n) walks the pixel tiles bx,
+// bx + gridDim.x, ... in order; each thread sums its tile rows in FP64 and the 64 lanes of a wave
+// combine with a fixed butterfly, so partial[(n * gridDim.x + bx) * CO + c] is reproducible.
+__global__ __launch_bounds__(TILE* TROWS) void conv_grad_rows_kernel(const float* __restrict__ dy,
+                                                                     const float* __restrict__ gate_y,
+                                                                     float* __restrict__ dyT,
+                                                                     double* __restrict__ partial, int OHW, int CO,
+                                                                     int act, float alpha) {
+    __shared__ float tile[TILE][TILE + 1];
+    const int n = blockIdx.z, c0 = blockIdx.y * TILE;
+    const int tx = threadIdx.x, ty = threadIdx.y;
+    const long long image = static_cast<long long>(n) * CO * OHW;
+    const float* src = dy + image;
+    const float* gate = gate_y ? gate_y + image : nullptr;
+    float* dst = dyT ? dyT + static_cast<long long>(n) * OHW * CO : nullptr;
+    double acc[TILE / TROWS];
+#pragma unroll
+    for (int k = 0; k < TILE / TROWS; ++k) acc[k] = 0.0;
+    for (int p0 = blockIdx.x * TILE; p0 < OHW; p0 += gridDim.x * TILE) {
+#pragma unroll
+        for (int k = 0; k < TILE / TROWS; ++k) {
+            const int c = c0 + ty + k * TROWS, p = p0 + tx;
+            float v = 0.0f;
+            if (p < OHW && c < CO) {
+                const int at = c * OHW + p;
+                v = src[at];
+                if (act == ACT_RELU) v = gate[at] > 0.0f ? v : 0.0f;
+                else if (act == ACT_LEAKY_RELU) v = gate[at] > 0.0f ? v : alpha * v;
+            }
+            tile[ty + k * TROWS][tx] = v;
+            acc[k] += static_cast<double>(v);
+        }
+        __syncthreads();
+        if (dst) {
+#pragma unroll
+            for (int k = 0; k < TILE / TROWS; ++k) {
+                const int p = p0 + ty + k * TROWS, c = c0 + tx;
+                if (p < OHW && c < CO) dst[p * CO + c] = tile[tx][ty + k * TROWS];
+            }
+        }
+        __syncthreads();
+    }
+    if (!partial) return;
+#pragma unroll
+    for (int k = 0; k < TILE / TROWS; ++k) {
+        double s = acc[k];
+#pragma unroll
+        for (int offset = 32; offset > 0; offset >>= 1) s += __shfl_xor(s, offset, 64);
+        const int c = c0 + ty + k * TROWS;
+        if (tx == 0 && c < CO) partial[(static_cast<long long>(n) * gridDim.x + blockIdx.x) * CO + c] = s;
+    }
+}
+
+// out[i] = (float) sum_{j = 0..count-1} partial[j * width + i], in order, in FP64.
+__global__ __launch_bounds__(128) void reduce_partials_kernel(const double* __restrict__ partial,
+                                                              float* __restrict__ out, int count, int width) {
+    const int i = blockIdx.x * 128 + threadIdx.x;
+    if (i >= width) return;
+    double s = 0.0;
+    for (int j = 0; j < count; ++j) s += partial[static_cast<long long>(j) * width + i];
+    out[i] = static_cast<float>(s);
+}
+
+__global__ __launch_bounds__(256) void add_bias_kernel(float* __restrict__ rows, const float* __restrict__ bias,
+                                                       int total, FastDiv div_n) {
+    const int idx = blockIdx.x * 256 + threadIdx.x;
+    if (idx >= total) return;
+    int col;
+    div_n.divmod(idx, col);
+    rows[idx] += bias[col];
+}
+
+// Window maximum in (kh, kw) row-major order with a strict '>' (the first maximum wins ties); a NaN
+// takes over, so any NaN in the window gives a NaN output. argmax is the flat index into x.
+__global__ __launch_bounds__(256) void pool_forward_kernel(const float* __restrict__ x, float* __restrict__ y,
+                                                           int* __restrict__ argmax, int total, FastDiv div_ow,
+                                                           FastDiv div_oh, int H, int W, int KH, int KW, int SH,
+                                                           int SW) {
+    const int idx = blockIdx.x * 256 + threadIdx.x;
+    if (idx >= total) return;
+    int ow, oh;
+    const int t = div_ow.divmod(idx, ow);
+    const int nc = div_oh.divmod(t, oh);
+    const int first = (nc * H + oh * SH) * W + ow * SW;
+    int best = first;
+    float value = x[first];
+    for (int kh = 0; kh < KH; ++kh) {
+        const float* row = x + first + kh * W;
+        for (int kw = 0; kw < KW; ++kw) {
+            const float v = row[kw];
+            if (v > value || v != v) {
+                value = v;
+                best = first + kh * W + kw;
+            }
+        }
+    }
+    y[idx] = value;
+    argmax[idx] = best;
+}
+
+// dx[i] = sum of dy over the windows (visited in increasing oh, ow order) whose argmax is i.
+__global__ __launch_bounds__(256) void pool_backward_kernel(const float* __restrict__ dy,
+                                                            const int* __restrict__ argmax, float* __restrict__ dx,
+                                                            int total, FastDiv div_w, FastDiv div_h, int OH, int OW,
+                                                            int KH, int KW, int SH, int SW) {
+    const int idx = blockIdx.x * 256 + threadIdx.x;
+    if (idx >= total) return;
+    int iw, ih;
+    const int t = div_w.divmod(idx, iw);
+    const int nc = div_h.divmod(t, ih);
+    const int oh_lo = ih >= KH ? (ih - KH) / SH + 1 : 0;
+    const int oh_hi = min(OH - 1, ih / SH);
+    const int ow_lo = iw >= KW ? (iw - KW) / SW + 1 : 0;
+    const int ow_hi = min(OW - 1, iw / SW);
+    float sum = 0.0f;
+    for (int oh = oh_lo; oh <= oh_hi; ++oh)
+        for (int ow = ow_lo; ow <= ow_hi; ++ow) {
+            const int out = (nc * OH + oh) * OW + ow;
+            if (argmax[out] == idx) sum += dy[out];
+        }
+    dx[idx] = sum;
+}
+
+}  // namespace
+
+int launch_im2col(const float* x, float* cols, const ConvDims& d, hipStream_t stream) {
+    const int K = d.CI * d.KH * d.KW;
+    const int total = d.N * d.OH * d.OW * K;
+    im2col_kernel<<<blocks_for(total, 256), 256, 0, stream>>>(x, cols, total, FastDiv(K), FastDiv(d.KW),
+                                                                FastDiv(d.KH), FastDiv(d.OW), FastDiv(d.OH), d.CI,
+                                                                d.H, d.W, d.SH, d.SW, d.PH, d.PW);
+    return MFH_CHECK_LAUNCH("im2col", stream);
+}
+
+int launch_col2im(const float* grad_cols, float* dx, const ConvDims& d, hipStream_t stream) {
+    const int total = d.N * d.CI * d.H * d.W;
+    col2im_kernel<<<blocks_for(total, 256), 256, 0, stream>>>(grad_cols, dx, total, FastDiv(d.W), FastDiv(d.H),
+                                                                FastDiv(d.CI), d.CI, d.KH, d.KW, d.OH, d.OW, d.SH,
+                                                                d.SW, d.PH, d.PW);
+    return MFH_CHECK_LAUNCH("col2im", stream);
+}
+
+int launch_conv_epilogue(const float* rows, const float* bias, float* y, int N, int OHW, int CO, int act,
+                         float alpha, hipStream_t stream) {
+    const dim3 grid(blocks_for(OHW, TILE), blocks_for(CO, TILE), N), block(TILE, TROWS);
+    conv_epilogue_kernel<<<grid, block, 0, stream>>>(rows, bias, y, OHW, CO, act, alpha);
+    return MFH_CHECK_LAUNCH("conv_epilogue", stream);
+}
+
+int conv_grad_tile() { return TILE; }
+
+int launch_conv_grad_rows(const float* dy, const float* y, float* dyT, double* partial, int N, int OHW, int CO,
+                          int grid_x, int act, float alpha, hipStream_t stream) {
+    const dim3 grid(grid_x, blocks_for(CO, TILE), N), block(TILE, TROWS);
+    conv_grad_rows_kernel<<<grid, block, 0, stream>>>(dy, y, dyT, partial, OHW, CO, act, alpha);
+    return MFH_CHECK_LAUNCH("conv_grad_rows", stream);
+}
+
+int launch_reduce_partials(const double* partial, float* out, int count, int width, hipStream_t stream) {
+    reduce_partials_kernel<<<blocks_for(width, 128), 128, 0, stream>>>(partial, out, count, width);
+    return MFH_CHECK_LAUNCH("reduce_partials", stream);
+}
+
+int launch_add_bias(float* rows, const float* bias, int M, int N, hipStream_t stream) {
+    const int total = M * N;
+    add_bias_kernel<<<blocks_for(total, 256), 256, 0, stream>>>(rows, bias, total, FastDiv(N));
+    return MFH_CHECK_LAUNCH("add_bias", stream);
+}
+
+int launch_pool_forward(const float* x, float* y, int* argmax, int N, int C, int H, int W, int OH, int OW, int KH,
+                        int KW, int SH, int SW, hipStream_t stream) {
+    const int total = N * C * OH * OW;
+    pool_forward_kernel<<<blocks_for(total, 256), 256, 0, stream>>>(x, y, argmax, total, FastDiv(OW), FastDiv(OH), H,
+                                                                      W, KH, KW, SH, SW);
+    return MFH_CHECK_LAUNCH("pool_forward", stream);
+}
+
+int launch_pool_backward(const float* dy, const int* argmax, float* dx, int N, int C, int H, int W, int OH, int OW,
+                         int KH, int KW, int SH, int SW, hipStream_t stream) {
+    const int total = N * C * H * W;
+    pool_backward_kernel<<<blocks_for(total, 256), 256, 0, stream>>>(dy, argmax, dx, total, FastDiv(W), FastDiv(H),
+                                                                       OH, OW, KH, KW, SH, SW);
+    return MFH_CHECK_LAUNCH("pool_backward", stream);
+}
+
+}  // namespace mfh
+
+namespace mfh {
+int conv_probe_kernels() {
+    hipFuncAttributes attributes;
+    const hipError_t status = hipFuncGetAttributes(&attributes, reinterpret_cast<const void*>(&im2col_kernel));
+    if (status != hipSuccess)
+        return MFH_FAIL(ERR_INIT, std::string("no usable gfx950 code object: ") + hipGetErrorString(status));
+    return OK;
+}
+}  // namespace mfh

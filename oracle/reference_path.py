@@ -1,0 +1,311 @@
+"""NumPy restatement of the reference's CPU path for the convolution / GEMM / pooling operators.
+
+TEST INFRASTRUCTURE ONLY. Nothing in ``myflows_amd`` imports this package; only ``tests/``,
+``__graft_entry__.smoke()`` and the ``cpu_baseline`` leg of ``bench.py`` use it, as the checker and
+as the timed CPU baseline. It never runs on the GPU.
+
+Every function follows a NumPy branch of the reference and cites it. Arrays are float32 in,
+float32 out, with the reference's FP64 reductions where it has them.
+
+Pinning (see tests/test_oracle.py): im2col/col2im and the conv/pool passes are checked against the
+FP64 loops of ``oracle.naive`` (the reference's own test oracles), against scipy.signal.correlate
+for the convolution forward, against the adjoint identities <conv(x), g> = <x, dX(g)> = <W, dW(g)>,
+and against the known answers of the reference tests (arange(25) * ones(3x3); the tie
+[[1, 1], [0, .5]] -> [[1, 0], [0, 0]]; NaN propagation). BatchNorm, Linear, MSE and Adam are
+checked against torch (CPU, float64) and closed forms.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+
+
+# ---------------------------------------------------------------------------------------------
+# im2col / col2im, ops/convolution.py:143-284
+# ---------------------------------------------------------------------------------------------
+def out_size(h, w, kernel_size, stride, padding):
+    kh, kw = kernel_size
+    sh, sw = stride
+    ph, pw = padding
+    return (h + 2 * ph - kh) // sh + 1, (w + 2 * pw - kw) // sw + 1
+
+
+def window_indices(channels, kernel_size, output_size, stride):
+    """(k, i, j) gather indices of every (feature, position); ops/convolution.py:143-158."""
+    kh, kw = kernel_size
+    oh, ow = output_size
+    sh, sw = stride
+    i0 = np.tile(np.repeat(np.arange(kh), kw), channels)
+    j0 = np.tile(np.arange(kw), kh * channels)
+    k = np.repeat(np.arange(channels), kh * kw).reshape(-1, 1)
+    i1 = (np.repeat(np.arange(oh), ow) * sh).reshape(1, -1)
+    j1 = (np.tile(np.arange(ow), oh) * sw).reshape(1, -1)
+    return k, i0.reshape(-1, 1) + i1, j0.reshape(-1, 1) + j1
+
+
+def im2col(x, kernel_size, stride=(1, 1), padding=(0, 0), pad_value=0.0):
+    """cols[(n*OH + oh)*OW + ow][(ci*KH + kh)*KW + kw]; ops/convolution.py:161-163,241-255."""
+    n, c, h, w = x.shape
+    ph, pw = padding
+    oh, ow = out_size(h, w, kernel_size, stride, padding)
+    k, i, j = window_indices(c, kernel_size, (oh, ow), stride)
+    xp = np.pad(x, ((0, 0), (0, 0), (ph, ph), (pw, pw)), mode="constant", constant_values=pad_value)
+    return xp[:, k, i, j].transpose(0, 2, 1).reshape(-1, k.shape[0])
+
+
+def col2im(rows, input_shape, kernel_size, stride=(1, 1), padding=(0, 0)):
+    """Adjoint of im2col by np.add.at into the padded input; ops/convolution.py:166-175,258-284."""
+    n, c, h, w = input_shape
+    ph, pw = padding
+    oh, ow = out_size(h, w, kernel_size, stride, padding)
+    k, i, j = window_indices(c, kernel_size, (oh, ow), stride)
+    cols = rows.reshape(n, oh * ow, k.shape[0]).transpose(0, 2, 1)
+    out = np.zeros((n, c, h + 2 * ph, w + 2 * pw), dtype=rows.dtype)
+    np.add.at(out, (np.arange(n)[:, None, None], k[None], i[None], j[None]), cols)
+    return out[:, :, ph:ph + h, pw:pw + w]
+
+
+def col2im_native(grad_cols, input_shape, kernel_size, stride=(1, 1), padding=(0, 0)):
+    """The native col2im semantics (ops/cuda_native/native_cublas.cpp:247-271): every input element
+    gathers its window positions in increasing (oh, ow) order and sums them in float32. Increasing oh
+    is decreasing kh, so the loops below run kh and kw downwards. Bit-exact reference for the kernel."""
+    n, c, h, w = input_shape
+    kh_, kw_ = kernel_size
+    sh, sw = stride
+    ph, pw = padding
+    oh_, ow_ = out_size(h, w, kernel_size, stride, padding)
+    rows = grad_cols.reshape(n, oh_, ow_, c, kh_, kw_)
+    ih = np.arange(h)[:, None]
+    iw = np.arange(w)[None, :]
+    dx = np.zeros((n, c, h, w), dtype=np.float32)
+    for kh in reversed(range(kh_)):
+        hp = ih + ph - kh
+        oh = hp // sh
+        valid_h = (hp >= 0) & (hp % sh == 0) & (oh < oh_)
+        for kw in reversed(range(kw_)):
+            wp = iw + pw - kw
+            ow = wp // sw
+            valid = valid_h & (wp >= 0) & (wp % sw == 0) & (ow < ow_)
+            tap = rows[:, :, :, :, kh, kw]  # (n, OH, OW, c)
+            term = tap[:, np.clip(oh, 0, oh_ - 1), np.clip(ow, 0, ow_ - 1), :]  # (n, h, w, c)
+            dx = np.where(valid[None, None], dx + term.transpose(0, 3, 1, 2), dx)
+    return dx
+
+
+# ---------------------------------------------------------------------------------------------
+# Conv2D_Op NumPy branch, ops/convolution.py:361-424 (forward) and :458-523 (backward), groups=1
+# ---------------------------------------------------------------------------------------------
+def conv2d_forward(x, weight, bias=None, stride=(1, 1), padding=(0, 0), activation=None, alpha=0.0):
+    """Return (y, cols): y = cols @ W^T reshaped to NCHW (+ bias), then the optional activation of
+    Conv2D_ReLU_Op / Conv2D_LeakyReLU_Op (ops/convolution.py:526-573)."""
+    n = x.shape[0]
+    co = weight.shape[0]
+    oh, ow = out_size(x.shape[2], x.shape[3], weight.shape[2:], stride, padding)
+    cols = im2col(x, weight.shape[2:], stride, padding)
+    y = (cols @ weight.reshape(co, -1).T).reshape(n, oh, ow, co).transpose(0, 3, 1, 2)
+    if bias is not None:
+        y = y + bias.reshape(1, co, 1, 1)
+    if activation == "relu":
+        y = np.maximum(0, y)
+    elif activation == "leaky_relu":
+        y = np.where(y > 0, y, np.float32(alpha) * y)
+    return np.ascontiguousarray(y, dtype=x.dtype), cols
+
+
+def conv2d_backward(x, weight, grad_y, cols=None, stride=(1, 1), padding=(0, 0), need_input_grad=True,
+                    need_weight_grad=True, need_bias_grad=True, activation=None, alpha=0.0, output=None):
+    """(dx, dw, db), None for what is not requested. db sums in FP64 (ops/convolution.py:481-483);
+    dW = gy^T cols, grad_cols = gy W, dx = col2im(grad_cols) (:491-523). A fused activation gates
+    grad_y through the forward output first (the native gate, y > 0)."""
+    if activation == "relu":
+        grad_y = np.where(output > 0, grad_y, grad_y.dtype.type(0))
+    elif activation == "leaky_relu":
+        grad_y = np.where(output > 0, grad_y, grad_y.dtype.type(alpha) * grad_y)
+    co = weight.shape[0]
+    db = grad_y.sum(axis=(0, 2, 3), dtype=np.float64).astype(grad_y.dtype) if need_bias_grad else None
+    gy = grad_y.transpose(0, 2, 3, 1).reshape(-1, co)
+    dw = None
+    if need_weight_grad:
+        if cols is None:
+            cols = im2col(x, weight.shape[2:], stride, padding)
+        dw = (gy.T @ cols).reshape(weight.shape)
+    dx = None
+    if need_input_grad:
+        dx = col2im(gy @ weight.reshape(co, -1), x.shape, weight.shape[2:], stride, padding)
+    return dx, dw, db
+
+
+# ---------------------------------------------------------------------------------------------
+# MaxPool2d_Op, ops/convolution.py:817-890
+# ---------------------------------------------------------------------------------------------
+def maxpool2d_forward(x, kernel_size=(2, 2), stride=(2, 2), padding=(0, 0)):
+    """NumPy branch (:841-859): -inf padding (:830-833), im2col patches, max, first-max mask via
+    cumsum == 1. Returns (y, mask, padded_shape)."""
+    ph, pw = padding
+    if ph or pw:
+        x = np.pad(x, ((0, 0), (0, 0), (ph, ph), (pw, pw)), constant_values=-np.inf)
+    n, c, h, w = x.shape
+    kh, kw = kernel_size
+    oh, ow = out_size(h, w, kernel_size, stride, (0, 0))
+    patches = im2col(x, kernel_size, stride, (0, 0)).reshape(n, oh * ow, c, kh * kw).transpose(0, 2, 1, 3)
+    y = np.max(patches, axis=-1)
+    eq = patches == y[..., None]
+    mask = eq & (eq.cumsum(axis=-1) == 1)
+    return y.reshape(n, c, oh, ow), mask, x.shape
+
+
+def maxpool2d_backward(grad_y, mask, padded_shape, kernel_size=(2, 2), stride=(2, 2), padding=(0, 0)):
+    """NumPy branch (:870-884): masked gradient rows scattered back with col2im, then unpadded."""
+    n, c, oh, ow = grad_y.shape
+    kh, kw = kernel_size
+    patches = mask * grad_y.reshape(n, c, oh * ow)[..., None]
+    rows = patches.transpose(0, 2, 1, 3).reshape(-1, c * kh * kw)
+    dx = col2im(rows.astype(grad_y.dtype), padded_shape, kernel_size, stride, (0, 0))
+    ph, pw = padding
+    return dx[:, :, ph:dx.shape[2] - ph, pw:dx.shape[3] - pw] if (ph or pw) else dx
+
+
+def maxpool2d_native_forward(x, kernel_size=(2, 2), stride=(2, 2)):
+    """The native pool semantics (ops/cuda_native/native_cublas.cpp:360-376): window scanned in (kh, kw)
+    order, a strictly larger value or a NaN takes over, y = x[argmax], argmax = flat index into x
+    (already padded by the caller). Bit-exact reference for the HIP kernel."""
+    n, c, h, w = x.shape
+    kh, kw = kernel_size
+    sh, sw = stride
+    oh, ow = out_size(h, w, kernel_size, stride, (0, 0))
+    flat = x.reshape(-1)
+    base = ((np.arange(n * c)[:, None, None] * h + np.arange(oh)[None, :, None] * sh) * w
+            + np.arange(ow)[None, None, :] * sw).reshape(n, c, oh, ow)
+    best = base.copy()
+    value = flat[base]
+    for i in range(kh):
+        for j in range(kw):
+            at = base + i * w + j
+            v = flat[at]
+            take = (v > value) | np.isnan(v)
+            value = np.where(take, v, value)
+            best = np.where(take, at, best)
+    return value.astype(x.dtype), best.astype(np.int32)
+
+
+def maxpool2d_native_backward(grad_y, argmax, input_shape):
+    """dx[i] = sum of grad_y over windows whose argmax is i, added in window order in float32
+    (native_cublas.cpp:378-393); np.add.at adds in index order, which is that order."""
+    dx = np.zeros(int(np.prod(input_shape)), dtype=np.float32)
+    np.add.at(dx, argmax.reshape(-1).astype(np.int64), grad_y.reshape(-1).astype(np.float32))
+    return dx.reshape(input_shape)
+
+
+# ---------------------------------------------------------------------------------------------
+# Linear (x @ W + b), ops/basic.py:67-164
+# ---------------------------------------------------------------------------------------------
+def reduce_to(grad, shape):
+    """Sum over broadcast axes in FP64, rounded once; ops/basic.py:67-73."""
+    lead = grad.ndim - len(shape)
+    axes = tuple(range(lead)) + tuple(lead + i for i, (gd, bd) in enumerate(zip(grad.shape[lead:], shape))
+                                      if bd == 1 and gd != 1)
+    total = grad.sum(axis=axes, dtype=np.float64) if axes else grad
+    return total.reshape(shape).astype(grad.dtype, copy=False)
+
+
+def linear_forward(x, w, b):
+    return x @ w + b
+
+
+def linear_backward(x, w, b_shape, grad, need_input_grad=True):
+    dx = grad @ w.T if need_input_grad else None
+    return dx, x.T @ grad, reduce_to(grad, b_shape)
+
+
+# ---------------------------------------------------------------------------------------------
+# BatchNorm2d, ops/fused.py:250-387 (NumPy branches)
+# ---------------------------------------------------------------------------------------------
+def _channel(a):
+    return a.reshape(1, -1, 1, 1)
+
+
+def batchnorm2d_forward(x, gamma, beta, running_mean, running_var, momentum=0.1, eps=1e-5, training=True,
+                        relu=False, residual=None):
+    """Return (y, mean (2, C) hi/lo split, inv_std); updates the running statistics in place."""
+    axes = (0, 2, 3)
+    if training:
+        mean64 = x.mean(axis=axes, dtype=np.float64)
+        centered = x.astype(np.float64) - _channel(mean64)
+        var64 = (centered * centered).mean(axis=axes)
+        running_mean[...] = (1.0 - momentum) * running_mean.astype(np.float64) + momentum * mean64
+        running_var[...] = (1.0 - momentum) * running_var.astype(np.float64) + momentum * var64
+    else:
+        mean64, var64 = running_mean.astype(np.float64), running_var.astype(np.float64)
+    hi = mean64.astype(x.dtype)
+    mean = np.stack([hi, (mean64 - hi).astype(x.dtype)])
+    inv_std = (1.0 / np.sqrt(var64 + eps)).astype(x.dtype)
+    y = (((x - _channel(mean[0])) - _channel(mean[1])) * _channel(inv_std)) * _channel(gamma) + _channel(beta)
+    if residual is not None:
+        y = y + residual
+    if relu:
+        y = np.maximum(0, y)
+    return y, mean, inv_std
+
+
+def batchnorm2d_backward(x, dy, gamma, mean, inv_std, training=True):
+    """(dx, dgamma, dbeta) with FP64 channel sums (ops/fused.py:353-380)."""
+    axes = (0, 2, 3)
+    count = x.shape[0] * x.shape[2] * x.shape[3]
+    istd = inv_std.astype(np.float64)
+    dy64 = dy.astype(np.float64)
+    sdy = dy64.sum(axis=axes)
+    centered = x.astype(np.float64) - _channel(mean[0].astype(np.float64) + mean[1].astype(np.float64))
+    dgamma = istd * (dy64 * centered).sum(axis=axes)
+    a = _channel((gamma.astype(np.float64) * istd).astype(x.dtype))
+    if training:
+        k1 = _channel((sdy / count).astype(x.dtype))
+        k2 = _channel((istd * dgamma / count).astype(x.dtype))
+        dx = a * (dy - k1 - ((x - _channel(mean[0])) - _channel(mean[1])) * k2)
+    else:
+        dx = a * dy
+    return dx, dgamma.astype(x.dtype), sdy.astype(x.dtype)
+
+
+# ---------------------------------------------------------------------------------------------
+# ReLU, Add, GlobalAvgPool2d, MSELoss: ops/activation.py:43-52, ops/fused.py:50-62,
+# ops/basic.py:5-39, ops/batchnorm.py:110-123, ops/loss.py:94-113
+# ---------------------------------------------------------------------------------------------
+def relu_backward(x, grad):
+    return np.where(x > 0, grad, 0).astype(x.dtype, copy=False)
+
+
+def gap_forward(x):
+    return x.mean(axis=(2, 3), dtype=np.float64).astype(x.dtype, copy=False)
+
+
+def gap_backward(grad, shape):
+    n, c, h, w = shape
+    return np.broadcast_to(grad.reshape(n, c, 1, 1) / (h * w), shape)
+
+
+def mse_forward(pred, target):
+    diff = pred - target
+    return np.mean(diff * diff, dtype=np.float64).astype(diff.dtype)
+
+
+def mse_backward(pred, target, grad=np.float32(1.0)):
+    n = max(pred.size, 1)
+    return grad * (2.0 * (pred - target) / n)
+
+
+# ---------------------------------------------------------------------------------------------
+# Adam, ops/fused.py:514-533 (NumPy branch, every operation rounded to float32 in this order)
+# ---------------------------------------------------------------------------------------------
+def adam_update(param, grad, m, v, *, lr, beta1, beta2, eps, step, grad_scale=1.0):
+    dtype = param.dtype.type
+    bc1, bc2 = 1.0 - beta1 ** step, 1.0 - beta2 ** step
+    scale, b1, omb1, b2, omb2, bc1, bc2, lr, eps = (dtype(v_) for v_ in (grad_scale, beta1, 1.0 - beta1, beta2,
+                                                                           1.0 - beta2, bc1, bc2, lr, eps))
+    gs = grad if scale == 1 else grad * scale
+    m *= b1
+    m += omb1 * gs
+    v *= b2
+    v += omb2 * (gs * gs)
+    denom = np.sqrt(v / bc2)
+    denom += eps
+    param -= (lr * (m / bc1)) / denom

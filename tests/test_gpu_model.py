@@ -1,0 +1,171 @@
+"""End-to-end parity on the GPU: Linear/Dense, the C3 convolution + pooling configuration, and the
+ResNet18 training step (C1 shape) through the Variable/Graph API on the hip_native backend.
+
+The model-level tolerance is "no worse than the reference FP32 path": the GPU result's normwise
+error against the same step computed in float64 by the oracle must stay within a small factor of the
+NumPy float32 path's own error (plus a floor of 1e-6 of the tensor's scale).
+"""
+
+import numpy as np
+import pytest
+import torch
+
+import myflows_amd as mf
+from myflows_amd import native
+from oracle import naive, reference_path as rp
+from oracle import resnet as oracle_resnet
+from tests.fixtures import EPS32, assert_near, gamma_k
+
+pytestmark = pytest.mark.gpu
+
+
+def gpu(a):
+    return torch.as_tensor(np.ascontiguousarray(a), device="cuda")
+
+
+def host(t):
+    torch.cuda.synchronize()
+    return t.detach().cpu().numpy()
+
+
+def normwise(a, ref):
+    return float(np.abs(np.asarray(a, np.float64) - ref).max() / max(np.abs(ref).max(), 1e-30))
+
+
+def test_linear_backends_match_fp64():
+    rng = np.random.default_rng(1)
+    x, w = rng.standard_normal((37, 300), dtype=np.float32), rng.standard_normal((300, 23), dtype=np.float32)
+    b, g = rng.standard_normal((1, 23), dtype=np.float32), rng.standard_normal((37, 23), dtype=np.float32)
+    x64, w64, b64, g64 = (a.astype(np.float64) for a in (x, w, b, g))
+    expected = (x64 @ w64 + b64, g64 @ w64.T, x64.T @ g64, g64.sum(axis=0, keepdims=True))
+    magnitude = (np.abs(x64) @ np.abs(w64) + np.abs(b64), np.abs(g64) @ np.abs(w64.T), np.abs(x64.T) @ np.abs(g64))
+    for backend in ("hip_native", "hip_native_kahan", "hip_native_dot2"):
+        nodes = [mf.Variable(gpu(x)), mf.Variable(gpu(w), trainable=True), mf.Variable(gpu(b), trainable=True)]
+        op = mf.Linear(*nodes, backend=backend)
+        op.forward(*(n.value for n in nodes))
+        op.grad = gpu(g)
+        op.backward()
+        got = [host(op.value)] + [host(n.grad) for n in nodes]
+        for actual, exact, bound in zip(got[:3], expected[:3], magnitude):
+            assert np.all(np.abs(actual - exact) <= gamma_k(300) * bound + EPS32 * np.abs(exact) + 1e-30), backend
+        assert np.all(np.abs(got[3] - expected[3]) <= np.spacing(np.abs(expected[3]).astype(np.float32))), backend
+    # skip dX for an input without requires_grad
+    nodes = [mf.Variable(gpu(x), requires_grad=False), mf.Variable(gpu(w), trainable=True),
+             mf.Variable(gpu(b), trainable=True)]
+    op = mf.Linear(*nodes, backend="hip_native")
+    op.forward(*(n.value for n in nodes))
+    op.grad = gpu(g)
+    op.backward()
+    assert nodes[0].grad is None
+
+
+def test_c3_convolution_and_pool_configuration():
+    """Conv 64->64 3x3/1/1 at N=32, 30x40 (forward, dX, dW, db), then MaxPool 2x2/2 forward/backward."""
+    rng = np.random.default_rng(0)
+    x = rng.standard_normal((32, 64, 30, 40)).astype(np.float32)
+    w = (rng.standard_normal((64, 64, 3, 3)) * np.sqrt(2.0 / 576)).astype(np.float32)
+    b = np.zeros(64, np.float32)
+    y, cols = native.conv2d_forward(gpu(x), gpu(w), gpu(b), stride=(1, 1), padding=(1, 1))
+    y_ref64, cols_ref = rp.conv2d_forward(x.astype(np.float64), w.astype(np.float64), b, (1, 1), (1, 1))
+    np.testing.assert_array_equal(host(cols), cols_ref.astype(np.float32))
+    assert_near(host(y), y_ref64, 1e-5, "y")
+    pooled, ctx = native.maxpool2d_forward(y, kernel_size=(2, 2), stride=(2, 2))
+    y_host = host(y)
+    p_ref, argmax_ref = rp.maxpool2d_native_forward(y_host, (2, 2), (2, 2))
+    np.testing.assert_array_equal(host(pooled), p_ref)
+    np.testing.assert_array_equal(host(ctx.argmax), argmax_ref)
+    dp = rng.standard_normal(p_ref.shape).astype(np.float32)
+    dy = native.maxpool2d_backward(gpu(dp), ctx)
+    dy_ref = rp.maxpool2d_native_backward(dp, argmax_ref, y_host.shape)
+    np.testing.assert_array_equal(host(dy), dy_ref)
+    dx, dw, db = native.conv2d_backward(gpu(x), gpu(w), dy, cols, stride=(1, 1), padding=(1, 1))
+    dx64, dw64, db64 = rp.conv2d_backward(x.astype(np.float64), w.astype(np.float64), dy_ref.astype(np.float64),
+                                          cols_ref, (1, 1), (1, 1))
+    assert_near(host(dx), dx64, 1e-5, "dx")
+    assert_near(host(dw), dw64, 1e-5, "dw")
+    assert np.all(np.abs(host(db) - db64) <= np.spacing(np.abs(db64).astype(np.float32)))
+
+
+def _build_gpu_resnet(batch, height, width, base_width=64, seed=0):
+    model = mf.ResNet18(output_dim=2, base_width=base_width, initializer=mf.make_initializer(seed=seed),
+                        conv_backend="hip_native")
+    x_np, t_np = oracle_resnet.synthetic_batch(batch, height, width, seed=seed)
+    x = mf.Variable(gpu(x_np), requires_grad=False, name="images")
+    t = mf.Variable(gpu(t_np), requires_grad=False, name="targets")
+    out = model(x)
+    loss = mf.MSELoss(out, t)
+    graph = mf.Graph(loss)
+    return model, graph, out, loss, x_np, t_np
+
+
+def _oracle_names(base_width):
+    params, _ = oracle_resnet.init_params(base_width=base_width, seed=0)
+    return list(params)
+
+
+@pytest.mark.parametrize("batch,height,width,base_width", [(2, 120, 160, 64), (4, 64, 64, 16)],
+                         ids=("C1-bs2-120x160", "small"))
+def test_resnet18_training_step_matches_numpy_reference(batch, height, width, base_width):
+    print("resnet step", batch, height, width, base_width, flush=True)
+    model, graph, out, loss, x_np, t_np = _build_gpu_resnet(batch, height, width, base_width)
+    opt = mf.Adam(graph, learning_rate=1e-3)
+    opt.one_step()
+    grads = [host(p.grad) for p in model.params]
+    gpu_out, gpu_loss = host(out.value), float(host(loss.value))
+    opt.update()
+    updated = [host(p.value) for p in model.params]
+
+    params32, running32 = oracle_resnet.init_params(base_width=base_width, seed=0)
+    params64, running64 = oracle_resnet.as_dtype(params32, running32, np.float64)
+    loss32, grads32, out32 = oracle_resnet.forward_backward(params32, running32, x_np, t_np)
+    loss64, grads64, out64 = oracle_resnet.forward_backward(params64, running64, x_np.astype(np.float64),
+                                                            t_np.astype(np.float64))
+    names = list(params32)
+    assert abs(gpu_loss - loss64) <= 1e-4 * abs(loss64)
+    assert normwise(gpu_out, out64) <= max(4 * normwise(out32, out64), 1e-5)
+    floor = 1e-5 * max(np.abs(g).max() for g in grads64.values())
+    for name, g in zip(names, grads):
+        ref = grads64[name]
+        err_gpu = np.abs(g - ref).max()
+        err_np = np.abs(grads32[name] - ref).max()
+        assert err_gpu <= 4 * err_np + 1e-5 * np.abs(ref).max() + floor, (name, err_gpu, err_np)
+    # The Adam step of the reference on the GPU gradients reproduces our update bit for bit.
+    for name, p_new, g in zip(names, updated, grads):
+        p = params32[name].copy()
+        m, v = np.zeros_like(p), np.zeros_like(p)
+        rp.adam_update(p, g, m, v, lr=1e-3, beta1=0.9, beta2=0.999, eps=1e-8, step=1)
+        np.testing.assert_allclose(p_new, p, rtol=0, atol=2 * np.spacing(np.abs(p).max()), err_msg=name)
+
+
+def test_resnet18_two_steps_are_deterministic():
+    runs = []
+    for _ in range(2):
+        model, graph, out, loss, _, _ = _build_gpu_resnet(2, 64, 64, base_width=16)
+        opt = mf.Adam(graph, learning_rate=1e-3)
+        for _ in range(2):
+            opt.one_step()
+            opt.update()
+        runs.append([host(p.value) for p in model.params])
+    for a, b in zip(*runs):
+        np.testing.assert_array_equal(a, b)
+
+
+def test_shared_weight_on_two_branches_accumulates():
+    rng = np.random.default_rng(9)
+    x_np = rng.standard_normal((2, 3, 10, 12)).astype(np.float32)
+    w_np = rng.standard_normal((4, 3, 3, 3)).astype(np.float32)
+    x = mf.Variable(gpu(x_np), requires_grad=False)
+    w = mf.Variable(gpu(w_np), trainable=True)
+    a = mf.Conv2D_Op(x, w, stride=1, padding=1, backend="hip_native")
+    b = mf.Conv2D_Op(x, w, stride=2, padding=0, backend="hip_native")
+    t1 = mf.Variable(torch.zeros((2, 4, 10, 12), device="cuda"), requires_grad=False)
+    t2 = mf.Variable(torch.zeros((2, 4, 4, 5), device="cuda"), requires_grad=False)
+    loss = mf.Add(mf.MSELoss(a, t1), mf.MSELoss(b, t2))
+    graph = mf.Graph(loss)
+    graph.forward()
+    graph.backward()
+    ya = naive.conv_forward(x_np.astype(np.float64), w_np.astype(np.float64), (1, 1), (1, 1))
+    yb = naive.conv_forward(x_np.astype(np.float64), w_np.astype(np.float64), (2, 2), (0, 0))
+    _, gwa = naive.conv_backward(x_np.astype(np.float64), w_np.astype(np.float64), 2 * ya / ya.size, (1, 1), (1, 1))
+    _, gwb = naive.conv_backward(x_np.astype(np.float64), w_np.astype(np.float64), 2 * yb / yb.size, (2, 2), (0, 0))
+    assert_near(host(w.grad), gwa + gwb, 1e-5, "shared dW")
