@@ -45,6 +45,21 @@ METRIC = "ResNet18 FP32 train images/s (bs64, 3×120×160); GEMM TFLOP/s vs FP32
 # Algorithmic work of one bs64 training step: 3x the forward conv + fc MACs minus the skipped stem
 # dX, 4.138 GFLOP per image.
 STEP_GFLOP = 264.85
+# HBM bytes per launch of the roofline GEMM, from the FETCH_SIZE / WRITE_SIZE counter runs recorded
+# in this summary (each counter scaled by what it reads for a copy kernel of known size).
+TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "gemm_mfma_4096_nn.md")
+
+
+def profiled_traffic(path=TRAFFIC_PROFILE):
+    """The "traffic_bytes_per_launch:" figure of a committed rocprofv3 summary, or None."""
+    try:
+        with open(path, encoding="utf-8") as handle:
+            for line in handle:
+                if line.startswith("traffic_bytes_per_launch:"):
+                    return int(line.split(":", 1)[1])
+    except OSError:
+        pass
+    return None
 
 
 def build_step(batch, height, width, seed=0):
@@ -92,8 +107,13 @@ def gemm_roofline(m=4096, n=4096, k=4096, reps=20):
     ms = start.elapsed_time(end) / reps
     achieved = 2.0 * m * n * k / (ms * 1e-3) / 1e12
     tile, slices = native.gemm_plan(m, n, k)
+    # A plain streaming kernel of known size (read 256 MiB, write 256 MiB): the calibration that
+    # FETCH_SIZE / WRITE_SIZE counter runs divide by to turn counter units into HBM bytes.
+    src = torch.empty((64 << 20,), device="cuda").fill_(1.0)
+    torch.neg(src, out=torch.empty_like(src))
+    torch.cuda.synchronize()
     return {"bound": "mfma", "achieved": round(achieved, 2), "peak": FP32_MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
-            "frac": round(achieved / FP32_MFMA_PEAK_TFLOPS, 4), "traffic": None,
+            "frac": round(achieved / FP32_MFMA_PEAK_TFLOPS, 4), "traffic": profiled_traffic(),
             "kernel": f"gemm_mfma_kernel NN {m}x{n}x{k} tile {tile} slices {slices}",
             "avg_launch_ms": round(ms, 4), "algorithmic_flop_per_launch": 2 * m * n * k}
 
