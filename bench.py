@@ -1,10 +1,12 @@
 """Benchmark of the hip_native hot path on one MI355X.
 
 Workload: one ResNet18(output_dim=2) training step with Adam through the
-Variable/Graph API, every convolution, the stem max-pool and the fc Linear on libmfhip; batch 64,
-input 3x120x160 ~ N(0, 1), targets ~ U(-1, 1), MSE loss, Kaiming weights from seed 0 (synthetic
-data, random-init weights of the reference architecture). ``value`` is images per second over the
-timed steps.
+Variable/Graph API, every convolution, the stem max-pool, the fc Linear, batch norm, ReLU and Adam
+on libmfhip; batch 64, input 3x120x160 ~ N(0, 1), targets ~ U(-1, 1), MSE loss, Kaiming weights
+from seed 0 (synthetic data, random-init weights of the reference architecture). The graph is built
+with Graph(optimize=True), which runs BN+ReLU and BN+Add+ReLU as single units (--plain-graph keeps
+them as separate nodes, as the reference's own training task does). ``value`` is images per second
+over the timed steps.
 
 ``roofline`` is the FP32 MFMA GEMM engine on the 4096^3 GEMM of BASELINE config 2 (the metric's
 "GEMM TFLOP/s vs FP32 peak"): algorithmic 2*M*N*K flop per launch divided by the average launch
@@ -12,7 +14,7 @@ time measured with HIP events on the launch stream, against the 157.3 TFLOP/s FP
 ``cpu_baseline`` is the NumPy restatement of the reference CPU path (oracle/resnet.py) timed on this
 host on a bounded sample: full forward + backward + Adam steps of ResNet18 at batch 2 (config 1).
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline] [--plain-graph]
 """
 
 from __future__ import annotations
@@ -62,7 +64,7 @@ def profiled_traffic(path=TRAFFIC_PROFILE):
     return None
 
 
-def build_step(batch, height, width, seed=0):
+def build_step(batch, height, width, seed=0, optimize=True):
     model = mf.ResNet18(output_dim=2, initializer=mf.make_initializer(seed=seed), conv_backend="hip_native")
     rng = np.random.default_rng(seed)
     x_np = rng.standard_normal((batch, 3, height, width)).astype(np.float32)
@@ -70,7 +72,7 @@ def build_step(batch, height, width, seed=0):
     x = mf.Variable(torch.as_tensor(x_np, device="cuda"), requires_grad=False, name="images")
     t = mf.Variable(torch.as_tensor(t_np, device="cuda"), requires_grad=False, name="targets")
     loss = mf.MSELoss(model(x), t)
-    graph = mf.Graph(loss)
+    graph = mf.Graph(loss, optimize=optimize)
     return mf.Adam(graph, learning_rate=1e-3), loss
 
 
@@ -153,6 +155,8 @@ def main():
     parser.add_argument("--warmup", type=int, default=3)
     parser.add_argument("--batch", type=int, default=64)
     parser.add_argument("--no-cpu-baseline", action="store_true")
+    parser.add_argument("--plain-graph", action="store_true",
+                        help="Graph(optimize=False): BN, Add and ReLU as separate nodes (the reference task's graph)")
     args = parser.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU: this build runs no multi-GPU path (use --gpus 1)", file=sys.stderr)
@@ -162,7 +166,7 @@ def main():
         return 2
     torch.cuda.set_device(0)
     native._library()
-    opt, _ = build_step(args.batch, 120, 160)
+    opt, _ = build_step(args.batch, 120, 160, optimize=not args.plain_graph)
     seconds = time_steps(opt, args.steps, args.warmup)
     ms_per_step = seconds * 1e3 / args.steps
     images_per_s = args.batch * args.steps / seconds
@@ -172,7 +176,8 @@ def main():
         "warmup": args.warmup, "ms_per_step": round(ms_per_step, 3), "higher_is_better": True, "scaling": "weak",
         "vs_baseline": None, "dtype": "f32", "data": "synthetic",
         "config": {"workload": "ResNet18(output_dim=2) train step (fwd+bwd+Adam), hip_native backend",
-                   "global_batch": args.batch, "input": [3, 120, 160], "loss": "MSE"},
+                   "global_batch": args.batch, "input": [3, 120, 160], "loss": "MSE",
+                   "graph": "optimize=False" if args.plain_graph else "optimize=True (BN+ReLU, BN+Add+ReLU units)"},
         "step_tflops": round(STEP_GFLOP * args.batch / 64 / (ms_per_step * 1e-3) / 1e3, 2),
         "roofline": roofline,
     }

@@ -1,23 +1,24 @@
 /*
  * libmfhip: the MI355X (gfx950) native library behind MyFlows' convolution / GEMM / max-pool hot
- * path. It replaces the NVRTC + cuBLAS scheduler of the reference (`ops/cuda_native/native_cublas.cpp`)
- * behind the same calling conventions:
+ * path and the batch-norm, ReLU and Adam kernels of the training step around it. It replaces the
+ * NVRTC + cuBLAS scheduler of the reference (ops/cuda_native/native_cublas.cpp) and the CuPy
+ * kernels of ops/fused.py behind the same calling conventions:
  *
- *   - every device buffer is a `uint64_t` device address owned by the caller (PyTorch here, CuPy in
+ *   - every device buffer is a uint64_t device address owned by the caller (PyTorch here, CuPy in
  *     the reference); the library never allocates device memory;
  *   - a null optional pointer means "not requested";
- *   - dimensions are `int`, the stream is a `uint64_t` hipStream_t handle (0 = null stream);
+ *   - dimensions are int, the stream is a uint64_t hipStream_t handle (0 = null stream);
  *   - launches are asynchronous on that stream; nothing synchronises unless debug sync is on
- *     (`mfh_set_debug_sync(1)` or `MFHIP_SYNC=1`);
+ *     (mfh_set_debug_sync(1) or MFHIP_SYNC=1);
  *   - every entry point returns a status: 0 OK, 1 initialisation failed, 2 invalid argument,
  *     3 HIP runtime error, 5 called on another device than mfh_init's (4 is unused; it was the
- *     cuBLAS status of the reference). The detail is this thread's `mfh_last_error()`, of the form
+ *     cuBLAS status of the reference). The detail is this thread's mfh_last_error(), of the form
  *     "<file>:<line>: <reason>".
  *
  * Kernels index buffers with int32 offsets; entry points reject problems whose buffers exceed
  * 2^31 - 1 elements.
  *
- * GEMM engine codes (`engine` arguments): 1 = the FP32 MFMA engine with its automatic tile and
+ * GEMM engine codes (engine arguments): 1 = the FP32 MFMA engine with its automatic tile and
  * split-K plan; 16 + tile * 128 + (slices - 1) = an explicit plan (tile index of
  * mfh_gemm_tile_info, 1..128 K slices). The reference's engine 0 (cuBLAS) does not exist here.
  */
@@ -31,6 +32,8 @@ extern "C" {
 #endif
 
 #define MFH_API __attribute__((visibility("default")))
+
+/* ---- library -------------------------------------------------------------------------------- */
 
 /* One-time initialisation on the current HIP device: checks that the device is gfx950, that the
  * embedded code objects load, reads the CU count and the MFHIP_SYNC flag.
@@ -49,31 +52,42 @@ MFH_API const char* mfh_info(void);
  * Replaces mf_set_debug_sync, native_cublas.cpp:1421-1423. */
 MFH_API void mfh_set_debug_sync(int enabled);
 
+/* ---- convolution ---------------------------------------------------------------------------- */
+
 /* cols (N*OH*OW, CI*KH*KW) = im2col(x), zero outside the padded input.
  * Replaces mf_conv_im2col, native_cublas.cpp:1430-1438. */
 MFH_API int mfh_conv_im2col(uint64_t x, uint64_t cols, int N, int CI, int H, int W, int CO, int KH, int KW, int OH,
                             int OW, int SH, int SW, int PH, int PW, uint64_t stream);
 
-/* y (N,CO,OH,OW) = act(conv(x, weight) + bias) through cols = im2col(x), rows = cols weight^T
- * (GEMM engine `engine`), then the NCHW epilogue. activation: 0 none, 1 ReLU, 2 LeakyReLU(alpha > 0).
- * bias may be 0. workspace (workspace_floats floats, may be 0) enables split-K.
+/* y (N,CO,OH,OW) = act(conv(x, weight) + bias). cols receives im2col(x) (kept by the caller for
+ * dW). With rows == 0 each image's output is one GEMM W cols_n^T written straight into NCHW with
+ * bias and activation in its epilogue; with rows (N*OH*OW x CO floats) given, rows = cols W^T is
+ * formed first and an epilogue kernel transposes it. activation: 0 none, 1 ReLU,
+ * 2 LeakyReLU(alpha > 0). bias may be 0. workspace (workspace_floats floats, may be 0) lets the
+ * rows GEMM split K.
  * Replaces mf_conv_forward, native_cublas.cpp:1441-1461. */
 MFH_API int mfh_conv_forward(uint64_t x, uint64_t weight, uint64_t bias, uint64_t cols, uint64_t rows, uint64_t y,
                              int N, int CI, int H, int W, int CO, int KH, int KW, int OH, int OW, int SH, int SW,
                              int PH, int PW, int activation, float alpha, int engine, uint64_t workspace,
                              int64_t workspace_floats, uint64_t stream);
 
-/* Backward of mfh_conv_forward. dyT (N*OH*OW, CO) = gate(dy) transposed, with per-block FP64 bias
- * partials in `partial` (N * grid_x * CO doubles, grid_x in [1, ceil(OH*OW / 64)]); db = in-order
- * FP64 sum of the partials; dw (CO, CI*KH*KW) = dyT^T cols on dw_engine; grad_cols = dyT weight on
- * dx_engine; dx = col2im(grad_cols). dx/grad_cols and partial/db are given together or not at all;
- * dw needs cols and dyT. With dx as the only output the gated NCHW dy is read directly per image.
+/* Backward of mfh_conv_forward. dy is gated by the fused activation through the forward output y.
+ *   db   = FP64 sum of dy per channel: per-tile FP64 partials in `partial` (N * grid_x * CO
+ *          doubles, grid_x in [1, ceil(OH*OW / 64)]) reduced in a fixed order;
+ *   dw   (CO, CI*KH*KW) = dyT^T cols, dyT (N*OH*OW x CO) being the gated, transposed dy (split-K on
+ *          dw_engine through the workspace);
+ *   dx   = col2im of grad_cols, where grad_cols (N*OH*OW*CI*KH*KW floats) receives, per image, the
+ *          transposed column gradient W^T dy_n (CI*KH*KW x OH*OW) on dx_engine.
+ * dx/grad_cols and partial/db are given together or not at all; dw needs cols and dyT; dx through
+ * an activation needs dyT.
  * Replaces mf_conv_backward_plans / mf_conv_backward, native_cublas.cpp:1465-1532. */
 MFH_API int mfh_conv_backward(uint64_t weight, uint64_t dy, uint64_t y, uint64_t cols, uint64_t dyT, uint64_t dw,
                               uint64_t grad_cols, uint64_t dx, uint64_t partial, uint64_t db, int N, int CI, int H,
                               int W, int CO, int KH, int KW, int OH, int OW, int SH, int SW, int PH, int PW,
                               int grid_x, int activation, float alpha, int dw_engine, int dx_engine,
                               uint64_t workspace, int64_t workspace_floats, uint64_t stream);
+
+/* ---- max pooling ---------------------------------------------------------------------------- */
 
 /* Max-pool without padding (the caller pads with -inf): y = window max in (kh, kw) order with the
  * first maximum winning ties and NaN taking over; argmax (int32) = flat index into x.
@@ -86,7 +100,9 @@ MFH_API int mfh_pool_forward(uint64_t x, uint64_t y, uint64_t argmax, int N, int
 MFH_API int mfh_pool_backward(uint64_t dy, uint64_t argmax, uint64_t dx, int N, int C, int H, int W, int OH, int OW,
                               int KH, int KW, int SH, int SW, uint64_t stream);
 
-/* C(M,N) = A(M,K) B(K,N) [+ bias(N)], row-major, with a lecture kernel. variant: 0 basic, 1 tiled,
+/* ---- GEMM ----------------------------------------------------------------------------------- */
+
+/* C(M,N) = A(M,K) B(K,N) [+ bias(N)], row-major, with a teaching kernel. variant: 0 basic, 1 tiled,
  * 2 shared, 4 register (3, cuBLAS in the reference, is rejected); tile 16/32 for variants 1-2;
  * accumulate: 0 fp32, 1 Kahan-grouped, 2 Dot2. variant 4 with accumulate 0 runs the MFMA engine.
  * Replaces mf_matmul, native_cublas.cpp:1567-1613. */
@@ -120,6 +136,63 @@ MFH_API int mfh_split_reduce(uint64_t partial, uint64_t c, int slices, int M, in
 MFH_API int mfh_gemm(int engine, int trans_a, int trans_b, uint64_t a, uint64_t b, uint64_t bias, uint64_t c, int M,
                      int N, int K, int lda, int ldb, int ldc, uint64_t workspace, int64_t workspace_floats,
                      uint64_t stream);
+
+/* ---- batch normalisation (+ residual add + ReLU) -------------------------------------------- */
+
+/* FP64 workspace (doubles) that mfh_bn_forward (training) and mfh_bn_backward need for an NCHW
+ * tensor of N x C x HW elements; -1 on error. No reference counterpart: the reference sizes its
+ * partial buffer inline (ops/fused.py:238-243, 265-266). */
+MFH_API int64_t mfh_bn_workspace(int N, int C, int HW);
+
+/* Batch norm of x (N, C, HW) per channel. Training: FP64 batch mean / biased variance, mean stored
+ * as the float pair mean[c] + mean[C + c], inv_std[c] = 1 / sqrt(var + eps) rounded once, running
+ * statistics updated with momentum (the variance scaled by var_scale). Eval: running statistics.
+ * y = (((x - mean_hi) - mean_lo) * inv_std) * gamma + beta, then + residual (optional), then ReLU
+ * when relu != 0, each operation rounded to float32.
+ * Replaces batchnorm2d_forward, ops/fused.py:250-305 (and the BatchNormActivation forward of
+ * ops/batchnorm.py:75-94). */
+MFH_API int mfh_bn_forward(uint64_t x, uint64_t gamma, uint64_t beta, uint64_t running_mean, uint64_t running_var,
+                           uint64_t residual, uint64_t y, uint64_t mean, uint64_t inv_std, uint64_t workspace,
+                           int64_t workspace_doubles, int N, int C, int HW, int training, int relu, double momentum,
+                           double eps, double var_scale, uint64_t stream);
+
+/* Gradients of mfh_bn_forward. g = dy, or dy where gate > 0 and 0 elsewhere when gate (the fused
+ * ReLU's output) is given; residual_grad (optional, needs gate) receives g. dgamma / dbeta are
+ * FP64 sums; x_grad = a * ((g - k1) - ((x - mean_hi) - mean_lo) * k2) in training,
+ * a * g in eval, with a = gamma * inv_std, k1 = sum(g) / count, k2 = inv_std * dgamma / count.
+ * Each output is stored, or added when its add_* flag is set.
+ * Replaces batchnorm2d_backward, ops/fused.py:308-380. */
+MFH_API int mfh_bn_backward(uint64_t x, uint64_t dy, uint64_t gate, uint64_t gamma, uint64_t mean, uint64_t inv_std,
+                            uint64_t x_grad, uint64_t gamma_grad, uint64_t beta_grad, uint64_t residual_grad,
+                            uint64_t workspace, int64_t workspace_doubles, int N, int C, int HW, int training,
+                            int add_x, int add_gamma, int add_beta, int add_residual, uint64_t stream);
+
+/* ---- activations and the optimiser ---------------------------------------------------------- */
+
+/* y = max(0, x) over count elements (NaN stays NaN).
+ * Replaces the forward of ReLU, ops/activation.py:43-48. */
+MFH_API int mfh_relu_forward(uint64_t x, uint64_t y, int64_t count, uint64_t stream);
+
+/* out = (x > 0 ? grad : alpha * grad), or out += that when add != 0 (alpha = 0: ReLU).
+ * Replaces relu_backward_accumulate / leaky_relu_backward_accumulate, ops/fused.py:50-77. */
+MFH_API int mfh_relu_backward(uint64_t x, uint64_t grad, uint64_t out, int64_t count, float alpha, int add,
+                              uint64_t stream);
+
+/* One tensor of an Adam step: parameter, gradient and moments (size floats each, contiguous), the
+ * learning rate, the weight decay and the bias corrections 1 - beta1^step, 1 - beta2^step, all
+ * rounded to float32. */
+typedef struct mfh_adam_tensor {
+    uint64_t param, grad, m, v;
+    int64_t size;
+    float lr, weight_decay, bias_correction1, bias_correction2;
+} mfh_adam_tensor;
+
+/* Adam over `count` tensors (the table is host memory, read during the call):
+ * m = b1 m + (1 - b1) gs; v = b2 v + (1 - b2) gs^2; p -= (lr (m / bc1)) / (sqrt(v / bc2) + eps),
+ * gs = g * grad_scale (+ weight_decay * p), every operation rounded to float32 in that order.
+ * Replaces adam_update / adam_update_many, ops/fused.py:514-533 and 609-621. */
+MFH_API int mfh_adam_step(const mfh_adam_tensor* tensors, int count, float grad_scale, float beta1,
+                          float one_minus_beta1, float beta2, float one_minus_beta2, float eps, uint64_t stream);
 
 #ifdef __cplusplus
 }

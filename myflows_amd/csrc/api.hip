@@ -1,12 +1,11 @@
 // The C ABI of libmfhip (declared in include/mfhip.h): initialisation, error reporting, argument
-// validation and the launch sequences of the convolution, pooling, GEMM and matmul entry points.
-// Validation follows the reference scheduler (ops/cuda_native/native_cublas.cpp:1379-1409 and the
-// MF_REQUIRE checks of its entry points) so that the same bad calls fail with status 2 and a message
-// naming the reason.
+// validation, and the launch sequences behind each entry point. Invalid calls return status 2 with
+// a message naming the reason, before anything is launched.
 #include <chrono>
 #include <cstdio>
 #include <cstdlib>
 #include <mutex>
+#include <vector>
 
 #include "../../include/mfhip.h"
 #include "common.h"
@@ -14,52 +13,68 @@
 namespace mfh {
 namespace {
 
-std::mutex init_mutex;
-bool initialized = false;
-bool debug_sync = false;
-int init_device = -1;
-int cu_count = 0;
-std::string info_text = "{}";
-thread_local std::string last_error;
-
-int check_ready() {
-    if (!initialized) return MFH_FAIL(ERR_INIT, "mfh_init has not succeeded");
+struct LibraryState {
+    std::mutex lock;
+    bool ready = false;
+    bool sync_each_launch = false;
     int device = -1;
-    const hipError_t status = hipGetDevice(&device);
-    if (status != hipSuccess) return MFH_FAIL(ERR_HIP, std::string("hipGetDevice: ") + hipGetErrorString(status));
-    if (device != init_device) return MFH_FAIL(ERR_DEVICE, "called on a different HIP device than the one used by mfh_init");
+    int cus = 0;
+    std::string info = "{}";
+};
+
+LibraryState& state() {
+    static LibraryState s;
+    return s;
+}
+
+thread_local std::string error_text;
+
+template <typename T>
+T* as_ptr(std::uint64_t address) {
+    return reinterpret_cast<T*>(static_cast<std::uintptr_t>(address));
+}
+
+hipStream_t as_stream(std::uint64_t handle) { return reinterpret_cast<hipStream_t>(static_cast<std::uintptr_t>(handle)); }
+
+int require_ready() {
+    LibraryState& s = state();
+    if (!s.ready) return MFH_FAIL(ERR_INIT, "mfh_init has not succeeded");
+    int device = -1;
+    const hipError_t rc = hipGetDevice(&device);
+    if (rc != hipSuccess) return MFH_FAIL(ERR_HIP, std::string("hipGetDevice: ") + hipGetErrorString(rc));
+    if (device != s.device) return MFH_FAIL(ERR_DEVICE, "called on a different HIP device than the one mfh_init used");
     return OK;
 }
 
-int check_conv(const ConvDims& d) {
-    const bool positive = d.N > 0 && d.CI > 0 && d.H > 0 && d.W > 0 && d.CO > 0 && d.KH > 0 && d.KW > 0 && d.OH > 0 &&
-                          d.OW > 0 && d.SH > 0 && d.SW > 0 && d.PH >= 0 && d.PW >= 0;
-    if (!positive) return MFH_FAIL(ERR_ARG, "convolution dimensions must be positive");
-    if (d.OH != (d.H + 2 * d.PH - d.KH) / d.SH + 1 || d.OW != (d.W + 2 * d.PW - d.KW) / d.SW + 1)
-        return MFH_FAIL(ERR_ARG, "convolution output size does not match input, kernel, stride and padding");
-    const std::int64_t rows = static_cast<std::int64_t>(d.N) * d.OH * d.OW;
-    const std::int64_t features = static_cast<std::int64_t>(d.CI) * d.KH * d.KW;
-    if (!fits_index(rows * features) || !fits_index(rows * d.CO) ||
-        !fits_index(static_cast<std::int64_t>(d.N) * d.CI * d.H * d.W) || !fits_index(features * d.CO))
-        return MFH_FAIL(ERR_ARG, "convolution buffers exceed the int32 indexing limit");
-    if (static_cast<unsigned>(d.N) > GRID_YZ_LIMIT || blocks_for(d.CO, conv_grad_tile()) > GRID_YZ_LIMIT)
-        return MFH_FAIL(ERR_ARG, "batch or channel count exceeds the grid limit");
+int validate(const ConvGeometry& g) {
+    const bool positive = g.N > 0 && g.CI > 0 && g.H > 0 && g.W > 0 && g.CO > 0 && g.KH > 0 && g.KW > 0 && g.OH > 0 &&
+                          g.OW > 0 && g.SH > 0 && g.SW > 0 && g.PH >= 0 && g.PW >= 0;
+    MFH_REQUIRE(positive, "convolution dimensions must be positive");
+    MFH_REQUIRE(g.OH == (g.H + 2 * g.PH - g.KH) / g.SH + 1 && g.OW == (g.W + 2 * g.PW - g.KW) / g.SW + 1,
+                "convolution output size does not match input, kernel, stride and padding");
+    const std::int64_t m = static_cast<std::int64_t>(g.N) * g.OH * g.OW;
+    const std::int64_t k = static_cast<std::int64_t>(g.CI) * g.KH * g.KW;
+    MFH_REQUIRE(fits_index(m * k) && fits_index(m * g.CO) && fits_index(static_cast<std::int64_t>(g.N) * g.CI * g.H * g.W) &&
+                    fits_index(k * g.CO),
+                "convolution buffers exceed the int32 indexing limit");
+    MFH_REQUIRE(static_cast<unsigned>(g.N) <= GRID_YZ_LIMIT && blocks_for(g.CO, conv_grad_tile()) <= GRID_YZ_LIMIT,
+                "batch or channel count exceeds the grid limit");
     return OK;
 }
 
-int check_activation(int activation, float alpha) {
-    if (activation != ACT_NONE && activation != ACT_RELU && activation != ACT_LEAKY_RELU)
-        return MFH_FAIL(ERR_ARG, "unknown activation code");
-    if (activation == ACT_LEAKY_RELU && !(alpha > 0.0f)) return MFH_FAIL(ERR_ARG, "fused LeakyReLU requires alpha > 0");
+int validate_activation(int activation, float alpha) {
+    MFH_REQUIRE(activation == ACT_NONE || activation == ACT_RELU || activation == ACT_LEAKY_RELU,
+                "unknown activation code");
+    MFH_REQUIRE(activation != ACT_LEAKY_RELU || alpha > 0.0f, "fused LeakyReLU requires alpha > 0");
     return OK;
 }
 
-int check_engine(int engine) {
-    if (!gemm_engine_valid(engine)) return MFH_FAIL(ERR_ARG, "unknown GEMM engine or plan code");
+int validate_engine(int engine) {
+    MFH_REQUIRE(gemm_engine_valid(engine), "unknown GEMM engine or plan code");
     return OK;
 }
 
-int check_pool(int N, int C, int H, int W, int OH, int OW, int KH, int KW, int SH, int SW) {
+int validate_pool(int N, int C, int H, int W, int OH, int OW, int KH, int KW, int SH, int SW) {
     MFH_REQUIRE(N > 0 && C > 0 && H > 0 && W > 0 && OH > 0 && OW > 0 && KH > 0 && KW > 0 && SH > 0 && SW > 0,
                 "pooling dimensions must be positive");
     MFH_REQUIRE(OH == (H - KH) / SH + 1 && OW == (W - KW) / SW + 1, "pooling output size does not match the input");
@@ -67,17 +82,46 @@ int check_pool(int N, int C, int H, int W, int OH, int OW, int KH, int KW, int S
     return OK;
 }
 
-template <typename T>
-T* ptr(std::uint64_t address) {
-    return reinterpret_cast<T*>(static_cast<std::uintptr_t>(address));
+int validate_norm(const NormShape& s) {
+    MFH_REQUIRE(s.N > 0 && s.C > 0 && s.HW > 0, "batch-norm dimensions must be positive");
+    MFH_REQUIRE(fits_index(static_cast<std::int64_t>(s.N) * s.C * s.HW), "batch-norm tensor exceeds int32 indexing");
+    MFH_REQUIRE(static_cast<unsigned>(s.C) <= GRID_YZ_LIMIT, "batch-norm channel count exceeds the grid limit");
+    return OK;
 }
 
-hipStream_t as_stream(std::uint64_t handle) { return reinterpret_cast<hipStream_t>(static_cast<std::uintptr_t>(handle)); }
+// The per-image column-gradient GEMM of dX: gcT[n] (K x OHW) = W^T dy_n, with dy_n read either from
+// the NCHW gradient (CO x OHW per image) or from its transposed rows dyT (OHW x CO per image).
+int column_gradient(int engine, const ConvGeometry& g, const float* weight, const float* dy_nchw, const float* dyT,
+                    float* gcT, hipStream_t stream) {
+    const int K = g.features(), ohw = g.ohw();
+    GemmOperands o{};
+    o.trans_a = true;  // W stored CO x K
+    o.M = K;
+    o.N = ohw;
+    o.K = g.CO;
+    o.a = weight;
+    o.lda = K;
+    if (dyT) {
+        o.trans_b = true;  // dyT_n stored OHW x CO
+        o.b = dyT;
+        o.ldb = g.CO;
+    } else {
+        o.trans_b = false;  // dy_n stored CO x OHW
+        o.b = dy_nchw;
+        o.ldb = ohw;
+    }
+    o.c = gcT;
+    o.ldc = ohw;
+    o.batch = g.N;
+    o.b_batch = static_cast<long long>(g.CO) * ohw;
+    o.c_batch = static_cast<long long>(K) * ohw;
+    return gemm_launch(engine, stream, o, GemmEpilogue{}, nullptr, 0);
+}
 
 }  // namespace
 
 int fail(int status, const char* file, int line, const std::string& what) {
-    last_error = std::string(file) + ":" + std::to_string(line) + ": " + what;
+    error_text = std::string(file) + ":" + std::to_string(line) + ": " + what;
     return status;
 }
 
@@ -85,7 +129,7 @@ int after_launch(const char* kernel, hipStream_t stream, const char* file, int l
     const hipError_t launched = hipGetLastError();
     if (launched != hipSuccess)
         return fail(ERR_HIP, file, line, std::string("launch ") + kernel + ": " + hipGetErrorString(launched));
-    if (debug_sync) {
+    if (state().sync_each_launch) {
         const hipError_t synced = hipStreamSynchronize(stream);
         if (synced != hipSuccess)
             return fail(ERR_HIP, file, line, std::string("after kernel ") + kernel + ": " + hipGetErrorString(synced));
@@ -93,8 +137,8 @@ int after_launch(const char* kernel, hipStream_t stream, const char* file, int l
     return OK;
 }
 
-bool debug_sync_enabled() { return debug_sync; }
-int device_cu_count() { return cu_count; }
+bool debug_sync_enabled() { return state().sync_each_launch; }
+int device_cu_count() { return state().cus; }
 
 }  // namespace mfh
 
@@ -102,73 +146,106 @@ using namespace mfh;
 
 extern "C" {
 
-MFH_API const char* mfh_last_error(void) { return last_error.c_str(); }
+MFH_API const char* mfh_last_error(void) { return error_text.c_str(); }
 
-MFH_API const char* mfh_info(void) { return info_text.c_str(); }
+MFH_API const char* mfh_info(void) { return state().info.c_str(); }
 
-MFH_API void mfh_set_debug_sync(int enabled) { debug_sync = enabled != 0; }
+MFH_API void mfh_set_debug_sync(int enabled) { state().sync_each_launch = enabled != 0; }
 
 MFH_API int mfh_init(void) {
-    std::lock_guard<std::mutex> lock(init_mutex);
-    if (initialized) return OK;
-    const auto start = std::chrono::steady_clock::now();
+    LibraryState& s = state();
+    std::lock_guard<std::mutex> guard(s.lock);
+    if (s.ready) return OK;
+    const auto t0 = std::chrono::steady_clock::now();
     int device = -1;
-    hipError_t status = hipGetDevice(&device);
-    if (status != hipSuccess) return MFH_FAIL(ERR_INIT, std::string("hipGetDevice: ") + hipGetErrorString(status));
+    hipError_t rc = hipGetDevice(&device);
+    if (rc != hipSuccess) return MFH_FAIL(ERR_INIT, std::string("hipGetDevice: ") + hipGetErrorString(rc));
     hipDeviceProp_t props;
-    status = hipGetDeviceProperties(&props, device);
-    if (status != hipSuccess)
-        return MFH_FAIL(ERR_INIT, std::string("hipGetDeviceProperties: ") + hipGetErrorString(status));
+    rc = hipGetDeviceProperties(&props, device);
+    if (rc != hipSuccess) return MFH_FAIL(ERR_INIT, std::string("hipGetDeviceProperties: ") + hipGetErrorString(rc));
     const std::string arch = props.gcnArchName;
     if (arch.rfind("gfx950", 0) != 0)
         return MFH_FAIL(ERR_INIT, "libmfhip is built for gfx950 only; the current device is " + arch);
-    MFH_TRY(conv_probe_kernels());
-    const char* sync_flag = std::getenv("MFHIP_SYNC");
-    if (sync_flag && sync_flag[0] && sync_flag[0] != '0') debug_sync = true;
+    MFH_TRY(probe_code_object());
+    const char* flag = std::getenv("MFHIP_SYNC");
+    if (flag && flag[0] && flag[0] != '0') s.sync_each_launch = true;
     int runtime = 0;
     hipRuntimeGetVersion(&runtime);
-    cu_count = props.multiProcessorCount;
-    init_device = device;
-    const double load_ms =
-        std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - start).count();
-    char info[512];
-    std::snprintf(info, sizeof(info),
+    s.cus = props.multiProcessorCount;
+    s.device = device;
+    const double ms = std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0).count();
+    char text[512];
+    std::snprintf(text, sizeof(text),
                   "{\"device_arch\": \"%s\", \"device_name\": \"%s\", \"device\": %d, \"cu_count\": %d, "
                   "\"binary\": \"hsaco\", \"offload_arch\": \"gfx950\", \"hip_runtime\": %d, \"load_ms\": %.3f, "
                   "\"lds_bytes_per_block\": %zu}",
-                  arch.c_str(), props.name, device, cu_count, runtime, load_ms, props.sharedMemPerBlock);
-    info_text = info;
-    initialized = true;
+                  arch.c_str(), props.name, device, s.cus, runtime, ms, props.sharedMemPerBlock);
+    s.info = text;
+    s.ready = true;
     return OK;
 }
 
 MFH_API int mfh_conv_im2col(std::uint64_t x, std::uint64_t cols, int N, int CI, int H, int W, int CO, int KH, int KW,
                             int OH, int OW, int SH, int SW, int PH, int PW, std::uint64_t stream) {
-    MFH_TRY(check_ready());
-    const ConvDims d{N, CI, H, W, CO, KH, KW, OH, OW, SH, SW, PH, PW};
-    MFH_TRY(check_conv(d));
-    MFH_REQUIRE(x && cols, "im2col requires input and output buffers");
-    return launch_im2col(ptr<const float>(x), ptr<float>(cols), d, as_stream(stream));
+    MFH_TRY(require_ready());
+    const ConvGeometry g{N, CI, H, W, CO, KH, KW, OH, OW, SH, SW, PH, PW};
+    MFH_TRY(validate(g));
+    MFH_REQUIRE(x && cols, "im2col needs input and output buffers");
+    return launch_im2col(as_ptr<const float>(x), as_ptr<float>(cols), g, as_stream(stream));
 }
 
 MFH_API int mfh_conv_forward(std::uint64_t x, std::uint64_t weight, std::uint64_t bias, std::uint64_t cols,
                              std::uint64_t rows, std::uint64_t y, int N, int CI, int H, int W, int CO, int KH, int KW,
                              int OH, int OW, int SH, int SW, int PH, int PW, int activation, float alpha, int engine,
                              std::uint64_t workspace, std::int64_t workspace_floats, std::uint64_t stream) {
-    MFH_TRY(check_ready());
-    const ConvDims d{N, CI, H, W, CO, KH, KW, OH, OW, SH, SW, PH, PW};
-    MFH_TRY(check_conv(d));
-    MFH_TRY(check_activation(activation, alpha));
-    MFH_TRY(check_engine(engine));
-    MFH_REQUIRE(x && weight && cols && rows && y, "conv forward received a null buffer");
+    MFH_TRY(require_ready());
+    const ConvGeometry g{N, CI, H, W, CO, KH, KW, OH, OW, SH, SW, PH, PW};
+    MFH_TRY(validate(g));
+    MFH_TRY(validate_activation(activation, alpha));
+    MFH_TRY(validate_engine(engine));
+    MFH_REQUIRE(x && weight && cols && y, "conv forward received a null buffer");
     MFH_REQUIRE(workspace_floats >= 0, "workspace size must be non-negative");
     const hipStream_t s = as_stream(stream);
-    const int M = N * OH * OW, K = CI * KH * KW;
-    MFH_TRY(launch_im2col(ptr<const float>(x), ptr<float>(cols), d, s));
-    MFH_TRY(gemm_rows(engine, s, false, true, M, CO, K, ptr<const float>(cols), K, ptr<const float>(weight), K,
-                      ptr<float>(rows), CO, ptr<float>(workspace), workspace_floats));
-    return launch_conv_epilogue(ptr<const float>(rows), ptr<const float>(bias), ptr<float>(y), N, OH * OW, CO,
-                                activation, alpha, s);
+    const int M = g.rows(), K = g.features(), ohw = g.ohw();
+    MFH_TRY(launch_im2col(as_ptr<const float>(x), as_ptr<float>(cols), g, s));
+    GemmEpilogue e;
+    e.bias = as_ptr<const float>(bias);
+    e.act = activation;
+    e.alpha = alpha;
+    if (rows) {
+        // rows (M x CO) = cols W^T, then the NCHW epilogue kernel (bias + activation).
+        GemmOperands o{};
+        o.trans_b = true;
+        o.M = M;
+        o.N = CO;
+        o.K = K;
+        o.a = as_ptr<const float>(cols);
+        o.lda = K;
+        o.b = as_ptr<const float>(weight);
+        o.ldb = K;
+        o.c = as_ptr<float>(rows);
+        o.ldc = CO;
+        MFH_TRY(gemm_launch(engine, s, o, GemmEpilogue{}, as_ptr<float>(workspace), workspace_floats));
+        return launch_conv_epilogue(as_ptr<const float>(rows), e.bias, as_ptr<float>(y), N, ohw, CO, activation, alpha,
+                                    s);
+    }
+    // Per image, y_n (CO x OHW) = W cols_n^T written straight into NCHW, bias per output row.
+    GemmOperands o{};
+    o.trans_b = true;  // cols_n stored OHW x K
+    o.M = CO;
+    o.N = ohw;
+    o.K = K;
+    o.a = as_ptr<const float>(weight);
+    o.lda = K;
+    o.b = as_ptr<const float>(cols);
+    o.ldb = K;
+    o.c = as_ptr<float>(y);
+    o.ldc = ohw;
+    o.batch = N;
+    o.b_batch = static_cast<long long>(ohw) * K;
+    o.c_batch = static_cast<long long>(CO) * ohw;
+    e.bias_mode = bias ? BIAS_ROW : BIAS_NONE;
+    return gemm_launch(engine, s, o, e, nullptr, 0);
 }
 
 MFH_API int mfh_conv_backward(std::uint64_t weight, std::uint64_t dy, std::uint64_t y, std::uint64_t cols,
@@ -177,93 +254,106 @@ MFH_API int mfh_conv_backward(std::uint64_t weight, std::uint64_t dy, std::uint6
                               int KW, int OH, int OW, int SH, int SW, int PH, int PW, int grid_x, int activation,
                               float alpha, int dw_engine, int dx_engine, std::uint64_t workspace,
                               std::int64_t workspace_floats, std::uint64_t stream) {
-    MFH_TRY(check_ready());
-    const ConvDims d{N, CI, H, W, CO, KH, KW, OH, OW, SH, SW, PH, PW};
-    MFH_TRY(check_conv(d));
-    MFH_TRY(check_activation(activation, alpha));
-    MFH_TRY(check_engine(dw_engine));
-    MFH_TRY(check_engine(dx_engine));
-    const bool direct_dx = dx && !dw && !db;
-    MFH_REQUIRE(weight && dy, "conv backward requires weight and dy");
-    MFH_REQUIRE(!dw || (cols && dyT), "dW requires cols and transposed dy");
-    MFH_REQUIRE(!dx || direct_dx || dyT, "dX requires a gradient matrix");
-    MFH_REQUIRE(!direct_dx || activation == ACT_NONE, "dX-only expects the gated NCHW gradient");
-    MFH_REQUIRE(activation == ACT_NONE || y, "a fused activation needs the forward output");
+    MFH_TRY(require_ready());
+    const ConvGeometry g{N, CI, H, W, CO, KH, KW, OH, OW, SH, SW, PH, PW};
+    MFH_TRY(validate(g));
+    MFH_TRY(validate_activation(activation, alpha));
+    MFH_TRY(validate_engine(dw_engine));
+    MFH_TRY(validate_engine(dx_engine));
+    const bool gated = activation != ACT_NONE;
+    MFH_REQUIRE(weight && dy, "conv backward needs weight and dy");
+    MFH_REQUIRE(!gated || y, "a fused activation needs the forward output");
     MFH_REQUIRE((grad_cols == 0) == (dx == 0), "grad_cols and dx must be given together");
     MFH_REQUIRE((partial == 0) == (db == 0), "partial and db must be given together");
+    MFH_REQUIRE(!dw || (cols && dyT), "dW needs cols and the transposed dy buffer");
+    MFH_REQUIRE(!(dx && gated) || dyT, "dX through a fused activation needs the transposed dy buffer");
     MFH_REQUIRE(workspace_floats >= 0, "workspace size must be non-negative");
-    const int OHW = OH * OW;
-    const int tiles = (OHW + conv_grad_tile() - 1) / conv_grad_tile();
+    const int ohw = g.ohw();
+    const int tiles = (ohw + conv_grad_tile() - 1) / conv_grad_tile();
     MFH_REQUIRE(grid_x > 0 && grid_x <= tiles, "grid_x must be in [1, spatial tiles]");
     MFH_REQUIRE(fits_index(static_cast<std::int64_t>(N) * grid_x * CO), "bias partial buffer exceeds int32 indexing");
     const hipStream_t s = as_stream(stream);
-    const int M = N * OHW, K = CI * KH * KW;
-    float* ws = ptr<float>(workspace);
-    if (dw || db)
-        MFH_TRY(launch_conv_grad_rows(ptr<const float>(dy), ptr<const float>(y), ptr<float>(dyT), ptr<double>(partial), N,
-                                      OHW, CO, grid_x, activation, alpha, s));
-    if (db) MFH_TRY(launch_reduce_partials(ptr<const double>(partial), ptr<float>(db), N * grid_x, CO, s));
-    // dW (CO x K) = dyT^T cols; grad_cols (M x K) = dyT W. Both reuse the workspace in stream order.
-    if (dw)
-        MFH_TRY(gemm_rows(dw_engine, s, true, false, CO, K, M, ptr<const float>(dyT), CO, ptr<const float>(cols), K,
-                          ptr<float>(dw), K, ws, workspace_floats));
-    if (!dx) return OK;
-    if (direct_dx) {
-        // Each NCHW image of dy is a contiguous CO x OHW matrix: read it transposed straight into the
-        // image's slab of grad_cols, without an NHWC copy of dy.
-        for (int n = 0; n < N; ++n) {
-            const float* image = ptr<const float>(dy) + static_cast<std::int64_t>(n) * CO * OHW;
-            float* grad_image = ptr<float>(grad_cols) + static_cast<std::int64_t>(n) * OHW * K;
-            MFH_TRY(gemm_rows(dx_engine, s, true, false, OHW, K, CO, image, OHW, ptr<const float>(weight), K, grad_image,
-                              K, ws, workspace_floats));
-        }
-    } else {
-        MFH_TRY(gemm_rows(dx_engine, s, false, false, M, K, CO, ptr<const float>(dyT), CO, ptr<const float>(weight), K,
-                          ptr<float>(grad_cols), K, ws, workspace_floats));
+    const int M = g.rows(), K = g.features();
+    // Gated, transposed dy (for dW, and for dX through an activation) and the db partials: one pass.
+    const bool need_rows = dw || (dx && gated);
+    if (need_rows || db)
+        MFH_TRY(launch_conv_grad_rows(as_ptr<const float>(dy), as_ptr<const float>(y),
+                                      need_rows ? as_ptr<float>(dyT) : nullptr, as_ptr<double>(partial), N, ohw, CO,
+                                      grid_x, activation, alpha, s));
+    if (db) MFH_TRY(launch_reduce_partials(as_ptr<const double>(partial), as_ptr<float>(db), N * grid_x, CO, s));
+    if (dw) {
+        // dW (CO x K) = dyT^T cols, split over the M = N*OH*OW pixels.
+        GemmOperands o{};
+        o.trans_a = true;
+        o.M = CO;
+        o.N = K;
+        o.K = M;
+        o.a = as_ptr<const float>(dyT);
+        o.lda = CO;
+        o.b = as_ptr<const float>(cols);
+        o.ldb = K;
+        o.c = as_ptr<float>(dw);
+        o.ldc = K;
+        MFH_TRY(gemm_launch(dw_engine, s, o, GemmEpilogue{}, as_ptr<float>(workspace), workspace_floats));
     }
-    return launch_col2im(ptr<const float>(grad_cols), ptr<float>(dx), d, s);
+    if (!dx) return OK;
+    MFH_TRY(column_gradient(dx_engine, g, as_ptr<const float>(weight), as_ptr<const float>(dy),
+                            gated ? as_ptr<const float>(dyT) : nullptr, as_ptr<float>(grad_cols), s));
+    return launch_col2im_t(as_ptr<const float>(grad_cols), as_ptr<float>(dx), g, s);
 }
 
 MFH_API int mfh_pool_forward(std::uint64_t x, std::uint64_t y, std::uint64_t argmax, int N, int C, int H, int W,
                              int OH, int OW, int KH, int KW, int SH, int SW, std::uint64_t stream) {
-    MFH_TRY(check_ready());
-    MFH_TRY(check_pool(N, C, H, W, OH, OW, KH, KW, SH, SW));
+    MFH_TRY(require_ready());
+    MFH_TRY(validate_pool(N, C, H, W, OH, OW, KH, KW, SH, SW));
     MFH_REQUIRE(x && y && argmax, "pool forward received a null buffer");
-    return launch_pool_forward(ptr<const float>(x), ptr<float>(y), ptr<int>(argmax), N, C, H, W, OH, OW, KH, KW, SH, SW,
-                               as_stream(stream));
+    return launch_pool_forward(as_ptr<const float>(x), as_ptr<float>(y), as_ptr<int>(argmax), N, C, H, W, OH, OW, KH,
+                               KW, SH, SW, as_stream(stream));
 }
 
 MFH_API int mfh_pool_backward(std::uint64_t dy, std::uint64_t argmax, std::uint64_t dx, int N, int C, int H, int W,
                               int OH, int OW, int KH, int KW, int SH, int SW, std::uint64_t stream) {
-    MFH_TRY(check_ready());
-    MFH_TRY(check_pool(N, C, H, W, OH, OW, KH, KW, SH, SW));
+    MFH_TRY(require_ready());
+    MFH_TRY(validate_pool(N, C, H, W, OH, OW, KH, KW, SH, SW));
     MFH_REQUIRE(dy && argmax && dx, "pool backward received a null buffer");
-    return launch_pool_backward(ptr<const float>(dy), ptr<const int>(argmax), ptr<float>(dx), N, C, H, W, OH, OW, KH, KW,
-                                SH, SW, as_stream(stream));
+    return launch_pool_backward(as_ptr<const float>(dy), as_ptr<const int>(argmax), as_ptr<float>(dx), N, C, H, W, OH,
+                                OW, KH, KW, SH, SW, as_stream(stream));
 }
 
 MFH_API int mfh_matmul(int variant, int tile, int accumulate, std::uint64_t a, std::uint64_t b, std::uint64_t bias,
                        std::uint64_t c, int M, int N, int K, std::uint64_t stream) {
-    MFH_TRY(check_ready());
+    MFH_TRY(require_ready());
     MFH_REQUIRE(M > 0 && N > 0 && K > 0, "matmul dimensions must be positive");
     MFH_REQUIRE(fits_index(static_cast<std::int64_t>(M) * K) && fits_index(static_cast<std::int64_t>(K) * N) &&
                     fits_index(static_cast<std::int64_t>(M) * N),
                 "matmul operands exceed int32 indexing");
     MFH_REQUIRE(a && b && c, "matmul received a null buffer");
     MFH_REQUIRE(variant == 0 || variant == 1 || variant == 2 || variant == 4,
-                "matmul variant must be 0 (basic), 1 (tiled), 2 (shared) or 4 (register); there is no cuBLAS variant");
+                "matmul variant must be 0 (basic), 1 (tiled), 2 (shared) or 4 (register); there is no vendor-BLAS variant");
     MFH_REQUIRE(accumulate >= 0 && accumulate <= 2, "accumulate must be 0, 1 or 2");
-    if (variant == 1 || variant == 2) MFH_REQUIRE(tile == 16 || tile == 32, "tile must be 16 or 32");
+    MFH_REQUIRE(!(variant == 1 || variant == 2) || tile == 16 || tile == 32, "tile must be 16 or 32");
     const hipStream_t s = as_stream(stream);
     if (variant == 4 && accumulate == 0) {
-        // The fp32 register variant is the GEMM engine in one pass over K (no workspace, so no split;
-        // the bias is fused in the epilogue).
-        return gemm_rows_bias(1, s, false, false, M, N, K, ptr<const float>(a), K, ptr<const float>(b), N,
-                              ptr<float>(c), N, ptr<const float>(bias), nullptr, 0);
+        // The fp32 register variant is the MFMA engine in one pass over K, bias fused.
+        GemmOperands o{};
+        o.M = M;
+        o.N = N;
+        o.K = K;
+        o.a = as_ptr<const float>(a);
+        o.lda = K;
+        o.b = as_ptr<const float>(b);
+        o.ldb = N;
+        o.c = as_ptr<float>(c);
+        o.ldc = N;
+        GemmEpilogue e;
+        e.bias = as_ptr<const float>(bias);
+        e.bias_mode = bias ? BIAS_COLUMN : BIAS_NONE;
+        return gemm_launch(1, s, o, e, nullptr, 0);
     }
-    MFH_TRY(launch_matmul(variant, tile, accumulate, ptr<const float>(a), ptr<const float>(b), ptr<float>(c), M, N, K, s));
+    MFH_TRY(launch_matmul(variant, tile, accumulate, as_ptr<const float>(a), as_ptr<const float>(b), as_ptr<float>(c), M,
+                          N, K, s));
     if (!bias) return OK;
-    return launch_add_bias(ptr<float>(c), ptr<const float>(bias), M, N, s);
+    return launch_add_bias(as_ptr<float>(c), as_ptr<const float>(bias), M, N, s);
 }
 
 MFH_API int mfh_gemm_tile_count(void) { return gemm_tile_count(); }
@@ -280,7 +370,7 @@ MFH_API int mfh_gemm_tile_info(int index, int* values) {
 }
 
 MFH_API int mfh_gemm_plan(int M, int N, int K, int* tile, int* slices) {
-    MFH_TRY(check_ready());
+    MFH_TRY(require_ready());
     MFH_REQUIRE(M > 0 && N > 0 && K > 0, "GEMM dimensions must be positive");
     MFH_REQUIRE(tile && slices, "mfh_gemm_plan received a null output");
     const GemmPlan plan = gemm_auto_plan(M, N, K);
@@ -290,7 +380,7 @@ MFH_API int mfh_gemm_plan(int M, int N, int K, int* tile, int* slices) {
 }
 
 MFH_API std::int64_t mfh_gemm_workspace(int M, int N, int K) {
-    if (check_ready() != OK) return -1;
+    if (require_ready() != OK) return -1;
     if (M <= 0 || N <= 0 || K <= 0) {
         MFH_FAIL(ERR_ARG, "GEMM dimensions must be positive");
         return -1;
@@ -300,20 +390,21 @@ MFH_API std::int64_t mfh_gemm_workspace(int M, int N, int K) {
 
 MFH_API int mfh_split_reduce(std::uint64_t partial, std::uint64_t c, int slices, int M, int N, int ldc, int reference,
                              std::uint64_t stream) {
-    MFH_TRY(check_ready());
-    MFH_REQUIRE(partial && c, "the split-K reduction requires partial and output buffers");
+    MFH_TRY(require_ready());
+    MFH_REQUIRE(partial && c, "the split-K reduction needs partial and output buffers");
     MFH_REQUIRE(slices >= 2 && M > 0 && N > 0 && ldc >= N, "the split-K reduction needs two or more slices and ldc >= N");
     MFH_REQUIRE(fits_index(static_cast<std::int64_t>(slices) * M * N) &&
                     fits_index(static_cast<std::int64_t>(M - 1) * ldc + N),
                 "split-K buffers exceed the int32 indexing limit");
-    return split_reduce(ptr<const float>(partial), ptr<float>(c), slices, M, N, ldc, reference != 0, as_stream(stream));
+    return split_reduce(as_ptr<const float>(partial), as_ptr<float>(c), slices, M, N, ldc, reference != 0,
+                        as_stream(stream));
 }
 
 MFH_API int mfh_gemm(int engine, int trans_a, int trans_b, std::uint64_t a, std::uint64_t b, std::uint64_t bias,
                      std::uint64_t c, int M, int N, int K, int lda, int ldb, int ldc, std::uint64_t workspace,
                      std::int64_t workspace_floats, std::uint64_t stream) {
-    MFH_TRY(check_ready());
-    MFH_TRY(check_engine(engine));
+    MFH_TRY(require_ready());
+    MFH_TRY(validate_engine(engine));
     MFH_REQUIRE(M > 0 && N > 0 && K > 0, "GEMM dimensions must be positive");
     MFH_REQUIRE(!(trans_a && trans_b), "GEMM supports A^T B and A B^T but not A^T B^T");
     MFH_REQUIRE(lda >= (trans_a ? M : K) && ldb >= (trans_b ? K : N) && ldc >= N,
@@ -324,9 +415,128 @@ MFH_API int mfh_gemm(int engine, int trans_a, int trans_b, std::uint64_t a, std:
     MFH_REQUIRE(a && b && c, "GEMM received a null buffer");
     MFH_REQUIRE(!bias || ldc == N, "GEMM bias needs ldc == N");
     MFH_REQUIRE(workspace_floats >= 0, "workspace size must be non-negative");
-    return gemm_rows_bias(engine, as_stream(stream), trans_a != 0, trans_b != 0, M, N, K, ptr<const float>(a), lda,
-                          ptr<const float>(b), ldb, ptr<float>(c), ldc, ptr<const float>(bias), ptr<float>(workspace),
-                          workspace_floats);
+    GemmOperands o{};
+    o.trans_a = trans_a != 0;
+    o.trans_b = trans_b != 0;
+    o.M = M;
+    o.N = N;
+    o.K = K;
+    o.a = as_ptr<const float>(a);
+    o.lda = lda;
+    o.b = as_ptr<const float>(b);
+    o.ldb = ldb;
+    o.c = as_ptr<float>(c);
+    o.ldc = ldc;
+    GemmEpilogue e;
+    e.bias = as_ptr<const float>(bias);
+    e.bias_mode = bias ? BIAS_COLUMN : BIAS_NONE;
+    return gemm_launch(engine, as_stream(stream), o, e, as_ptr<float>(workspace), workspace_floats);
+}
+
+MFH_API std::int64_t mfh_bn_workspace(int N, int C, int HW) {
+    if (require_ready() != OK) return -1;
+    const NormShape s{N, C, HW};
+    if (validate_norm(s) != OK) return -1;
+    return norm_workspace_doubles(s);
+}
+
+MFH_API int mfh_bn_forward(std::uint64_t x, std::uint64_t gamma, std::uint64_t beta, std::uint64_t running_mean,
+                           std::uint64_t running_var, std::uint64_t residual, std::uint64_t y, std::uint64_t mean,
+                           std::uint64_t inv_std, std::uint64_t workspace, std::int64_t workspace_doubles, int N, int C,
+                           int HW, int training, int relu, double momentum, double eps, double var_scale,
+                           std::uint64_t stream) {
+    MFH_TRY(require_ready());
+    const NormShape s{N, C, HW};
+    MFH_TRY(validate_norm(s));
+    MFH_REQUIRE(x && gamma && beta && running_mean && running_var && y && mean && inv_std,
+                "batch-norm forward received a null buffer");
+    MFH_REQUIRE(!training || (workspace && workspace_doubles >= norm_workspace_doubles(s)),
+                "batch-norm workspace is smaller than mfh_bn_workspace");
+    MFH_REQUIRE(eps >= 0.0 && momentum >= 0.0 && momentum <= 1.0, "batch-norm eps and momentum are out of range");
+    NormForward f{};
+    f.x = as_ptr<const float>(x);
+    f.gamma = as_ptr<const float>(gamma);
+    f.beta = as_ptr<const float>(beta);
+    f.running_mean = as_ptr<float>(running_mean);
+    f.running_var = as_ptr<float>(running_var);
+    f.residual = as_ptr<const float>(residual);
+    f.y = as_ptr<float>(y);
+    f.mean = as_ptr<float>(mean);
+    f.inv_std = as_ptr<float>(inv_std);
+    f.partial = as_ptr<double>(workspace);
+    f.training = training != 0;
+    f.relu = relu != 0;
+    f.momentum = momentum;
+    f.eps = eps;
+    f.var_scale = var_scale;
+    return norm_forward(s, f, as_stream(stream));
+}
+
+MFH_API int mfh_bn_backward(std::uint64_t x, std::uint64_t dy, std::uint64_t gate, std::uint64_t gamma,
+                            std::uint64_t mean, std::uint64_t inv_std, std::uint64_t x_grad, std::uint64_t gamma_grad,
+                            std::uint64_t beta_grad, std::uint64_t residual_grad, std::uint64_t workspace,
+                            std::int64_t workspace_doubles, int N, int C, int HW, int training, int add_x,
+                            int add_gamma, int add_beta, int add_residual, std::uint64_t stream) {
+    MFH_TRY(require_ready());
+    const NormShape s{N, C, HW};
+    MFH_TRY(validate_norm(s));
+    MFH_REQUIRE(x && dy && gamma && mean && inv_std, "batch-norm backward received a null buffer");
+    MFH_REQUIRE(!residual_grad || gate, "a residual gradient comes from a fused ReLU: pass its output as gate");
+    MFH_REQUIRE(workspace && workspace_doubles >= norm_workspace_doubles(s),
+                "batch-norm workspace is smaller than mfh_bn_workspace");
+    NormBackward b{};
+    b.x = as_ptr<const float>(x);
+    b.dy = as_ptr<const float>(dy);
+    b.gate = as_ptr<const float>(gate);
+    b.gamma = as_ptr<const float>(gamma);
+    b.mean = as_ptr<const float>(mean);
+    b.inv_std = as_ptr<const float>(inv_std);
+    b.x_grad = as_ptr<float>(x_grad);
+    b.gamma_grad = as_ptr<float>(gamma_grad);
+    b.beta_grad = as_ptr<float>(beta_grad);
+    b.residual_grad = as_ptr<float>(residual_grad);
+    double* ws = as_ptr<double>(workspace);
+    b.partial = ws;
+    b.coef = reinterpret_cast<float*>(ws + 2LL * s.C * norm_slices(s));
+    b.training = training != 0;
+    b.add_x = add_x != 0;
+    b.add_gamma = add_gamma != 0;
+    b.add_beta = add_beta != 0;
+    b.add_residual = add_residual != 0;
+    return norm_backward(s, b, as_stream(stream));
+}
+
+MFH_API int mfh_relu_forward(std::uint64_t x, std::uint64_t y, std::int64_t count, std::uint64_t stream) {
+    MFH_TRY(require_ready());
+    MFH_REQUIRE(count >= 0, "element count must be non-negative");
+    MFH_REQUIRE(count == 0 || (x && y), "relu forward received a null buffer");
+    return launch_relu_forward(as_ptr<const float>(x), as_ptr<float>(y), count, as_stream(stream));
+}
+
+MFH_API int mfh_relu_backward(std::uint64_t x, std::uint64_t grad, std::uint64_t out, std::int64_t count, float alpha,
+                              int add, std::uint64_t stream) {
+    MFH_TRY(require_ready());
+    MFH_REQUIRE(count >= 0, "element count must be non-negative");
+    MFH_REQUIRE(count == 0 || (x && grad && out), "relu backward received a null buffer");
+    return launch_relu_backward(as_ptr<const float>(x), as_ptr<const float>(grad), as_ptr<float>(out), count, alpha,
+                                add != 0, as_stream(stream));
+}
+
+MFH_API int mfh_adam_step(const mfh_adam_tensor* tensors, int count, float grad_scale, float beta1,
+                          float one_minus_beta1, float beta2, float one_minus_beta2, float eps, std::uint64_t stream) {
+    MFH_TRY(require_ready());
+    MFH_REQUIRE(count >= 0 && (count == 0 || tensors), "adam needs a tensor table");
+    std::vector<AdamTensor> table(static_cast<std::size_t>(count));
+    for (int i = 0; i < count; ++i) {
+        const mfh_adam_tensor& t = tensors[i];
+        MFH_REQUIRE(t.size >= 0, "adam tensor sizes must be non-negative");
+        MFH_REQUIRE(t.size == 0 || (t.param && t.grad && t.m && t.v), "adam tensor received a null buffer");
+        MFH_REQUIRE(t.size <= INDEX_LIMIT, "adam tensor exceeds int32 indexing");
+        table[i] = AdamTensor{as_ptr<float>(t.param), as_ptr<const float>(t.grad), as_ptr<float>(t.m), as_ptr<float>(t.v),
+                              t.size, t.lr, t.weight_decay, t.bias_correction1, t.bias_correction2};
+    }
+    const AdamScalars s{grad_scale, beta1, one_minus_beta1, beta2, one_minus_beta2, eps};
+    return launch_adam(table.data(), count, s, as_stream(stream));
 }
 
 }  // extern "C"

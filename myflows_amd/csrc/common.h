@@ -1,7 +1,7 @@
-// Shared host-side plumbing of libmfhip: status codes, the thread-local error text, launch checks
-// and the declarations through which the C-ABI translation unit (api.hip) reaches the kernels of
-// conv.hip, gemm.hip and matmul.hip. Every kernel indexes its buffers with int32 offsets; the
-// entry points reject larger problems before launching anything.
+// Host-side plumbing shared by the translation units of libmfhip: status codes, the thread-local
+// error text, launch checks, and the internal interfaces through which the C ABI (api.hip) reaches
+// the kernels of conv.hip, gemm.hip, matmul.hip, norm.hip and pointwise.hip. Every kernel indexes
+// its buffers with int32 offsets; the entry points reject larger problems before launching anything.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -20,10 +20,11 @@ enum Status : int {
     ERR_DEVICE = 5,
 };
 
-enum Activation : int { ACT_NONE = 0, ACT_RELU = 1, ACT_LEAKY_RELU = 2 };
+// Activation codes of the C ABI.
+constexpr int ACT_NONE = 0, ACT_RELU = 1, ACT_LEAKY_RELU = 2;
 
 constexpr std::int64_t INDEX_LIMIT = 2147483647;  // int32 element offsets inside every kernel
-constexpr unsigned GRID_YZ_LIMIT = 65535;
+constexpr unsigned GRID_YZ_LIMIT = 65535;         // hardware limit of gridDim.y and gridDim.z
 
 // Records "file:line: what" as this thread's last error and returns status.
 int fail(int status, const char* file, int line, const std::string& what);
@@ -41,24 +42,29 @@ inline unsigned blocks_for(std::int64_t total, unsigned threads) {
 inline bool fits_index(std::int64_t value) { return value >= 0 && value <= INDEX_LIMIT; }
 
 #define MFH_FAIL(status, what) ::mfh::fail((status), __FILE_NAME__, __LINE__, (what))
-#define MFH_TRY(call)                           \
-    do {                                        \
-        const int mfh_rc_ = (call);             \
+#define MFH_TRY(call)                             \
+    do {                                          \
+        const int mfh_rc_ = (call);               \
         if (mfh_rc_ != ::mfh::OK) return mfh_rc_; \
     } while (0)
-#define MFH_REQUIRE(condition, message)                                   \
-    do {                                                                  \
-        if (!(condition)) return MFH_FAIL(::mfh::ERR_ARG, (message));     \
+#define MFH_REQUIRE(condition, message)                               \
+    do {                                                              \
+        if (!(condition)) return MFH_FAIL(::mfh::ERR_ARG, (message)); \
     } while (0)
 #define MFH_CHECK_LAUNCH(name, stream) ::mfh::after_launch((name), (stream), __FILE_NAME__, __LINE__)
 
-struct ConvDims {
+// Geometry of one 2-D convolution (NCHW input, OIHW weight).
+struct ConvGeometry {
     int N, CI, H, W, CO, KH, KW, OH, OW, SH, SW, PH, PW;
+    int ohw() const { return OH * OW; }
+    int rows() const { return N * OH * OW; }     // M of the im2col matrix
+    int features() const { return CI * KH * KW; }  // K of the im2col matrix
 };
 
 // ---- conv.hip ---------------------------------------------------------------------------------
-int launch_im2col(const float* x, float* cols, const ConvDims& d, hipStream_t stream);
-int launch_col2im(const float* grad_cols, float* dx, const ConvDims& d, hipStream_t stream);
+int launch_im2col(const float* x, float* cols, const ConvGeometry& g, hipStream_t stream);
+// dx from the per-image transposed column gradient gcT[n][CI*KH*KW][OH*OW].
+int launch_col2im_t(const float* gcT, float* dx, const ConvGeometry& g, hipStream_t stream);
 int launch_conv_epilogue(const float* rows, const float* bias, float* y, int N, int OHW, int CO, int act,
                          float alpha, hipStream_t stream);
 int conv_grad_tile();  // pixels per conv_grad_rows tile (grid_x counts these tiles)
@@ -71,8 +77,8 @@ int launch_pool_forward(const float* x, float* y, int* argmax, int N, int C, int
 int launch_pool_backward(const float* dy, const int* argmax, float* dx, int N, int C, int H, int W, int OH,
                          int OW, int KH, int KW, int SH, int SW, hipStream_t stream);
 
-// Loads the code object of this file's kernels (fails when the device has no gfx950 binary).
-int conv_probe_kernels();
+// Loads the code object of this library's kernels (fails when the device has no gfx950 binary).
+int probe_code_object();
 
 // ---- gemm.hip ---------------------------------------------------------------------------------
 struct GemmTile {
@@ -91,19 +97,116 @@ int gemm_plan_from_engine(int engine, int M, int N, int K, GemmPlan* plan);
 bool gemm_engine_valid(int engine);
 std::int64_t gemm_workspace_floats(const GemmPlan& plan, int M, int N);
 
-// Row-major C(M x N) = op(A) op(B); A stored K x M when trans_a, B stored N x K when trans_b.
-// Splits K through the workspace only when it holds the plan's slices * M * N floats.
-int gemm_rows(int engine, hipStream_t stream, bool trans_a, bool trans_b, int M, int N, int K, const float* a,
-              int lda, const float* b, int ldb, float* c, int ldc, float* workspace, std::int64_t workspace_floats);
-int gemm_rows_bias(int engine, hipStream_t stream, bool trans_a, bool trans_b, int M, int N, int K, const float* a,
-                   int lda, const float* b, int ldb, float* c, int ldc, const float* bias, float* workspace,
-                   std::int64_t workspace_floats);
+constexpr int BIAS_NONE = 0, BIAS_COLUMN = 1, BIAS_ROW = 2;
+
+// Kernel argument block of the MFMA GEMM (see gemm.hip for the meaning of split and the batches).
+struct GemmParams {
+    const float* A;
+    const float* B;
+    float* C;
+    const float* bias;
+    int M, N, K, lda, ldb, ldc;
+    int k_chunk, split;
+    long long a_batch, b_batch, c_batch;
+    int bias_mode, act;
+    float alpha;
+};
+
+// One GEMM problem, or `batch` of them at constant strides: C(M x N) = op(A) op(B), row-major;
+// A is stored K x M when trans_a, B is stored N x K when trans_b.
+struct GemmOperands {
+    bool trans_a, trans_b;
+    int M, N, K;
+    const float* a;
+    int lda;
+    const float* b;
+    int ldb;
+    float* c;
+    int ldc;
+    int batch = 1;
+    long long a_batch = 0, b_batch = 0, c_batch = 0;
+};
+
+// What happens to each output after the product: + bias (per column or per row), activation.
+struct GemmEpilogue {
+    const float* bias = nullptr;
+    int bias_mode = BIAS_NONE;
+    int act = ACT_NONE;
+    float alpha = 0.0f;
+};
+
+// Runs the engine; splits K through the workspace (never for batches) only when it holds the
+// plan's slices * M * N floats.
+int gemm_launch(int engine, hipStream_t stream, const GemmOperands& operands, const GemmEpilogue& epilogue,
+                float* workspace, std::int64_t workspace_floats);
 int split_reduce(const float* partial, float* c, int slices, int M, int N, int ldc, bool reference,
                  hipStream_t stream);
 
 // ---- matmul.hip -------------------------------------------------------------------------------
-// variant 0 basic, 1 tiled, 2 shared, 4 register (kahan / dot2 accumulation only); see matmul.hip.
+// variant 0 basic, 1 tiled, 2 shared, 4 register (compensated modes); see matmul.hip.
 int launch_matmul(int variant, int tile, int accumulate, const float* a, const float* b, float* c, int M, int N,
                   int K, hipStream_t stream);
+
+// ---- norm.hip ---------------------------------------------------------------------------------
+// Batch normalisation over the (N, H*W) positions of each channel of an NCHW tensor.
+struct NormShape {
+    int N, C, HW;
+};
+// Per-channel slices of the FP64 partial-sum pass and the workspace doubles they need.
+int norm_slices(const NormShape& s);
+std::int64_t norm_workspace_doubles(const NormShape& s);
+
+struct NormForward {
+    const float* x;
+    const float* gamma;
+    const float* beta;
+    float* running_mean;  // updated in place when training
+    float* running_var;
+    const float* residual;  // optional same-shape tensor added after the affine transform
+    float* y;
+    float* mean;     // 2 x C: FP64 mean split into hi + lo floats
+    float* inv_std;  // C
+    double* partial;
+    bool training, relu;
+    double momentum, eps, var_scale;
+};
+int norm_forward(const NormShape& s, const NormForward& f, hipStream_t stream);
+
+struct NormBackward {
+    const float* x;
+    const float* dy;
+    const float* gate;  // optional forward output of a fused ReLU: dy counts only where gate > 0
+    const float* gamma;
+    const float* mean;
+    const float* inv_std;
+    float* x_grad;
+    float* gamma_grad;
+    float* beta_grad;
+    float* residual_grad;  // optional: receives the gated dy (the residual branch of a fused Add)
+    double* partial;
+    float* coef;  // 3 x C scratch for the dx coefficients
+    bool training, add_x, add_gamma, add_beta, add_residual;
+};
+int norm_backward(const NormShape& s, const NormBackward& b, hipStream_t stream);
+
+// ---- pointwise.hip ----------------------------------------------------------------------------
+int launch_relu_forward(const float* x, float* y, std::int64_t count, hipStream_t stream);
+// out (+)= x > 0 ? g : alpha * g   (alpha = 0 for ReLU)
+int launch_relu_backward(const float* x, const float* g, float* out, std::int64_t count, float alpha, bool add,
+                         hipStream_t stream);
+
+// One tensor of a multi-tensor Adam step.
+struct AdamTensor {
+    float* param;
+    const float* grad;
+    float* m;
+    float* v;
+    std::int64_t size;
+    float lr, decay, bc1, bc2;  // learning rate, weight decay, bias corrections 1 - beta^step (float32)
+};
+struct AdamScalars {
+    float grad_scale, b1, omb1, b2, omb2, eps;
+};
+int launch_adam(const AdamTensor* tensors, int count, const AdamScalars& s, hipStream_t stream);
 
 }  // namespace mfh

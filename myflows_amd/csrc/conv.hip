@@ -1,10 +1,12 @@
-// Bandwidth-bound kernels of the convolution and pooling path: im2col, col2im (gather), the NCHW
-// epilogue (bias + activation), the transposed/gated dy with FP64 bias partials, the in-order FP64
-// partial reduction, the GEMM bias epilogue and max-pool forward/backward.
+// Bandwidth-bound kernels of the convolution and pooling path: im2col, col2im (gather from the
+// transposed column gradient), the NCHW epilogue (bias + activation), the transposed/gated dy with
+// FP64 bias partials, the fixed-order FP64 partial reduction, the GEMM bias epilogue and max-pool
+// forward/backward.
 //
 // Layouts (row-major, NCHW): cols[(n*OH + oh)*OW + ow][(ci*KH + kh)*KW + kw] is the im2col matrix
-// (M = N*OH*OW rows, K = CI*KH*KW features); rows[(n*OHW + p)][co] is the GEMM output before the
-// epilogue. Every reduction sums in a fixed order, so each kernel is bitwise reproducible.
+// (M = N*OH*OW rows, K = CI*KH*KW features); rows[(n*OHW + p)][co] is a GEMM output before the
+// epilogue; gcT[n][(ci*KH + kh)*KW + kw][oh*OW + ow] is the per-image transposed column gradient.
+// Every reduction sums in a fixed order, so each kernel is bitwise reproducible.
 #include "common.h"
 #include "fastdiv.h"
 
@@ -32,11 +34,15 @@ __global__ __launch_bounds__(256) void im2col_kernel(const float* __restrict__ x
     cols[idx] = v;
 }
 
-// dx[n, ci, ih, iw] = sum of grad_cols over every window position that reads (ih, iw), visited in
-// increasing (oh, ow) order; no atomics, so the result is deterministic.
-__global__ __launch_bounds__(256) void col2im_kernel(const float* __restrict__ grad_cols, float* __restrict__ dx,
-                                                     int total, FastDiv div_w, FastDiv div_h, FastDiv div_ci, int CI,
-                                                     int KH, int KW, int OH, int OW, int SH, int SW, int PH, int PW) {
+// dx[n, ci, ih, iw] = sum over every window position (oh, ow) that reads (ih, iw), visited in
+// increasing (oh, ow) order, of the column gradient of feature (ci, kh, kw) at that position.
+// The column gradient arrives transposed per image, gcT[n][(ci*KH + kh)*KW + kw][oh*OW + ow], so
+// for a fixed (kh, kw) the threads of consecutive iw read consecutive ow: the gather is coalesced.
+// No atomics, so the result is deterministic.
+__global__ __launch_bounds__(256) void col2im_t_kernel(const float* __restrict__ gcT, float* __restrict__ dx,
+                                                       int total, FastDiv div_w, FastDiv div_h, FastDiv div_ci,
+                                                       int CI, int KH, int KW, int OH, int OW, int SH, int SW, int PH,
+                                                       int PW) {
     const int idx = blockIdx.x * 256 + threadIdx.x;
     if (idx >= total) return;
     int iw, ih, ci;
@@ -44,19 +50,20 @@ __global__ __launch_bounds__(256) void col2im_kernel(const float* __restrict__ g
     const int t2 = div_h.divmod(t, ih);
     const int n = div_ci.divmod(t2, ci);
     const int hp = ih + PH, wp = iw + PW;  // coordinates in the zero-padded input
-    // Windows oh with oh*SH <= hp <= oh*SH + KH - 1.
+    // Windows oh with oh*SH <= hp <= oh*SH + KH - 1, likewise ow.
     const int oh_lo = hp >= KH ? (hp - KH) / SH + 1 : 0;
     const int oh_hi = min(OH - 1, hp / SH);
     const int ow_lo = wp >= KW ? (wp - KW) / SW + 1 : 0;
     const int ow_hi = min(OW - 1, wp / SW);
-    const int features = CI * KH * KW;
+    const int ohw = OH * OW;
+    const float* image = gcT + (static_cast<long long>(n) * CI + ci) * KH * KW * ohw;
     float sum = 0.0f;
     for (int oh = oh_lo; oh <= oh_hi; ++oh) {
         const int kh = hp - oh * SH;
-        const float* base = grad_cols + ((n * OH + oh) * OW) * features + (ci * KH + kh) * KW;
+        const float* plane_row = image + kh * KW * ohw + oh * OW;
         for (int ow = ow_lo; ow <= ow_hi; ++ow) {
             const int kw = wp - ow * SW;
-            sum += base[ow * features + kw];
+            sum += plane_row[kw * ohw + ow];
         }
     }
     dx[idx] = sum;
@@ -150,14 +157,28 @@ __global__ __launch_bounds__(TILE* TROWS) void conv_grad_rows_kernel(const float
     }
 }
 
-// out[i] = (float) sum_{j = 0..count-1} partial[j * width + i], in order, in FP64.
-__global__ __launch_bounds__(128) void reduce_partials_kernel(const double* __restrict__ partial,
-                                                              float* __restrict__ out, int count, int width) {
-    const int i = blockIdx.x * 128 + threadIdx.x;
-    if (i >= width) return;
+constexpr int RP_COLS = 16, RP_LANES = 16;  // columns per workgroup, row lanes per column
+
+// out[i] = (float) sum_{j = 0..count-1} partial[j * width + i] in FP64, in a fixed order: lane r of
+// column i sums the rows j = r, r + 16, r + 32, ... in increasing j, then the 16 lane sums are added
+// in lane order. Deterministic, and with 16 independent chains per column the loads overlap.
+__global__ __launch_bounds__(RP_COLS* RP_LANES) void reduce_partials_kernel(const double* __restrict__ partial,
+                                                                            float* __restrict__ out, int count,
+                                                                            int width) {
+    __shared__ double lane_sum[RP_LANES][RP_COLS];
+    const int c = threadIdx.x % RP_COLS, r = threadIdx.x / RP_COLS;
+    const int i = blockIdx.x * RP_COLS + c;
     double s = 0.0;
-    for (int j = 0; j < count; ++j) s += partial[static_cast<long long>(j) * width + i];
-    out[i] = static_cast<float>(s);
+    if (i < width)
+        for (int j = r; j < count; j += RP_LANES) s += partial[static_cast<long long>(j) * width + i];
+    lane_sum[r][c] = s;
+    __syncthreads();
+    if (r == 0 && i < width) {
+        double total = 0.0;
+#pragma unroll
+        for (int k = 0; k < RP_LANES; ++k) total += lane_sum[k][c];
+        out[i] = static_cast<float>(total);
+    }
 }
 
 __global__ __launch_bounds__(256) void add_bias_kernel(float* __restrict__ rows, const float* __restrict__ bias,
@@ -222,21 +243,21 @@ __global__ __launch_bounds__(256) void pool_backward_kernel(const float* __restr
 
 }  // namespace
 
-int launch_im2col(const float* x, float* cols, const ConvDims& d, hipStream_t stream) {
-    const int K = d.CI * d.KH * d.KW;
-    const int total = d.N * d.OH * d.OW * K;
-    im2col_kernel<<<blocks_for(total, 256), 256, 0, stream>>>(x, cols, total, FastDiv(K), FastDiv(d.KW),
-                                                                FastDiv(d.KH), FastDiv(d.OW), FastDiv(d.OH), d.CI,
-                                                                d.H, d.W, d.SH, d.SW, d.PH, d.PW);
+int launch_im2col(const float* x, float* cols, const ConvGeometry& g, hipStream_t stream) {
+    const int K = g.features();
+    const int total = g.rows() * K;
+    im2col_kernel<<<blocks_for(total, 256), 256, 0, stream>>>(x, cols, total, FastDiv(K), FastDiv(g.KW),
+                                                                FastDiv(g.KH), FastDiv(g.OW), FastDiv(g.OH), g.CI,
+                                                                g.H, g.W, g.SH, g.SW, g.PH, g.PW);
     return MFH_CHECK_LAUNCH("im2col", stream);
 }
 
-int launch_col2im(const float* grad_cols, float* dx, const ConvDims& d, hipStream_t stream) {
-    const int total = d.N * d.CI * d.H * d.W;
-    col2im_kernel<<<blocks_for(total, 256), 256, 0, stream>>>(grad_cols, dx, total, FastDiv(d.W), FastDiv(d.H),
-                                                                FastDiv(d.CI), d.CI, d.KH, d.KW, d.OH, d.OW, d.SH,
-                                                                d.SW, d.PH, d.PW);
-    return MFH_CHECK_LAUNCH("col2im", stream);
+int launch_col2im_t(const float* gcT, float* dx, const ConvGeometry& g, hipStream_t stream) {
+    const int total = g.N * g.CI * g.H * g.W;
+    col2im_t_kernel<<<blocks_for(total, 256), 256, 0, stream>>>(gcT, dx, total, FastDiv(g.W), FastDiv(g.H),
+                                                                  FastDiv(g.CI), g.CI, g.KH, g.KW, g.OH, g.OW, g.SH,
+                                                                  g.SW, g.PH, g.PW);
+    return MFH_CHECK_LAUNCH("col2im_t", stream);
 }
 
 int launch_conv_epilogue(const float* rows, const float* bias, float* y, int N, int OHW, int CO, int act,
@@ -256,7 +277,7 @@ int launch_conv_grad_rows(const float* dy, const float* y, float* dyT, double* p
 }
 
 int launch_reduce_partials(const double* partial, float* out, int count, int width, hipStream_t stream) {
-    reduce_partials_kernel<<<blocks_for(width, 128), 128, 0, stream>>>(partial, out, count, width);
+    reduce_partials_kernel<<<blocks_for(width, RP_COLS), RP_COLS * RP_LANES, 0, stream>>>(partial, out, count, width);
     return MFH_CHECK_LAUNCH("reduce_partials", stream);
 }
 
@@ -282,14 +303,12 @@ int launch_pool_backward(const float* dy, const int* argmax, float* dx, int N, i
     return MFH_CHECK_LAUNCH("pool_backward", stream);
 }
 
-}  // namespace mfh
-
-namespace mfh {
-int conv_probe_kernels() {
+int probe_code_object() {
     hipFuncAttributes attributes;
     const hipError_t status = hipFuncGetAttributes(&attributes, reinterpret_cast<const void*>(&im2col_kernel));
     if (status != hipSuccess)
         return MFH_FAIL(ERR_INIT, std::string("no usable gfx950 code object: ") + hipGetErrorString(status));
     return OK;
 }
+
 }  // namespace mfh

@@ -1,15 +1,16 @@
-// FP32 GEMM engine on the CDNA4 matrix cores: C(M x N) = op(A) op(B) (+ bias), row-major.
+// FP32 GEMM engine on the CDNA4 matrix cores: C(M x N) = op(A) op(B) (+ bias) (activation),
+// row-major, with op(X) = X or X^T chosen per operand.
 //
-// Work decomposition. A block computes a BM x BN tile of C with (BM/WM) x (BN/WN) wave64s; a wave
-// owns a WM x WN sub-tile made of (WM/32) x (WN/32) accumulators of v_mfma_f32_32x32x2_f32
-// (16 floats per lane each). The K range of the block is consumed in BK-deep stages that are
+// Work decomposition. A workgroup computes a BM x BN tile of C with (BM/WM) x (BN/WN) wave64s; a
+// wave owns a WM x WN sub-tile made of (WM/32) x (WN/32) accumulators of v_mfma_f32_32x32x2_f32
+// (16 floats per lane each). The K range of the workgroup is consumed in BK-deep stages that are
 // double buffered in LDS: the global loads of stage t+1 are in flight while the waves run the
 // MFMAs of stage t, with one barrier per stage.
 //
 // LDS layout. Each operand tile is kept in LDS in the orientation it has in global memory, so the
 // global->LDS copy is a straight (float4 when aligned) row copy with no transpose:
-//   * "k-contiguous" operands (A when not trans_a, B when trans_b) live as [rows][BK + 4];
-//   * "mn-contiguous" operands (A when trans_a, B when not trans_b) live as [BK][rows + 4].
+//   * "k-contiguous" operands (A when not transposed, B when transposed) live as [rows][BK + 4];
+//   * "mn-contiguous" operands (A when transposed, B when not transposed) live as [BK][rows + 4].
 // The +4 floats of padding keep 16-byte alignment and move successive rows to other banks.
 //
 // MFMA operand mapping. v_mfma_f32_32x32x2_f32 multiplies a 32x2 slice of A (lane l supplies
@@ -19,10 +20,14 @@
 // half h consumes k = h * BK/2 + s for s = 0 .. BK/2 - 1: a k-contiguous operand then reads four
 // consecutive k of its row with one 16-byte LDS load.
 //
-// Split-K. blockIdx.z selects the K slice [z * k_chunk, min(K, (z + 1) * k_chunk)) and the slice
-// writes its partial product to C + z * c_stride; split_reduce then sums the slices in a fixed
-// order in FP64. Every output of an unsplit launch is produced by one wave in one fixed order, so
-// the engine is bitwise reproducible run to run.
+// The third grid dimension has two uses:
+//   * split-K (GemmParams::split = 1): z selects the K slice [z * k_chunk, min(K, (z+1) * k_chunk))
+//     and writes its partial product to C + z * c_batch; split_reduce then sums the slices in a fixed
+//     order in FP64;
+//   * batches (split = 0): z is an independent problem at A + z * a_batch, B + z * b_batch,
+//     C + z * c_batch (one per image for the convolution's per-image GEMMs).
+// Every output element is produced by one wave in one fixed order, so results are bitwise
+// reproducible run to run.
 #include "common.h"
 
 namespace mfh {
@@ -46,9 +51,10 @@ constexpr int PLAN_BASE = 16;     // engine codes >= PLAN_BASE name a tile and a
 constexpr int MAX_SLICES = 128;   // slices per explicit plan code
 constexpr int MIN_CHUNK = 128;    // smallest K slice the automatic planner makes
 
+// A ROWS x COLS tile whose COLS dimension is contiguous in global memory (row stride ld), staged
+// through registers: load() issues the global reads, store() writes them to LDS.
 template <int ROWS, int COLS, int THREADS, bool VEC>
 struct TileLoader {
-    // A ROWS x COLS tile whose COLS dimension is contiguous in global memory (row stride ld).
     static constexpr int ELEMS = VEC ? ROWS * COLS / 4 : ROWS * COLS;
     static constexpr int PER_THREAD = (ELEMS + THREADS - 1) / THREADS;
     static constexpr int VCOLS = VEC ? COLS / 4 : COLS;
@@ -90,10 +96,14 @@ struct TileLoader {
     }
 };
 
+__device__ __forceinline__ float activate(float v, int act, float alpha) {
+    if (act == ACT_RELU) return v < 0.0f ? 0.0f : v;  // NaN stays NaN
+    if (act == ACT_LEAKY_RELU) return v > 0.0f ? v : alpha * v;
+    return v;
+}
+
 template <int BM, int BN, int BK, int WM, int WN, bool TA, bool TB, bool VEC>
-__global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void gemm_mfma_kernel(
-    const float* __restrict__ A, const float* __restrict__ B, float* __restrict__ C, const float* __restrict__ bias,
-    int M, int N, int K, int lda, int ldb, int ldc, int k_chunk, long long c_stride) {
+__global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void gemm_mfma_kernel(GemmParams p) {
     constexpr int WGN = BN / WN, THREADS = (BM / WM) * WGN * 64;
     constexpr int TM = WM / 32, TN = WN / 32, HALF = BK / 2;
     static_assert(BK % 8 == 0, "each lane half consumes groups of four k");
@@ -108,20 +118,24 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void gemm_mfma_kernel(
     const int lm = lane % 32, h = lane / 32;
     const int wm0 = (wave / WGN) * WM, wn0 = (wave % WGN) * WN;
     const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
-    const int k_begin = blockIdx.z * k_chunk;
-    const int k_end = min(K, k_begin + k_chunk);
-    C += blockIdx.z * c_stride;
+    const int z = blockIdx.z;
+    const float* __restrict__ A = p.A + (p.split ? 0 : z * p.a_batch);
+    const float* __restrict__ B = p.B + (p.split ? 0 : z * p.b_batch);
+    float* __restrict__ C = p.C + z * p.c_batch;
+    const int k_begin = p.split ? z * p.k_chunk : 0;
+    const int k_end = p.split ? min(p.K, k_begin + p.k_chunk) : p.K;
+    const int M = p.M, N = p.N;
 
     // A tile: rows = m (k-contiguous) or k (mn-contiguous); likewise B.
     TileLoader<TA ? BK : BM, TA ? BM : BK, THREADS, VEC> la;
     TileLoader<TB ? BN : BK, TB ? BK : BN, THREADS, VEC> lb;
-    auto load = [&](int kt) {
-        if constexpr (TA) la.load(A, lda, kt, k_end, m0, M, tid);
-        else la.load(A, lda, m0, M, kt, k_end, tid);
-        if constexpr (TB) lb.load(B, ldb, n0, N, kt, k_end, tid);
-        else lb.load(B, ldb, kt, k_end, n0, N, tid);
+    auto fetch = [&](int kt) {
+        if constexpr (TA) la.load(A, p.lda, kt, k_end, m0, M, tid);
+        else la.load(A, p.lda, m0, M, kt, k_end, tid);
+        if constexpr (TB) lb.load(B, p.ldb, n0, N, kt, k_end, tid);
+        else lb.load(B, p.ldb, kt, k_end, n0, N, tid);
     };
-    auto store = [&](int buf) {
+    auto stage = [&](int buf) {
         la.template store<LDA_S>(smem + buf * (A_SIZE + B_SIZE), tid);
         lb.template store<LDB_S>(smem + buf * (A_SIZE + B_SIZE) + A_SIZE, tid);
     };
@@ -136,13 +150,13 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void gemm_mfma_kernel(
 
     const int stages = k_end > k_begin ? (k_end - k_begin + BK - 1) / BK : 0;
     if (stages > 0) {
-        load(k_begin);
-        store(0);
+        fetch(k_begin);
+        stage(0);
     }
     __syncthreads();
     for (int t = 0; t < stages; ++t) {
         const bool more = t + 1 < stages;
-        if (more) load(k_begin + (t + 1) * BK);
+        if (more) fetch(k_begin + (t + 1) * BK);
         const float* As = smem + (t & 1) * (A_SIZE + B_SIZE);
         const float* Bs = As + A_SIZE;
 #pragma unroll
@@ -175,14 +189,16 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void gemm_mfma_kernel(
                     acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[i].w, b[j].w, acc[i][j], 0, 0, 0);
                 }
         }
-        if (more) store((t + 1) & 1);
+        if (more) stage((t + 1) & 1);
         __syncthreads();
     }
 
+    // Epilogue: bias (per output column or per output row), then the activation, then the store.
+    const float* __restrict__ bias = p.bias;
 #pragma unroll
     for (int j = 0; j < TN; ++j) {
         const int col = n0 + wn0 + j * 32 + lm;
-        const float add = bias && col < N ? bias[col] : 0.f;
+        const float col_bias = p.bias_mode == BIAS_COLUMN && col < N ? bias[col] : 0.f;
 #pragma unroll
         for (int i = 0; i < TM; ++i)
 #pragma unroll
@@ -190,29 +206,32 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void gemm_mfma_kernel(
                 const int row = m0 + wm0 + i * 32 + 8 * (r / 4) + 4 * h + r % 4;
                 if (row < M && col < N) {
                     float v = acc[i][j][r];
-                    if (bias) v += add;
-                    C[static_cast<long long>(row) * ldc + col] = v;
+                    if (p.bias_mode == BIAS_COLUMN) v += col_bias;
+                    else if (p.bias_mode == BIAS_ROW) v += bias[row];
+                    C[static_cast<long long>(row) * p.ldc + col] = activate(v, p.act, p.alpha);
                 }
             }
     }
 }
 
-// C = (float)(((0.0 + p0) + p1) + ... + p[S-1]) in FP64, then + bias in FP32 when given.
+// C = act((float)(((0.0 + p0) + p1) + ... + p[S-1]) [+ bias]) with the FP64 sum in slice order,
+// the bias (per column or per row) added in FP32 after the rounding.
 __global__ __launch_bounds__(256) void split_reduce_kernel(const float* __restrict__ partial, float* __restrict__ C,
-                                                           const float* __restrict__ bias, int slices, int M, int N,
-                                                           int ldc) {
+                                                           const float* __restrict__ bias, int bias_mode, int act,
+                                                           float alpha, int slices, int M, int N, int ldc) {
     const long long i = blockIdx.x * 256LL + threadIdx.x, total = static_cast<long long>(M) * N;
     if (i >= total) return;
     double s = 0.0;
     for (int z = 0; z < slices; ++z) s += static_cast<double>(partial[z * total + i]);
     const long long row = i / N, col = i % N;
     float v = static_cast<float>(s);
-    if (bias) v += bias[col];
-    C[row * ldc + col] = v;
+    if (bias_mode == BIAS_COLUMN) v += bias[col];
+    else if (bias_mode == BIAS_ROW) v += bias[row];
+    C[row * ldc + col] = activate(v, act, alpha);
 }
 
-using GemmFn = void (*)(const float*, const float*, float*, const float*, int, int, int, int, int, int, int,
-                        long long);
+using GemmFn = void (*)(GemmParams);
+constexpr int VARIANTS = 8;  // 4 layouts (NN, NT, TN, TT) x scalar / float4 loads
 
 template <int T, bool TA, bool TB, bool VEC>
 constexpr GemmFn kernel_of() {
@@ -220,17 +239,19 @@ constexpr GemmFn kernel_of() {
 }
 
 template <int T>
-constexpr void fill_row(GemmFn (&row)[6]) {
+constexpr void fill_row(GemmFn (&row)[VARIANTS]) {
     row[0] = kernel_of<T, false, false, false>();
     row[1] = kernel_of<T, false, false, true>();
     row[2] = kernel_of<T, false, true, false>();
     row[3] = kernel_of<T, false, true, true>();
     row[4] = kernel_of<T, true, false, false>();
     row[5] = kernel_of<T, true, false, true>();
+    row[6] = kernel_of<T, true, true, false>();
+    row[7] = kernel_of<T, true, true, true>();
 }
 
 struct KernelTable {
-    GemmFn fn[NUM_TILES][6];
+    GemmFn fn[NUM_TILES][VARIANTS];
     KernelTable() {
         fill_row<0>(fn[0]);
         fill_row<1>(fn[1]);
@@ -251,20 +272,25 @@ const KernelTable& kernel_table() {
 
 int threads_of(const GemmTile& t) { return (t.bm / t.wm) * (t.bn / t.wn) * 64; }
 
+bool aligned16(const void* p) { return (reinterpret_cast<std::uintptr_t>(p) & 15) == 0; }
+
+int tile_for_shape(int M, int N) {
+    if (N <= 32) return 4;
+    if (M <= 32) return 5;
+    if (N <= 64) return M <= 64 ? 3 : 1;
+    if (M <= 64) return 2;
+    return 0;
+}
+
 }  // namespace
 
 int gemm_tile_count() { return NUM_TILES; }
 const GemmTile& gemm_tile(int index) { return TILES[index]; }
 
-// Tile by output shape; split K when the output covers fewer than two blocks per CU and K is long
-// relative to the output (K >= M + N): the weight-gradient GEMMs, whose K is the pixel count.
+// Tile by output shape; split K when the output covers fewer than two workgroups per CU and K is
+// long relative to the output (K >= M + N): the weight-gradient GEMMs, whose K is the pixel count.
 GemmPlan gemm_auto_plan(int M, int N, int K) {
-    int tile;
-    if (N <= 32) tile = 4;
-    else if (M <= 32) tile = 5;
-    else if (N <= 64) tile = M <= 64 ? 3 : 1;
-    else if (M <= 64) tile = 2;
-    else tile = 0;
+    const int tile = tile_for_shape(M, N);
     GemmPlan plan{tile, 1, K};
     const std::int64_t tiles = static_cast<std::int64_t>(blocks_for(M, TILES[tile].bm)) * blocks_for(N, TILES[tile].bn);
     const std::int64_t target = 2LL * device_cu_count();
@@ -301,51 +327,68 @@ std::int64_t gemm_workspace_floats(const GemmPlan& plan, int M, int N) {
     return plan.slices > 1 ? static_cast<std::int64_t>(plan.slices) * M * N : 0;
 }
 
-int split_reduce_bias(const float* partial, float* c, const float* bias, int slices, int M, int N, int ldc,
-                      hipStream_t stream) {
+int split_reduce_epilogue(const float* partial, float* c, const GemmEpilogue& e, int slices, int M, int N, int ldc,
+                          hipStream_t stream) {
     const std::int64_t outputs = static_cast<std::int64_t>(M) * N;
-    split_reduce_kernel<<<blocks_for(outputs, 256), 256, 0, stream>>>(partial, c, bias, slices, M, N, ldc);
+    split_reduce_kernel<<<blocks_for(outputs, 256), 256, 0, stream>>>(partial, c, e.bias, e.bias_mode, e.act, e.alpha,
+                                                                        slices, M, N, ldc);
     return MFH_CHECK_LAUNCH("split_reduce", stream);
 }
 
 int split_reduce(const float* partial, float* c, int slices, int M, int N, int ldc, bool /*reference*/,
                  hipStream_t stream) {
-    return split_reduce_bias(partial, c, nullptr, slices, M, N, ldc, stream);
+    return split_reduce_epilogue(partial, c, GemmEpilogue{}, slices, M, N, ldc, stream);
 }
 
-int gemm_rows_bias(int engine, hipStream_t stream, bool trans_a, bool trans_b, int M, int N, int K, const float* a,
-                   int lda, const float* b, int ldb, float* c, int ldc, const float* bias, float* workspace,
-                   std::int64_t workspace_floats) {
-    if (trans_a && trans_b) return MFH_FAIL(ERR_ARG, "the GEMM engine has no A^T B^T kernel");
+int gemm_launch(int engine, hipStream_t stream, const GemmOperands& o, const GemmEpilogue& e, float* workspace,
+                std::int64_t workspace_floats) {
+    const int M = o.M, N = o.N, K = o.K;
     GemmPlan plan;
     MFH_TRY(gemm_plan_from_engine(engine, M, N, K, &plan));
-    if (plan.slices > 1 && (!workspace || workspace_floats < gemm_workspace_floats(plan, M, N)))
+    if (o.batch > 1 || (plan.slices > 1 && (!workspace || workspace_floats < gemm_workspace_floats(plan, M, N))))
         plan = GemmPlan{plan.tile, 1, K};
     const bool split = plan.slices > 1;
-    float* out = split ? workspace : c;
-    const int ld_out = split ? N : ldc;
-    const long long stride = split ? static_cast<long long>(M) * N : 0;
-    const auto aligned = [](const void* p) { return (reinterpret_cast<std::uintptr_t>(p) & 15) == 0; };
-    // float4 loads need the contiguous extent of each operand, the leading dimensions and the
-    // pointers to be multiples of 4 floats / 16 bytes; the K slices are multiples of BK.
-    const bool vec = (trans_a ? M : K) % 4 == 0 && (trans_b ? K : N) % 4 == 0 && lda % 4 == 0 && ldb % 4 == 0 &&
-                     aligned(a) && aligned(b);
+    // float4 loads need the contiguous extent of each operand, its leading dimension, its batch
+    // stride and its base pointer to be multiples of 4 floats / 16 bytes; K slices are multiples of BK.
+    const bool vec = (o.trans_a ? M : K) % 4 == 0 && (o.trans_b ? K : N) % 4 == 0 && o.lda % 4 == 0 &&
+                     o.ldb % 4 == 0 && o.a_batch % 4 == 0 && o.b_batch % 4 == 0 && aligned16(o.a) && aligned16(o.b);
     const GemmTile& tile = TILES[plan.tile];
     if (blocks_for(M, tile.bm) > GRID_YZ_LIMIT) return MFH_FAIL(ERR_ARG, "GEMM rows exceed the grid limit");
-    const int layout = trans_a ? 2 : trans_b ? 1 : 0;  // nn, nt, tn
+    if (static_cast<unsigned>(o.batch) > GRID_YZ_LIMIT) return MFH_FAIL(ERR_ARG, "GEMM batch exceeds the grid limit");
+    GemmParams p{};
+    p.A = o.a;
+    p.B = o.b;
+    p.M = M;
+    p.N = N;
+    p.K = K;
+    p.lda = o.lda;
+    p.ldb = o.ldb;
+    p.a_batch = o.a_batch;
+    p.b_batch = o.b_batch;
+    if (split) {
+        p.C = workspace;
+        p.ldc = N;
+        p.c_batch = static_cast<long long>(M) * N;
+        p.split = 1;
+        p.k_chunk = plan.k_chunk;
+    } else {
+        p.C = o.c;
+        p.ldc = o.ldc;
+        p.c_batch = o.c_batch;
+        p.split = 0;
+        p.k_chunk = K;
+        p.bias = e.bias;
+        p.bias_mode = e.bias_mode;
+        p.act = e.act;
+        p.alpha = e.alpha;
+    }
+    const int layout = (o.trans_a ? 2 : 0) + (o.trans_b ? 1 : 0);  // NN, NT, TN, TT
     const GemmFn fn = kernel_table().fn[plan.tile][layout * 2 + (vec ? 1 : 0)];
-    const dim3 grid(blocks_for(N, tile.bn), blocks_for(M, tile.bm), plan.slices);
-    hipLaunchKernelGGL(fn, grid, dim3(threads_of(tile)), 0, stream, a, b, out, split ? nullptr : bias, M, N, K, lda,
-                       ldb, ld_out, plan.k_chunk, stride);
+    const dim3 grid(blocks_for(N, tile.bn), blocks_for(M, tile.bm), split ? plan.slices : o.batch);
+    hipLaunchKernelGGL(fn, grid, dim3(threads_of(tile)), 0, stream, p);
     MFH_TRY(MFH_CHECK_LAUNCH("gemm_mfma", stream));
     if (!split) return OK;
-    return split_reduce_bias(workspace, c, bias, plan.slices, M, N, ldc, stream);
-}
-
-int gemm_rows(int engine, hipStream_t stream, bool trans_a, bool trans_b, int M, int N, int K, const float* a,
-              int lda, const float* b, int ldb, float* c, int ldc, float* workspace, std::int64_t workspace_floats) {
-    return gemm_rows_bias(engine, stream, trans_a, trans_b, M, N, K, a, lda, b, ldb, c, ldc, nullptr, workspace,
-                          workspace_floats);
+    return split_reduce_epilogue(workspace, o.c, e, plan.slices, M, N, o.ldc, stream);
 }
 
 }  // namespace mfh

@@ -1,196 +1,195 @@
-// The lecture matmul family behind native.matmul: C(M,N) = A(M,K) B(K,N), all row-major, with
-// three summation modes. These kernels are the correctness and accuracy references of the API;
-// the fast path is the MFMA engine in gemm.hip.
-//   accumulate 0: sequential FMA.
-//   accumulate 1: FMA inside groups of G consecutive terms; groups are combined with TwoSum and the
-//                 rounding errors are carried in a separate compensation term (Kahan-style).
-//   accumulate 2: Dot2 of Ogita, Rump and Oishi (SIAM J. Sci. Comput. 26(6), 2005): TwoProduct and
-//                 TwoSum on every term, i.e. the dot product as if accumulated in twice the working
-//                 precision and rounded once.
-// Error-free transformations must not be contracted into FMAs, so they are compiled with
-// contraction off; the FMA in TwoProduct is explicit.
+// The teaching matmul family behind native.matmul: C(M,N) = A(M,K) B(K,N), all row-major, with
+// three summation modes. These kernels are the accuracy references of the API; the fast path is the
+// MFMA engine in gemm.hip.
+//
+// Summation modes (per output element, terms taken in increasing k):
+//   SEQUENTIAL   one FMA chain over all K terms.
+//   GROUPED      an FMA chain inside each group of G consecutive terms; each group's chain is folded
+//                into a compensated pair (sum, err) with Knuth's TwoSum, so the error no longer
+//                grows with K.
+//   DOT2         Ogita, Rump and Oishi, "Accurate sum and dot product", SIAM J. Sci. Comput. 26(6),
+//                2005, Algorithm Dot2: every product is split exactly (TwoProduct via FMA) and added
+//                with TwoSum, as if accumulated in twice the working precision and rounded once.
+// The error-free transformations are compiled with contraction off; the FMA in TwoProduct is
+// explicit. Group sizes: 32 for the one-thread-per-output and register-blocked kernels, TILE for
+// the tiled and LDS kernels, so the register-blocked kernel repeats the exact operation sequence of
+// the one-thread-per-output kernel and the two agree bit for bit.
 #include "common.h"
 
 namespace mfh {
 namespace {
 
-__device__ __forceinline__ void two_sum(float a, float b, float& s, float& e) {
+enum SumMode { SEQUENTIAL = 0, GROUPED = 1, DOT2 = 2 };
+
+// Knuth's TwoSum: hi + lo == a + b exactly, hi = fl(a + b).
+__device__ __forceinline__ void knuth_two_sum(float a, float b, float& hi, float& lo) {
 #pragma clang fp contract(off)
-    s = a + b;
-    const float z = s - a;
-    e = (a - (s - z)) + (b - z);
+    hi = a + b;
+    const float b_virtual = hi - a;
+    const float a_virtual = hi - b_virtual;
+    lo = (a - a_virtual) + (b - b_virtual);
 }
 
-template <int ACC>
-struct Accum;
+// Running state of one output element.
+template <int MODE>
+struct DotState {
+    float chain = 0.f;  // SEQUENTIAL, GROUPED: the current FMA chain
+    float sum = 0.f;    // GROUPED, DOT2: compensated pair
+    float err = 0.f;
 
-template <>
-struct Accum<0> {
-    float s = 0.f;
-    __device__ __forceinline__ void add(float a, float b) { s = __builtin_fmaf(a, b, s); }
-    __device__ __forceinline__ void group_end() {}
-    __device__ __forceinline__ float result() { return s; }
-};
+    __device__ __forceinline__ void term(float a, float b) {
+#pragma clang fp contract(off)
+        if constexpr (MODE == DOT2) {
+            const float product = a * b;
+            const float product_err = __builtin_fmaf(a, b, -product);
+            float hi, lo;
+            knuth_two_sum(sum, product, hi, lo);
+            err = err + (lo + product_err);
+            sum = hi;
+        } else {
+            chain = __builtin_fmaf(a, b, chain);
+        }
+    }
 
-template <>
-struct Accum<1> {
-    float s = 0.f, c = 0.f, part = 0.f;
-    __device__ __forceinline__ void add(float a, float b) { part = __builtin_fmaf(a, b, part); }
-    __device__ __forceinline__ void group_end() {
+    __device__ __forceinline__ void close_group() {
 #pragma clang fp contract(off)
-        float t, e;
-        two_sum(s, part, t, e);
-        c = c + e;
-        s = t;
-        part = 0.f;
+        if constexpr (MODE == GROUPED) {
+            float hi, lo;
+            knuth_two_sum(sum, chain, hi, lo);
+            err = err + lo;
+            sum = hi;
+            chain = 0.f;
+        }
     }
-    __device__ __forceinline__ float result() {
-#pragma clang fp contract(off)
-        group_end();
-        return s + c;
-    }
-};
 
-template <>
-struct Accum<2> {
-    float s = 0.f, c = 0.f;
-    __device__ __forceinline__ void add(float a, float b) {
+    __device__ __forceinline__ float value() {
 #pragma clang fp contract(off)
-        const float p = a * b;
-        const float pe = __builtin_fmaf(a, b, -p);
-        float t, se;
-        two_sum(s, p, t, se);
-        c = c + (se + pe);
-        s = t;
-    }
-    __device__ __forceinline__ void group_end() {}
-    __device__ __forceinline__ float result() {
-#pragma clang fp contract(off)
-        return s + c;
+        if constexpr (MODE == SEQUENTIAL) return chain;
+        close_group();
+        return sum + err;
     }
 };
 
-// Row of A (stride 1) times column of B (stride N) from global memory, in groups of G terms.
-template <int G, int ACC>
-__device__ __forceinline__ float dot_global(const float* a, const float* b, int N, int K) {
-    Accum<ACC> acc;
+// Row `a` (stride 1) times column `b` (stride ldb) from global memory, groups of G terms.
+template <int G, int MODE>
+__device__ __forceinline__ float global_dot(const float* a, const float* b, int ldb, int K) {
+    DotState<MODE> st;
     for (int k0 = 0; k0 < K; k0 += G) {
         const int k1 = min(k0 + G, K);
-        for (int k = k0; k < k1; ++k) acc.add(a[k], b[static_cast<long long>(k) * N]);
-        acc.group_end();
+        for (int k = k0; k < k1; ++k) st.term(a[k], b[static_cast<long long>(k) * ldb]);
+        st.close_group();
     }
-    return acc.result();
+    return st.value();
 }
 
-// basic: one thread per output element on a 1-D grid.
-template <int ACC>
-__global__ __launch_bounds__(256) void matmul_basic(const float* A, const float* B, float* C, int M, int N, int K) {
-    const int idx = blockIdx.x * 256 + threadIdx.x;
-    if (idx >= M * N) return;
-    const int row = idx / N, col = idx % N;
-    C[idx] = dot_global<32, ACC>(A + static_cast<long long>(row) * K, B + col, N, K);
+// One thread per output element on a 1-D grid of 256-thread workgroups.
+template <int MODE>
+__global__ __launch_bounds__(256) void matmul_per_output(const float* A, const float* B, float* C, int M, int N,
+                                                         int K) {
+    const long long e = static_cast<long long>(blockIdx.x) * 256 + threadIdx.x;
+    if (e >= static_cast<long long>(M) * N) return;
+    const int i = static_cast<int>(e / N), j = static_cast<int>(e % N);
+    C[e] = global_dot<32, MODE>(A + static_cast<long long>(i) * K, B + j, N, K);
 }
 
-// tiled: TILE x TILE thread blocks, one per output tile, operands straight from global memory.
-template <int TILE, int ACC>
+// TILE x TILE workgroups, one per output tile, operands straight from global memory.
+template <int TILE, int MODE>
 __global__ __launch_bounds__(TILE* TILE) void matmul_tiled(const float* A, const float* B, float* C, int M, int N,
                                                            int K) {
-    const int row = blockIdx.y * TILE + threadIdx.y, col = blockIdx.x * TILE + threadIdx.x;
-    if (row >= M || col >= N) return;
-    C[static_cast<long long>(row) * N + col] = dot_global<TILE, ACC>(A + static_cast<long long>(row) * K, B + col, N, K);
+    const int i = blockIdx.y * TILE + threadIdx.y, j = blockIdx.x * TILE + threadIdx.x;
+    if (i < M && j < N) C[static_cast<long long>(i) * N + j] = global_dot<TILE, MODE>(A + static_cast<long long>(i) * K, B + j, N, K);
 }
 
-// shared: TILE x TILE tiles of A and B staged in LDS, each element reused TILE times.
-template <int TILE, int ACC>
-__global__ __launch_bounds__(TILE* TILE) void matmul_shared(const float* A, const float* B, float* C, int M, int N,
-                                                            int K) {
-    __shared__ float As[TILE][TILE + 1];
-    __shared__ float Bs[TILE][TILE + 1];
-    const int tx = threadIdx.x, ty = threadIdx.y;
-    const int row = blockIdx.y * TILE + ty, col = blockIdx.x * TILE + tx;
-    Accum<ACC> acc;
+// TILE x TILE tiles of A and B staged in LDS; each staged element is used TILE times.
+template <int TILE, int MODE>
+__global__ __launch_bounds__(TILE* TILE) void matmul_lds(const float* A, const float* B, float* C, int M, int N,
+                                                         int K) {
+    __shared__ float a_tile[TILE][TILE + 1];
+    __shared__ float b_tile[TILE][TILE + 1];
+    const int c = threadIdx.x, r = threadIdx.y;
+    const int i = blockIdx.y * TILE + r, j = blockIdx.x * TILE + c;
+    DotState<MODE> st;
     for (int k0 = 0; k0 < K; k0 += TILE) {
-        As[ty][tx] = (row < M && k0 + tx < K) ? A[static_cast<long long>(row) * K + k0 + tx] : 0.f;
-        Bs[ty][tx] = (k0 + ty < K && col < N) ? B[static_cast<long long>(k0 + ty) * N + col] : 0.f;
+        a_tile[r][c] = (i < M && k0 + c < K) ? A[static_cast<long long>(i) * K + k0 + c] : 0.f;
+        b_tile[r][c] = (k0 + r < K && j < N) ? B[static_cast<long long>(k0 + r) * N + j] : 0.f;
         __syncthreads();
-        const int kn = min(TILE, K - k0);
-        for (int k = 0; k < kn; ++k) acc.add(As[ty][k], Bs[k][tx]);
-        acc.group_end();
+        const int depth = min(TILE, K - k0);
+        for (int k = 0; k < depth; ++k) st.term(a_tile[r][k], b_tile[k][c]);
+        st.close_group();
         __syncthreads();
     }
-    if (row < M && col < N) C[static_cast<long long>(row) * N + col] = acc.result();
+    if (i < M && j < N) C[static_cast<long long>(i) * N + j] = st.value();
 }
 
-// register: 64 x 64 block tiles, 256 threads with 4 x 4 outputs each (rows ty + 16 i, columns
-// tx + 16 j), BK = 32 deep LDS stages. Every output sums k = 0 .. K-1 in order with a group end
-// after each 32 terms, exactly the operation sequence of matmul_basic, so the two agree bit for bit.
-template <int ACC>
-__global__ __launch_bounds__(256) void matmul_register(const float* A, const float* B, float* C, int M, int N, int K) {
-    constexpr int BT = 64, BK = 32;
-    __shared__ float As[BK][BT + 1];
-    __shared__ float Bs[BK][BT + 1];
-    const int tid = threadIdx.x, tx = tid % 16, ty = tid / 16;
-    const int m0 = blockIdx.y * BT, n0 = blockIdx.x * BT;
-    Accum<ACC> acc[4][4];
-    for (int k0 = 0; k0 < K; k0 += BK) {
-        for (int f = tid; f < BT * BK; f += 256) {
-            const int r = f / BK, k = f % BK;  // A: 64 rows x 32 k, read along k
-            const int row = m0 + r;
-            As[k][r] = (row < M && k0 + k < K) ? A[static_cast<long long>(row) * K + k0 + k] : 0.f;
-            const int kb = f / BT, c = f % BT;  // B: 32 k x 64 columns, read along columns
-            const int col = n0 + c;
-            Bs[kb][c] = (k0 + kb < K && col < N) ? B[static_cast<long long>(k0 + kb) * N + col] : 0.f;
+// Register-blocked: 64 x 64 workgroup tiles, 256 threads with 4 x 4 outputs each (rows ry + 16 u,
+// columns rx + 16 v), 32-deep LDS stages. Each stage is one group of 32 terms, in increasing k.
+template <int MODE>
+__global__ __launch_bounds__(256) void matmul_register(const float* A, const float* B, float* C, int M, int N,
+                                                       int K) {
+    constexpr int T = 64, D = 32;
+    __shared__ float a_stage[D][T + 1];
+    __shared__ float b_stage[D][T + 1];
+    const int tid = threadIdx.x, rx = tid % 16, ry = tid / 16;
+    const int i0 = blockIdx.y * T, j0 = blockIdx.x * T;
+    DotState<MODE> st[4][4];
+    for (int k0 = 0; k0 < K; k0 += D) {
+        for (int f = tid; f < T * D; f += 256) {
+            const int ar = f / D, ak = f % D;  // A: 64 rows x 32 k, read along k
+            a_stage[ak][ar] = (i0 + ar < M && k0 + ak < K) ? A[static_cast<long long>(i0 + ar) * K + k0 + ak] : 0.f;
+            const int bk = f / T, bc = f % T;  // B: 32 k x 64 columns, read along columns
+            b_stage[bk][bc] = (k0 + bk < K && j0 + bc < N) ? B[static_cast<long long>(k0 + bk) * N + j0 + bc] : 0.f;
         }
         __syncthreads();
-        const int kn = min(BK, K - k0);
-        for (int k = 0; k < kn; ++k) {
-            float a[4], b[4];
+        const int depth = min(D, K - k0);
+        for (int k = 0; k < depth; ++k) {
+            float av[4], bv[4];
 #pragma unroll
-            for (int i = 0; i < 4; ++i) a[i] = As[k][ty + 16 * i];
+            for (int u = 0; u < 4; ++u) av[u] = a_stage[k][ry + 16 * u];
 #pragma unroll
-            for (int j = 0; j < 4; ++j) b[j] = Bs[k][tx + 16 * j];
+            for (int v = 0; v < 4; ++v) bv[v] = b_stage[k][rx + 16 * v];
 #pragma unroll
-            for (int i = 0; i < 4; ++i)
+            for (int u = 0; u < 4; ++u)
 #pragma unroll
-                for (int j = 0; j < 4; ++j) acc[i][j].add(a[i], b[j]);
+                for (int v = 0; v < 4; ++v) st[u][v].term(av[u], bv[v]);
         }
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
+        for (int u = 0; u < 4; ++u)
 #pragma unroll
-            for (int j = 0; j < 4; ++j) acc[i][j].group_end();
+            for (int v = 0; v < 4; ++v) st[u][v].close_group();
         __syncthreads();
     }
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int u = 0; u < 4; ++u)
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const int row = m0 + ty + 16 * i, col = n0 + tx + 16 * j;
-            if (row < M && col < N) C[static_cast<long long>(row) * N + col] = acc[i][j].result();
+        for (int v = 0; v < 4; ++v) {
+            const int i = i0 + ry + 16 * u, j = j0 + rx + 16 * v;
+            if (i < M && j < N) C[static_cast<long long>(i) * N + j] = st[u][v].value();
         }
 }
 
-template <int ACC>
-int launch_acc(int variant, int tile, const float* a, const float* b, float* c, int M, int N, int K,
-               hipStream_t stream) {
+template <int MODE>
+int launch_mode(int variant, int tile, const float* a, const float* b, float* c, int M, int N, int K,
+                hipStream_t stream) {
     if (variant == 0) {
-        matmul_basic<ACC><<<blocks_for(static_cast<std::int64_t>(M) * N, 256), 256, 0, stream>>>(a, b, c, M, N, K);
-        return MFH_CHECK_LAUNCH("matmul_basic", stream);
+        matmul_per_output<MODE><<<blocks_for(static_cast<std::int64_t>(M) * N, 256), 256, 0, stream>>>(a, b, c, M, N,
+                                                                                                       K);
+        return MFH_CHECK_LAUNCH("matmul_per_output", stream);
     }
     if (variant == 4) {
         if (blocks_for(M, 64) > GRID_YZ_LIMIT) return MFH_FAIL(ERR_ARG, "matmul rows exceed the grid limit");
-        matmul_register<ACC><<<dim3(blocks_for(N, 64), blocks_for(M, 64)), 256, 0, stream>>>(a, b, c, M, N, K);
+        matmul_register<MODE><<<dim3(blocks_for(N, 64), blocks_for(M, 64)), 256, 0, stream>>>(a, b, c, M, N, K);
         return MFH_CHECK_LAUNCH("matmul_register", stream);
     }
     if (blocks_for(M, tile) > GRID_YZ_LIMIT) return MFH_FAIL(ERR_ARG, "matmul rows exceed the grid limit");
     const dim3 grid(blocks_for(N, tile), blocks_for(M, tile)), block(tile, tile);
     if (variant == 1) {
-        if (tile == 16) matmul_tiled<16, ACC><<<grid, block, 0, stream>>>(a, b, c, M, N, K);
-        else matmul_tiled<32, ACC><<<grid, block, 0, stream>>>(a, b, c, M, N, K);
+        if (tile == 16) matmul_tiled<16, MODE><<<grid, block, 0, stream>>>(a, b, c, M, N, K);
+        else matmul_tiled<32, MODE><<<grid, block, 0, stream>>>(a, b, c, M, N, K);
         return MFH_CHECK_LAUNCH("matmul_tiled", stream);
     }
-    if (tile == 16) matmul_shared<16, ACC><<<grid, block, 0, stream>>>(a, b, c, M, N, K);
-    else matmul_shared<32, ACC><<<grid, block, 0, stream>>>(a, b, c, M, N, K);
-    return MFH_CHECK_LAUNCH("matmul_shared", stream);
+    if (tile == 16) matmul_lds<16, MODE><<<grid, block, 0, stream>>>(a, b, c, M, N, K);
+    else matmul_lds<32, MODE><<<grid, block, 0, stream>>>(a, b, c, M, N, K);
+    return MFH_CHECK_LAUNCH("matmul_lds", stream);
 }
 
 }  // namespace
@@ -198,9 +197,9 @@ int launch_acc(int variant, int tile, const float* a, const float* b, float* c, 
 int launch_matmul(int variant, int tile, int accumulate, const float* a, const float* b, float* c, int M, int N,
                   int K, hipStream_t stream) {
     switch (accumulate) {
-        case 0: return launch_acc<0>(variant, tile, a, b, c, M, N, K, stream);
-        case 1: return launch_acc<1>(variant, tile, a, b, c, M, N, K, stream);
-        default: return launch_acc<2>(variant, tile, a, b, c, M, N, K, stream);
+        case SEQUENTIAL: return launch_mode<SEQUENTIAL>(variant, tile, a, b, c, M, N, K, stream);
+        case GROUPED: return launch_mode<GROUPED>(variant, tile, a, b, c, M, N, K, stream);
+        default: return launch_mode<DOT2>(variant, tile, a, b, c, M, N, K, stream);
     }
 }
 

@@ -1,15 +1,14 @@
-"""Device selection for the framework's arrays (torch tensors).
-
-Mirrors the reference's global CPU/CUDA switch (``core/device.py:146-170``): parameters and inputs
-are created on the active device. The ``hip_native`` operators run only on the GPU; handing them CPU
-tensors raises the same ``ValueError`` the reference raises for a native backend on the CPU device.
+"""The active device for new parameters and inputs (the reference's CPU / CUDA switch,
+``core/device.py:146-170``). Arrays are torch tensors; ``"cuda"`` is the current HIP GPU. The
+hip_native operators run only on the GPU and reject CPU tensors with a ValueError.
 """
 
 from __future__ import annotations
 
 import torch
 
-_DEVICE = "cuda" if torch.cuda.is_available() else "cpu"
+_active = "cuda" if torch.cuda.is_available() else "cpu"
+_GPU_NAMES = ("cuda", "gpu", "hip", "cuda:0")
 
 
 def cuda_available() -> bool:
@@ -17,29 +16,29 @@ def cuda_available() -> bool:
 
 
 def get_device() -> str:
-    return _DEVICE
+    return _active
 
 
 def set_device(device: str) -> str:
-    global _DEVICE
+    global _active
     name = str(device).strip().lower()
     if name == "cpu":
-        _DEVICE = "cpu"
-    elif name in ("cuda", "gpu", "hip", "cuda:0"):
+        _active = "cpu"
+    elif name in _GPU_NAMES:
         if not torch.cuda.is_available():
             raise RuntimeError("a GPU was requested but none is visible")
-        _DEVICE = "cuda"
+        _active = "cuda"
     else:
         raise ValueError(f"unsupported device {device!r}; use 'cpu' or 'cuda'")
-    return _DEVICE
+    return _active
 
 
 def torch_device():
-    return torch.device("cuda", torch.cuda.current_device()) if _DEVICE == "cuda" else torch.device("cpu")
+    return torch.device("cuda", torch.cuda.current_device()) if _active == "cuda" else torch.device("cpu")
 
 
 def asarray(value, dtype=torch.float32):
-    """A tensor on the active device (numpy arrays and Python values are copied there)."""
+    """A tensor of ``dtype`` on the active device (NumPy arrays and Python values are copied)."""
     if isinstance(value, torch.Tensor):
         return value.to(device=torch_device(), dtype=dtype)
     return torch.as_tensor(value, dtype=dtype, device=torch_device())

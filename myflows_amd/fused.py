@@ -1,0 +1,190 @@
+"""Batch norm (+ residual + ReLU), ReLU backward and Adam on libmfhip.
+
+Same names, arguments and results as the reference's ``ops/fused.py``: ``batchnorm2d_forward``
+(:250-305), ``batchnorm2d_backward`` (:308-380), ``relu_backward_accumulate`` /
+``leaky_relu_backward_accumulate`` (:50-77), ``adam_update`` (:514-533) and ``adam_update_many``
+(:609-621). Every tensor is a float32 GPU tensor; there is no host path.
+"""
+
+from __future__ import annotations
+
+from functools import lru_cache
+
+import torch
+
+from . import native
+
+
+def _f32(value, name):
+    return native._device_f32(value, name)
+
+
+@lru_cache(maxsize=256)
+def _bn_workspace_doubles(n, c, hw):
+    doubles = native._library().mfh_bn_workspace(n, c, hw)
+    if doubles < 0:
+        native._raise_for(2, native._library())
+    return doubles
+
+
+def _bn_shape(x):
+    if x.ndim != 4:
+        raise ValueError("batch norm expects an NCHW tensor")
+    n, c, h, w = (int(v) for v in x.shape)
+    native._within_int32(x=n * c * h * w)
+    return n, c, h * w
+
+
+def _channel_vector(value, c, name):
+    value = _f32(value, name)
+    if tuple(value.shape) != (c,):
+        raise ValueError(f"{name} must have shape (C,)")
+    return value
+
+
+def batchnorm2d_forward(x, gamma, beta, running_mean, running_var, *, momentum, eps, training,
+                        unbiased_running_var=False, relu=False, residual=None):
+    """(y, mean, inv_std); updates running_mean / running_var in place when training.
+
+    mean has shape (2, C): the FP64 batch mean as the float pair mean[0] + mean[1], to be passed
+    unchanged to batchnorm2d_backward. The normalisation uses the biased batch variance; with
+    unbiased_running_var the running variance tracks count / (count - 1) times it.
+    """
+    x = _f32(x, "x")
+    n, c, hw = _bn_shape(x)
+    gamma, beta = _channel_vector(gamma, c, "gamma"), _channel_vector(beta, c, "beta")
+    for name, stat in (("running_mean", running_mean), ("running_var", running_var)):
+        if not (isinstance(stat, torch.Tensor) and stat.dtype == torch.float32 and stat.is_cuda
+                and stat.is_contiguous() and tuple(stat.shape) == (c,)):
+            raise ValueError(f"{name} must be a contiguous float32 GPU tensor of shape (C,)")
+    if residual is not None:
+        residual = _f32(residual, "residual")
+        if residual.shape != x.shape:
+            raise ValueError("residual must have x's shape")
+    count = n * hw
+    var_scale = count / (count - 1) if unbiased_running_var and count > 1 else 1.0
+    y = torch.empty_like(x)
+    mean = torch.empty((2, c), dtype=torch.float32, device=x.device)
+    inv_std = torch.empty((c,), dtype=torch.float32, device=x.device)
+    doubles = _bn_workspace_doubles(n, c, hw) if training else 0
+    workspace = torch.empty(doubles, dtype=torch.float64, device=x.device) if doubles else None
+    native._call("mfh_bn_forward", x.data_ptr(), gamma.data_ptr(), beta.data_ptr(), running_mean.data_ptr(),
+                 running_var.data_ptr(), native._addr(residual), y.data_ptr(), mean.data_ptr(), inv_std.data_ptr(),
+                 native._addr(workspace), doubles, n, c, hw, int(bool(training)), int(bool(relu)), float(momentum),
+                 float(eps), float(var_scale), native._stream())
+    return y, mean, inv_std
+
+
+def _gradient_buffer(value, like, name):
+    if value is None:
+        return None
+    if not (isinstance(value, torch.Tensor) and value.dtype == torch.float32 and value.is_cuda
+            and value.is_contiguous() and value.shape == like.shape):
+        raise ValueError(f"{name} must be a contiguous float32 GPU tensor shaped like its forward value")
+    return value
+
+
+def batchnorm2d_backward(x, dy, gamma, mean, inv_std, *, training, x_grad, gamma_grad, beta_grad,
+                         accumulate=(True, True, True), gate=None, residual_grad=None, add_residual=False):
+    """Write (or add, per ``accumulate``) the requested gradients into x_grad, gamma_grad and beta_grad.
+
+    With ``gate`` (the output of a fused ReLU) dy counts only where gate > 0, and that gated dy is
+    also stored (or added, with add_residual) into ``residual_grad``.
+    """
+    x, dy = _f32(x, "x"), _f32(dy, "dy")
+    n, c, hw = _bn_shape(x)
+    if dy.shape != x.shape:
+        raise ValueError("dy must have x's shape")
+    gamma = _channel_vector(gamma, c, "gamma")
+    mean, inv_std = _f32(mean, "mean"), _channel_vector(inv_std, c, "inv_std")
+    if tuple(mean.shape) != (2, c):
+        raise ValueError("mean must be the (2, C) pair from batchnorm2d_forward")
+    x_grad = _gradient_buffer(x_grad, x, "x_grad")
+    gamma_grad = _gradient_buffer(gamma_grad, gamma, "gamma_grad")
+    beta_grad = _gradient_buffer(beta_grad, gamma, "beta_grad")
+    if gate is not None:
+        gate = _f32(gate, "gate")
+        if gate.shape != x.shape:
+            raise ValueError("gate must have x's shape")
+    elif residual_grad is not None:
+        raise ValueError("a residual gradient needs the fused ReLU's output as gate")
+    residual_grad = _gradient_buffer(residual_grad, x, "residual_grad")
+    if x_grad is None and gamma_grad is None and beta_grad is None and residual_grad is None:
+        return
+    doubles = _bn_workspace_doubles(n, c, hw)
+    workspace = torch.empty(doubles, dtype=torch.float64, device=x.device)
+    add_x, add_gamma, add_beta = (int(bool(a)) for a in accumulate)
+    native._call("mfh_bn_backward", x.data_ptr(), dy.data_ptr(), native._addr(gate), gamma.data_ptr(),
+                 mean.data_ptr(), inv_std.data_ptr(), native._addr(x_grad), native._addr(gamma_grad),
+                 native._addr(beta_grad), native._addr(residual_grad), workspace.data_ptr(), doubles, n, c, hw,
+                 int(bool(training)), add_x, add_gamma, add_beta, int(bool(add_residual)), native._stream())
+
+
+def relu_forward(x):
+    """max(0, x) (NaN stays NaN)."""
+    x = _f32(x, "x")
+    y = torch.empty_like(x)
+    native._call("mfh_relu_forward", x.data_ptr(), y.data_ptr(), x.numel(), native._stream())
+    return y
+
+
+def _relu_backward(x, grad, out, alpha):
+    x, grad = _f32(x, "x"), _f32(grad, "grad")
+    if grad.shape != x.shape:
+        raise ValueError("grad must have x's shape")
+    add = out is not None
+    if out is None:
+        out = torch.empty_like(x)
+    elif not (isinstance(out, torch.Tensor) and out.dtype == torch.float32 and out.is_cuda and out.is_contiguous()
+              and out.shape == x.shape):
+        raise ValueError("out must be a contiguous float32 GPU tensor shaped like x")
+    native._call("mfh_relu_backward", x.data_ptr(), grad.data_ptr(), out.data_ptr(), x.numel(), float(alpha),
+                 int(add), native._stream())
+    return out
+
+
+def relu_backward_accumulate(x, grad, out):
+    """out += grad where x > 0 (a new tensor when out is None)."""
+    return _relu_backward(x, grad, out, 0.0)
+
+
+def leaky_relu_backward_accumulate(x, grad, out, alpha):
+    """out += grad where x > 0 and alpha * grad elsewhere (a new tensor when out is None)."""
+    return _relu_backward(x, grad, out, float(alpha))
+
+
+def _adam_row(param, grad, m, v, lr, decay, step, beta1, beta2):
+    # The scalars are formed in double precision and rounded once to float32 by the c_float fields.
+    tensors = [_f32(t, name) for t, name in ((param, "param"), (grad, "grad"), (m, "m"), (v, "v"))]
+    for t, original in zip(tensors, (param, grad, m, v)):
+        if t.data_ptr() != original.data_ptr() or t.shape != param.shape:
+            raise ValueError("Adam updates contiguous tensors of the parameter's shape in place")
+    return native.AdamTensor(param.data_ptr(), grad.data_ptr(), m.data_ptr(), v.data_ptr(), param.numel(),
+                             float(lr), float(decay), 1.0 - beta1 ** step, 1.0 - beta2 ** step)
+
+
+def _adam_launch(rows, beta1, beta2, eps, grad_scale):
+    if not rows:
+        return
+    table = (native.AdamTensor * len(rows))(*rows)
+    native._call("mfh_adam_step", table, len(rows), float(grad_scale), float(beta1), 1.0 - beta1, float(beta2),
+                 1.0 - beta2, float(eps), native._stream())
+
+
+def adam_update(param, grad, m, v, *, lr, beta1, beta2, eps, step, grad_scale=1.0, weight_decay=0.0):
+    """One Adam step (zero-initialised moments, bias-corrected) applied in place."""
+    _adam_launch([_adam_row(param, grad, m, v, lr, weight_decay, step, beta1, beta2)], beta1, beta2, eps, grad_scale)
+
+
+def adam_update_many(updates, *, beta1, beta2, eps, grad_scale):
+    """Adam for (param, grad, m, v, lr, decay, step) tuples in one multi-tensor launch per 16 tensors.
+
+    The tensors must not overlap one another (each parameter is read and written once).
+    """
+    rows = [_adam_row(p, g, m, v, lr, decay, step, beta1, beta2) for p, g, m, v, lr, decay, step in updates]
+    spans = sorted((t.data_ptr(), t.data_ptr() + 4 * t.numel()) for p, g, m, v, *_ in updates for t in (p, m, v)
+                   if t.numel())
+    for (_, end), (start, _) in zip(spans, spans[1:]):
+        if start < end:
+            raise ValueError("adam_update_many needs non-overlapping parameters and moments")
+    _adam_launch(rows, beta1, beta2, eps, grad_scale)

@@ -1,0 +1,256 @@
+"""The dynamic graph: nodes, leaves and the executor that runs them over torch GPU tensors.
+
+Keeps the semantics of the reference's ``core/node.py:5-123`` and ``core/graph.py:5-162``, so the
+``hip_native`` operators plug in under an unchanged Variable/Graph API:
+
+* ``Variable(value, trainable, name, constant, requires_grad)``: a trainable leaf always needs a
+  gradient; another leaf with ``requires_grad=False`` (input images, labels) lets the operators
+  skip the gradient work for it (e.g. the dX GEMMs of the stem convolution);
+* ``accumulate_grad(contribution, owned=...)``: the first contribution becomes the gradient (kept
+  without a copy only when its producer hands it over), later ones are added in place, each
+  rounded to the value's dtype;
+* ``Graph(target)``: topological order; for each combination of leaf flags (and retained
+  intermediates) an execution plan of which nodes need gradients; ``forward()`` in order,
+  ``backward()`` in reverse seeded with ones; intermediate gradients are released as soon as their
+  node has consumed them.
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass
+
+import torch
+
+
+class Node:
+    """A vertex of the graph: parents in, one value out, one gradient back."""
+
+    # Set per node by the executing Graph; a standalone operator behaves as if it needs gradients.
+    requires_grad = True
+
+    def __init__(self, *parents, trainable=False, name=None):
+        self.parents = list(parents)
+        self.children = []
+        for parent in self.parents:
+            parent.children.append(self)
+        self.value = None
+        self.grad = None
+        self.trainable = trainable
+        self.name = name or type(self).__name__
+
+    def forward(self, *inputs):
+        raise NotImplementedError
+
+    def backward(self):
+        raise NotImplementedError
+
+    def clear_grad(self):
+        """Zero gradient of the value's shape (None before the first forward)."""
+        self.grad = None if self.value is None else torch.zeros_like(self.value)
+
+    def accumulate_grad(self, contribution, *, owned=False):
+        """Add a gradient contribution. The first one becomes the gradient: as is when the caller
+        owns a fresh contiguous tensor of the value's shape (owned=True), otherwise as a copy."""
+        target = self.value
+        if not isinstance(contribution, torch.Tensor):
+            contribution = torch.as_tensor(contribution, device=target.device)
+        if self.grad is not None:
+            self.grad += contribution.to(target.dtype)
+            return
+        if contribution.shape != target.shape:
+            contribution, owned = contribution.expand(target.shape), False
+        contribution = contribution.to(target.dtype)
+        if owned and contribution.is_contiguous():
+            self.grad = contribution
+        else:
+            self.grad = contribution.clone(memory_format=torch.contiguous_format)
+
+    def grad_buffer(self):
+        """(tensor, add): where to write this node's gradient, and whether to add to what is
+        there (True) or overwrite a fresh, uninitialised buffer (False)."""
+        if self.grad is not None:
+            return self.grad, True
+        self.grad = torch.empty_like(self.value)
+        return self.grad, False
+
+
+class GradientOp(Node):
+    """An operator whose backward writes its parents' gradients itself (first write included)."""
+
+
+class Variable(Node):
+    """A leaf: parameter (trainable), input or constant."""
+
+    def __init__(self, value=None, trainable=False, name=None, constant=False, requires_grad=True):
+        self._is_parameter = False
+        super().__init__(trainable=trainable, name=name)
+        self.value = value
+        self.constant = bool(constant)
+        self.requires_grad = requires_grad
+
+    @property
+    def trainable(self):
+        return self._trainable
+
+    @trainable.setter
+    def trainable(self, flag):
+        self._trainable = bool(flag)
+        self._is_parameter = self._is_parameter or self._trainable
+
+    @property
+    def requires_grad(self):
+        # Once a parameter, the trainable flag decides; other leaves keep their own flag.
+        return self._trainable if self._is_parameter else self._wants_grad
+
+    @requires_grad.setter
+    def requires_grad(self, flag):
+        self._wants_grad = bool(flag)
+
+    def forward(self):
+        pass
+
+    def backward(self):
+        pass
+
+
+def topological_order(root):
+    """Post-order of a depth-first walk over parents (parents in order), iteratively."""
+    order, seen = [], set()
+    stack = [(root, False)]
+    while stack:
+        node, done = stack.pop()
+        if done:
+            order.append(node)
+            continue
+        if node in seen:
+            continue
+        seen.add(node)
+        stack.append((node, True))
+        for parent in reversed(node.parents):
+            if parent not in seen:
+                stack.append((parent, False))
+    return order
+
+
+@dataclass(frozen=True)
+class _Plan:
+    """What one combination of leaf flags and retained nodes asks of a graph."""
+    needs: tuple            # (node, needs a gradient) for every node, in topological order
+    active: frozenset       # nodes that need a gradient
+    forward_units: tuple    # nodes (or fused groups) to run forward, in order
+    backward_units: tuple   # (unit, node whose gradient the unit consumes), in reverse order
+    pre_clear: dict         # non-GradientOp unit -> its parents that need a zero gradient first
+    keep: tuple             # nodes whose gradient survives backward (leaves, retained nodes)
+    groups: frozenset       # fused groups in use
+
+
+class Graph:
+    """Forward and backward over the subgraph that produces ``target_node``."""
+
+    _installed = None  # the plan whose per-node flags are written into the (possibly shared) nodes
+
+    def __init__(self, target_node, optimize=False, fold_constants=False, fuse_linear=True, fuse_activations=True):
+        self._opt_stats = None
+        if optimize:
+            from .fusion import apply_graph_optimizations
+            target_node, self._opt_stats = apply_graph_optimizations(
+                target_node, fold_constants=fold_constants, fuse_linear=fuse_linear,
+                fuse_activations=fuse_activations)
+        self.target_node = target_node
+        self.sorted_nodes = topological_order(target_node)
+        self.nodes = self.sorted_nodes
+        self._bn_groups = {}
+        if optimize and fuse_activations:
+            from .fusion import batchnorm_activation_groups
+            self._bn_groups = batchnorm_activation_groups(self.nodes)
+        if self._opt_stats is not None:
+            self._opt_stats["bn_activation_fusions"] = len(self._bn_groups)
+        self.profiler = None
+        self._leaves = tuple(node for node in self.nodes if not node.parents)
+        self._retained = set()
+        self._plans = {}
+        self._forward_plan = None
+
+    def retain_grad(self, *nodes):
+        """Keep the gradients of these intermediates (or differentiable leaves) after backward."""
+        for node in nodes:
+            if node not in self.nodes or (not node.parents and not node.requires_grad):
+                raise ValueError("retain_grad expects a graph intermediate or a differentiable leaf")
+        self._retained.update(node for node in nodes if node.parents)
+        self._plans.clear()
+
+    def _make_plan(self, flags):
+        needs = dict(zip(self._leaves, flags))
+        propagating = []
+        for node in self.nodes:
+            if node.parents:
+                from_parents = any(needs[p] for p in node.parents)
+                needs[node] = from_parents or node in self._retained
+                if from_parents:
+                    propagating.append(node)
+        groups = {out: g for out, g in self._bn_groups.items() if self._retained.isdisjoint(g.hidden)}
+        hidden = {node for g in groups.values() for node in g.hidden}
+        forward_units = tuple(groups.get(n, n) for n in self.nodes if n not in hidden)
+        backward_units = tuple((groups.get(n, n), n) for n in reversed(propagating) if n not in hidden)
+        pre_clear = {n: tuple(p for p in n.parents if needs[p]) for n in propagating if not isinstance(n, GradientOp)}
+        keep = tuple(n for n in self.nodes if needs[n] and (not n.parents or n in self._retained))
+        return _Plan(tuple(needs.items()), frozenset(n for n, need in needs.items() if need), forward_units,
+                     backward_units, pre_clear, keep, frozenset(groups))
+
+    def _plan(self):
+        flags = tuple(leaf.requires_grad for leaf in self._leaves)
+        plan = self._plans.get(flags)
+        if plan is None:
+            plan = self._plans[flags] = self._make_plan(flags)
+        if Graph._installed is not plan:
+            # Another graph may share these nodes with other needs: write this plan's flags back.
+            for node, need in plan.needs:
+                if node.parents:
+                    node.requires_grad = need
+                if not need:
+                    node.grad = None
+            Graph._installed = plan
+        return plan
+
+    def forward(self):
+        plan = self._plan()
+        self._forward_plan = plan
+        profiler = self.profiler
+        for unit in plan.forward_units:
+            if not unit.parents:
+                continue
+            inputs = [p.value for p in unit.parents]
+            if profiler is None:
+                unit.forward(*inputs)
+            else:
+                with profiler.node(unit, "forward"):
+                    unit.forward(*inputs)
+
+    def backward(self, loss_scale=1.0):
+        plan = self._plan()
+        ran = self._forward_plan
+        if ran is not None and ran is not plan and (not plan.active <= ran.active or plan.groups != ran.groups):
+            raise RuntimeError("new gradients requested after forward; run forward again to rebuild saved tensors")
+        if self.target_node not in plan.active:
+            return
+        for node in plan.active:
+            node.grad = None
+        seed = self.target_node.value
+        self.target_node.grad = torch.ones_like(seed) if loss_scale == 1.0 else torch.full_like(seed, loss_scale)
+        profiler = self.profiler
+        for unit, output in plan.backward_units:
+            if output.grad is None:
+                continue
+            for parent in plan.pre_clear.get(unit, ()):
+                if parent.grad is None:  # a plain Node may add into parent.grad directly
+                    parent.clear_grad()
+            retained = output.grad if output in self._retained else None
+            if profiler is None:
+                unit.backward()
+            else:
+                with profiler.node(unit, "backward"):
+                    unit.backward()
+            output.grad = retained  # release the consumed intermediate gradient unless retained
+        for node in plan.keep:
+            if node.grad is None:
+                node.clear_grad()

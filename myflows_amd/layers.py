@@ -1,18 +1,34 @@
-"""Layers with the reference's constructor arguments (``layers/layer.py:36-383``): Dense, Conv2D,
-MaxPool2d and Flatten, each taking ``backend=`` ("hip_native" or "auto", which is hip_native on the
-GPU). Parameters are drawn with the seeded initialisers in float64 and cast to float32 on the
-active device, so a seeded model matches the reference's weights."""
+"""Layers with the reference's constructor arguments (``layers/layer.py:36-383``): ``Dense``,
+``Conv2D``, ``MaxPool2d`` and ``Flatten``, each taking ``backend=`` ("hip_native", or "auto", which
+is hip_native on the GPU). Parameters are drawn by the seeded initialiser in float64 and cast to
+float32 on the active device, so a seeded model holds the reference model's weights.
+"""
 
 from __future__ import annotations
 
-from .basic import Linear, _linear_backend
-from .convolution import Conv2D_Op, Conv2D_ReLU_Op, Flatten_Op, MaxPool2d_Op, _backend_name, _normalize_pair
-from .core import Variable
+import torch
+
 from .device import asarray
-from .initializers import make_initializer
+from .graph import Variable
+from .init import make_initializer
+from .ops_basic import Linear, ReLU, _linear_backend
+from .ops_conv import Conv2D_Op, Conv2D_ReLU_Op, Flatten_Op, MaxPool2d_Op, _backend_name, _int_pair
+
+
+def _count(value, name):
+    value = int(value)
+    if value <= 0:
+        raise ValueError(f"{name} must be positive, got {value}")
+    return value
+
+
+def _parameter(data, layer_name, suffix):
+    return Variable(asarray(data), trainable=True, name=f"{layer_name}_{suffix}" if layer_name else suffix)
 
 
 class Layer:
+    """Builds graph nodes on call; ``params`` lists its trainable Variables."""
+
     def __init__(self, name=None):
         self.name = name
         self.params = []
@@ -22,15 +38,15 @@ class Layer:
 
 
 class Dense(Layer):
-    """Z = X W + b (layers/layer.py:46-76)."""
+    """Z = X W + b, with W (input_dim, output_dim) and b (1, output_dim)."""
 
     def __init__(self, input_dim, output_dim, activation=None, name=None, initializer=None, dtype=None,
                  backend="auto"):
         super().__init__(name=name)
         self.backend = _linear_backend(backend)
-        init = make_initializer(initializer)
-        self.W = Variable(asarray(init((input_dim, output_dim))), trainable=True, name=f"{name}_W" if name else "W")
-        self.b = Variable(asarray([[0.0] * output_dim]), trainable=True, name=f"{name}_b" if name else "b")
+        draw = make_initializer(initializer)
+        self.W = _parameter(draw((input_dim, output_dim)), name, "W")
+        self.b = _parameter(torch.zeros((1, output_dim), dtype=torch.float64), name, "b")
         self.params = [self.W, self.b]
         self.activation = activation
 
@@ -40,42 +56,37 @@ class Dense(Layer):
 
 
 class Conv2D(Layer):
-    """layers/layer.py:79-170; groups and dilation other than 1 are rejected by the native operator."""
+    """2-D convolution, kernel (out, in, kh, kw) and optional bias (out,). With activation=ReLU and
+    fuse_activation, the ReLU runs in the convolution's epilogue (Conv2D_ReLU_Op)."""
 
     def __init__(self, in_channels, out_channels, kernel_size=3, stride=1, padding=0, groups=1, dilation=1,
                  activation=None, fuse_activation=True, name=None, initializer=None, dtype=None, backend="auto",
                  bias=True, recompute_im2col=None):
         super().__init__(name=name)
         self.backend = _backend_name(backend)
+        self.in_channels, self.out_channels = _count(in_channels, "in_channels"), _count(out_channels, "out_channels")
+        self.groups = _count(groups, "groups")
+        if self.in_channels % self.groups or self.out_channels % self.groups:
+            raise ValueError("in_channels and out_channels must be divisible by groups")
+        self.kernel_size = _int_pair(kernel_size, "kernel_size")
+        self.stride = _int_pair(stride, "stride")
+        self.padding = _int_pair(padding, "padding", minimum=0)
+        self.dilation = _int_pair(dilation, "dilation")
         self.recompute_im2col = recompute_im2col
-        if int(in_channels) <= 0 or int(out_channels) <= 0 or int(groups) <= 0:
-            raise ValueError("channel counts and groups must be positive")
-        kh, kw = _normalize_pair(kernel_size, "kernel_size")
-        self.stride = _normalize_pair(stride, "stride")
-        self.padding = _normalize_pair(padding, "padding", allow_zero=True)
-        self.dilation = _normalize_pair(dilation, "dilation")
-        if in_channels % groups or out_channels % groups:
-            raise ValueError("channels must be divisible by groups")
-        init = make_initializer(initializer)
-        self.kernel = Variable(asarray(init((out_channels, in_channels // groups, kh, kw))), trainable=True,
-                               name=f"{name}_kernel" if name else "kernel")
-        self.b = (Variable(asarray([0.0] * out_channels), trainable=True, name=f"{name}_bias" if name else "bias")
-                  if bias else None)
+        draw = make_initializer(initializer)
+        shape = (self.out_channels, self.in_channels // self.groups, *self.kernel_size)
+        self.kernel = _parameter(draw(shape), name, "kernel")
+        self.b = _parameter(torch.zeros(self.out_channels, dtype=torch.float64), name, "bias") if bias else None
         self.params = [self.kernel] if self.b is None else [self.kernel, self.b]
-        self.in_channels, self.out_channels = in_channels, out_channels
-        self.kernel_size = (kh, kw)
-        self.groups = groups
         self.activation = activation
         self.fuse_activation = bool(fuse_activation)
 
     def forward(self, input_node):
-        from .activation import ReLU
-
-        kwargs = dict(stride=self.stride, padding=self.padding, groups=self.groups, dilation=self.dilation,
-                      bias=self.b, backend=self.backend, recompute_im2col=self.recompute_im2col)
+        options = dict(stride=self.stride, padding=self.padding, groups=self.groups, dilation=self.dilation,
+                       bias=self.b, backend=self.backend, recompute_im2col=self.recompute_im2col)
         if self.fuse_activation and self.activation is ReLU:
-            return Conv2D_ReLU_Op(input_node, self.kernel, **kwargs)
-        out = Conv2D_Op(input_node, self.kernel, **kwargs)
+            return Conv2D_ReLU_Op(input_node, self.kernel, **options)
+        out = Conv2D_Op(input_node, self.kernel, **options)
         return self.activation(out) if self.activation else out
 
 
@@ -84,7 +95,7 @@ class MaxPool2d(Layer):
         super().__init__(name=name)
         self.backend = _backend_name(backend)
         self.k, self.s = kernel_size, stride
-        self.padding = _normalize_pair(padding, "padding", allow_zero=True)
+        self.padding = _int_pair(padding, "padding", minimum=0)
 
     def forward(self, input_node):
         return MaxPool2d_Op(input_node, self.k, self.s, backend=self.backend, padding=self.padding)

@@ -1,0 +1,191 @@
+"""Convolution, max-pool and flatten operators on the ``hip_native`` backend.
+
+The operator API of the reference's ``ops/convolution.py``: ``Conv2D_Op`` (:287-523; native
+forward :347-360, native backward :426-457), ``Conv2D_ReLU_Op`` (:526-545), ``Conv2D_LeakyReLU_Op``
+(:548-573), ``MaxPool2d_Op`` (:817-890) and ``Flatten_Op`` (:893-898), with the backend value
+``hip_native`` (``auto`` means hip_native on the GPU; ``cuda_native_register`` is accepted as an
+alias so code written for the reference's native backend runs unchanged). This package has no CPU
+path: CPU tensors are rejected as the reference rejects a native backend on the CPU device.
+"""
+
+from __future__ import annotations
+
+import os
+
+import torch
+
+from . import native
+from .graph import GradientOp
+
+NATIVE_BACKENDS = {"hip_native": "mfma", "cuda_native_register": "mfma"}
+BACKENDS = ("auto", *NATIVE_BACKENDS)
+
+
+def _backend_name(backend):
+    if backend not in BACKENDS:
+        raise ValueError(f"unknown convolution backend {backend!r}; this build offers {BACKENDS}")
+    return backend
+
+
+def _resolve_backend(backend, *arrays):
+    """The backend that runs now (``auto`` -> hip_native), after checking that every array is a GPU
+    tensor on the current device."""
+    chosen = "hip_native" if backend == "auto" else backend
+    current = torch.cuda.current_device() if torch.cuda.is_available() else None
+    for value in arrays:
+        if value is None:
+            continue
+        if not isinstance(value, torch.Tensor):
+            raise TypeError("operator arrays must be torch tensors on the active device")
+        if value.device.type != "cuda":
+            raise ValueError(f"backend={chosen} is incompatible with device=cpu")
+        if value.device.index != current:
+            raise ValueError("operator arrays must be on the current GPU")
+    return chosen
+
+
+def _int_pair(value, name, minimum=1):
+    if isinstance(value, int):
+        value = (value, value)
+    if not (isinstance(value, (tuple, list)) and len(value) == 2):
+        raise TypeError(f"{name} must be an int or a pair of ints, got {value!r}")
+    pair = (int(value[0]), int(value[1]))
+    if min(pair) < minimum:
+        raise ValueError(f"{name} must be {'non-negative' if minimum == 0 else 'positive'}, got {value!r}")
+    return pair
+
+
+class Conv2D_Op(GradientOp):
+    """y = conv(x, kernel) (+ bias), NCHW / OIHW, through im2col and the MFMA GEMM engine.
+
+    The im2col columns are kept for dW only when the kernel needs a gradient and
+    ``recompute_im2col`` is off; the inputs are kept only when this node needs gradients.
+    """
+
+    fused_activation = None  # "relu" / "leaky_relu" in the fused subclasses
+
+    def __init__(self, x, kernel, stride=1, padding=0, groups=1, dilation=1, bias=None, backend="auto",
+                 recompute_im2col=None):
+        super().__init__(*((x, kernel) if bias is None else (x, kernel, bias)))
+        self.backend = _backend_name(backend)
+        if int(groups) != 1 or _int_pair(dilation, "dilation") != (1, 1):
+            raise ValueError(f"{backend} supports only groups=1 and dilation=1")
+        self.bias = bias
+        self.stride = _int_pair(stride, "stride")
+        self.padding = _int_pair(padding, "padding", minimum=0)
+        self.groups, self.dilation = 1, (1, 1)
+        if recompute_im2col is None:
+            recompute_im2col = os.environ.get("MYFLOWS_RECOMPUTE_IM2COL") == "1"
+        self.recompute_im2col = bool(recompute_im2col)
+        self._activation_fused = False
+        self._saved = None
+
+    def _activation_alpha(self):
+        return 0.0
+
+    def forward(self, x_val, kernel_val, bias_val=None):
+        self.actual_backend = _resolve_backend(self.backend, x_val, kernel_val, bias_val)
+        if self.bias is not None and bias_val is None:
+            raise ValueError("bias value is missing")
+        self.value, cols = native.conv2d_forward(
+            x_val, kernel_val, bias_val, stride=self.stride, padding=self.padding,
+            activation=self.fused_activation, alpha=self._activation_alpha(),
+            engine=NATIVE_BACKENDS[self.actual_backend])
+        self._activation_fused = self.fused_activation is not None
+        keep_cols = self.parents[1].requires_grad and not self.recompute_im2col
+        self._saved = (x_val, kernel_val, cols if keep_cols else None) if self.requires_grad else None
+
+    def backward(self):
+        if not hasattr(self, "actual_backend"):
+            raise RuntimeError("forward must run before backward")
+        _resolve_backend(self.actual_backend, self.grad, *(p.value for p in self.parents))
+        x_node, kernel_node = self.parents[0], self.parents[1]
+        need_x, need_w = x_node.requires_grad, kernel_node.requires_grad
+        need_b = self.bias is not None and self.bias.requires_grad
+        if not (need_x or need_w or need_b):
+            return
+        x_val, kernel_val, cols = self._saved
+        grads = native.conv2d_backward(
+            x_val, kernel_val, self.grad, cols, stride=self.stride, padding=self.padding, need_bias_grad=need_b,
+            need_weight_grad=need_w, need_input_grad=need_x,
+            activation=self.fused_activation if self._activation_fused else None, alpha=self._activation_alpha(),
+            output=self.value, engine=NATIVE_BACKENDS[self.actual_backend], recompute_cols=self.recompute_im2col)
+        for parent, grad in zip(self.parents, grads):
+            if grad is not None:
+                parent.accumulate_grad(grad, owned=True)
+
+
+class Conv2D_ReLU_Op(Conv2D_Op):
+    """Conv2D(+bias) then ReLU: the activation runs in the GEMM epilogue and the backward gates dy
+    by the output inside the transposed-gradient kernel."""
+
+    fused_activation = "relu"
+
+
+class Conv2D_LeakyReLU_Op(Conv2D_Op):
+    """Conv2D(+bias) then LeakyReLU. Fused only for alpha > 0 (then y > 0 exactly where the
+    pre-activation is > 0, so the output alone can gate the backward); otherwise applied after."""
+
+    def __init__(self, *args, alpha=0.01, **kwargs):
+        super().__init__(*args, **kwargs)
+        self.alpha = float(alpha)
+        self.fused_activation = "leaky_relu" if self.alpha > 0 else None
+        self._positive = None
+
+    def _activation_alpha(self):
+        return self.alpha
+
+    def forward(self, x_val, kernel_val, bias_val=None):
+        super().forward(x_val, kernel_val, bias_val=bias_val)
+        if self._activation_fused:
+            return
+        positive = self.value > 0
+        self.value = torch.where(positive, self.value, self.alpha * self.value)
+        self._positive = positive if self.requires_grad else None
+
+    def backward(self):
+        if not self._activation_fused:
+            self.grad = torch.where(self._positive, self.grad, self.alpha * self.grad)
+        super().backward()
+
+
+class MaxPool2d_Op(GradientOp):
+    """Max pooling. ``padding`` pads with -inf (as torch.nn.MaxPool2d); the native kernels then see an
+    unpadded input and the input gradient is cropped back."""
+
+    def __init__(self, x, kernel_size=2, stride=2, backend="auto", padding=0):
+        super().__init__(x)
+        self.backend = _backend_name(backend)
+        self.kernel_size = _int_pair(kernel_size, "kernel_size")
+        self.stride = _int_pair(stride, "stride")
+        self.padding = _int_pair(padding, "padding", minimum=0)
+        self._context = None
+
+    def forward(self, x_val):
+        self.actual_backend = _resolve_backend(self.backend, x_val)
+        ph, pw = self.padding
+        if ph or pw:
+            x_val = torch.nn.functional.pad(x_val, (pw, pw, ph, ph), value=float("-inf"))
+        self.value, context = native.maxpool2d_forward(x_val, kernel_size=self.kernel_size, stride=self.stride)
+        self._context = context if self.requires_grad else None
+
+    def backward(self):
+        if not hasattr(self, "actual_backend"):
+            raise RuntimeError("forward must run before backward")
+        _resolve_backend(self.actual_backend, self.grad, self.parents[0].value)
+        dx = native.maxpool2d_backward(self.grad, self._context)
+        ph, pw = self.padding
+        if ph or pw:
+            dx = dx[:, :, ph:dx.shape[2] - ph, pw:dx.shape[3] - pw]
+        self.parents[0].accumulate_grad(dx, owned=not (ph or pw))
+
+
+class Flatten_Op(GradientOp):
+    """(N, ...) -> (N, prod(...)), a view."""
+
+    def forward(self, x):
+        self.in_shape = tuple(x.shape)
+        self.value = x.reshape(x.shape[0], -1)
+
+    def backward(self):
+        self.parents[0].accumulate_grad(self.grad.reshape(self.in_shape))

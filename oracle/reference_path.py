@@ -201,11 +201,11 @@ def maxpool2d_native_backward(grad_y, argmax, input_shape):
 # ---------------------------------------------------------------------------------------------
 def reduce_to(grad, shape):
     """Sum over broadcast axes in FP64, rounded once; ops/basic.py:67-73."""
-    lead = grad.ndim - len(shape)
-    axes = tuple(range(lead)) + tuple(lead + i for i, (gd, bd) in enumerate(zip(grad.shape[lead:], shape))
-                                      if bd == 1 and gd != 1)
-    total = grad.sum(axis=axes, dtype=np.float64) if axes else grad
-    return total.reshape(shape).astype(grad.dtype, copy=False)
+    padded = (1,) * (grad.ndim - len(shape)) + tuple(shape)
+    summed = [axis for axis, (size, target) in enumerate(zip(grad.shape, padded)) if target == 1 and size != 1]
+    if not summed:
+        return grad.reshape(shape)
+    return np.sum(grad, axis=tuple(summed), dtype=np.float64).reshape(shape).astype(grad.dtype)
 
 
 def linear_forward(x, w, b):
@@ -220,50 +220,66 @@ def linear_backward(x, w, b_shape, grad, need_input_grad=True):
 # ---------------------------------------------------------------------------------------------
 # BatchNorm2d, ops/fused.py:250-387 (NumPy branches)
 # ---------------------------------------------------------------------------------------------
-def _channel(a):
-    return a.reshape(1, -1, 1, 1)
+_PER_CHANNEL = (0, 2, 3)
+
+
+def _as_channel(v):
+    return np.asarray(v)[None, :, None, None]
 
 
 def batchnorm2d_forward(x, gamma, beta, running_mean, running_var, momentum=0.1, eps=1e-5, training=True,
                         relu=False, residual=None):
-    """Return (y, mean (2, C) hi/lo split, inv_std); updates the running statistics in place."""
-    axes = (0, 2, 3)
+    """Return (y, mean (2, C) hi/lo split, inv_std); updates the running statistics in place.
+
+    NumPy branch of ops/fused.py:287-305. Statistics: FP64 mean, then the FP64 mean of squared
+    deviations (two passes). The mean is kept as the float32 pair hi + lo. The output is formed in
+    float32 one rounded operation at a time: x - hi, - lo, * inv_std, * gamma, + beta, then
+    + residual and max(0, .)."""
     if training:
-        mean64 = x.mean(axis=axes, dtype=np.float64)
-        centered = x.astype(np.float64) - _channel(mean64)
-        var64 = (centered * centered).mean(axis=axes)
-        running_mean[...] = (1.0 - momentum) * running_mean.astype(np.float64) + momentum * mean64
-        running_var[...] = (1.0 - momentum) * running_var.astype(np.float64) + momentum * var64
+        mu = np.mean(x, axis=_PER_CHANNEL, dtype=np.float64)
+        deviation = x.astype(np.float64) - _as_channel(mu)
+        sigma2 = np.mean(deviation ** 2, axis=_PER_CHANNEL)
+        keep = 1.0 - momentum
+        running_mean[...] = keep * running_mean.astype(np.float64) + momentum * mu
+        running_var[...] = keep * running_var.astype(np.float64) + momentum * sigma2
     else:
-        mean64, var64 = running_mean.astype(np.float64), running_var.astype(np.float64)
-    hi = mean64.astype(x.dtype)
-    mean = np.stack([hi, (mean64 - hi).astype(x.dtype)])
-    inv_std = (1.0 / np.sqrt(var64 + eps)).astype(x.dtype)
-    y = (((x - _channel(mean[0])) - _channel(mean[1])) * _channel(inv_std)) * _channel(gamma) + _channel(beta)
+        mu, sigma2 = running_mean.astype(np.float64), running_var.astype(np.float64)
+    mean_hi = mu.astype(np.float32)
+    mean_lo = (mu - mean_hi.astype(np.float64)).astype(np.float32)
+    inv_std = (1.0 / np.sqrt(sigma2 + eps)).astype(np.float32)
+    step = np.subtract(x, _as_channel(mean_hi))
+    step = np.subtract(step, _as_channel(mean_lo))
+    step = np.multiply(step, _as_channel(inv_std))
+    step = np.multiply(step, _as_channel(gamma))
+    y = np.add(step, _as_channel(beta))
     if residual is not None:
-        y = y + residual
+        y = np.add(y, residual)
     if relu:
-        y = np.maximum(0, y)
-    return y, mean, inv_std
+        y = np.maximum(np.float32(0), y)
+    return y, np.stack([mean_hi, mean_lo]), inv_std
 
 
 def batchnorm2d_backward(x, dy, gamma, mean, inv_std, training=True):
-    """(dx, dgamma, dbeta) with FP64 channel sums (ops/fused.py:353-380)."""
-    axes = (0, 2, 3)
+    """(dx, dgamma, dbeta); NumPy branch of ops/fused.py:353-380.
+
+    FP64 channel sums S1 = sum(dy), S2 = sum(dy * (x - mean)); dgamma = inv_std * S2, dbeta = S1.
+    dx = a * ((dy - k1) - ((x - hi) - lo) * k2) in float32 with the float32 coefficients
+    a = gamma * inv_std, k1 = S1 / count, k2 = inv_std * dgamma / count (each formed in FP64 and
+    rounded once); a * dy in eval mode."""
     count = x.shape[0] * x.shape[2] * x.shape[3]
-    istd = inv_std.astype(np.float64)
-    dy64 = dy.astype(np.float64)
-    sdy = dy64.sum(axis=axes)
-    centered = x.astype(np.float64) - _channel(mean[0].astype(np.float64) + mean[1].astype(np.float64))
-    dgamma = istd * (dy64 * centered).sum(axis=axes)
-    a = _channel((gamma.astype(np.float64) * istd).astype(x.dtype))
-    if training:
-        k1 = _channel((sdy / count).astype(x.dtype))
-        k2 = _channel((istd * dgamma / count).astype(x.dtype))
-        dx = a * (dy - k1 - ((x - _channel(mean[0])) - _channel(mean[1])) * k2)
-    else:
-        dx = a * dy
-    return dx, dgamma.astype(x.dtype), sdy.astype(x.dtype)
+    inv64 = inv_std.astype(np.float64)
+    g64 = dy.astype(np.float64)
+    s1 = np.sum(g64, axis=_PER_CHANNEL)
+    deviation = x.astype(np.float64) - _as_channel(mean[0].astype(np.float64) + mean[1].astype(np.float64))
+    dgamma = inv64 * np.sum(g64 * deviation, axis=_PER_CHANNEL)
+    a = _as_channel((gamma.astype(np.float64) * inv64).astype(np.float32))
+    if not training:
+        return a * dy, dgamma.astype(np.float32), s1.astype(np.float32)
+    k1 = _as_channel((s1 / count).astype(np.float32))
+    k2 = _as_channel((inv64 * dgamma / count).astype(np.float32))
+    x_hat = np.subtract(np.subtract(x, _as_channel(mean[0])), _as_channel(mean[1]))
+    dx = np.multiply(a, np.subtract(np.subtract(dy, k1), np.multiply(x_hat, k2)))
+    return dx, dgamma.astype(np.float32), s1.astype(np.float32)
 
 
 # ---------------------------------------------------------------------------------------------
@@ -296,16 +312,19 @@ def mse_backward(pred, target, grad=np.float32(1.0)):
 # ---------------------------------------------------------------------------------------------
 # Adam, ops/fused.py:514-533 (NumPy branch, every operation rounded to float32 in this order)
 # ---------------------------------------------------------------------------------------------
-def adam_update(param, grad, m, v, *, lr, beta1, beta2, eps, step, grad_scale=1.0):
-    dtype = param.dtype.type
-    bc1, bc2 = 1.0 - beta1 ** step, 1.0 - beta2 ** step
-    scale, b1, omb1, b2, omb2, bc1, bc2, lr, eps = (dtype(v_) for v_ in (grad_scale, beta1, 1.0 - beta1, beta2,
-                                                                           1.0 - beta2, bc1, bc2, lr, eps))
-    gs = grad if scale == 1 else grad * scale
-    m *= b1
-    m += omb1 * gs
-    v *= b2
-    v += omb2 * (gs * gs)
-    denom = np.sqrt(v / bc2)
-    denom += eps
-    param -= (lr * (m / bc1)) / denom
+def adam_update(param, grad, m, v, *, lr, beta1, beta2, eps, step, grad_scale=1.0, weight_decay=0.0):
+    """In-place Adam step on float32 arrays (ops/fused.py:514-533). Scalars are formed in FP64 and
+    rounded to float32 once; every array operation is one float32 rounding, in this order:
+    g = g*scale + decay*p (with a decay; else g*scale, skipped for scale 1);
+    m = b1*m + (1-b1)*g; v = b2*v + (1-b2)*(g*g); p = p - (lr*(m/bc1)) / (sqrt(v/bc2) + eps)."""
+    f32 = np.float32
+    b1, b2, c1, c2 = f32(beta1), f32(beta2), f32(1.0 - beta1), f32(1.0 - beta2)
+    bias1, bias2 = f32(1.0 - beta1 ** step), f32(1.0 - beta2 ** step)
+    if weight_decay:
+        g = np.add(np.multiply(grad, f32(grad_scale)), np.multiply(param, f32(weight_decay)))
+    else:
+        g = grad if f32(grad_scale) == 1 else np.multiply(grad, f32(grad_scale))
+    m[...] = np.add(np.multiply(m, b1), np.multiply(g, c1))
+    v[...] = np.add(np.multiply(v, b2), np.multiply(np.multiply(g, g), c2))
+    denominator = np.add(np.sqrt(np.divide(v, bias2)), f32(eps))
+    param[...] = np.subtract(param, np.divide(np.multiply(f32(lr), np.divide(m, bias1)), denominator))

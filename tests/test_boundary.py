@@ -1,8 +1,16 @@
-"""The C ABI and the Python boundary without a GPU: the built library loads and exports every
-symbol include/mfhip.h declares, and the host-side argument checks raise before any device call."""
+"""The C ABI and the Python boundary without a GPU.
+
+* the built library exports every symbol include/mfhip.h declares, and native.py declares each with
+  the header's number of parameters;
+* the one struct of the ABI (mfh_adam_tensor) has the same layout in C (gcc on the header) and in
+  ctypes;
+* host-side argument checks raise before any device call; operators reject CPU tensors;
+* seeded model weights, the graph executor and the graph rewrites, on CPU tensors.
+"""
 
 import ctypes
 import re
+import subprocess
 from pathlib import Path
 
 import numpy as np
@@ -11,35 +19,53 @@ import torch
 
 import myflows_amd as mf
 from myflows_amd import native
+from myflows_amd.graph import GradientOp
 
 HEADER = Path(__file__).resolve().parents[1] / "include" / "mfhip.h"
 
 
-def declared_symbols():
-    return re.findall(r"MFH_API\s+[\w\s\*]+?\b(mfh_\w+)\s*\(", HEADER.read_text())
+def header_prototypes():
+    """{symbol: parameter count} of every MFH_API function in the header."""
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    found = {}
+    for name, params in re.findall(r"MFH_API\s+[\w\s\*]+?\b(mfh_\w+)\s*\(([^)]*)\)", text):
+        params = params.strip()
+        found[name] = 0 if params in ("", "void") else params.count(",") + 1
+    return found
 
 
-def test_library_exports_every_declared_symbol():
+def test_library_exports_every_declared_symbol_with_its_arity():
     lib = native.load_library()
-    declared = declared_symbols()
-    assert len(declared) == 16
-    assert sorted(declared) == sorted(native.EXPORTS)
-    for name in declared:
+    prototypes = header_prototypes()
+    assert sorted(prototypes) == sorted(native.EXPORTS)
+    for name, count in prototypes.items():
         assert hasattr(lib, name), name
+        assert len(native._SIGNATURES[name][1]) == count, name
 
 
-def test_tile_catalog_and_plan_codes():
-    catalog = native.tile_catalog()
-    assert catalog["128x128"][0] == 0 and all(v[-1] == 16 for v in catalog.values())
-    assert native._plan_code("128x128", 1) == 16
-    assert native._plan_code("256x64", 3) == 16 + 128 + 2
-    with pytest.raises(ValueError):
-        native._plan_code("7x7", 1)
-    with pytest.raises(ValueError):
-        native._plan_code("128x128", 0)
-    with pytest.raises(ValueError):
-        native._plan_code("128x128", 129)
-    assert native._slices(3000, 5, 16) == 5 and native._slices(100, 7, 16) == 7 and native._slices(10, 4, 16) == 1
+def test_adam_table_layout_matches_the_header(tmp_path):
+    probe = tmp_path / "probe.c"
+    probe.write_text(
+        '#include <stddef.h>\n#include <stdio.h>\n#include "mfhip.h"\n'
+        "int main(void) { printf(\"%zu %zu %zu %zu\\n\", sizeof(mfh_adam_tensor), offsetof(mfh_adam_tensor, size),"
+        " offsetof(mfh_adam_tensor, lr), offsetof(mfh_adam_tensor, bias_correction2)); return 0; }\n")
+    subprocess.run(["gcc", "-I", str(HEADER.parent), str(probe), "-o", str(tmp_path / "probe")], check=True)
+    c_layout = [int(v) for v in subprocess.run([str(tmp_path / "probe")], capture_output=True, text=True,
+                                               check=True).stdout.split()]
+    t = native.AdamTensor
+    assert c_layout == [ctypes.sizeof(t), t.size.offset, t.lr.offset, t.bias_correction2.offset]
+
+
+def test_tile_catalogue_and_plan_codes():
+    catalogue = native.tile_catalog()
+    assert catalogue["128x128"][0] == 0 and all(entry[-1] == 16 for entry in catalogue.values())
+    assert native._plan_code("128x128", 1) == native.PLAN_BASE
+    assert native._plan_code("256x64", 3) == native.PLAN_BASE + native.PLAN_SLICES + 2
+    for bad in (("7x7", 1), ("128x128", 0), ("128x128", native.PLAN_SLICES + 1), ("128x128", 2.0)):
+        with pytest.raises(ValueError):
+            native._plan_code(*bad)
+    # requested slices -> slices made, with BK-aligned chunks
+    assert [native._slices(k, r, 16) for k, r in ((3000, 5), (100, 7), (10, 4), (4096, 1))] == [5, 7, 1, 1]
 
 
 def test_argument_checks_raise_before_any_device_call():
@@ -49,19 +75,25 @@ def test_argument_checks_raise_before_any_device_call():
     with pytest.raises(ValueError, match="engine"):
         native.conv2d_forward(cpu, torch.zeros((1, 1, 3, 3)), engine="tf32")
     with pytest.raises(ValueError, match="int32"):
-        native._guard_index(columns=2**31)
+        native._within_int32(columns=2**31)
     with pytest.raises(ValueError, match="alpha > 0"):
-        native._activation("leaky_relu", 0.0)
+        native._activation_code("leaky_relu", 0.0)
     with pytest.raises(ValueError):
-        native._dims(torch.zeros((1, 2, 4, 4), device="meta"), torch.zeros((1, 3, 3, 3), device="meta"), (1, 1), (0, 0))
-    with pytest.raises(ValueError, match="not positive"):
-        native._dims(torch.zeros((1, 1, 2, 2), device="meta"), torch.zeros((1, 1, 3, 3), device="meta"), (1, 1), (0, 0))
+        native._activation_code("gelu", 0.0)
+    with pytest.raises(ValueError, match="input channels"):
+        native.ConvGeometry.of((1, 2, 4, 4), (1, 3, 3, 3), (1, 1), (0, 0))
+    with pytest.raises(ValueError, match="empty"):
+        native.ConvGeometry.of((1, 1, 2, 2), (1, 1, 3, 3), (1, 1), (0, 0))
     with pytest.raises(ValueError):
-        native._pool_dims(torch.zeros((1, 1, 2, 2), device="meta"), (3, 3), (1, 1))
+        native.ConvGeometry.of((1, 1, 8, 8), (1, 1, 3, 3), (0, 1), (0, 0))
+    g = native.ConvGeometry.of((2, 3, 7, 9), (4, 3, 3, 3), (2, 2), (1, 1))
+    assert (g.oh, g.ow, g.m, g.k) == (4, 5, 40, 27) and len(g.c_args()) == 13
     with pytest.raises(ValueError):
         native.matmul(cpu.reshape(4, 4), cpu.reshape(4, 4), variant="cublas")
     with pytest.raises(ValueError):
         native.gemm(cpu.reshape(4, 4), cpu.reshape(4, 4), trans_a=True, trans_b=True)
+    with pytest.raises(TypeError):
+        mf.fused.relu_forward(cpu)
 
 
 def test_operators_reject_cpu_arrays_and_unsupported_options():
@@ -74,10 +106,11 @@ def test_operators_reject_cpu_arrays_and_unsupported_options():
         pool = mf.MaxPool2d(2, 2, backend="hip_native")(x)
         with pytest.raises(ValueError, match="incompatible with device=cpu"):
             pool.forward(x.value)
-        with pytest.raises(ValueError):
-            mf.Conv2D_Op(x, mf.Variable(torch.zeros((2, 1, 3, 3))), groups=2, backend="hip_native")
-        with pytest.raises(ValueError):
-            mf.Conv2D_Op(x, mf.Variable(torch.zeros((2, 1, 3, 3))), dilation=2, backend="hip_native")
+        with pytest.raises(ValueError, match="GPU tensor"):
+            mf.ReLU(x).forward(x.value)
+        for options in ({"groups": 2}, {"dilation": 2}):
+            with pytest.raises(ValueError):
+                mf.Conv2D_Op(x, mf.Variable(torch.zeros((2, 1, 3, 3))), backend="hip_native", **options)
         with pytest.raises(ValueError):
             mf.Conv2D(1, 2, backend="cudnn")
         with pytest.raises(ValueError):
@@ -88,7 +121,8 @@ def test_operators_reject_cpu_arrays_and_unsupported_options():
 
 
 def test_seeded_resnet_weights_match_the_oracle_draw_order():
-    """ResNet18(initializer=make_initializer(seed=0)) draws the same weights as the oracle model."""
+    """ResNet18(initializer=make_initializer(seed=0)) holds exactly the oracle model's weights, in the
+    reference's parameter order."""
     from oracle import resnet as oracle_resnet
 
     mf.set_device("cpu")
@@ -98,28 +132,87 @@ def test_seeded_resnet_weights_match_the_oracle_draw_order():
         if torch.cuda.is_available():
             mf.set_device("cuda")
     params, _ = oracle_resnet.init_params(seed=0)
-    ours = [p.value.numpy() for p in model.params]
-    assert len(ours) == len(params)
-    # order: stem conv (kernel, bias), stem bn, blocks..., fc
-    oracle_order = list(params.values())
-    for a, b in zip(ours, oracle_order):
-        assert a.shape == b.shape
-        assert np.array_equal(a, b)
+    assert len(model.params) == len(params) == 82  # stem 4, eight blocks 8 each, three shortcuts 4 each, fc 2
+    assert sum(p.value.numel() for p in model.params) == 11_182_338
+    for ours, expected in zip(model.params, params.values()):
+        assert np.array_equal(ours.value.numpy(), expected)
 
 
-def test_graph_engine_on_cpu_tensors():
-    """Graph planning and gradient accumulation with the device-agnostic operators (Add, ReLU,
-    MSELoss): a leaf used twice accumulates, a requires_grad=False leaf gets no gradient."""
+class _Square(GradientOp):
+    """x * x: a test-local operator, so the executor is exercised without libmfhip."""
+
+    def forward(self, x):
+        self.value = x * x
+
+    def backward(self):
+        self.parents[0].accumulate_grad(2 * self.parents[0].value * self.grad, owned=True)
+
+
+def test_graph_executor_on_cpu_tensors():
+    """Gradient accumulation over a leaf used three times, a requires_grad=False leaf, gradient
+    release of intermediates, retain_grad, and the plan rebuilt when a leaf flag changes."""
     a = mf.Variable(torch.tensor([1.0, -2.0, 3.0]), trainable=True, name="a")
     c = mf.Variable(torch.tensor([0.5, 0.5, 0.5]), requires_grad=False, name="c")
     t = mf.Variable(torch.zeros(3), requires_grad=False, name="t")
-    loss = mf.MSELoss(mf.Add(mf.ReLU(a), mf.Add(a, c)), t)
+    square = _Square(a)
+    pred = mf.Add(square, mf.Add(a, mf.Add(a, c)))
+    loss = mf.MSELoss(pred, t)
     graph = mf.Graph(loss)
     graph.forward()
     graph.backward()
-    relu_a = torch.clamp_min(a.value, 0)
-    pred = relu_a + a.value + c.value
-    expected = 2.0 * pred / 3 * ((a.value > 0).float() + 1.0)
-    torch.testing.assert_close(a.grad, expected)
-    assert c.grad is None
-    assert abs(loss.value.item() - float((pred * pred).mean())) < 1e-6
+    p = a.value ** 2 + 2 * a.value + c.value
+    dpred = 2.0 * p / 3
+    torch.testing.assert_close(a.grad, dpred * (2 * a.value + 2))
+    assert c.grad is None and square.grad is None
+    assert abs(loss.value.item() - float((p * p).mean())) < 1e-6
+    graph.retain_grad(square)
+    graph.forward()
+    graph.backward()
+    torch.testing.assert_close(square.grad, dpred)
+    c.requires_grad = True  # needs a new plan; asking for it without a new forward is an error
+    with pytest.raises(RuntimeError, match="run forward again"):
+        graph.backward()
+    graph.forward()
+    graph.backward()
+    torch.testing.assert_close(c.grad, dpred)
+
+
+def test_graph_rewrites_on_cpu():
+    """Conv+ReLU fusion, eval-mode BN folding (FP64 folded parameters, model parameters untouched),
+    constant folding, and the BN(+Add)+ReLU groups of a ResNet block."""
+    mf.set_device("cpu")
+    try:
+        x = mf.Variable(torch.zeros((1, 3, 8, 8)), requires_grad=False)
+        conv = mf.Conv2D(3, 4, 3, padding=1, fuse_activation=False, initializer=mf.make_initializer(seed=1),
+                         backend="hip_native")
+        root, stats = mf.apply_graph_optimizations(mf.ReLU(conv(x)), fold_constants=False)
+        assert type(root) is mf.Conv2D_ReLU_Op and stats["conv_act_fusions"] == 1
+
+        bn = mf.BatchNorm2d(4)
+        bn.running_mean.copy_(torch.tensor([0.1, -0.2, 0.3, 0.0]))
+        bn.running_var.copy_(torch.tensor([0.5, 1.5, 1.0, 2.0]))
+        bn.gamma.value.copy_(torch.tensor([1.0, 2.0, 0.5, -1.0]))
+        bn.beta.value.copy_(torch.tensor([0.0, 0.1, -0.1, 0.2]))
+        bn.eval()
+        kernel_before = conv.kernel.value.clone()
+        root, stats = mf.apply_graph_optimizations(bn(conv(x)), mode="inference", fold_constants=False)
+        assert type(root) is mf.Conv2D_Op and stats["bn_folds"] == 1
+        scale = bn.gamma.value.double() / torch.sqrt(bn.running_var.double() + bn.eps)
+        torch.testing.assert_close(root.parents[1].value, (kernel_before.double() * scale[:, None, None, None]).float())
+        torch.testing.assert_close(root.parents[2].value,
+                                   ((0 - bn.running_mean.double()) * scale + bn.beta.value.double()).float())
+        assert torch.equal(conv.kernel.value, kernel_before)
+
+        k1 = mf.Variable(torch.ones(3), constant=True)
+        k2 = mf.Variable(torch.full((3,), 2.0), constant=True)
+        root, stats = mf.apply_graph_optimizations(mf.Add(k1, k2))
+        assert stats["constant_folds"] == 1 and torch.equal(root.value, torch.full((3,), 3.0))
+
+        block = mf.BasicBlock(4, 8, stride=2, conv_backend="hip_native")
+        out = block(mf.Variable(torch.zeros((1, 4, 8, 8)), requires_grad=False))
+        graph = mf.Graph(out, optimize=True)
+        names = sorted(g.name for g in graph._bn_groups.values())
+        assert names == ["BatchNormAddReLU", "BatchNormReLU"]
+    finally:
+        if torch.cuda.is_available():
+            mf.set_device("cuda")

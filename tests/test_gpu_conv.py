@@ -1,0 +1,176 @@
+"""Convolution parity on the GPU, through the operator API and the native.py boundary.
+
+Bit-exact: the im2col matrix, and col2im (integer-valued dy and W make every GEMM product and
+window sum exact in float32, so any index or window error shows as a bit difference) on each dX
+path (from NCHW dy, from the transposed gated dy). Tolerance: outputs and gradients within 1e-5 of
+max|ref| of the FP64 loops of the reference's tests (normwise, the reference's own criterion), db
+within one float32 ulp of the FP64 sum.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+import myflows_amd as mf
+from myflows_amd import native
+from oracle import naive, reference_path as rp
+from tests.fixtures import CONV_CASES, EPS32, PERFORMANCE_CASES, assert_near, conv_fixture
+
+pytestmark = pytest.mark.gpu
+
+
+def gpu(a):
+    return torch.as_tensor(np.ascontiguousarray(a), device="cuda")
+
+
+def host(t):
+    torch.cuda.synchronize()
+    return t.detach().cpu().numpy()
+
+
+def run_operator(case, op_class=mf.Conv2D_Op, input_grad=True, **options):
+    """Forward + backward of one convolution operator; returns (op, y, [dx, dw, db])."""
+    x, w, b, dy = (gpu(a) for a in conv_fixture(case))
+    leaves = [mf.Variable(x, requires_grad=input_grad), mf.Variable(w, trainable=True), mf.Variable(b, trainable=True)]
+    op = op_class(leaves[0], leaves[1], stride=case[3], padding=case[4], bias=leaves[2], backend="hip_native",
+                  **options)
+    op.forward(x, w, b)
+    op.grad = dy
+    op.backward()
+    return op, host(op.value), [None if leaf.grad is None else host(leaf.grad) for leaf in leaves]
+
+
+def fp64_case(case):
+    x, w, b, dy = (a.astype(np.float64) for a in conv_fixture(case))
+    return x, w, b, dy, naive.conv_forward(x, w, case[3], case[4]) + b[None, :, None, None]
+
+
+@pytest.mark.parametrize("case", CONV_CASES + PERFORMANCE_CASES, ids=lambda c: c[0])
+def test_forward_and_gradients_match_fp64_loops(case):
+    """Covers both forward paths: OH*OW < 32 (rows GEMM + epilogue) and the per-image NCHW GEMM."""
+    print("conv case", case[0], flush=True)
+    x, w, _, dy, pre = fp64_case(case)
+    op, y, (dx, dw, db) = run_operator(case)
+    assert op.value.is_contiguous()
+    ref_dx, ref_dw = naive.conv_backward(x, w, dy, case[3], case[4])
+    assert_near(y, pre, 1e-5, "y")
+    assert_near(dx, ref_dx, 1e-5, "dx")
+    assert_near(dw, ref_dw, 1e-5, "dw")
+    ref_db = dy.sum(axis=(0, 2, 3))
+    assert np.all(np.abs(db - ref_db) <= np.spacing(np.abs(ref_db).astype(np.float32))), "db beyond one ulp"
+
+
+def test_known_answer_t0_is_exact():
+    """arange(25) correlated with ones(3x3): every output is its 3x3 window sum, exactly."""
+    _, y, _ = run_operator(CONV_CASES[0])
+    grid = np.arange(25.0).reshape(5, 5)
+    windows = np.array([[grid[i:i + 3, j:j + 3].sum() for j in range(3)] for i in range(3)], np.float32)
+    np.testing.assert_array_equal(y[0, 0], windows)
+
+
+@pytest.mark.parametrize("case", (CONV_CASES[1], CONV_CASES[3], PERFORMANCE_CASES[2]), ids=lambda c: c[0])
+@pytest.mark.parametrize("variant", ("relu", "leaky"))
+def test_fused_activation_forward_and_gated_backward(case, variant):
+    print("fused", variant, case[0], flush=True)
+    x, w, _, dy, pre = fp64_case(case)
+    op_class, options, slope = ((mf.Conv2D_ReLU_Op, {}, 0.0) if variant == "relu"
+                                else (mf.Conv2D_LeakyReLU_Op, {"alpha": 0.2}, 0.2))
+    op, y, (dx, dw, db) = run_operator(case, op_class, **options)
+    assert op._activation_fused
+    gate = np.where(pre > 0, 1.0, slope)
+    ref_dx, ref_dw = naive.conv_backward(x, w, dy * gate, case[3], case[4])
+    assert_near(y, np.where(pre > 0, pre, slope * pre), 1e-5, "y")
+    assert_near(dx, ref_dx, 1e-5, "dx")
+    assert_near(dw, ref_dw, 1e-5, "dw")
+    assert_near(db, (dy * gate).sum(axis=(0, 2, 3)), 4 * EPS32, "db")
+
+
+def test_frozen_input_skips_dx_and_keeps_weight_gradients_bitwise():
+    case = PERFORMANCE_CASES[0]
+    _, _, (_, dw_all, db_all) = run_operator(case)
+    _, _, (dx, dw, db) = run_operator(case, input_grad=False)
+    assert dx is None
+    np.testing.assert_array_equal(dw, dw_all)
+    np.testing.assert_array_equal(db, db_all)
+
+
+def test_dx_only_through_fused_relu():
+    """Frozen weight and bias: only dX, gated by the fused ReLU's output (the transposed-dy path)."""
+    case = PERFORMANCE_CASES[2]
+    x, w, b, dy = conv_fixture(case)
+    xv = mf.Variable(gpu(x))
+    wv, bv = mf.Variable(gpu(w), requires_grad=False), mf.Variable(gpu(b), requires_grad=False)
+    op = mf.Conv2D_ReLU_Op(xv, wv, stride=case[3], padding=case[4], bias=bv, backend="hip_native")
+    op.forward(xv.value, wv.value, bv.value)
+    op.grad = gpu(dy)
+    op.backward()
+    pre = naive.conv_forward(x.astype(np.float64), w.astype(np.float64), case[3], case[4]) + b[None, :, None, None]
+    ref_dx, _ = naive.conv_backward(x.astype(np.float64), w.astype(np.float64), dy * (pre > 0), case[3], case[4])
+    assert wv.grad is None and bv.grad is None
+    assert_near(host(xv.grad), ref_dx, 1e-5, "dx")
+
+
+@pytest.mark.parametrize("case", (PERFORMANCE_CASES[0], PERFORMANCE_CASES[1]), ids=lambda c: c[0])
+def test_gradients_are_bitwise_reproducible(case):
+    first = run_operator(case)[2]
+    second = run_operator(case)[2]
+    for a, b in zip(first, second):
+        np.testing.assert_array_equal(a, b)
+
+
+def test_recomputed_columns_give_identical_gradients():
+    case = PERFORMANCE_CASES[0]
+    saved = run_operator(case)[2]
+    recomputed = run_operator(case, recompute_im2col=True)[2]
+    for a, b in zip(saved, recomputed):
+        np.testing.assert_array_equal(a, b)
+
+
+@pytest.mark.parametrize("shape,kernel,stride,padding", [
+    ((2, 3, 7, 9), (3, 3), (1, 1), (1, 1)), ((1, 2, 8, 9), (3, 2), (2, 3), (1, 0)),
+    ((2, 3, 16, 16), (7, 7), (2, 2), (3, 3)), ((3, 5, 6, 5), (1, 1), (2, 2), (0, 0)),
+    ((2, 64, 30, 40), (3, 3), (1, 1), (1, 1)), ((2, 16, 29, 39), (3, 3), (2, 2), (1, 1))])
+def test_im2col_and_col2im_are_bit_exact(shape, kernel, stride, padding):
+    print("im2col", shape, kernel, stride, padding, flush=True)
+    rng = np.random.default_rng(3)
+    x = rng.standard_normal(shape).astype(np.float32)
+    co = 4
+    w_shape = (co, shape[1], *kernel)
+    cols = native.conv2d_im2col(gpu(x), w_shape, stride=stride, padding=padding)
+    np.testing.assert_array_equal(host(cols), rp.im2col(x, kernel, stride, padding))
+    np.testing.assert_array_equal(host(cols), naive.im2col(x, kernel, stride, padding))
+    oh, ow = rp.out_size(shape[2], shape[3], kernel, stride, padding)
+    w = rng.integers(-2, 3, size=w_shape).astype(np.float32)
+    dy = rng.integers(-3, 4, size=(shape[0], co, oh, ow)).astype(np.float32)
+    grad_cols = dy.transpose(0, 2, 3, 1).reshape(-1, co).astype(np.float64) @ w.reshape(co, -1)
+    expected = rp.col2im_native(grad_cols.astype(np.float32), shape, kernel, stride, padding)
+    np.testing.assert_array_equal(expected, naive.col2im(grad_cols, shape, kernel, stride, padding))
+    ones = gpu(np.ones(dy.shape, np.float32))  # a ReLU gate that passes everything
+    for need_w, activation in ((False, None), (True, None), (False, "relu"), (True, "relu")):
+        dx, _, _ = native.conv2d_backward(gpu(x), gpu(w), gpu(dy), cols, stride=stride, padding=padding,
+                                          need_bias_grad=need_w, need_weight_grad=need_w, activation=activation,
+                                          output=ones)
+        np.testing.assert_array_equal(host(dx), expected)
+
+
+def test_native_errors_name_the_reason():
+    lib = native._library()
+    x = torch.zeros((1, 1, 4, 4), device="cuda")
+    p = x.data_ptr()
+    status = lib.mfh_conv_forward(p, p, p, p, p, p, 1, 1, 4, 4, 1, 3, 3, 9, 9, 1, 1, 0, 0, 0, 0.0, 1, 0, 0, 0)
+    with pytest.raises(native.NativeHipError, match=r"invalid argument.*api\.hip:\d+: .*output size"):
+        native._raise_for(status, lib)
+    status = lib.mfh_gemm(7, 0, 0, p, p, p, p, 2, 2, 2, 2, 2, 2, 0, 0, 0)
+    with pytest.raises(native.NativeHipError, match="engine"):
+        native._raise_for(status, lib)
+
+
+def test_debug_sync_and_build_info():
+    facts = native.info()
+    assert facts["device_arch"].startswith("gfx950")
+    assert facts["binary"] == "hsaco" and facts["cu_count"] > 0
+    native.set_debug_sync(True)
+    try:
+        run_operator(CONV_CASES[1])
+    finally:
+        native.set_debug_sync(False)

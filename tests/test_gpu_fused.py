@@ -1,0 +1,196 @@
+"""Batch norm (+ residual + ReLU), ReLU and Adam kernels on the GPU against the oracle.
+
+* Adam: bit-exact against the oracle's float32 NumPy step (IEEE division and square root, the same
+  rounding order), single and multi-tensor, with a gradient scale and weight decay.
+* ReLU: bit-exact (a selection and, when accumulating, one float32 addition).
+* Batch norm: the GPU forms its FP64 statistics in one shifted pass, the oracle in two passes; the
+  float32 results agree to within 4 ulp of the largest output (written in each test); the running
+  statistics, dgamma and dbeta within 2e-6 relative.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from myflows_amd import fused
+from oracle import reference_path as rp
+from tests.fixtures import assert_near
+
+pytestmark = pytest.mark.gpu
+
+
+def gpu(a):
+    return torch.as_tensor(np.ascontiguousarray(a), device="cuda")
+
+
+def host(t):
+    torch.cuda.synchronize()
+    return t.detach().cpu().numpy()
+
+
+def ulps_of_max(got, expected, ulps):
+    scale = np.spacing(np.float32(np.abs(expected).max()))
+    worst = float(np.abs(got.astype(np.float64) - expected).max())
+    assert worst <= ulps * scale, f"max error {worst:.3e} > {ulps} ulp(max|ref|) = {ulps * scale:.3e}"
+
+
+def bn_inputs(shape, seed):
+    rng = np.random.default_rng(seed)
+    c = shape[1]
+    x = rng.normal(0.7, 2.0, size=shape).astype(np.float32)
+    gamma = rng.uniform(0.5, 1.5, c).astype(np.float32)
+    beta = rng.normal(size=c).astype(np.float32)
+    rm = rng.normal(0, 0.1, c).astype(np.float32)
+    rv = rng.uniform(0.5, 1.5, c).astype(np.float32)
+    return x, gamma, beta, rm, rv, rng
+
+
+SHAPES = ((2, 3, 5, 7), (4, 16, 30, 40), (64, 64, 29, 39), (3, 512, 4, 5))
+
+
+@pytest.mark.parametrize("shape", SHAPES, ids=str)
+@pytest.mark.parametrize("relu,residual", ((False, False), (True, False), (True, True)))
+def test_batchnorm_forward_training(shape, relu, residual):
+    print("bn forward", shape, relu, residual, flush=True)
+    x, gamma, beta, rm, rv, rng = bn_inputs(shape, 11)
+    res = rng.normal(size=shape).astype(np.float32) if residual else None
+    rm_ref, rv_ref = rm.copy(), rv.copy()
+    y_ref, mean_ref, inv_ref = rp.batchnorm2d_forward(x, gamma, beta, rm_ref, rv_ref, momentum=0.1, eps=1e-5,
+                                                      relu=relu, residual=res)
+    rm_gpu, rv_gpu = gpu(rm), gpu(rv)
+    y, mean, inv_std = fused.batchnorm2d_forward(gpu(x), gpu(gamma), gpu(beta), rm_gpu, rv_gpu, momentum=0.1,
+                                                 eps=1e-5, training=True, relu=relu,
+                                                 residual=None if res is None else gpu(res))
+    ulps_of_max(host(y), y_ref, 4)
+    np.testing.assert_allclose(host(mean).astype(np.float64).sum(0), mean_ref.astype(np.float64).sum(0),
+                               rtol=1e-12, atol=1e-12)
+    np.testing.assert_allclose(host(inv_std), inv_ref, rtol=2e-7)
+    np.testing.assert_allclose(host(rm_gpu), rm_ref, rtol=2e-6, atol=1e-7)
+    np.testing.assert_allclose(host(rv_gpu), rv_ref, rtol=2e-6)
+    if relu:
+        assert (host(y) >= 0).all()
+
+
+def test_batchnorm_forward_eval_and_unbiased_running_variance():
+    x, gamma, beta, rm, rv, _ = bn_inputs((4, 8, 6, 6), 12)
+    y_ref, _, _ = rp.batchnorm2d_forward(x, gamma, beta, rm.copy(), rv.copy(), training=False)
+    rm_gpu, rv_gpu = gpu(rm), gpu(rv)
+    y, mean, _ = fused.batchnorm2d_forward(gpu(x), gpu(gamma), gpu(beta), rm_gpu, rv_gpu, momentum=0.1, eps=1e-5,
+                                           training=False)
+    ulps_of_max(host(y), y_ref, 2)
+    np.testing.assert_array_equal(host(rm_gpu), rm)  # eval leaves the running statistics alone
+    np.testing.assert_array_equal(host(mean)[0], rm)
+    # training with the torch convention: the running variance tracks the unbiased batch variance
+    rv_gpu = gpu(rv)
+    fused.batchnorm2d_forward(gpu(x), gpu(gamma), gpu(beta), gpu(rm), rv_gpu, momentum=0.1, eps=1e-5, training=True,
+                              unbiased_running_var=True)
+    count = 4 * 36
+    batch_var = x.astype(np.float64).var(axis=(0, 2, 3))
+    np.testing.assert_allclose(host(rv_gpu), 0.9 * rv + 0.1 * batch_var * count / (count - 1), rtol=2e-6)
+
+
+@pytest.mark.parametrize("shape", SHAPES, ids=str)
+@pytest.mark.parametrize("training", (True, False))
+def test_batchnorm_backward(shape, training):
+    print("bn backward", shape, training, flush=True)
+    x, gamma, beta, rm, rv, rng = bn_inputs(shape, 13)
+    dy = rng.normal(size=shape).astype(np.float32)
+    _, mean_ref, inv_ref = rp.batchnorm2d_forward(x, gamma, beta, rm.copy(), rv.copy(), training=training)
+    dx_ref, dgamma_ref, dbeta_ref = rp.batchnorm2d_backward(x, dy, gamma, mean_ref, inv_ref, training=training)
+    x_grad = torch.full(shape, 0.25, device="cuda")  # accumulate into an existing gradient
+    gamma_grad, beta_grad = torch.empty(shape[1], device="cuda"), torch.empty(shape[1], device="cuda")
+    fused.batchnorm2d_backward(gpu(x), gpu(dy), gpu(gamma), gpu(mean_ref), gpu(inv_ref), training=training,
+                               x_grad=x_grad, gamma_grad=gamma_grad, beta_grad=beta_grad,
+                               accumulate=(True, False, False))
+    assert_near(host(x_grad) - np.float32(0.25), dx_ref, 1e-5, "dx")
+    np.testing.assert_allclose(host(gamma_grad), dgamma_ref, rtol=2e-6, atol=1e-6 * np.abs(dgamma_ref).max())
+    np.testing.assert_allclose(host(beta_grad), dbeta_ref, rtol=2e-6, atol=1e-6 * np.abs(dbeta_ref).max())
+
+
+def test_batchnorm_backward_through_fused_relu_and_residual():
+    """g = dy where the ReLU output > 0: the residual branch receives g, BN's gradients use g."""
+    shape = (8, 32, 15, 20)
+    x, gamma, beta, rm, rv, rng = bn_inputs(shape, 14)
+    res = rng.normal(size=shape).astype(np.float32)
+    dy = rng.normal(size=shape).astype(np.float32)
+    y_ref, mean_ref, inv_ref = rp.batchnorm2d_forward(x, gamma, beta, rm.copy(), rv.copy(), relu=True, residual=res)
+    g = np.where(y_ref > 0, dy, np.float32(0))
+    dx_ref, dgamma_ref, dbeta_ref = rp.batchnorm2d_backward(x, g, gamma, mean_ref, inv_ref)
+    x_grad = torch.empty(shape, device="cuda")
+    gamma_grad, beta_grad = torch.zeros(shape[1], device="cuda"), torch.zeros(shape[1], device="cuda")
+    residual_grad = torch.empty(shape, device="cuda")
+    fused.batchnorm2d_backward(gpu(x), gpu(dy), gpu(gamma), gpu(mean_ref), gpu(inv_ref), training=True,
+                               x_grad=x_grad, gamma_grad=gamma_grad, beta_grad=beta_grad,
+                               accumulate=(False, True, True), gate=gpu(y_ref), residual_grad=residual_grad)
+    np.testing.assert_array_equal(host(residual_grad), g)
+    assert_near(host(x_grad), dx_ref, 1e-5, "dx")
+    np.testing.assert_allclose(host(gamma_grad), dgamma_ref, rtol=2e-6, atol=1e-6 * np.abs(dgamma_ref).max())
+    np.testing.assert_allclose(host(beta_grad), dbeta_ref, rtol=2e-6, atol=1e-6 * np.abs(dbeta_ref).max())
+
+
+def test_batchnorm_is_bitwise_reproducible():
+    x, gamma, beta, rm, rv, rng = bn_inputs((16, 64, 30, 40), 15)
+    dy = gpu(rng.normal(size=x.shape).astype(np.float32))
+    runs = []
+    for _ in range(2):
+        y, mean, inv = fused.batchnorm2d_forward(gpu(x), gpu(gamma), gpu(beta), gpu(rm), gpu(rv), momentum=0.1,
+                                                 eps=1e-5, training=True)
+        grads = [torch.empty_like(y), torch.empty(64, device="cuda"), torch.empty(64, device="cuda")]
+        fused.batchnorm2d_backward(gpu(x), dy, gpu(gamma), mean, inv, training=True, x_grad=grads[0],
+                                   gamma_grad=grads[1], beta_grad=grads[2], accumulate=(False, False, False))
+        runs.append([host(t) for t in (y, mean, inv, *grads)])
+    for a, b in zip(*runs):
+        np.testing.assert_array_equal(a, b)
+
+
+def test_relu_forward_and_backward_are_exact():
+    rng = np.random.default_rng(16)
+    x = rng.normal(size=(3, 5, 7, 11)).astype(np.float32)
+    x.reshape(-1)[:4] = [0.0, -0.0, np.nan, -np.inf]
+    g = rng.normal(size=x.shape).astype(np.float32)
+    y = host(fused.relu_forward(gpu(x)))
+    np.testing.assert_array_equal(np.isnan(y), np.isnan(x))
+    finite = ~np.isnan(x)
+    np.testing.assert_array_equal(y[finite], np.maximum(x, 0)[finite])
+    np.testing.assert_array_equal(host(fused.relu_backward_accumulate(gpu(x), gpu(g), None)), rp.relu_backward(x, g))
+    out = gpu(g)
+    fused.relu_backward_accumulate(gpu(x), gpu(g), out)
+    np.testing.assert_array_equal(host(out), g + rp.relu_backward(x, g))
+    leaky = host(fused.leaky_relu_backward_accumulate(gpu(x), gpu(g), None, 0.2))
+    np.testing.assert_array_equal(leaky, np.where(x > 0, g, np.float32(0.2) * g))
+
+
+@pytest.mark.parametrize("scale,decay", ((1.0, 0.0), (0.5, 0.0), (0.25, 1e-2)))
+def test_adam_matches_the_oracle_bit_for_bit(scale, decay):
+    rng = np.random.default_rng(17)
+    sizes = (1, 7, 256, 257, 4096, 100003)
+    params = [rng.normal(size=s).astype(np.float32) for s in sizes]
+    state = [(np.zeros(s, np.float32), np.zeros(s, np.float32)) for s in sizes]
+    dev_params = [gpu(p) for p in params]
+    dev_state = [(gpu(m), gpu(v)) for m, v in state]
+    for step in (1, 2, 3):
+        grads = [rng.normal(size=s).astype(np.float32) for s in sizes]
+        for p, g, (m, v) in zip(params, grads, state):
+            rp.adam_update(p, g, m, v, lr=1e-3, beta1=0.9, beta2=0.999, eps=1e-8, step=step, grad_scale=scale,
+                           weight_decay=decay)
+        updates = [(p, gpu(g), m, v, 1e-3, decay, step) for p, g, (m, v) in zip(dev_params, grads, dev_state)]
+        fused.adam_update_many(updates, beta1=0.9, beta2=0.999, eps=1e-8, grad_scale=scale)
+        for p, p_ref, (m, v), (m_ref, v_ref) in zip(dev_params, params, dev_state, state):
+            np.testing.assert_array_equal(host(p), p_ref)
+            np.testing.assert_array_equal(host(m), m_ref)
+            np.testing.assert_array_equal(host(v), v_ref)
+    single = gpu(params[3])
+    m, v = gpu(state[3][0]), gpu(state[3][1])
+    g = rng.normal(size=sizes[3]).astype(np.float32)
+    fused.adam_update(single, gpu(g), m, v, lr=1e-3, beta1=0.9, beta2=0.999, eps=1e-8, step=4, grad_scale=scale,
+                      weight_decay=decay)
+    rp.adam_update(params[3], g, *state[3], lr=1e-3, beta1=0.9, beta2=0.999, eps=1e-8, step=4, grad_scale=scale,
+                   weight_decay=decay)
+    np.testing.assert_array_equal(host(single), params[3])
+
+
+def test_adam_rejects_overlapping_tensors():
+    p = torch.zeros(16, device="cuda")
+    with pytest.raises(ValueError):
+        fused.adam_update_many([(p, p, p[:8], p[8:], 1e-3, 0.0, 1)], beta1=0.9, beta2=0.999, eps=1e-8,
+                               grad_scale=1.0)

@@ -1,9 +1,10 @@
-"""End-to-end parity on the GPU: Linear/Dense, the C3 convolution + pooling configuration, and the
-ResNet18 training step (C1 shape) through the Variable/Graph API on the hip_native backend.
+"""End-to-end parity on the GPU through the Variable/Graph API on the hip_native backend: Linear,
+the C3 convolution + pooling configuration, the ResNet18 training step (C1 shape, both graph modes),
+and ResNet18 inference with BN folding and the Conv+ReLU epilogue (a small C5).
 
-The model-level tolerance is "no worse than the reference FP32 path": the GPU result's normwise
-error against the same step computed in float64 by the oracle must stay within a small factor of the
-NumPy float32 path's own error (plus a floor of 1e-6 of the tensor's scale).
+Model-level tolerance, "no worse than the reference FP32 path": against the same step computed in
+float64 by the oracle, the GPU's normwise error stays within 4x the NumPy float32 path's own error
+plus 1e-5 of the tensor's scale.
 """
 
 import numpy as np
@@ -37,26 +38,26 @@ def test_linear_backends_match_fp64():
     x, w = rng.standard_normal((37, 300), dtype=np.float32), rng.standard_normal((300, 23), dtype=np.float32)
     b, g = rng.standard_normal((1, 23), dtype=np.float32), rng.standard_normal((37, 23), dtype=np.float32)
     x64, w64, b64, g64 = (a.astype(np.float64) for a in (x, w, b, g))
-    expected = (x64 @ w64 + b64, g64 @ w64.T, x64.T @ g64, g64.sum(axis=0, keepdims=True))
+    exact = (x64 @ w64 + b64, g64 @ w64.T, x64.T @ g64)
     magnitude = (np.abs(x64) @ np.abs(w64) + np.abs(b64), np.abs(g64) @ np.abs(w64.T), np.abs(x64.T) @ np.abs(g64))
+    db_exact = g64.sum(axis=0, keepdims=True)
     for backend in ("hip_native", "hip_native_kahan", "hip_native_dot2"):
-        nodes = [mf.Variable(gpu(x)), mf.Variable(gpu(w), trainable=True), mf.Variable(gpu(b), trainable=True)]
-        op = mf.Linear(*nodes, backend=backend)
-        op.forward(*(n.value for n in nodes))
+        leaves = [mf.Variable(gpu(x)), mf.Variable(gpu(w), trainable=True), mf.Variable(gpu(b), trainable=True)]
+        op = mf.Linear(*leaves, backend=backend)
+        op.forward(*(leaf.value for leaf in leaves))
         op.grad = gpu(g)
         op.backward()
-        got = [host(op.value)] + [host(n.grad) for n in nodes]
-        for actual, exact, bound in zip(got[:3], expected[:3], magnitude):
-            assert np.all(np.abs(actual - exact) <= gamma_k(300) * bound + EPS32 * np.abs(exact) + 1e-30), backend
-        assert np.all(np.abs(got[3] - expected[3]) <= np.spacing(np.abs(expected[3]).astype(np.float32))), backend
-    # skip dX for an input without requires_grad
-    nodes = [mf.Variable(gpu(x), requires_grad=False), mf.Variable(gpu(w), trainable=True),
-             mf.Variable(gpu(b), trainable=True)]
-    op = mf.Linear(*nodes, backend="hip_native")
-    op.forward(*(n.value for n in nodes))
+        got = [host(op.value)] + [host(leaf.grad) for leaf in leaves]
+        for actual, ref, bound in zip(got[:3], exact, magnitude):
+            assert np.all(np.abs(actual - ref) <= gamma_k(300) * bound + EPS32 * np.abs(ref) + 1e-30), backend
+        assert np.all(np.abs(got[3] - db_exact) <= np.spacing(np.abs(db_exact).astype(np.float32))), backend
+    leaves = [mf.Variable(gpu(x), requires_grad=False), mf.Variable(gpu(w), trainable=True),
+              mf.Variable(gpu(b), trainable=True)]
+    op = mf.Linear(*leaves, backend="hip_native")
+    op.forward(*(leaf.value for leaf in leaves))
     op.grad = gpu(g)
     op.backward()
-    assert nodes[0].grad is None
+    assert leaves[0].grad is None  # an input without requires_grad skips the dX GEMM
 
 
 def test_c3_convolution_and_pool_configuration():
@@ -66,15 +67,15 @@ def test_c3_convolution_and_pool_configuration():
     w = (rng.standard_normal((64, 64, 3, 3)) * np.sqrt(2.0 / 576)).astype(np.float32)
     b = np.zeros(64, np.float32)
     y, cols = native.conv2d_forward(gpu(x), gpu(w), gpu(b), stride=(1, 1), padding=(1, 1))
-    y_ref64, cols_ref = rp.conv2d_forward(x.astype(np.float64), w.astype(np.float64), b, (1, 1), (1, 1))
+    y64, cols_ref = rp.conv2d_forward(x.astype(np.float64), w.astype(np.float64), b, (1, 1), (1, 1))
     np.testing.assert_array_equal(host(cols), cols_ref.astype(np.float32))
-    assert_near(host(y), y_ref64, 1e-5, "y")
+    assert_near(host(y), y64, 1e-5, "y")
     pooled, ctx = native.maxpool2d_forward(y, kernel_size=(2, 2), stride=(2, 2))
     y_host = host(y)
-    p_ref, argmax_ref = rp.maxpool2d_native_forward(y_host, (2, 2), (2, 2))
-    np.testing.assert_array_equal(host(pooled), p_ref)
+    pooled_ref, argmax_ref = rp.maxpool2d_native_forward(y_host, (2, 2), (2, 2))
+    np.testing.assert_array_equal(host(pooled), pooled_ref)
     np.testing.assert_array_equal(host(ctx.argmax), argmax_ref)
-    dp = rng.standard_normal(p_ref.shape).astype(np.float32)
+    dp = rng.standard_normal(pooled_ref.shape).astype(np.float32)
     dy = native.maxpool2d_backward(gpu(dp), ctx)
     dy_ref = rp.maxpool2d_native_backward(dp, argmax_ref, y_host.shape)
     np.testing.assert_array_equal(host(dy), dy_ref)
@@ -86,7 +87,7 @@ def test_c3_convolution_and_pool_configuration():
     assert np.all(np.abs(host(db) - db64) <= np.spacing(np.abs(db64).astype(np.float32)))
 
 
-def _build_gpu_resnet(batch, height, width, base_width=64, seed=0):
+def build_resnet(batch, height, width, base_width=64, seed=0, optimize=False):
     model = mf.ResNet18(output_dim=2, base_width=base_width, initializer=mf.make_initializer(seed=seed),
                         conv_backend="hip_native")
     x_np, t_np = oracle_resnet.synthetic_batch(batch, height, width, seed=seed)
@@ -94,20 +95,17 @@ def _build_gpu_resnet(batch, height, width, base_width=64, seed=0):
     t = mf.Variable(gpu(t_np), requires_grad=False, name="targets")
     out = model(x)
     loss = mf.MSELoss(out, t)
-    graph = mf.Graph(loss)
-    return model, graph, out, loss, x_np, t_np
+    return model, mf.Graph(loss, optimize=optimize), out, loss, x_np, t_np
 
 
-def _oracle_names(base_width):
-    params, _ = oracle_resnet.init_params(base_width=base_width, seed=0)
-    return list(params)
-
-
-@pytest.mark.parametrize("batch,height,width,base_width", [(2, 120, 160, 64), (4, 64, 64, 16)],
-                         ids=("C1-bs2-120x160", "small"))
-def test_resnet18_training_step_matches_numpy_reference(batch, height, width, base_width):
-    print("resnet step", batch, height, width, base_width, flush=True)
-    model, graph, out, loss, x_np, t_np = _build_gpu_resnet(batch, height, width, base_width)
+@pytest.mark.parametrize("batch,height,width,base_width,optimize",
+                         [(2, 120, 160, 64, False), (2, 120, 160, 64, True), (4, 64, 64, 16, True)],
+                         ids=("C1-bs2-120x160", "C1-bs2-120x160-fused-units", "small-fused-units"))
+def test_resnet18_training_step_matches_numpy_reference(batch, height, width, base_width, optimize):
+    print("resnet step", batch, height, width, base_width, optimize, flush=True)
+    model, graph, out, loss, x_np, t_np = build_resnet(batch, height, width, base_width, optimize=optimize)
+    if optimize:
+        assert len(graph._bn_groups) == 17  # stem + 8 blocks x (BN+ReLU, BN+Add+ReLU)
     opt = mf.Adam(graph, learning_rate=1e-3)
     opt.one_step()
     grads = [host(p.grad) for p in model.params]
@@ -117,30 +115,40 @@ def test_resnet18_training_step_matches_numpy_reference(batch, height, width, ba
 
     params32, running32 = oracle_resnet.init_params(base_width=base_width, seed=0)
     params64, running64 = oracle_resnet.as_dtype(params32, running32, np.float64)
-    loss32, grads32, out32 = oracle_resnet.forward_backward(params32, running32, x_np, t_np)
+    _, grads32, out32 = oracle_resnet.forward_backward(params32, running32, x_np, t_np)
     loss64, grads64, out64 = oracle_resnet.forward_backward(params64, running64, x_np.astype(np.float64),
                                                             t_np.astype(np.float64))
-    names = list(params32)
     assert abs(gpu_loss - loss64) <= 1e-4 * abs(loss64)
     assert normwise(gpu_out, out64) <= max(4 * normwise(out32, out64), 1e-5)
     floor = 1e-5 * max(np.abs(g).max() for g in grads64.values())
-    for name, g in zip(names, grads):
+    for name, g in zip(params32, grads):
         ref = grads64[name]
-        err_gpu = np.abs(g - ref).max()
-        err_np = np.abs(grads32[name] - ref).max()
-        assert err_gpu <= 4 * err_np + 1e-5 * np.abs(ref).max() + floor, (name, err_gpu, err_np)
-    # The Adam step of the reference on the GPU gradients reproduces our update bit for bit.
-    for name, p_new, g in zip(names, updated, grads):
+        err_gpu, err_numpy = np.abs(g - ref).max(), np.abs(grads32[name] - ref).max()
+        assert err_gpu <= 4 * err_numpy + 1e-5 * np.abs(ref).max() + floor, (name, err_gpu, err_numpy)
+    # The reference's Adam step applied to the GPU's gradients reproduces the GPU update bit for bit.
+    for name, p_new, g in zip(params32, updated, grads):
         p = params32[name].copy()
-        m, v = np.zeros_like(p), np.zeros_like(p)
-        rp.adam_update(p, g, m, v, lr=1e-3, beta1=0.9, beta2=0.999, eps=1e-8, step=1)
-        np.testing.assert_allclose(p_new, p, rtol=0, atol=2 * np.spacing(np.abs(p).max()), err_msg=name)
+        rp.adam_update(p, g, np.zeros_like(p), np.zeros_like(p), lr=1e-3, beta1=0.9, beta2=0.999, eps=1e-8, step=1)
+        np.testing.assert_array_equal(p_new, p, err_msg=name)
+
+
+def test_fused_units_reproduce_the_unfused_graph_bit_for_bit():
+    """Graph(optimize=True) runs BN+ReLU and BN+Add+ReLU as single units with the same float32
+    operations as the separate BN, Add and ReLU nodes, so both graphs give the same bits."""
+    runs = []
+    for optimize in (False, True):
+        model, graph, out, loss, _, _ = build_resnet(2, 64, 64, base_width=16, optimize=optimize)
+        graph.forward()
+        graph.backward()
+        runs.append([host(out.value)] + [host(p.grad) for p in model.params])
+    for a, b in zip(*runs):
+        np.testing.assert_array_equal(a, b)
 
 
 def test_resnet18_two_steps_are_deterministic():
     runs = []
     for _ in range(2):
-        model, graph, out, loss, _, _ = _build_gpu_resnet(2, 64, 64, base_width=16)
+        model, graph, _, _, _, _ = build_resnet(2, 64, 64, base_width=16)
         opt = mf.Adam(graph, learning_rate=1e-3)
         for _ in range(2):
             opt.one_step()
@@ -160,12 +168,46 @@ def test_shared_weight_on_two_branches_accumulates():
     b = mf.Conv2D_Op(x, w, stride=2, padding=0, backend="hip_native")
     t1 = mf.Variable(torch.zeros((2, 4, 10, 12), device="cuda"), requires_grad=False)
     t2 = mf.Variable(torch.zeros((2, 4, 4, 5), device="cuda"), requires_grad=False)
-    loss = mf.Add(mf.MSELoss(a, t1), mf.MSELoss(b, t2))
-    graph = mf.Graph(loss)
+    graph = mf.Graph(mf.Add(mf.MSELoss(a, t1), mf.MSELoss(b, t2)))
     graph.forward()
     graph.backward()
-    ya = naive.conv_forward(x_np.astype(np.float64), w_np.astype(np.float64), (1, 1), (1, 1))
-    yb = naive.conv_forward(x_np.astype(np.float64), w_np.astype(np.float64), (2, 2), (0, 0))
-    _, gwa = naive.conv_backward(x_np.astype(np.float64), w_np.astype(np.float64), 2 * ya / ya.size, (1, 1), (1, 1))
-    _, gwb = naive.conv_backward(x_np.astype(np.float64), w_np.astype(np.float64), 2 * yb / yb.size, (2, 2), (0, 0))
+    x64, w64 = x_np.astype(np.float64), w_np.astype(np.float64)
+    ya, yb = naive.conv_forward(x64, w64, (1, 1), (1, 1)), naive.conv_forward(x64, w64, (2, 2), (0, 0))
+    _, gwa = naive.conv_backward(x64, w64, 2 * ya / ya.size, (1, 1), (1, 1))
+    _, gwb = naive.conv_backward(x64, w64, 2 * yb / yb.size, (2, 2), (0, 0))
     assert_near(host(w.grad), gwa + gwb, 1e-5, "shared dW")
+
+
+def test_resnet18_inference_with_bn_folding_and_conv_relu_epilogue():
+    """A small C5: eval-mode BN with random running statistics, folded into the convolutions, the
+    stem and conv1 ReLUs fused into their epilogues by a second pass; the output against the
+    oracle's eval-mode forward in float64."""
+    batch, size, width = 4, 64, 16
+    model = mf.ResNet18(output_dim=2, base_width=width, initializer=mf.make_initializer(seed=0),
+                        conv_backend="hip_native")
+    params32, running32 = oracle_resnet.init_params(base_width=width, seed=0)
+    rng = np.random.default_rng(5)
+    bns = [model.stem_bn] + [bn for block in model.blocks()
+                             for bn in (block.bn1, block.bn2, *((block.downsample_bn,) if block.downsample else ()))]
+    assert len(bns) == len(running32)
+    for bn, name in zip(bns, running32):
+        mean = rng.normal(0, 0.1, bn.num_features).astype(np.float32)
+        var = rng.uniform(0.5, 1.5, bn.num_features).astype(np.float32)
+        bn.running_mean.copy_(gpu(mean))
+        bn.running_var.copy_(gpu(var))
+        running32[name] = (mean, var)
+    model.eval()
+    x_np, t_np = oracle_resnet.synthetic_batch(batch, size, size, seed=0)
+    out = model(mf.Variable(gpu(x_np), requires_grad=False))
+    root, stats = mf.apply_graph_optimizations(out, mode="inference", fold_constants=False)
+    assert stats["bn_folds"] == 20
+    graph = mf.Graph(root, optimize=True)
+    assert graph._opt_stats["conv_act_fusions"] == 9  # stem + conv1 of each block
+    graph.forward()
+    got = host(graph.target_node.value)
+    params64, running64 = oracle_resnet.as_dtype(params32, running32, np.float64)
+    _, _, out64 = oracle_resnet.forward_backward(params64, running64, x_np.astype(np.float64),
+                                                 t_np.astype(np.float64), training=False)
+    _, _, out32 = oracle_resnet.forward_backward(params32, {k: (m.copy(), v.copy()) for k, (m, v) in running32.items()},
+                                                 x_np, t_np, training=False)
+    assert normwise(got, out64) <= max(4 * normwise(out32, out64), 1e-5)
