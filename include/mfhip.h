@@ -60,11 +60,11 @@ MFH_API int mfh_conv_im2col(uint64_t x, uint64_t cols, int N, int CI, int H, int
                             int OW, int SH, int SW, int PH, int PW, uint64_t stream);
 
 /* y (N,CO,OH,OW) = act(conv(x, weight) + bias). cols receives im2col(x) (kept by the caller for
- * dW). With rows == 0 each image's output is one GEMM W cols_n^T written straight into NCHW with
- * bias and activation in its epilogue; with rows (N*OH*OW x CO floats) given, rows = cols W^T is
- * formed first and an epilogue kernel transposes it. activation: 0 none, 1 ReLU,
- * 2 LeakyReLU(alpha > 0). bias may be 0. workspace (workspace_floats floats, may be 0) lets the
- * rows GEMM split K.
+ * dW). With rows == 0 one GEMM W cols^T over all images writes y straight into NCHW, bias and
+ * activation in its epilogue (workspace: the mfh_gemm_workspace(CO, N*OH*OW, CI*KH*KW) floats that
+ * let it split K, or 0); with rows (N*OH*OW x CO floats) given, rows = cols W^T is formed first
+ * (workspace: mfh_gemm_workspace(N*OH*OW, CO, CI*KH*KW)) and an epilogue kernel transposes it.
+ * activation: 0 none, 1 ReLU, 2 LeakyReLU(alpha > 0). bias may be 0.
  * Replaces mf_conv_forward, native_cublas.cpp:1441-1461. */
 MFH_API int mfh_conv_forward(uint64_t x, uint64_t weight, uint64_t bias, uint64_t cols, uint64_t rows, uint64_t y,
                              int N, int CI, int H, int W, int CO, int KH, int KW, int OH, int OW, int SH, int SW,
@@ -76,8 +76,9 @@ MFH_API int mfh_conv_forward(uint64_t x, uint64_t weight, uint64_t bias, uint64_
  *          doubles, grid_x in [1, ceil(OH*OW / 64)]) reduced in a fixed order;
  *   dw   (CO, CI*KH*KW) = dyT^T cols, dyT (N*OH*OW x CO) being the gated, transposed dy (split-K on
  *          dw_engine through the workspace);
- *   dx   = col2im of grad_cols, where grad_cols (N*OH*OW*CI*KH*KW floats) receives, per image, the
- *          transposed column gradient W^T dy_n (CI*KH*KW x OH*OW) on dx_engine.
+ *   dx   = col2im of grad_cols (N*OH*OW*CI*KH*KW floats), which receives the feature-major column
+ *          gradient on dx_engine: W^T dyT^T (CI*KH*KW x N*OH*OW) when dyT is formed (dw requested
+ *          or a fused activation), else W^T dy_n (CI*KH*KW x OH*OW) per image from the NCHW dy.
  * dx/grad_cols and partial/db are given together or not at all; dw needs cols and dyT; dx through
  * an activation needs dyT.
  * Replaces mf_conv_backward_plans / mf_conv_backward, native_cublas.cpp:1465-1532. */

@@ -89,32 +89,36 @@ int validate_norm(const NormShape& s) {
     return OK;
 }
 
-// The per-image column-gradient GEMM of dX: gcT[n] (K x OHW) = W^T dy_n, with dy_n read either from
-// the NCHW gradient (CO x OHW per image) or from its transposed rows dyT (OHW x CO per image).
+// The column gradient of dX, feature-major: with the transposed rows dyT (M x CO) one GEMM
+// gcT (K x M) = W^T dyT^T over every image; from the NCHW gradient alone one GEMM per image,
+// gcT[n] (K x OHW) = W^T dy_n (dy_n is CO x OHW). Returns whether the layout is per image.
 int column_gradient(int engine, const ConvGeometry& g, const float* weight, const float* dy_nchw, const float* dyT,
-                    float* gcT, hipStream_t stream) {
+                    float* gcT, bool* per_image, hipStream_t stream) {
     const int K = g.features(), ohw = g.ohw();
     GemmOperands o{};
     o.trans_a = true;  // W stored CO x K
     o.M = K;
-    o.N = ohw;
     o.K = g.CO;
     o.a = weight;
     o.lda = K;
+    o.c = gcT;
+    *per_image = dyT == nullptr;
     if (dyT) {
-        o.trans_b = true;  // dyT_n stored OHW x CO
+        o.trans_b = true;  // dyT stored M x CO
+        o.N = g.rows();
         o.b = dyT;
         o.ldb = g.CO;
+        o.ldc = g.rows();
     } else {
         o.trans_b = false;  // dy_n stored CO x OHW
+        o.N = ohw;
         o.b = dy_nchw;
         o.ldb = ohw;
+        o.ldc = ohw;
+        o.batch = g.N;
+        o.b_batch = static_cast<long long>(g.CO) * ohw;
+        o.c_batch = static_cast<long long>(K) * ohw;
     }
-    o.c = gcT;
-    o.ldc = ohw;
-    o.batch = g.N;
-    o.b_batch = static_cast<long long>(g.CO) * ohw;
-    o.c_batch = static_cast<long long>(K) * ohw;
     return gemm_launch(engine, stream, o, GemmEpilogue{}, nullptr, 0);
 }
 
@@ -229,11 +233,12 @@ MFH_API int mfh_conv_forward(std::uint64_t x, std::uint64_t weight, std::uint64_
         return launch_conv_epilogue(as_ptr<const float>(rows), e.bias, as_ptr<float>(y), N, ohw, CO, activation, alpha,
                                     s);
     }
-    // Per image, y_n (CO x OHW) = W cols_n^T written straight into NCHW, bias per output row.
+    // One GEMM over every image: Y (CO x N*OH*OW) = W cols^T, with output column j = (n, p) stored at
+    // y[n][co][p] (a segmented epilogue), bias per output row; the workspace lets it split K.
     GemmOperands o{};
-    o.trans_b = true;  // cols_n stored OHW x K
+    o.trans_b = true;  // cols stored M x K
     o.M = CO;
-    o.N = ohw;
+    o.N = M;
     o.K = K;
     o.a = as_ptr<const float>(weight);
     o.lda = K;
@@ -241,11 +246,10 @@ MFH_API int mfh_conv_forward(std::uint64_t x, std::uint64_t weight, std::uint64_
     o.ldb = K;
     o.c = as_ptr<float>(y);
     o.ldc = ohw;
-    o.batch = N;
-    o.b_batch = static_cast<long long>(ohw) * K;
-    o.c_batch = static_cast<long long>(CO) * ohw;
     e.bias_mode = bias ? BIAS_ROW : BIAS_NONE;
-    return gemm_launch(engine, s, o, e, nullptr, 0);
+    e.segment = ohw;
+    e.segment_stride = static_cast<long long>(CO) * ohw;
+    return gemm_launch(engine, s, o, e, as_ptr<float>(workspace), workspace_floats);
 }
 
 MFH_API int mfh_conv_backward(std::uint64_t weight, std::uint64_t dy, std::uint64_t y, std::uint64_t cols,
@@ -297,9 +301,12 @@ MFH_API int mfh_conv_backward(std::uint64_t weight, std::uint64_t dy, std::uint6
         MFH_TRY(gemm_launch(dw_engine, s, o, GemmEpilogue{}, as_ptr<float>(workspace), workspace_floats));
     }
     if (!dx) return OK;
+    // dX from the transposed rows when they were formed (one GEMM over all pixels), else per image
+    // from the NCHW gradient.
+    bool per_image = false;
     MFH_TRY(column_gradient(dx_engine, g, as_ptr<const float>(weight), as_ptr<const float>(dy),
-                            gated ? as_ptr<const float>(dyT) : nullptr, as_ptr<float>(grad_cols), s));
-    return launch_col2im_t(as_ptr<const float>(grad_cols), as_ptr<float>(dx), g, s);
+                            need_rows ? as_ptr<const float>(dyT) : nullptr, as_ptr<float>(grad_cols), &per_image, s));
+    return launch_col2im_t(as_ptr<const float>(grad_cols), as_ptr<float>(dx), g, per_image, s);
 }
 
 MFH_API int mfh_pool_forward(std::uint64_t x, std::uint64_t y, std::uint64_t argmax, int N, int C, int H, int W,

@@ -9,6 +9,8 @@
 #include <cstdint>
 #include <string>
 
+#include "fastdiv.h"
+
 namespace mfh {
 
 enum Status : int {
@@ -63,8 +65,9 @@ struct ConvGeometry {
 
 // ---- conv.hip ---------------------------------------------------------------------------------
 int launch_im2col(const float* x, float* cols, const ConvGeometry& g, hipStream_t stream);
-// dx from the per-image transposed column gradient gcT[n][CI*KH*KW][OH*OW].
-int launch_col2im_t(const float* gcT, float* dx, const ConvGeometry& g, hipStream_t stream);
+// dx from the feature-major column gradient: gcT[n][CI*KH*KW][OH*OW] when per_image, else
+// gcT[CI*KH*KW][N*OH*OW].
+int launch_col2im_t(const float* gcT, float* dx, const ConvGeometry& g, bool per_image, hipStream_t stream);
 int launch_conv_epilogue(const float* rows, const float* bias, float* y, int N, int OHW, int CO, int act,
                          float alpha, hipStream_t stream);
 int conv_grad_tile();  // pixels per conv_grad_rows tile (grid_x counts these tiles)
@@ -90,16 +93,17 @@ const GemmTile& gemm_tile(int index);
 struct GemmPlan {
     int tile, slices, k_chunk;
 };
-// Tile and split-K choice for C(M, N) over K (the engine's automatic plan).
-GemmPlan gemm_auto_plan(int M, int N, int K);
+// Tile and split-K choice for C(M, N) over K, or for `batch` such problems at once (never split).
+GemmPlan gemm_auto_plan(int M, int N, int K, int batch = 1);
 // Plan from an engine code: 1 = automatic, 16 + tile * 128 + (slices - 1) = explicit.
-int gemm_plan_from_engine(int engine, int M, int N, int K, GemmPlan* plan);
+int gemm_plan_from_engine(int engine, int M, int N, int K, GemmPlan* plan, int batch = 1);
 bool gemm_engine_valid(int engine);
 std::int64_t gemm_workspace_floats(const GemmPlan& plan, int M, int N);
 
 constexpr int BIAS_NONE = 0, BIAS_COLUMN = 1, BIAS_ROW = 2;
 
-// Kernel argument block of the MFMA GEMM (see gemm.hip for the meaning of split and the batches).
+// Kernel argument block of the MFMA GEMM (see gemm.hip for the meaning of split, the batches and
+// the segmented output).
 struct GemmParams {
     const float* A;
     const float* B;
@@ -110,6 +114,9 @@ struct GemmParams {
     long long a_batch, b_batch, c_batch;
     int bias_mode, act;
     float alpha;
+    int segment;               // 0: C is dense; > 0: output column j is (j / segment, j % segment)
+    FastDiv segment_div;       // division by segment
+    long long segment_stride;  // distance between consecutive segments of C
 };
 
 // One GEMM problem, or `batch` of them at constant strides: C(M x N) = op(A) op(B), row-major;
@@ -127,12 +134,17 @@ struct GemmOperands {
     long long a_batch = 0, b_batch = 0, c_batch = 0;
 };
 
-// What happens to each output after the product: + bias (per column or per row), activation.
+// What happens to each output after the product: + bias (per column or per row), activation, and
+// where it goes. With segment > 0 output (i, j) is stored at
+// c + (j / segment) * segment_stride + i * ldc + j % segment: one GEMM over all images writes an
+// NCHW tensor (segment = OH*OW, segment_stride = C*OH*OW, ldc = OH*OW).
 struct GemmEpilogue {
     const float* bias = nullptr;
     int bias_mode = BIAS_NONE;
     int act = ACT_NONE;
     float alpha = 0.0f;
+    int segment = 0;
+    long long segment_stride = 0;
 };
 
 // Runs the engine; splits K through the workspace (never for batches) only when it holds the

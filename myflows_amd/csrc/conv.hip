@@ -34,15 +34,49 @@ __global__ __launch_bounds__(256) void im2col_kernel(const float* __restrict__ x
     cols[idx] = v;
 }
 
+// The same matrix four features at a time (K % 4 == 0): thread t writes cols elements 4t .. 4t+3 of
+// one row with one 16-byte store, stepping (ci, kh, kw) forward from the first without divisions.
+__global__ __launch_bounds__(256) void im2col_vec4_kernel(const float* __restrict__ x, float* __restrict__ cols,
+                                                          int quads, FastDiv div_k, FastDiv div_kw, FastDiv div_kh,
+                                                          FastDiv div_ow, FastDiv div_oh, int CI, int KH, int KW,
+                                                          int H, int W, int SH, int SW, int PH, int PW) {
+    const int q = blockIdx.x * 256 + threadIdx.x;
+    if (q >= quads) return;
+    const int first = q * 4;
+    int feature, kw, kh, ow, oh;
+    const int row = div_k.divmod(first, feature);
+    const int t = div_kw.divmod(feature, kw);
+    int ci = div_kh.divmod(t, kh);
+    const int t2 = div_ow.divmod(row, ow);
+    const int n = div_oh.divmod(t2, oh);
+    const int ih0 = oh * SH - PH, iw0 = ow * SW - PW;
+    const float* image = x + static_cast<long long>(n) * CI * H * W;
+    float v[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int ih = ih0 + kh, iw = iw0 + kw;
+        v[j] = (ih >= 0 && ih < H && iw >= 0 && iw < W) ? image[(ci * H + ih) * W + iw] : 0.0f;
+        if (++kw == KW) {
+            kw = 0;
+            if (++kh == KH) {
+                kh = 0;
+                ++ci;
+            }
+        }
+    }
+    *reinterpret_cast<float4*>(cols + first) = make_float4(v[0], v[1], v[2], v[3]);
+}
+
 // dx[n, ci, ih, iw] = sum over every window position (oh, ow) that reads (ih, iw), visited in
-// increasing (oh, ow) order, of the column gradient of feature (ci, kh, kw) at that position.
-// The column gradient arrives transposed per image, gcT[n][(ci*KH + kh)*KW + kw][oh*OW + ow], so
-// for a fixed (kh, kw) the threads of consecutive iw read consecutive ow: the gather is coalesced.
-// No atomics, so the result is deterministic.
+// increasing (oh, ow) order, of the column gradient of feature f = (ci*KH + kh)*KW + kw at that
+// position. The column gradient is feature-major, element (f, n, oh*OW + ow) at
+// f * f_stride + n * n_stride + oh*OW + ow ([f][n*OH*OW + p] or [n][f][p]), so for a fixed (kh, kw)
+// the threads of consecutive iw read consecutive ow: the gather is coalesced. No atomics, so the
+// result is deterministic.
 __global__ __launch_bounds__(256) void col2im_t_kernel(const float* __restrict__ gcT, float* __restrict__ dx,
                                                        int total, FastDiv div_w, FastDiv div_h, FastDiv div_ci,
                                                        int CI, int KH, int KW, int OH, int OW, int SH, int SW, int PH,
-                                                       int PW) {
+                                                       int PW, long long f_stride, long long n_stride) {
     const int idx = blockIdx.x * 256 + threadIdx.x;
     if (idx >= total) return;
     int iw, ih, ci;
@@ -55,15 +89,14 @@ __global__ __launch_bounds__(256) void col2im_t_kernel(const float* __restrict__
     const int oh_hi = min(OH - 1, hp / SH);
     const int ow_lo = wp >= KW ? (wp - KW) / SW + 1 : 0;
     const int ow_hi = min(OW - 1, wp / SW);
-    const int ohw = OH * OW;
-    const float* image = gcT + (static_cast<long long>(n) * CI + ci) * KH * KW * ohw;
+    const float* image = gcT + n * n_stride + static_cast<long long>(ci) * KH * KW * f_stride;
     float sum = 0.0f;
     for (int oh = oh_lo; oh <= oh_hi; ++oh) {
         const int kh = hp - oh * SH;
-        const float* plane_row = image + kh * KW * ohw + oh * OW;
+        const float* row = image + kh * KW * f_stride + oh * OW;
         for (int ow = ow_lo; ow <= ow_hi; ++ow) {
             const int kw = wp - ow * SW;
-            sum += plane_row[kw * ohw + ow];
+            sum += row[kw * f_stride + ow];
         }
     }
     dx[idx] = sum;
@@ -246,17 +279,27 @@ __global__ __launch_bounds__(256) void pool_backward_kernel(const float* __restr
 int launch_im2col(const float* x, float* cols, const ConvGeometry& g, hipStream_t stream) {
     const int K = g.features();
     const int total = g.rows() * K;
+    if (K % 4 == 0 && (reinterpret_cast<std::uintptr_t>(cols) & 15) == 0) {
+        const int quads = total / 4;
+        im2col_vec4_kernel<<<blocks_for(quads, 256), 256, 0, stream>>>(
+            x, cols, quads, FastDiv(K), FastDiv(g.KW), FastDiv(g.KH), FastDiv(g.OW), FastDiv(g.OH), g.CI, g.KH, g.KW,
+            g.H, g.W, g.SH, g.SW, g.PH, g.PW);
+        return MFH_CHECK_LAUNCH("im2col_vec4", stream);
+    }
     im2col_kernel<<<blocks_for(total, 256), 256, 0, stream>>>(x, cols, total, FastDiv(K), FastDiv(g.KW),
                                                                 FastDiv(g.KH), FastDiv(g.OW), FastDiv(g.OH), g.CI,
                                                                 g.H, g.W, g.SH, g.SW, g.PH, g.PW);
     return MFH_CHECK_LAUNCH("im2col", stream);
 }
 
-int launch_col2im_t(const float* gcT, float* dx, const ConvGeometry& g, hipStream_t stream) {
+int launch_col2im_t(const float* gcT, float* dx, const ConvGeometry& g, bool per_image, hipStream_t stream) {
     const int total = g.N * g.CI * g.H * g.W;
+    const long long ohw = g.ohw();
+    const long long f_stride = per_image ? ohw : static_cast<long long>(g.rows());
+    const long long n_stride = per_image ? ohw * g.features() : ohw;
     col2im_t_kernel<<<blocks_for(total, 256), 256, 0, stream>>>(gcT, dx, total, FastDiv(g.W), FastDiv(g.H),
                                                                   FastDiv(g.CI), g.CI, g.KH, g.KW, g.OH, g.OW, g.SH,
-                                                                  g.SW, g.PH, g.PW);
+                                                                  g.SW, g.PH, g.PW, f_stride, n_stride);
     return MFH_CHECK_LAUNCH("col2im_t", stream);
 }
 

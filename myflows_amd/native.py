@@ -38,7 +38,7 @@ MATMUL_ACCUMULATION = {"fp32": 0, "kahan": 1, "dot2": 2}
 ACTIVATION_CODES = {None: 0, "relu": 1, "leaky_relu": 2}
 PLAN_BASE, PLAN_SLICES = 16, 128       # explicit plan code = PLAN_BASE + tile * PLAN_SLICES + slices - 1
 CONV_GRAD_TILE = 64                    # pixels per tile of the transposed-gradient kernel
-ROWS_PATH_MAX_PIXELS = 32              # conv forward through a rows GEMM + epilogue below this OH*OW
+ROWS_PATH_MAX_PIXELS = 0               # conv forward through a rows GEMM + epilogue below this OH*OW
 _STATUS_TEXT = {1: "initialization failed", 2: "invalid argument", 3: "HIP runtime error", 5: "wrong HIP device"}
 
 
@@ -358,12 +358,13 @@ def conv2d_forward(x, weight, bias=None, *, stride=(1, 1), padding=(0, 0), activ
     device = x.device
     cols = torch.empty((g.m, g.k), dtype=torch.float32, device=device)
     y = torch.empty(g.out_shape, dtype=torch.float32, device=device)
-    rows = workspace = None
-    floats = 0
-    if g.ohw < ROWS_PATH_MAX_PIXELS:
+    rows = None
+    if g.ohw < ROWS_PATH_MAX_PIXELS:  # rows = cols W^T, then the NCHW epilogue kernel
         rows = torch.empty((g.m, g.co), dtype=torch.float32, device=device)
         engine = _engine_for(engine, "NT", g.m, g.co, g.k)
         workspace, floats = _workspace((engine, g.m, g.co, g.k))
+    else:  # one GEMM W cols^T over all images, stored into NCHW
+        workspace, floats = _workspace((engine, g.co, g.m, g.k))
     _call("mfh_conv_forward", x.data_ptr(), weight.data_ptr(), _addr(bias), cols.data_ptr(), _addr(rows),
           y.data_ptr(), *g.c_args(), act, alpha, engine, _addr(workspace), floats, _stream())
     return y, cols

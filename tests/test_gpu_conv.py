@@ -47,7 +47,8 @@ def fp64_case(case):
 
 @pytest.mark.parametrize("case", CONV_CASES + PERFORMANCE_CASES, ids=lambda c: c[0])
 def test_forward_and_gradients_match_fp64_loops(case):
-    """Covers both forward paths: OH*OW < 32 (rows GEMM + epilogue) and the per-image NCHW GEMM."""
+    """The forward is one GEMM over all images stored into NCHW (split over K when the planner asks);
+    dX goes through the transposed rows, dW through a split-K GEMM."""
     print("conv case", case[0], flush=True)
     x, w, _, dy, pre = fp64_case(case)
     op, y, (dx, dw, db) = run_operator(case)
@@ -174,3 +175,17 @@ def test_debug_sync_and_build_info():
         run_operator(CONV_CASES[1])
     finally:
         native.set_debug_sync(False)
+
+
+@pytest.mark.parametrize("case", (CONV_CASES[1], PERFORMANCE_CASES[0]), ids=lambda c: c[0])
+def test_rows_path_forward_matches_the_nchw_gemm(case, monkeypatch):
+    """The reference's forward sequence (rows = cols W^T, then the NCHW epilogue kernel) and the
+    single segmented GEMM agree within the FP64 tolerance and both keep the activation."""
+    _, w_np, b_np, _ = conv_fixture(case)
+    x, w, b = (gpu(a) for a in conv_fixture(case)[:3])
+    direct, _ = native.conv2d_forward(x, w, b, stride=case[3], padding=case[4], activation="relu")
+    monkeypatch.setattr(native, "ROWS_PATH_MAX_PIXELS", 1 << 30)
+    rows, _ = native.conv2d_forward(x, w, b, stride=case[3], padding=case[4], activation="relu")
+    _, _, _, _, pre = fp64_case(case)
+    assert_near(host(direct), np.maximum(pre, 0), 1e-5, "direct")
+    assert_near(host(rows), np.maximum(pre, 0), 1e-5, "rows")

@@ -179,3 +179,16 @@ def test_teaching_kernel_bias_and_argument_checks():
         native.matmul(gpu(a), gpu(b), tile=8)
     with pytest.raises(TypeError):
         native.matmul(gpu(a).double(), gpu(b))
+
+
+@pytest.mark.parametrize("layout", LAYOUTS)
+def test_every_unsplit_tile_adds_in_the_same_order(layout):
+    """All tiles use the same stage depth and k mapping, so one-pass products are bit-identical
+    whatever the tile (and the XCD tile order)."""
+    trans_a, trans_b = LAYOUTS[layout]
+    rng = np.random.default_rng(6)
+    a, b, _, _ = operands(rng, 300, 260, 1000, trans_a, trans_b)
+    results = [native.gemm(gpu(a), gpu(b), trans_a=trans_a, trans_b=trans_b, plan=(tile, 1))
+               for tile in native.tile_catalog()]
+    for other in results[1:]:
+        assert torch.equal(results[0], other)
