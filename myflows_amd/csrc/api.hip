@@ -174,7 +174,7 @@ MFH_API int mfh_init(void) {
     const char* flag = std::getenv("MFHIP_SYNC");
     if (flag && flag[0] && flag[0] != '0') s.sync_each_launch = true;
     int runtime = 0;
-    hipRuntimeGetVersion(&runtime);
+    if (hipRuntimeGetVersion(&runtime) != hipSuccess) runtime = 0;
     s.cus = props.multiProcessorCount;
     s.device = device;
     const double ms = std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0).count();
@@ -306,6 +306,81 @@ MFH_API int mfh_conv_backward(std::uint64_t weight, std::uint64_t dy, std::uint6
     bool per_image = false;
     MFH_TRY(column_gradient(dx_engine, g, as_ptr<const float>(weight), as_ptr<const float>(dy),
                             need_rows ? as_ptr<const float>(dyT) : nullptr, as_ptr<float>(grad_cols), &per_image, s));
+    return launch_col2im_t(as_ptr<const float>(grad_cols), as_ptr<float>(dx), g, per_image, s);
+}
+
+MFH_API int mfh_conv_forward_implicit(std::uint64_t x, std::uint64_t weight, std::uint64_t bias, std::uint64_t y,
+                                      int N, int CI, int H, int W, int CO, int KH, int KW, int OH, int OW, int SH,
+                                      int SW, int PH, int PW, int activation, float alpha, int engine,
+                                      std::uint64_t workspace, std::int64_t workspace_floats, std::uint64_t stream) {
+    MFH_TRY(require_ready());
+    const ConvGeometry g{N, CI, H, W, CO, KH, KW, OH, OW, SH, SW, PH, PW};
+    MFH_TRY(validate(g));
+    MFH_TRY(validate_activation(activation, alpha));
+    MFH_TRY(validate_engine(engine));
+    MFH_REQUIRE(x && weight && y, "conv forward received a null buffer");
+    MFH_REQUIRE(workspace_floats >= 0, "workspace size must be non-negative");
+    return conv_implicit_forward(g, as_ptr<const float>(x), as_ptr<const float>(weight), as_ptr<const float>(bias),
+                                 as_ptr<float>(y), activation, alpha, engine, as_ptr<float>(workspace),
+                                 workspace_floats, as_stream(stream));
+}
+
+MFH_API std::int64_t mfh_conv_implicit_workspace(int N, int CI, int H, int W, int CO, int KH, int KW, int OH, int OW,
+                                                 int SH, int SW, int PH, int PW, int pass) {
+    if (require_ready() != OK) return -1;
+    const ConvGeometry g{N, CI, H, W, CO, KH, KW, OH, OW, SH, SW, PH, PW};
+    if (validate(g) != OK) return -1;
+    if (pass < IMPLICIT_FORWARD || pass > IMPLICIT_DGRAD) {
+        MFH_FAIL(ERR_ARG, "pass must be 0 (forward), 1 (dW) or 2 (dX)");
+        return -1;
+    }
+    return implicit_workspace_floats(g, pass);
+}
+
+MFH_API int mfh_conv_backward_implicit(std::uint64_t x, std::uint64_t weight, std::uint64_t dy, std::uint64_t y,
+                                       std::uint64_t gated, std::uint64_t dw, std::uint64_t dx, std::uint64_t wflip,
+                                       std::uint64_t grad_cols, std::uint64_t partial, std::uint64_t db, int N, int CI,
+                                       int H, int W, int CO, int KH, int KW, int OH, int OW, int SH, int SW, int PH,
+                                       int PW, int activation, float alpha, int dw_engine, int dx_engine,
+                                       std::uint64_t workspace, std::int64_t workspace_floats, std::uint64_t stream) {
+    MFH_TRY(require_ready());
+    const ConvGeometry g{N, CI, H, W, CO, KH, KW, OH, OW, SH, SW, PH, PW};
+    MFH_TRY(validate(g));
+    MFH_TRY(validate_activation(activation, alpha));
+    MFH_TRY(validate_engine(dw_engine));
+    MFH_TRY(validate_engine(dx_engine));
+    const bool gated_dy = activation != ACT_NONE;
+    const bool unit_stride = SH == 1 && SW == 1;
+    MFH_REQUIRE(weight && dy, "conv backward needs weight and dy");
+    MFH_REQUIRE(!gated_dy || (y && gated), "a fused activation needs the forward output and the gated buffer");
+    MFH_REQUIRE((partial == 0) == (db == 0), "partial and db must be given together");
+    MFH_REQUIRE(!dw || x, "dW needs x");
+    MFH_REQUIRE(!dx || (unit_stride ? wflip != 0 : grad_cols != 0),
+                "dX needs wflip (stride 1) or grad_cols (other strides)");
+    MFH_REQUIRE(workspace_floats >= 0, "workspace size must be non-negative");
+    const hipStream_t s = as_stream(stream);
+    const float* grad = as_ptr<const float>(dy);
+    const std::int64_t count = static_cast<std::int64_t>(N) * CO * g.ohw();
+    if (gated_dy) {
+        MFH_TRY(launch_relu_backward(as_ptr<const float>(y), grad, as_ptr<float>(gated), count,
+                                     activation == ACT_LEAKY_RELU ? alpha : 0.0f, false, s));
+        grad = as_ptr<const float>(gated);
+    }
+    if (db) {
+        MFH_TRY(launch_row_sums(grad, as_ptr<double>(partial), N * CO, g.ohw(), s));
+        MFH_TRY(launch_reduce_partials(as_ptr<const double>(partial), as_ptr<float>(db), N, CO, s));
+    }
+    float* ws = as_ptr<float>(workspace);
+    if (dw)
+        MFH_TRY(conv_implicit_wgrad(g, as_ptr<const float>(x), grad, as_ptr<float>(dw), dw_engine, ws,
+                                    workspace_floats, s));
+    if (!dx) return OK;
+    if (unit_stride)
+        return conv_implicit_dgrad(g, grad, as_ptr<const float>(weight), as_ptr<float>(wflip), as_ptr<float>(dx),
+                                   dx_engine, ws, workspace_floats, s);
+    bool per_image = false;
+    MFH_TRY(column_gradient(dx_engine, g, as_ptr<const float>(weight), grad, nullptr, as_ptr<float>(grad_cols),
+                            &per_image, s));
     return launch_col2im_t(as_ptr<const float>(grad_cols), as_ptr<float>(dx), g, per_image, s);
 }
 

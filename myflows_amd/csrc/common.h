@@ -87,14 +87,30 @@ int probe_code_object();
 struct GemmTile {
     int bm, bn, bk, wm, wn;  // block tile, reduction depth per LDS stage, wave tile
 };
+// Tile catalogue of the MFMA kernels: block tile BM x BN, stage depth BK, wave tile WM x WN
+// (multiples of 32).
+inline constexpr GemmTile GEMM_TILES[] = {
+    {128, 128, 16, 64, 64},  // 0: general
+    {256, 64, 16, 64, 64},   // 1: tall outputs, N <= 64
+    {64, 128, 16, 32, 64},   // 2: short outputs, M <= 64
+    {64, 64, 16, 32, 32},    // 3: small outputs
+    {128, 32, 16, 32, 32},   // 4: N <= 32
+    {32, 128, 16, 32, 32},   // 5: M <= 32
+    {256, 128, 16, 64, 64},  // 6: large outputs, 8 waves
+    {128, 256, 16, 64, 64},  // 7: large outputs, 8 waves
+};
+constexpr int GEMM_TILE_COUNT = sizeof(GEMM_TILES) / sizeof(GEMM_TILES[0]);
+constexpr unsigned ALL_TILES = (1u << GEMM_TILE_COUNT) - 1;
+constexpr GemmTile gemm_tile_constexpr(int index) { return GEMM_TILES[index]; }
 int gemm_tile_count();
 const GemmTile& gemm_tile(int index);
 
 struct GemmPlan {
     int tile, slices, k_chunk;
 };
-// Tile and split-K choice for C(M, N) over K, or for `batch` such problems at once (never split).
-GemmPlan gemm_auto_plan(int M, int N, int K, int batch = 1);
+// Tile and split-K choice for C(M, N) over K, or for `batch` such problems at once (never split),
+// among the tiles whose bits are set in `tiles`.
+GemmPlan gemm_auto_plan(int M, int N, int K, int batch = 1, unsigned tiles = ALL_TILES);
 // Plan from an engine code: 1 = automatic, 16 + tile * 128 + (slices - 1) = explicit.
 int gemm_plan_from_engine(int engine, int M, int N, int K, GemmPlan* plan, int batch = 1);
 bool gemm_engine_valid(int engine);
@@ -153,6 +169,40 @@ int gemm_launch(int engine, hipStream_t stream, const GemmOperands& operands, co
                 float* workspace, std::int64_t workspace_floats);
 int split_reduce(const float* partial, float* c, int slices, int M, int N, int ldc, bool reference,
                  hipStream_t stream);
+// The FP64 slice-order reduction of split-K partials (slices x M x N, dense) followed by the
+// epilogue e (bias, activation, dense rows of ldc or segmented output).
+int split_reduce_epilogue(const float* partial, float* c, const GemmEpilogue& e, int M, int N, int ldc, int slices,
+                          hipStream_t stream);
+
+// ---- implicit.hip -----------------------------------------------------------------------------
+// The im2col view of an NCHW source read in place: view[k][q] = src[n, c, oh*SH - PH + kh,
+// ow*SW - PW + kw] (0 outside), feature k = (c*KH + kh)*KW + kw, pixel q = (n*OH + oh)*OW + ow.
+struct ConvGather {
+    const float* src;
+    int C, H, W;
+    int KH, KW, SH, SW, PH, PW;
+    int OH, OW;
+    int pixels;    // N * OH * OW
+    int features;  // C * KH * KW
+    int hw, chw;   // H * W, C * H * W
+    FastDiv div_ohw, div_ow, div_khkw, div_kw;
+};
+constexpr int IMPLICIT_FORWARD = 0, IMPLICIT_WGRAD = 1, IMPLICIT_DGRAD = 2;
+unsigned implicit_forward_tiles();
+// Split-K workspace floats of one pass of the implicit convolution under the automatic plan.
+std::int64_t implicit_workspace_floats(const ConvGeometry& g, int pass);
+// y = act(conv(x, w) + bias), NCHW, without an im2col buffer.
+int conv_implicit_forward(const ConvGeometry& g, const float* x, const float* w, const float* bias, float* y, int act,
+                          float alpha, int engine, float* workspace, std::int64_t workspace_floats, hipStream_t stream);
+// dW = dy . im2col(x), with dy read in place from NCHW.
+int conv_implicit_wgrad(const ConvGeometry& g, const float* x, const float* dy, float* dw, int engine,
+                        float* workspace, std::int64_t workspace_floats, hipStream_t stream);
+// dX of a stride-1 convolution as a forward convolution of dy with the flipped kernel (written to
+// wflip, CI x CO*KH*KW floats).
+int conv_implicit_dgrad(const ConvGeometry& g, const float* dy, const float* w, float* wflip, float* dx, int engine,
+                        float* workspace, std::int64_t workspace_floats, hipStream_t stream);
+// partial[r] = FP64 sum of row r (rows x length floats).
+int launch_row_sums(const float* src, double* partial, int rows, int length, hipStream_t stream);
 
 // ---- matmul.hip -------------------------------------------------------------------------------
 // variant 0 basic, 1 tiled, 2 shared, 4 register (compensated modes); see matmul.hip.

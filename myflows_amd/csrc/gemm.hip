@@ -1,30 +1,7 @@
 // FP32 GEMM engine on the CDNA4 matrix cores: C(M x N) = op(A) op(B) (+ bias) (activation),
-// row-major, with op(X) = X or X^T chosen per operand.
-//
-// Work decomposition. A workgroup computes a BM x BN tile of C with (BM/WM) x (BN/WN) wave64s; a
-// wave owns a WM x WN sub-tile made of (WM/32) x (WN/32) accumulators of v_mfma_f32_32x32x2_f32
-// (16 floats per lane each). The K range of the workgroup is consumed in BK-deep stages that are
-// double buffered in LDS: the global loads of stage t+1 are in flight while the waves run the
-// MFMAs of stage t, with one barrier per stage.
-//
-// LDS layout. Each operand tile is kept in LDS in the orientation it has in global memory, so the
-// global->LDS copy is a straight (float4 when aligned) row copy with no transpose:
-//   * "k-contiguous" operands (A when not transposed, B when transposed) live as [rows][BK + 4];
-//   * "mn-contiguous" operands (A when transposed, B when not transposed) live as [BK][rows + 4].
-// The +4 floats of padding keep 16-byte alignment and move successive rows to other banks.
-//
-// MFMA operand mapping. v_mfma_f32_32x32x2_f32 multiplies a 32x2 slice of A (lane l supplies
-// A[l % 32][l / 32]) by a 2x32 slice of B (lane l supplies B[l / 32][l % 32]) and accumulates the
-// 32x32 product; lane l holds output column l % 32, rows 8 * (r / 4) + 4 * (l / 32) + r % 4 in its
-// register r. Which k a lane half (l / 32) feeds at each step is free as long as A and B agree, so
-// half h consumes k = h * BK/2 + s for s = 0 .. BK/2 - 1: a k-contiguous operand then reads four
-// consecutive k of its row with one 16-byte LDS load. Every tile uses the same BK and the same k
-// mapping, so an unsplit product adds each output's K terms in the same order whatever the tile.
-//
-// Tile order. Workgroups are handed to the 8 XCDs round-robin by their linear id, and each XCD has
-// its own L2. The kernel renumbers the workgroups so that XCD x receives one contiguous run of
-// tiles, walked in groups of GROUP_M tile rows (column by column inside a group): the tiles an XCD
-// runs at the same time share A row panels and B column panels in its L2.
+// row-major, with op(X) = X or X^T chosen per operand. The MFMA main loop, the LDS layouts, the
+// XCD-grouped tile order and the epilogue are in gemm_core.h; this file holds the dense operand
+// loads, the split-K reduction, the tile catalogue and the planner.
 //
 // The third grid dimension has two uses:
 //   * split-K (GemmParams::split = 1): z selects the K slice [z * k_chunk, min(K, (z+1) * k_chunk))
@@ -37,127 +14,26 @@
 #include <algorithm>
 
 #include "common.h"
+#include "gemm_core.h"
 
 namespace mfh {
 namespace {
 
-typedef float v16f __attribute__((ext_vector_type(16)));
-
-// Tile catalogue: block tile BM x BN, stage depth BK, wave tile WM x WN (multiples of 32).
-constexpr GemmTile TILES[] = {
-    {128, 128, 16, 64, 64},  // 0: general
-    {256, 64, 16, 64, 64},   // 1: tall outputs, N <= 64
-    {64, 128, 16, 32, 64},   // 2: short outputs, M <= 64
-    {64, 64, 16, 32, 32},    // 3: small outputs
-    {128, 32, 16, 32, 32},   // 4: N <= 32
-    {32, 128, 16, 32, 32},   // 5: M <= 32
-    {256, 128, 16, 64, 64},  // 6: large outputs, 8 waves
-    {128, 256, 16, 64, 64},  // 7: large outputs, 8 waves
-};
-constexpr int NUM_TILES = sizeof(TILES) / sizeof(TILES[0]);
+constexpr const GemmTile* TILES = GEMM_TILES;
+constexpr int NUM_TILES = GEMM_TILE_COUNT;
 constexpr int PLAN_BASE = 16;     // engine codes >= PLAN_BASE name a tile and a slice count
 constexpr int MAX_SLICES = 128;   // slices per explicit plan code
 constexpr int MIN_CHUNK = 256;    // smallest K slice the automatic planner makes
-constexpr int GROUP_M = 8;        // tile rows per group of the tile order
-constexpr int XCDS = 8;           // accelerator complex dies of an MI355X
-
-// A ROWS x COLS tile whose COLS dimension is contiguous in global memory (row stride ld), staged
-// through registers: load() issues the global reads, store() writes them to LDS.
-template <int ROWS, int COLS, int THREADS, bool VEC>
-struct TileLoader {
-    static constexpr int ELEMS = VEC ? ROWS * COLS / 4 : ROWS * COLS;
-    static constexpr int PER_THREAD = (ELEMS + THREADS - 1) / THREADS;
-    static constexpr int VCOLS = VEC ? COLS / 4 : COLS;
-    float4 v[VEC ? PER_THREAD : 1];
-    float s[VEC ? 1 : PER_THREAD];
-
-    __device__ __forceinline__ void load(const float* __restrict__ base, int ld, int row0, int row_limit, int col0,
-                                         int col_limit, int tid) {
-#pragma unroll
-        for (int i = 0; i < PER_THREAD; ++i) {
-            const int f = tid + i * THREADS;
-            const int r = f / VCOLS, c = f % VCOLS;
-            const int row = row0 + r;
-            if constexpr (VEC) {
-                const int col = col0 + c * 4;
-                float4 value = make_float4(0.f, 0.f, 0.f, 0.f);
-                if (f < ELEMS && row < row_limit && col < col_limit)
-                    value = *reinterpret_cast<const float4*>(base + static_cast<long long>(row) * ld + col);
-                v[i] = value;
-            } else {
-                const int col = col0 + c;
-                float value = 0.f;
-                if (f < ELEMS && row < row_limit && col < col_limit) value = base[static_cast<long long>(row) * ld + col];
-                s[i] = value;
-            }
-        }
-    }
-
-    template <int LD>
-    __device__ __forceinline__ void store(float* lds, int tid) const {
-#pragma unroll
-        for (int i = 0; i < PER_THREAD; ++i) {
-            const int f = tid + i * THREADS;
-            if (f >= ELEMS) continue;
-            const int r = f / VCOLS, c = f % VCOLS;
-            if constexpr (VEC) *reinterpret_cast<float4*>(lds + r * LD + c * 4) = v[i];
-            else lds[r * LD + c] = s[i];
-        }
-    }
-};
-
-__device__ __forceinline__ float activate(float v, int act, float alpha) {
-    if (act == ACT_RELU) return v < 0.0f ? 0.0f : v;  // NaN stays NaN
-    if (act == ACT_LEAKY_RELU) return v > 0.0f ? v : alpha * v;
-    return v;
-}
-
-// Where output (row, col) of problem z lives.
-__device__ __forceinline__ long long output_offset(const GemmParams& p, int row, int col) {
-    if (p.segment) {
-        int within;
-        const int segment = p.segment_div.divmod(col, within);
-        return segment * p.segment_stride + static_cast<long long>(row) * p.ldc + within;
-    }
-    return static_cast<long long>(row) * p.ldc + col;
-}
-
-// (tile row, tile column, z) of this workgroup in the XCD-grouped order described above.
-__device__ __forceinline__ void tile_of_workgroup(int& tile_m, int& tile_n, int& z) {
-    const int gx = gridDim.x, gy = gridDim.y;
-    const int plane = gx * gy;
-    const int total = plane * gridDim.z;
-    const int linear = blockIdx.x + gx * (blockIdx.y + gy * blockIdx.z);
-    const int xcd = linear % XCDS, position = linear / XCDS;
-    const int base = total / XCDS, extra = total % XCDS;
-    const int logical = xcd * base + min(xcd, extra) + position;
-    z = logical / plane;
-    const int t = logical - z * plane;
-    const int group_span = GROUP_M * gx;
-    const int first_m = (t / group_span) * GROUP_M;
-    const int rows = min(gy - first_m, GROUP_M);
-    const int in_group = t - (t / group_span) * group_span;
-    tile_m = first_m + in_group % rows;
-    tile_n = in_group / rows;
-}
 
 template <int BM, int BN, int BK, int WM, int WN, bool TA, bool TB, bool VA, bool VB>
 __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void gemm_mfma_kernel(GemmParams p) {
-    constexpr int WGN = BN / WN, THREADS = (BM / WM) * WGN * 64;
-    constexpr int TM = WM / 32, TN = WN / 32, HALF = BK / 2;
-    static_assert(BK % 8 == 0, "each lane half consumes groups of four k");
-    // LDS row lengths (floats) of the A and B tiles in their global orientation.
-    constexpr int LDA_S = TA ? BM + 4 : BK + 4;
-    constexpr int LDB_S = TB ? BK + 4 : BN + 4;
-    constexpr int A_SIZE = TA ? BK * LDA_S : BM * LDA_S;
-    constexpr int B_SIZE = TB ? BN * LDB_S : BK * LDB_S;
-    __shared__ __attribute__((aligned(16))) float smem[2 * (A_SIZE + B_SIZE)];
+    using S = MfmaShape<BM, BN, BK, WM, WN, TA, TB>;
+    __shared__ __attribute__((aligned(16))) float smem[2 * S::STAGE];
 
     int tile_m, tile_n, z;
     tile_of_workgroup(tile_m, tile_n, z);
     const int tid = threadIdx.x, wave = tid / 64, lane = tid % 64;
-    const int lm = lane % 32, h = lane / 32;
-    const int wm0 = (wave / WGN) * WM, wn0 = (wave % WGN) * WN;
+    const int wm0 = (wave / S::WGN) * WM, wn0 = (wave % S::WGN) * WN;
     const int m0 = tile_m * BM, n0 = tile_n * BN;
     const float* __restrict__ A = p.A + (p.split ? 0 : z * p.a_batch);
     const float* __restrict__ B = p.B + (p.split ? 0 : z * p.b_batch);
@@ -167,93 +43,23 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void gemm_mfma_kernel(G
     const int M = p.M, N = p.N;
 
     // A tile: rows = m (k-contiguous) or k (mn-contiguous); likewise B.
-    TileLoader<TA ? BK : BM, TA ? BM : BK, THREADS, VA> la;
-    TileLoader<TB ? BN : BK, TB ? BK : BN, THREADS, VB> lb;
+    TileLoader<TA ? BK : BM, TA ? BM : BK, S::THREADS, VA> la;
+    TileLoader<TB ? BN : BK, TB ? BK : BN, S::THREADS, VB> lb;
     auto fetch = [&](int kt) {
         if constexpr (TA) la.load(A, p.lda, kt, k_end, m0, M, tid);
         else la.load(A, p.lda, m0, M, kt, k_end, tid);
         if constexpr (TB) lb.load(B, p.ldb, n0, N, kt, k_end, tid);
         else lb.load(B, p.ldb, kt, k_end, n0, N, tid);
     };
-    auto stage = [&](int buf) {
-        la.template store<LDA_S>(smem + buf * (A_SIZE + B_SIZE), tid);
-        lb.template store<LDB_S>(smem + buf * (A_SIZE + B_SIZE) + A_SIZE, tid);
+    auto store = [&](float* a_lds, float* b_lds) {
+        la.template store<S::LDA_S>(a_lds, tid);
+        lb.template store<S::LDB_S>(b_lds, tid);
     };
 
-    v16f acc[TM][TN];
-#pragma unroll
-    for (int i = 0; i < TM; ++i)
-#pragma unroll
-        for (int j = 0; j < TN; ++j)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
-
-    const int stages = k_end > k_begin ? (k_end - k_begin + BK - 1) / BK : 0;
-    if (stages > 0) {
-        fetch(k_begin);
-        stage(0);
-    }
-    __syncthreads();
-    for (int t = 0; t < stages; ++t) {
-        const bool more = t + 1 < stages;
-        if (more) fetch(k_begin + (t + 1) * BK);
-        const float* As = smem + (t & 1) * (A_SIZE + B_SIZE);
-        const float* Bs = As + A_SIZE;
-#pragma unroll
-        for (int kk = 0; kk < HALF; kk += 4) {
-            const int k = h * HALF + kk;
-            float4 a[TM], b[TN];
-#pragma unroll
-            for (int i = 0; i < TM; ++i) {
-                const int m = wm0 + i * 32 + lm;
-                if constexpr (TA)
-                    a[i] = make_float4(As[k * LDA_S + m], As[(k + 1) * LDA_S + m], As[(k + 2) * LDA_S + m],
-                                       As[(k + 3) * LDA_S + m]);
-                else a[i] = *reinterpret_cast<const float4*>(As + m * LDA_S + k);
-            }
-#pragma unroll
-            for (int j = 0; j < TN; ++j) {
-                const int n = wn0 + j * 32 + lm;
-                if constexpr (TB) b[j] = *reinterpret_cast<const float4*>(Bs + n * LDB_S + k);
-                else
-                    b[j] = make_float4(Bs[k * LDB_S + n], Bs[(k + 1) * LDB_S + n], Bs[(k + 2) * LDB_S + n],
-                                       Bs[(k + 3) * LDB_S + n]);
-            }
-#pragma unroll
-            for (int i = 0; i < TM; ++i)
-#pragma unroll
-                for (int j = 0; j < TN; ++j) {
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[i].x, b[j].x, acc[i][j], 0, 0, 0);
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[i].y, b[j].y, acc[i][j], 0, 0, 0);
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[i].z, b[j].z, acc[i][j], 0, 0, 0);
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[i].w, b[j].w, acc[i][j], 0, 0, 0);
-                }
-        }
-        if (more) stage((t + 1) & 1);
-        __syncthreads();
-    }
-
-    // Epilogue: bias (per output column or per output row), the activation, then the store.
-    const float* __restrict__ bias = p.bias;
-#pragma unroll
-    for (int j = 0; j < TN; ++j) {
-        const int col = n0 + wn0 + j * 32 + lm;
-        if (col >= N) continue;
-        const float col_bias = p.bias_mode == BIAS_COLUMN ? bias[col] : 0.f;
-        const long long col_offset = output_offset(p, 0, col);
-#pragma unroll
-        for (int i = 0; i < TM; ++i)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const int row = m0 + wm0 + i * 32 + 8 * (r / 4) + 4 * h + r % 4;
-                if (row < M) {
-                    float v = acc[i][j][r];
-                    if (p.bias_mode == BIAS_COLUMN) v += col_bias;
-                    else if (p.bias_mode == BIAS_ROW) v += bias[row];
-                    C[col_offset + static_cast<long long>(row) * p.ldc] = activate(v, p.act, p.alpha);
-                }
-            }
-    }
+    v16f acc[S::TM][S::TN];
+    zero_acc<S>(acc);
+    mfma_k_loop<S>(smem, k_begin, k_end, fetch, store, acc, wm0, wn0, lane);
+    store_acc<S>(p, C, acc, m0, n0, wm0, wn0, lane);
 }
 
 // C = act((float)(((0.0 + p0) + p1) + ... + p[S-1]) [+ bias]) with the FP64 sum in slice order,
@@ -410,10 +216,11 @@ const GemmTile& gemm_tile(int index) { return TILES[index]; }
 // The plan of least estimated cost over every tile and (for a single problem) every split of K
 // into slices of at least MIN_CHUNK: large outputs take large tiles; small outputs trade tile size
 // and K slices for enough workgroups to fill the GPU.
-GemmPlan gemm_auto_plan(int M, int N, int K, int batch) {
+GemmPlan gemm_auto_plan(int M, int N, int K, int batch, unsigned tiles) {
     GemmPlan best{0, 1, K};
     double best_cost = -1.0;
     for (int tile = 0; tile < NUM_TILES; ++tile) {
+        if (!(tiles & (1u << tile))) continue;
         const GemmTile& t = TILES[tile];
         const std::int64_t tiles = static_cast<std::int64_t>(blocks_for(M, t.bm)) * blocks_for(N, t.bn) * batch;
         if (blocks_for(M, t.bm) > GRID_YZ_LIMIT) continue;
@@ -489,6 +296,11 @@ int launch_split_reduce(const float* partial, float* c, const GemmParams& p, int
 int split_reduce(const float* partial, float* c, int slices, int M, int N, int ldc, bool /*reference*/,
                  hipStream_t stream) {
     return launch_split_reduce(partial, c, epilogue_params(GemmEpilogue{}, M, N, ldc), slices, stream);
+}
+
+int split_reduce_epilogue(const float* partial, float* c, const GemmEpilogue& e, int M, int N, int ldc, int slices,
+                          hipStream_t stream) {
+    return launch_split_reduce(partial, c, epilogue_params(e, M, N, ldc), slices, stream);
 }
 
 int gemm_launch(int engine, hipStream_t stream, const GemmOperands& o, const GemmEpilogue& e, float* workspace,

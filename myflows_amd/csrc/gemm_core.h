@@ -1,0 +1,227 @@
+// The MFMA main loop and epilogue shared by the dense GEMM engine (gemm.hip) and the implicit-GEMM
+// convolution kernels (implicit.hip). Only the way a stage's operand tiles are read from global
+// memory differs between them: a dense row copy, or a gather from an NCHW tensor.
+//
+// Work decomposition. A workgroup computes a BM x BN tile of C with (BM/WM) x (BN/WN) wave64s; a
+// wave owns a WM x WN sub-tile made of (WM/32) x (WN/32) accumulators of v_mfma_f32_32x32x2_f32
+// (16 floats per lane each). The K range of the workgroup is consumed in BK-deep stages that are
+// double buffered in LDS: the global loads of stage t+1 are in flight while the waves run the
+// MFMAs of stage t, with one barrier per stage.
+//
+// LDS layout. Each operand tile is kept in LDS in the orientation it has in global memory, so the
+// global->LDS copy is a straight row copy with no transpose:
+//   * "k-contiguous" operands (A when TA is false, B when TB is true) live as [rows][BK + 4];
+//   * "mn-contiguous" operands (A when TA is true, B when TB is false) live as [BK][rows + 4].
+// The +4 floats of padding keep 16-byte alignment and move successive rows to other banks.
+//
+// MFMA operand mapping. v_mfma_f32_32x32x2_f32 multiplies a 32x2 slice of A (lane l supplies
+// A[l % 32][l / 32]) by a 2x32 slice of B (lane l supplies B[l / 32][l % 32]) and accumulates the
+// 32x32 product; lane l holds output column l % 32, rows 8 * (r / 4) + 4 * (l / 32) + r % 4 in its
+// register r. Which k a lane half (l / 32) feeds at each step is free as long as A and B agree, so
+// half h consumes k = h * BK/2 + s for s = 0 .. BK/2 - 1: a k-contiguous operand then reads four
+// consecutive k of its row with one 16-byte LDS load. Every tile uses the same BK and the same k
+// mapping, so an unsplit product adds each output's K terms in the same order whatever the tile.
+#pragma once
+
+#include "common.h"
+
+namespace mfh {
+
+typedef float v16f __attribute__((ext_vector_type(16)));
+
+constexpr int GROUP_M = 8;  // tile rows per group of the tile order
+constexpr int XCDS = 8;     // accelerator complex dies of an MI355X
+
+template <int BM_, int BN_, int BK_, int WM_, int WN_, bool TA_, bool TB_>
+struct MfmaShape {
+    static constexpr int BM = BM_, BN = BN_, BK = BK_, WM = WM_, WN = WN_;
+    static constexpr bool TA = TA_, TB = TB_;
+    static constexpr int WGN = BN / WN, WAVES = (BM / WM) * WGN, THREADS = WAVES * 64;
+    static constexpr int TM = WM / 32, TN = WN / 32, HALF = BK / 2;
+    static constexpr int LDA_S = TA ? BM + 4 : BK + 4;  // LDS row lengths (floats)
+    static constexpr int LDB_S = TB ? BK + 4 : BN + 4;
+    static constexpr int A_SIZE = TA ? BK * LDA_S : BM * LDA_S;
+    static constexpr int B_SIZE = TB ? BN * LDB_S : BK * LDB_S;
+    static constexpr int STAGE = A_SIZE + B_SIZE;
+    static_assert(BK % 8 == 0, "each lane half consumes groups of four k");
+};
+
+// A ROWS x COLS tile whose COLS dimension is contiguous in global memory (row stride ld), staged
+// through registers: load() issues the global reads, store() writes them to LDS.
+template <int ROWS, int COLS, int THREADS, bool VEC>
+struct TileLoader {
+    static constexpr int ELEMS = VEC ? ROWS * COLS / 4 : ROWS * COLS;
+    static constexpr int PER_THREAD = (ELEMS + THREADS - 1) / THREADS;
+    static constexpr int VCOLS = VEC ? COLS / 4 : COLS;
+    float4 v[VEC ? PER_THREAD : 1];
+    float s[VEC ? 1 : PER_THREAD];
+
+    __device__ __forceinline__ void load(const float* __restrict__ base, int ld, int row0, int row_limit, int col0,
+                                         int col_limit, int tid) {
+#pragma unroll
+        for (int i = 0; i < PER_THREAD; ++i) {
+            const int f = tid + i * THREADS;
+            const int r = f / VCOLS, c = f % VCOLS;
+            const int row = row0 + r;
+            if constexpr (VEC) {
+                const int col = col0 + c * 4;
+                float4 value = make_float4(0.f, 0.f, 0.f, 0.f);
+                if (f < ELEMS && row < row_limit && col < col_limit)
+                    value = *reinterpret_cast<const float4*>(base + static_cast<long long>(row) * ld + col);
+                v[i] = value;
+            } else {
+                const int col = col0 + c;
+                float value = 0.f;
+                if (f < ELEMS && row < row_limit && col < col_limit) value = base[static_cast<long long>(row) * ld + col];
+                s[i] = value;
+            }
+        }
+    }
+
+    template <int LD>
+    __device__ __forceinline__ void store(float* lds, int tid) const {
+#pragma unroll
+        for (int i = 0; i < PER_THREAD; ++i) {
+            const int f = tid + i * THREADS;
+            if (f >= ELEMS) continue;
+            const int r = f / VCOLS, c = f % VCOLS;
+            if constexpr (VEC) *reinterpret_cast<float4*>(lds + r * LD + c * 4) = v[i];
+            else lds[r * LD + c] = s[i];
+        }
+    }
+};
+
+__device__ __forceinline__ float activate(float v, int act, float alpha) {
+    if (act == ACT_RELU) return v < 0.0f ? 0.0f : v;  // NaN stays NaN
+    if (act == ACT_LEAKY_RELU) return v > 0.0f ? v : alpha * v;
+    return v;
+}
+
+// Where output (row, col) lives: dense row * ldc + col, or segmented (column j is element j % segment
+// of segment j / segment, segments segment_stride apart).
+__device__ __forceinline__ long long output_offset(const GemmParams& p, int row, int col) {
+    if (p.segment) {
+        int within;
+        const int segment = p.segment_div.divmod(col, within);
+        return segment * p.segment_stride + static_cast<long long>(row) * p.ldc + within;
+    }
+    return static_cast<long long>(row) * p.ldc + col;
+}
+
+// (tile row, tile column, z) of this workgroup. Workgroups are handed to the 8 XCDs round-robin by
+// their linear id, and each XCD has its own L2: the renumbering gives XCD x one contiguous run of
+// tiles, walked in groups of GROUP_M tile rows (column by column inside a group), so the tiles an
+// XCD runs at the same time share A row panels and B column panels in its L2.
+__device__ __forceinline__ void tile_of_workgroup(int& tile_m, int& tile_n, int& z) {
+    const int gx = gridDim.x, gy = gridDim.y;
+    const int plane = gx * gy;
+    const int total = plane * gridDim.z;
+    const int linear = blockIdx.x + gx * (blockIdx.y + gy * blockIdx.z);
+    const int xcd = linear % XCDS, position = linear / XCDS;
+    const int base = total / XCDS, extra = total % XCDS;
+    const int logical = xcd * base + min(xcd, extra) + position;
+    z = logical / plane;
+    const int t = logical - z * plane;
+    const int group_span = GROUP_M * gx;
+    const int first_m = (t / group_span) * GROUP_M;
+    const int rows = min(gy - first_m, GROUP_M);
+    const int in_group = t - (t / group_span) * group_span;
+    tile_m = first_m + in_group % rows;
+    tile_n = in_group / rows;
+}
+
+template <class S>
+__device__ __forceinline__ void zero_acc(v16f (&acc)[S::TM][S::TN]) {
+#pragma unroll
+    for (int i = 0; i < S::TM; ++i)
+#pragma unroll
+        for (int j = 0; j < S::TN; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+}
+
+// The K loop over [k_begin, k_end) in BK stages. fetch(kt) issues the global reads of the stage
+// starting at kt; store(a_lds, b_lds) writes the fetched registers into one LDS stage buffer.
+template <class S, class Fetch, class Store>
+__device__ __forceinline__ void mfma_k_loop(float* smem, int k_begin, int k_end, Fetch&& fetch, Store&& store,
+                                            v16f (&acc)[S::TM][S::TN], int wm0, int wn0, int lane) {
+    constexpr int BK = S::BK, HALF = S::HALF, LDA_S = S::LDA_S, LDB_S = S::LDB_S;
+    const int lm = lane % 32, h = lane / 32;
+    const int stages = k_end > k_begin ? (k_end - k_begin + BK - 1) / BK : 0;
+    if (stages > 0) {
+        fetch(k_begin);
+        store(smem, smem + S::A_SIZE);
+    }
+    __syncthreads();
+    for (int t = 0; t < stages; ++t) {
+        const bool more = t + 1 < stages;
+        if (more) fetch(k_begin + (t + 1) * BK);
+        const float* As = smem + (t & 1) * S::STAGE;
+        const float* Bs = As + S::A_SIZE;
+#pragma unroll
+        for (int kk = 0; kk < HALF; kk += 4) {
+            const int k = h * HALF + kk;
+            float4 a[S::TM], b[S::TN];
+#pragma unroll
+            for (int i = 0; i < S::TM; ++i) {
+                const int m = wm0 + i * 32 + lm;
+                if constexpr (S::TA)
+                    a[i] = make_float4(As[k * LDA_S + m], As[(k + 1) * LDA_S + m], As[(k + 2) * LDA_S + m],
+                                       As[(k + 3) * LDA_S + m]);
+                else a[i] = *reinterpret_cast<const float4*>(As + m * LDA_S + k);
+            }
+#pragma unroll
+            for (int j = 0; j < S::TN; ++j) {
+                const int n = wn0 + j * 32 + lm;
+                if constexpr (S::TB) b[j] = *reinterpret_cast<const float4*>(Bs + n * LDB_S + k);
+                else
+                    b[j] = make_float4(Bs[k * LDB_S + n], Bs[(k + 1) * LDB_S + n], Bs[(k + 2) * LDB_S + n],
+                                       Bs[(k + 3) * LDB_S + n]);
+            }
+#pragma unroll
+            for (int i = 0; i < S::TM; ++i)
+#pragma unroll
+                for (int j = 0; j < S::TN; ++j) {
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[i].x, b[j].x, acc[i][j], 0, 0, 0);
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[i].y, b[j].y, acc[i][j], 0, 0, 0);
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[i].z, b[j].z, acc[i][j], 0, 0, 0);
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[i].w, b[j].w, acc[i][j], 0, 0, 0);
+                }
+        }
+        if (more) {
+            float* next = smem + ((t + 1) & 1) * S::STAGE;
+            store(next, next + S::A_SIZE);
+        }
+        __syncthreads();
+    }
+}
+
+// Epilogue: bias (per output column or per output row), the activation, then the store of the
+// wave's accumulators into C (dense or segmented, see output_offset).
+template <class S>
+__device__ __forceinline__ void store_acc(const GemmParams& p, float* __restrict__ C, const v16f (&acc)[S::TM][S::TN],
+                                          int m0, int n0, int wm0, int wn0, int lane) {
+    const int lm = lane % 32, h = lane / 32;
+    const float* __restrict__ bias = p.bias;
+#pragma unroll
+    for (int j = 0; j < S::TN; ++j) {
+        const int col = n0 + wn0 + j * 32 + lm;
+        if (col >= p.N) continue;
+        const float col_bias = p.bias_mode == BIAS_COLUMN ? bias[col] : 0.f;
+        const long long col_offset = output_offset(p, 0, col);
+#pragma unroll
+        for (int i = 0; i < S::TM; ++i)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int row = m0 + wm0 + i * 32 + 8 * (r / 4) + 4 * h + r % 4;
+                if (row < p.M) {
+                    float v = acc[i][j][r];
+                    if (p.bias_mode == BIAS_COLUMN) v += col_bias;
+                    else if (p.bias_mode == BIAS_ROW) v += bias[row];
+                    C[col_offset + static_cast<long long>(row) * p.ldc] = activate(v, p.act, p.alpha);
+                }
+            }
+    }
+}
+
+}  // namespace mfh

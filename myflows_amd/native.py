@@ -39,6 +39,10 @@ ACTIVATION_CODES = {None: 0, "relu": 1, "leaky_relu": 2}
 PLAN_BASE, PLAN_SLICES = 16, 128       # explicit plan code = PLAN_BASE + tile * PLAN_SLICES + slices - 1
 CONV_GRAD_TILE = 64                    # pixels per tile of the transposed-gradient kernel
 ROWS_PATH_MAX_PIXELS = 0               # conv forward through a rows GEMM + epilogue below this OH*OW
+# How convolutions form their GEMM operand: "implicit" gathers the im2col view inside the GEMM's
+# loads (no cols buffer); "im2col" writes cols (N*OH*OW x CI*KH*KW) first and keeps it for dW.
+CONV_ALGORITHMS = ("implicit", "im2col")
+IMPLICIT_PASSES = {"forward": 0, "dw": 1, "dx": 2}
 _STATUS_TEXT = {1: "initialization failed", 2: "invalid argument", 3: "HIP runtime error", 5: "wrong HIP device"}
 
 
@@ -68,6 +72,9 @@ _SIGNATURES = {
     "mfh_conv_im2col": ("i", "pp" + _CONV + "p"),
     "mfh_conv_forward": ("i", "pppppp" + _CONV + "ifipqp"),
     "mfh_conv_backward": ("i", "pppppppppp" + _CONV + "iifiipqp"),
+    "mfh_conv_forward_implicit": ("i", "pppp" + _CONV + "ifipqp"),
+    "mfh_conv_implicit_workspace": ("q", _CONV + "i"),
+    "mfh_conv_backward_implicit": ("i", "ppppppppppp" + _CONV + "ifiipqp"),
     "mfh_pool_forward": ("i", "ppp" + "i" * 10 + "p"),
     "mfh_pool_backward": ("i", "ppp" + "i" * 10 + "p"),
     "mfh_matmul": ("i", "iiipppp" + "iii" + "p"),
@@ -343,11 +350,41 @@ def conv2d_im2col(x, kernel_shape, *, stride=(1, 1), padding=(0, 0)):
     return cols
 
 
+def default_conv_algorithm():
+    """The convolution algorithm of calls that do not name one: MFHIP_CONV_ALGO, else "implicit"."""
+    return _conv_algorithm(os.environ.get("MFHIP_CONV_ALGO", "implicit"))
+
+
+def _conv_algorithm(algorithm):
+    if algorithm is None:
+        return default_conv_algorithm()
+    if algorithm not in CONV_ALGORITHMS:
+        raise ValueError(f"algorithm must be one of {CONV_ALGORITHMS}, not {algorithm!r}")
+    return algorithm
+
+
+@lru_cache(maxsize=1024)
+def _implicit_workspace_floats(g, pass_name):
+    floats = _library().mfh_conv_implicit_workspace(*g.c_args(), IMPLICIT_PASSES[pass_name])
+    if floats < 0:
+        _raise_for(2, _library())
+    return floats
+
+
+def _implicit_workspace(g, *passes):
+    floats = max((_implicit_workspace_floats(g, p) for p in passes), default=0)
+    if not floats:
+        return None, 0
+    return torch.empty(floats, dtype=torch.float32, device="cuda"), floats
+
+
 def conv2d_forward(x, weight, bias=None, *, stride=(1, 1), padding=(0, 0), activation=None, alpha=0.0,
-                   engine="mfma"):
+                   engine="mfma", algorithm=None):
     """(y, cols): the contiguous NCHW output with bias and activation applied, and the im2col
-    columns of x that conv2d_backward needs for dW."""
+    columns of x that conv2d_backward needs for dW. With algorithm "implicit" (the default) the GEMM
+    gathers the columns from x itself and cols is None; "im2col" writes and returns them."""
     engine = _engine_code(engine)
+    algorithm = _conv_algorithm(algorithm)
     x, weight = _device_f32(x, "x"), _device_f32(weight, "weight")
     if bias is not None:
         bias = _device_f32(bias, "bias")
@@ -356,8 +393,13 @@ def conv2d_forward(x, weight, bias=None, *, stride=(1, 1), padding=(0, 0), activ
     g = ConvGeometry.of(tuple(x.shape), tuple(weight.shape), stride, padding)
     act, alpha = _activation_code(activation, alpha)
     device = x.device
-    cols = torch.empty((g.m, g.k), dtype=torch.float32, device=device)
     y = torch.empty(g.out_shape, dtype=torch.float32, device=device)
+    if algorithm == "implicit":
+        workspace, floats = _implicit_workspace(g, "forward")
+        _call("mfh_conv_forward_implicit", x.data_ptr(), weight.data_ptr(), _addr(bias), y.data_ptr(), *g.c_args(),
+              act, alpha, engine, _addr(workspace), floats, _stream())
+        return y, None
+    cols = torch.empty((g.m, g.k), dtype=torch.float32, device=device)
     rows = None
     if g.ohw < ROWS_PATH_MAX_PIXELS:  # rows = cols W^T, then the NCHW epilogue kernel
         rows = torch.empty((g.m, g.co), dtype=torch.float32, device=device)
@@ -372,15 +414,23 @@ def conv2d_forward(x, weight, bias=None, *, stride=(1, 1), padding=(0, 0), activ
 
 def conv2d_backward(x, weight, grad_y, cols, *, stride=(1, 1), padding=(0, 0), need_bias_grad=True,
                     need_input_grad=True, need_weight_grad=True, activation=None, alpha=0.0, output=None,
-                    engine="mfma", recompute_cols=False):
-    """(dx, dw, db), None for each gradient not requested. Only dW reads the forward's cols
-    (recomputed from x when recompute_cols); a fused activation gates grad_y through output."""
+                    engine="mfma", recompute_cols=False, algorithm=None):
+    """(dx, dw, db), None for each gradient not requested; a fused activation gates grad_y through
+    output. algorithm "im2col" computes dW from the forward's cols (recomputed from x when
+    recompute_cols); "implicit" gathers them from x inside the GEMM. Without an algorithm, a call
+    that passes cols (and does not recompute them) takes "im2col", any other the default."""
     engine = _engine_code(engine)
+    if algorithm is None and cols is not None and not recompute_cols:
+        algorithm = "im2col"
+    algorithm = _conv_algorithm(algorithm)
     x, weight, grad_y = _device_f32(x, "x"), _device_f32(weight, "weight"), _device_f32(grad_y, "grad_y")
     g = ConvGeometry.of(tuple(x.shape), tuple(weight.shape), stride, padding)
     act, alpha = _activation_code(activation, alpha)
     if tuple(grad_y.shape) != g.out_shape:
         raise ValueError("grad_y does not have the convolution's output shape")
+    if algorithm == "implicit":
+        return _conv2d_backward_implicit(x, weight, grad_y, g, need_bias_grad, need_input_grad, need_weight_grad,
+                                         act, alpha, output, engine)
     if need_weight_grad:
         cols = (conv2d_im2col(x, tuple(weight.shape), stride=stride, padding=padding) if recompute_cols
                 else _device_f32(cols, "cols"))
@@ -411,6 +461,35 @@ def conv2d_backward(x, weight, grad_y, cols, *, stride=(1, 1), padding=(0, 0), n
     _call("mfh_conv_backward", weight.data_ptr(), grad_y.data_ptr(), _addr(gate), _addr(cols), _addr(dy_rows),
           _addr(dw), _addr(grad_cols), _addr(dx), _addr(partial), _addr(db), *g.c_args(), tiles, act, alpha,
           dw_engine, engine, _addr(workspace), floats, _stream())
+    return dx, dw, db
+
+
+def _conv2d_backward_implicit(x, weight, grad_y, g, need_bias_grad, need_input_grad, need_weight_grad, act, alpha,
+                              output, engine):
+    gate = None
+    if act:
+        if output is None:
+            raise ValueError("a fused activation needs the forward output")
+        gate = _device_f32(output, "output")
+        if gate.shape != grad_y.shape:
+            raise ValueError("output does not have grad_y's shape")
+    if not (need_input_grad or need_weight_grad or need_bias_grad):
+        return None, None, None
+    device = x.device
+    empty = lambda *shape, dtype=torch.float32: torch.empty(shape, dtype=dtype, device=device)
+    unit_stride = g.sh == 1 and g.sw == 1
+    gated = torch.empty_like(grad_y) if act else None
+    dw = torch.empty_like(weight) if need_weight_grad else None
+    dx = torch.empty_like(x) if need_input_grad else None
+    wflip = empty(g.ci * g.co * g.kh * g.kw) if need_input_grad and unit_stride else None
+    grad_cols = empty(g.m * g.k) if need_input_grad and not unit_stride else None
+    partial = empty(g.n * g.co, dtype=torch.float64) if need_bias_grad else None
+    db = empty(g.co) if need_bias_grad else None
+    passes = (("dw",) if need_weight_grad else ()) + (("dx",) if need_input_grad and unit_stride else ())
+    workspace, floats = _implicit_workspace(g, *passes)
+    _call("mfh_conv_backward_implicit", x.data_ptr(), weight.data_ptr(), grad_y.data_ptr(), _addr(gate),
+          _addr(gated), _addr(dw), _addr(dx), _addr(wflip), _addr(grad_cols), _addr(partial), _addr(db),
+          *g.c_args(), act, alpha, engine, engine, _addr(workspace), floats, _stream())
     return dx, dw, db
 
 

@@ -1,11 +1,16 @@
-"""Convolution parity on the GPU, through the operator API and the native.py boundary.
+"""Convolution parity on the GPU, through the operator API and the native.py boundary, for both
+convolution algorithms: "implicit" (the GEMM gathers the im2col view from x; dX of stride-1
+convolutions is a convolution of dy with the flipped kernel) and "im2col" (cols written first).
 
 Bit-exact: the im2col matrix, and col2im (integer-valued dy and W make every GEMM product and
 window sum exact in float32, so any index or window error shows as a bit difference) on each dX
-path (from NCHW dy, from the transposed gated dy). Tolerance: outputs and gradients within 1e-5 of
-max|ref| of the FP64 loops of the reference's tests (normwise, the reference's own criterion), db
-within one float32 ulp of the FP64 sum.
+path (from NCHW dy, from the transposed gated dy), and the implicit path on the same integer data.
+Tolerance: outputs and gradients within 1e-5 of max|ref| of the FP64 loops of the reference's tests
+(normwise, the reference's own criterion), db within one float32 ulp of the FP64 sum.
 """
+
+import contextlib
+import os
 
 import numpy as np
 import pytest
@@ -28,8 +33,40 @@ def host(t):
     return t.detach().cpu().numpy()
 
 
-def run_operator(case, op_class=mf.Conv2D_Op, input_grad=True, **options):
+ALGORITHMS = native.CONV_ALGORITHMS
+# ResNet18's convolution shapes at batch 2 (stem, layer1, a stride-2 3x3, a 1x1 downsample, layer4),
+# plus a padding wider than the kernel, which makes the flipped dX convolution's padding negative.
+RESNET_CASES = (
+    ("stem", (2, 3, 48, 64), (64, 3, 7, 7), (2, 2), (3, 3)),
+    ("l1", (2, 64, 29, 39), (64, 64, 3, 3), (1, 1), (1, 1)),
+    ("l2down3x3", (2, 64, 29, 39), (128, 64, 3, 3), (2, 2), (1, 1)),
+    ("l2ds1x1", (2, 64, 29, 39), (128, 64, 1, 1), (2, 2), (0, 0)),
+    ("l4", (2, 512, 4, 5), (512, 512, 3, 3), (1, 1), (1, 1)),
+    ("widepad", (1, 2, 5, 6), (3, 2, 1, 2), (1, 1), (1, 2)),
+)
+
+
+@contextlib.contextmanager
+def conv_algorithm(name):
+    """Make `name` the default convolution algorithm (MFHIP_CONV_ALGO) inside the block."""
+    previous = os.environ.get("MFHIP_CONV_ALGO")
+    os.environ["MFHIP_CONV_ALGO"] = name
+    try:
+        yield
+    finally:
+        if previous is None:
+            os.environ.pop("MFHIP_CONV_ALGO", None)
+        else:
+            os.environ["MFHIP_CONV_ALGO"] = previous
+
+
+def run_operator(case, op_class=mf.Conv2D_Op, input_grad=True, algorithm="implicit", **options):
     """Forward + backward of one convolution operator; returns (op, y, [dx, dw, db])."""
+    with conv_algorithm(algorithm):
+        return _run_operator(case, op_class, input_grad, **options)
+
+
+def _run_operator(case, op_class, input_grad, **options):
     x, w, b, dy = (gpu(a) for a in conv_fixture(case))
     leaves = [mf.Variable(x, requires_grad=input_grad), mf.Variable(w, trainable=True), mf.Variable(b, trainable=True)]
     op = op_class(leaves[0], leaves[1], stride=case[3], padding=case[4], bias=leaves[2], backend="hip_native",
@@ -45,13 +82,15 @@ def fp64_case(case):
     return x, w, b, dy, naive.conv_forward(x, w, case[3], case[4]) + b[None, :, None, None]
 
 
-@pytest.mark.parametrize("case", CONV_CASES + PERFORMANCE_CASES, ids=lambda c: c[0])
-def test_forward_and_gradients_match_fp64_loops(case):
+@pytest.mark.parametrize("algorithm", ALGORITHMS)
+@pytest.mark.parametrize("case", CONV_CASES + PERFORMANCE_CASES + RESNET_CASES, ids=lambda c: c[0])
+def test_forward_and_gradients_match_fp64_loops(case, algorithm):
     """The forward is one GEMM over all images stored into NCHW (split over K when the planner asks);
-    dX goes through the transposed rows, dW through a split-K GEMM."""
-    print("conv case", case[0], flush=True)
+    dW is a split-K GEMM; dX is the flipped-kernel convolution (implicit, stride 1) or a column
+    gradient GEMM and col2im."""
+    print("conv case", case[0], algorithm, flush=True)
     x, w, _, dy, pre = fp64_case(case)
-    op, y, (dx, dw, db) = run_operator(case)
+    op, y, (dx, dw, db) = run_operator(case, algorithm=algorithm)
     assert op.value.is_contiguous()
     ref_dx, ref_dw = naive.conv_backward(x, w, dy, case[3], case[4])
     assert_near(y, pre, 1e-5, "y")
@@ -69,14 +108,15 @@ def test_known_answer_t0_is_exact():
     np.testing.assert_array_equal(y[0, 0], windows)
 
 
+@pytest.mark.parametrize("algorithm", ALGORITHMS)
 @pytest.mark.parametrize("case", (CONV_CASES[1], CONV_CASES[3], PERFORMANCE_CASES[2]), ids=lambda c: c[0])
 @pytest.mark.parametrize("variant", ("relu", "leaky"))
-def test_fused_activation_forward_and_gated_backward(case, variant):
-    print("fused", variant, case[0], flush=True)
+def test_fused_activation_forward_and_gated_backward(case, variant, algorithm):
+    print("fused", variant, case[0], algorithm, flush=True)
     x, w, _, dy, pre = fp64_case(case)
     op_class, options, slope = ((mf.Conv2D_ReLU_Op, {}, 0.0) if variant == "relu"
                                 else (mf.Conv2D_LeakyReLU_Op, {"alpha": 0.2}, 0.2))
-    op, y, (dx, dw, db) = run_operator(case, op_class, **options)
+    op, y, (dx, dw, db) = run_operator(case, op_class, algorithm=algorithm, **options)
     assert op._activation_fused
     gate = np.where(pre > 0, 1.0, slope)
     ref_dx, ref_dw = naive.conv_backward(x, w, dy * gate, case[3], case[4])
@@ -86,45 +126,74 @@ def test_fused_activation_forward_and_gated_backward(case, variant):
     assert_near(db, (dy * gate).sum(axis=(0, 2, 3)), 4 * EPS32, "db")
 
 
-def test_frozen_input_skips_dx_and_keeps_weight_gradients_bitwise():
+@pytest.mark.parametrize("algorithm", ALGORITHMS)
+def test_frozen_input_skips_dx_and_keeps_weight_gradients_bitwise(algorithm):
     case = PERFORMANCE_CASES[0]
-    _, _, (_, dw_all, db_all) = run_operator(case)
-    _, _, (dx, dw, db) = run_operator(case, input_grad=False)
+    _, _, (_, dw_all, db_all) = run_operator(case, algorithm=algorithm)
+    _, _, (dx, dw, db) = run_operator(case, input_grad=False, algorithm=algorithm)
     assert dx is None
     np.testing.assert_array_equal(dw, dw_all)
     np.testing.assert_array_equal(db, db_all)
 
 
-def test_dx_only_through_fused_relu():
-    """Frozen weight and bias: only dX, gated by the fused ReLU's output (the transposed-dy path)."""
-    case = PERFORMANCE_CASES[2]
+@pytest.mark.parametrize("algorithm", ALGORITHMS)
+@pytest.mark.parametrize("case", (PERFORMANCE_CASES[2], RESNET_CASES[1]), ids=lambda c: c[0])
+def test_dx_only_through_fused_relu(case, algorithm):
+    """Frozen weight and bias: only dX, gated by the fused ReLU's output."""
     x, w, b, dy = conv_fixture(case)
     xv = mf.Variable(gpu(x))
     wv, bv = mf.Variable(gpu(w), requires_grad=False), mf.Variable(gpu(b), requires_grad=False)
-    op = mf.Conv2D_ReLU_Op(xv, wv, stride=case[3], padding=case[4], bias=bv, backend="hip_native")
-    op.forward(xv.value, wv.value, bv.value)
-    op.grad = gpu(dy)
-    op.backward()
+    with conv_algorithm(algorithm):
+        op = mf.Conv2D_ReLU_Op(xv, wv, stride=case[3], padding=case[4], bias=bv, backend="hip_native")
+        op.forward(xv.value, wv.value, bv.value)
+        op.grad = gpu(dy)
+        op.backward()
     pre = naive.conv_forward(x.astype(np.float64), w.astype(np.float64), case[3], case[4]) + b[None, :, None, None]
     ref_dx, _ = naive.conv_backward(x.astype(np.float64), w.astype(np.float64), dy * (pre > 0), case[3], case[4])
     assert wv.grad is None and bv.grad is None
     assert_near(host(xv.grad), ref_dx, 1e-5, "dx")
 
 
-@pytest.mark.parametrize("case", (PERFORMANCE_CASES[0], PERFORMANCE_CASES[1]), ids=lambda c: c[0])
-def test_gradients_are_bitwise_reproducible(case):
-    first = run_operator(case)[2]
-    second = run_operator(case)[2]
+@pytest.mark.parametrize("algorithm", ALGORITHMS)
+@pytest.mark.parametrize("case", (PERFORMANCE_CASES[0], PERFORMANCE_CASES[1], RESNET_CASES[1]),
+                         ids=lambda c: c[0])
+def test_gradients_are_bitwise_reproducible(case, algorithm):
+    first = run_operator(case, algorithm=algorithm)[2]
+    second = run_operator(case, algorithm=algorithm)[2]
     for a, b in zip(first, second):
         np.testing.assert_array_equal(a, b)
 
 
 def test_recomputed_columns_give_identical_gradients():
     case = PERFORMANCE_CASES[0]
-    saved = run_operator(case)[2]
-    recomputed = run_operator(case, recompute_im2col=True)[2]
+    saved = run_operator(case, algorithm="im2col")[2]
+    recomputed = run_operator(case, algorithm="im2col", recompute_im2col=True)[2]
     for a, b in zip(saved, recomputed):
         np.testing.assert_array_equal(a, b)
+
+
+@pytest.mark.parametrize("case", CONV_CASES[1:] + RESNET_CASES, ids=lambda c: c[0])
+def test_implicit_path_is_exact_on_integer_data(case):
+    """Small integers make every product and every partial sum exact in float32, whatever the
+    summation order: the implicit forward, dW and dX must then equal the FP64 loops bit for bit,
+    which pins the gather's indexing, padding and image boundaries (and the flipped dX kernel)."""
+    print("integer", case[0], flush=True)
+    _, x_shape, w_shape, stride, padding = case
+    rng = np.random.default_rng(7)
+    x = rng.integers(-2, 3, size=x_shape).astype(np.float32)
+    w = rng.integers(-2, 3, size=w_shape).astype(np.float32)
+    n, co, oh, ow = (x_shape[0], w_shape[0], *rp.out_size(x_shape[2], x_shape[3], w_shape[2:], stride, padding))
+    dy = rng.integers(-2, 3, size=(n, co, oh, ow)).astype(np.float32)
+    y, cols = native.conv2d_forward(gpu(x), gpu(w), stride=stride, padding=padding, algorithm="implicit")
+    assert cols is None
+    dx, dw, db = native.conv2d_backward(gpu(x), gpu(w), gpu(dy), None, stride=stride, padding=padding,
+                                        algorithm="implicit")
+    x64, w64 = x.astype(np.float64), w.astype(np.float64)
+    ref_dx, ref_dw = naive.conv_backward(x64, w64, dy.astype(np.float64), stride, padding)
+    np.testing.assert_array_equal(host(y), naive.conv_forward(x64, w64, stride, padding))
+    np.testing.assert_array_equal(host(dx), ref_dx)
+    np.testing.assert_array_equal(host(dw), ref_dw)
+    np.testing.assert_array_equal(host(db), dy.astype(np.float64).sum(axis=(0, 2, 3)))
 
 
 @pytest.mark.parametrize("shape,kernel,stride,padding", [
@@ -183,9 +252,11 @@ def test_rows_path_forward_matches_the_nchw_gemm(case, monkeypatch):
     single segmented GEMM agree within the FP64 tolerance and both keep the activation."""
     _, w_np, b_np, _ = conv_fixture(case)
     x, w, b = (gpu(a) for a in conv_fixture(case)[:3])
-    direct, _ = native.conv2d_forward(x, w, b, stride=case[3], padding=case[4], activation="relu")
+    direct, _ = native.conv2d_forward(x, w, b, stride=case[3], padding=case[4], activation="relu",
+                                      algorithm="im2col")
     monkeypatch.setattr(native, "ROWS_PATH_MAX_PIXELS", 1 << 30)
-    rows, _ = native.conv2d_forward(x, w, b, stride=case[3], padding=case[4], activation="relu")
+    rows, _ = native.conv2d_forward(x, w, b, stride=case[3], padding=case[4], activation="relu",
+                                    algorithm="im2col")
     _, _, _, _, pre = fp64_case(case)
     assert_near(host(direct), np.maximum(pre, 0), 1e-5, "direct")
     assert_near(host(rows), np.maximum(pre, 0), 1e-5, "rows")

@@ -60,15 +60,22 @@ def test_linear_backends_match_fp64():
     assert leaves[0].grad is None  # an input without requires_grad skips the dX GEMM
 
 
-def test_c3_convolution_and_pool_configuration():
-    """Conv 64->64 3x3/1/1 at N=32, 30x40 (forward, dX, dW, db), then MaxPool 2x2/2 forward/backward."""
+@pytest.mark.parametrize("algorithm", native.CONV_ALGORITHMS)
+def test_c3_convolution_and_pool_configuration(algorithm):
+    """Conv 64->64 3x3/1/1 at N=32, 30x40 (forward, dX, dW, db), then MaxPool 2x2/2 forward/backward;
+    the im2col matrix bit-exact (written by the forward, or by conv2d_im2col for the implicit path)."""
     rng = np.random.default_rng(0)
     x = rng.standard_normal((32, 64, 30, 40)).astype(np.float32)
     w = (rng.standard_normal((64, 64, 3, 3)) * np.sqrt(2.0 / 576)).astype(np.float32)
     b = np.zeros(64, np.float32)
-    y, cols = native.conv2d_forward(gpu(x), gpu(w), gpu(b), stride=(1, 1), padding=(1, 1))
+    y, cols = native.conv2d_forward(gpu(x), gpu(w), gpu(b), stride=(1, 1), padding=(1, 1), algorithm=algorithm)
     y64, cols_ref = rp.conv2d_forward(x.astype(np.float64), w.astype(np.float64), b, (1, 1), (1, 1))
-    np.testing.assert_array_equal(host(cols), cols_ref.astype(np.float32))
+    if algorithm == "implicit":
+        assert cols is None
+        cols_check = native.conv2d_im2col(gpu(x), w.shape, stride=(1, 1), padding=(1, 1))
+    else:
+        cols_check = cols
+    np.testing.assert_array_equal(host(cols_check), cols_ref.astype(np.float32))
     assert_near(host(y), y64, 1e-5, "y")
     pooled, ctx = native.maxpool2d_forward(y, kernel_size=(2, 2), stride=(2, 2))
     y_host = host(y)
@@ -79,7 +86,8 @@ def test_c3_convolution_and_pool_configuration():
     dy = native.maxpool2d_backward(gpu(dp), ctx)
     dy_ref = rp.maxpool2d_native_backward(dp, argmax_ref, y_host.shape)
     np.testing.assert_array_equal(host(dy), dy_ref)
-    dx, dw, db = native.conv2d_backward(gpu(x), gpu(w), dy, cols, stride=(1, 1), padding=(1, 1))
+    dx, dw, db = native.conv2d_backward(gpu(x), gpu(w), dy, cols, stride=(1, 1), padding=(1, 1),
+                                        algorithm=algorithm)
     dx64, dw64, db64 = rp.conv2d_backward(x.astype(np.float64), w.astype(np.float64), dy_ref.astype(np.float64),
                                           cols_ref, (1, 1), (1, 1))
     assert_near(host(dx), dx64, 1e-5, "dx")
