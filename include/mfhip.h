@@ -91,13 +91,15 @@ MFH_API int mfh_conv_backward(uint64_t weight, uint64_t dy, uint64_t y, uint64_t
 /* Implicit-GEMM convolution forward: y (N,CO,OH,OW) = act(conv(x, weight) + bias) with the im2col
  * matrix gathered from x inside the GEMM's operand loads (no cols buffer). One GEMM
  * W (CO x K) . view (K x N*OH*OW) over every image, stored straight into NCHW with the bias and
- * activation in its epilogue. workspace: mfh_conv_implicit_workspace(..., 0) floats let it split K
- * (0 is allowed: no split). Arguments otherwise as mfh_conv_forward.
+ * activation in its epilogue. When CI is a multiple of 16 the features run in channel chunks of 16
+ * per window tap and `wt` (CO*CI*KH*KW floats, 16-byte aligned) receives the kernel in that order;
+ * otherwise wt is unused and may be 0. workspace: mfh_conv_implicit_workspace(..., 0) floats let
+ * it split K (0 is allowed: no split). Arguments otherwise as mfh_conv_forward.
  * Has no single counterpart in the reference: it replaces the im2col + gemm_rows + epilogue sequence
  * of mf_conv_forward, native_cublas.cpp:1441-1461, when the caller does not keep cols. */
-MFH_API int mfh_conv_forward_implicit(uint64_t x, uint64_t weight, uint64_t bias, uint64_t y, int N, int CI, int H,
-                                      int W, int CO, int KH, int KW, int OH, int OW, int SH, int SW, int PH, int PW,
-                                      int activation, float alpha, int engine, uint64_t workspace,
+MFH_API int mfh_conv_forward_implicit(uint64_t x, uint64_t weight, uint64_t wt, uint64_t bias, uint64_t y, int N,
+                                      int CI, int H, int W, int CO, int KH, int KW, int OH, int OW, int SH, int SW,
+                                      int PH, int PW, int activation, float alpha, int engine, uint64_t workspace,
                                       int64_t workspace_floats, uint64_t stream);
 
 /* Split-K workspace floats of one pass of the implicit convolution under the automatic plan
@@ -113,7 +115,8 @@ MFH_API int64_t mfh_conv_implicit_workspace(int N, int CI, int H, int W, int CO,
  *   dw   (CO, CI*KH*KW) = dy . im2col(x) with dy read in place (split over the pixels on dw_engine
  *          through the workspace); needs x;
  *   dx   stride 1: a forward convolution of dy with the flipped kernel, written to `wflip`
- *          (CI*CO*KH*KW floats), straight into NCHW dx; other strides: the per-image column
+ *          (CI*CO*KH*KW floats, 16-byte aligned; in chunks of 16 output channels per tap when CO
+ *          is a multiple of 16), straight into NCHW dx; other strides: the per-image column
  *          gradient W^T dy_n in grad_cols (N*CI*KH*KW*OH*OW floats) and the col2im gather.
  * workspace: at least the larger of mfh_conv_implicit_workspace passes 1 and 2 that are requested.
  * Has no single counterpart in the reference: it replaces mf_conv_backward_plans,

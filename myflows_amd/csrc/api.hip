@@ -309,9 +309,9 @@ MFH_API int mfh_conv_backward(std::uint64_t weight, std::uint64_t dy, std::uint6
     return launch_col2im_t(as_ptr<const float>(grad_cols), as_ptr<float>(dx), g, per_image, s);
 }
 
-MFH_API int mfh_conv_forward_implicit(std::uint64_t x, std::uint64_t weight, std::uint64_t bias, std::uint64_t y,
-                                      int N, int CI, int H, int W, int CO, int KH, int KW, int OH, int OW, int SH,
-                                      int SW, int PH, int PW, int activation, float alpha, int engine,
+MFH_API int mfh_conv_forward_implicit(std::uint64_t x, std::uint64_t weight, std::uint64_t wt, std::uint64_t bias,
+                                      std::uint64_t y, int N, int CI, int H, int W, int CO, int KH, int KW, int OH,
+                                      int OW, int SH, int SW, int PH, int PW, int activation, float alpha, int engine,
                                       std::uint64_t workspace, std::int64_t workspace_floats, std::uint64_t stream) {
     MFH_TRY(require_ready());
     const ConvGeometry g{N, CI, H, W, CO, KH, KW, OH, OW, SH, SW, PH, PW};
@@ -319,10 +319,11 @@ MFH_API int mfh_conv_forward_implicit(std::uint64_t x, std::uint64_t weight, std
     MFH_TRY(validate_activation(activation, alpha));
     MFH_TRY(validate_engine(engine));
     MFH_REQUIRE(x && weight && y, "conv forward received a null buffer");
+    MFH_REQUIRE(wt || !implicit_chunked(CI), "the implicit forward needs the reordered-kernel buffer wt");
     MFH_REQUIRE(workspace_floats >= 0, "workspace size must be non-negative");
-    return conv_implicit_forward(g, as_ptr<const float>(x), as_ptr<const float>(weight), as_ptr<const float>(bias),
-                                 as_ptr<float>(y), activation, alpha, engine, as_ptr<float>(workspace),
-                                 workspace_floats, as_stream(stream));
+    return conv_implicit_forward(g, as_ptr<const float>(x), as_ptr<const float>(weight), as_ptr<float>(wt),
+                                 as_ptr<const float>(bias), as_ptr<float>(y), activation, alpha, engine,
+                                 as_ptr<float>(workspace), workspace_floats, as_stream(stream));
 }
 
 MFH_API std::int64_t mfh_conv_implicit_workspace(int N, int CI, int H, int W, int CO, int KH, int KW, int OH, int OW,

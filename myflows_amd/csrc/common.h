@@ -133,6 +133,8 @@ struct GemmParams {
     int segment;               // 0: C is dense; > 0: output column j is (j / segment, j % segment)
     FastDiv segment_div;       // division by segment
     long long segment_stride;  // distance between consecutive segments of C
+    int taps;                  // > 0: columns are convolution features in chunked order (see ConvGather)
+    FastDiv taps_div;          // division by taps
 };
 
 // One GEMM problem, or `batch` of them at constant strides: C(M x N) = op(A) op(B), row-major;
@@ -161,6 +163,7 @@ struct GemmEpilogue {
     float alpha = 0.0f;
     int segment = 0;
     long long segment_stride = 0;
+    int taps = 0;  // KH*KW when the output columns are features in chunked order; stored in natural order
 };
 
 // Runs the engine; splits K through the workspace (never for batches) only when it holds the
@@ -176,7 +179,10 @@ int split_reduce_epilogue(const float* partial, float* c, const GemmEpilogue& e,
 
 // ---- implicit.hip -----------------------------------------------------------------------------
 // The im2col view of an NCHW source read in place: view[k][q] = src[n, c, oh*SH - PH + kh,
-// ow*SW - PW + kw] (0 outside), feature k = (c*KH + kh)*KW + kw, pixel q = (n*OH + oh)*OW + ow.
+// ow*SW - PW + kw] (0 outside), pixel q = (n*OH + oh)*OW + ow. Feature k is (c, tap = kh*KW + kw)
+// in natural order, k = c*KH*KW + tap, or, when `chunked` (C a multiple of 32), in chunked order
+// k = ((c / 32)*KH*KW + tap)*32 + c % 32: every run of 32 features then shares one window tap.
+constexpr int CHANNEL_CHUNK = 32;
 struct ConvGather {
     const float* src;
     int C, H, W;
@@ -185,20 +191,24 @@ struct ConvGather {
     int pixels;    // N * OH * OW
     int features;  // C * KH * KW
     int hw, chw;   // H * W, C * H * W
+    int chunked;
     FastDiv div_ohw, div_ow, div_khkw, div_kw;
 };
 constexpr int IMPLICIT_FORWARD = 0, IMPLICIT_WGRAD = 1, IMPLICIT_DGRAD = 2;
-unsigned implicit_forward_tiles();
 // Split-K workspace floats of one pass of the implicit convolution under the automatic plan.
 std::int64_t implicit_workspace_floats(const ConvGeometry& g, int pass);
-// y = act(conv(x, w) + bias), NCHW, without an im2col buffer.
-int conv_implicit_forward(const ConvGeometry& g, const float* x, const float* w, const float* bias, float* y, int act,
-                          float alpha, int engine, float* workspace, std::int64_t workspace_floats, hipStream_t stream);
+// Whether the implicit kernels take a convolution over C input channels in chunked feature order.
+inline bool implicit_chunked(int C) { return C % CHANNEL_CHUNK == 0; }
+// y = act(conv(x, w) + bias), NCHW, without an im2col buffer; wt (CO*CI*KH*KW floats) receives
+// the kernel in the feature order of the GEMM.
+int conv_implicit_forward(const ConvGeometry& g, const float* x, const float* w, float* wt, const float* bias, float* y,
+                          int act, float alpha, int engine, float* workspace, std::int64_t workspace_floats,
+                          hipStream_t stream);
 // dW = dy . im2col(x), with dy read in place from NCHW.
 int conv_implicit_wgrad(const ConvGeometry& g, const float* x, const float* dy, float* dw, int engine,
                         float* workspace, std::int64_t workspace_floats, hipStream_t stream);
 // dX of a stride-1 convolution as a forward convolution of dy with the flipped kernel (written to
-// wflip, CI x CO*KH*KW floats).
+// wflip, CI x CO*KH*KW floats, in the GEMM's feature order).
 int conv_implicit_dgrad(const ConvGeometry& g, const float* dy, const float* w, float* wflip, float* dx, int engine,
                         float* workspace, std::int64_t workspace_floats, hipStream_t stream);
 // partial[r] = FP64 sum of row r (rows x length floats).

@@ -278,6 +278,8 @@ GemmParams epilogue_params(const GemmEpilogue& e, int M, int N, int ldc) {
     p.segment = e.segment;
     if (e.segment > 0) p.segment_div = FastDiv(e.segment);
     p.segment_stride = e.segment_stride;
+    p.taps = e.taps;
+    if (e.taps > 0) p.taps_div = FastDiv(e.taps);
     return p;
 }
 
@@ -338,6 +340,7 @@ int gemm_launch(int engine, hipStream_t stream, const GemmOperands& o, const Gem
         p.bias_mode = BIAS_NONE;
         p.act = ACT_NONE;
         p.segment = 0;
+        p.taps = 0;
     } else {
         p.C = o.c;
         p.c_batch = o.c_batch;

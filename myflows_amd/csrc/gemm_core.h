@@ -32,14 +32,17 @@ typedef float v16f __attribute__((ext_vector_type(16)));
 constexpr int GROUP_M = 8;  // tile rows per group of the tile order
 constexpr int XCDS = 8;     // accelerator complex dies of an MI355X
 
-template <int BM_, int BN_, int BK_, int WM_, int WN_, bool TA_, bool TB_>
+// PAD_A / PAD_B: floats of padding after each LDS row. k-contiguous tiles need it (the float4
+// reads of consecutive rows at one k would otherwise share banks); an mn-contiguous tile is read
+// along its rows and can go without.
+template <int BM_, int BN_, int BK_, int WM_, int WN_, bool TA_, bool TB_, int PAD_A = 4, int PAD_B = 4>
 struct MfmaShape {
     static constexpr int BM = BM_, BN = BN_, BK = BK_, WM = WM_, WN = WN_;
     static constexpr bool TA = TA_, TB = TB_;
     static constexpr int WGN = BN / WN, WAVES = (BM / WM) * WGN, THREADS = WAVES * 64;
     static constexpr int TM = WM / 32, TN = WN / 32, HALF = BK / 2;
-    static constexpr int LDA_S = TA ? BM + 4 : BK + 4;  // LDS row lengths (floats)
-    static constexpr int LDB_S = TB ? BK + 4 : BN + 4;
+    static constexpr int LDA_S = TA ? BM + PAD_A : BK + PAD_A;  // LDS row lengths (floats)
+    static constexpr int LDB_S = TB ? BK + PAD_B : BN + PAD_B;
     static constexpr int A_SIZE = TA ? BK * LDA_S : BM * LDA_S;
     static constexpr int B_SIZE = TB ? BN * LDB_S : BK * LDB_S;
     static constexpr int STAGE = A_SIZE + B_SIZE;
@@ -98,8 +101,14 @@ __device__ __forceinline__ float activate(float v, int act, float alpha) {
 }
 
 // Where output (row, col) lives: dense row * ldc + col, or segmented (column j is element j % segment
-// of segment j / segment, segments segment_stride apart).
+// of segment j / segment, segments segment_stride apart), after mapping a chunked-order feature
+// column back to its natural index when p.taps is set.
 __device__ __forceinline__ long long output_offset(const GemmParams& p, int row, int col) {
+    if (p.taps) {  // chunked feature order -> natural order c * taps + tap
+        int tap;
+        const int chunk = p.taps_div.divmod(col / CHANNEL_CHUNK, tap);
+        col = (chunk * CHANNEL_CHUNK + col % CHANNEL_CHUNK) * p.taps + tap;
+    }
     if (p.segment) {
         int within;
         const int segment = p.segment_div.divmod(col, within);
@@ -140,13 +149,50 @@ __device__ __forceinline__ void zero_acc(v16f (&acc)[S::TM][S::TN]) {
             for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
 }
 
+// One stage of MFMAs on the LDS tiles As / Bs (see the operand mapping above).
+template <class S>
+__device__ __forceinline__ void mfma_stage(const float* As, const float* Bs, v16f (&acc)[S::TM][S::TN], int wm0,
+                                           int wn0, int lane) {
+    constexpr int HALF = S::HALF, LDA_S = S::LDA_S, LDB_S = S::LDB_S;
+    const int lm = lane % 32, h = lane / 32;
+#pragma unroll
+    for (int kk = 0; kk < HALF; kk += 4) {
+        const int k = h * HALF + kk;
+        float4 a[S::TM], b[S::TN];
+#pragma unroll
+        for (int i = 0; i < S::TM; ++i) {
+            const int m = wm0 + i * 32 + lm;
+            if constexpr (S::TA)
+                a[i] = make_float4(As[k * LDA_S + m], As[(k + 1) * LDA_S + m], As[(k + 2) * LDA_S + m],
+                                   As[(k + 3) * LDA_S + m]);
+            else a[i] = *reinterpret_cast<const float4*>(As + m * LDA_S + k);
+        }
+#pragma unroll
+        for (int j = 0; j < S::TN; ++j) {
+            const int n = wn0 + j * 32 + lm;
+            if constexpr (S::TB) b[j] = *reinterpret_cast<const float4*>(Bs + n * LDB_S + k);
+            else
+                b[j] = make_float4(Bs[k * LDB_S + n], Bs[(k + 1) * LDB_S + n], Bs[(k + 2) * LDB_S + n],
+                                   Bs[(k + 3) * LDB_S + n]);
+        }
+#pragma unroll
+        for (int i = 0; i < S::TM; ++i)
+#pragma unroll
+            for (int j = 0; j < S::TN; ++j) {
+                acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[i].x, b[j].x, acc[i][j], 0, 0, 0);
+                acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[i].y, b[j].y, acc[i][j], 0, 0, 0);
+                acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[i].z, b[j].z, acc[i][j], 0, 0, 0);
+                acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[i].w, b[j].w, acc[i][j], 0, 0, 0);
+            }
+    }
+}
+
 // The K loop over [k_begin, k_end) in BK stages. fetch(kt) issues the global reads of the stage
 // starting at kt; store(a_lds, b_lds) writes the fetched registers into one LDS stage buffer.
 template <class S, class Fetch, class Store>
 __device__ __forceinline__ void mfma_k_loop(float* smem, int k_begin, int k_end, Fetch&& fetch, Store&& store,
                                             v16f (&acc)[S::TM][S::TN], int wm0, int wn0, int lane) {
-    constexpr int BK = S::BK, HALF = S::HALF, LDA_S = S::LDA_S, LDB_S = S::LDB_S;
-    const int lm = lane % 32, h = lane / 32;
+    constexpr int BK = S::BK;
     const int stages = k_end > k_begin ? (k_end - k_begin + BK - 1) / BK : 0;
     if (stages > 0) {
         fetch(k_begin);
@@ -157,37 +203,7 @@ __device__ __forceinline__ void mfma_k_loop(float* smem, int k_begin, int k_end,
         const bool more = t + 1 < stages;
         if (more) fetch(k_begin + (t + 1) * BK);
         const float* As = smem + (t & 1) * S::STAGE;
-        const float* Bs = As + S::A_SIZE;
-#pragma unroll
-        for (int kk = 0; kk < HALF; kk += 4) {
-            const int k = h * HALF + kk;
-            float4 a[S::TM], b[S::TN];
-#pragma unroll
-            for (int i = 0; i < S::TM; ++i) {
-                const int m = wm0 + i * 32 + lm;
-                if constexpr (S::TA)
-                    a[i] = make_float4(As[k * LDA_S + m], As[(k + 1) * LDA_S + m], As[(k + 2) * LDA_S + m],
-                                       As[(k + 3) * LDA_S + m]);
-                else a[i] = *reinterpret_cast<const float4*>(As + m * LDA_S + k);
-            }
-#pragma unroll
-            for (int j = 0; j < S::TN; ++j) {
-                const int n = wn0 + j * 32 + lm;
-                if constexpr (S::TB) b[j] = *reinterpret_cast<const float4*>(Bs + n * LDB_S + k);
-                else
-                    b[j] = make_float4(Bs[k * LDB_S + n], Bs[(k + 1) * LDB_S + n], Bs[(k + 2) * LDB_S + n],
-                                       Bs[(k + 3) * LDB_S + n]);
-            }
-#pragma unroll
-            for (int i = 0; i < S::TM; ++i)
-#pragma unroll
-                for (int j = 0; j < S::TN; ++j) {
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[i].x, b[j].x, acc[i][j], 0, 0, 0);
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[i].y, b[j].y, acc[i][j], 0, 0, 0);
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[i].z, b[j].z, acc[i][j], 0, 0, 0);
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[i].w, b[j].w, acc[i][j], 0, 0, 0);
-                }
-        }
+        mfma_stage<S>(As, As + S::A_SIZE, acc, wm0, wn0, lane);
         if (more) {
             float* next = smem + ((t + 1) & 1) * S::STAGE;
             store(next, next + S::A_SIZE);

@@ -16,16 +16,27 @@
 //   * dX (stride 1): a forward convolution of dy with the kernel flipped and transposed,
 //     wflip[ci][co][kh][kw] = W[co][ci][KH-1-kh][KW-1-kw], padding KH-1-PH / KW-1-PW, written
 //     straight into NCHW dx: no column gradient and no col2im pass.
+// Feature order. When the source has a multiple of 32 channels the features are taken in chunked
+// order k = ((c / 32)*KH*KW + tap)*32 + c % 32 (tap = kh*KW + kw), so a 32-deep stage of the
+// forward product covers 32 channels at one window tap: the tap is decomposed once per stage (a
+// scalar), each thread tests its pixel's window bounds once per stage and then reads 16/RSTEP
+// channels at a fixed stride. The kernel is reordered to match by weight_order_kernel (with the
+// dX flip folded in), and dW's output columns are mapped back to natural order by the epilogue.
+// Other channel counts (the 3-channel stem) take the natural order k = c*KH*KW + tap, decomposed
+// per feature row (a wave-uniform scalar computation).
 // Both gather loaders keep one pixel per thread column so that the pixel's decomposition
-// (n, oh, ow) is done once per stage (dW) or once per kernel (forward); in the forward loader every
-// wave reads one feature row k, so k's decomposition is a wave-uniform scalar computation.
+// (n, oh, ow) is done once per stage (dW) or once per kernel (forward).
+#include <algorithm>
+#include <type_traits>
+
 #include "common.h"
 #include "gemm_core.h"
 
 namespace mfh {
 namespace {
 
-constexpr int BK = 16;
+constexpr int BK = 32;     // stage depth of the forward / dX products (one channel chunk)
+constexpr int BK_WG = 16;  // stage depth of the dW products (a run of pixels)
 constexpr int FAR = -(1 << 24);  // window offset of a feature row past the end: every pixel is out of bounds
 
 // Forward orientation: a BK x BN tile of the view, rows = features [kt, kt + BK), columns = pixels
@@ -74,7 +85,66 @@ struct GatherFeatureRows {
     }
 };
 
-// The decomposition of one output pixel q (dW orientation: thread t handles pixel kt + t % BK).
+// The same tile in chunked feature order: stage kt covers channels [c0, c0 + 16) at one tap.
+template <int BN, int THREADS>
+struct GatherChunkRows {
+    static_assert(BN % 64 == 0 && THREADS % BN == 0, "rows split over whole waves");
+    static constexpr int RSTEP = THREADS / BN, PER = BK / RSTEP;
+    static_assert(BK == CHANNEL_CHUNK && BK % RSTEP == 0, "one stage is one channel chunk");
+    int origin, ih0, iw0;
+    bool valid;
+    float v[PER];
+
+    __device__ __forceinline__ void init(const ConvGather& g, int n0, int tid) {
+        const int q = n0 + tid % BN;
+        valid = q < g.pixels;
+        int rem, ow;
+        const int n = g.div_ohw.divmod(valid ? q : 0, rem);
+        const int oh = g.div_ow.divmod(rem, ow);
+        ih0 = oh * g.SH - g.PH;
+        iw0 = ow * g.SW - g.PW;
+        origin = n * g.chw + ih0 * g.W + iw0;
+    }
+
+    __device__ __forceinline__ void load(const ConvGather& g, int kt, int k_end, int tid) {
+        int tap, kw;
+        const int chunk = g.div_khkw.divmod(kt / CHANNEL_CHUNK, tap);
+        const int kh = g.div_kw.divmod(tap, kw);
+        const int ih = ih0 + kh, iw = iw0 + kw;
+        const bool ok = valid && kt < k_end && static_cast<unsigned>(ih) < static_cast<unsigned>(g.H) &&
+                        static_cast<unsigned>(iw) < static_cast<unsigned>(g.W);
+        const int offset = origin + (chunk * CHANNEL_CHUNK + tid / BN) * g.hw + kh * g.W + kw;
+        const int step = RSTEP * g.hw;
+        if (ok) {
+#pragma unroll
+            for (int i = 0; i < PER; ++i) v[i] = g.src[offset + i * step];
+        } else {
+#pragma unroll
+            for (int i = 0; i < PER; ++i) v[i] = 0.0f;
+        }
+    }
+
+    template <int LD>
+    __device__ __forceinline__ void store(float* lds, int tid) const {
+        const int r0 = tid / BN, col = tid % BN;
+#pragma unroll
+        for (int i = 0; i < PER; ++i) lds[(r0 + i * RSTEP) * LD + col] = v[i];
+    }
+};
+
+// (c, kh, kw) of feature k in the gather's feature order.
+__device__ __forceinline__ void feature_of(const ConvGather& g, int k, int& c, int& kh, int& kw) {
+    int tap;
+    if (g.chunked) {
+        const int chunk = g.div_khkw.divmod(k / CHANNEL_CHUNK, tap);
+        c = chunk * CHANNEL_CHUNK + k % CHANNEL_CHUNK;
+    } else {
+        c = g.div_khkw.divmod(k, tap);
+    }
+    kh = g.div_kw.divmod(tap, kw);
+}
+
+// The decomposition of one output pixel q (dW orientation: thread t handles pixel kt + t % BK_WG).
 struct PixelAt {
     bool valid;
     int n, p;       // image and pixel within the image (p = oh*OW + ow)
@@ -92,24 +162,23 @@ __device__ __forceinline__ PixelAt pixel_at(const ConvGather& g, int q, int q_en
     return at;
 }
 
-// dW orientation: a BN x BK tile of the transposed view, rows = features [n0, n0 + BN), columns =
-// pixels [kt, kt + BK), stored k-contiguous ([BN][BK + 4]). A thread's feature rows are fixed for
+// dW orientation: a BN x BK_WG tile of the transposed view, rows = features [n0, n0 + BN), columns =
+// pixels [kt, kt + BK_WG), stored k-contiguous ([BN][BK_WG + 4]). A thread's feature rows are fixed for
 // the whole kernel, so their (c, kh, kw) offsets are decomposed once.
 template <int BN, int THREADS>
 struct GatherPixelColumns {
-    static_assert(THREADS % BK == 0 && BN % (THREADS / BK) == 0, "rows split evenly over the threads");
-    static constexpr int RSTEP = THREADS / BK, PER = BN / RSTEP;
+    static_assert(THREADS % BK_WG == 0 && BN % (THREADS / BK_WG) == 0, "rows split evenly over the threads");
+    static constexpr int RSTEP = THREADS / BK_WG, PER = BN / RSTEP;
     int offset[PER], kh[PER], kw[PER];
     float v[PER];
 
     __device__ __forceinline__ void init(const ConvGather& g, int n0, int tid) {
 #pragma unroll
         for (int i = 0; i < PER; ++i) {
-            const int k = n0 + tid / BK + i * RSTEP;
+            const int k = n0 + tid / BK_WG + i * RSTEP;
             if (k < g.features) {
-                int rem, w;
-                const int c = g.div_khkw.divmod(k, rem);
-                const int h = g.div_kw.divmod(rem, w);
+                int c, h, w;
+                feature_of(g, k, c, h, w);
                 offset[i] = c * g.hw + h * g.W + w;
                 kh[i] = h;
                 kw[i] = w;
@@ -134,33 +203,33 @@ struct GatherPixelColumns {
 
     template <int LD>
     __device__ __forceinline__ void store(float* lds, int tid) const {
-        const int r0 = tid / BK, col = tid % BK;
+        const int r0 = tid / BK_WG, col = tid % BK_WG;
 #pragma unroll
         for (int i = 0; i < PER; ++i) lds[(r0 + i * RSTEP) * LD + col] = v[i];
     }
 };
 
-// dW's A operand: dy read in place, A[co][q] = dy[n, co, p] for pixel q = (n, p), as a BM x BK
+// dW's A operand: dy read in place, A[co][q] = dy[n, co, p] for pixel q = (n, p), as a BM x BK_WG
 // k-contiguous tile (rows = output channels, columns = the same pixels as the gathered tile).
 template <int BM, int THREADS>
 struct GradRowsInPlace {
-    static constexpr int RSTEP = THREADS / BK, PER = BM / RSTEP;
+    static constexpr int RSTEP = THREADS / BK_WG, PER = BM / RSTEP;
     static_assert(BM % RSTEP == 0, "rows split evenly over the threads");
     float v[PER];
 
     __device__ __forceinline__ void load(const float* __restrict__ dy, int CO, int ohw, int m0, const PixelAt& at,
                                          int tid) {
-        const int base = (at.n * CO + m0 + tid / BK) * ohw + at.p;
+        const int base = (at.n * CO + m0 + tid / BK_WG) * ohw + at.p;
 #pragma unroll
         for (int i = 0; i < PER; ++i) {
-            const int row = m0 + tid / BK + i * RSTEP;
+            const int row = m0 + tid / BK_WG + i * RSTEP;
             v[i] = at.valid && row < CO ? dy[base + i * RSTEP * ohw] : 0.0f;
         }
     }
 
     template <int LD>
     __device__ __forceinline__ void store(float* lds, int tid) const {
-        const int r0 = tid / BK, col = tid % BK;
+        const int r0 = tid / BK_WG, col = tid % BK_WG;
 #pragma unroll
         for (int i = 0; i < PER; ++i) lds[(r0 + i * RSTEP) * LD + col] = v[i];
     }
@@ -168,7 +237,7 @@ struct GradRowsInPlace {
 
 // Y (M x pixels) = A (M x K, row-major, lda) . view (K x pixels). Split-K writes dense partials
 // (z-th slice at C + z * c_batch); otherwise the epilogue of p (segmented NCHW, bias, activation).
-template <int BM, int BN, int WM, int WN, bool VA>
+template <int BM, int BN, int WM, int WN, bool VA, bool CHUNKED>
 __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void conv_implicit_forward_kernel(GemmParams p,
                                                                                           ConvGather g) {
     using S = MfmaShape<BM, BN, BK, WM, WN, false, false>;
@@ -183,7 +252,7 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void conv_implicit_forw
     float* __restrict__ C = p.C + (p.split ? z * p.c_batch : 0);
 
     TileLoader<BM, BK, S::THREADS, VA> la;
-    GatherFeatureRows<BN, S::THREADS> lb;
+    std::conditional_t<CHUNKED, GatherChunkRows<BN, S::THREADS>, GatherFeatureRows<BN, S::THREADS>> lb;
     lb.init(g, n0, tid);
     auto fetch = [&](int kt) {
         la.load(p.A, p.lda, m0, p.M, kt, k_end, tid);
@@ -203,7 +272,7 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void conv_implicit_forw
 template <int BM, int BN, int WM, int WN>
 __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void conv_implicit_wgrad_kernel(GemmParams p,
                                                                                         ConvGather g) {
-    using S = MfmaShape<BM, BN, BK, WM, WN, false, true>;
+    using S = MfmaShape<BM, BN, BK_WG, WM, WN, false, true>;
     __shared__ __attribute__((aligned(16))) float smem[2 * S::STAGE];
     int tile_m, tile_n, z;
     tile_of_workgroup(tile_m, tile_n, z);
@@ -219,7 +288,7 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void conv_implicit_wgra
     GatherPixelColumns<BN, S::THREADS> lb;
     lb.init(g, n0, tid);
     auto fetch = [&](int kt) {
-        const PixelAt at = pixel_at(g, kt + tid % BK, k_end);
+        const PixelAt at = pixel_at(g, kt + tid % BK_WG, k_end);
         la.load(p.A, p.M, ohw, m0, at, tid);
         lb.load(g, at);
     };
@@ -233,15 +302,26 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void conv_implicit_wgra
     store_acc<S>(p, C, acc, m0, n0, wm0, wn0, lane);
 }
 
-// wflip[ci][co][kh][kw] = w[co][ci][KH-1-kh][KW-1-kw]: the kernel of dX as a forward convolution.
-__global__ __launch_bounds__(256) void weight_flip_kernel(const float* __restrict__ w, float* __restrict__ wflip,
-                                                          int total, int CO, int CI, int KHW) {
+// The kernel as the A operand of an implicit product: out[o][k] for O rows and features k over C
+// channels and T = KH*KW taps, in chunked order when `chunked` (else natural order c*T + tap).
+// Forward (flip = 0): O = CO, C = CI, out[co][(c, tap)] = w[co][c][tap]. dX (flip = 1): O = CI,
+// C = CO, out[ci][(co, tap)] = w[co][ci][T - 1 - tap], the flipped and transposed kernel.
+__global__ __launch_bounds__(256) void weight_order_kernel(const float* __restrict__ w, float* __restrict__ out,
+                                                           int total, int O, int C, int T, int chunked, int flip) {
     const int idx = blockIdx.x * 256 + threadIdx.x;
     if (idx >= total) return;
-    const int tap = idx % KHW;
-    const int co = (idx / KHW) % CO;
-    const int ci = idx / (KHW * CO);
-    wflip[idx] = w[(co * CI + ci) * KHW + (KHW - 1 - tap)];
+    const int row_len = C * T;
+    const int o = idx / row_len, k = idx % row_len;
+    int c, tap;
+    if (chunked) {
+        const int group = k / CHANNEL_CHUNK;
+        tap = group % T;
+        c = (group / T) * CHANNEL_CHUNK + k % CHANNEL_CHUNK;
+    } else {
+        c = k / T;
+        tap = k % T;
+    }
+    out[idx] = flip ? w[(c * O + o) * T + (T - 1 - tap)] : w[(o * C + c) * T + tap];
 }
 
 // partial[row] = sum of the row's `length` floats in FP64 (rows are the (n, co) planes of dy). One
@@ -260,47 +340,60 @@ __global__ __launch_bounds__(256) void row_sums_kernel(const float* __restrict__
 
 using ConvFn = void (*)(GemmParams, ConvGather);
 
-// Forward tiles need BN to be a multiple of 64 (one feature row per wave); every tile serves dW.
-constexpr unsigned FORWARD_TILES = (1u << 0) | (1u << 1) | (1u << 2) | (1u << 3) | (1u << 6) | (1u << 7);
+// Tile catalogue of the implicit products: block tile BM x BN, wave tile WM x WN. The 64 x 64 wave
+// tiles keep four independent MFMA accumulators per wave and read half as much LDS per MFMA as
+// 32 x 32 ones; tiles 6 and 7 (32 x 32 waves) serve outputs too small to fill the GPU otherwise.
+struct ImplicitTile {
+    int bm, bn, wm, wn;
+};
+constexpr ImplicitTile TILE_TABLE[] = {
+    {64, 64, 64, 64},    // 0: one wave
+    {64, 128, 64, 64},   // 1: two waves
+    {128, 64, 64, 64},   // 2: two waves
+    {128, 128, 64, 64},  // 3: four waves
+    {64, 256, 64, 64},   // 4: four waves
+    {256, 64, 64, 64},   // 5: four waves
+    {64, 64, 32, 32},    // 6: four 32 x 32 waves
+    {32, 64, 32, 32},    // 7: two 32 x 32 waves
+};
+constexpr int TILE_COUNT = sizeof(TILE_TABLE) / sizeof(TILE_TABLE[0]);
+constexpr int threads_of(const ImplicitTile& t) { return (t.bm / t.wm) * (t.bn / t.wn) * 64; }
 
-template <int T, bool VA>
+template <int T, bool VA, bool CHUNKED>
 constexpr ConvFn forward_of() {
-    constexpr GemmTile t = gemm_tile_constexpr(T);
-    return conv_implicit_forward_kernel<t.bm, t.bn, t.wm, t.wn, VA>;
+    constexpr ImplicitTile t = TILE_TABLE[T];
+    return conv_implicit_forward_kernel<t.bm, t.bn, t.wm, t.wn, VA, CHUNKED>;
 }
 
 template <int T>
 constexpr ConvFn wgrad_of() {
-    constexpr GemmTile t = gemm_tile_constexpr(T);
+    constexpr ImplicitTile t = TILE_TABLE[T];
     return conv_implicit_wgrad_kernel<t.bm, t.bn, t.wm, t.wn>;
 }
 
+// forward[tile][0 | 1 | 2]: natural feature order with scalar / float4 A loads, chunked order.
 struct ConvKernels {
-    ConvFn forward[8][2] = {};
-    ConvFn wgrad[8] = {};
+    ConvFn forward[TILE_COUNT][3] = {};
+    ConvFn wgrad[TILE_COUNT] = {};
+    template <int T>
+    void fill() {
+        forward[T][0] = forward_of<T, false, false>();
+        forward[T][1] = forward_of<T, true, false>();
+        forward[T][2] = forward_of<T, true, true>();
+        wgrad[T] = wgrad_of<T>();
+    }
     ConvKernels() {
-        forward[0][0] = forward_of<0, false>();
-        forward[0][1] = forward_of<0, true>();
-        forward[1][0] = forward_of<1, false>();
-        forward[1][1] = forward_of<1, true>();
-        forward[2][0] = forward_of<2, false>();
-        forward[2][1] = forward_of<2, true>();
-        forward[3][0] = forward_of<3, false>();
-        forward[3][1] = forward_of<3, true>();
-        forward[6][0] = forward_of<6, false>();
-        forward[6][1] = forward_of<6, true>();
-        forward[7][0] = forward_of<7, false>();
-        forward[7][1] = forward_of<7, true>();
-        wgrad[0] = wgrad_of<0>();
-        wgrad[1] = wgrad_of<1>();
-        wgrad[2] = wgrad_of<2>();
-        wgrad[3] = wgrad_of<3>();
-        wgrad[4] = wgrad_of<4>();
-        wgrad[5] = wgrad_of<5>();
-        wgrad[6] = wgrad_of<6>();
-        wgrad[7] = wgrad_of<7>();
+        fill<0>();
+        fill<1>();
+        fill<2>();
+        fill<3>();
+        fill<4>();
+        fill<5>();
+        fill<6>();
+        fill<7>();
     }
 };
+static_assert(TILE_COUNT == 8, "ConvKernels fills every tile");
 
 const ConvKernels& conv_kernels() {
     static const ConvKernels table;
@@ -328,6 +421,7 @@ ConvGather gather_of(const float* src, int C, int H, int W, int KH, int KW, int 
     g.features = C * KH * KW;
     g.hw = H * W;
     g.chw = C * H * W;
+    g.chunked = implicit_chunked(C) ? 1 : 0;
     g.div_ohw = FastDiv(OH * OW);
     g.div_ow = FastDiv(OW);
     g.div_khkw = FastDiv(KH * KW);
@@ -335,17 +429,80 @@ ConvGather gather_of(const float* src, int C, int H, int W, int KH, int KW, int 
     return g;
 }
 
-// The plan of a product: tile and K split, from an engine code, limited to the tiles a kernel
-// family has; the split is dropped when the workspace cannot hold it.
-int implicit_plan(int engine, int M, int N, int K, unsigned tiles, float* workspace, std::int64_t workspace_floats,
+// Planner model. Each tile runs at a fraction `efficiency` of the matrix peak once the GPU is
+// full; a launch of W waves occupies each of the 4 * CUs SIMDs for ceil(W / SIMDs) wave-times (the
+// last, partial round costs a whole one). A split over K adds its partials' HBM round trip and the
+// reduction launch. The constants are fitted to a sweep of every tile and split on MI355X over
+// ResNet18's batch-64 convolutions (forward, dW and dX).
+constexpr double FORWARD_EFFICIENCY[TILE_COUNT] = {0.49, 0.53, 0.54, 0.43, 0.32, 0.49, 0.56, 0.42};
+constexpr double WGRAD_EFFICIENCY[TILE_COUNT] = {0.76, 0.66, 0.50, 0.82, 0.34, 0.75, 0.69, 0.47};
+constexpr double SIMD_MACS_PER_S = 157.3e12 / 2 / 1024;  // FP32 multiply-adds per second per SIMD
+constexpr double HBM_BYTES_PER_S = 6.0e12;               // achieved rate of the split-K partial traffic
+constexpr double LAUNCH_S = 3.0e-6;
+constexpr int SPLIT_CHOICES[] = {1, 2, 3, 4, 6, 8, 12, 16, 24, 32, 48, 64, 96, 128};
+
+double implicit_cost(bool wgrad, int tile, int M, int N, int slices, int chunk) {
+    const ImplicitTile& t = TILE_TABLE[tile];
+    const int waves = (t.bm / t.wm) * (t.bn / t.wn);
+    const std::int64_t tiles = static_cast<std::int64_t>(blocks_for(M, t.bm)) * blocks_for(N, t.bn);
+    const int simds = 4 * std::max(1, device_cu_count());
+    const std::int64_t rounds = (tiles * slices * waves + simds - 1) / simds;
+    const double wave_macs = static_cast<double>(t.wm) * t.wn * chunk;
+    const double efficiency = wgrad ? WGRAD_EFFICIENCY[tile] : FORWARD_EFFICIENCY[tile];
+    double cost = rounds * wave_macs / (SIMD_MACS_PER_S * efficiency);
+    if (slices > 1) cost += 4.0 * (2.0 * slices + 1.0) * M * N / HBM_BYTES_PER_S + LAUNCH_S;
+    return cost;
+}
+
+// A plan's K slices as whole stages of depth bk.
+GemmPlan whole_stages(int tile, int K, int requested, int bk) {
+    const int chunk = (static_cast<int>((static_cast<std::int64_t>(K) + requested - 1) / requested) + bk - 1) / bk * bk;
+    const int slices = (K + chunk - 1) / chunk;
+    return slices > 1 ? GemmPlan{tile, slices, chunk} : GemmPlan{tile, 1, K};
+}
+
+bool tile_fits(int tile, int M) { return blocks_for(M, TILE_TABLE[tile].bm) <= GRID_YZ_LIMIT; }
+
+// The plan of least estimated cost of a forward-orientation (forward, dX) or dW product.
+GemmPlan implicit_auto_plan(bool wgrad, int M, int N, int K) {
+    const int bk = wgrad ? BK_WG : BK;
+    GemmPlan best{-1, 1, K};
+    double best_cost = 0.0;
+    for (int tile = 0; tile < TILE_COUNT; ++tile) {
+        if (!tile_fits(tile, M)) continue;
+        for (const int requested : SPLIT_CHOICES) {
+            if (requested > 1 && K / requested < bk) break;
+            const GemmPlan plan = whole_stages(tile, K, requested, bk);
+            if (plan.slices > static_cast<int>(GRID_YZ_LIMIT)) continue;
+            const double cost = implicit_cost(wgrad, tile, M, N, plan.slices, plan.slices > 1 ? plan.k_chunk : K);
+            if (best.tile < 0 || cost < best_cost) {
+                best = plan;
+                best_cost = cost;
+            }
+        }
+    }
+    return best;
+}
+
+// The plan of a product from an engine code (1 = automatic; 16 + tile * 128 + slices - 1 names a
+// tile of TILE_TABLE and a requested K split); the split is dropped when the workspace cannot hold
+// it.
+int implicit_plan(bool wgrad, int engine, int M, int N, int K, float* workspace, std::int64_t workspace_floats,
                   GemmPlan* plan) {
-    if (engine == 1) *plan = gemm_auto_plan(M, N, K, 1, tiles);
-    else MFH_TRY(gemm_plan_from_engine(engine, M, N, K, plan));
-    if (!(tiles & (1u << plan->tile))) return MFH_FAIL(ERR_ARG, "this GEMM tile cannot run the implicit convolution");
+    if (engine == 1) {
+        *plan = implicit_auto_plan(wgrad, M, N, K);
+    } else {
+        const int code = engine - 16;
+        const int tile = code / 128, requested = code % 128 + 1;
+        if (code < 0 || tile >= TILE_COUNT) return MFH_FAIL(ERR_ARG, "unknown implicit convolution plan code");
+        *plan = whole_stages(tile, K, requested, wgrad ? BK_WG : BK);
+    }
+    if (plan->tile < 0 || !tile_fits(plan->tile, M))
+        return MFH_FAIL(ERR_ARG, "this tile cannot run the implicit convolution");
     if (plan->slices > 1 && (!workspace || workspace_floats < gemm_workspace_floats(*plan, M, N)))
         *plan = GemmPlan{plan->tile, 1, K};
-    const GemmTile& t = gemm_tile(plan->tile);
-    if (blocks_for(M, t.bm) > GRID_YZ_LIMIT || static_cast<unsigned>(plan->slices) > GRID_YZ_LIMIT ||
+    const ImplicitTile& t = TILE_TABLE[plan->tile];
+    if (static_cast<unsigned>(plan->slices) > GRID_YZ_LIMIT ||
         static_cast<std::int64_t>(blocks_for(M, t.bm)) * blocks_for(N, t.bn) * plan->slices > INDEX_LIMIT)
         return MFH_FAIL(ERR_ARG, "implicit convolution grid exceeds the launch limits");
     return OK;
@@ -378,12 +535,16 @@ int run_implicit(bool wgrad, const GemmPlan& plan, const float* a, int lda, int 
         p.segment = e.segment;
         if (e.segment > 0) p.segment_div = FastDiv(e.segment);
         p.segment_stride = e.segment_stride;
+        p.taps = e.taps;
+        if (e.taps > 0) p.taps_div = FastDiv(e.taps);
     }
-    const GemmTile& t = gemm_tile(plan.tile);
+    const ImplicitTile& t = TILE_TABLE[plan.tile];
     const dim3 grid(blocks_for(N, t.bn), blocks_for(M, t.bm), static_cast<unsigned>(plan.slices));
-    const dim3 block((t.bm / t.wm) * (t.bn / t.wn) * 64);
+    const dim3 block(threads_of(t));
     const bool vec_a = K % 4 == 0 && lda % 4 == 0 && aligned16(a);
-    const ConvFn fn = wgrad ? conv_kernels().wgrad[plan.tile] : conv_kernels().forward[plan.tile][vec_a ? 1 : 0];
+    const int variant = g.chunked ? 2 : vec_a ? 1 : 0;
+    if (!wgrad && g.chunked && !vec_a) return MFH_FAIL(ERR_ARG, "the reordered kernel buffer must be 16-byte aligned");
+    const ConvFn fn = wgrad ? conv_kernels().wgrad[plan.tile] : conv_kernels().forward[plan.tile][variant];
     hipLaunchKernelGGL(fn, grid, block, 0, stream, p, g);
     MFH_TRY(MFH_CHECK_LAUNCH(wgrad ? "conv_implicit_wgrad" : "conv_implicit_forward", stream));
     if (!split) return OK;
@@ -392,25 +553,34 @@ int run_implicit(bool wgrad, const GemmPlan& plan, const float* a, int lda, int 
 
 }  // namespace
 
-unsigned implicit_forward_tiles() { return FORWARD_TILES; }
-
 std::int64_t implicit_workspace_floats(const ConvGeometry& g, int pass) {
     GemmPlan plan;
-    if (pass == IMPLICIT_FORWARD) plan = gemm_auto_plan(g.CO, g.rows(), g.features(), 1, FORWARD_TILES);
-    else if (pass == IMPLICIT_WGRAD) plan = gemm_auto_plan(g.CO, g.features(), g.rows(), 1, ALL_TILES);
-    else plan = gemm_auto_plan(g.CI, g.N * g.H * g.W, g.CO * g.KH * g.KW, 1, FORWARD_TILES);
+    if (pass == IMPLICIT_FORWARD) plan = implicit_auto_plan(false, g.CO, g.rows(), g.features());
+    else if (pass == IMPLICIT_WGRAD) plan = implicit_auto_plan(true, g.CO, g.features(), g.rows());
+    else plan = implicit_auto_plan(false, g.CI, g.N * g.H * g.W, g.CO * g.KH * g.KW);
     return pass == IMPLICIT_WGRAD ? gemm_workspace_floats(plan, g.CO, g.features())
                                   : gemm_workspace_floats(plan, pass == IMPLICIT_FORWARD ? g.CO : g.CI,
                                                           pass == IMPLICIT_FORWARD ? g.rows() : g.N * g.H * g.W);
 }
 
-int conv_implicit_forward(const ConvGeometry& g, const float* x, const float* w, const float* bias, float* y, int act,
-                          float alpha, int engine, float* workspace, std::int64_t workspace_floats,
+int launch_weight_order(const float* w, float* out, int O, int C, int T, bool flip, hipStream_t stream) {
+    const int total = O * C * T;
+    weight_order_kernel<<<blocks_for(total, 256), 256, 0, stream>>>(w, out, total, O, C, T,
+                                                                     implicit_chunked(C) ? 1 : 0, flip ? 1 : 0);
+    return MFH_CHECK_LAUNCH("weight_order", stream);
+}
+
+int conv_implicit_forward(const ConvGeometry& g, const float* x, const float* w, float* wt, const float* bias,
+                          float* y, int act, float alpha, int engine, float* workspace, std::int64_t workspace_floats,
                           hipStream_t stream) {
     const int M = g.CO, N = g.rows(), K = g.features();
     GemmPlan plan;
-    MFH_TRY(implicit_plan(engine, M, N, K, FORWARD_TILES, workspace, workspace_floats, &plan));
+    MFH_TRY(implicit_plan(false, engine, M, N, K, workspace, workspace_floats, &plan));
     const ConvGather gather = gather_of(x, g.CI, g.H, g.W, g.KH, g.KW, g.SH, g.SW, g.PH, g.PW, g.N, g.OH, g.OW);
+    if (gather.chunked) {
+        MFH_TRY(launch_weight_order(w, wt, g.CO, g.CI, g.KH * g.KW, false, stream));
+        w = wt;
+    }
     GemmEpilogue e;
     e.bias = bias;
     e.bias_mode = bias ? BIAS_ROW : BIAS_NONE;
@@ -425,20 +595,20 @@ int conv_implicit_wgrad(const ConvGeometry& g, const float* x, const float* dy, 
                         float* workspace, std::int64_t workspace_floats, hipStream_t stream) {
     const int M = g.CO, N = g.features(), K = g.rows();
     GemmPlan plan;
-    MFH_TRY(implicit_plan(engine, M, N, K, ALL_TILES, workspace, workspace_floats, &plan));
+    MFH_TRY(implicit_plan(true, engine, M, N, K, workspace, workspace_floats, &plan));
     const ConvGather gather = gather_of(x, g.CI, g.H, g.W, g.KH, g.KW, g.SH, g.SW, g.PH, g.PW, g.N, g.OH, g.OW);
-    return run_implicit(true, plan, dy, g.ohw(), M, N, K, gather, dw, N, GemmEpilogue{}, workspace, stream);
+    GemmEpilogue e;
+    if (gather.chunked) e.taps = g.KH * g.KW;
+    return run_implicit(true, plan, dy, g.ohw(), M, N, K, gather, dw, N, e, workspace, stream);
 }
 
 int conv_implicit_dgrad(const ConvGeometry& g, const float* dy, const float* w, float* wflip, float* dx, int engine,
                         float* workspace, std::int64_t workspace_floats, hipStream_t stream) {
     const int khw = g.KH * g.KW;
     const int M = g.CI, N = g.N * g.H * g.W, K = g.CO * khw;
-    const int total = g.CI * K;
-    weight_flip_kernel<<<blocks_for(total, 256), 256, 0, stream>>>(w, wflip, total, g.CO, g.CI, khw);
-    MFH_TRY(MFH_CHECK_LAUNCH("weight_flip", stream));
+    MFH_TRY(launch_weight_order(w, wflip, g.CI, g.CO, khw, true, stream));
     GemmPlan plan;
-    MFH_TRY(implicit_plan(engine, M, N, K, FORWARD_TILES, workspace, workspace_floats, &plan));
+    MFH_TRY(implicit_plan(false, engine, M, N, K, workspace, workspace_floats, &plan));
     // dy as the source of a stride-1 convolution with padding KH-1-PH whose output grid is H x W.
     const ConvGather gather =
         gather_of(dy, g.CO, g.OH, g.OW, g.KH, g.KW, 1, 1, g.KH - 1 - g.PH, g.KW - 1 - g.PW, g.N, g.H, g.W);

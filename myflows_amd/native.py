@@ -72,7 +72,7 @@ _SIGNATURES = {
     "mfh_conv_im2col": ("i", "pp" + _CONV + "p"),
     "mfh_conv_forward": ("i", "pppppp" + _CONV + "ifipqp"),
     "mfh_conv_backward": ("i", "pppppppppp" + _CONV + "iifiipqp"),
-    "mfh_conv_forward_implicit": ("i", "pppp" + _CONV + "ifipqp"),
+    "mfh_conv_forward_implicit": ("i", "ppppp" + _CONV + "ifipqp"),
     "mfh_conv_implicit_workspace": ("q", _CONV + "i"),
     "mfh_conv_backward_implicit": ("i", "ppppppppppp" + _CONV + "ifiipqp"),
     "mfh_pool_forward": ("i", "ppp" + "i" * 10 + "p"),
@@ -396,8 +396,9 @@ def conv2d_forward(x, weight, bias=None, *, stride=(1, 1), padding=(0, 0), activ
     y = torch.empty(g.out_shape, dtype=torch.float32, device=device)
     if algorithm == "implicit":
         workspace, floats = _implicit_workspace(g, "forward")
-        _call("mfh_conv_forward_implicit", x.data_ptr(), weight.data_ptr(), _addr(bias), y.data_ptr(), *g.c_args(),
-              act, alpha, engine, _addr(workspace), floats, _stream())
+        wt = torch.empty_like(weight) if g.ci % 16 == 0 else None  # the kernel in chunked feature order
+        _call("mfh_conv_forward_implicit", x.data_ptr(), weight.data_ptr(), _addr(wt), _addr(bias), y.data_ptr(),
+              *g.c_args(), act, alpha, engine, _addr(workspace), floats, _stream())
         return y, None
     cols = torch.empty((g.m, g.k), dtype=torch.float32, device=device)
     rows = None
