@@ -578,9 +578,7 @@ MFH_API int mfh_bn_backward(std::uint64_t x, std::uint64_t dy, std::uint64_t gat
     b.gamma_grad = as_ptr<float>(gamma_grad);
     b.beta_grad = as_ptr<float>(beta_grad);
     b.residual_grad = as_ptr<float>(residual_grad);
-    double* ws = as_ptr<double>(workspace);
-    b.partial = ws;
-    b.coef = reinterpret_cast<float*>(ws + 2LL * s.C * norm_slices(s));
+    b.partial = as_ptr<double>(workspace);
     b.training = training != 0;
     b.add_x = add_x != 0;
     b.add_gamma = add_gamma != 0;

@@ -256,7 +256,6 @@ struct NormBackward {
     float* beta_grad;
     float* residual_grad;  // optional: receives the gated dy (the residual branch of a fused Add)
     double* partial;
-    float* coef;  // 3 x C scratch for the dx coefficients
     bool training, add_x, add_gamma, add_beta, add_residual;
 };
 int norm_backward(const NormShape& s, const NormBackward& b, hipStream_t stream);

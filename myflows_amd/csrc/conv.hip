@@ -7,6 +7,8 @@
 // (M = N*OH*OW rows, K = CI*KH*KW features); rows[(n*OHW + p)][co] is a GEMM output before the
 // epilogue; gcT[n][(ci*KH + kh)*KW + kw][oh*OW + ow] is the per-image transposed column gradient.
 // Every reduction sums in a fixed order, so each kernel is bitwise reproducible.
+#include <algorithm>
+
 #include "common.h"
 #include "fastdiv.h"
 
@@ -75,8 +77,9 @@ __global__ __launch_bounds__(256) void im2col_vec4_kernel(const float* __restric
 // result is deterministic.
 __global__ __launch_bounds__(256) void col2im_t_kernel(const float* __restrict__ gcT, float* __restrict__ dx,
                                                        int total, FastDiv div_w, FastDiv div_h, FastDiv div_ci,
-                                                       int CI, int KH, int KW, int OH, int OW, int SH, int SW, int PH,
-                                                       int PW, long long f_stride, long long n_stride) {
+                                                       int CI, int KH, int KW, int OH, int OW, int SH, int SW,
+                                                       FastDiv div_sh, FastDiv div_sw, int PH, int PW,
+                                                       long long f_stride, long long n_stride) {
     const int idx = blockIdx.x * 256 + threadIdx.x;
     if (idx >= total) return;
     int iw, ih, ci;
@@ -85,10 +88,10 @@ __global__ __launch_bounds__(256) void col2im_t_kernel(const float* __restrict__
     const int n = div_ci.divmod(t2, ci);
     const int hp = ih + PH, wp = iw + PW;  // coordinates in the zero-padded input
     // Windows oh with oh*SH <= hp <= oh*SH + KH - 1, likewise ow.
-    const int oh_lo = hp >= KH ? (hp - KH) / SH + 1 : 0;
-    const int oh_hi = min(OH - 1, hp / SH);
-    const int ow_lo = wp >= KW ? (wp - KW) / SW + 1 : 0;
-    const int ow_hi = min(OW - 1, wp / SW);
+    const int oh_lo = hp >= KH ? div_sh.div(hp - KH) + 1 : 0;
+    const int oh_hi = min(OH - 1, div_sh.div(hp));
+    const int ow_lo = wp >= KW ? div_sw.div(wp - KW) + 1 : 0;
+    const int ow_hi = min(OW - 1, div_sw.div(wp));
     const float* image = gcT + n * n_stride + static_cast<long long>(ci) * KH * KW * f_stride;
     float sum = 0.0f;
     for (int oh = oh_lo; oh <= oh_hi; ++oh) {
@@ -255,16 +258,16 @@ __global__ __launch_bounds__(256) void pool_forward_kernel(const float* __restri
 __global__ __launch_bounds__(256) void pool_backward_kernel(const float* __restrict__ dy,
                                                             const int* __restrict__ argmax, float* __restrict__ dx,
                                                             int total, FastDiv div_w, FastDiv div_h, int OH, int OW,
-                                                            int KH, int KW, int SH, int SW) {
+                                                            int KH, int KW, FastDiv div_sh, FastDiv div_sw) {
     const int idx = blockIdx.x * 256 + threadIdx.x;
     if (idx >= total) return;
     int iw, ih;
     const int t = div_w.divmod(idx, iw);
     const int nc = div_h.divmod(t, ih);
-    const int oh_lo = ih >= KH ? (ih - KH) / SH + 1 : 0;
-    const int oh_hi = min(OH - 1, ih / SH);
-    const int ow_lo = iw >= KW ? (iw - KW) / SW + 1 : 0;
-    const int ow_hi = min(OW - 1, iw / SW);
+    const int oh_lo = ih >= KH ? div_sh.div(ih - KH) + 1 : 0;
+    const int oh_hi = min(OH - 1, div_sh.div(ih));
+    const int ow_lo = iw >= KW ? div_sw.div(iw - KW) + 1 : 0;
+    const int ow_hi = min(OW - 1, div_sw.div(iw));
     float sum = 0.0f;
     for (int oh = oh_lo; oh <= oh_hi; ++oh)
         for (int ow = ow_lo; ow <= ow_hi; ++ow) {
@@ -274,11 +277,153 @@ __global__ __launch_bounds__(256) void pool_backward_kernel(const float* __restr
     dx[idx] = sum;
 }
 
+constexpr int PLANE_FLOATS = 12288;   // floats of one workgroup's LDS plane buffer (48 KB)
+constexpr int ROW_FLOATS = 12288;     // floats of the im2col row kernel's LDS input band (48 KB)
+
+// im2col of one output row (n, oh) per workgroup: the KH input rows it reads, for every channel and
+// with the padding columns and rows as zeros, are staged in LDS with coalesced reads; then the
+// OW x K block of cols that this row owns (contiguous in memory) is written in order, four features
+// per 16-byte store when K % 4 == 0.
+template <bool VEC>
+__global__ __launch_bounds__(256) void im2col_row_kernel(const float* __restrict__ x, float* __restrict__ cols,
+                                                         int CI, int H, int W, int KH, int KW, int OH, int OW, int SH,
+                                                         int SW, int PH, int PW, FastDiv div_k, FastDiv div_khkw,
+                                                         FastDiv div_kw, FastDiv div_wp, FastDiv div_oh) {
+    extern __shared__ float band[];  // CI * KH * (W + 2 PW) floats
+    int oh;
+    const int n = div_oh.divmod(blockIdx.x, oh);
+    const int WP = W + 2 * PW;
+    const int entries = CI * KH * WP;
+    const float* image = x + static_cast<long long>(n) * CI * H * W;
+    for (int e = threadIdx.x; e < entries; e += 256) {
+        int col;
+        const int r = div_wp.divmod(e, col);  // r = ci * KH + kh
+        int kh;
+        const int ci = r / KH;
+        kh = r - ci * KH;
+        const int ih = oh * SH - PH + kh, iw = col - PW;
+        band[e] = (ih >= 0 && ih < H && iw >= 0 && iw < W) ? image[(ci * H + ih) * W + iw] : 0.0f;
+    }
+    __syncthreads();
+    const int K = CI * KH * KW;
+    const int count = OW * K;
+    float* out = cols + (static_cast<long long>(n) * OH + oh) * OW * K;
+    auto value = [&](int j) {
+        int f;
+        const int ow = div_k.divmod(j, f);
+        int tap;
+        const int ci = div_khkw.divmod(f, tap);
+        int kw;
+        const int kh = div_kw.divmod(tap, kw);
+        return band[(ci * KH + kh) * WP + ow * SW + kw];
+    };
+    if constexpr (VEC) {
+        for (int j = threadIdx.x * 4; j < count; j += 256 * 4)
+            *reinterpret_cast<float4*>(out + j) = make_float4(value(j), value(j + 1), value(j + 2), value(j + 3));
+    } else {
+        for (int j = threadIdx.x; j < count; j += 256) out[j] = value(j);
+    }
+}
+
+// Max-pool forward over `per` consecutive (n, c) planes per workgroup, each staged whole in LDS with
+// coalesced reads; the window rule is pool_forward_kernel's.
+__global__ __launch_bounds__(256) void pool_forward_plane_kernel(const float* __restrict__ x, float* __restrict__ y,
+                                                                 int* __restrict__ argmax, int planes, int per, int H,
+                                                                 int W, int OH, int OW, int KH, int KW, int SH, int SW,
+                                                                 FastDiv div_ohw, FastDiv div_ow, int vec) {
+    extern __shared__ float tile[];  // per * H * W floats
+    const int first_plane = blockIdx.x * per;
+    const int count = min(per, planes - first_plane);
+    const int hw = H * W, ohw = OH * OW;
+    const long long base = static_cast<long long>(first_plane) * hw;
+    const int elems = count * hw;
+    if (vec) {  // x is 16-byte aligned and H*W % 4 == 0: every plane starts aligned, copy in float4s
+        const float4* src = reinterpret_cast<const float4*>(x + base);
+        for (int q = threadIdx.x; q < elems / 4; q += 256) reinterpret_cast<float4*>(tile)[q] = src[q];
+    } else {
+        for (int e = threadIdx.x; e < elems; e += 256) tile[e] = x[base + e];
+    }
+    __syncthreads();
+    for (int o = threadIdx.x; o < count * ohw; o += 256) {
+        int within, ow;
+        const int pl = div_ohw.divmod(o, within);
+        const int oh = div_ow.divmod(within, ow);
+        const int first = pl * hw + oh * SH * W + ow * SW;  // LDS index of the window's first element
+        int best = first;
+        float value = tile[first];
+        for (int kh = 0; kh < KH; ++kh)
+            for (int kw = 0; kw < KW; ++kw) {
+                const float v = tile[first + kh * W + kw];
+                if (v > value || v != v) {
+                    value = v;
+                    best = first + kh * W + kw;
+                }
+            }
+        const long long out = static_cast<long long>(first_plane) * ohw + o;
+        y[out] = value;
+        argmax[out] = static_cast<int>(base + best);
+    }
+}
+
+// Max-pool backward over `per` consecutive planes per workgroup: the planes' dy and argmax are
+// staged in LDS, then every input pixel gathers the windows that cover it, in (oh, ow) order.
+__global__ __launch_bounds__(256) void pool_backward_plane_kernel(const float* __restrict__ dy,
+                                                                  const int* __restrict__ argmax,
+                                                                  float* __restrict__ dx, int planes, int per, int H,
+                                                                  int W, int OH, int OW, int KH, int KW,
+                                                                  FastDiv div_hw, FastDiv div_w, FastDiv div_sh,
+                                                                  FastDiv div_sw) {
+    extern __shared__ float staged[];  // per * OH * OW floats of dy, then as many int32 argmax
+    const int first_plane = blockIdx.x * per;
+    const int count = min(per, planes - first_plane);
+    const int hw = H * W, ohw = OH * OW;
+    float* grad = staged;
+    int* where = reinterpret_cast<int*>(staged + per * ohw);
+    const long long out_base = static_cast<long long>(first_plane) * ohw;
+    for (int o = threadIdx.x; o < count * ohw; o += 256) {
+        grad[o] = dy[out_base + o];
+        where[o] = argmax[out_base + o];
+    }
+    __syncthreads();
+    const long long in_base = static_cast<long long>(first_plane) * hw;
+    for (int e = threadIdx.x; e < count * hw; e += 256) {
+        int within, iw;
+        const int pl = div_hw.divmod(e, within);
+        const int ih = div_w.divmod(within, iw);
+        const int oh_lo = ih >= KH ? div_sh.div(ih - KH) + 1 : 0;
+        const int oh_hi = min(OH - 1, div_sh.div(ih));
+        const int ow_lo = iw >= KW ? div_sw.div(iw - KW) + 1 : 0;
+        const int ow_hi = min(OW - 1, div_sw.div(iw));
+        const int target = static_cast<int>(in_base + e);
+        float sum = 0.0f;
+        for (int oh = oh_lo; oh <= oh_hi; ++oh)
+            for (int ow = ow_lo; ow <= ow_hi; ++ow) {
+                const int o = pl * ohw + oh * OW + ow;
+                if (where[o] == target) sum += grad[o];
+            }
+        dx[in_base + e] = sum;
+    }
+}
+
 }  // namespace
 
 int launch_im2col(const float* x, float* cols, const ConvGeometry& g, hipStream_t stream) {
     const int K = g.features();
     const int total = g.rows() * K;
+    const int band = g.CI * g.KH * (g.W + 2 * g.PW);
+    if (band <= ROW_FLOATS && static_cast<long long>(g.N) * g.OH <= INDEX_LIMIT) {
+        const bool vec = K % 4 == 0 && (reinterpret_cast<std::uintptr_t>(cols) & 15) == 0;
+        const unsigned blocks = static_cast<unsigned>(g.N * g.OH);
+        const FastDiv dk(K), dkk(g.KH * g.KW), dkw(g.KW), dwp(g.W + 2 * g.PW), doh(g.OH);
+        const size_t lds = static_cast<size_t>(band) * sizeof(float);
+        if (vec)
+            im2col_row_kernel<true><<<blocks, 256, lds, stream>>>(x, cols, g.CI, g.H, g.W, g.KH, g.KW, g.OH, g.OW, g.SH,
+                                                                  g.SW, g.PH, g.PW, dk, dkk, dkw, dwp, doh);
+        else
+            im2col_row_kernel<false><<<blocks, 256, lds, stream>>>(x, cols, g.CI, g.H, g.W, g.KH, g.KW, g.OH, g.OW,
+                                                                   g.SH, g.SW, g.PH, g.PW, dk, dkk, dkw, dwp, doh);
+        return MFH_CHECK_LAUNCH("im2col_row", stream);
+    }
     if (K % 4 == 0 && (reinterpret_cast<std::uintptr_t>(cols) & 15) == 0) {
         const int quads = total / 4;
         im2col_vec4_kernel<<<blocks_for(quads, 256), 256, 0, stream>>>(
@@ -299,7 +444,8 @@ int launch_col2im_t(const float* gcT, float* dx, const ConvGeometry& g, bool per
     const long long n_stride = per_image ? ohw * g.features() : ohw;
     col2im_t_kernel<<<blocks_for(total, 256), 256, 0, stream>>>(gcT, dx, total, FastDiv(g.W), FastDiv(g.H),
                                                                   FastDiv(g.CI), g.CI, g.KH, g.KW, g.OH, g.OW, g.SH,
-                                                                  g.SW, g.PH, g.PW, f_stride, n_stride);
+                                                                  g.SW, FastDiv(g.SH), FastDiv(g.SW), g.PH, g.PW,
+                                                                  f_stride, n_stride);
     return MFH_CHECK_LAUNCH("col2im_t", stream);
 }
 
@@ -330,9 +476,25 @@ int launch_add_bias(float* rows, const float* bias, int M, int N, hipStream_t st
     return MFH_CHECK_LAUNCH("add_bias", stream);
 }
 
+// Planes per workgroup for the LDS pooling kernels: about 2048 elements of work each, within the
+// LDS plane buffer; 0 when one plane does not fit.
+int pool_planes_per_block(int plane_floats, int capacity) {
+    if (plane_floats > capacity) return 0;
+    return std::max(1, std::min(2048 / plane_floats, capacity / plane_floats));
+}
+
 int launch_pool_forward(const float* x, float* y, int* argmax, int N, int C, int H, int W, int OH, int OW, int KH,
                         int KW, int SH, int SW, hipStream_t stream) {
     const int total = N * C * OH * OW;
+    const int per = pool_planes_per_block(H * W, PLANE_FLOATS);
+    if (per > 0) {
+        const int planes = N * C;
+        const size_t lds = static_cast<size_t>(per) * H * W * sizeof(float);
+        pool_forward_plane_kernel<<<blocks_for(planes, per), 256, lds, stream>>>(
+            x, y, argmax, planes, per, H, W, OH, OW, KH, KW, SH, SW, FastDiv(OH * OW), FastDiv(OW),
+            (H * W) % 4 == 0 && (reinterpret_cast<std::uintptr_t>(x) & 15) == 0 ? 1 : 0);
+        return MFH_CHECK_LAUNCH("pool_forward_plane", stream);
+    }
     pool_forward_kernel<<<blocks_for(total, 256), 256, 0, stream>>>(x, y, argmax, total, FastDiv(OW), FastDiv(OH), H,
                                                                       W, KH, KW, SH, SW);
     return MFH_CHECK_LAUNCH("pool_forward", stream);
@@ -341,8 +503,17 @@ int launch_pool_forward(const float* x, float* y, int* argmax, int N, int C, int
 int launch_pool_backward(const float* dy, const int* argmax, float* dx, int N, int C, int H, int W, int OH, int OW,
                          int KH, int KW, int SH, int SW, hipStream_t stream) {
     const int total = N * C * H * W;
+    const int per = std::min(pool_planes_per_block(OH * OW, PLANE_FLOATS / 2),
+                             pool_planes_per_block(H * W, 1 << 30));
+    if (per > 0) {
+        const int planes = N * C;
+        const size_t lds = static_cast<size_t>(per) * OH * OW * 2 * sizeof(float);
+        pool_backward_plane_kernel<<<blocks_for(planes, per), 256, lds, stream>>>(
+            dy, argmax, dx, planes, per, H, W, OH, OW, KH, KW, FastDiv(H * W), FastDiv(W), FastDiv(SH), FastDiv(SW));
+        return MFH_CHECK_LAUNCH("pool_backward_plane", stream);
+    }
     pool_backward_kernel<<<blocks_for(total, 256), 256, 0, stream>>>(dy, argmax, dx, total, FastDiv(W), FastDiv(H),
-                                                                       OH, OW, KH, KW, SH, SW);
+                                                                       OH, OW, KH, KW, FastDiv(SH), FastDiv(SW));
     return MFH_CHECK_LAUNCH("pool_backward", stream);
 }
 

@@ -325,14 +325,22 @@ __global__ __launch_bounds__(256) void weight_order_kernel(const float* __restri
 }
 
 // partial[row] = sum of the row's `length` floats in FP64 (rows are the (n, co) planes of dy). One
-// wave per row: lane l adds elements l, l + 64, ... in order, then a fixed butterfly adds the lanes.
+// wave per row: lane l runs four chains over elements l + 64 (4 t + u), u = 0..3 (four loads in
+// flight), adds the chains in order, then a fixed butterfly adds the lanes.
 __global__ __launch_bounds__(256) void row_sums_kernel(const float* __restrict__ src, double* __restrict__ partial,
                                                        int rows, int length) {
     const int row = blockIdx.x * 4 + threadIdx.x / 64, lane = threadIdx.x % 64;
     if (row >= rows) return;
     const float* r = src + static_cast<long long>(row) * length;
-    double s = 0.0;
-    for (int i = lane; i < length; i += 64) s += static_cast<double>(r[i]);
+    double chain[4] = {0.0, 0.0, 0.0, 0.0};
+    for (int i = lane; i < length; i += 256) {
+        float v[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) v[u] = i + 64 * u < length ? r[i + 64 * u] : 0.0f;
+#pragma unroll
+        for (int u = 0; u < 4; ++u) chain[u] += static_cast<double>(v[u]);
+    }
+    double s = (chain[0] + chain[1]) + (chain[2] + chain[3]);
 #pragma unroll
     for (int offset = 32; offset > 0; offset >>= 1) s += __shfl_xor(s, offset, 64);
     if (lane == 0) partial[row] = s;
@@ -434,11 +442,14 @@ ConvGather gather_of(const float* src, int C, int H, int W, int KH, int KW, int 
 // last, partial round costs a whole one). A split over K adds its partials' HBM round trip and the
 // reduction launch. The constants are fitted to a sweep of every tile and split on MI355X over
 // ResNet18's batch-64 convolutions (forward, dW and dX).
-constexpr double FORWARD_EFFICIENCY[TILE_COUNT] = {0.49, 0.53, 0.54, 0.43, 0.32, 0.49, 0.56, 0.42};
-constexpr double WGRAD_EFFICIENCY[TILE_COUNT] = {0.76, 0.66, 0.50, 0.82, 0.34, 0.75, 0.69, 0.47};
+struct PlannerModel {
+    double efficiency[TILE_COUNT];
+    double hbm_bytes_per_s;  // achieved rate of the split-K partial traffic
+    double launch_s;         // cost of the extra reduction launch
+};
+constexpr PlannerModel FORWARD_MODEL = {{0.49, 0.53, 0.54, 0.43, 0.32, 0.49, 0.56, 0.42}, 6.0e12, 2.0e-6};
+constexpr PlannerModel WGRAD_MODEL = {{0.57, 0.37, 0.49, 0.72, 0.56, 0.34, 0.55, 0.32}, 3.0e12, 2.0e-6};
 constexpr double SIMD_MACS_PER_S = 157.3e12 / 2 / 1024;  // FP32 multiply-adds per second per SIMD
-constexpr double HBM_BYTES_PER_S = 6.0e12;               // achieved rate of the split-K partial traffic
-constexpr double LAUNCH_S = 3.0e-6;
 constexpr int SPLIT_CHOICES[] = {1, 2, 3, 4, 6, 8, 12, 16, 24, 32, 48, 64, 96, 128};
 
 double implicit_cost(bool wgrad, int tile, int M, int N, int slices, int chunk) {
@@ -448,9 +459,9 @@ double implicit_cost(bool wgrad, int tile, int M, int N, int slices, int chunk) 
     const int simds = 4 * std::max(1, device_cu_count());
     const std::int64_t rounds = (tiles * slices * waves + simds - 1) / simds;
     const double wave_macs = static_cast<double>(t.wm) * t.wn * chunk;
-    const double efficiency = wgrad ? WGRAD_EFFICIENCY[tile] : FORWARD_EFFICIENCY[tile];
-    double cost = rounds * wave_macs / (SIMD_MACS_PER_S * efficiency);
-    if (slices > 1) cost += 4.0 * (2.0 * slices + 1.0) * M * N / HBM_BYTES_PER_S + LAUNCH_S;
+    const PlannerModel& model = wgrad ? WGRAD_MODEL : FORWARD_MODEL;
+    double cost = rounds * wave_macs / (SIMD_MACS_PER_S * model.efficiency[tile]);
+    if (slices > 1) cost += 4.0 * (2.0 * slices + 1.0) * M * N / model.hbm_bytes_per_s + model.launch_s;
     return cost;
 }
 

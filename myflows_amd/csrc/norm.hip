@@ -1,27 +1,35 @@
 // Batch normalisation of an NCHW tensor over the N*H*W positions of each channel, forward and
 // backward, with an optional residual add and ReLU fused into the same passes.
 //
-// Forward (training): three launches.
+// Forward (training): two launches.
 //   1. norm_partials<STATS>: workgroup (s, c) sums d = x - x[n=0, c, 0] and d*d over slice s of
 //      channel c in FP64 (the shift keeps the one-pass variance from cancelling);
-//   2. norm_stats_finalize: per channel, adds the slices in slice order, forms the FP64 mean and
-//      biased variance, stores the mean as the unevaluated float pair hi + lo (about 48 bits), the
-//      inverse standard deviation rounded once, and updates the running statistics;
-//   3. norm_apply: y = (((x - hi) - lo) * inv_std) * gamma + beta [+ residual] [ReLU], each
-//      operation rounded to float32 in that order (no contraction), as the NumPy path computes it.
+//   2. norm_apply: every workgroup first finalises the channels its elements belong to (adds the
+//      slices in slice order, forms the FP64 mean and biased variance, the mean as the unevaluated
+//      float pair hi + lo (about 48 bits) and the inverse standard deviation rounded once), then
+//      y = (((x - hi) - lo) * inv_std) * gamma + beta [+ residual] [ReLU], each operation rounded to
+//      float32 in that order (no contraction), as the NumPy path computes it. The workgroup that
+//      holds the first element of image 0 of a channel also stores that channel's mean / inv_std
+//      and updates its running statistics, so each is written exactly once.
 // Backward: norm_partials<GRADS> sums g and g * (x - mean) in FP64 (g = dy, or dy gated by the
-// fused ReLU's output, also written to the residual gradient), norm_grad_finalize forms dgamma,
-// dbeta and the coefficients of dx = a * ((g - k1) - ((x - hi) - lo) * k2), and norm_dx applies them.
-// Every sum has a fixed order (lanes, then waves, then slices), so results are reproducible.
+// fused ReLU's output, also written to the residual gradient); norm_dx finalises the channels it
+// touches (dgamma, dbeta and the coefficients of dx = a * ((g - k1) - ((x - hi) - lo) * k2)) and
+// applies them. Every sum has a fixed order (four interleaved chains per thread, then lanes, waves
+// and slices), so results are reproducible; every workgroup finalises a channel with the same
+// arithmetic, so they all agree.
 #include "common.h"
 #include "fastdiv.h"
 
 namespace mfh {
 namespace {
 
-constexpr int PT = 256;              // threads per partial-sum workgroup
-constexpr int MIN_SLICE = 2048;      // fewest positions a slice covers
+constexpr int PT = 256;           // threads per partial-sum workgroup
+constexpr int CHAINS = 4;         // independent load / add chains per thread in the partial sums
+constexpr int MIN_SLICE = 2048;   // fewest positions a slice covers
 constexpr int APPLY_THREADS = 256;
+constexpr int APPLY_ELEMS = 4;    // elements per thread in norm_apply / norm_dx
+constexpr int APPLY_SPAN = APPLY_THREADS * APPLY_ELEMS;
+constexpr int MAX_PLANES = 128;   // (n, c) planes a workgroup finalises at once; more are taken in rounds
 
 enum PartialMode { STATS = 0, GRADS = 1 };
 
@@ -63,6 +71,9 @@ __device__ __forceinline__ void workgroup_sum(double& a, double& b) {
     }
 }
 
+// Workgroup (s, c) sums slice s of channel c. Each thread runs CHAINS interleaved chains (positions
+// j, j + PT, j + 2 PT, j + 3 PT, then the next 4 PT), so CHAINS loads are in flight at a time; the
+// chains are added in chain order at the end.
 template <int MODE>
 __global__ __launch_bounds__(PT) void norm_partials_kernel(PartialArgs p) {
     const int s = blockIdx.x, c = blockIdx.y, slices = gridDim.x;
@@ -71,129 +82,251 @@ __global__ __launch_bounds__(PT) void norm_partials_kernel(PartialArgs p) {
     // STATS: shift by the channel's first element; GRADS: centre on the saved FP64 mean (hi + lo).
     const double centre = MODE == STATS ? static_cast<double>(p.x[c * p.HW])
                                         : static_cast<double>(p.mean[c]) + static_cast<double>(p.mean[p.C + c]);
-    double a = 0.0, b = 0.0;
-    for (int j = j0 + threadIdx.x; j < j1; j += PT) {
-        int hw;
-        const int n = p.div_hw.divmod(j, hw);
-        const int at = n * plane + c * p.HW + hw;
-        const double d = static_cast<double>(p.x[at]) - centre;
-        if constexpr (MODE == STATS) {
-            a += d;
-            b = fma(d, d, b);
-        } else {
-            const float g = p.gate && !(p.gate[at] > 0.0f) ? 0.0f : p.dy[at];
-            if (p.residual_grad) p.residual_grad[at] = p.add_residual ? p.residual_grad[at] + g : g;
-            a += static_cast<double>(g);
-            b = fma(static_cast<double>(g), d, b);
+    double a[CHAINS] = {}, b[CHAINS] = {};
+    for (int base = j0 + threadIdx.x; base < j1; base += CHAINS * PT) {
+        float xv[CHAINS], gv[CHAINS];
+        int at[CHAINS];
+#pragma unroll
+        for (int u = 0; u < CHAINS; ++u) {
+            const int j = base + u * PT;
+            int hw;
+            const int n = p.div_hw.divmod(j < j1 ? j : j0, hw);
+            at[u] = n * plane + c * p.HW + hw;
+            xv[u] = j < j1 ? p.x[at[u]] : 0.0f;
+            if constexpr (MODE == GRADS) {
+                float g = 0.0f;
+                if (j < j1) g = p.gate && !(p.gate[at[u]] > 0.0f) ? 0.0f : p.dy[at[u]];
+                gv[u] = g;
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < CHAINS; ++u) {
+            if (base + u * PT >= j1) continue;
+            const double d = static_cast<double>(xv[u]) - centre;
+            if constexpr (MODE == STATS) {
+                a[u] += d;
+                b[u] = fma(d, d, b[u]);
+            } else {
+                if (p.residual_grad)
+                    p.residual_grad[at[u]] = p.add_residual ? p.residual_grad[at[u]] + gv[u] : gv[u];
+                a[u] += static_cast<double>(gv[u]);
+                b[u] = fma(static_cast<double>(gv[u]), d, b[u]);
+            }
         }
     }
-    workgroup_sum(a, b);
+    double sa = a[0], sb = b[0];
+#pragma unroll
+    for (int u = 1; u < CHAINS; ++u) {
+        sa += a[u];
+        sb += b[u];
+    }
+    workgroup_sum(sa, sb);
     if (threadIdx.x == 0) {
-        p.partial[(static_cast<long long>(c) * slices + s) * 2] = a;
-        p.partial[(static_cast<long long>(c) * slices + s) * 2 + 1] = b;
+        p.partial[(static_cast<long long>(c) * slices + s) * 2] = sa;
+        p.partial[(static_cast<long long>(c) * slices + s) * 2 + 1] = sb;
     }
 }
 
-__global__ __launch_bounds__(128) void norm_stats_finalize_kernel(const double* __restrict__ partial,
-                                                                  const float* __restrict__ x, float* mean,
-                                                                  float* inv_std, float* running_mean,
-                                                                  float* running_var, int C, int HW, int slices,
-                                                                  double count, double momentum, double eps,
-                                                                  double var_scale, int training) {
-    const int c = blockIdx.x * 128 + threadIdx.x;
-    if (c >= C) return;
-    double mu, var;
-    if (training) {
-        double sum = 0.0, sq = 0.0;
-        for (int s = 0; s < slices; ++s) {
-            sum += partial[(static_cast<long long>(c) * slices + s) * 2];
-            sq += partial[(static_cast<long long>(c) * slices + s) * 2 + 1];
-        }
-        const double shifted = sum / count;
-        var = fmax(sq / count - shifted * shifted, 0.0);
-        mu = static_cast<double>(x[c * HW]) + shifted;
-        running_mean[c] = static_cast<float>((1.0 - momentum) * static_cast<double>(running_mean[c]) + momentum * mu);
-        running_var[c] =
-            static_cast<float>((1.0 - momentum) * static_cast<double>(running_var[c]) + momentum * var * var_scale);
-    } else {
-        mu = static_cast<double>(running_mean[c]);
-        var = static_cast<double>(running_var[c]);
-    }
-    const float hi = static_cast<float>(mu);
-    mean[c] = hi;
-    mean[C + c] = static_cast<float>(mu - static_cast<double>(hi));
-    inv_std[c] = static_cast<float>(1.0 / sqrt(var + eps));
-}
-
-__global__ __launch_bounds__(128) void norm_grad_finalize_kernel(const double* __restrict__ partial,
-                                                                 const float* __restrict__ gamma,
-                                                                 const float* __restrict__ inv_std, float* gamma_grad,
-                                                                 float* beta_grad, float* coef, int C, int slices,
-                                                                 double count, int training, int add_gamma,
-                                                                 int add_beta) {
-    const int c = blockIdx.x * 128 + threadIdx.x;
-    if (c >= C) return;
-    double sdy = 0.0, sdyx = 0.0;
+// Sum of channel c's slice partials in slice order.
+__device__ __forceinline__ void slice_sums(const double* __restrict__ partial, int c, int slices, double& a,
+                                           double& b) {
+    a = 0.0;
+    b = 0.0;
     for (int s = 0; s < slices; ++s) {
-        sdy += partial[(static_cast<long long>(c) * slices + s) * 2];
-        sdyx += partial[(static_cast<long long>(c) * slices + s) * 2 + 1];
+        a += partial[(static_cast<long long>(c) * slices + s) * 2];
+        b += partial[(static_cast<long long>(c) * slices + s) * 2 + 1];
     }
-    const double istd = static_cast<double>(inv_std[c]);
-    const double dgamma = istd * sdyx;
-    if (gamma_grad) gamma_grad[c] = add_gamma ? gamma_grad[c] + static_cast<float>(dgamma) : static_cast<float>(dgamma);
-    if (beta_grad) beta_grad[c] = add_beta ? beta_grad[c] + static_cast<float>(sdy) : static_cast<float>(sdy);
-    coef[c] = static_cast<float>(static_cast<double>(gamma[c]) * istd);
-    coef[C + c] = training ? static_cast<float>(sdy / count) : 0.0f;
-    coef[2 * C + c] = training ? static_cast<float>(istd * dgamma / count) : 0.0f;
 }
 
-// Channel of flat NCHW element e: (e / HW) % C.
-struct ChannelOf {
+struct ApplyArgs {
+    const float* x;
+    const float* gamma;
+    const float* beta;
+    const float* residual;
+    float* y;
+    float* mean;     // 2 x C (hi, lo), written by the first-element workgroups
+    float* inv_std;  // C
+    float* running_mean;
+    float* running_var;
+    const double* partial;
+    int total, C, HW, slices, training, relu;
+    double count, momentum, eps, var_scale;
     FastDiv div_hw, div_c;
-    __device__ __forceinline__ int operator()(int e) const {
-        int c;
-        div_c.divmod(div_hw.div(e), c);
-        return c;
-    }
 };
 
-__global__ __launch_bounds__(APPLY_THREADS) void norm_apply_kernel(const float* __restrict__ x,
-                                                                   const float* __restrict__ mean,
-                                                                   const float* __restrict__ inv_std,
-                                                                   const float* __restrict__ gamma,
-                                                                   const float* __restrict__ beta,
-                                                                   const float* __restrict__ residual,
-                                                                   float* __restrict__ y, int total, int C,
-                                                                   ChannelOf channel_of, int relu) {
-#pragma clang fp contract(off)
-    const int e = blockIdx.x * APPLY_THREADS + threadIdx.x;
-    if (e >= total) return;
-    const int c = channel_of(e);
-    float v = (((x[e] - mean[c]) - mean[C + c]) * inv_std[c]) * gamma[c] + beta[c];
-    if (residual) v = v + residual[e];
-    if (relu) v = v < 0.0f ? 0.0f : v;  // NaN stays NaN
-    y[e] = v;
+struct DxArgs {
+    const float* x;
+    const float* dy;
+    const float* gate;
+    const float* gamma;
+    const float* mean;
+    const float* inv_std;
+    float* dx;
+    float* gamma_grad;
+    float* beta_grad;
+    const double* partial;
+    int total, C, HW, slices, training, add, add_gamma, add_beta, sums;
+    double count;
+    FastDiv div_hw, div_c;
+};
+
+// The planes [p0, p1] that elements [e0, e0 + APPLY_SPAN) of a workgroup touch; plane pl is
+// (n, c) = (pl / C, pl % C). A plane's first element lies in exactly one workgroup.
+__device__ __forceinline__ void planes_of(int e0, int total, const FastDiv& div_hw, int& p0, int& p1) {
+    p0 = div_hw.div(e0);
+    p1 = div_hw.div(min(total, e0 + APPLY_SPAN) - 1);
 }
 
-__global__ __launch_bounds__(APPLY_THREADS) void norm_dx_kernel(const float* __restrict__ x,
-                                                                const float* __restrict__ dy,
-                                                                const float* __restrict__ gate,
-                                                                const float* __restrict__ mean,
-                                                                const float* __restrict__ coef, float* dx, int total,
-                                                                int C, ChannelOf channel_of, int training, int add) {
+// norm_apply with the statistics finalised in the workgroup: coefficients (hi, lo, inv_std, gamma,
+// beta) of the planes it touches go to LDS, then every element is normalised.
+template <int VEC>
+__global__ __launch_bounds__(APPLY_THREADS) void norm_apply_kernel(ApplyArgs p) {
 #pragma clang fp contract(off)
-    const int e = blockIdx.x * APPLY_THREADS + threadIdx.x;
-    if (e >= total) return;
-    const int c = channel_of(e);
-    const float g = gate && !(gate[e] > 0.0f) ? 0.0f : dy[e];
-    const float a = coef[c];
-    float v;
-    if (training) v = a * ((g - coef[C + c]) - ((x[e] - mean[c]) - mean[C + c]) * coef[2 * C + c]);
-    else v = a * g;
-    dx[e] = add ? dx[e] + v : v;
+    __shared__ float coef[5][MAX_PLANES];
+    const int e0 = blockIdx.x * APPLY_SPAN;
+    int p0, p1;
+    planes_of(e0, p.total, p.div_hw, p0, p1);
+    for (int first = p0; first <= p1; first += MAX_PLANES) {
+        const int last = min(p1, first + MAX_PLANES - 1);
+        for (int i = threadIdx.x; i <= last - first; i += APPLY_THREADS) {
+            const int pl = first + i;
+            int c;
+            p.div_c.divmod(pl, c);
+            double mu, var;
+            if (p.training) {
+                double sum, sq;
+                slice_sums(p.partial, c, p.slices, sum, sq);
+                const double shifted = sum / p.count;
+                var = fmax(sq / p.count - shifted * shifted, 0.0);
+                mu = static_cast<double>(p.x[c * p.HW]) + shifted;
+            } else {
+                mu = static_cast<double>(p.running_mean[c]);
+                var = static_cast<double>(p.running_var[c]);
+            }
+            const float hi = static_cast<float>(mu);
+            const float lo = static_cast<float>(mu - static_cast<double>(hi));
+            const float istd = static_cast<float>(1.0 / sqrt(var + p.eps));
+            coef[0][i] = hi;
+            coef[1][i] = lo;
+            coef[2][i] = istd;
+            coef[3][i] = p.gamma[c];
+            coef[4][i] = p.beta[c];
+            if (pl < p.C && static_cast<long long>(pl) * p.HW >= e0) {  // image 0's plane of channel c starts here
+                p.mean[c] = hi;
+                p.mean[p.C + c] = lo;
+                p.inv_std[c] = istd;
+                if (p.training) {
+                    p.running_mean[c] = static_cast<float>((1.0 - p.momentum) * static_cast<double>(p.running_mean[c]) +
+                                                           p.momentum * mu);
+                    p.running_var[c] = static_cast<float>((1.0 - p.momentum) * static_cast<double>(p.running_var[c]) +
+                                                          p.momentum * var * p.var_scale);
+                }
+            }
+        }
+        __syncthreads();
+        const int lo_e = max(e0, first * p.HW), hi_e = min(min(p.total, e0 + APPLY_SPAN), (last + 1) * p.HW);
+        for (int e = lo_e + threadIdx.x * VEC; e < hi_e; e += APPLY_THREADS * VEC) {
+            const int i = p.div_hw.div(e) - first;  // all VEC elements share a plane (HW % VEC == 0)
+            const float m_hi = coef[0][i], m_lo = coef[1][i], istd = coef[2][i], g = coef[3][i], b = coef[4][i];
+            float xv[VEC], rv[VEC], out[VEC];
+            if constexpr (VEC == 4) {
+                const float4 x4 = *reinterpret_cast<const float4*>(p.x + e);
+                xv[0] = x4.x; xv[1] = x4.y; xv[2] = x4.z; xv[3] = x4.w;
+                if (p.residual) {
+                    const float4 r4 = *reinterpret_cast<const float4*>(p.residual + e);
+                    rv[0] = r4.x; rv[1] = r4.y; rv[2] = r4.z; rv[3] = r4.w;
+                }
+            } else {
+                xv[0] = p.x[e];
+                if (p.residual) rv[0] = p.residual[e];
+            }
+#pragma unroll
+            for (int u = 0; u < VEC; ++u) {
+                float v = (((xv[u] - m_hi) - m_lo) * istd) * g + b;
+                if (p.residual) v = v + rv[u];
+                if (p.relu) v = v < 0.0f ? 0.0f : v;  // NaN stays NaN
+                out[u] = v;
+            }
+            if constexpr (VEC == 4) *reinterpret_cast<float4*>(p.y + e) = make_float4(out[0], out[1], out[2], out[3]);
+            else p.y[e] = out[0];
+        }
+        __syncthreads();
+    }
 }
 
-ChannelOf channel_of(const NormShape& s) { return ChannelOf{FastDiv(s.HW), FastDiv(s.C)}; }
+// norm_dx with dgamma / dbeta and the dx coefficients finalised in the workgroup.
+template <int VEC>
+__global__ __launch_bounds__(APPLY_THREADS) void norm_dx_kernel(DxArgs p) {
+#pragma clang fp contract(off)
+    __shared__ float coef[5][MAX_PLANES];
+    const int e0 = blockIdx.x * APPLY_SPAN;
+    int p0, p1;
+    planes_of(e0, p.total, p.div_hw, p0, p1);
+    for (int first = p0; first <= p1; first += MAX_PLANES) {
+        const int last = min(p1, first + MAX_PLANES - 1);
+        for (int i = threadIdx.x; i <= last - first; i += APPLY_THREADS) {
+            const int pl = first + i;
+            int c;
+            p.div_c.divmod(pl, c);
+            double sdy = 0.0, sdyx = 0.0;
+            if (p.sums) slice_sums(p.partial, c, p.slices, sdy, sdyx);
+            const double istd = static_cast<double>(p.inv_std[c]);
+            const double dgamma = istd * sdyx;
+            coef[0][i] = static_cast<float>(static_cast<double>(p.gamma[c]) * istd);
+            coef[1][i] = p.training ? static_cast<float>(sdy / p.count) : 0.0f;
+            coef[2][i] = p.training ? static_cast<float>(istd * dgamma / p.count) : 0.0f;
+            coef[3][i] = p.mean[c];
+            coef[4][i] = p.mean[p.C + c];
+            if (pl < p.C && static_cast<long long>(pl) * p.HW >= e0) {
+                if (p.gamma_grad)
+                    p.gamma_grad[c] = p.add_gamma ? p.gamma_grad[c] + static_cast<float>(dgamma) : static_cast<float>(dgamma);
+                if (p.beta_grad)
+                    p.beta_grad[c] = p.add_beta ? p.beta_grad[c] + static_cast<float>(sdy) : static_cast<float>(sdy);
+            }
+        }
+        __syncthreads();
+        if (p.dx) {
+            const int lo_e = max(e0, first * p.HW), hi_e = min(min(p.total, e0 + APPLY_SPAN), (last + 1) * p.HW);
+            for (int e = lo_e + threadIdx.x * VEC; e < hi_e; e += APPLY_THREADS * VEC) {
+                const int i = p.div_hw.div(e) - first;
+                const float a = coef[0][i], k1 = coef[1][i], k2 = coef[2][i], m_hi = coef[3][i], m_lo = coef[4][i];
+                float xv[VEC], gv[VEC], tv[VEC], prev[VEC];
+                if constexpr (VEC == 4) {
+                    const float4 x4 = *reinterpret_cast<const float4*>(p.x + e);
+                    const float4 d4 = *reinterpret_cast<const float4*>(p.dy + e);
+                    xv[0] = x4.x; xv[1] = x4.y; xv[2] = x4.z; xv[3] = x4.w;
+                    gv[0] = d4.x; gv[1] = d4.y; gv[2] = d4.z; gv[3] = d4.w;
+                    if (p.gate) {
+                        const float4 t4 = *reinterpret_cast<const float4*>(p.gate + e);
+                        tv[0] = t4.x; tv[1] = t4.y; tv[2] = t4.z; tv[3] = t4.w;
+                    }
+                    if (p.add) {
+                        const float4 o4 = *reinterpret_cast<const float4*>(p.dx + e);
+                        prev[0] = o4.x; prev[1] = o4.y; prev[2] = o4.z; prev[3] = o4.w;
+                    }
+                } else {
+                    xv[0] = p.x[e];
+                    gv[0] = p.dy[e];
+                    if (p.gate) tv[0] = p.gate[e];
+                    if (p.add) prev[0] = p.dx[e];
+                }
+                float out[VEC];
+#pragma unroll
+                for (int u = 0; u < VEC; ++u) {
+                    const float g = p.gate && !(tv[u] > 0.0f) ? 0.0f : gv[u];
+                    float v;
+                    if (p.training) v = a * ((g - k1) - ((xv[u] - m_hi) - m_lo) * k2);
+                    else v = a * g;
+                    out[u] = p.add ? prev[u] + v : v;
+                }
+                if constexpr (VEC == 4)
+                    *reinterpret_cast<float4*>(p.dx + e) = make_float4(out[0], out[1], out[2], out[3]);
+                else p.dx[e] = out[0];
+            }
+        }
+        __syncthreads();
+    }
+}
 
 int run_partials(int mode, const NormShape& s, const PartialArgs& args, hipStream_t stream) {
     const dim3 grid(norm_slices(s), s.C);
@@ -201,6 +334,8 @@ int run_partials(int mode, const NormShape& s, const PartialArgs& args, hipStrea
     else norm_partials_kernel<GRADS><<<grid, PT, 0, stream>>>(args);
     return MFH_CHECK_LAUNCH(mode == STATS ? "norm_partials<stats>" : "norm_partials<grads>", stream);
 }
+
+bool aligned16(const void* q) { return (reinterpret_cast<std::uintptr_t>(q) & 15) == 0; }
 
 }  // namespace
 
@@ -212,8 +347,8 @@ int norm_slices(const NormShape& s) {
 }
 
 std::int64_t norm_workspace_doubles(const NormShape& s) {
-    // FP64 (sum, second sum) per slice and channel, then 3 * C floats of dx coefficients.
-    return 2LL * s.C * norm_slices(s) + (3LL * s.C + 1) / 2;
+    // FP64 (sum, second sum) per slice and channel.
+    return 2LL * s.C * norm_slices(s);
 }
 
 int norm_forward(const NormShape& s, const NormForward& f, hipStream_t stream) {
@@ -230,12 +365,33 @@ int norm_forward(const NormShape& s, const NormForward& f, hipStream_t stream) {
         args.div_hw = FastDiv(s.HW);
         MFH_TRY(run_partials(STATS, s, args, stream));
     }
-    norm_stats_finalize_kernel<<<blocks_for(s.C, 128), 128, 0, stream>>>(
-        f.partial, f.x, f.mean, f.inv_std, f.running_mean, f.running_var, s.C, s.HW, slices,
-        static_cast<double>(s.N) * s.HW, f.momentum, f.eps, f.var_scale, f.training ? 1 : 0);
-    MFH_TRY(MFH_CHECK_LAUNCH("norm_stats_finalize", stream));
-    norm_apply_kernel<<<blocks_for(total, APPLY_THREADS), APPLY_THREADS, 0, stream>>>(
-        f.x, f.mean, f.inv_std, f.gamma, f.beta, f.residual, f.y, total, s.C, channel_of(s), f.relu ? 1 : 0);
+    ApplyArgs a{};
+    a.x = f.x;
+    a.gamma = f.gamma;
+    a.beta = f.beta;
+    a.residual = f.residual;
+    a.y = f.y;
+    a.mean = f.mean;
+    a.inv_std = f.inv_std;
+    a.running_mean = f.running_mean;
+    a.running_var = f.running_var;
+    a.partial = f.partial;
+    a.total = total;
+    a.C = s.C;
+    a.HW = s.HW;
+    a.slices = slices;
+    a.training = f.training ? 1 : 0;
+    a.relu = f.relu ? 1 : 0;
+    a.count = static_cast<double>(s.N) * s.HW;
+    a.momentum = f.momentum;
+    a.eps = f.eps;
+    a.var_scale = f.var_scale;
+    a.div_hw = FastDiv(s.HW);
+    a.div_c = FastDiv(s.C);
+    const bool vec = s.HW % 4 == 0 && aligned16(f.x) && aligned16(f.y) && (!f.residual || aligned16(f.residual));
+    const unsigned blocks = blocks_for(total, APPLY_SPAN);
+    if (vec) norm_apply_kernel<4><<<blocks, APPLY_THREADS, 0, stream>>>(a);
+    else norm_apply_kernel<1><<<blocks, APPLY_THREADS, 0, stream>>>(a);
     return MFH_CHECK_LAUNCH("norm_apply", stream);
 }
 
@@ -260,14 +416,34 @@ int norm_backward(const NormShape& s, const NormBackward& b, hipStream_t stream)
         MFH_TRY(run_partials(GRADS, s, args, stream));
     }
     if (!b.x_grad && !sums) return OK;
-    norm_grad_finalize_kernel<<<blocks_for(s.C, 128), 128, 0, stream>>>(
-        b.partial, b.gamma, b.inv_std, b.gamma_grad, b.beta_grad, b.coef, s.C, sums ? slices : 0,
-        static_cast<double>(s.N) * s.HW, b.training ? 1 : 0, b.add_gamma ? 1 : 0, b.add_beta ? 1 : 0);
-    MFH_TRY(MFH_CHECK_LAUNCH("norm_grad_finalize", stream));
-    if (!b.x_grad) return OK;
-    norm_dx_kernel<<<blocks_for(total, APPLY_THREADS), APPLY_THREADS, 0, stream>>>(
-        b.x, b.dy, b.gate, b.mean, b.coef, b.x_grad, total, s.C, channel_of(s), b.training ? 1 : 0,
-        b.add_x ? 1 : 0);
+    DxArgs d{};
+    d.x = b.x;
+    d.dy = b.dy;
+    d.gate = b.gate;
+    d.gamma = b.gamma;
+    d.mean = b.mean;
+    d.inv_std = b.inv_std;
+    d.dx = b.x_grad;
+    d.gamma_grad = b.gamma_grad;
+    d.beta_grad = b.beta_grad;
+    d.partial = b.partial;
+    d.total = total;
+    d.C = s.C;
+    d.HW = s.HW;
+    d.slices = slices;
+    d.training = b.training ? 1 : 0;
+    d.add = b.add_x ? 1 : 0;
+    d.add_gamma = b.add_gamma ? 1 : 0;
+    d.add_beta = b.add_beta ? 1 : 0;
+    d.sums = sums ? 1 : 0;
+    d.count = static_cast<double>(s.N) * s.HW;
+    d.div_hw = FastDiv(s.HW);
+    d.div_c = FastDiv(s.C);
+    const bool vec = s.HW % 4 == 0 && aligned16(b.x) && aligned16(b.dy) && (!b.gate || aligned16(b.gate)) &&
+                     (!b.x_grad || aligned16(b.x_grad));
+    const unsigned blocks = blocks_for(total, APPLY_SPAN);
+    if (vec) norm_dx_kernel<4><<<blocks, APPLY_THREADS, 0, stream>>>(d);
+    else norm_dx_kernel<1><<<blocks, APPLY_THREADS, 0, stream>>>(d);
     return MFH_CHECK_LAUNCH("norm_dx", stream);
 }
 
