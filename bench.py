@@ -120,6 +120,75 @@ def gemm_roofline(m=4096, n=4096, k=4096, reps=20):
             "avg_launch_ms": round(ms, 4), "algorithmic_flop_per_launch": 2 * m * n * k}
 
 
+def _event_time_us(fn, reps=20, warmup=3):
+    """Average time of fn() in microseconds, from HIP events on the current stream."""
+    stream = torch.cuda.current_stream()
+    for _ in range(warmup):
+        fn()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    start.record(stream)
+    for _ in range(reps):
+        fn()
+    end.record(stream)
+    end.synchronize()
+    return start.elapsed_time(end) * 1e3 / reps
+
+
+def c3_kernels():
+    """BASELINE config 3 on its own: Conv2D 64->64 3x3/1/1 at N=32, 30x40, then MaxPool 2x2/2. The
+    bandwidth-bound kernels against the 8 TB/s HBM peak (algorithmic bytes: each required read or
+    write once), the convolution products against the FP32 matrix peak."""
+    lib = native._library()
+    stream = torch.cuda.current_stream().cuda_stream
+    n, ci, h, w, co = 32, 64, 30, 40, 64
+    g = torch.Generator().manual_seed(0)
+    x = torch.randn((n, ci, h, w), generator=g).cuda()
+    weight = (torch.randn((co, ci, 3, 3), generator=g) * (2.0 / (ci * 9)) ** 0.5).cuda()
+    dims = (n, ci, h, w, co, 3, 3, h, w, 1, 1, 1, 1)
+    m, k = n * h * w, ci * 9
+    cols = torch.empty((m, k), device="cuda")
+    y = torch.empty((n, co, h, w), device="cuda")
+    wt = torch.empty_like(weight)
+
+    def im2col():
+        native._raise_for(lib.mfh_conv_im2col(x.data_ptr(), cols.data_ptr(), *dims, stream), lib)
+
+    def conv_forward():
+        native._raise_for(lib.mfh_conv_forward_implicit(x.data_ptr(), weight.data_ptr(), wt.data_ptr(), 0,
+                                                        y.data_ptr(), *dims, 0, 0.0, 1, 0, 0, stream), lib)
+
+    pooled = torch.empty((n, co, h // 2, w // 2), device="cuda")
+    argmax = torch.empty((n, co, h // 2, w // 2), dtype=torch.int32, device="cuda")
+    dx = torch.empty_like(y)
+    pool_dims = (n, co, h, w, h // 2, w // 2, 2, 2, 2, 2)
+
+    def pool_forward():
+        native._raise_for(lib.mfh_pool_forward(y.data_ptr(), pooled.data_ptr(), argmax.data_ptr(), *pool_dims,
+                                               stream), lib)
+
+    def pool_backward():
+        native._raise_for(lib.mfh_pool_backward(pooled.data_ptr(), argmax.data_ptr(), dx.data_ptr(), *pool_dims,
+                                                stream), lib)
+
+    conv_forward()
+    pool_forward()
+    out = {"config": "Conv2D 64->64 3x3/1/1, N=32, 30x40; MaxPool 2x2/2", "peak_GB/s": HBM_PEAK_GBS,
+           "peak_TFLOP/s": FP32_MFMA_PEAK_TFLOPS}
+    bytes_im2col = 4 * (n * ci * h * w + m * k)
+    bytes_pool = 4 * n * co * h * w + 8 * n * co * (h // 2) * (w // 2)
+    for name, fn, nbytes in (("im2col", im2col, bytes_im2col), ("pool_forward", pool_forward, bytes_pool),
+                             ("pool_backward", pool_backward, bytes_pool)):
+        us = _event_time_us(fn)
+        gbs = nbytes / (us * 1e-6) / 1e9
+        out[name] = {"us": round(us, 2), "bytes": nbytes, "GB/s": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 3)}
+    us = _event_time_us(conv_forward)
+    tflops = 2.0 * m * co * k / (us * 1e-6) / 1e12
+    out["conv_forward_implicit"] = {"us": round(us, 2), "TFLOP/s": round(tflops, 2),
+                                    "frac": round(tflops / FP32_MFMA_PEAK_TFLOPS, 3)}
+    return out
+
+
 def cpu_baseline(min_seconds=10.0, batch=2):
     """The NumPy reference-path ResNet18 step (forward + backward + Adam) on this host."""
     from oracle import resnet as oracle_resnet
@@ -180,6 +249,7 @@ def main():
                    "graph": "optimize=False" if args.plain_graph else "optimize=True (BN+ReLU, BN+Add+ReLU units)"},
         "step_tflops": round(STEP_GFLOP * args.batch / 64 / (ms_per_step * 1e-3) / 1e3, 2),
         "roofline": roofline,
+        "c3_kernels": c3_kernels(),
     }
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline()

@@ -474,8 +474,31 @@ GemmPlan whole_stages(int tile, int K, int requested, int bk) {
 
 bool tile_fits(int tile, int M) { return blocks_for(M, TILE_TABLE[tile].bm) <= GRID_YZ_LIMIT; }
 
-// The plan of least estimated cost of a forward-orientation (forward, dX) or dW product.
+// dW products reduce over the pixels into a small output, so they are split over K. The rule below
+// reproduces the fastest plan of a sweep over every tile and split on MI355X for ResNet18's batch-64
+// dW products: four 64 x 64 waves per tile (tile 3) for outputs of at least 128 x 1024, else four
+// 32 x 32 waves (tile 6); the K split brings the launch to about 432 (tile 3) or 1000 (tile 6)
+// workgroups, with slices of at least 160 pixels.
+constexpr int WGRAD_MIN_SLICE = 160;
+constexpr int WGRAD_MAX_SLICES = 128;
+
+GemmPlan wgrad_plan(int M, int N, int K) {
+    const int tile = (M >= 128 && N >= 1024) ? 3 : 6;
+    const ImplicitTile& t = TILE_TABLE[tile];
+    const std::int64_t tiles = static_cast<std::int64_t>(blocks_for(M, t.bm)) * blocks_for(N, t.bn);
+    const std::int64_t target = tile == 3 ? 432 : 1000;
+    const int most = std::max(1, std::min(WGRAD_MAX_SLICES, K / WGRAD_MIN_SLICE));
+    int wanted = static_cast<int>(std::max<std::int64_t>(1, (target + tiles / 2) / tiles));
+    wanted = std::min(wanted, most);
+    int requested = 1;
+    for (const int choice : SPLIT_CHOICES)
+        if (choice <= wanted) requested = choice;
+    return whole_stages(tile, K, requested, BK_WG);
+}
+
+// The plan of least estimated cost of a forward-orientation (forward, dX) product, or the dW rule.
 GemmPlan implicit_auto_plan(bool wgrad, int M, int N, int K) {
+    if (wgrad && tile_fits(3, M) && tile_fits(6, M)) return wgrad_plan(M, N, K);
     const int bk = wgrad ? BK_WG : BK;
     GemmPlan best{-1, 1, K};
     double best_cost = 0.0;
