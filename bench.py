@@ -155,7 +155,7 @@ def c3_kernels():
         native._raise_for(lib.mfh_conv_im2col(x.data_ptr(), cols.data_ptr(), *dims, stream), lib)
 
     def conv_forward():
-        native._raise_for(lib.mfh_conv_forward_implicit(x.data_ptr(), weight.data_ptr(), wt.data_ptr(), 0,
+        native._raise_for(lib.mfh_conv_forward_implicit(x.data_ptr(), weight.data_ptr(), wt.data_ptr(), 0, 0,
                                                         y.data_ptr(), *dims, 0, 0.0, 1, 0, 0, stream), lib)
 
     pooled = torch.empty((n, co, h // 2, w // 2), device="cuda")

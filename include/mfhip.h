@@ -91,33 +91,54 @@ MFH_API int mfh_conv_backward(uint64_t weight, uint64_t dy, uint64_t y, uint64_t
 /* Implicit-GEMM convolution forward: y (N,CO,OH,OW) = act(conv(x, weight) + bias) with the im2col
  * matrix gathered from x inside the GEMM's operand loads (no cols buffer). One GEMM
  * W (CO x K) . view (K x N*OH*OW) over every image, stored straight into NCHW with the bias and
- * activation in its epilogue. When CI is a multiple of 16 the features run in channel chunks of 16
- * per window tap and `wt` (CO*CI*KH*KW floats, 16-byte aligned) receives the kernel in that order;
- * otherwise wt is unused and may be 0. workspace: mfh_conv_implicit_workspace(..., 0) floats let
+ * activation in its epilogue. When CI is a multiple of 32 the features run in channel chunks of 32
+ * per window tap and the product reads the kernel in that order from `wt` (CO*CI*KH*KW floats,
+ * 16-byte aligned): with prepared = 0 this call writes it there from `weight`; with prepared = 1
+ * wt already holds it (mfh_conv_weight_orders, flip 0) and `weight` is not read (it may be 0).
+ * Otherwise wt is unused and may be 0. workspace: mfh_conv_implicit_workspace(..., 0) floats let
  * it split K (0 is allowed: no split). Arguments otherwise as mfh_conv_forward.
  * Has no single counterpart in the reference: it replaces the im2col + gemm_rows + epilogue sequence
  * of mf_conv_forward, native_cublas.cpp:1441-1461, when the caller does not keep cols. */
-MFH_API int mfh_conv_forward_implicit(uint64_t x, uint64_t weight, uint64_t wt, uint64_t bias, uint64_t y, int N,
-                                      int CI, int H, int W, int CO, int KH, int KW, int OH, int OW, int SH, int SW,
-                                      int PH, int PW, int activation, float alpha, int engine, uint64_t workspace,
-                                      int64_t workspace_floats, uint64_t stream);
+MFH_API int mfh_conv_forward_implicit(uint64_t x, uint64_t weight, uint64_t wt, int prepared, uint64_t bias,
+                                      uint64_t y, int N, int CI, int H, int W, int CO, int KH, int KW, int OH, int OW,
+                                      int SH, int SW, int PH, int PW, int activation, float alpha, int engine,
+                                      uint64_t workspace, int64_t workspace_floats, uint64_t stream);
+
+/* The kernels of several convolutions in the orders the implicit products read them, in one
+ * launch for up to 32 kernels (more take more launches). Kernel i is weights[i] (CO, CI, KH, KW)
+ * with dims[5i .. 5i+4] = CO, CI, KH, KW, flip; outs[i] receives CO*CI*KH*KW floats (16-byte
+ * aligned): flip 0, the forward order (rows co, features (ci, tap), in chunks of 32 channels per tap
+ * when CI is a multiple of 32); flip 1, the stride-1 dX order, flipped and transposed (rows ci,
+ * features (co, KH*KW-1-tap), chunked when CO is a multiple of 32). The three arrays are host memory.
+ * Has no counterpart in the reference (its products read the kernel in place): it lets a network
+ * reorder all of its kernels once per step instead of once per convolution call. */
+MFH_API int mfh_conv_weight_orders(const uint64_t* weights, const uint64_t* outs, const int* dims, int count,
+                                   uint64_t stream);
 
 /* Split-K workspace floats of one pass of the implicit convolution under the automatic plan
  * (pass 0 forward, 1 dW, 2 dX of a stride-1 convolution); 0 when it does not split, -1 on error. */
 MFH_API int64_t mfh_conv_implicit_workspace(int N, int CI, int H, int W, int CO, int KH, int KW, int OH, int OW,
                                             int SH, int SW, int PH, int PW, int pass);
 
+/* flags of mfh_conv_backward_implicit */
+#define MFH_CONV_WFLIP_READY 1   /* wflip already holds the dX order (mfh_conv_weight_orders, flip 1) */
+#define MFH_CONV_ACCUMULATE_DX 2 /* dx += the input gradient (dx holds a gradient already) */
+
 /* Backward of a convolution without cols, from x and the NCHW dy:
  *   gated (N*CO*OH*OW floats) receives dy gated by the fused activation through y; required when
  *          activation != 0, and then used in place of dy below;
- *   db   = FP64 sum of dy per channel: per-(n, co) FP64 row sums in `partial` (N * CO doubles),
- *          reduced over n in order;
+ *   db   = FP64 sum of dy per channel: with dw, the dW product's first feature tile sums dy over
+ *          its pixel slice in FP64 (into `partial` when the product is split over the pixels, then
+ *          added in slice order by the split-K reduction launch); without dw, per-(n, co) FP64 row
+ *          sums reduced over n in order. partial holds CO * max(N, 128) doubles;
  *   dw   (CO, CI*KH*KW) = dy . im2col(x) with dy read in place (split over the pixels on dw_engine
  *          through the workspace); needs x;
- *   dx   stride 1: a forward convolution of dy with the flipped kernel, written to `wflip`
- *          (CI*CO*KH*KW floats, 16-byte aligned; in chunks of 16 output channels per tap when CO
- *          is a multiple of 16), straight into NCHW dx; other strides: the per-image column
+ *   dx   stride 1: a forward convolution of dy with the flipped kernel read from `wflip`
+ *          (CI*CO*KH*KW floats, 16-byte aligned, in chunks of 32 output channels per tap when CO
+ *          is a multiple of 32), which this call fills from `weight` unless flags has
+ *          MFH_CONV_WFLIP_READY; straight into NCHW dx; other strides: the per-image column
  *          gradient W^T dy_n in grad_cols (N*CI*KH*KW*OH*OW floats) and the col2im gather.
+ *          With MFH_CONV_ACCUMULATE_DX, dx = dx + the gradient (one rounding, as a separate add).
  * workspace: at least the larger of mfh_conv_implicit_workspace passes 1 and 2 that are requested.
  * Has no single counterpart in the reference: it replaces mf_conv_backward_plans,
  * native_cublas.cpp:1465-1532, when the caller does not keep cols. */
@@ -125,8 +146,8 @@ MFH_API int mfh_conv_backward_implicit(uint64_t x, uint64_t weight, uint64_t dy,
                                        uint64_t dw, uint64_t dx, uint64_t wflip, uint64_t grad_cols, uint64_t partial,
                                        uint64_t db, int N, int CI, int H, int W, int CO, int KH, int KW, int OH,
                                        int OW, int SH, int SW, int PH, int PW, int activation, float alpha,
-                                       int dw_engine, int dx_engine, uint64_t workspace, int64_t workspace_floats,
-                                       uint64_t stream);
+                                       int dw_engine, int dx_engine, int flags, uint64_t workspace,
+                                       int64_t workspace_floats, uint64_t stream);
 
 /* ---- max pooling ---------------------------------------------------------------------------- */
 

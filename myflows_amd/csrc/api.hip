@@ -306,24 +306,44 @@ MFH_API int mfh_conv_backward(std::uint64_t weight, std::uint64_t dy, std::uint6
     bool per_image = false;
     MFH_TRY(column_gradient(dx_engine, g, as_ptr<const float>(weight), as_ptr<const float>(dy),
                             need_rows ? as_ptr<const float>(dyT) : nullptr, as_ptr<float>(grad_cols), &per_image, s));
-    return launch_col2im_t(as_ptr<const float>(grad_cols), as_ptr<float>(dx), g, per_image, s);
+    return launch_col2im_t(as_ptr<const float>(grad_cols), as_ptr<float>(dx), g, per_image, false, s);
 }
 
-MFH_API int mfh_conv_forward_implicit(std::uint64_t x, std::uint64_t weight, std::uint64_t wt, std::uint64_t bias,
-                                      std::uint64_t y, int N, int CI, int H, int W, int CO, int KH, int KW, int OH,
-                                      int OW, int SH, int SW, int PH, int PW, int activation, float alpha, int engine,
-                                      std::uint64_t workspace, std::int64_t workspace_floats, std::uint64_t stream) {
+MFH_API int mfh_conv_forward_implicit(std::uint64_t x, std::uint64_t weight, std::uint64_t wt, int prepared,
+                                      std::uint64_t bias, std::uint64_t y, int N, int CI, int H, int W, int CO, int KH,
+                                      int KW, int OH, int OW, int SH, int SW, int PH, int PW, int activation,
+                                      float alpha, int engine, std::uint64_t workspace, std::int64_t workspace_floats,
+                                      std::uint64_t stream) {
     MFH_TRY(require_ready());
     const ConvGeometry g{N, CI, H, W, CO, KH, KW, OH, OW, SH, SW, PH, PW};
     MFH_TRY(validate(g));
     MFH_TRY(validate_activation(activation, alpha));
     MFH_TRY(validate_engine(engine));
-    MFH_REQUIRE(x && weight && y, "conv forward received a null buffer");
+    MFH_REQUIRE(x && y && (weight || (prepared && wt)), "conv forward received a null buffer");
     MFH_REQUIRE(wt || !implicit_chunked(CI), "the implicit forward needs the reordered-kernel buffer wt");
+    MFH_REQUIRE(prepared == 0 || prepared == 1, "prepared must be 0 or 1");
     MFH_REQUIRE(workspace_floats >= 0, "workspace size must be non-negative");
     return conv_implicit_forward(g, as_ptr<const float>(x), as_ptr<const float>(weight), as_ptr<float>(wt),
-                                 as_ptr<const float>(bias), as_ptr<float>(y), activation, alpha, engine,
+                                 prepared == 1, as_ptr<const float>(bias), as_ptr<float>(y), activation, alpha, engine,
                                  as_ptr<float>(workspace), workspace_floats, as_stream(stream));
+}
+
+MFH_API int mfh_conv_weight_orders(const std::uint64_t* weights, const std::uint64_t* outs, const int* dims, int count,
+                                   std::uint64_t stream) {
+    MFH_TRY(require_ready());
+    MFH_REQUIRE(count >= 0, "count must be non-negative");
+    MFH_REQUIRE(count == 0 || (weights && outs && dims), "weight orders need the weights, outputs and dims arrays");
+    std::vector<WeightOrder> orders(static_cast<size_t>(count));
+    for (int i = 0; i < count; ++i) {
+        const int* d = dims + 5 * i;
+        const int CO = d[0], CI = d[1], KH = d[2], KW = d[3], flip = d[4];
+        MFH_REQUIRE(weights[i] && outs[i], "weight order received a null buffer");
+        MFH_REQUIRE(CO > 0 && CI > 0 && KH > 0 && KW > 0, "kernel dimensions must be positive");
+        MFH_REQUIRE(static_cast<std::int64_t>(CO) * CI * KH * KW <= INDEX_LIMIT, "kernel exceeds the int32 index range");
+        MFH_REQUIRE(flip == 0 || flip == 1, "flip must be 0 or 1");
+        orders[i] = WeightOrder{as_ptr<const float>(weights[i]), as_ptr<float>(outs[i]), CO, CI, KH * KW, flip};
+    }
+    return launch_weight_orders(orders.data(), count, as_stream(stream));
 }
 
 MFH_API std::int64_t mfh_conv_implicit_workspace(int N, int CI, int H, int W, int CO, int KH, int KW, int OH, int OW,
@@ -342,7 +362,7 @@ MFH_API int mfh_conv_backward_implicit(std::uint64_t x, std::uint64_t weight, st
                                        std::uint64_t gated, std::uint64_t dw, std::uint64_t dx, std::uint64_t wflip,
                                        std::uint64_t grad_cols, std::uint64_t partial, std::uint64_t db, int N, int CI,
                                        int H, int W, int CO, int KH, int KW, int OH, int OW, int SH, int SW, int PH,
-                                       int PW, int activation, float alpha, int dw_engine, int dx_engine,
+                                       int PW, int activation, float alpha, int dw_engine, int dx_engine, int flags,
                                        std::uint64_t workspace, std::int64_t workspace_floats, std::uint64_t stream) {
     MFH_TRY(require_ready());
     const ConvGeometry g{N, CI, H, W, CO, KH, KW, OH, OW, SH, SW, PH, PW};
@@ -352,7 +372,9 @@ MFH_API int mfh_conv_backward_implicit(std::uint64_t x, std::uint64_t weight, st
     MFH_TRY(validate_engine(dx_engine));
     const bool gated_dy = activation != ACT_NONE;
     const bool unit_stride = SH == 1 && SW == 1;
-    MFH_REQUIRE(weight && dy, "conv backward needs weight and dy");
+    const bool prepared = (flags & MFH_CONV_WFLIP_READY) != 0, accumulate = (flags & MFH_CONV_ACCUMULATE_DX) != 0;
+    MFH_REQUIRE((flags & ~(MFH_CONV_WFLIP_READY | MFH_CONV_ACCUMULATE_DX)) == 0, "unknown conv backward flags");
+    MFH_REQUIRE(dy && (weight || (unit_stride && prepared)), "conv backward needs weight and dy");
     MFH_REQUIRE(!gated_dy || (y && gated), "a fused activation needs the forward output and the gated buffer");
     MFH_REQUIRE((partial == 0) == (db == 0), "partial and db must be given together");
     MFH_REQUIRE(!dw || x, "dW needs x");
@@ -367,22 +389,25 @@ MFH_API int mfh_conv_backward_implicit(std::uint64_t x, std::uint64_t weight, st
                                      activation == ACT_LEAKY_RELU ? alpha : 0.0f, false, s));
         grad = as_ptr<const float>(gated);
     }
-    if (db) {
-        MFH_TRY(launch_row_sums(grad, as_ptr<double>(partial), N * CO, g.ohw(), s));
-        MFH_TRY(launch_reduce_partials(as_ptr<const double>(partial), as_ptr<float>(db), N, CO, s));
-    }
     float* ws = as_ptr<float>(workspace);
-    if (dw)
-        MFH_TRY(conv_implicit_wgrad(g, as_ptr<const float>(x), grad, as_ptr<float>(dw), dw_engine, ws,
-                                    workspace_floats, s));
+    double* bias_rows = as_ptr<double>(partial);
+    if (dw) {
+        // db rides on the dW product: its first feature tile sums dy over each pixel slice, and
+        // the split-K reduction (or the product itself, when unsplit) finishes it.
+        MFH_TRY(conv_implicit_wgrad(g, as_ptr<const float>(x), grad, as_ptr<float>(dw), bias_rows, as_ptr<float>(db),
+                                    dw_engine, ws, workspace_floats, s));
+    } else if (db) {
+        MFH_TRY(launch_row_sums(grad, bias_rows, N * CO, g.ohw(), s));
+        MFH_TRY(launch_reduce_partials(bias_rows, as_ptr<float>(db), N, CO, s));
+    }
     if (!dx) return OK;
     if (unit_stride)
-        return conv_implicit_dgrad(g, grad, as_ptr<const float>(weight), as_ptr<float>(wflip), as_ptr<float>(dx),
-                                   dx_engine, ws, workspace_floats, s);
+        return conv_implicit_dgrad(g, grad, as_ptr<const float>(weight), as_ptr<float>(wflip), prepared,
+                                   as_ptr<float>(dx), accumulate, dx_engine, ws, workspace_floats, s);
     bool per_image = false;
     MFH_TRY(column_gradient(dx_engine, g, as_ptr<const float>(weight), grad, nullptr, as_ptr<float>(grad_cols),
                             &per_image, s));
-    return launch_col2im_t(as_ptr<const float>(grad_cols), as_ptr<float>(dx), g, per_image, s);
+    return launch_col2im_t(as_ptr<const float>(grad_cols), as_ptr<float>(dx), g, per_image, accumulate, s);
 }
 
 MFH_API int mfh_pool_forward(std::uint64_t x, std::uint64_t y, std::uint64_t argmax, int N, int C, int H, int W,

@@ -66,8 +66,9 @@ struct ConvGeometry {
 // ---- conv.hip ---------------------------------------------------------------------------------
 int launch_im2col(const float* x, float* cols, const ConvGeometry& g, hipStream_t stream);
 // dx from the feature-major column gradient: gcT[n][CI*KH*KW][OH*OW] when per_image, else
-// gcT[CI*KH*KW][N*OH*OW].
-int launch_col2im_t(const float* gcT, float* dx, const ConvGeometry& g, bool per_image, hipStream_t stream);
+// gcT[CI*KH*KW][N*OH*OW]. With accumulate, dx += the gathered sums instead of dx = them.
+int launch_col2im_t(const float* gcT, float* dx, const ConvGeometry& g, bool per_image, bool accumulate,
+                    hipStream_t stream);
 int launch_conv_epilogue(const float* rows, const float* bias, float* y, int N, int OHW, int CO, int act,
                          float alpha, hipStream_t stream);
 int conv_grad_tile();  // pixels per conv_grad_rows tile (grid_x counts these tiles)
@@ -135,6 +136,12 @@ struct GemmParams {
     long long segment_stride;  // distance between consecutive segments of C
     int taps;                  // > 0: columns are convolution features in chunked order (see ConvGather)
     FastDiv taps_div;          // division by taps
+    int accumulate;            // 1: each output is added to what C holds (C = C + result)
+    // Split-K reduction only: also row_out[r] = (float) sum over z of row_partial[z * row_count + r]
+    // (FP64, in z order) for r < row_count, with row_slices values of z.
+    const double* row_partial;
+    float* row_out;
+    int row_count, row_slices;
 };
 
 // One GEMM problem, or `batch` of them at constant strides: C(M x N) = op(A) op(B), row-major;
@@ -164,6 +171,12 @@ struct GemmEpilogue {
     int segment = 0;
     long long segment_stride = 0;
     int taps = 0;  // KH*KW when the output columns are features in chunked order; stored in natural order
+    bool accumulate = false;  // C = C + result: a gradient added to one already there, in one pass
+    // With a split-K reduction: row sums of FP64 slice partials finished in the same launch
+    // (row_out[r] = sum over the slices of row_partial[z * row_count + r]).
+    const double* row_partial = nullptr;
+    float* row_out = nullptr;
+    int row_count = 0;
 };
 
 // Runs the engine; splits K through the workspace (never for batches) only when it holds the
@@ -199,18 +212,36 @@ constexpr int IMPLICIT_FORWARD = 0, IMPLICIT_WGRAD = 1, IMPLICIT_DGRAD = 2;
 std::int64_t implicit_workspace_floats(const ConvGeometry& g, int pass);
 // Whether the implicit kernels take a convolution over C input channels in chunked feature order.
 inline bool implicit_chunked(int C) { return C % CHANNEL_CHUNK == 0; }
-// y = act(conv(x, w) + bias), NCHW, without an im2col buffer; wt (CO*CI*KH*KW floats) receives
-// the kernel in the feature order of the GEMM.
-int conv_implicit_forward(const ConvGeometry& g, const float* x, const float* w, float* wt, const float* bias, float* y,
-                          int act, float alpha, int engine, float* workspace, std::int64_t workspace_floats,
-                          hipStream_t stream);
-// dW = dy . im2col(x), with dy read in place from NCHW.
-int conv_implicit_wgrad(const ConvGeometry& g, const float* x, const float* dy, float* dw, int engine,
-                        float* workspace, std::int64_t workspace_floats, hipStream_t stream);
-// dX of a stride-1 convolution as a forward convolution of dy with the flipped kernel (written to
-// wflip, CI x CO*KH*KW floats, in the GEMM's feature order).
-int conv_implicit_dgrad(const ConvGeometry& g, const float* dy, const float* w, float* wflip, float* dx, int engine,
-                        float* workspace, std::int64_t workspace_floats, hipStream_t stream);
+// y = act(conv(x, w) + bias), NCHW, without an im2col buffer. When C is chunked the product reads
+// the kernel in the order launch_weight_orders writes (flip 0): from wt, which this call fills
+// from w unless `prepared` says that it holds that order already.
+int conv_implicit_forward(const ConvGeometry& g, const float* x, const float* w, float* wt, bool prepared,
+                          const float* bias, float* y, int act, float alpha, int engine, float* workspace,
+                          std::int64_t workspace_floats, hipStream_t stream);
+// dW = dy . im2col(x), with dy read in place from NCHW. With db, the workgroups of the first
+// feature tile also sum dy over their pixel slice in FP64; an unsplit product writes db itself, a
+// split one leaves bias_partial[z * CO + co] for slice z (at most WGRAD_MAX_SLICES) and its
+// reduction finishes db in slice order.
+int conv_implicit_wgrad(const ConvGeometry& g, const float* x, const float* dy, float* dw, double* bias_partial,
+                        float* db, int engine, float* workspace, std::int64_t workspace_floats, hipStream_t stream);
+// dX of a stride-1 convolution as a forward convolution of dy with the flipped kernel, read from
+// wflip (CI x CO*KH*KW floats in the order launch_weight_orders writes with flip 1), which this call
+// fills from w unless `prepared`. With accumulate, dx += the result.
+int conv_implicit_dgrad(const ConvGeometry& g, const float* dy, const float* w, float* wflip, bool prepared, float* dx,
+                        bool accumulate, int engine, float* workspace, std::int64_t workspace_floats,
+                        hipStream_t stream);
+// The kernel W (CO, CI, KH, KW) in the order an implicit product reads it: flip 0 for the forward
+// (CO rows over (ci, tap) features), flip 1 for the stride-1 dX (CI rows over (co, flipped tap)
+// features), each in chunked feature order when its channel count is chunked.
+struct WeightOrder {
+    const float* w;
+    float* out;
+    int CO, CI, taps, flip;
+};
+// All `count` orders in as few launches as the kernel arguments allow.
+int launch_weight_orders(const WeightOrder* orders, int count, hipStream_t stream);
+// Largest number of pixel slices the dW plan makes (rows of conv_implicit_wgrad's bias_partial).
+constexpr int WGRAD_MAX_SLICES = 128;
 // partial[r] = FP64 sum of row r (rows x length floats).
 int launch_row_sums(const float* src, double* partial, int rows, int length, hipStream_t stream);
 

@@ -79,7 +79,7 @@ __global__ __launch_bounds__(256) void col2im_t_kernel(const float* __restrict__
                                                        int total, FastDiv div_w, FastDiv div_h, FastDiv div_ci,
                                                        int CI, int KH, int KW, int OH, int OW, int SH, int SW,
                                                        FastDiv div_sh, FastDiv div_sw, int PH, int PW,
-                                                       long long f_stride, long long n_stride) {
+                                                       long long f_stride, long long n_stride, int accumulate) {
     const int idx = blockIdx.x * 256 + threadIdx.x;
     if (idx >= total) return;
     int iw, ih, ci;
@@ -102,7 +102,7 @@ __global__ __launch_bounds__(256) void col2im_t_kernel(const float* __restrict__
             sum += row[kw * f_stride + ow];
         }
     }
-    dx[idx] = sum;
+    dx[idx] = accumulate ? dx[idx] + sum : sum;
 }
 
 constexpr int TILE = 64;   // pixels x channels per transpose tile (one wave64 per row of the tile)
@@ -437,7 +437,8 @@ int launch_im2col(const float* x, float* cols, const ConvGeometry& g, hipStream_
     return MFH_CHECK_LAUNCH("im2col", stream);
 }
 
-int launch_col2im_t(const float* gcT, float* dx, const ConvGeometry& g, bool per_image, hipStream_t stream) {
+int launch_col2im_t(const float* gcT, float* dx, const ConvGeometry& g, bool per_image, bool accumulate,
+                    hipStream_t stream) {
     const int total = g.N * g.CI * g.H * g.W;
     const long long ohw = g.ohw();
     const long long f_stride = per_image ? ohw : static_cast<long long>(g.rows());
@@ -445,7 +446,7 @@ int launch_col2im_t(const float* gcT, float* dx, const ConvGeometry& g, bool per
     col2im_t_kernel<<<blocks_for(total, 256), 256, 0, stream>>>(gcT, dx, total, FastDiv(g.W), FastDiv(g.H),
                                                                   FastDiv(g.CI), g.CI, g.KH, g.KW, g.OH, g.OW, g.SH,
                                                                   g.SW, FastDiv(g.SH), FastDiv(g.SW), g.PH, g.PW,
-                                                                  f_stride, n_stride);
+                                                                  f_stride, n_stride, accumulate ? 1 : 0);
     return MFH_CHECK_LAUNCH("col2im_t", stream);
 }
 

@@ -64,22 +64,39 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void gemm_mfma_kernel(G
 
 // C = act((float)(((0.0 + p0) + p1) + ... + p[S-1]) [+ bias]) with the FP64 sum in slice order,
 // the bias (per column or per row) added in FP32 after the rounding, stored dense (row * ldc + col)
-// or segmented like the GEMM's own epilogue.
+// or segmented like the GEMM's own epilogue (C = C + that when p.accumulate).
 __device__ __forceinline__ void finish_output(const GemmParams& p, float* C, long long i, double s) {
     const int row = static_cast<int>(i / p.N), col = static_cast<int>(i % p.N);
     float v = static_cast<float>(s);
     if (p.bias_mode == BIAS_COLUMN) v += p.bias[col];
     else if (p.bias_mode == BIAS_ROW) v += p.bias[row];
-    C[output_offset(p, row, col)] = activate(v, p.act, p.alpha);
+    float* out = C + output_offset(p, row, col);
+    v = activate(v, p.act, p.alpha);
+    *out = p.accumulate ? *out + v : v;
 }
 
 constexpr int REDUCE_AHEAD = 8;  // slices loaded before they are added
+
+// The rows riding on a split-K reduction (GemmParams::row_out): wave w of the launch finishes row
+// w. Lane l adds slices l, l + 64, ... in order, then a fixed butterfly adds the lanes (FP64
+// throughout), so the result does not depend on timing.
+__device__ __forceinline__ void finish_row(const GemmParams& p, long long t) {
+    const long long row = t / 64;
+    if (row >= p.row_count) return;  // uniform over the wave
+    const int lane = static_cast<int>(t % 64);
+    double s = 0.0;
+    for (int z = lane; z < p.row_slices; z += 64) s += p.row_partial[static_cast<long long>(z) * p.row_count + row];
+#pragma unroll
+    for (int offset = 32; offset > 0; offset >>= 1) s += __shfl_xor(s, offset, 64);
+    if (lane == 0) p.row_out[row] = static_cast<float>(s);
+}
 
 // One thread per output; the loads of REDUCE_AHEAD slices are issued before their additions, which
 // still run one at a time in slice order.
 __global__ __launch_bounds__(256) void split_reduce_kernel(const float* __restrict__ partial, float* __restrict__ C,
                                                            GemmParams p, int slices) {
     const long long i = blockIdx.x * 256LL + threadIdx.x, total = static_cast<long long>(p.M) * p.N;
+    if (p.row_out) finish_row(p, i);
     if (i >= total) return;
     double s = 0.0;
     int z = 0;
@@ -99,6 +116,7 @@ __global__ __launch_bounds__(256) void split_reduce_kernel(const float* __restri
 __global__ __launch_bounds__(256) void split_reduce_vec4_kernel(const float* __restrict__ partial,
                                                                 float* __restrict__ C, GemmParams p, int slices) {
     const long long q = blockIdx.x * 256LL + threadIdx.x, total = static_cast<long long>(p.M) * p.N;
+    if (p.row_out) finish_row(p, q);
     if (q * 4 >= total) return;
     const float4* quads = reinterpret_cast<const float4*>(partial);
     const long long stride = total / 4;
@@ -280,16 +298,23 @@ GemmParams epilogue_params(const GemmEpilogue& e, int M, int N, int ldc) {
     p.segment_stride = e.segment_stride;
     p.taps = e.taps;
     if (e.taps > 0) p.taps_div = FastDiv(e.taps);
+    p.accumulate = e.accumulate ? 1 : 0;
+    p.row_partial = e.row_partial;
+    p.row_out = e.row_out;
+    p.row_count = e.row_out ? e.row_count : 0;
     return p;
 }
 
-int launch_split_reduce(const float* partial, float* c, const GemmParams& p, int slices, hipStream_t stream) {
+int launch_split_reduce(const float* partial, float* c, GemmParams p, int slices, hipStream_t stream) {
     const std::int64_t outputs = static_cast<std::int64_t>(p.M) * p.N;
+    p.row_slices = slices;
     if (outputs % 4 == 0 && aligned16(partial)) {
-        split_reduce_vec4_kernel<<<blocks_for(outputs / 4, 256), 256, 0, stream>>>(partial, c, p, slices);
+        const std::int64_t threads = std::max<std::int64_t>(outputs / 4, 64LL * p.row_count);
+        split_reduce_vec4_kernel<<<blocks_for(threads, 256), 256, 0, stream>>>(partial, c, p, slices);
         return MFH_CHECK_LAUNCH("split_reduce_vec4", stream);
     }
-    split_reduce_kernel<<<blocks_for(outputs, 256), 256, 0, stream>>>(partial, c, p, slices);
+    const std::int64_t threads = std::max<std::int64_t>(outputs, 64LL * p.row_count);
+    split_reduce_kernel<<<blocks_for(threads, 256), 256, 0, stream>>>(partial, c, p, slices);
     return MFH_CHECK_LAUNCH("split_reduce", stream);
 }
 
@@ -341,6 +366,7 @@ int gemm_launch(int engine, hipStream_t stream, const GemmOperands& o, const Gem
         p.act = ACT_NONE;
         p.segment = 0;
         p.taps = 0;
+        p.accumulate = 0;
     } else {
         p.C = o.c;
         p.c_batch = o.c_batch;

@@ -213,7 +213,8 @@ __device__ __forceinline__ void mfma_k_loop(float* smem, int k_begin, int k_end,
 }
 
 // Epilogue: bias (per output column or per output row), the activation, then the store of the
-// wave's accumulators into C (dense or segmented, see output_offset).
+// wave's accumulators into C (dense or segmented, see output_offset), added to what C holds when
+// p.accumulate.
 template <class S>
 __device__ __forceinline__ void store_acc(const GemmParams& p, float* __restrict__ C, const v16f (&acc)[S::TM][S::TN],
                                           int m0, int n0, int wm0, int wn0, int lane) {
@@ -234,7 +235,9 @@ __device__ __forceinline__ void store_acc(const GemmParams& p, float* __restrict
                     float v = acc[i][j][r];
                     if (p.bias_mode == BIAS_COLUMN) v += col_bias;
                     else if (p.bias_mode == BIAS_ROW) v += bias[row];
-                    C[col_offset + static_cast<long long>(row) * p.ldc] = activate(v, p.act, p.alpha);
+                    float* out = C + col_offset + static_cast<long long>(row) * p.ldc;
+                    v = activate(v, p.act, p.alpha);
+                    *out = p.accumulate ? *out + v : v;
                 }
             }
     }

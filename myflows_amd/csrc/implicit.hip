@@ -19,9 +19,10 @@
 // Feature order. When the source has a multiple of 32 channels the features are taken in chunked
 // order k = ((c / 32)*KH*KW + tap)*32 + c % 32 (tap = kh*KW + kw), so a 32-deep stage of the
 // forward product covers 32 channels at one window tap: the tap is decomposed once per stage (a
-// scalar), each thread tests its pixel's window bounds once per stage and then reads 16/RSTEP
+// scalar), each thread tests its pixel's window bounds once per stage and then reads 32/RSTEP
 // channels at a fixed stride. The kernel is reordered to match by weight_order_kernel (with the
-// dX flip folded in), and dW's output columns are mapped back to natural order by the epilogue.
+// dX flip folded in; one launch can reorder every kernel of a network), and dW's output columns
+// are mapped back to natural order by the epilogue.
 // Other channel counts (the 3-channel stem) take the natural order k = c*KH*KW + tap, decomposed
 // per feature row (a wave-uniform scalar computation).
 // Both gather loaders keep one pixel per thread column so that the pixel's decomposition
@@ -233,6 +234,30 @@ struct GradRowsInPlace {
 #pragma unroll
         for (int i = 0; i < PER; ++i) lds[(r0 + i * RSTEP) * LD + col] = v[i];
     }
+
+    // Adds the loaded values (0 outside the pixel range) to the thread's FP64 row sums.
+    __device__ __forceinline__ void add_to(double (&sums)[PER]) const {
+#pragma unroll
+        for (int i = 0; i < PER; ++i) sums[i] += static_cast<double>(v[i]);
+    }
+
+    // The row sums over this workgroup's pixels: the BK_WG threads of a row (adjacent lanes)
+    // combine their sums with a fixed butterfly, then the first of them stores the FP64 sum to
+    // out[row], or, when the workgroup covers every pixel, its float rounding to final[row].
+    __device__ __forceinline__ void store_sums(double (&sums)[PER], double* out, float* final, int CO, int m0,
+                                               int tid) const {
+#pragma unroll
+        for (int i = 0; i < PER; ++i) {
+            double s = sums[i];
+#pragma unroll
+            for (int offset = BK_WG / 2; offset > 0; offset >>= 1) s += __shfl_xor(s, offset, BK_WG);
+            const int row = m0 + tid / BK_WG + i * RSTEP;
+            if (tid % BK_WG == 0 && row < CO) {
+                if (final) final[row] = static_cast<float>(s);
+                else out[row] = s;
+            }
+        }
+    }
 };
 
 // Y (M x pixels) = A (M x K, row-major, lda) . view (K x pixels). Split-K writes dense partials
@@ -269,9 +294,11 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void conv_implicit_forw
 }
 
 // dW (CO x K) = dy (CO x pixels) . view^T (pixels x K), the pixel range split over z when p.split.
-template <int BM, int BN, int WM, int WN>
-__global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void conv_implicit_wgrad_kernel(GemmParams p,
-                                                                                        ConvGather g) {
+// SUMS: the workgroups of feature tile 0 also sum each dy row over their pixel range in FP64, the
+// conv bias gradient: db[co] directly when unsplit, else sums[z * CO + co] for the reduction.
+template <int BM, int BN, int WM, int WN, bool SUMS>
+__global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void conv_implicit_wgrad_kernel(GemmParams p, ConvGather g,
+                                                                                        double* sums, float* db) {
     using S = MfmaShape<BM, BN, BK_WG, WM, WN, false, true>;
     __shared__ __attribute__((aligned(16))) float smem[2 * S::STAGE];
     int tile_m, tile_n, z;
@@ -284,9 +311,14 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void conv_implicit_wgra
     float* __restrict__ C = p.C + (p.split ? z * p.c_batch : 0);
     const int ohw = g.OH * g.OW;
 
-    GradRowsInPlace<BM, S::THREADS> la;
+    using RowLoader = GradRowsInPlace<BM, S::THREADS>;
+    RowLoader la;
     GatherPixelColumns<BN, S::THREADS> lb;
     lb.init(g, n0, tid);
+    const bool summing = SUMS && tile_n == 0;
+    double row_sums[RowLoader::PER];
+#pragma unroll
+    for (int i = 0; i < RowLoader::PER; ++i) row_sums[i] = 0.0;
     auto fetch = [&](int kt) {
         const PixelAt at = pixel_at(g, kt + tid % BK_WG, k_end);
         la.load(p.A, p.M, ohw, m0, at, tid);
@@ -295,33 +327,119 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void conv_implicit_wgra
     auto store = [&](float* a_lds, float* b_lds) {
         la.template store<S::LDA_S>(a_lds, tid);
         lb.template store<S::LDB_S>(b_lds, tid);
+        if constexpr (SUMS)
+            if (summing) la.add_to(row_sums);
     };
     v16f acc[S::TM][S::TN];
     zero_acc<S>(acc);
     mfma_k_loop<S>(smem, k_begin, k_end, fetch, store, acc, wm0, wn0, lane);
     store_acc<S>(p, C, acc, m0, n0, wm0, wn0, lane);
+    if constexpr (SUMS)
+        if (summing)
+            la.store_sums(row_sums, sums + static_cast<long long>(z) * p.M, p.split ? nullptr : db, p.M, m0, tid);
 }
 
 // The kernel as the A operand of an implicit product: out[o][k] for O rows and features k over C
 // channels and T = KH*KW taps, in chunked order when `chunked` (else natural order c*T + tap).
 // Forward (flip = 0): O = CO, C = CI, out[co][(c, tap)] = w[co][c][tap]. dX (flip = 1): O = CI,
 // C = CO, out[ci][(co, tap)] = w[co][ci][T - 1 - tap], the flipped and transposed kernel.
-__global__ __launch_bounds__(256) void weight_order_kernel(const float* __restrict__ w, float* __restrict__ out,
-                                                           int total, int O, int C, int T, int chunked, int flip) {
-    const int idx = blockIdx.x * 256 + threadIdx.x;
-    if (idx >= total) return;
-    const int row_len = C * T;
-    const int o = idx / row_len, k = idx % row_len;
-    int c, tap;
-    if (chunked) {
-        const int group = k / CHANNEL_CHUNK;
-        tap = group % T;
-        c = (group / T) * CHANNEL_CHUNK + k % CHANNEL_CHUNK;
-    } else {
-        c = k / T;
-        tap = k % T;
+// One launch writes up to ORDER_BATCH orders: order i owns the workgroups [first_block[i],
+// first_block[i + 1]).
+//   * Chunked orders with at most TILE_TAPS taps go through LDS, one workgroup per 32 output rows x
+//     one chunk of 32 channels: both the reads and the writes are contiguous runs of 32*T floats
+//     (forward: the row's 32*T source floats of that chunk; dX: for each of the chunk's 32 output
+//     channels, the 32*T floats of the 32 rows' input channels).
+//   * Other orders (natural channel counts, wider windows) take one output element per thread.
+constexpr int ORDER_BATCH = 32;
+constexpr int TILE_TAPS = 9;
+constexpr int TILE_STRIDE = 32 * TILE_TAPS + 1;  // floats per channel-within-chunk slab of the LDS tile
+struct OrderJob {
+    const float* w;
+    float* out;
+    int O, C, T, chunked, flip, total;
+    int tiled;               // LDS path: blocks are (row block, chunk), chunk fastest
+    FastDiv div_row, div_t;  // by C * T, by T
+    FastDiv div_panel;       // by 32 * T
+    FastDiv div_chunks;      // by C / 32
+};
+struct OrderBatch {
+    OrderJob job[ORDER_BATCH];
+    int first_block[ORDER_BATCH + 1];
+    int count;
+};
+
+// Elements a thread moves per batch of the tiled path: their loads are all issued before the
+// first LDS store (the loop is otherwise one global-load latency per element).
+constexpr int ORDER_UNROLL = 12;
+
+__device__ __forceinline__ void order_tiled(const OrderJob& job, int block, float* tile) {
+    const int T = job.T, panel = 32 * T, per_thread = panel / 8;  // 32 * panel elements / 256 threads
+    int chunk;
+    const int ob = job.div_chunks.divmod(block, chunk);
+    const int rows = min(32, job.O - ob * 32);
+    const long long row_len = static_cast<long long>(job.C) * T;
+    // Source run s (flip: output channel co = chunk*32 + s of W, over the rows' input channels and
+    // all taps; forward: output row ob*32 + s, over the chunk's 32 input channels and all taps).
+    const float* src = job.flip ? job.w + static_cast<long long>(chunk) * 32 * job.O * T + static_cast<long long>(ob) * panel
+                                : job.w + static_cast<long long>(ob) * 32 * row_len + static_cast<long long>(chunk) * panel;
+    const long long run_stride = job.flip ? static_cast<long long>(job.O) * T : row_len;
+    for (int base = 0; base < per_thread; base += ORDER_UNROLL) {
+        float v[ORDER_UNROLL];
+        int slot[ORDER_UNROLL];
+#pragma unroll
+        for (int u = 0; u < ORDER_UNROLL; ++u) {
+            const int idx = threadIdx.x + (base + u) * 256;
+            slot[u] = -1;
+            v[u] = 0.0f;
+            if (base + u < per_thread) {
+                int e;
+                const int run = job.div_panel.divmod(idx, e);
+                int tap;
+                const int q = job.div_t.divmod(e, tap);  // flip: row r = q; forward: channel j = q
+                const int r = job.flip ? q : run, j = job.flip ? run : q;
+                if (r < rows) {
+                    v[u] = src[run * run_stride + e];
+                    slot[u] = j * TILE_STRIDE + r * T + (job.flip ? T - 1 - tap : tap);
+                }
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < ORDER_UNROLL; ++u)
+            if (slot[u] >= 0) tile[slot[u]] = v[u];
     }
-    out[idx] = flip ? w[(c * O + o) * T + (T - 1 - tap)] : w[(o * C + c) * T + tap];
+    __syncthreads();
+    // Destination run r: row ob*32 + r, features (chunk, tap, j) = tap*32 + j within the chunk.
+    float* dst = job.out + static_cast<long long>(ob) * 32 * row_len + static_cast<long long>(chunk) * panel;
+    for (int idx = threadIdx.x; idx < 32 * panel; idx += 256) {
+        int d;
+        const int r = job.div_panel.divmod(idx, d);
+        const int tap = d / 32, j = d % 32;
+        if (r < rows) dst[r * row_len + d] = tile[j * TILE_STRIDE + r * T + tap];
+    }
+}
+
+__global__ __launch_bounds__(256) void weight_order_kernel(OrderBatch batch) {
+    __shared__ float tile[32 * TILE_STRIDE];
+    int j = 0;
+    while (j + 1 < batch.count && static_cast<int>(blockIdx.x) >= batch.first_block[j + 1]) ++j;
+    const OrderJob& job = batch.job[j];
+    const int block = static_cast<int>(blockIdx.x) - batch.first_block[j];
+    if (job.tiled) {
+        order_tiled(job, block, tile);
+        return;
+    }
+    const int idx = block * 256 + threadIdx.x;
+    if (idx >= job.total) return;
+    int k, c, tap;
+    const int o = job.div_row.divmod(idx, k);
+    if (job.chunked) {
+        const int group = k / CHANNEL_CHUNK;
+        const int chunk = job.div_t.divmod(group, tap);
+        c = chunk * CHANNEL_CHUNK + k % CHANNEL_CHUNK;
+    } else {
+        c = job.div_t.divmod(k, tap);
+    }
+    job.out[idx] = job.flip ? job.w[(c * job.O + o) * job.T + (job.T - 1 - tap)] : job.w[(o * job.C + c) * job.T + tap];
 }
 
 // partial[row] = sum of the row's `length` floats in FP64 (rows are the (n, co) planes of dy). One
@@ -373,22 +491,26 @@ constexpr ConvFn forward_of() {
     return conv_implicit_forward_kernel<t.bm, t.bn, t.wm, t.wn, VA, CHUNKED>;
 }
 
-template <int T>
-constexpr ConvFn wgrad_of() {
+using WgradFn = void (*)(GemmParams, ConvGather, double*, float*);
+
+template <int T, bool SUMS>
+constexpr WgradFn wgrad_of() {
     constexpr ImplicitTile t = TILE_TABLE[T];
-    return conv_implicit_wgrad_kernel<t.bm, t.bn, t.wm, t.wn>;
+    return conv_implicit_wgrad_kernel<t.bm, t.bn, t.wm, t.wn, SUMS>;
 }
 
-// forward[tile][0 | 1 | 2]: natural feature order with scalar / float4 A loads, chunked order.
+// forward[tile][0 | 1 | 2]: natural feature order with scalar / float4 A loads, chunked order;
+// wgrad[tile][0 | 1]: without / with the FP64 row sums of dy.
 struct ConvKernels {
     ConvFn forward[TILE_COUNT][3] = {};
-    ConvFn wgrad[TILE_COUNT] = {};
+    WgradFn wgrad[TILE_COUNT][2] = {};
     template <int T>
     void fill() {
         forward[T][0] = forward_of<T, false, false>();
         forward[T][1] = forward_of<T, true, false>();
         forward[T][2] = forward_of<T, true, true>();
-        wgrad[T] = wgrad_of<T>();
+        wgrad[T][0] = wgrad_of<T, false>();
+        wgrad[T][1] = wgrad_of<T, true>();
     }
     ConvKernels() {
         fill<0>();
@@ -480,7 +602,6 @@ bool tile_fits(int tile, int M) { return blocks_for(M, TILE_TABLE[tile].bm) <= G
 // 32 x 32 waves (tile 6); the K split brings the launch to about 432 (tile 3) or 1000 (tile 6)
 // workgroups, with slices of at least 160 pixels.
 constexpr int WGRAD_MIN_SLICE = 160;
-constexpr int WGRAD_MAX_SLICES = 128;
 
 GemmPlan wgrad_plan(int M, int N, int K) {
     const int tile = (M >= 128 && N >= 1024) ? 3 : 6;
@@ -545,7 +666,8 @@ int implicit_plan(bool wgrad, int engine, int M, int N, int K, float* workspace,
 // Runs one implicit product with the epilogue e (directly, or through split-K partials and the
 // FP64 slice reduction).
 int run_implicit(bool wgrad, const GemmPlan& plan, const float* a, int lda, int M, int N, int K, const ConvGather& g,
-                 float* c, int ldc, const GemmEpilogue& e, float* workspace, hipStream_t stream) {
+                 float* c, int ldc, GemmEpilogue e, float* workspace, hipStream_t stream,
+                 double* row_sums = nullptr, float* row_out = nullptr) {
     const bool split = plan.slices > 1;
     GemmParams p{};
     p.A = a;
@@ -571,6 +693,7 @@ int run_implicit(bool wgrad, const GemmPlan& plan, const float* a, int lda, int 
         p.segment_stride = e.segment_stride;
         p.taps = e.taps;
         if (e.taps > 0) p.taps_div = FastDiv(e.taps);
+        p.accumulate = e.accumulate ? 1 : 0;
     }
     const ImplicitTile& t = TILE_TABLE[plan.tile];
     const dim3 grid(blocks_for(N, t.bn), blocks_for(M, t.bm), static_cast<unsigned>(plan.slices));
@@ -578,10 +701,18 @@ int run_implicit(bool wgrad, const GemmPlan& plan, const float* a, int lda, int 
     const bool vec_a = K % 4 == 0 && lda % 4 == 0 && aligned16(a);
     const int variant = g.chunked ? 2 : vec_a ? 1 : 0;
     if (!wgrad && g.chunked && !vec_a) return MFH_FAIL(ERR_ARG, "the reordered kernel buffer must be 16-byte aligned");
-    const ConvFn fn = wgrad ? conv_kernels().wgrad[plan.tile] : conv_kernels().forward[plan.tile][variant];
-    hipLaunchKernelGGL(fn, grid, block, 0, stream, p, g);
+    if (wgrad)
+        hipLaunchKernelGGL(conv_kernels().wgrad[plan.tile][row_out ? 1 : 0], grid, block, 0, stream, p, g, row_sums,
+                           row_out);
+    else
+        hipLaunchKernelGGL(conv_kernels().forward[plan.tile][variant], grid, block, 0, stream, p, g);
     MFH_TRY(MFH_CHECK_LAUNCH(wgrad ? "conv_implicit_wgrad" : "conv_implicit_forward", stream));
     if (!split) return OK;
+    if (row_out) {  // the row sums' slice partials are finished by the same reduction launch
+        e.row_partial = row_sums;
+        e.row_out = row_out;
+        e.row_count = M;
+    }
     return split_reduce_epilogue(workspace, c, e, M, N, ldc, plan.slices, stream);
 }
 
@@ -597,22 +728,52 @@ std::int64_t implicit_workspace_floats(const ConvGeometry& g, int pass) {
                                                           pass == IMPLICIT_FORWARD ? g.rows() : g.N * g.H * g.W);
 }
 
-int launch_weight_order(const float* w, float* out, int O, int C, int T, bool flip, hipStream_t stream) {
-    const int total = O * C * T;
-    weight_order_kernel<<<blocks_for(total, 256), 256, 0, stream>>>(w, out, total, O, C, T,
-                                                                     implicit_chunked(C) ? 1 : 0, flip ? 1 : 0);
-    return MFH_CHECK_LAUNCH("weight_order", stream);
+int launch_weight_orders(const WeightOrder* orders, int count, hipStream_t stream) {
+    for (int first = 0; first < count; first += ORDER_BATCH) {
+        OrderBatch batch{};
+        batch.count = std::min(ORDER_BATCH, count - first);
+        int blocks = 0;
+        for (int i = 0; i < batch.count; ++i) {
+            const WeightOrder& o = orders[first + i];
+            OrderJob& job = batch.job[i];
+            const int rows = o.flip ? o.CI : o.CO, channels = o.flip ? o.CO : o.CI;
+            job.w = o.w;
+            job.out = o.out;
+            job.O = rows;
+            job.C = channels;
+            job.T = o.taps;
+            job.chunked = implicit_chunked(channels) ? 1 : 0;
+            job.flip = o.flip;
+            job.total = rows * channels * o.taps;
+            job.div_row = FastDiv(channels * o.taps);
+            job.div_t = FastDiv(o.taps);
+            job.tiled = job.chunked && o.taps <= TILE_TAPS ? 1 : 0;
+            job.div_panel = FastDiv(32 * o.taps);
+            job.div_chunks = FastDiv(std::max(1, channels / CHANNEL_CHUNK));
+            batch.first_block[i] = blocks;
+            blocks += static_cast<int>(job.tiled ? blocks_for(rows, 32) * (channels / CHANNEL_CHUNK)
+                                                 : blocks_for(job.total, 256));
+        }
+        batch.first_block[batch.count] = blocks;
+        if (blocks == 0) continue;
+        weight_order_kernel<<<blocks, 256, 0, stream>>>(batch);
+        MFH_TRY(MFH_CHECK_LAUNCH("weight_order", stream));
+    }
+    return OK;
 }
 
-int conv_implicit_forward(const ConvGeometry& g, const float* x, const float* w, float* wt, const float* bias,
-                          float* y, int act, float alpha, int engine, float* workspace, std::int64_t workspace_floats,
-                          hipStream_t stream) {
+int conv_implicit_forward(const ConvGeometry& g, const float* x, const float* w, float* wt, bool prepared,
+                          const float* bias, float* y, int act, float alpha, int engine, float* workspace,
+                          std::int64_t workspace_floats, hipStream_t stream) {
     const int M = g.CO, N = g.rows(), K = g.features();
     GemmPlan plan;
     MFH_TRY(implicit_plan(false, engine, M, N, K, workspace, workspace_floats, &plan));
     const ConvGather gather = gather_of(x, g.CI, g.H, g.W, g.KH, g.KW, g.SH, g.SW, g.PH, g.PW, g.N, g.OH, g.OW);
     if (gather.chunked) {
-        MFH_TRY(launch_weight_order(w, wt, g.CO, g.CI, g.KH * g.KW, false, stream));
+        if (!prepared) {
+            const WeightOrder order{w, wt, g.CO, g.CI, g.KH * g.KW, 0};
+            MFH_TRY(launch_weight_orders(&order, 1, stream));
+        }
         w = wt;
     }
     GemmEpilogue e;
@@ -625,22 +786,28 @@ int conv_implicit_forward(const ConvGeometry& g, const float* x, const float* w,
     return run_implicit(false, plan, w, K, M, N, K, gather, y, g.ohw(), e, workspace, stream);
 }
 
-int conv_implicit_wgrad(const ConvGeometry& g, const float* x, const float* dy, float* dw, int engine,
-                        float* workspace, std::int64_t workspace_floats, hipStream_t stream) {
+int conv_implicit_wgrad(const ConvGeometry& g, const float* x, const float* dy, float* dw, double* bias_partial,
+                        float* db, int engine, float* workspace, std::int64_t workspace_floats, hipStream_t stream) {
     const int M = g.CO, N = g.features(), K = g.rows();
     GemmPlan plan;
     MFH_TRY(implicit_plan(true, engine, M, N, K, workspace, workspace_floats, &plan));
+    if (db && (!bias_partial || plan.slices > WGRAD_MAX_SLICES))
+        return MFH_FAIL(ERR_ARG, "the dW plan's bias partials need bias_partial rows for every pixel slice");
     const ConvGather gather = gather_of(x, g.CI, g.H, g.W, g.KH, g.KW, g.SH, g.SW, g.PH, g.PW, g.N, g.OH, g.OW);
     GemmEpilogue e;
     if (gather.chunked) e.taps = g.KH * g.KW;
-    return run_implicit(true, plan, dy, g.ohw(), M, N, K, gather, dw, N, e, workspace, stream);
+    return run_implicit(true, plan, dy, g.ohw(), M, N, K, gather, dw, N, e, workspace, stream, bias_partial, db);
 }
 
-int conv_implicit_dgrad(const ConvGeometry& g, const float* dy, const float* w, float* wflip, float* dx, int engine,
-                        float* workspace, std::int64_t workspace_floats, hipStream_t stream) {
+int conv_implicit_dgrad(const ConvGeometry& g, const float* dy, const float* w, float* wflip, bool prepared, float* dx,
+                        bool accumulate, int engine, float* workspace, std::int64_t workspace_floats,
+                        hipStream_t stream) {
     const int khw = g.KH * g.KW;
     const int M = g.CI, N = g.N * g.H * g.W, K = g.CO * khw;
-    MFH_TRY(launch_weight_order(w, wflip, g.CI, g.CO, khw, true, stream));
+    if (!prepared) {
+        const WeightOrder order{w, wflip, g.CO, g.CI, khw, 1};
+        MFH_TRY(launch_weight_orders(&order, 1, stream));
+    }
     GemmPlan plan;
     MFH_TRY(implicit_plan(false, engine, M, N, K, workspace, workspace_floats, &plan));
     // dy as the source of a stride-1 convolution with padding KH-1-PH whose output grid is H x W.
@@ -649,6 +816,7 @@ int conv_implicit_dgrad(const ConvGeometry& g, const float* dy, const float* w, 
     GemmEpilogue e;
     e.segment = g.H * g.W;
     e.segment_stride = static_cast<long long>(g.CI) * g.H * g.W;
+    e.accumulate = accumulate;
     return run_implicit(false, plan, wflip, K, M, N, K, gather, dx, g.H * g.W, e, workspace, stream);
 }
 

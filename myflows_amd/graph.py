@@ -12,7 +12,8 @@ Keeps the semantics of the reference's ``core/node.py:5-123`` and ``core/graph.p
 * ``Graph(target)``: topological order; for each combination of leaf flags (and retained
   intermediates) an execution plan of which nodes need gradients; ``forward()`` in order,
   ``backward()`` in reverse seeded with ones; intermediate gradients are released as soon as their
-  node has consumed them.
+  node has consumed them. Before each pass, the kernel reorders that the pass's implicit-GEMM
+  convolutions read are made by one native launch for all of them (``weight_orders``).
 """
 
 from __future__ import annotations
@@ -132,6 +133,27 @@ def topological_order(root):
     return order
 
 
+def _prepare_weight_orders(units, phase):
+    """Batch the kernel reorders of every unit that asks for some in this pass (a convolution's
+    ``weight_orders(phase)``) into one native launch and hand each unit its results. Returns the
+    units served, whose unused results the caller drops after the pass."""
+    pending = []
+    for unit in units:
+        wants = getattr(unit, "weight_orders", None)
+        requests = wants(phase) if wants is not None else None
+        if requests:
+            pending.append((unit, requests))
+    if not pending:
+        return ()
+    from . import native
+    made = native.conv_weight_orders([r for _, requests in pending for r in requests])
+    first = 0
+    for unit, requests in pending:
+        unit.take_weight_orders(phase, made[first:first + len(requests)])
+        first += len(requests)
+    return tuple(unit for unit, _ in pending)
+
+
 @dataclass(frozen=True)
 class _Plan:
     """What one combination of leaf flags and retained nodes asks of a graph."""
@@ -216,6 +238,7 @@ class Graph:
         plan = self._plan()
         self._forward_plan = plan
         profiler = self.profiler
+        served = _prepare_weight_orders((u for u in plan.forward_units if u.parents), "forward")
         for unit in plan.forward_units:
             if not unit.parents:
                 continue
@@ -225,6 +248,8 @@ class Graph:
             else:
                 with profiler.node(unit, "forward"):
                     unit.forward(*inputs)
+        for unit in served:
+            unit.drop_weight_orders("forward")
 
     def backward(self, loss_scale=1.0):
         plan = self._plan()
@@ -238,6 +263,7 @@ class Graph:
         seed = self.target_node.value
         self.target_node.grad = torch.ones_like(seed) if loss_scale == 1.0 else torch.full_like(seed, loss_scale)
         profiler = self.profiler
+        served = _prepare_weight_orders((unit for unit, _ in plan.backward_units), "backward")
         for unit, output in plan.backward_units:
             if output.grad is None:
                 continue
@@ -251,6 +277,8 @@ class Graph:
                 with profiler.node(unit, "backward"):
                     unit.backward()
             output.grad = retained  # release the consumed intermediate gradient unless retained
+        for unit in served:
+            unit.drop_weight_orders("backward")
         for node in plan.keep:
             if node.grad is None:
                 node.clear_grad()

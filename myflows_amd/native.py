@@ -43,6 +43,9 @@ ROWS_PATH_MAX_PIXELS = 0               # conv forward through a rows GEMM + epil
 # loads (no cols buffer); "im2col" writes cols (N*OH*OW x CI*KH*KW) first and keeps it for dW.
 CONV_ALGORITHMS = ("implicit", "im2col")
 IMPLICIT_PASSES = {"forward": 0, "dw": 1, "dx": 2}
+CHANNEL_CHUNK = 32        # implicit products take features in chunks of this many channels per tap
+BIAS_PARTIAL_ROWS = 128   # rows of FP64 bias partials a dW product may write (its pixel slices)
+CONV_WFLIP_READY, CONV_ACCUMULATE_DX = 1, 2  # flags of mfh_conv_backward_implicit
 _STATUS_TEXT = {1: "initialization failed", 2: "invalid argument", 3: "HIP runtime error", 5: "wrong HIP device"}
 
 
@@ -59,9 +62,10 @@ class AdamTensor(ctypes.Structure):
 
 
 # Argument codes: p device pointer / stream (uint64), i int32, q int64, f float, d double,
-# t pointer to an AdamTensor table, P pointer to int32 (outputs).
+# t pointer to an AdamTensor table, P pointer to int32 (host array), U pointer to uint64 (host array).
 _CTYPE = {"p": ctypes.c_uint64, "i": ctypes.c_int, "q": ctypes.c_int64, "f": ctypes.c_float, "d": ctypes.c_double,
-          "t": ctypes.POINTER(AdamTensor), "P": ctypes.POINTER(ctypes.c_int), "s": ctypes.c_char_p, "-": None}
+          "t": ctypes.POINTER(AdamTensor), "P": ctypes.POINTER(ctypes.c_int), "s": ctypes.c_char_p, "-": None,
+          "U": ctypes.POINTER(ctypes.c_uint64)}
 _CONV = "i" * 13
 # symbol: (result code, argument codes); mirrors include/mfhip.h.
 _SIGNATURES = {
@@ -72,9 +76,10 @@ _SIGNATURES = {
     "mfh_conv_im2col": ("i", "pp" + _CONV + "p"),
     "mfh_conv_forward": ("i", "pppppp" + _CONV + "ifipqp"),
     "mfh_conv_backward": ("i", "pppppppppp" + _CONV + "iifiipqp"),
-    "mfh_conv_forward_implicit": ("i", "ppppp" + _CONV + "ifipqp"),
+    "mfh_conv_forward_implicit": ("i", "pppipp" + _CONV + "ifipqp"),
+    "mfh_conv_weight_orders": ("i", "UUPip"),
     "mfh_conv_implicit_workspace": ("q", _CONV + "i"),
-    "mfh_conv_backward_implicit": ("i", "ppppppppppp" + _CONV + "ifiipqp"),
+    "mfh_conv_backward_implicit": ("i", "ppppppppppp" + _CONV + "ifiiipqp"),
     "mfh_pool_forward": ("i", "ppp" + "i" * 10 + "p"),
     "mfh_pool_backward": ("i", "ppp" + "i" * 10 + "p"),
     "mfh_matmul": ("i", "iiipppp" + "iii" + "p"),
@@ -378,11 +383,51 @@ def _implicit_workspace(g, *passes):
     return torch.empty(floats, dtype=torch.float32, device="cuda"), floats
 
 
+def implicit_chunked(channels):
+    """Whether an implicit product over this many channels reads them in chunks of CHANNEL_CHUNK."""
+    return int(channels) % CHANNEL_CHUNK == 0
+
+
+def conv_weight_orders(requests):
+    """The kernels of several convolutions in the orders the implicit products read them, from one
+    launch: requests = [(weight (CO, CI, KH, KW), flip)], flip 0 for the forward (pass the result
+    to conv2d_forward as weight_order), 1 for the stride-1 dX (conv2d_backward's weight_flip).
+    Returns one flat float32 tensor per request."""
+    requests = list(requests)
+    if not requests:
+        return []
+    weights, outs, dims = [], [], []
+    for weight, flip in requests:
+        weight = _device_f32(weight, "weight")
+        if weight.ndim != 4:
+            raise ValueError("weight must have shape (CO, CI, KH, KW)")
+        if flip not in (0, 1):
+            raise ValueError("flip must be 0 or 1")
+        out = torch.empty(weight.numel(), dtype=torch.float32, device=weight.device)
+        weights.append(weight)
+        outs.append(out)
+        dims.extend((*(int(v) for v in weight.shape), int(flip)))
+    count = len(requests)
+    _call("mfh_conv_weight_orders", (ctypes.c_uint64 * count)(*(w.data_ptr() for w in weights)),
+          (ctypes.c_uint64 * count)(*(o.data_ptr() for o in outs)), (ctypes.c_int * len(dims))(*dims), count,
+          _stream())
+    return outs
+
+
+def _weight_order_buffer(order, weight, name):
+    order = _device_f32(order, name)
+    if order.numel() != weight.numel() or order.data_ptr() % 16:
+        raise ValueError(f"{name} must be a 16-byte aligned float32 tensor of the kernel's size")
+    return order
+
+
 def conv2d_forward(x, weight, bias=None, *, stride=(1, 1), padding=(0, 0), activation=None, alpha=0.0,
-                   engine="mfma", algorithm=None):
+                   engine="mfma", algorithm=None, weight_order=None):
     """(y, cols): the contiguous NCHW output with bias and activation applied, and the im2col
     columns of x that conv2d_backward needs for dW. With algorithm "implicit" (the default) the GEMM
-    gathers the columns from x itself and cols is None; "im2col" writes and returns them."""
+    gathers the columns from x itself and cols is None; "im2col" writes and returns them.
+    weight_order: this kernel from conv_weight_orders(flip 0), which the implicit product then reads
+    instead of reordering the kernel itself."""
     engine = _engine_code(engine)
     algorithm = _conv_algorithm(algorithm)
     x, weight = _device_f32(x, "x"), _device_f32(weight, "weight")
@@ -396,9 +441,15 @@ def conv2d_forward(x, weight, bias=None, *, stride=(1, 1), padding=(0, 0), activ
     y = torch.empty(g.out_shape, dtype=torch.float32, device=device)
     if algorithm == "implicit":
         workspace, floats = _implicit_workspace(g, "forward")
-        wt = torch.empty_like(weight) if g.ci % 16 == 0 else None  # the kernel in chunked feature order
-        _call("mfh_conv_forward_implicit", x.data_ptr(), weight.data_ptr(), _addr(wt), _addr(bias), y.data_ptr(),
-              *g.c_args(), act, alpha, engine, _addr(workspace), floats, _stream())
+        prepared = 0
+        wt = None
+        if implicit_chunked(g.ci):  # the kernel in chunked feature order
+            if weight_order is not None:
+                wt, prepared = _weight_order_buffer(weight_order, weight, "weight_order"), 1
+            else:
+                wt = torch.empty_like(weight)
+        _call("mfh_conv_forward_implicit", x.data_ptr(), weight.data_ptr(), _addr(wt), prepared, _addr(bias),
+              y.data_ptr(), *g.c_args(), act, alpha, engine, _addr(workspace), floats, _stream())
         return y, None
     cols = torch.empty((g.m, g.k), dtype=torch.float32, device=device)
     rows = None
@@ -415,11 +466,14 @@ def conv2d_forward(x, weight, bias=None, *, stride=(1, 1), padding=(0, 0), activ
 
 def conv2d_backward(x, weight, grad_y, cols, *, stride=(1, 1), padding=(0, 0), need_bias_grad=True,
                     need_input_grad=True, need_weight_grad=True, activation=None, alpha=0.0, output=None,
-                    engine="mfma", recompute_cols=False, algorithm=None):
+                    engine="mfma", recompute_cols=False, algorithm=None, weight_flip=None, input_grad=None):
     """(dx, dw, db), None for each gradient not requested; a fused activation gates grad_y through
     output. algorithm "im2col" computes dW from the forward's cols (recomputed from x when
     recompute_cols); "implicit" gathers them from x inside the GEMM. Without an algorithm, a call
-    that passes cols (and does not recompute them) takes "im2col", any other the default."""
+    that passes cols (and does not recompute them) takes "im2col", any other the default.
+    Implicit only: weight_flip is this kernel from conv_weight_orders(flip 1) for a stride-1 dX;
+    input_grad is a gradient of x already there, to which dX is added in place (it is then the
+    returned dx)."""
     engine = _engine_code(engine)
     if algorithm is None and cols is not None and not recompute_cols:
         algorithm = "im2col"
@@ -431,7 +485,9 @@ def conv2d_backward(x, weight, grad_y, cols, *, stride=(1, 1), padding=(0, 0), n
         raise ValueError("grad_y does not have the convolution's output shape")
     if algorithm == "implicit":
         return _conv2d_backward_implicit(x, weight, grad_y, g, need_bias_grad, need_input_grad, need_weight_grad,
-                                         act, alpha, output, engine)
+                                         act, alpha, output, engine, weight_flip, input_grad)
+    if weight_flip is not None or input_grad is not None:
+        raise ValueError("weight_flip and input_grad apply to the implicit algorithm only")
     if need_weight_grad:
         cols = (conv2d_im2col(x, tuple(weight.shape), stride=stride, padding=padding) if recompute_cols
                 else _device_f32(cols, "cols"))
@@ -466,7 +522,7 @@ def conv2d_backward(x, weight, grad_y, cols, *, stride=(1, 1), padding=(0, 0), n
 
 
 def _conv2d_backward_implicit(x, weight, grad_y, g, need_bias_grad, need_input_grad, need_weight_grad, act, alpha,
-                              output, engine):
+                              output, engine, weight_flip=None, input_grad=None):
     gate = None
     if act:
         if output is None:
@@ -479,18 +535,33 @@ def _conv2d_backward_implicit(x, weight, grad_y, g, need_bias_grad, need_input_g
     device = x.device
     empty = lambda *shape, dtype=torch.float32: torch.empty(shape, dtype=dtype, device=device)
     unit_stride = g.sh == 1 and g.sw == 1
+    flags = 0
     gated = torch.empty_like(grad_y) if act else None
     dw = torch.empty_like(weight) if need_weight_grad else None
-    dx = torch.empty_like(x) if need_input_grad else None
-    wflip = empty(g.ci * g.co * g.kh * g.kw) if need_input_grad and unit_stride else None
+    dx = None
+    if need_input_grad:
+        if input_grad is not None:
+            if (not isinstance(input_grad, torch.Tensor) or input_grad.dtype != torch.float32
+                    or tuple(input_grad.shape) != tuple(x.shape) or not input_grad.is_contiguous()
+                    or input_grad.device != device):
+                raise ValueError("input_grad must be a contiguous float32 tensor of x's shape on x's device")
+            dx, flags = input_grad, flags | CONV_ACCUMULATE_DX
+        else:
+            dx = torch.empty_like(x)
+    wflip = None
+    if need_input_grad and unit_stride:
+        if weight_flip is not None:
+            wflip, flags = _weight_order_buffer(weight_flip, weight, "weight_flip"), flags | CONV_WFLIP_READY
+        else:
+            wflip = empty(g.ci * g.co * g.kh * g.kw)
     grad_cols = empty(g.m * g.k) if need_input_grad and not unit_stride else None
-    partial = empty(g.n * g.co, dtype=torch.float64) if need_bias_grad else None
+    partial = empty(max(g.n, BIAS_PARTIAL_ROWS) * g.co, dtype=torch.float64) if need_bias_grad else None
     db = empty(g.co) if need_bias_grad else None
     passes = (("dw",) if need_weight_grad else ()) + (("dx",) if need_input_grad and unit_stride else ())
     workspace, floats = _implicit_workspace(g, *passes)
     _call("mfh_conv_backward_implicit", x.data_ptr(), weight.data_ptr(), grad_y.data_ptr(), _addr(gate),
           _addr(gated), _addr(dw), _addr(dx), _addr(wflip), _addr(grad_cols), _addr(partial), _addr(db),
-          *g.c_args(), act, alpha, engine, engine, _addr(workspace), floats, _stream())
+          *g.c_args(), act, alpha, engine, engine, flags, _addr(workspace), floats, _stream())
     return dx, dw, db
 
 

@@ -79,18 +79,64 @@ class Conv2D_Op(GradientOp):
         self.recompute_im2col = bool(recompute_im2col)
         self._activation_fused = False
         self._saved = None
+        self._orders = {}  # phase -> (kernel tensor, its reordered copy) handed over by the Graph
 
     def _activation_alpha(self):
         return 0.0
+
+    def _implicit(self):
+        return native.default_conv_algorithm() == "implicit"
+
+    def weight_orders(self, phase):
+        """The kernel reorders this node's next forward ("forward") or backward ("backward") pass
+        reads, as (kernel, flip) requests: a Graph batches them over every convolution of a pass
+        into one launch (native.conv_weight_orders) and hands the results to take_weight_orders."""
+        kernel = self.parents[1].value
+        if not self._implicit() or not isinstance(kernel, torch.Tensor) or kernel.device.type != "cuda":
+            return []  # the operator's own forward reports what is wrong with a non-GPU kernel
+        if phase == "forward":
+            if kernel.ndim != 4 or not native.implicit_chunked(kernel.shape[1]):
+                return []
+            return [(kernel, 0)]
+        if self._saved is None or not self.parents[0].requires_grad or self.stride != (1, 1):
+            return []
+        return [(self._saved[1], 1)]
+
+    def take_weight_orders(self, phase, tensors):
+        kernel = self.parents[1].value if phase == "forward" else self._saved[1]
+        self._orders[phase] = (kernel, kernel._version, tensors[0])
+
+    def drop_weight_orders(self, phase):
+        self._orders.pop(phase, None)
+
+    def _order_for(self, phase, kernel):
+        """The reordered kernel handed over for this pass, if it was made from this kernel tensor
+        as it is now (same object, no in-place change since); used once."""
+        handed = self._orders.pop(phase, None)
+        if handed is None or handed[0] is not kernel or handed[1] != kernel._version:
+            return None
+        return handed[2]
+
+    @staticmethod
+    def _grad_target(node, like):
+        """node's gradient as an in-place dX target (contiguous float32 of x's shape), else None."""
+        grad = node.grad
+        if (isinstance(grad, torch.Tensor) and grad.dtype == torch.float32 and grad.shape == like.shape
+                and grad.is_contiguous() and grad.device == like.device):
+            return node.grad_buffer()[0]
+        return None
 
     def forward(self, x_val, kernel_val, bias_val=None):
         self.actual_backend = _resolve_backend(self.backend, x_val, kernel_val, bias_val)
         if self.bias is not None and bias_val is None:
             raise ValueError("bias value is missing")
+        self._orders.pop("backward", None)
+        order = self._order_for("forward", kernel_val)
+        extra = {"weight_order": order} if order is not None else {}
         self.value, cols = native.conv2d_forward(
             x_val, kernel_val, bias_val, stride=self.stride, padding=self.padding,
             activation=self.fused_activation, alpha=self._activation_alpha(),
-            engine=NATIVE_BACKENDS[self.actual_backend])
+            engine=NATIVE_BACKENDS[self.actual_backend], **extra)
         self._activation_fused = self.fused_activation is not None
         keep_cols = self.parents[1].requires_grad and not self.recompute_im2col
         self._saved = (x_val, kernel_val, cols if keep_cols else None) if self.requires_grad else None
@@ -105,14 +151,25 @@ class Conv2D_Op(GradientOp):
         if not (need_x or need_w or need_b):
             return
         x_val, kernel_val, cols = self._saved
+        extra = {}
+        implicit = self._implicit() and (cols is None or self.recompute_im2col)
+        if implicit:
+            flip = self._order_for("backward", kernel_val)
+            if flip is not None:
+                extra["weight_flip"] = flip
+            target = self._grad_target(x_node, x_val) if need_x else None
+            if target is not None:  # dX is added to the gradient x already has, in the same pass
+                extra["input_grad"] = target
         grads = native.conv2d_backward(
             x_val, kernel_val, self.grad, cols, stride=self.stride, padding=self.padding, need_bias_grad=need_b,
             need_weight_grad=need_w, need_input_grad=need_x,
             activation=self.fused_activation if self._activation_fused else None, alpha=self._activation_alpha(),
-            output=self.value, engine=NATIVE_BACKENDS[self.actual_backend], recompute_cols=self.recompute_im2col)
+            output=self.value, engine=NATIVE_BACKENDS[self.actual_backend], recompute_cols=self.recompute_im2col,
+            **({"algorithm": "implicit"} if implicit else {}), **extra)
         for parent, grad in zip(self.parents, grads):
-            if grad is not None:
-                parent.accumulate_grad(grad, owned=True)
+            if grad is None or ("input_grad" in extra and parent is x_node):
+                continue
+            parent.accumulate_grad(grad, owned=True)
 
 
 class Conv2D_ReLU_Op(Conv2D_Op):

@@ -260,3 +260,72 @@ def test_rows_path_forward_matches_the_nchw_gemm(case, monkeypatch):
     _, _, _, _, pre = fp64_case(case)
     assert_near(host(direct), np.maximum(pre, 0), 1e-5, "direct")
     assert_near(host(rows), np.maximum(pre, 0), 1e-5, "rows")
+
+
+def permuted_kernel(w, flip):
+    """The kernel in the order an implicit product reads it, by plain tensor permutes: rows co over
+    features (ci, tap) (flip 0), or rows ci over (co, KH*KW-1-tap) (flip 1); a multiple of 32
+    channels takes the chunked order (channel chunk, tap, channel within the chunk)."""
+    co, ci, kh, kw = w.shape
+    t = w.reshape(co, ci, kh * kw)
+    if flip:
+        t = t.flip(2).transpose(0, 1)
+    rows, channels, taps = t.shape
+    if channels % 32 == 0:
+        t = t.reshape(rows, channels // 32, 32, taps).permute(0, 1, 3, 2)
+    return t.contiguous().reshape(-1)
+
+
+def test_batched_weight_orders_match_the_permutation():
+    """One conv_weight_orders call over more kernels than one launch takes (several launches), both
+    orders, chunked and natural channel counts: each result equals the permuted kernel bit for bit."""
+    g = torch.Generator().manual_seed(11)
+    shapes = [case[2] for case in RESNET_CASES] + [(32, 96, 3, 3), (64, 32, 1, 1), (5, 7, 2, 3), (40, 64, 3, 3),
+                                                    (64, 40, 3, 3), (32, 32, 5, 5)]
+    requests = []
+    for i in range(2 * len(shapes) + 7):
+        w = torch.randn(shapes[(i // 2) % len(shapes)], generator=g).cuda()
+        requests.append((w, i % 2))
+    made = native.conv_weight_orders(requests)
+    assert len(made) == len(requests)
+    for (w, flip), out in zip(requests, made):
+        np.testing.assert_array_equal(host(out), host(permuted_kernel(w, flip)), err_msg=f"{tuple(w.shape)} {flip}")
+
+
+@pytest.mark.parametrize("case", (RESNET_CASES[1], RESNET_CASES[2], RESNET_CASES[3], RESNET_CASES[4],
+                                  RESNET_CASES[5], PERFORMANCE_CASES[0]), ids=lambda c: c[0])
+def test_prepared_orders_and_in_place_dx_give_the_same_bits(case):
+    """A forward that reads a prepared kernel order, a stride-1 dX that reads a prepared flipped
+    kernel and a dX added in place to an existing gradient give exactly the results of the plain
+    calls (the in-place add is the same float32 addition as a separate one)."""
+    print("prepared", case[0], flush=True)
+    x, w, b, dy = (gpu(a) for a in conv_fixture(case))
+    stride, padding = case[3], case[4]
+    plain_y, _ = native.conv2d_forward(x, w, b, stride=stride, padding=padding, algorithm="implicit")
+    order, flip = native.conv_weight_orders([(w, 0), (w, 1)])
+    prepared_y, _ = native.conv2d_forward(x, w, b, stride=stride, padding=padding, algorithm="implicit",
+                                          weight_order=order)
+    np.testing.assert_array_equal(host(prepared_y), host(plain_y))
+    dx, dw, db = native.conv2d_backward(x, w, dy, None, stride=stride, padding=padding, algorithm="implicit")
+    existing = torch.randn(x.shape, generator=torch.Generator().manual_seed(5)).cuda()
+    expected = host(existing) + host(dx)
+    extra = {"weight_flip": flip} if stride == (1, 1) else {}
+    dx2, dw2, db2 = native.conv2d_backward(x, w, dy, None, stride=stride, padding=padding, algorithm="implicit",
+                                           input_grad=existing, **extra)
+    assert dx2 is existing
+    np.testing.assert_array_equal(host(dx2), expected)
+    np.testing.assert_array_equal(host(dw2), host(dw))
+    np.testing.assert_array_equal(host(db2), host(db))
+
+
+@pytest.mark.parametrize("case", (RESNET_CASES[0], RESNET_CASES[1], RESNET_CASES[4]), ids=lambda c: c[0])
+def test_bias_gradient_with_and_without_the_weight_product(case):
+    """db rides on the dW product when dW is requested (FP64 sums per pixel slice) and takes the
+    per-image row sums otherwise: both within one float32 ulp of the FP64 sum."""
+    x, w, _, dy = (gpu(a) for a in conv_fixture(case))
+    ref = conv_fixture(case)[3].astype(np.float64).sum(axis=(0, 2, 3))
+    for need_w in (True, False):
+        _, dw, db = native.conv2d_backward(x, w, dy, None, stride=case[3], padding=case[4], algorithm="implicit",
+                                           need_input_grad=False, need_weight_grad=need_w)
+        assert (dw is not None) == need_w
+        assert np.all(np.abs(host(db) - ref) <= np.spacing(np.abs(ref).astype(np.float32))), need_w

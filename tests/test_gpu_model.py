@@ -219,3 +219,22 @@ def test_resnet18_inference_with_bn_folding_and_conv_relu_epilogue():
     _, _, out32 = oracle_resnet.forward_backward(params32, {k: (m.copy(), v.copy()) for k, (m, v) in running32.items()},
                                                  x_np, t_np, training=False)
     assert normwise(got, out64) <= max(4 * normwise(out32, out64), 1e-5)
+
+
+def test_batched_kernel_orders_and_in_place_dx_reproduce_the_per_call_path(monkeypatch):
+    """The Graph reorders every convolution kernel of a pass in one launch and adds dX into an
+    existing input gradient in place; turning both off (each convolution reorders its own kernel,
+    dX goes through a separate add) gives the same bits."""
+    from myflows_amd import graph as graph_module, ops_conv
+
+    runs = []
+    for batched in (True, False):
+        if not batched:
+            monkeypatch.setattr(graph_module, "_prepare_weight_orders", lambda units, phase: ())
+            monkeypatch.setattr(ops_conv.Conv2D_Op, "_grad_target", staticmethod(lambda node, like: None))
+        model, graph, out, _, _, _ = build_resnet(2, 64, 64, base_width=32, optimize=True)
+        graph.forward()
+        graph.backward()
+        runs.append([host(out.value)] + [host(p.grad) for p in model.params])
+    for a, b in zip(*runs):
+        np.testing.assert_array_equal(a, b)
