@@ -13,6 +13,10 @@ over the timed steps.
 time measured with HIP events on the launch stream, against the 157.3 TFLOP/s FP32 matrix peak.
 ``cpu_baseline`` is the NumPy restatement of the reference CPU path (oracle/resnet.py) timed on this
 host on a bounded sample: full forward + backward + Adam steps of ResNet18 at batch 2 (config 1).
+The other configurations are reported beside the headline: ``c2_gemms`` (the standalone GEMMs of
+config 2 against the FP32 matrix peak), ``c3_kernels`` (config 3's im2col and max-pool kernels
+against the HBM peak, its convolution against the matrix peak) and ``c5_inference`` (config 5,
+ResNet18 inference at batch 256, 224x224, with BN folded into the convolutions).
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline] [--plain-graph]
 """
@@ -189,6 +193,64 @@ def c3_kernels():
     return out
 
 
+def c2_gemms(reps=20):
+    """the standalone FP32 GEMMs C = A B (A, B ~ N(0, 1) seed 0) at M=N=K in
+    {512, 1024, 2048, 4096}, the im2col-shaped 38400 x 64 x 576 product and its dW form A^T B
+    (A stored 38400 x 576, B 38400 x 64, C 576 x 64), each under the automatic plan; TFLOP/s from
+    HIP events over `reps` launches against the FP32 matrix peak."""
+    out = {"peak_TFLOP/s": FP32_MFMA_PEAK_TFLOPS}
+    g = torch.Generator().manual_seed(0)
+    cases = [(f"{n}^3", n, n, n, False) for n in (512, 1024, 2048, 4096)]
+    cases += [("im2col 38400x64x576", 38400, 64, 576, False), ("dW A^T B 576x64 over 38400", 576, 64, 38400, True)]
+    for name, m, n, k, trans_a in cases:
+        a = torch.randn((k, m) if trans_a else (m, k), generator=g).cuda()
+        b = torch.randn((k, n), generator=g).cuda()
+        c = torch.empty((m, n), device="cuda")
+        us = _event_time_us(lambda: native.gemm(a, b, trans_a=trans_a, out=c), reps=reps)
+        tflops = 2.0 * m * n * k / (us * 1e-6) / 1e12
+        tile, slices = native.gemm_plan(m, n, k, layout="TN" if trans_a else "NN")
+        out[name] = {"us": round(us, 2), "TFLOP/s": round(tflops, 2), "frac": round(tflops / FP32_MFMA_PEAK_TFLOPS, 3),
+                     "plan": f"tile {tile} slices {slices}"}
+        del a, b, c
+    return out
+
+
+# Algorithmic work of one bs256 224x224 ResNet18 forward (convolutions + fc), 3.594 GFLOP per image.
+C5_STEP_GFLOP = 920.2
+
+
+def c5_inference(batch=256, size=224, reps=10, warmup=3, seed=0):
+    """ResNet18(output_dim=2) inference at batch 256, 3x224x224 ~ N(0, 1), eval-mode
+    batch norm with running variance ~ U(0.5, 1.5) and mean ~ N(0, 0.1) (seeded), BN folded into the
+    convolutions and ReLU fused into their epilogues (apply_graph_optimizations(mode="inference"),
+    then Graph(optimize=True)). Images per second over `reps` forward passes."""
+    model = mf.ResNet18(output_dim=2, initializer=mf.make_initializer(seed=seed), conv_backend="hip_native")
+    rng = np.random.default_rng(seed)
+    x_np = rng.standard_normal((batch, 3, size, size)).astype(np.float32)
+    bns = [model.stem_bn] + [bn for block in model.blocks()
+                             for bn in (block.bn1, block.bn2, *((block.downsample_bn,) if block.downsample else ()))]
+    for bn in bns:
+        bn.running_mean.copy_(torch.as_tensor(rng.normal(0, 0.1, bn.num_features).astype(np.float32)))
+        bn.running_var.copy_(torch.as_tensor(rng.uniform(0.5, 1.5, bn.num_features).astype(np.float32)))
+    model.eval()
+    out = model(mf.Variable(torch.as_tensor(x_np, device="cuda"), requires_grad=False, name="images"))
+    root, stats = mf.apply_graph_optimizations(out, mode="inference", fold_constants=False)
+    graph = mf.Graph(root, optimize=True)
+    for _ in range(warmup):
+        graph.forward()
+    torch.cuda.synchronize()
+    start = time.perf_counter()
+    for _ in range(reps):
+        graph.forward()
+    torch.cuda.synchronize()
+    seconds = time.perf_counter() - start
+    ms = seconds * 1e3 / reps
+    return {"config": f"ResNet18 inference bs{batch} 3x{size}x{size}, BN folded, Conv+ReLU epilogues",
+            "images/s": round(batch * reps / seconds, 1), "ms_per_batch": round(ms, 3),
+            "TFLOP/s": round(C5_STEP_GFLOP * batch / 256 / (ms * 1e-3) / 1e3, 2), "bn_folds": stats["bn_folds"],
+            "conv_act_fusions": graph._opt_stats["conv_act_fusions"]}
+
+
 def cpu_baseline(min_seconds=10.0, batch=2):
     """The NumPy reference-path ResNet18 step (forward + backward + Adam) on this host."""
     from oracle import resnet as oracle_resnet
@@ -249,7 +311,9 @@ def main():
                    "graph": "optimize=False" if args.plain_graph else "optimize=True (BN+ReLU, BN+Add+ReLU units)"},
         "step_tflops": round(STEP_GFLOP * args.batch / 64 / (ms_per_step * 1e-3) / 1e3, 2),
         "roofline": roofline,
+        "c2_gemms": c2_gemms(),
         "c3_kernels": c3_kernels(),
+        "c5_inference": c5_inference(),
     }
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline()

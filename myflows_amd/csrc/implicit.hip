@@ -345,21 +345,23 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void conv_implicit_wgra
 // C = CO, out[ci][(co, tap)] = w[co][ci][T - 1 - tap], the flipped and transposed kernel.
 // One launch writes up to ORDER_BATCH orders: order i owns the workgroups [first_block[i],
 // first_block[i + 1]).
-//   * Chunked orders with at most TILE_TAPS taps go through LDS, one workgroup per 32 output rows x
-//     one chunk of 32 channels: both the reads and the writes are contiguous runs of 32*T floats
-//     (forward: the row's 32*T source floats of that chunk; dX: for each of the chunk's 32 output
-//     channels, the 32*T floats of the 32 rows' input channels).
+//   * Chunked orders with at most TILE_TAPS taps go through LDS, one workgroup per TILE_ROWS output
+//     rows x one chunk of 32 channels: the reads and the writes are contiguous runs (forward: each
+//     row's 32*T source floats of that chunk; dX: for each of the chunk's 32 output channels, the
+//     TILE_ROWS*T floats of the rows' input channels; writes: each row's 32*T floats).
 //   * Other orders (natural channel counts, wider windows) take one output element per thread.
 constexpr int ORDER_BATCH = 32;
 constexpr int TILE_TAPS = 9;
-constexpr int TILE_STRIDE = 32 * TILE_TAPS + 1;  // floats per channel-within-chunk slab of the LDS tile
+constexpr int TILE_ROWS = 8;
+constexpr int TILE_STRIDE = TILE_ROWS * TILE_TAPS + 1;  // floats per channel-within-chunk slab of the LDS tile
 struct OrderJob {
     const float* w;
     float* out;
     int O, C, T, chunked, flip, total;
     int tiled;               // LDS path: blocks are (row block, chunk), chunk fastest
     FastDiv div_row, div_t;  // by C * T, by T
-    FastDiv div_panel;       // by 32 * T
+    FastDiv div_panel;       // by 32 * T (a destination run)
+    FastDiv div_run;         // by the length of a source run: 32 * T (forward) or TILE_ROWS * T (dX)
     FastDiv div_chunks;      // by C / 32
 };
 struct OrderBatch {
@@ -368,58 +370,63 @@ struct OrderBatch {
     int count;
 };
 
-// Elements a thread moves per batch of the tiled path: their loads are all issued before the
-// first LDS store (the loop is otherwise one global-load latency per element).
+// Elements a thread moves per batch of the tiled path (TILE_ROWS * 32 * T / 256 = T at most 9):
+// all of its loads are issued before the first LDS store.
 constexpr int ORDER_UNROLL = 12;
+static_assert(TILE_ROWS * 32 * TILE_TAPS <= 256 * ORDER_UNROLL, "one batch covers a workgroup's tile");
 
 __device__ __forceinline__ void order_tiled(const OrderJob& job, int block, float* tile) {
-    const int T = job.T, panel = 32 * T, per_thread = panel / 8;  // 32 * panel elements / 256 threads
+    const int T = job.T, panel = 32 * T, per_thread = TILE_ROWS * T / 8;  // TILE_ROWS*32*T / 256
     int chunk;
     const int ob = job.div_chunks.divmod(block, chunk);
-    const int rows = min(32, job.O - ob * 32);
+    const int rows = min(TILE_ROWS, job.O - ob * TILE_ROWS);
     const long long row_len = static_cast<long long>(job.C) * T;
-    // Source run s (flip: output channel co = chunk*32 + s of W, over the rows' input channels and
-    // all taps; forward: output row ob*32 + s, over the chunk's 32 input channels and all taps).
-    const float* src = job.flip ? job.w + static_cast<long long>(chunk) * 32 * job.O * T + static_cast<long long>(ob) * panel
-                                : job.w + static_cast<long long>(ob) * 32 * row_len + static_cast<long long>(chunk) * panel;
+    // Source run s (flip: output channel co = chunk*32 + s of W over the rows' input channels and all
+    // taps, TILE_ROWS*T floats; forward: output row ob*TILE_ROWS + s over the chunk's 32 input
+    // channels and all taps, 32*T floats).
+    const float* src =
+        job.flip ? job.w + static_cast<long long>(chunk) * 32 * job.O * T + static_cast<long long>(ob) * TILE_ROWS * T
+                 : job.w + static_cast<long long>(ob) * TILE_ROWS * row_len + static_cast<long long>(chunk) * panel;
     const long long run_stride = job.flip ? static_cast<long long>(job.O) * T : row_len;
-    for (int base = 0; base < per_thread; base += ORDER_UNROLL) {
-        float v[ORDER_UNROLL];
-        int slot[ORDER_UNROLL];
+    float v[ORDER_UNROLL];
+    int slot[ORDER_UNROLL];
 #pragma unroll
-        for (int u = 0; u < ORDER_UNROLL; ++u) {
-            const int idx = threadIdx.x + (base + u) * 256;
-            slot[u] = -1;
-            v[u] = 0.0f;
-            if (base + u < per_thread) {
-                int e;
-                const int run = job.div_panel.divmod(idx, e);
-                int tap;
-                const int q = job.div_t.divmod(e, tap);  // flip: row r = q; forward: channel j = q
-                const int r = job.flip ? q : run, j = job.flip ? run : q;
-                if (r < rows) {
-                    v[u] = src[run * run_stride + e];
-                    slot[u] = j * TILE_STRIDE + r * T + (job.flip ? T - 1 - tap : tap);
-                }
+    for (int u = 0; u < ORDER_UNROLL; ++u) {
+        const int idx = threadIdx.x + u * 256;
+        slot[u] = -1;
+        v[u] = 0.0f;
+        if (u < per_thread) {
+            int e;
+            const int run = job.div_run.divmod(idx, e);
+            int tap;
+            const int q = job.div_t.divmod(e, tap);  // flip: row r = q; forward: channel j = q
+            const int r = job.flip ? q : run, j = job.flip ? run : q;
+            if (r < rows) {
+                v[u] = src[run * run_stride + e];
+                slot[u] = j * TILE_STRIDE + r * T + (job.flip ? T - 1 - tap : tap);
             }
         }
-#pragma unroll
-        for (int u = 0; u < ORDER_UNROLL; ++u)
-            if (slot[u] >= 0) tile[slot[u]] = v[u];
     }
+#pragma unroll
+    for (int u = 0; u < ORDER_UNROLL; ++u)
+        if (slot[u] >= 0) tile[slot[u]] = v[u];
     __syncthreads();
-    // Destination run r: row ob*32 + r, features (chunk, tap, j) = tap*32 + j within the chunk.
-    float* dst = job.out + static_cast<long long>(ob) * 32 * row_len + static_cast<long long>(chunk) * panel;
-    for (int idx = threadIdx.x; idx < 32 * panel; idx += 256) {
-        int d;
-        const int r = job.div_panel.divmod(idx, d);
-        const int tap = d / 32, j = d % 32;
-        if (r < rows) dst[r * row_len + d] = tile[j * TILE_STRIDE + r * T + tap];
+    // Destination run r: row ob*TILE_ROWS + r, features (chunk, tap, j) = tap*32 + j within the chunk.
+    float* dst = job.out + static_cast<long long>(ob) * TILE_ROWS * row_len + static_cast<long long>(chunk) * panel;
+#pragma unroll
+    for (int u = 0; u < ORDER_UNROLL; ++u) {
+        const int idx = threadIdx.x + u * 256;
+        if (u < per_thread) {
+            int d;
+            const int r = job.div_panel.divmod(idx, d);
+            const int tap = d / 32, j = d % 32;
+            if (r < rows) dst[r * row_len + d] = tile[j * TILE_STRIDE + r * T + tap];
+        }
     }
 }
 
 __global__ __launch_bounds__(256) void weight_order_kernel(OrderBatch batch) {
-    __shared__ float tile[32 * TILE_STRIDE];
+    __shared__ float tile[CHANNEL_CHUNK * TILE_STRIDE];
     int j = 0;
     while (j + 1 < batch.count && static_cast<int>(blockIdx.x) >= batch.first_block[j + 1]) ++j;
     const OrderJob& job = batch.job[j];
@@ -749,9 +756,10 @@ int launch_weight_orders(const WeightOrder* orders, int count, hipStream_t strea
             job.div_t = FastDiv(o.taps);
             job.tiled = job.chunked && o.taps <= TILE_TAPS ? 1 : 0;
             job.div_panel = FastDiv(32 * o.taps);
+            job.div_run = FastDiv((o.flip ? TILE_ROWS : 32) * o.taps);
             job.div_chunks = FastDiv(std::max(1, channels / CHANNEL_CHUNK));
             batch.first_block[i] = blocks;
-            blocks += static_cast<int>(job.tiled ? blocks_for(rows, 32) * (channels / CHANNEL_CHUNK)
+            blocks += static_cast<int>(job.tiled ? blocks_for(rows, TILE_ROWS) * (channels / CHANNEL_CHUNK)
                                                  : blocks_for(job.total, 256));
         }
         batch.first_block[batch.count] = blocks;
