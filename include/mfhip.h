@@ -96,7 +96,8 @@ MFH_API int mfh_conv_backward(uint64_t weight, uint64_t dy, uint64_t y, uint64_t
  * 16-byte aligned): with prepared = 0 this call writes it there from `weight`; with prepared = 1
  * wt already holds it (mfh_conv_weight_orders, flip 0) and `weight` is not read (it may be 0).
  * Otherwise wt is unused and may be 0. workspace: mfh_conv_implicit_workspace(..., 0) floats let
- * it split K (0 is allowed: no split). Arguments otherwise as mfh_conv_forward.
+ * it split K (0 is allowed: no split). engine: 1 (automatic plan) or 16 + tile * 128 + slices - 1
+ * over the 12 tiles of the implicit products. Arguments otherwise as mfh_conv_forward.
  * Has no single counterpart in the reference: it replaces the im2col + gemm_rows + epilogue sequence
  * of mf_conv_forward, native_cublas.cpp:1441-1461, when the caller does not keep cols. */
 MFH_API int mfh_conv_forward_implicit(uint64_t x, uint64_t weight, uint64_t wt, int prepared, uint64_t bias,
@@ -140,6 +141,8 @@ MFH_API int64_t mfh_conv_implicit_workspace(int N, int CI, int H, int W, int CO,
  *          gradient W^T dy_n in grad_cols (N*CI*KH*KW*OH*OW floats) and the col2im gather.
  *          With MFH_CONV_ACCUMULATE_DX, dx = dx + the gradient (one rounding, as a separate add).
  * workspace: at least the larger of mfh_conv_implicit_workspace passes 1 and 2 that are requested.
+ * dw_engine and a stride-1 dx_engine are implicit plan codes (as mfh_conv_forward_implicit); the
+ * dx_engine of other strides is a GEMM engine code (as mfh_gemm).
  * Has no single counterpart in the reference: it replaces mf_conv_backward_plans,
  * native_cublas.cpp:1465-1532, when the caller does not keep cols. */
 MFH_API int mfh_conv_backward_implicit(uint64_t x, uint64_t weight, uint64_t dy, uint64_t y, uint64_t gated,

@@ -318,7 +318,7 @@ MFH_API int mfh_conv_forward_implicit(std::uint64_t x, std::uint64_t weight, std
     const ConvGeometry g{N, CI, H, W, CO, KH, KW, OH, OW, SH, SW, PH, PW};
     MFH_TRY(validate(g));
     MFH_TRY(validate_activation(activation, alpha));
-    MFH_TRY(validate_engine(engine));
+    MFH_REQUIRE(implicit_engine_valid(engine), "unknown implicit convolution engine or plan code");
     MFH_REQUIRE(x && y && (weight || (prepared && wt)), "conv forward received a null buffer");
     MFH_REQUIRE(wt || !implicit_chunked(CI), "the implicit forward needs the reordered-kernel buffer wt");
     MFH_REQUIRE(prepared == 0 || prepared == 1, "prepared must be 0 or 1");
@@ -368,10 +368,12 @@ MFH_API int mfh_conv_backward_implicit(std::uint64_t x, std::uint64_t weight, st
     const ConvGeometry g{N, CI, H, W, CO, KH, KW, OH, OW, SH, SW, PH, PW};
     MFH_TRY(validate(g));
     MFH_TRY(validate_activation(activation, alpha));
-    MFH_TRY(validate_engine(dw_engine));
-    MFH_TRY(validate_engine(dx_engine));
     const bool gated_dy = activation != ACT_NONE;
     const bool unit_stride = SH == 1 && SW == 1;
+    // dW and the stride-1 dX are implicit products; other strides' dX is a dense GEMM.
+    MFH_REQUIRE(implicit_engine_valid(dw_engine), "unknown implicit convolution engine or plan code");
+    if (unit_stride) MFH_REQUIRE(implicit_engine_valid(dx_engine), "unknown implicit convolution engine or plan code");
+    else MFH_TRY(validate_engine(dx_engine));
     const bool prepared = (flags & MFH_CONV_WFLIP_READY) != 0, accumulate = (flags & MFH_CONV_ACCUMULATE_DX) != 0;
     MFH_REQUIRE((flags & ~(MFH_CONV_WFLIP_READY | MFH_CONV_ACCUMULATE_DX)) == 0, "unknown conv backward flags");
     MFH_REQUIRE(dy && (weight || (unit_stride && prepared)), "conv backward needs weight and dy");

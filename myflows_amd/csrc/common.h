@@ -210,6 +210,8 @@ struct ConvGather {
 constexpr int IMPLICIT_FORWARD = 0, IMPLICIT_WGRAD = 1, IMPLICIT_DGRAD = 2;
 // Split-K workspace floats of one pass of the implicit convolution under the automatic plan.
 std::int64_t implicit_workspace_floats(const ConvGeometry& g, int pass);
+// Whether an engine code names the automatic plan or a tile and split of the implicit products.
+bool implicit_engine_valid(int engine);
 // Whether the implicit kernels take a convolution over C input channels in chunked feature order.
 inline bool implicit_chunked(int C) { return C % CHANNEL_CHUNK == 0; }
 // y = act(conv(x, w) + bias), NCHW, without an im2col buffer. When C is chunked the product reads

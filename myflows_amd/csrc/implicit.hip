@@ -86,10 +86,11 @@ struct GatherFeatureRows {
     }
 };
 
-// The same tile in chunked feature order: stage kt covers channels [c0, c0 + 16) at one tap.
+// The same tile in chunked feature order: stage kt covers channels [c0, c0 + 32) at one tap. The
+// tap is uniform over the stage, so a wave may span two rows (BN a multiple of 32).
 template <int BN, int THREADS>
 struct GatherChunkRows {
-    static_assert(BN % 64 == 0 && THREADS % BN == 0, "rows split over whole waves");
+    static_assert(BN % 32 == 0 && THREADS % BN == 0, "whole rows per thread group");
     static constexpr int RSTEP = THREADS / BN, PER = BK / RSTEP;
     static_assert(BK == CHANNEL_CHUNK && BK % RSTEP == 0, "one stage is one channel chunk");
     int origin, ih0, iw0;
@@ -475,7 +476,9 @@ using ConvFn = void (*)(GemmParams, ConvGather);
 
 // Tile catalogue of the implicit products: block tile BM x BN, wave tile WM x WN. The 64 x 64 wave
 // tiles keep four independent MFMA accumulators per wave and read half as much LDS per MFMA as
-// 32 x 32 ones; tiles 6 and 7 (32 x 32 waves) serve outputs too small to fill the GPU otherwise.
+// 32 x 32 ones; the tiles of 32 x 32 (or 32 x 64) waves serve the batch-64 products, whose outputs
+// are too small to fill the GPU with large waves. Tile 11's 96-pixel columns exist only for the
+// chunked forward orientation.
 struct ImplicitTile {
     int bm, bn, wm, wn;
 };
@@ -488,9 +491,19 @@ constexpr ImplicitTile TILE_TABLE[] = {
     {256, 64, 64, 64},   // 5: four waves
     {64, 64, 32, 32},    // 6: four 32 x 32 waves
     {32, 64, 32, 32},    // 7: two 32 x 32 waves
+    {64, 128, 32, 32},   // 8: eight 32 x 32 waves
+    {128, 64, 32, 32},   // 9: eight 32 x 32 waves
+    {128, 128, 32, 64},  // 10: eight 32 x 64 waves
+    {128, 96, 32, 32},   // 11: twelve 32 x 32 waves (chunked forward only)
 };
 constexpr int TILE_COUNT = sizeof(TILE_TABLE) / sizeof(TILE_TABLE[0]);
 constexpr int threads_of(const ImplicitTile& t) { return (t.bm / t.wm) * (t.bn / t.wn) * 64; }
+// Which kernels a tile has: the natural-order forward loader reads whole waves of one feature row
+// (BN a multiple of 64); the dW loaders split BM and BN rows evenly over THREADS / BK_WG threads.
+constexpr bool has_natural(const ImplicitTile& t) { return t.bn % 64 == 0; }
+constexpr bool has_wgrad(const ImplicitTile& t) {
+    return t.bn % 64 == 0 && t.bm % (threads_of(t) / BK_WG) == 0 && t.bn % (threads_of(t) / BK_WG) == 0;
+}
 
 template <int T, bool VA, bool CHUNKED>
 constexpr ConvFn forward_of() {
@@ -513,11 +526,15 @@ struct ConvKernels {
     WgradFn wgrad[TILE_COUNT][2] = {};
     template <int T>
     void fill() {
-        forward[T][0] = forward_of<T, false, false>();
-        forward[T][1] = forward_of<T, true, false>();
+        if constexpr (has_natural(TILE_TABLE[T])) {
+            forward[T][0] = forward_of<T, false, false>();
+            forward[T][1] = forward_of<T, true, false>();
+        }
         forward[T][2] = forward_of<T, true, true>();
-        wgrad[T][0] = wgrad_of<T, false>();
-        wgrad[T][1] = wgrad_of<T, true>();
+        if constexpr (has_wgrad(TILE_TABLE[T])) {
+            wgrad[T][0] = wgrad_of<T, false>();
+            wgrad[T][1] = wgrad_of<T, true>();
+        }
     }
     ConvKernels() {
         fill<0>();
@@ -528,9 +545,20 @@ struct ConvKernels {
         fill<5>();
         fill<6>();
         fill<7>();
+        fill<8>();
+        fill<9>();
+        fill<10>();
+        fill<11>();
     }
 };
-static_assert(TILE_COUNT == 8, "ConvKernels fills every tile");
+static_assert(TILE_COUNT == 12, "ConvKernels fills every tile");
+
+// Whether tile `tile` has a kernel for this product (dW, or the forward orientation in chunked or
+// natural feature order).
+bool tile_available(int tile, bool wgrad, bool chunked) {
+    const ImplicitTile& t = TILE_TABLE[tile];
+    return wgrad ? has_wgrad(t) : (chunked || has_natural(t));
+}
 
 const ConvKernels& conv_kernels() {
     static const ConvKernels table;
@@ -576,8 +604,9 @@ struct PlannerModel {
     double hbm_bytes_per_s;  // achieved rate of the split-K partial traffic
     double launch_s;         // cost of the extra reduction launch
 };
-constexpr PlannerModel FORWARD_MODEL = {{0.49, 0.53, 0.54, 0.43, 0.32, 0.49, 0.56, 0.42}, 6.0e12, 2.0e-6};
-constexpr PlannerModel WGRAD_MODEL = {{0.57, 0.37, 0.49, 0.72, 0.56, 0.34, 0.55, 0.32}, 3.0e12, 2.0e-6};
+// Tiles 8-11 have no fitted efficiency (0): the model leaves them to the measured plans below.
+constexpr PlannerModel FORWARD_MODEL = {{0.49, 0.53, 0.54, 0.43, 0.32, 0.49, 0.56, 0.42, 0, 0, 0, 0}, 6.0e12, 2.0e-6};
+constexpr PlannerModel WGRAD_MODEL = {{0.57, 0.37, 0.49, 0.72, 0.56, 0.34, 0.55, 0.32, 0, 0, 0, 0}, 3.0e12, 2.0e-6};
 constexpr double SIMD_MACS_PER_S = 157.3e12 / 2 / 1024;  // FP32 multiply-adds per second per SIMD
 constexpr int SPLIT_CHOICES[] = {1, 2, 3, 4, 6, 8, 12, 16, 24, 32, 48, 64, 96, 128};
 
@@ -624,14 +653,45 @@ GemmPlan wgrad_plan(int M, int N, int K) {
     return whole_stages(tile, K, requested, BK_WG);
 }
 
-// The plan of least estimated cost of a forward-orientation (forward, dX) product, or the dW rule.
-GemmPlan implicit_auto_plan(bool wgrad, int M, int N, int K) {
+// Measured plans: products whose best tile and split, in a sweep of every tile and split on MI355X,
+// beat the automatic plan below by at least 2 % (ResNet18's batch-64 convolutions at 3x120x160).
+// Key: orientation (0 forward / dX, 1 dW), M, N, K; value: tile and requested K split.
+struct MeasuredPlan {
+    int wgrad, M, N, K, tile, requested;
+};
+constexpr MeasuredPlan MEASURED_PLANS[] = {
+    {0, 64, 307200, 147, 8, 1},    // stem forward
+    {0, 128, 19200, 576, 11, 1},   // layer2.0 conv1 forward (stride 2)
+    {0, 128, 19200, 1152, 11, 1},  // layer2 3x3 forward and dX
+    {0, 128, 19200, 64, 11, 1},    // layer2 1x1 downsample forward
+    {0, 256, 5120, 1152, 9, 3},    // layer3.0 conv1 forward
+    {0, 256, 5120, 2304, 9, 3},    // layer3 3x3 forward and dX
+    {0, 256, 5120, 128, 9, 1},     // layer3 1x1 downsample forward
+    {0, 512, 1280, 2304, 9, 6},    // layer4.0 conv1 forward
+    {0, 512, 1280, 4608, 9, 6},    // layer4 3x3 forward and dX
+    {1, 64, 576, 72384, 8, 96},    // layer1 dW
+    {1, 128, 576, 19200, 10, 48},  // layer2.0 conv1 dW
+    {1, 128, 1152, 19200, 10, 48}, // layer2 3x3 dW
+    {1, 128, 64, 19200, 6, 128},   // layer2 1x1 downsample dW
+    {1, 256, 1152, 5120, 9, 32},   // layer3.0 conv1 dW
+    {1, 512, 2304, 1280, 9, 8},    // layer4.0 conv1 dW
+    {1, 512, 4608, 1280, 8, 8},    // layer4 3x3 dW
+};
+
+// The plan of a product: a measured plan when one matches, else the dW rule, else the plan of least
+// estimated cost (forward orientation).
+GemmPlan implicit_auto_plan(bool wgrad, int M, int N, int K, bool chunked) {
+    for (const MeasuredPlan& m : MEASURED_PLANS)
+        if (m.wgrad == (wgrad ? 1 : 0) && m.M == M && m.N == N && m.K == K && tile_available(m.tile, wgrad, chunked) &&
+            tile_fits(m.tile, M))
+            return whole_stages(m.tile, K, m.requested, wgrad ? BK_WG : BK);
     if (wgrad && tile_fits(3, M) && tile_fits(6, M)) return wgrad_plan(M, N, K);
     const int bk = wgrad ? BK_WG : BK;
+    const PlannerModel& model = wgrad ? WGRAD_MODEL : FORWARD_MODEL;
     GemmPlan best{-1, 1, K};
     double best_cost = 0.0;
     for (int tile = 0; tile < TILE_COUNT; ++tile) {
-        if (!tile_fits(tile, M)) continue;
+        if (!tile_fits(tile, M) || model.efficiency[tile] <= 0.0 || !tile_available(tile, wgrad, chunked)) continue;
         for (const int requested : SPLIT_CHOICES) {
             if (requested > 1 && K / requested < bk) break;
             const GemmPlan plan = whole_stages(tile, K, requested, bk);
@@ -649,14 +709,16 @@ GemmPlan implicit_auto_plan(bool wgrad, int M, int N, int K) {
 // The plan of a product from an engine code (1 = automatic; 16 + tile * 128 + slices - 1 names a
 // tile of TILE_TABLE and a requested K split); the split is dropped when the workspace cannot hold
 // it.
-int implicit_plan(bool wgrad, int engine, int M, int N, int K, float* workspace, std::int64_t workspace_floats,
-                  GemmPlan* plan) {
+int implicit_plan(bool wgrad, bool chunked, int engine, int M, int N, int K, float* workspace,
+                  std::int64_t workspace_floats, GemmPlan* plan) {
     if (engine == 1) {
-        *plan = implicit_auto_plan(wgrad, M, N, K);
+        *plan = implicit_auto_plan(wgrad, M, N, K, chunked);
     } else {
         const int code = engine - 16;
         const int tile = code / 128, requested = code % 128 + 1;
         if (code < 0 || tile >= TILE_COUNT) return MFH_FAIL(ERR_ARG, "unknown implicit convolution plan code");
+        if (!tile_available(tile, wgrad, chunked))
+            return MFH_FAIL(ERR_ARG, "this implicit convolution tile has no kernel for this product");
         *plan = whole_stages(tile, K, requested, wgrad ? BK_WG : BK);
     }
     if (plan->tile < 0 || !tile_fits(plan->tile, M))
@@ -725,11 +787,13 @@ int run_implicit(bool wgrad, const GemmPlan& plan, const float* a, int lda, int 
 
 }  // namespace
 
+bool implicit_engine_valid(int engine) { return engine == 1 || (engine >= 16 && engine < 16 + TILE_COUNT * 128); }
+
 std::int64_t implicit_workspace_floats(const ConvGeometry& g, int pass) {
     GemmPlan plan;
-    if (pass == IMPLICIT_FORWARD) plan = implicit_auto_plan(false, g.CO, g.rows(), g.features());
-    else if (pass == IMPLICIT_WGRAD) plan = implicit_auto_plan(true, g.CO, g.features(), g.rows());
-    else plan = implicit_auto_plan(false, g.CI, g.N * g.H * g.W, g.CO * g.KH * g.KW);
+    if (pass == IMPLICIT_FORWARD) plan = implicit_auto_plan(false, g.CO, g.rows(), g.features(), implicit_chunked(g.CI));
+    else if (pass == IMPLICIT_WGRAD) plan = implicit_auto_plan(true, g.CO, g.features(), g.rows(), implicit_chunked(g.CI));
+    else plan = implicit_auto_plan(false, g.CI, g.N * g.H * g.W, g.CO * g.KH * g.KW, implicit_chunked(g.CO));
     return pass == IMPLICIT_WGRAD ? gemm_workspace_floats(plan, g.CO, g.features())
                                   : gemm_workspace_floats(plan, pass == IMPLICIT_FORWARD ? g.CO : g.CI,
                                                           pass == IMPLICIT_FORWARD ? g.rows() : g.N * g.H * g.W);
@@ -775,7 +839,7 @@ int conv_implicit_forward(const ConvGeometry& g, const float* x, const float* w,
                           std::int64_t workspace_floats, hipStream_t stream) {
     const int M = g.CO, N = g.rows(), K = g.features();
     GemmPlan plan;
-    MFH_TRY(implicit_plan(false, engine, M, N, K, workspace, workspace_floats, &plan));
+    MFH_TRY(implicit_plan(false, implicit_chunked(g.CI), engine, M, N, K, workspace, workspace_floats, &plan));
     const ConvGather gather = gather_of(x, g.CI, g.H, g.W, g.KH, g.KW, g.SH, g.SW, g.PH, g.PW, g.N, g.OH, g.OW);
     if (gather.chunked) {
         if (!prepared) {
@@ -798,7 +862,7 @@ int conv_implicit_wgrad(const ConvGeometry& g, const float* x, const float* dy, 
                         float* db, int engine, float* workspace, std::int64_t workspace_floats, hipStream_t stream) {
     const int M = g.CO, N = g.features(), K = g.rows();
     GemmPlan plan;
-    MFH_TRY(implicit_plan(true, engine, M, N, K, workspace, workspace_floats, &plan));
+    MFH_TRY(implicit_plan(true, implicit_chunked(g.CI), engine, M, N, K, workspace, workspace_floats, &plan));
     if (db && (!bias_partial || plan.slices > WGRAD_MAX_SLICES))
         return MFH_FAIL(ERR_ARG, "the dW plan's bias partials need bias_partial rows for every pixel slice");
     const ConvGather gather = gather_of(x, g.CI, g.H, g.W, g.KH, g.KW, g.SH, g.SW, g.PH, g.PW, g.N, g.OH, g.OW);
@@ -812,12 +876,12 @@ int conv_implicit_dgrad(const ConvGeometry& g, const float* dy, const float* w, 
                         hipStream_t stream) {
     const int khw = g.KH * g.KW;
     const int M = g.CI, N = g.N * g.H * g.W, K = g.CO * khw;
+    GemmPlan plan;
+    MFH_TRY(implicit_plan(false, implicit_chunked(g.CO), engine, M, N, K, workspace, workspace_floats, &plan));
     if (!prepared) {
         const WeightOrder order{w, wflip, g.CO, g.CI, khw, 1};
         MFH_TRY(launch_weight_orders(&order, 1, stream));
     }
-    GemmPlan plan;
-    MFH_TRY(implicit_plan(false, engine, M, N, K, workspace, workspace_floats, &plan));
     // dy as the source of a stride-1 convolution with padding KH-1-PH whose output grid is H x W.
     const ConvGather gather =
         gather_of(dy, g.CO, g.OH, g.OW, g.KH, g.KW, 1, 1, g.KH - 1 - g.PH, g.KW - 1 - g.PW, g.N, g.H, g.W);

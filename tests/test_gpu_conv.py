@@ -329,3 +329,55 @@ def test_bias_gradient_with_and_without_the_weight_product(case):
                                            need_input_grad=False, need_weight_grad=need_w)
         assert (dw is not None) == need_w
         assert np.all(np.abs(host(db) - ref) <= np.spacing(np.abs(ref).astype(np.float32))), need_w
+
+
+IMPLICIT_TILES = 12  # tiles of the implicit products (plan code 16 + tile * 128 + slices - 1)
+
+
+@pytest.mark.parametrize("case", (RESNET_CASES[1], ("l2s", (2, 128, 15, 20), (128, 128, 3, 3), (1, 1), (1, 1))),
+                         ids=lambda c: c[0])
+def test_every_implicit_tile_is_exact_on_integer_data(case):
+    """Each tile of the implicit catalogue (forced through its plan code, unsplit and split over K)
+    gives the FP64 loops' forward, dX, dW and db bit for bit on integer data; a tile without a dW
+    kernel (the 96-pixel one) is refused with a reason instead of launched."""
+    _, x_shape, w_shape, stride, padding = case
+    print("tiles", case[0], flush=True)
+    rng = np.random.default_rng(17)
+    x = rng.integers(-2, 3, size=x_shape).astype(np.float32)
+    w = rng.integers(-2, 3, size=w_shape).astype(np.float32)
+    n, co = x_shape[0], w_shape[0]
+    oh, ow = rp.out_size(x_shape[2], x_shape[3], w_shape[2:], stride, padding)
+    dy = rng.integers(-2, 3, size=(n, co, oh, ow)).astype(np.float32)
+    x64, w64, dy64 = x.astype(np.float64), w.astype(np.float64), dy.astype(np.float64)
+    ref_y = naive.conv_forward(x64, w64, stride, padding)
+    ref_dx, ref_dw = naive.conv_backward(x64, w64, dy64, stride, padding)
+    ref_db = dy64.sum(axis=(0, 2, 3))
+    g = native.ConvGeometry.of(x_shape, w_shape, stride, padding)
+    lib, stream = native._library(), torch.cuda.current_stream().cuda_stream
+    xg, wg, dyg = gpu(x), gpu(w), gpu(dy)
+    order, flip = native.conv_weight_orders([(wg, 0), (wg, 1)])
+    y, dx, dw = torch.empty(g.out_shape, device="cuda"), torch.empty_like(xg), torch.empty_like(wg)
+    db = torch.empty(co, device="cuda")
+    partial = torch.empty(max(n, native.BIAS_PARTIAL_ROWS) * co, dtype=torch.float64, device="cuda")
+    workspace = torch.empty(1 << 24, device="cuda")
+    for tile in range(IMPLICIT_TILES):
+        for slices in (1, 3):
+            code = native.PLAN_BASE + tile * native.PLAN_SLICES + slices - 1
+            native._raise_for(lib.mfh_conv_forward_implicit(
+                xg.data_ptr(), wg.data_ptr(), order.data_ptr(), 1, 0, y.data_ptr(), *g.c_args(), 0, 0.0, code,
+                workspace.data_ptr(), workspace.numel(), stream), lib)
+            native._raise_for(lib.mfh_conv_backward_implicit(
+                xg.data_ptr(), wg.data_ptr(), dyg.data_ptr(), 0, 0, 0, dx.data_ptr(), flip.data_ptr(), 0, 0, 0,
+                *g.c_args(), 0, 0.0, 1, code, native.CONV_WFLIP_READY, workspace.data_ptr(), workspace.numel(),
+                stream), lib)
+            np.testing.assert_array_equal(host(y), ref_y, err_msg=f"forward tile {tile} slices {slices}")
+            np.testing.assert_array_equal(host(dx), ref_dx, err_msg=f"dX tile {tile} slices {slices}")
+            status = lib.mfh_conv_backward_implicit(
+                xg.data_ptr(), wg.data_ptr(), dyg.data_ptr(), 0, 0, dw.data_ptr(), 0, 0, 0, partial.data_ptr(),
+                db.data_ptr(), *g.c_args(), 0, 0.0, code, 1, 0, workspace.data_ptr(), workspace.numel(), stream)
+            if tile == 11:
+                assert status == 2 and "no kernel" in lib.mfh_last_error().decode()
+                continue
+            native._raise_for(status, lib)
+            np.testing.assert_array_equal(host(dw), ref_dw, err_msg=f"dW tile {tile} slices {slices}")
+            np.testing.assert_array_equal(host(db), ref_db, err_msg=f"db tile {tile} slices {slices}")
