@@ -17,6 +17,9 @@
 // applies them. Every sum has a fixed order (four interleaved chains per thread, then lanes, waves
 // and slices), so results are reproducible; every workgroup finalises a channel with the same
 // arithmetic, so they all agree.
+// When a channel has at most CHANNEL_FUSED_MAX positions it is a single slice, and each pass is one
+// launch of one workgroup per channel (norm_forward_channel / norm_backward_channel): the partial
+// sums, the finalisation and the element pass in a row, with the arithmetic of the two-launch path.
 #include "common.h"
 #include "fastdiv.h"
 
@@ -30,6 +33,7 @@ constexpr int APPLY_THREADS = 256;
 constexpr int APPLY_ELEMS = 4;    // elements per thread in norm_apply / norm_dx
 constexpr int APPLY_SPAN = APPLY_THREADS * APPLY_ELEMS;
 constexpr int MAX_PLANES = 128;   // (n, c) planes a workgroup finalises at once; more are taken in rounds
+constexpr int CHANNEL_FUSED_MAX = 8192;  // positions per channel up to which a pass is one launch
 
 enum PartialMode { STATS = 0, GRADS = 1 };
 
@@ -73,10 +77,9 @@ __device__ __forceinline__ void workgroup_sum(double& a, double& b) {
 
 // Workgroup (s, c) sums slice s of channel c. Each thread runs CHAINS interleaved chains (positions
 // j, j + PT, j + 2 PT, j + 3 PT, then the next 4 PT), so CHAINS loads are in flight at a time; the
-// chains are added in chain order at the end.
+// chains are added in chain order at the end. The sums are valid in thread 0.
 template <int MODE>
-__global__ __launch_bounds__(PT) void norm_partials_kernel(PartialArgs p) {
-    const int s = blockIdx.x, c = blockIdx.y, slices = gridDim.x;
+__device__ __forceinline__ void channel_partial(const PartialArgs& p, int c, int s, double& sa, double& sb) {
     const int j0 = s * p.chunk, j1 = min(p.total, j0 + p.chunk);
     const int plane = p.C * p.HW;
     // STATS: shift by the channel's first element; GRADS: centre on the saved FP64 mean (hi + lo).
@@ -114,13 +117,21 @@ __global__ __launch_bounds__(PT) void norm_partials_kernel(PartialArgs p) {
             }
         }
     }
-    double sa = a[0], sb = b[0];
+    sa = a[0];
+    sb = b[0];
 #pragma unroll
     for (int u = 1; u < CHAINS; ++u) {
         sa += a[u];
         sb += b[u];
     }
     workgroup_sum(sa, sb);
+}
+
+template <int MODE>
+__global__ __launch_bounds__(PT) void norm_partials_kernel(PartialArgs p) {
+    const int s = blockIdx.x, c = blockIdx.y, slices = gridDim.x;
+    double sa, sb;
+    channel_partial<MODE>(p, c, s, sa, sb);
     if (threadIdx.x == 0) {
         p.partial[(static_cast<long long>(c) * slices + s) * 2] = sa;
         p.partial[(static_cast<long long>(c) * slices + s) * 2 + 1] = sb;
@@ -177,6 +188,51 @@ __device__ __forceinline__ void planes_of(int e0, int total, const FastDiv& div_
     p1 = div_hw.div(min(total, e0 + APPLY_SPAN) - 1);
 }
 
+// A channel's forward coefficients from its FP64 (shifted sum, second sum) when training, else from
+// the running statistics: the mean as the float pair hi + lo, inv_std rounded once.
+struct ApplyCoef {
+    double mu, var;
+    float hi, lo, istd;
+};
+__device__ __forceinline__ ApplyCoef apply_coef(const ApplyArgs& p, int c, double sum, double sq) {
+    ApplyCoef k;
+    if (p.training) {
+        const double shifted = sum / p.count;
+        k.var = fmax(sq / p.count - shifted * shifted, 0.0);
+        k.mu = static_cast<double>(p.x[c * p.HW]) + shifted;
+    } else {
+        k.mu = static_cast<double>(p.running_mean[c]);
+        k.var = static_cast<double>(p.running_var[c]);
+    }
+    k.hi = static_cast<float>(k.mu);
+    k.lo = static_cast<float>(k.mu - static_cast<double>(k.hi));
+    k.istd = static_cast<float>(1.0 / sqrt(k.var + p.eps));
+    return k;
+}
+
+// The saved mean / inv_std of channel c and, when training, its running statistics.
+__device__ __forceinline__ void store_statistics(const ApplyArgs& p, int c, const ApplyCoef& k) {
+    p.mean[c] = k.hi;
+    p.mean[p.C + c] = k.lo;
+    p.inv_std[c] = k.istd;
+    if (p.training) {
+        p.running_mean[c] =
+            static_cast<float>((1.0 - p.momentum) * static_cast<double>(p.running_mean[c]) + p.momentum * k.mu);
+        p.running_var[c] = static_cast<float>((1.0 - p.momentum) * static_cast<double>(p.running_var[c]) +
+                                              p.momentum * k.var * p.var_scale);
+    }
+}
+
+// y = (((x - hi) - lo) * inv_std) * gamma + beta [+ residual] [ReLU], rounded per operation.
+__device__ __forceinline__ float apply_value(const ApplyArgs& p, float x, float r, float m_hi, float m_lo, float istd,
+                                             float g, float b) {
+#pragma clang fp contract(off)
+    float v = (((x - m_hi) - m_lo) * istd) * g + b;
+    if (p.residual) v = v + r;
+    if (p.relu) v = v < 0.0f ? 0.0f : v;  // NaN stays NaN
+    return v;
+}
+
 // norm_apply with the statistics finalised in the workgroup: coefficients (hi, lo, inv_std, gamma,
 // beta) of the planes it touches go to LDS, then every element is normalised.
 template <int VEC>
@@ -192,43 +248,23 @@ __global__ __launch_bounds__(APPLY_THREADS) void norm_apply_kernel(ApplyArgs p) 
             const int pl = first + i;
             int c;
             p.div_c.divmod(pl, c);
-            double mu, var;
-            if (p.training) {
-                double sum, sq;
-                slice_sums(p.partial, c, p.slices, sum, sq);
-                const double shifted = sum / p.count;
-                var = fmax(sq / p.count - shifted * shifted, 0.0);
-                mu = static_cast<double>(p.x[c * p.HW]) + shifted;
-            } else {
-                mu = static_cast<double>(p.running_mean[c]);
-                var = static_cast<double>(p.running_var[c]);
-            }
-            const float hi = static_cast<float>(mu);
-            const float lo = static_cast<float>(mu - static_cast<double>(hi));
-            const float istd = static_cast<float>(1.0 / sqrt(var + p.eps));
-            coef[0][i] = hi;
-            coef[1][i] = lo;
-            coef[2][i] = istd;
+            double sum = 0.0, sq = 0.0;
+            if (p.training) slice_sums(p.partial, c, p.slices, sum, sq);
+            const ApplyCoef k = apply_coef(p, c, sum, sq);
+            coef[0][i] = k.hi;
+            coef[1][i] = k.lo;
+            coef[2][i] = k.istd;
             coef[3][i] = p.gamma[c];
             coef[4][i] = p.beta[c];
-            if (pl < p.C && static_cast<long long>(pl) * p.HW >= e0) {  // image 0's plane of channel c starts here
-                p.mean[c] = hi;
-                p.mean[p.C + c] = lo;
-                p.inv_std[c] = istd;
-                if (p.training) {
-                    p.running_mean[c] = static_cast<float>((1.0 - p.momentum) * static_cast<double>(p.running_mean[c]) +
-                                                           p.momentum * mu);
-                    p.running_var[c] = static_cast<float>((1.0 - p.momentum) * static_cast<double>(p.running_var[c]) +
-                                                          p.momentum * var * p.var_scale);
-                }
-            }
+            if (pl < p.C && static_cast<long long>(pl) * p.HW >= e0)  // image 0's plane of channel c starts here
+                store_statistics(p, c, k);
         }
         __syncthreads();
         const int lo_e = max(e0, first * p.HW), hi_e = min(min(p.total, e0 + APPLY_SPAN), (last + 1) * p.HW);
         for (int e = lo_e + threadIdx.x * VEC; e < hi_e; e += APPLY_THREADS * VEC) {
             const int i = p.div_hw.div(e) - first;  // all VEC elements share a plane (HW % VEC == 0)
             const float m_hi = coef[0][i], m_lo = coef[1][i], istd = coef[2][i], g = coef[3][i], b = coef[4][i];
-            float xv[VEC], rv[VEC], out[VEC];
+            float xv[VEC], rv[VEC] = {}, out[VEC];
             if constexpr (VEC == 4) {
                 const float4 x4 = *reinterpret_cast<const float4*>(p.x + e);
                 xv[0] = x4.x; xv[1] = x4.y; xv[2] = x4.z; xv[3] = x4.w;
@@ -241,17 +277,42 @@ __global__ __launch_bounds__(APPLY_THREADS) void norm_apply_kernel(ApplyArgs p) 
                 if (p.residual) rv[0] = p.residual[e];
             }
 #pragma unroll
-            for (int u = 0; u < VEC; ++u) {
-                float v = (((xv[u] - m_hi) - m_lo) * istd) * g + b;
-                if (p.residual) v = v + rv[u];
-                if (p.relu) v = v < 0.0f ? 0.0f : v;  // NaN stays NaN
-                out[u] = v;
-            }
+            for (int u = 0; u < VEC; ++u) out[u] = apply_value(p, xv[u], rv[u], m_hi, m_lo, istd, g, b);
             if constexpr (VEC == 4) *reinterpret_cast<float4*>(p.y + e) = make_float4(out[0], out[1], out[2], out[3]);
             else p.y[e] = out[0];
         }
         __syncthreads();
     }
+}
+
+// A channel's dx coefficients from its FP64 (sum g, sum g (x - mean)): dx = a ((g - k1) - x_hat k2)
+// when training (a g otherwise), and dgamma.
+struct DxCoef {
+    double dgamma;
+    float a, k1, k2;
+};
+__device__ __forceinline__ DxCoef dx_coef(const DxArgs& p, int c, double sdy, double sdyx) {
+    DxCoef k;
+    const double istd = static_cast<double>(p.inv_std[c]);
+    k.dgamma = istd * sdyx;
+    k.a = static_cast<float>(static_cast<double>(p.gamma[c]) * istd);
+    k.k1 = p.training ? static_cast<float>(sdy / p.count) : 0.0f;
+    k.k2 = p.training ? static_cast<float>(istd * k.dgamma / p.count) : 0.0f;
+    return k;
+}
+
+__device__ __forceinline__ void store_param_grads(const DxArgs& p, int c, const DxCoef& k, double sdy) {
+    if (p.gamma_grad)
+        p.gamma_grad[c] = p.add_gamma ? p.gamma_grad[c] + static_cast<float>(k.dgamma) : static_cast<float>(k.dgamma);
+    if (p.beta_grad) p.beta_grad[c] = p.add_beta ? p.beta_grad[c] + static_cast<float>(sdy) : static_cast<float>(sdy);
+}
+
+__device__ __forceinline__ float dx_value(const DxArgs& p, float x, float dy, float gate, float prev, float a, float k1,
+                                          float k2, float m_hi, float m_lo) {
+#pragma clang fp contract(off)
+    const float g = p.gate && !(gate > 0.0f) ? 0.0f : dy;
+    const float v = p.training ? a * ((g - k1) - ((x - m_hi) - m_lo) * k2) : a * g;
+    return p.add ? prev + v : v;
 }
 
 // norm_dx with dgamma / dbeta and the dx coefficients finalised in the workgroup.
@@ -270,19 +331,13 @@ __global__ __launch_bounds__(APPLY_THREADS) void norm_dx_kernel(DxArgs p) {
             p.div_c.divmod(pl, c);
             double sdy = 0.0, sdyx = 0.0;
             if (p.sums) slice_sums(p.partial, c, p.slices, sdy, sdyx);
-            const double istd = static_cast<double>(p.inv_std[c]);
-            const double dgamma = istd * sdyx;
-            coef[0][i] = static_cast<float>(static_cast<double>(p.gamma[c]) * istd);
-            coef[1][i] = p.training ? static_cast<float>(sdy / p.count) : 0.0f;
-            coef[2][i] = p.training ? static_cast<float>(istd * dgamma / p.count) : 0.0f;
+            const DxCoef k = dx_coef(p, c, sdy, sdyx);
+            coef[0][i] = k.a;
+            coef[1][i] = k.k1;
+            coef[2][i] = k.k2;
             coef[3][i] = p.mean[c];
             coef[4][i] = p.mean[p.C + c];
-            if (pl < p.C && static_cast<long long>(pl) * p.HW >= e0) {
-                if (p.gamma_grad)
-                    p.gamma_grad[c] = p.add_gamma ? p.gamma_grad[c] + static_cast<float>(dgamma) : static_cast<float>(dgamma);
-                if (p.beta_grad)
-                    p.beta_grad[c] = p.add_beta ? p.beta_grad[c] + static_cast<float>(sdy) : static_cast<float>(sdy);
-            }
+            if (pl < p.C && static_cast<long long>(pl) * p.HW >= e0) store_param_grads(p, c, k, sdy);
         }
         __syncthreads();
         if (p.dx) {
@@ -290,7 +345,7 @@ __global__ __launch_bounds__(APPLY_THREADS) void norm_dx_kernel(DxArgs p) {
             for (int e = lo_e + threadIdx.x * VEC; e < hi_e; e += APPLY_THREADS * VEC) {
                 const int i = p.div_hw.div(e) - first;
                 const float a = coef[0][i], k1 = coef[1][i], k2 = coef[2][i], m_hi = coef[3][i], m_lo = coef[4][i];
-                float xv[VEC], gv[VEC], tv[VEC], prev[VEC];
+                float xv[VEC], gv[VEC], tv[VEC] = {}, prev[VEC] = {};
                 if constexpr (VEC == 4) {
                     const float4 x4 = *reinterpret_cast<const float4*>(p.x + e);
                     const float4 d4 = *reinterpret_cast<const float4*>(p.dy + e);
@@ -312,19 +367,126 @@ __global__ __launch_bounds__(APPLY_THREADS) void norm_dx_kernel(DxArgs p) {
                 }
                 float out[VEC];
 #pragma unroll
-                for (int u = 0; u < VEC; ++u) {
-                    const float g = p.gate && !(tv[u] > 0.0f) ? 0.0f : gv[u];
-                    float v;
-                    if (p.training) v = a * ((g - k1) - ((xv[u] - m_hi) - m_lo) * k2);
-                    else v = a * g;
-                    out[u] = p.add ? prev[u] + v : v;
-                }
+                for (int u = 0; u < VEC; ++u) out[u] = dx_value(p, xv[u], gv[u], tv[u], prev[u], a, k1, k2, m_hi, m_lo);
                 if constexpr (VEC == 4)
                     *reinterpret_cast<float4*>(p.dx + e) = make_float4(out[0], out[1], out[2], out[3]);
                 else p.dx[e] = out[0];
             }
         }
         __syncthreads();
+    }
+}
+
+// One workgroup per channel when a channel is a single slice (at most CHANNEL_FUSED_MAX positions):
+// the partial-sum pass, the finalisation and the element pass of norm_apply (forward) or norm_dx
+// (backward) in one launch. Thread t holds the channel's positions j = t + i * PT (i < CHANNEL_PER)
+// in registers, loaded once, and adds them into the same four chains in the same order as
+// channel_partial, so the results are the bits of the two-launch path. Position j is
+// (n, hw) = (j / HW, j % HW).
+constexpr int CHANNEL_PER = CHANNEL_FUSED_MAX / PT;
+
+__global__ __launch_bounds__(PT) void norm_forward_channel_kernel(PartialArgs pa, ApplyArgs p) {
+    __shared__ float coef[3];
+    const int c = blockIdx.x, total = pa.total, plane = p.C * p.HW;
+    const double centre = static_cast<double>(p.x[c * p.HW]);
+    float xv[CHANNEL_PER];
+    int at[CHANNEL_PER];
+#pragma unroll
+    for (int i = 0; i < CHANNEL_PER; ++i) {
+        const int j = threadIdx.x + i * PT;
+        int hw;
+        const int n = p.div_hw.divmod(j < total ? j : 0, hw);
+        at[i] = n * plane + c * p.HW + hw;
+        xv[i] = j < total ? p.x[at[i]] : 0.0f;
+    }
+    double a[CHAINS] = {}, b[CHAINS] = {};
+#pragma unroll
+    for (int i = 0; i < CHANNEL_PER; ++i) {
+        if (threadIdx.x + i * PT >= total) continue;
+        const double d = static_cast<double>(xv[i]) - centre;
+        a[i % CHAINS] += d;
+        b[i % CHAINS] = fma(d, d, b[i % CHAINS]);
+    }
+    double sa = a[0], sb = b[0];
+#pragma unroll
+    for (int u = 1; u < CHAINS; ++u) {
+        sa += a[u];
+        sb += b[u];
+    }
+    workgroup_sum(sa, sb);
+    if (threadIdx.x == 0) {
+        double sum = 0.0, sq = 0.0;  // the one-slice slice_sums
+        sum += sa;
+        sq += sb;
+        const ApplyCoef k = apply_coef(p, c, sum, sq);
+        coef[0] = k.hi;
+        coef[1] = k.lo;
+        coef[2] = k.istd;
+        store_statistics(p, c, k);
+    }
+    __syncthreads();
+    const float m_hi = coef[0], m_lo = coef[1], istd = coef[2], g = p.gamma[c], bt = p.beta[c];
+#pragma unroll
+    for (int i = 0; i < CHANNEL_PER; ++i) {
+        if (threadIdx.x + i * PT >= total) continue;
+        const float r = p.residual ? p.residual[at[i]] : 0.0f;
+        p.y[at[i]] = apply_value(p, xv[i], r, m_hi, m_lo, istd, g, bt);
+    }
+}
+
+__global__ __launch_bounds__(PT) void norm_backward_channel_kernel(PartialArgs pa, DxArgs p) {
+    __shared__ float coef[3];
+    const int c = blockIdx.x, total = pa.total, plane = p.C * p.HW;
+    const double centre = static_cast<double>(p.mean[c]) + static_cast<double>(p.mean[p.C + c]);
+    float xv[CHANNEL_PER], dv[CHANNEL_PER], tv[CHANNEL_PER];
+    int at[CHANNEL_PER];
+#pragma unroll
+    for (int i = 0; i < CHANNEL_PER; ++i) {
+        const int j = threadIdx.x + i * PT;
+        int hw;
+        const int n = p.div_hw.divmod(j < total ? j : 0, hw);
+        at[i] = n * plane + c * p.HW + hw;
+        const bool in = j < total;
+        xv[i] = in ? p.x[at[i]] : 0.0f;
+        dv[i] = in ? p.dy[at[i]] : 0.0f;
+        tv[i] = in && p.gate ? p.gate[at[i]] : 0.0f;
+    }
+    double a[CHAINS] = {}, b[CHAINS] = {};
+#pragma unroll
+    for (int i = 0; i < CHANNEL_PER; ++i) {
+        if (threadIdx.x + i * PT >= total) continue;
+        const float gv = p.gate && !(tv[i] > 0.0f) ? 0.0f : dv[i];
+        if (pa.residual_grad)
+            pa.residual_grad[at[i]] = pa.add_residual ? pa.residual_grad[at[i]] + gv : gv;
+        const double d = static_cast<double>(xv[i]) - centre;
+        a[i % CHAINS] += static_cast<double>(gv);
+        b[i % CHAINS] = fma(static_cast<double>(gv), d, b[i % CHAINS]);
+    }
+    double sa = a[0], sb = b[0];
+#pragma unroll
+    for (int u = 1; u < CHAINS; ++u) {
+        sa += a[u];
+        sb += b[u];
+    }
+    workgroup_sum(sa, sb);
+    if (threadIdx.x == 0) {
+        double sdy = 0.0, sdyx = 0.0;  // the one-slice slice_sums
+        sdy += sa;
+        sdyx += sb;
+        const DxCoef k = dx_coef(p, c, sdy, sdyx);
+        coef[0] = k.a;
+        coef[1] = k.k1;
+        coef[2] = k.k2;
+        store_param_grads(p, c, k, sdy);
+    }
+    __syncthreads();
+    if (!p.dx) return;
+    const float ka = coef[0], k1 = coef[1], k2 = coef[2], m_hi = p.mean[c], m_lo = p.mean[p.C + c];
+#pragma unroll
+    for (int i = 0; i < CHANNEL_PER; ++i) {
+        if (threadIdx.x + i * PT >= total) continue;
+        const float prev = p.add ? p.dx[at[i]] : 0.0f;
+        p.dx[at[i]] = dx_value(p, xv[i], dv[i], tv[i], prev, ka, k1, k2, m_hi, m_lo);
     }
 }
 
@@ -341,6 +503,7 @@ bool aligned16(const void* q) { return (reinterpret_cast<std::uintptr_t>(q) & 15
 
 int norm_slices(const NormShape& s) {
     const std::int64_t positions = static_cast<std::int64_t>(s.N) * s.HW;
+    if (positions <= CHANNEL_FUSED_MAX) return 1;  // one workgroup per channel, one launch per pass
     const std::int64_t wanted = (4LL * device_cu_count() + s.C - 1) / s.C;
     const std::int64_t most = std::max<std::int64_t>(1, positions / MIN_SLICE);
     return static_cast<int>(std::max<std::int64_t>(1, std::min(wanted, most)));
@@ -354,17 +517,14 @@ std::int64_t norm_workspace_doubles(const NormShape& s) {
 int norm_forward(const NormShape& s, const NormForward& f, hipStream_t stream) {
     const int total = s.N * s.C * s.HW;
     const int slices = norm_slices(s);
-    if (f.training) {
-        PartialArgs args{};
-        args.x = f.x;
-        args.partial = f.partial;
-        args.C = s.C;
-        args.HW = s.HW;
-        args.total = s.N * s.HW;
-        args.chunk = (args.total + slices - 1) / slices;
-        args.div_hw = FastDiv(s.HW);
-        MFH_TRY(run_partials(STATS, s, args, stream));
-    }
+    PartialArgs args{};
+    args.x = f.x;
+    args.partial = f.partial;
+    args.C = s.C;
+    args.HW = s.HW;
+    args.total = s.N * s.HW;
+    args.chunk = (args.total + slices - 1) / slices;
+    args.div_hw = FastDiv(s.HW);
     ApplyArgs a{};
     a.x = f.x;
     a.gamma = f.gamma;
@@ -389,6 +549,11 @@ int norm_forward(const NormShape& s, const NormForward& f, hipStream_t stream) {
     a.div_hw = FastDiv(s.HW);
     a.div_c = FastDiv(s.C);
     const bool vec = s.HW % 4 == 0 && aligned16(f.x) && aligned16(f.y) && (!f.residual || aligned16(f.residual));
+    if (f.training && slices == 1) {
+        norm_forward_channel_kernel<<<s.C, PT, 0, stream>>>(args, a);
+        return MFH_CHECK_LAUNCH("norm_forward_channel", stream);
+    }
+    if (f.training) MFH_TRY(run_partials(STATS, s, args, stream));
     const unsigned blocks = blocks_for(total, APPLY_SPAN);
     if (vec) norm_apply_kernel<4><<<blocks, APPLY_THREADS, 0, stream>>>(a);
     else norm_apply_kernel<1><<<blocks, APPLY_THREADS, 0, stream>>>(a);
@@ -399,22 +564,21 @@ int norm_backward(const NormShape& s, const NormBackward& b, hipStream_t stream)
     const int total = s.N * s.C * s.HW;
     const int slices = norm_slices(s);
     const bool sums = b.gamma_grad || b.beta_grad || (b.training && b.x_grad);
-    if (sums || b.residual_grad) {
-        PartialArgs args{};
-        args.x = b.x;
-        args.dy = b.dy;
-        args.gate = b.gate;
-        args.mean = b.mean;
-        args.residual_grad = b.residual_grad;
-        args.add_residual = b.add_residual ? 1 : 0;
-        args.partial = b.partial;
-        args.C = s.C;
-        args.HW = s.HW;
-        args.total = s.N * s.HW;
-        args.chunk = (args.total + slices - 1) / slices;
-        args.div_hw = FastDiv(s.HW);
-        MFH_TRY(run_partials(GRADS, s, args, stream));
-    }
+    PartialArgs args{};
+    args.x = b.x;
+    args.dy = b.dy;
+    args.gate = b.gate;
+    args.mean = b.mean;
+    args.residual_grad = b.residual_grad;
+    args.add_residual = b.add_residual ? 1 : 0;
+    args.partial = b.partial;
+    args.C = s.C;
+    args.HW = s.HW;
+    args.total = s.N * s.HW;
+    args.chunk = (args.total + slices - 1) / slices;
+    args.div_hw = FastDiv(s.HW);
+    const bool fused = sums && slices == 1;
+    if ((sums || b.residual_grad) && !fused) MFH_TRY(run_partials(GRADS, s, args, stream));
     if (!b.x_grad && !sums) return OK;
     DxArgs d{};
     d.x = b.x;
@@ -441,6 +605,10 @@ int norm_backward(const NormShape& s, const NormBackward& b, hipStream_t stream)
     d.div_c = FastDiv(s.C);
     const bool vec = s.HW % 4 == 0 && aligned16(b.x) && aligned16(b.dy) && (!b.gate || aligned16(b.gate)) &&
                      (!b.x_grad || aligned16(b.x_grad));
+    if (fused) {
+        norm_backward_channel_kernel<<<s.C, PT, 0, stream>>>(args, d);
+        return MFH_CHECK_LAUNCH("norm_backward_channel", stream);
+    }
     const unsigned blocks = blocks_for(total, APPLY_SPAN);
     if (vec) norm_dx_kernel<4><<<blocks, APPLY_THREADS, 0, stream>>>(d);
     else norm_dx_kernel<1><<<blocks, APPLY_THREADS, 0, stream>>>(d);
