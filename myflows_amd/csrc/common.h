@@ -189,6 +189,10 @@ int split_reduce(const float* partial, float* c, int slices, int M, int N, int l
 // epilogue e (bias, activation, dense rows of ldc or segmented output).
 int split_reduce_epilogue(const float* partial, float* c, const GemmEpilogue& e, int M, int N, int ldc, int slices,
                           hipStream_t stream);
+// The same reduction for many slices over few outputs: the slices in 8 contiguous groups, each
+// summed in slice order in FP64, then the groups added in order (a fixed regrouping of the sum).
+int split_reduce_grouped(const float* partial, float* c, const GemmEpilogue& e, int M, int N, int ldc, int slices,
+                         hipStream_t stream);
 
 // ---- implicit.hip -----------------------------------------------------------------------------
 // The im2col view of an NCHW source read in place: view[k][q] = src[n, c, oh*SH - PH + kh,

@@ -147,6 +147,60 @@ __global__ __launch_bounds__(256) void split_reduce_vec4_kernel(const float* __r
     finish_output(p, C, q * 4 + 3, s3);
 }
 
+// Many slices over few outputs (a dW product split over the pixels): thread (q, g) of a block of
+// GROUP_QUADS x REDUCE_GROUPS threads sums the slices [g * per, (g + 1) * per) of outputs 4q .. 4q+3 in
+// slice order in FP64; the group sums are then added in group order. The order is fixed, so the
+// result does not depend on timing (it is the slice-order sum regrouped, not its bits).
+constexpr int REDUCE_GROUPS = 8, GROUP_QUADS = 32;
+__global__ __launch_bounds__(REDUCE_GROUPS* GROUP_QUADS) void split_reduce_grouped_kernel(
+    const float* __restrict__ partial, float* __restrict__ C, GemmParams p, int slices) {
+    __shared__ double group_sum[REDUCE_GROUPS][GROUP_QUADS][4];
+    const long long t = blockIdx.x * static_cast<long long>(REDUCE_GROUPS * GROUP_QUADS) + threadIdx.x;
+    if (p.row_out) finish_row(p, t);
+    const int g = threadIdx.x / GROUP_QUADS, qi = threadIdx.x % GROUP_QUADS;
+    const long long q = blockIdx.x * static_cast<long long>(GROUP_QUADS) + qi, total = static_cast<long long>(p.M) * p.N;
+    const long long stride = total / 4;
+    const int per = (slices + REDUCE_GROUPS - 1) / REDUCE_GROUPS;
+    const int z0 = g * per, z1 = min(slices, z0 + per);
+    double s0 = 0.0, s1 = 0.0, s2 = 0.0, s3 = 0.0;
+    if (q < stride) {
+        const float4* quads = reinterpret_cast<const float4*>(partial);
+        int z = z0;
+        for (; z + REDUCE_AHEAD <= z1; z += REDUCE_AHEAD) {
+            float4 part[REDUCE_AHEAD];
+#pragma unroll
+            for (int u = 0; u < REDUCE_AHEAD; ++u) part[u] = quads[(z + u) * stride + q];
+#pragma unroll
+            for (int u = 0; u < REDUCE_AHEAD; ++u) {
+                s0 += static_cast<double>(part[u].x);
+                s1 += static_cast<double>(part[u].y);
+                s2 += static_cast<double>(part[u].z);
+                s3 += static_cast<double>(part[u].w);
+            }
+        }
+        for (; z < z1; ++z) {
+            const float4 part = quads[z * stride + q];
+            s0 += static_cast<double>(part.x);
+            s1 += static_cast<double>(part.y);
+            s2 += static_cast<double>(part.z);
+            s3 += static_cast<double>(part.w);
+        }
+    }
+    group_sum[g][qi][0] = s0;
+    group_sum[g][qi][1] = s1;
+    group_sum[g][qi][2] = s2;
+    group_sum[g][qi][3] = s3;
+    __syncthreads();
+    if (g != 0 || q >= stride) return;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        double sum = group_sum[0][qi][r];
+#pragma unroll
+        for (int h = 1; h < REDUCE_GROUPS; ++h) sum += group_sum[h][qi][r];
+        finish_output(p, C, q * 4 + r, sum);
+    }
+}
+
 using GemmFn = void (*)(GemmParams);
 constexpr int VARIANTS = 16;  // 4 layouts (NN, NT, TN, TT) x float4 loads of A (yes/no) x of B
 
@@ -323,6 +377,18 @@ int launch_split_reduce(const float* partial, float* c, GemmParams p, int slices
 int split_reduce(const float* partial, float* c, int slices, int M, int N, int ldc, bool /*reference*/,
                  hipStream_t stream) {
     return launch_split_reduce(partial, c, epilogue_params(GemmEpilogue{}, M, N, ldc), slices, stream);
+}
+
+int split_reduce_grouped(const float* partial, float* c, const GemmEpilogue& e, int M, int N, int ldc, int slices,
+                         hipStream_t stream) {
+    GemmParams p = epilogue_params(e, M, N, ldc);
+    p.row_slices = slices;
+    const std::int64_t outputs = static_cast<std::int64_t>(M) * N;
+    if (outputs % 4 != 0 || !aligned16(partial)) return launch_split_reduce(partial, c, p, slices, stream);
+    const std::int64_t blocks = std::max<std::int64_t>(blocks_for(outputs / 4, GROUP_QUADS),
+                                                       blocks_for(64LL * p.row_count, REDUCE_GROUPS * GROUP_QUADS));
+    split_reduce_grouped_kernel<<<blocks, REDUCE_GROUPS * GROUP_QUADS, 0, stream>>>(partial, c, p, slices);
+    return MFH_CHECK_LAUNCH("split_reduce_grouped", stream);
 }
 
 int split_reduce_epilogue(const float* partial, float* c, const GemmEpilogue& e, int M, int N, int ldc, int slices,

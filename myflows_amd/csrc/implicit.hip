@@ -38,6 +38,7 @@ namespace {
 
 constexpr int BK = 32;     // stage depth of the forward / dX products (one channel chunk)
 constexpr int BK_WG = 16;  // stage depth of the dW products (a run of pixels)
+constexpr int GROUPED_REDUCE_SLICES = 16;  // dW splits from which the partials take the grouped reduction
 constexpr int FAR = -(1 << 24);  // window offset of a feature row past the end: every pixel is out of bounds
 
 // Forward orientation: a BK x BN tile of the view, rows = features [kt, kt + BK), columns = pixels
@@ -782,6 +783,10 @@ int run_implicit(bool wgrad, const GemmPlan& plan, const float* a, int lda, int 
         e.row_out = row_out;
         e.row_count = M;
     }
+    // dW products split into many pixel slices over a small output: a grouped reduction keeps the
+    // whole GPU busy (one thread per output would leave most CUs idle).
+    if (wgrad && plan.slices >= GROUPED_REDUCE_SLICES)
+        return split_reduce_grouped(workspace, c, e, M, N, ldc, plan.slices, stream);
     return split_reduce_epilogue(workspace, c, e, M, N, ldc, plan.slices, stream);
 }
 

@@ -337,9 +337,10 @@ IMPLICIT_TILES = 12  # tiles of the implicit products (plan code 16 + tile * 128
 @pytest.mark.parametrize("case", (RESNET_CASES[1], ("l2s", (2, 128, 15, 20), (128, 128, 3, 3), (1, 1), (1, 1))),
                          ids=lambda c: c[0])
 def test_every_implicit_tile_is_exact_on_integer_data(case):
-    """Each tile of the implicit catalogue (forced through its plan code, unsplit and split over K)
-    gives the FP64 loops' forward, dX, dW and db bit for bit on integer data; a tile without a dW
-    kernel (the 96-pixel one) is refused with a reason instead of launched."""
+    """Each tile of the implicit catalogue (forced through its plan code, unsplit and split over K;
+    the 24-way dW split takes the grouped reduction) gives the FP64 loops' forward, dX, dW and db
+    bit for bit on integer data; a tile without a dW kernel (the 96-pixel one) is refused with a
+    reason instead of launched."""
     _, x_shape, w_shape, stride, padding = case
     print("tiles", case[0], flush=True)
     rng = np.random.default_rng(17)
@@ -361,7 +362,7 @@ def test_every_implicit_tile_is_exact_on_integer_data(case):
     partial = torch.empty(max(n, native.BIAS_PARTIAL_ROWS) * co, dtype=torch.float64, device="cuda")
     workspace = torch.empty(1 << 24, device="cuda")
     for tile in range(IMPLICIT_TILES):
-        for slices in (1, 3):
+        for slices in (1, 3, 24):
             code = native.PLAN_BASE + tile * native.PLAN_SLICES + slices - 1
             native._raise_for(lib.mfh_conv_forward_implicit(
                 xg.data_ptr(), wg.data_ptr(), order.data_ptr(), 1, 0, y.data_ptr(), *g.c_args(), 0, 0.0, code,
