@@ -9,14 +9,17 @@
 //   p  = p - (lr * (m / bc1)) / (sqrt(v / bc2) + eps)
 // One launch covers up to ADAM_GROUP tensors whose descriptors travel in the kernel arguments, so
 // the step needs no device-side table and no host-to-device copy; workgroup w finds its tensor
-// from the running workgroup offsets.
+// from the running workgroup offsets. A tensor whose size is a multiple of 4 with 16-byte aligned
+// arrays takes four elements per thread (16-byte loads and stores), others one.
+#include <cstdint>
+
 #include "common.h"
 
 namespace mfh {
 namespace {
 
 constexpr int EW_THREADS = 256;
-constexpr int ADAM_GROUP = 16;
+constexpr int ADAM_GROUP = 48;
 
 __global__ __launch_bounds__(EW_THREADS) void relu_forward_kernel(const float* __restrict__ x,
                                                                   float* __restrict__ y, long long count) {
@@ -41,18 +44,15 @@ __global__ __launch_bounds__(EW_THREADS) void relu_backward_kernel(const float* 
 struct AdamGroup {
     AdamTensor t[ADAM_GROUP];
     unsigned first_block[ADAM_GROUP + 1];  // workgroups [first_block[i], first_block[i + 1]) update t[i]
+    unsigned char vec[ADAM_GROUP];         // 1: four elements per thread
     int count;
 };
 
-__global__ __launch_bounds__(EW_THREADS) void adam_kernel(AdamGroup group, AdamScalars s) {
+static_assert(sizeof(AdamGroup) + sizeof(AdamScalars) <= 4096, "Adam descriptors must fit the kernel arguments");
+
+__device__ __forceinline__ void adam_update(float& p, float& m, float& v, float g, const AdamTensor& t,
+                                            const AdamScalars& s) {
 #pragma clang fp contract(off)
-    int k = 0;
-    while (k + 1 < group.count && blockIdx.x >= group.first_block[k + 1]) ++k;
-    const AdamTensor& t = group.t[k];
-    const long long i = static_cast<long long>(blockIdx.x - group.first_block[k]) * EW_THREADS + threadIdx.x;
-    if (i >= t.size) return;
-    float m = t.m[i], v = t.v[i], p = t.param[i];
-    const float g = t.grad[i];
     float gs;
     if (t.decay != 0.0f) gs = g * s.grad_scale + t.decay * p;  // decoupled into the gradient, scale applied
     else gs = s.grad_scale == 1.0f ? g : g * s.grad_scale;
@@ -60,10 +60,38 @@ __global__ __launch_bounds__(EW_THREADS) void adam_kernel(AdamGroup group, AdamS
     v = s.b2 * v + s.omb2 * (gs * gs);
     const float denom = sqrtf(v / t.bc2) + s.eps;
     p = p - (t.lr * (m / t.bc1)) / denom;
+}
+
+__global__ __launch_bounds__(EW_THREADS) void adam_kernel(AdamGroup group, AdamScalars s) {
+    int k = 0;
+    while (k + 1 < group.count && blockIdx.x >= group.first_block[k + 1]) ++k;
+    const AdamTensor& t = group.t[k];
+    const long long local = blockIdx.x - group.first_block[k];
+    if (group.vec[k]) {
+        const long long i = (local * EW_THREADS + threadIdx.x) * 4;
+        if (i >= t.size) return;
+        float4 m = *reinterpret_cast<const float4*>(t.m + i), v = *reinterpret_cast<const float4*>(t.v + i);
+        float4 p = *reinterpret_cast<const float4*>(t.param + i);
+        const float4 g = *reinterpret_cast<const float4*>(t.grad + i);
+        adam_update(p.x, m.x, v.x, g.x, t, s);
+        adam_update(p.y, m.y, v.y, g.y, t, s);
+        adam_update(p.z, m.z, v.z, g.z, t, s);
+        adam_update(p.w, m.w, v.w, g.w, t, s);
+        *reinterpret_cast<float4*>(t.m + i) = m;
+        *reinterpret_cast<float4*>(t.v + i) = v;
+        *reinterpret_cast<float4*>(t.param + i) = p;
+        return;
+    }
+    const long long i = local * EW_THREADS + threadIdx.x;
+    if (i >= t.size) return;
+    float m = t.m[i], v = t.v[i], p = t.param[i];
+    adam_update(p, m, v, t.grad[i], t, s);
     t.m[i] = m;
     t.v[i] = v;
     t.param[i] = p;
 }
+
+bool aligned16(const void* q) { return (reinterpret_cast<std::uintptr_t>(q) & 15) == 0; }
 
 }  // namespace
 
@@ -87,9 +115,13 @@ int launch_adam(const AdamTensor* tensors, int count, const AdamScalars& s, hipS
         AdamGroup group{};
         unsigned blocks = 0;
         for (int k = 0; k < ADAM_GROUP && base + k < count; ++k) {
-            group.t[group.count] = tensors[base + k];
+            const AdamTensor& t = tensors[base + k];
+            const bool vec = t.size % 4 == 0 && aligned16(t.param) && aligned16(t.grad) && aligned16(t.m) &&
+                             aligned16(t.v);
+            group.t[group.count] = t;
+            group.vec[group.count] = vec ? 1 : 0;
             group.first_block[group.count] = blocks;
-            blocks += blocks_for(tensors[base + k].size, EW_THREADS);
+            blocks += blocks_for(vec ? t.size / 4 : t.size, EW_THREADS);
             ++group.count;
         }
         group.first_block[group.count] = blocks;

@@ -189,6 +189,24 @@ def test_adam_matches_the_oracle_bit_for_bit(scale, decay):
     np.testing.assert_array_equal(host(single), params[3])
 
 
+def test_adam_over_more_tensors_than_one_launch_takes():
+    """ResNet18 has 62 parameter tensors: one step spans two launches, with 4-element (size a
+    multiple of 4) and 1-element tensors mixed in each; every element matches the oracle's step."""
+    rng = np.random.default_rng(23)
+    sizes = [64 * (i % 5 + 1) + (3 if i % 7 == 0 else 0) for i in range(62)]
+    params = [rng.normal(size=s).astype(np.float32) for s in sizes]
+    grads = [rng.normal(size=s).astype(np.float32) for s in sizes]
+    state = [(np.zeros(s, np.float32), np.zeros(s, np.float32)) for s in sizes]
+    dev = [(gpu(p), gpu(g), gpu(m), gpu(v)) for p, g, (m, v) in zip(params, grads, state)]
+    fused.adam_update_many([(p, g, m, v, 1e-3, 0.0, 1) for p, g, m, v in dev], beta1=0.9, beta2=0.999, eps=1e-8,
+                           grad_scale=1.0)
+    for p, g, (m, v), (dp, _, dm, dv) in zip(params, grads, state, dev):
+        rp.adam_update(p, g, m, v, lr=1e-3, beta1=0.9, beta2=0.999, eps=1e-8, step=1)
+        np.testing.assert_array_equal(host(dp), p)
+        np.testing.assert_array_equal(host(dm), m)
+        np.testing.assert_array_equal(host(dv), v)
+
+
 def test_adam_rejects_overlapping_tensors():
     p = torch.zeros(16, device="cuda")
     with pytest.raises(ValueError):
