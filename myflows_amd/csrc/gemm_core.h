@@ -150,13 +150,15 @@ __device__ __forceinline__ void zero_acc(v16f (&acc)[S::TM][S::TN]) {
 }
 
 // One stage of MFMAs on the LDS tiles As / Bs (see the operand mapping above).
-template <class S>
+// KK0 / KK1 select a part of the stage (groups of four k per lane half), for a loop that puts
+// other work between the parts.
+template <class S, int KK0 = 0, int KK1 = S::HALF>
 __device__ __forceinline__ void mfma_stage(const float* As, const float* Bs, v16f (&acc)[S::TM][S::TN], int wm0,
                                            int wn0, int lane) {
     constexpr int HALF = S::HALF, LDA_S = S::LDA_S, LDB_S = S::LDB_S;
     const int lm = lane % 32, h = lane / 32;
 #pragma unroll
-    for (int kk = 0; kk < HALF; kk += 4) {
+    for (int kk = KK0; kk < KK1; kk += 4) {
         const int k = h * HALF + kk;
         float4 a[S::TM], b[S::TN];
 #pragma unroll
@@ -187,9 +189,19 @@ __device__ __forceinline__ void mfma_stage(const float* As, const float* Bs, v16
     }
 }
 
+// Instruction order inside a stage, chosen per kernel by measurement on MI355X (the arithmetic and
+// its order are the same for all of them):
+//   STAGE_PLAIN     MFMAs of the stage, then the LDS store of the next stage, then the barrier;
+//   STAGE_PRIORITY  the same, with the wave's issue priority raised (s_setprio 1) from the start of
+//                   its MFMAs to the barrier, so that waves in their MFMA phase issue first while
+//                   the others store and wait: 4 % on the dense 256x128 GEMM;
+//   STAGE_MID_STORE the LDS store of the next stage between the first and the second half of the
+//                   stage's MFMAs: 3-5 % on the dW products, whose stores carry gathered operands.
+enum StageOrder : int { STAGE_PLAIN = 0, STAGE_PRIORITY = 1, STAGE_MID_STORE = 2 };
+
 // The K loop over [k_begin, k_end) in BK stages. fetch(kt) issues the global reads of the stage
 // starting at kt; store(a_lds, b_lds) writes the fetched registers into one LDS stage buffer.
-template <class S, class Fetch, class Store>
+template <class S, int ORDER = STAGE_PLAIN, class Fetch, class Store>
 __device__ __forceinline__ void mfma_k_loop(float* smem, int k_begin, int k_end, Fetch&& fetch, Store&& store,
                                             v16f (&acc)[S::TM][S::TN], int wm0, int wn0, int lane) {
     constexpr int BK = S::BK;
@@ -203,10 +215,17 @@ __device__ __forceinline__ void mfma_k_loop(float* smem, int k_begin, int k_end,
         const bool more = t + 1 < stages;
         if (more) fetch(k_begin + (t + 1) * BK);
         const float* As = smem + (t & 1) * S::STAGE;
-        mfma_stage<S>(As, As + S::A_SIZE, acc, wm0, wn0, lane);
-        if (more) {
-            float* next = smem + ((t + 1) & 1) * S::STAGE;
-            store(next, next + S::A_SIZE);
+        float* next = smem + ((t + 1) & 1) * S::STAGE;
+        if constexpr (ORDER == STAGE_MID_STORE && S::HALF >= 8) {
+            constexpr int MID = S::HALF / 8 * 4;
+            mfma_stage<S, 0, MID>(As, As + S::A_SIZE, acc, wm0, wn0, lane);
+            if (more) store(next, next + S::A_SIZE);
+            mfma_stage<S, MID, S::HALF>(As, As + S::A_SIZE, acc, wm0, wn0, lane);
+        } else {
+            if constexpr (ORDER == STAGE_PRIORITY) __builtin_amdgcn_s_setprio(1);
+            mfma_stage<S>(As, As + S::A_SIZE, acc, wm0, wn0, lane);
+            if (more) store(next, next + S::A_SIZE);
+            if constexpr (ORDER == STAGE_PRIORITY) __builtin_amdgcn_s_setprio(0);
         }
         __syncthreads();
     }

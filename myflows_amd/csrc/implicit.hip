@@ -334,7 +334,7 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void conv_implicit_wgra
     };
     v16f acc[S::TM][S::TN];
     zero_acc<S>(acc);
-    mfma_k_loop<S>(smem, k_begin, k_end, fetch, store, acc, wm0, wn0, lane);
+    mfma_k_loop<S, STAGE_MID_STORE>(smem, k_begin, k_end, fetch, store, acc, wm0, wn0, lane);
     store_acc<S>(p, C, acc, m0, n0, wm0, wn0, lane);
     if constexpr (SUMS)
         if (summing)
