@@ -93,16 +93,30 @@ def time_steps(opt, steps, warmup):
     return time.perf_counter() - start
 
 
-def gemm_roofline(m=4096, n=4096, k=4096, reps=20):
+def _settle(fn, warmup, settle_ms):
+    """Untimed launches: `warmup` of them, then more until `settle_ms` of wall time has passed under
+    the load. The GPU raises its shader clock over the first tens of milliseconds of sustained work
+    after an idle spell (host-side set-up between the legs), so a kernel is timed at the clock it
+    holds under load, not during the ramp."""
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    start = time.perf_counter()
+    while (time.perf_counter() - start) * 1e3 < settle_ms:
+        for _ in range(4):
+            fn()
+        torch.cuda.synchronize()
+
+
+def gemm_roofline(m=4096, n=4096, k=4096, reps=20, settle_ms=100.0):
     """Average launch time of the MFMA GEMM on C = A B (A, B ~ N(0, 1) seed 0), from HIP events on
-    the stream the kernels are launched on."""
+    the stream the kernels are launched on, after the clock has settled under the load."""
     g = torch.Generator().manual_seed(0)
     a = torch.randn((m, k), generator=g).cuda()
     b = torch.randn((k, n), generator=g).cuda()
     out = torch.empty((m, n), device="cuda")
     stream = torch.cuda.current_stream()
-    for _ in range(3):
-        native.gemm(a, b, out=out)
+    _settle(lambda: native.gemm(a, b, out=out), 3, settle_ms)
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
     start.record(stream)
@@ -124,11 +138,10 @@ def gemm_roofline(m=4096, n=4096, k=4096, reps=20):
             "avg_launch_ms": round(ms, 4), "algorithmic_flop_per_launch": 2 * m * n * k}
 
 
-def _event_time_us(fn, reps=20, warmup=3):
-    """Average time of fn() in microseconds, from HIP events on the current stream."""
+def _event_time_us(fn, reps=20, warmup=3, settle_ms=30.0):
+    """Average time of fn() in microseconds, from HIP events on the current stream (after _settle)."""
     stream = torch.cuda.current_stream()
-    for _ in range(warmup):
-        fn()
+    _settle(fn, warmup, settle_ms)
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
     start.record(stream)
@@ -236,9 +249,7 @@ def c5_inference(batch=256, size=224, reps=10, warmup=3, seed=0):
     out = model(mf.Variable(torch.as_tensor(x_np, device="cuda"), requires_grad=False, name="images"))
     root, stats = mf.apply_graph_optimizations(out, mode="inference", fold_constants=False)
     graph = mf.Graph(root, optimize=True)
-    for _ in range(warmup):
-        graph.forward()
-    torch.cuda.synchronize()
+    _settle(graph.forward, warmup, 100.0)
     start = time.perf_counter()
     for _ in range(reps):
         graph.forward()
