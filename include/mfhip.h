@@ -131,7 +131,7 @@ MFH_API int64_t mfh_conv_implicit_workspace(int N, int CI, int H, int W, int CO,
  *   db   = FP64 sum of dy per channel: with dw, the dW product's first feature tile sums dy over
  *          its pixel slice in FP64 (into `partial` when the product is split over the pixels, then
  *          added in slice order by the split-K reduction launch); without dw, per-(n, co) FP64 row
- *          sums reduced over n in order. partial holds CO * max(N, 128) doubles;
+ *          sums reduced over n in order. partial holds CO * max(N, 256) doubles;
  *   dw   (CO, CI*KH*KW) = dy . im2col(x) with dy read in place (split over the pixels on dw_engine
  *          through the workspace); needs x;
  *   dx   stride 1: a forward convolution of dy with the flipped kernel read from `wflip`

@@ -247,7 +247,7 @@ struct WeightOrder {
 // All `count` orders in as few launches as the kernel arguments allow.
 int launch_weight_orders(const WeightOrder* orders, int count, hipStream_t stream);
 // Largest number of pixel slices the dW plan makes (rows of conv_implicit_wgrad's bias_partial).
-constexpr int WGRAD_MAX_SLICES = 128;
+constexpr int WGRAD_MAX_SLICES = 256;
 // partial[r] = FP64 sum of row r (rows x length floats).
 int launch_row_sums(const float* src, double* partial, int rows, int length, hipStream_t stream);
 

@@ -670,6 +670,7 @@ constexpr MeasuredPlan MEASURED_PLANS[] = {
     {0, 256, 5120, 128, 9, 1},     // layer3 1x1 downsample forward
     {0, 512, 1280, 2304, 9, 6},    // layer4.0 conv1 forward
     {0, 512, 1280, 4608, 9, 6},    // layer4 3x3 forward and dX
+    {1, 64, 147, 307200, 6, 256},  // stem dW (more slices than the dW rule makes: its gathers need the waves)
     {1, 64, 576, 72384, 8, 96},    // layer1 dW
     {1, 128, 576, 19200, 10, 48},  // layer2.0 conv1 dW
     {1, 128, 1152, 19200, 10, 48}, // layer2 3x3 dW

@@ -44,7 +44,7 @@ ROWS_PATH_MAX_PIXELS = 0               # conv forward through a rows GEMM + epil
 CONV_ALGORITHMS = ("implicit", "im2col")
 IMPLICIT_PASSES = {"forward": 0, "dw": 1, "dx": 2}
 CHANNEL_CHUNK = 32        # implicit products take features in chunks of this many channels per tap
-BIAS_PARTIAL_ROWS = 128   # rows of FP64 bias partials a dW product may write (its pixel slices)
+BIAS_PARTIAL_ROWS = 256   # rows of FP64 bias partials a dW product may write (its pixel slices)
 CONV_WFLIP_READY, CONV_ACCUMULATE_DX = 1, 2  # flags of mfh_conv_backward_implicit
 _STATUS_TEXT = {1: "initialization failed", 2: "invalid argument", 3: "HIP runtime error", 5: "wrong HIP device"}
 

@@ -331,6 +331,25 @@ def test_bias_gradient_with_and_without_the_weight_product(case):
         assert np.all(np.abs(host(db) - ref) <= np.spacing(np.abs(ref).astype(np.float32))), need_w
 
 
+def test_stem_weight_gradient_at_batch_64_is_exact_on_integer_data():
+    """The bs64 stem dW (64 x 147 over 307200 pixels: the measured plan splits it into 256 pixel
+    slices, with the bias sums of every slice) on integer data, where every float32 partial sum is
+    exact (|sum| <= 4 * 307200 < 2**24): dW and db equal the FP64 product bit for bit."""
+    print("stem dW bs64", flush=True)
+    rng = np.random.default_rng(23)
+    x = rng.integers(-2, 3, size=(64, 3, 120, 160)).astype(np.float32)
+    w = rng.integers(-2, 3, size=(64, 3, 7, 7)).astype(np.float32)
+    dy = rng.integers(-2, 3, size=(64, 64, 60, 80)).astype(np.float32)
+    _, dw, db = native.conv2d_backward(gpu(x), gpu(w), gpu(dy), None, stride=(2, 2), padding=(3, 3),
+                                       algorithm="implicit", need_input_grad=False)
+    padded = np.pad(x.astype(np.float64), ((0, 0), (0, 0), (3, 3), (3, 3)))
+    windows = np.lib.stride_tricks.sliding_window_view(padded, (7, 7), axis=(2, 3))[:, :, ::2, ::2]
+    cols = windows.transpose(0, 2, 3, 1, 4, 5).reshape(64 * 60 * 80, 3 * 49)
+    rows = dy.astype(np.float64).reshape(64, 64, 4800).transpose(1, 0, 2).reshape(64, -1)
+    np.testing.assert_array_equal(host(dw).reshape(64, -1), rows @ cols)
+    np.testing.assert_array_equal(host(db), rows.sum(axis=1))
+
+
 IMPLICIT_TILES = 12  # tiles of the implicit products (plan code 16 + tile * 128 + slices - 1)
 
 
