@@ -243,6 +243,31 @@ MFH_API int mfh_relu_forward(uint64_t x, uint64_t y, int64_t count, uint64_t str
 MFH_API int mfh_relu_backward(uint64_t x, uint64_t grad, uint64_t out, int64_t count, float alpha, int add,
                               uint64_t stream);
 
+/* ---- head and loss ---------------------------------------------------------------------------- */
+
+/* y[p] = float(FP64 sum of x[p*hw .. p*hw + hw) / hw) for `planes` contiguous planes of hw floats:
+ * the global average pool of an NCHW tensor (planes = N*C, hw = H*W).
+ * Replaces GlobalAvgPool2d_Op.forward, ops/batchnorm.py:113-116. */
+MFH_API int mfh_plane_mean(uint64_t x, uint64_t y, int64_t planes, int hw, uint64_t stream);
+
+/* dx[p*hw + i] = dy[p] / float(hw), or dx += that when add != 0.
+ * Replaces GlobalAvgPool2d_Op.backward, ops/batchnorm.py:118-123 (the broadcast gradient written out). */
+MFH_API int mfh_plane_mean_backward(uint64_t dy, uint64_t dx, int64_t planes, int hw, int add, uint64_t stream);
+
+/* loss[0] = float(FP64 sum of float32 (pred - target)^2 / count) (count = 0: 0).
+ * Replaces MSELoss.forward, ops/loss.py:99-106. */
+MFH_API int mfh_mse_loss(uint64_t pred, uint64_t target, uint64_t loss, int64_t count, uint64_t stream);
+
+/* grad = seed[0] * ((2 * (pred - target)) / float(count)), each operation rounded to float32, or
+ * grad += that when add != 0 (seed: the loss gradient, one float on the device).
+ * Replaces MSELoss.backward, ops/loss.py:108-113. */
+MFH_API int mfh_mse_loss_backward(uint64_t pred, uint64_t target, uint64_t seed, uint64_t grad, int64_t count, int add,
+                                  uint64_t stream);
+
+/* out[j] = float(FP64 sum over r < rows of src[r*cols + j]): a Linear layer's bias gradient.
+ * Replaces _reduce_to(grad, b.shape) in Linear.backward, ops/basic.py:164. */
+MFH_API int mfh_column_sums(uint64_t src, uint64_t out, int64_t rows, int64_t cols, uint64_t stream);
+
 /* One tensor of an Adam step: parameter, gradient and moments (size floats each, contiguous), the
  * learning rate, the weight decay and the bias corrections 1 - beta1^step, 1 - beta2^step, all
  * rounded to float32. */

@@ -630,6 +630,48 @@ MFH_API int mfh_relu_backward(std::uint64_t x, std::uint64_t grad, std::uint64_t
                                 add != 0, as_stream(stream));
 }
 
+MFH_API int mfh_plane_mean(std::uint64_t x, std::uint64_t y, std::int64_t planes, int hw, std::uint64_t stream) {
+    MFH_TRY(require_ready());
+    MFH_REQUIRE(planes >= 0 && hw > 0 && fits_index(planes * hw), "plane mean needs planes >= 0 and hw > 0 within the index range");
+    MFH_REQUIRE(planes == 0 || (x && y), "plane mean received a null buffer");
+    return launch_plane_mean(as_ptr<const float>(x), as_ptr<float>(y), planes, hw, as_stream(stream));
+}
+
+MFH_API int mfh_plane_mean_backward(std::uint64_t dy, std::uint64_t dx, std::int64_t planes, int hw, int add,
+                                    std::uint64_t stream) {
+    MFH_TRY(require_ready());
+    MFH_REQUIRE(planes >= 0 && hw > 0 && fits_index(planes * hw), "plane mean backward needs planes >= 0 and hw > 0 within the index range");
+    MFH_REQUIRE(planes == 0 || (dy && dx), "plane mean backward received a null buffer");
+    return launch_plane_mean_backward(as_ptr<const float>(dy), as_ptr<float>(dx), planes, hw, add != 0,
+                                      as_stream(stream));
+}
+
+MFH_API int mfh_mse_loss(std::uint64_t pred, std::uint64_t target, std::uint64_t loss, std::int64_t count,
+                         std::uint64_t stream) {
+    MFH_TRY(require_ready());
+    MFH_REQUIRE(count >= 0 && fits_index(count), "mse element count out of range");
+    MFH_REQUIRE(loss && (count == 0 || (pred && target)), "mse loss received a null buffer");
+    return launch_mse_loss(as_ptr<const float>(pred), as_ptr<const float>(target), as_ptr<float>(loss), count,
+                           as_stream(stream));
+}
+
+MFH_API int mfh_mse_loss_backward(std::uint64_t pred, std::uint64_t target, std::uint64_t seed, std::uint64_t grad,
+                                  std::int64_t count, int add, std::uint64_t stream) {
+    MFH_TRY(require_ready());
+    MFH_REQUIRE(count >= 0 && fits_index(count), "mse element count out of range");
+    MFH_REQUIRE(count == 0 || (pred && target && seed && grad), "mse loss backward received a null buffer");
+    return launch_mse_grad(as_ptr<const float>(pred), as_ptr<const float>(target), as_ptr<const float>(seed),
+                           as_ptr<float>(grad), count, add != 0, as_stream(stream));
+}
+
+MFH_API int mfh_column_sums(std::uint64_t src, std::uint64_t out, std::int64_t rows, std::int64_t cols,
+                            std::uint64_t stream) {
+    MFH_TRY(require_ready());
+    MFH_REQUIRE(rows >= 0 && cols >= 0 && fits_index(rows * cols), "column sums shape out of range");
+    MFH_REQUIRE(cols == 0 || (out && (rows == 0 || src)), "column sums received a null buffer");
+    return launch_column_sums(as_ptr<const float>(src), as_ptr<float>(out), rows, cols, as_stream(stream));
+}
+
 MFH_API int mfh_adam_step(const mfh_adam_tensor* tensors, int count, float grad_scale, float beta1,
                           float one_minus_beta1, float beta2, float one_minus_beta2, float eps, std::uint64_t stream) {
     MFH_TRY(require_ready());

@@ -317,4 +317,17 @@ struct AdamScalars {
 };
 int launch_adam(const AdamTensor* tensors, int count, const AdamScalars& s, hipStream_t stream);
 
+// ---- head.hip -------------------------------------------------------------------------------
+// y[p] = float(FP64 mean of x[p * hw .. p * hw + hw))
+int launch_plane_mean(const float* x, float* y, std::int64_t planes, int hw, hipStream_t stream);
+// dx[p * hw + i] (+)= dy[p] / float(hw)
+int launch_plane_mean_backward(const float* dy, float* dx, std::int64_t planes, int hw, bool add, hipStream_t stream);
+// loss[0] = float(FP64 sum of float32 (pred - target)^2 / count)
+int launch_mse_loss(const float* pred, const float* target, float* loss, std::int64_t count, hipStream_t stream);
+// grad (+)= seed[0] * ((2 * (pred - target)) / float(count)), float32 in that order
+int launch_mse_grad(const float* pred, const float* target, const float* seed, float* grad, std::int64_t count,
+                    bool add, hipStream_t stream);
+// out[j] = float(FP64 sum over r of src[r * cols + j])
+int launch_column_sums(const float* src, float* out, std::int64_t rows, std::int64_t cols, hipStream_t stream);
+
 }  // namespace mfh

@@ -3,7 +3,10 @@
 Same names, arguments and results as the reference's ``ops/fused.py``: ``batchnorm2d_forward``
 (:250-305), ``batchnorm2d_backward`` (:308-380), ``relu_backward_accumulate`` /
 ``leaky_relu_backward_accumulate`` (:50-77), ``adam_update`` (:514-533) and ``adam_update_many``
-(:609-621). Every tensor is a float32 GPU tensor; there is no host path.
+(:609-621). The head of the network runs here too: the global average pool
+(``ops/batchnorm.py:110-123``), the MSE loss and its gradient (``ops/loss.py:94-113``) and a
+Linear layer's bias gradient (``ops/basic.py:164``). Every tensor is a float32 GPU tensor; there is
+no host path.
 """
 
 from __future__ import annotations
@@ -17,6 +20,12 @@ from . import native
 
 def _f32(value, name):
     return native._device_f32(value, name)
+
+
+def on_libmfhip(value):
+    """Whether an operator's tensor runs on libmfhip: a float32 GPU tensor. (Operators that also
+    accept host tensors compute those with torch on the host, as before.)"""
+    return isinstance(value, torch.Tensor) and value.is_cuda and value.dtype == torch.float32
 
 
 @lru_cache(maxsize=256)
@@ -151,6 +160,77 @@ def relu_backward_accumulate(x, grad, out):
 def leaky_relu_backward_accumulate(x, grad, out, alpha):
     """out += grad where x > 0 and alpha * grad elsewhere (a new tensor when out is None)."""
     return _relu_backward(x, grad, out, float(alpha))
+
+
+def _output(out, add, shape, device):
+    """The buffer a result goes to: a new tensor when out is None (add must then be False), else
+    `out`, a contiguous float32 GPU tensor of `shape`, overwritten (add False) or added to."""
+    if out is None:
+        if add:
+            raise ValueError("add needs an out tensor")
+        return torch.empty(tuple(shape), dtype=torch.float32, device=device)
+    if not (isinstance(out, torch.Tensor) and out.dtype == torch.float32 and out.is_cuda and out.is_contiguous()
+            and tuple(out.shape) == tuple(shape)):
+        raise ValueError(f"out must be a contiguous float32 GPU tensor of shape {tuple(shape)}")
+    return out
+
+
+def global_avg_pool_forward(x):
+    """(N, C, H, W) -> (N, C): FP64 mean over H, W rounded once to float32."""
+    x = _f32(x, "x")
+    if x.ndim != 4:
+        raise ValueError("global average pool takes an (N, C, H, W) tensor")
+    n, c, h, w = x.shape
+    y = torch.empty((n, c), dtype=torch.float32, device=x.device)
+    if h * w == 0:
+        raise ValueError("global average pool needs H * W > 0")
+    native._call("mfh_plane_mean", x.data_ptr(), y.data_ptr(), n * c, h * w, native._stream())
+    return y
+
+
+def global_avg_pool_backward(grad, in_shape, out=None, add=False):
+    """dx = grad[n, c] / (H * W) broadcast over (H, W), written to (or, with add, added to) out."""
+    grad = _f32(grad, "grad")
+    n, c, h, w = (int(v) for v in in_shape)
+    if grad.numel() != n * c or h * w == 0:
+        raise ValueError("grad must hold one value per (n, c) plane of a non-empty input")
+    buffer = _output(out, add, (n, c, h, w), grad.device)
+    native._call("mfh_plane_mean_backward", grad.data_ptr(), buffer.data_ptr(), n * c, h * w, int(add),
+                 native._stream())
+    return buffer
+
+
+def mse_loss_forward(pred, target):
+    """FP64 mean of the float32 squared differences, rounded to a 0-d float32 tensor."""
+    pred, target = _f32(pred, "pred"), _f32(target, "target")
+    if pred.shape != target.shape:
+        raise ValueError("pred and target must have the same shape")
+    loss = torch.empty((), dtype=torch.float32, device=pred.device)
+    native._call("mfh_mse_loss", pred.data_ptr(), target.data_ptr(), loss.data_ptr(), pred.numel(), native._stream())
+    return loss
+
+
+def mse_loss_backward(pred, target, seed, out=None, add=False):
+    """seed * (2 * (pred - target) / pred.numel()), each step rounded to float32, written to (or,
+    with add, added to) out."""
+    pred, target, seed = _f32(pred, "pred"), _f32(target, "target"), _f32(seed, "seed")
+    if pred.shape != target.shape or seed.numel() != 1:
+        raise ValueError("pred and target must match and seed must hold one value")
+    buffer = _output(out, add, pred.shape, pred.device)
+    native._call("mfh_mse_loss_backward", pred.data_ptr(), target.data_ptr(), seed.data_ptr(), buffer.data_ptr(),
+                 pred.numel(), int(add), native._stream())
+    return buffer
+
+
+def column_sums(grad):
+    """FP64 sums over the rows of a 2-D tensor, rounded once: (rows, cols) -> (cols,)."""
+    grad = _f32(grad, "grad")
+    if grad.ndim != 2:
+        raise ValueError("column sums take a 2-D tensor")
+    rows, cols = grad.shape
+    out = torch.empty((cols,), dtype=torch.float32, device=grad.device)
+    native._call("mfh_column_sums", grad.data_ptr(), out.data_ptr(), rows, cols, native._stream())
+    return out
 
 
 def _adam_row(param, grad, m, v, lr, decay, step, beta1, beta2):

@@ -95,6 +95,11 @@ _SIGNATURES = {
     "mfh_relu_forward": ("i", "ppqp"),
     "mfh_relu_backward": ("i", "pppqfip"),
     "mfh_adam_step": ("i", "ti" + "ffffff" + "p"),
+    "mfh_plane_mean": ("i", "ppqip"),
+    "mfh_plane_mean_backward": ("i", "ppqiip"),
+    "mfh_mse_loss": ("i", "pppqp"),
+    "mfh_mse_loss_backward": ("i", "ppppqip"),
+    "mfh_column_sums": ("i", "ppqqp"),
 }
 EXPORTS = tuple(_SIGNATURES)
 

@@ -10,8 +10,9 @@ Operator API of the reference's ``ops/basic.py`` (``Add`` :5-35, ``Linear`` :76-
   FP64 sum rounded once; an input with requires_grad=False skips the dX GEMM.
 * ``ReLU`` / ``LeakyReLU`` run on libmfhip (forward, and a backward that gates and accumulates in
   one pass); they accept GPU tensors only.
-* ``Add`` and ``MSELoss`` are device tensor arithmetic (torch): broadcast add with the reduction of
-  the broadcast axes in backward, and the FP64 mean of squared errors.
+* ``Add`` is device tensor arithmetic (torch): broadcast add with the reduction of the broadcast
+  axes in backward. ``MSELoss`` (the FP64 mean of squared errors and its gradient) and a 2-D
+  Linear's bias gradient run on libmfhip for float32 GPU tensors (torch on host tensors).
 """
 
 from __future__ import annotations
@@ -19,6 +20,7 @@ from __future__ import annotations
 import torch
 
 from . import fused, native
+from .fused import on_libmfhip as _on_libmfhip
 from .graph import GradientOp
 
 LINEAR_BACKENDS = ("auto", "hip_native", "hip_native_kahan", "hip_native_dot2", "cuda_native_register",
@@ -112,7 +114,10 @@ class Linear(GradientOp):
         if w.requires_grad:
             w.accumulate_grad(self._product(x.value, g, trans_a=True), owned=True)
         if b.requires_grad:
-            b.accumulate_grad(_reduce_to(g, tuple(b.value.shape)))
+            if _on_libmfhip(g) and g.ndim == 2 and b.value.numel() == g.shape[1]:
+                b.accumulate_grad(fused.column_sums(g).reshape(b.value.shape), owned=True)
+            else:
+                b.accumulate_grad(_reduce_to(g, tuple(b.value.shape)))
 
 
 def _gpu_only(value, op):
@@ -155,12 +160,20 @@ class MSELoss(GradientOp):
         super().__init__(y_pred, y_true, name=name)
 
     def forward(self, y_pred_val, y_true_val):
+        if _on_libmfhip(y_pred_val) and _on_libmfhip(y_true_val) and y_pred_val.shape == y_true_val.shape:
+            self.value = fused.mse_loss_forward(y_pred_val, y_true_val)
+            return
         diff = y_pred_val - y_true_val
         self.value = torch.mean(diff * diff, dtype=torch.float64).to(diff.dtype)
 
     def backward(self):
         y_pred, y_true = self.parents
         if not y_pred.requires_grad:
+            return
+        if (_on_libmfhip(y_pred.value) and _on_libmfhip(y_true.value) and _on_libmfhip(self.grad)
+                and y_pred.value.shape == y_true.value.shape and self.grad.numel() == 1):
+            buffer, add = y_pred.grad_buffer()
+            fused.mse_loss_backward(y_pred.value, y_true.value, self.grad, buffer, add)
             return
         count = max(y_pred.value.numel(), 1)
         y_pred.accumulate_grad(self.grad * (2.0 * (y_pred.value - y_true.value) / count), owned=True)

@@ -11,6 +11,7 @@ from __future__ import annotations
 import torch
 
 from . import fused
+from .fused import on_libmfhip as _on_libmfhip
 from .graph import GradientOp
 
 
@@ -108,8 +109,16 @@ class GlobalAvgPool2d_Op(GradientOp):
 
     def forward(self, x_val):
         self._in_shape = tuple(x_val.shape)
-        self.value = x_val.mean(dim=(2, 3), dtype=torch.float64).to(x_val.dtype)
+        if _on_libmfhip(x_val):
+            self.value = fused.global_avg_pool_forward(x_val)
+        else:
+            self.value = x_val.mean(dim=(2, 3), dtype=torch.float64).to(x_val.dtype)
 
     def backward(self):
         n, c, h, w = self._in_shape
-        self.parents[0].accumulate_grad(self.grad.reshape(n, c, 1, 1) / (h * w))
+        x = self.parents[0]
+        if _on_libmfhip(x.value):
+            buffer, add = x.grad_buffer()
+            fused.global_avg_pool_backward(self.grad, self._in_shape, buffer, add)
+        else:
+            x.accumulate_grad(self.grad.reshape(n, c, 1, 1) / (h * w))

@@ -3,6 +3,9 @@
 * Adam: bit-exact against the oracle's float32 NumPy step (IEEE division and square root, the same
   rounding order), single and multi-tensor, with a gradient scale and weight decay.
 * ReLU: bit-exact (a selection and, when accumulating, one float32 addition).
+* Head: the global average pool, the MSE loss and a Linear bias gradient sum in FP64 and round
+  once, their gradients are float32 divisions and products in the operator's order: bit-exact
+  where the FP64 sums are exact (the network's shapes), within one ulp on long sums.
 * Batch norm: the GPU forms its FP64 statistics in one shifted pass, the oracle in two passes; the
   float32 results agree to within 4 ulp of the largest output (written in each test); the running
   statistics, dgamma and dbeta within 2e-6 relative.
@@ -158,6 +161,54 @@ def test_relu_forward_and_backward_are_exact():
     np.testing.assert_array_equal(host(out), g + rp.relu_backward(x, g))
     leaky = host(fused.leaky_relu_backward_accumulate(gpu(x), gpu(g), None, 0.2))
     np.testing.assert_array_equal(leaky, np.where(x > 0, g, np.float32(0.2) * g))
+
+
+def test_global_avg_pool_forward_and_backward_match_the_oracle():
+    print("global average pool", flush=True)
+    rng = np.random.default_rng(31)
+    x = rng.normal(size=(64, 512, 4, 5)).astype(np.float32)
+    np.testing.assert_array_equal(host(fused.global_avg_pool_forward(gpu(x))), rp.gap_forward(x))
+    wide = rng.normal(size=(3, 7, 60, 80)).astype(np.float32)
+    got, ref = host(fused.global_avg_pool_forward(gpu(wide))), rp.gap_forward(wide)
+    assert np.all(np.abs(got - ref) <= np.spacing(np.abs(ref))), "long plane sums within one ulp"
+    g = rng.normal(size=(64, 512)).astype(np.float32)
+    expected = rp.gap_backward(g, x.shape)
+    np.testing.assert_array_equal(host(fused.global_avg_pool_backward(gpu(g), x.shape)), expected)
+    base = rng.normal(size=x.shape).astype(np.float32)
+    out = gpu(base)
+    fused.global_avg_pool_backward(gpu(g), x.shape, out, add=True)
+    np.testing.assert_array_equal(host(out), base + expected)
+    with pytest.raises(ValueError):
+        fused.global_avg_pool_backward(gpu(g), x.shape, None, add=True)
+
+
+@pytest.mark.parametrize("shape", ((64, 2), (3, 1000, 37)))
+def test_mse_loss_and_gradient_match_the_oracle(shape):
+    print("mse", shape, flush=True)
+    rng = np.random.default_rng(32)
+    pred = rng.normal(size=shape).astype(np.float32)
+    target = rng.uniform(-1, 1, size=shape).astype(np.float32)
+    loss, ref = host(fused.mse_loss_forward(gpu(pred), gpu(target))), rp.mse_forward(pred, target)
+    assert loss.shape == () and abs(float(loss) - float(ref)) <= np.spacing(np.float32(ref)), (loss, ref)
+    if pred.size <= 1024:
+        np.testing.assert_array_equal(loss, ref)
+    for seed in (np.float32(1.0), np.float32(0.37)):
+        expected = rp.mse_backward(pred, target, seed)
+        got = host(fused.mse_loss_backward(gpu(pred), gpu(target), gpu(np.array(seed))))
+        np.testing.assert_array_equal(got, expected)
+    base = rng.normal(size=shape).astype(np.float32)
+    out = gpu(base)
+    fused.mse_loss_backward(gpu(pred), gpu(target), gpu(np.array(np.float32(1.0))), out, add=True)
+    np.testing.assert_array_equal(host(out), base + rp.mse_backward(pred, target))
+
+
+def test_linear_bias_gradient_column_sums():
+    rng = np.random.default_rng(33)
+    g = rng.normal(size=(64, 2)).astype(np.float32)
+    np.testing.assert_array_equal(host(fused.column_sums(gpu(g))), rp.reduce_to(g, (2,)))
+    tall = rng.normal(size=(5000, 300)).astype(np.float32)
+    got, ref = host(fused.column_sums(gpu(tall))), rp.reduce_to(tall, (300,))
+    assert np.all(np.abs(got - ref) <= np.spacing(np.abs(ref))), "long column sums within one ulp"
 
 
 @pytest.mark.parametrize("scale,decay", ((1.0, 0.0), (0.5, 0.0), (0.25, 1e-2)))
