@@ -106,11 +106,15 @@ MFH_API int mfh_conv_forward_implicit(uint64_t x, uint64_t weight, uint64_t wt, 
                                       uint64_t workspace, int64_t workspace_floats, uint64_t stream);
 
 /* The kernels of several convolutions in the orders the implicit products read them, in one
- * launch for up to 32 kernels (more take more launches). Kernel i is weights[i] (CO, CI, KH, KW)
- * with dims[5i .. 5i+4] = CO, CI, KH, KW, flip; outs[i] receives CO*CI*KH*KW floats (16-byte
- * aligned): flip 0, the forward order (rows co, features (ci, tap), in chunks of 32 channels per tap
- * when CI is a multiple of 32); flip 1, the stride-1 dX order, flipped and transposed (rows ci,
- * features (co, KH*KW-1-tap), chunked when CO is a multiple of 32). The three arrays are host memory.
+ * launch for up to 32 orders (more take more launches). Kernel i is weights[i] (CO, CI, KH, KW)
+ * with dims[9i .. 9i+8] = CO, CI, KH, KW, flip, SH, SW, PH, PW; outs[i] receives CO*CI*KH*KW
+ * floats (16-byte aligned): flip 0, the forward order (rows co, features (ci, tap), in chunks of 32
+ * channels per tap when CI is a multiple of 32); flip 1, the dX order: for stride 1 the kernel
+ * flipped and transposed (rows ci, features (co, KH*KW-1-tap), chunked when CO is a multiple of
+ * 32); for larger strides the same for the sub-kernel of each dX phase in turn (phase (a, b) in
+ * [0, SH) x [0, SW), a-major: the taps kh = (a+PH)%SH + SH*t, kw = (b+PW)%SW + SW*u, flipped),
+ * back to back. Stride and padding matter for the strided dX order only. The three arrays are
+ * host memory.
  * Has no counterpart in the reference (its products read the kernel in place): it lets a network
  * reorder all of its kernels once per step instead of once per convolution call. */
 MFH_API int mfh_conv_weight_orders(const uint64_t* weights, const uint64_t* outs, const int* dims, int count,
@@ -134,15 +138,20 @@ MFH_API int64_t mfh_conv_implicit_workspace(int N, int CI, int H, int W, int CO,
  *          sums reduced over n in order. partial holds CO * max(N, 256) doubles;
  *   dw   (CO, CI*KH*KW) = dy . im2col(x) with dy read in place (split over the pixels on dw_engine
  *          through the workspace); needs x;
- *   dx   stride 1: a forward convolution of dy with the flipped kernel read from `wflip`
- *          (CI*CO*KH*KW floats, 16-byte aligned, in chunks of 32 output channels per tap when CO
- *          is a multiple of 32), which this call fills from `weight` unless flags has
- *          MFH_CONV_WFLIP_READY; straight into NCHW dx; other strides: the per-image column
- *          gradient W^T dy_n in grad_cols (N*CI*KH*KW*OH*OW floats) and the col2im gather.
+ *   dx   with `wflip` (CI*CO*KH*KW floats, 16-byte aligned, the dX order of
+ *          mfh_conv_weight_orders for this geometry, which this call fills from `weight` unless
+ *          flags has MFH_CONV_WFLIP_READY): stride 1, a forward convolution of dy with the flipped
+ *          kernel; larger strides, one such stride-1 convolution of dy with the flipped sub-kernel
+ *          of each phase (a, b) (input positions SH*i + a, SW*j + b; the taps that reach them),
+ *          each written to its lattice of dx, positions that no tap reaches set to 0; straight
+ *          into NCHW dx. Strides above 1 without wflip: the per-image column gradient W^T dy_n in
+ *          grad_cols (N*CI*KH*KW*OH*OW floats) and the col2im gather.
  *          With MFH_CONV_ACCUMULATE_DX, dx = dx + the gradient (one rounding, as a separate add).
- * workspace: at least the larger of mfh_conv_implicit_workspace passes 1 and 2 that are requested.
- * dw_engine and a stride-1 dx_engine are implicit plan codes (as mfh_conv_forward_implicit); the
- * dx_engine of other strides is a GEMM engine code (as mfh_gemm).
+ * workspace: at least the larger of mfh_conv_implicit_workspace passes 1 and 2 that are requested
+ * (pass 2 covers the largest phase product of a strided dX).
+ * dw_engine and the dx_engine of a dX through wflip are implicit plan codes (as
+ * mfh_conv_forward_implicit; applied to every phase product); with grad_cols, dx_engine is a GEMM
+ * engine code (as mfh_gemm).
  * Has no single counterpart in the reference: it replaces mf_conv_backward_plans,
  * native_cublas.cpp:1465-1532, when the caller does not keep cols. */
 MFH_API int mfh_conv_backward_implicit(uint64_t x, uint64_t weight, uint64_t dy, uint64_t y, uint64_t gated,

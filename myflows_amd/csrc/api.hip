@@ -335,13 +335,15 @@ MFH_API int mfh_conv_weight_orders(const std::uint64_t* weights, const std::uint
     MFH_REQUIRE(count == 0 || (weights && outs && dims), "weight orders need the weights, outputs and dims arrays");
     std::vector<WeightOrder> orders(static_cast<size_t>(count));
     for (int i = 0; i < count; ++i) {
-        const int* d = dims + 5 * i;
-        const int CO = d[0], CI = d[1], KH = d[2], KW = d[3], flip = d[4];
+        const int* d = dims + WEIGHT_ORDER_DIMS * i;
+        const int CO = d[0], CI = d[1], KH = d[2], KW = d[3], flip = d[4], SH = d[5], SW = d[6], PH = d[7], PW = d[8];
         MFH_REQUIRE(weights[i] && outs[i], "weight order received a null buffer");
         MFH_REQUIRE(CO > 0 && CI > 0 && KH > 0 && KW > 0, "kernel dimensions must be positive");
         MFH_REQUIRE(static_cast<std::int64_t>(CO) * CI * KH * KW <= INDEX_LIMIT, "kernel exceeds the int32 index range");
         MFH_REQUIRE(flip == 0 || flip == 1, "flip must be 0 or 1");
-        orders[i] = WeightOrder{as_ptr<const float>(weights[i]), as_ptr<float>(outs[i]), CO, CI, KH * KW, flip};
+        MFH_REQUIRE(SH > 0 && SW > 0 && PH >= 0 && PW >= 0, "stride must be positive and padding non-negative");
+        orders[i] = WeightOrder{as_ptr<const float>(weights[i]), as_ptr<float>(outs[i]), CO, CI, KH, KW, flip,
+                                SH, SW, PH, PW};
     }
     return launch_weight_orders(orders.data(), count, as_stream(stream));
 }
@@ -370,18 +372,20 @@ MFH_API int mfh_conv_backward_implicit(std::uint64_t x, std::uint64_t weight, st
     MFH_TRY(validate_activation(activation, alpha));
     const bool gated_dy = activation != ACT_NONE;
     const bool unit_stride = SH == 1 && SW == 1;
-    // dW and the stride-1 dX are implicit products; other strides' dX is a dense GEMM.
+    // dW and dX given wflip are implicit products (a strided dX as its phase products); a strided dX
+    // given grad_cols is a dense GEMM into the column gradient and col2im.
+    const bool phases = !unit_stride && wflip != 0;
     MFH_REQUIRE(implicit_engine_valid(dw_engine), "unknown implicit convolution engine or plan code");
-    if (unit_stride) MFH_REQUIRE(implicit_engine_valid(dx_engine), "unknown implicit convolution engine or plan code");
+    if (unit_stride || phases) MFH_REQUIRE(implicit_engine_valid(dx_engine), "unknown implicit convolution engine or plan code");
     else MFH_TRY(validate_engine(dx_engine));
     const bool prepared = (flags & MFH_CONV_WFLIP_READY) != 0, accumulate = (flags & MFH_CONV_ACCUMULATE_DX) != 0;
     MFH_REQUIRE((flags & ~(MFH_CONV_WFLIP_READY | MFH_CONV_ACCUMULATE_DX)) == 0, "unknown conv backward flags");
-    MFH_REQUIRE(dy && (weight || (unit_stride && prepared)), "conv backward needs weight and dy");
+    MFH_REQUIRE(dy && (weight || ((unit_stride || phases) && prepared)), "conv backward needs weight and dy");
     MFH_REQUIRE(!gated_dy || (y && gated), "a fused activation needs the forward output and the gated buffer");
     MFH_REQUIRE((partial == 0) == (db == 0), "partial and db must be given together");
     MFH_REQUIRE(!dw || x, "dW needs x");
-    MFH_REQUIRE(!dx || (unit_stride ? wflip != 0 : grad_cols != 0),
-                "dX needs wflip (stride 1) or grad_cols (other strides)");
+    MFH_REQUIRE(!dx || wflip != 0 || (!unit_stride && grad_cols != 0),
+                "dX needs wflip (any stride) or grad_cols (strides above 1)");
     MFH_REQUIRE(workspace_floats >= 0, "workspace size must be non-negative");
     const hipStream_t s = as_stream(stream);
     const float* grad = as_ptr<const float>(dy);
@@ -406,6 +410,9 @@ MFH_API int mfh_conv_backward_implicit(std::uint64_t x, std::uint64_t weight, st
     if (unit_stride)
         return conv_implicit_dgrad(g, grad, as_ptr<const float>(weight), as_ptr<float>(wflip), prepared,
                                    as_ptr<float>(dx), accumulate, dx_engine, ws, workspace_floats, s);
+    if (phases)
+        return conv_implicit_dgrad_phases(g, grad, as_ptr<const float>(weight), as_ptr<float>(wflip), prepared,
+                                          as_ptr<float>(dx), accumulate, dx_engine, ws, workspace_floats, s);
     bool per_image = false;
     MFH_TRY(column_gradient(dx_engine, g, as_ptr<const float>(weight), grad, nullptr, as_ptr<float>(grad_cols),
                             &per_image, s));

@@ -137,6 +137,15 @@ struct GemmParams {
     int taps;                  // > 0: columns are convolution features in chunked order (see ConvGather)
     FastDiv taps_div;          // division by taps
     int accumulate;            // 1: each output is added to what C holds (C = C + result)
+    // > 0: a segment is a lattice_w-wide grid of a larger plane, element (i, j) of the segment at
+    // i * lattice_row + j * lattice_col + lattice_offset (the phases of a strided dX).
+    int lattice_w;
+    FastDiv lattice_div;       // division by lattice_w
+    int lattice_row, lattice_col, lattice_offset;
+    // > 0 (lattice of phase (0, 0) only): element (i, j) also zeroes the other positions of its
+    // cell_h x cell_w cell (rows cell_h * i + a, columns cell_w * j + b of a plane_h x plane_w
+    // plane), which no product writes (the other phases of a strided dX have no taps).
+    int cell_h, cell_w, plane_h, plane_w;
     // Split-K reduction only: also row_out[r] = (float) sum over z of row_partial[z * row_count + r]
     // (FP64, in z order) for r < row_count, with row_slices values of z.
     const double* row_partial;
@@ -172,6 +181,9 @@ struct GemmEpilogue {
     long long segment_stride = 0;
     int taps = 0;  // KH*KW when the output columns are features in chunked order; stored in natural order
     bool accumulate = false;  // C = C + result: a gradient added to one already there, in one pass
+    // Segments spread over a lattice of a larger plane (see GemmParams::lattice_w); 0: contiguous.
+    int lattice_w = 0, lattice_row = 0, lattice_col = 0, lattice_offset = 0;
+    int cell_h = 0, cell_w = 0, plane_h = 0, plane_w = 0;  // see GemmParams::cell_h
     // With a split-K reduction: row sums of FP64 slice partials finished in the same launch
     // (row_out[r] = sum over the slices of row_partial[z * row_count + r]).
     const double* row_partial = nullptr;
@@ -236,14 +248,49 @@ int conv_implicit_wgrad(const ConvGeometry& g, const float* x, const float* dy, 
 int conv_implicit_dgrad(const ConvGeometry& g, const float* dy, const float* w, float* wflip, bool prepared, float* dx,
                         bool accumulate, int engine, float* workspace, std::int64_t workspace_floats,
                         hipStream_t stream);
+// dX of a strided convolution as SH*SW phase products (see DgradPhase), each a stride-1 implicit
+// convolution of dy with its flipped sub-kernel whose epilogue writes the phase's lattice of dx.
+// The sub-kernels are read from wphase (CI*CO*KH*KW floats in the order launch_weight_orders
+// writes with flip 1 for this geometry), which this call fills from w unless `prepared`. Input
+// positions that no tap reaches are zeroed (or left as they are with accumulate).
+int conv_implicit_dgrad_phases(const ConvGeometry& g, const float* dy, const float* w, float* wphase, bool prepared,
+                               float* dx, bool accumulate, int engine, float* workspace,
+                               std::int64_t workspace_floats, hipStream_t stream);
+// One phase of the dX of a strided convolution (sub-pixel decomposition). The input positions
+// (ih, iw) = (SH*i + a, SW*j + b) receive dy only through the taps kh = rh + SH*t, kw = rw + SW*u
+// (t < th, u < tw), from dy[oh = i + ch - t][ow = j + cw - u]: a stride-1 convolution of dy with
+// that sub-kernel, flipped, under padding (pad_h, pad_w), over an hp x wp output grid. The phases
+// (a, b) in [0, SH) x [0, SW) partition both the input positions and the taps; stride 1 has the
+// single phase (0, 0), the whole kernel flipped under padding KH-1-PH.
+struct DgradPhase {
+    int a, b, rh, rw, th, tw, hp, wp, pad_h, pad_w;
+};
+inline DgradPhase dgrad_phase(const ConvGeometry& g, int a, int b) {
+    DgradPhase p{};
+    p.a = a;
+    p.b = b;
+    p.rh = (a + g.PH) % g.SH;
+    p.rw = (b + g.PW) % g.SW;
+    p.th = p.rh < g.KH ? (g.KH - p.rh + g.SH - 1) / g.SH : 0;
+    p.tw = p.rw < g.KW ? (g.KW - p.rw + g.SW - 1) / g.SW : 0;
+    p.hp = a < g.H ? (g.H - a + g.SH - 1) / g.SH : 0;
+    p.wp = b < g.W ? (g.W - b + g.SW - 1) / g.SW : 0;
+    p.pad_h = p.th - 1 - (a + g.PH - p.rh) / g.SH;
+    p.pad_w = p.tw - 1 - (b + g.PW - p.rw) / g.SW;
+    return p;
+}
+
 // The kernel W (CO, CI, KH, KW) in the order an implicit product reads it: flip 0 for the forward
-// (CO rows over (ci, tap) features), flip 1 for the stride-1 dX (CI rows over (co, flipped tap)
-// features), each in chunked feature order when its channel count is chunked.
+// (CO rows over (ci, tap) features), flip 1 for the dX (CI rows over (co, flipped tap) features;
+// for a stride above 1, the flipped sub-kernel of each dX phase in turn, phases in (a, b) order),
+// each in chunked feature order when its channel count is chunked. SH, SW, PH, PW matter for the
+// strided dX order only.
 struct WeightOrder {
     const float* w;
     float* out;
-    int CO, CI, taps, flip;
+    int CO, CI, KH, KW, flip, SH = 1, SW = 1, PH = 0, PW = 0;
 };
+constexpr int WEIGHT_ORDER_DIMS = 9;  // ints per kernel in mfh_conv_weight_orders' dims
 // All `count` orders in as few launches as the kernel arguments allow.
 int launch_weight_orders(const WeightOrder* orders, int count, hipStream_t stream);
 // Largest number of pixel slices the dW plan makes (rows of conv_implicit_wgrad's bias_partial).
@@ -299,6 +346,8 @@ int norm_backward(const NormShape& s, const NormBackward& b, hipStream_t stream)
 
 // ---- pointwise.hip ----------------------------------------------------------------------------
 int launch_relu_forward(const float* x, float* y, std::int64_t count, hipStream_t stream);
+// p[0 .. count) = 0 (a kernel, not a memset, so that it may sit in a captured graph)
+int launch_fill_zero(float* p, std::int64_t count, hipStream_t stream);
 // out (+)= x > 0 ? g : alpha * g   (alpha = 0 for ReLU)
 int launch_relu_backward(const float* x, const float* g, float* out, std::int64_t count, float alpha, bool add,
                          hipStream_t stream);

@@ -70,9 +70,7 @@ __device__ __forceinline__ void finish_output(const GemmParams& p, float* C, lon
     float v = static_cast<float>(s);
     if (p.bias_mode == BIAS_COLUMN) v += p.bias[col];
     else if (p.bias_mode == BIAS_ROW) v += p.bias[row];
-    float* out = C + output_offset(p, row, col);
-    v = activate(v, p.act, p.alpha);
-    *out = p.accumulate ? *out + v : v;
+    write_output(p, C, row, col, activate(v, p.act, p.alpha));
 }
 
 constexpr int REDUCE_AHEAD = 8;  // slices loaded before they are added
@@ -353,6 +351,15 @@ GemmParams epilogue_params(const GemmEpilogue& e, int M, int N, int ldc) {
     p.taps = e.taps;
     if (e.taps > 0) p.taps_div = FastDiv(e.taps);
     p.accumulate = e.accumulate ? 1 : 0;
+    p.lattice_w = e.lattice_w;
+    if (e.lattice_w > 0) p.lattice_div = FastDiv(e.lattice_w);
+    p.lattice_row = e.lattice_row;
+    p.lattice_col = e.lattice_col;
+    p.lattice_offset = e.lattice_offset;
+    p.cell_h = e.cell_h;
+    p.cell_w = e.cell_w;
+    p.plane_h = e.plane_h;
+    p.plane_w = e.plane_w;
     p.row_partial = e.row_partial;
     p.row_out = e.row_out;
     p.row_count = e.row_out ? e.row_count : 0;

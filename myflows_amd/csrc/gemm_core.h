@@ -101,8 +101,9 @@ __device__ __forceinline__ float activate(float v, int act, float alpha) {
 }
 
 // Where output (row, col) lives: dense row * ldc + col, or segmented (column j is element j % segment
-// of segment j / segment, segments segment_stride apart), after mapping a chunked-order feature
-// column back to its natural index when p.taps is set.
+// of segment j / segment, segments segment_stride apart, the element spread over a lattice when
+// p.lattice_w is set), after mapping a chunked-order feature column back to its natural index when
+// p.taps is set.
 __device__ __forceinline__ long long output_offset(const GemmParams& p, int row, int col) {
     if (p.taps) {  // chunked feature order -> natural order c * taps + tap
         int tap;
@@ -112,9 +113,39 @@ __device__ __forceinline__ long long output_offset(const GemmParams& p, int row,
     if (p.segment) {
         int within;
         const int segment = p.segment_div.divmod(col, within);
+        if (p.lattice_w) {
+            int j;
+            const int i = p.lattice_div.divmod(within, j);
+            within = i * p.lattice_row + j * p.lattice_col + p.lattice_offset;
+        }
         return segment * p.segment_stride + static_cast<long long>(row) * p.ldc + within;
     }
     return static_cast<long long>(row) * p.ldc + col;
+}
+
+// The zeros of output (row, col)'s lattice cell besides the output itself (GemmParams::cell_h).
+__device__ __forceinline__ void zero_cell(const GemmParams& p, float* __restrict__ C, int row, int col) {
+    int within, j;
+    const int segment = p.segment_div.divmod(col, within);
+    const int i = p.lattice_div.divmod(within, j);
+    float* base = C + segment * p.segment_stride + static_cast<long long>(row) * p.ldc;
+    for (int a = 0; a < p.cell_h; ++a) {
+        const int h = p.cell_h * i + a;
+        if (h >= p.plane_h) break;
+        for (int b = 0; b < p.cell_w; ++b) {
+            const int w = p.cell_w * j + b;
+            if (w >= p.plane_w) break;
+            if (a | b) base[h * p.plane_w + w] = 0.0f;
+        }
+    }
+}
+
+// One output: stored (or added, with p.accumulate) where output_offset puts it, and its lattice
+// cell's other positions zeroed when p.cell_h is set.
+__device__ __forceinline__ void write_output(const GemmParams& p, float* __restrict__ C, int row, int col, float v) {
+    float* out = C + output_offset(p, row, col);
+    *out = p.accumulate ? *out + v : v;
+    if (p.cell_h) zero_cell(p, C, row, col);
 }
 
 // (tile row, tile column, z) of this workgroup. Workgroups are handed to the 8 XCDs round-robin by
@@ -257,6 +288,7 @@ __device__ __forceinline__ void store_acc(const GemmParams& p, float* __restrict
                     float* out = C + col_offset + static_cast<long long>(row) * p.ldc;
                     v = activate(v, p.act, p.alpha);
                     *out = p.accumulate ? *out + v : v;
+                    if (p.cell_h) zero_cell(p, C, row, col);
                 }
             }
     }

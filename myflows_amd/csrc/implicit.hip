@@ -29,6 +29,7 @@
 // (n, oh, ow) is done once per stage (dW) or once per kernel (forward).
 #include <algorithm>
 #include <type_traits>
+#include <vector>
 
 #include "common.h"
 #include "gemm_core.h"
@@ -361,6 +362,10 @@ struct OrderJob {
     float* out;
     int O, C, T, chunked, flip, total;
     int tiled;               // LDS path: blocks are (row block, chunk), chunk fastest
+    // A phase of a strided dX (flip 1): T = th * tw sub-kernel taps; sub-tap (t, u) reads tap
+    // (rh + sh * (th - 1 - t), rw + sw * (tw - 1 - u)) of the source kernel's src_T = KH * KW taps.
+    int phase, src_T, src_kw, rh, rw, sh, sw, th, tw;
+    FastDiv div_tw;
     FastDiv div_row, div_t;  // by C * T, by T
     FastDiv div_panel;       // by 32 * T (a destination run)
     FastDiv div_run;         // by the length of a source run: 32 * T (forward) or TILE_ROWS * T (dX)
@@ -447,6 +452,13 @@ __global__ __launch_bounds__(256) void weight_order_kernel(OrderBatch batch) {
         c = chunk * CHANNEL_CHUNK + k % CHANNEL_CHUNK;
     } else {
         c = job.div_t.divmod(k, tap);
+    }
+    if (job.phase) {
+        int u;
+        const int t = job.div_tw.divmod(tap, u);
+        const int kh = job.rh + job.sh * (job.th - 1 - t), kw = job.rw + job.sw * (job.tw - 1 - u);
+        job.out[idx] = job.w[(c * job.O + o) * job.src_T + kh * job.src_kw + kw];
+        return;
     }
     job.out[idx] = job.flip ? job.w[(c * job.O + o) * job.T + (job.T - 1 - tap)] : job.w[(o * job.C + c) * job.T + tap];
 }
@@ -765,6 +777,15 @@ int run_implicit(bool wgrad, const GemmPlan& plan, const float* a, int lda, int 
         p.taps = e.taps;
         if (e.taps > 0) p.taps_div = FastDiv(e.taps);
         p.accumulate = e.accumulate ? 1 : 0;
+        p.lattice_w = e.lattice_w;
+        if (e.lattice_w > 0) p.lattice_div = FastDiv(e.lattice_w);
+        p.lattice_row = e.lattice_row;
+        p.lattice_col = e.lattice_col;
+        p.lattice_offset = e.lattice_offset;
+        p.cell_h = e.cell_h;
+        p.cell_w = e.cell_w;
+        p.plane_h = e.plane_h;
+        p.plane_w = e.plane_w;
     }
     const ImplicitTile& t = TILE_TABLE[plan.tile];
     const dim3 grid(blocks_for(N, t.bn), blocks_for(M, t.bm), static_cast<unsigned>(plan.slices));
@@ -796,6 +817,18 @@ int run_implicit(bool wgrad, const GemmPlan& plan, const float* a, int lda, int 
 bool implicit_engine_valid(int engine) { return engine == 1 || (engine >= 16 && engine < 16 + TILE_COUNT * 128); }
 
 std::int64_t implicit_workspace_floats(const ConvGeometry& g, int pass) {
+    if (pass == IMPLICIT_DGRAD && (g.SH > 1 || g.SW > 1)) {
+        std::int64_t most = 0;
+        for (int a = 0; a < g.SH; ++a)
+            for (int b = 0; b < g.SW; ++b) {
+                const DgradPhase ph = dgrad_phase(g, a, b);
+                if (ph.th * ph.tw == 0 || ph.hp == 0 || ph.wp == 0) continue;
+                const int M = g.CI, N = g.N * ph.hp * ph.wp, K = g.CO * ph.th * ph.tw;
+                const GemmPlan plan = implicit_auto_plan(false, M, N, K, implicit_chunked(g.CO));
+                most = std::max(most, gemm_workspace_floats(plan, M, N));
+            }
+        return most;
+    }
     GemmPlan plan;
     if (pass == IMPLICIT_FORWARD) plan = implicit_auto_plan(false, g.CO, g.rows(), g.features(), implicit_chunked(g.CI));
     else if (pass == IMPLICIT_WGRAD) plan = implicit_auto_plan(true, g.CO, g.features(), g.rows(), implicit_chunked(g.CI));
@@ -805,31 +838,68 @@ std::int64_t implicit_workspace_floats(const ConvGeometry& g, int pass) {
                                                           pass == IMPLICIT_FORWARD ? g.rows() : g.N * g.H * g.W);
 }
 
+// The jobs of one order: one, or one per non-empty phase of a strided dX (sub-kernels back to back).
+void order_jobs(const WeightOrder& o, std::vector<OrderJob>& jobs) {
+    const int rows = o.flip ? o.CI : o.CO, channels = o.flip ? o.CO : o.CI;
+    auto base = [&](OrderJob& job, float* out, int taps) {
+        job.w = o.w;
+        job.out = out;
+        job.O = rows;
+        job.C = channels;
+        job.T = taps;
+        job.chunked = implicit_chunked(channels) ? 1 : 0;
+        job.flip = o.flip;
+        job.total = rows * channels * taps;
+        job.div_row = FastDiv(channels * taps);
+        job.div_t = FastDiv(taps);
+        job.div_panel = FastDiv(32 * taps);
+        job.div_run = FastDiv((o.flip ? TILE_ROWS : 32) * taps);
+        job.div_chunks = FastDiv(std::max(1, channels / CHANNEL_CHUNK));
+    };
+    if (!o.flip || (o.SH == 1 && o.SW == 1)) {
+        OrderJob job{};
+        base(job, o.out, o.KH * o.KW);
+        job.tiled = job.chunked && job.T <= TILE_TAPS ? 1 : 0;
+        jobs.push_back(job);
+        return;
+    }
+    const ConvGeometry g{1, o.CI, 1, 1, o.CO, o.KH, o.KW, 1, 1, o.SH, o.SW, o.PH, o.PW};
+    long long offset = 0;
+    for (int a = 0; a < o.SH; ++a)
+        for (int b = 0; b < o.SW; ++b) {
+            const DgradPhase ph = dgrad_phase(g, a, b);
+            const int taps = ph.th * ph.tw;
+            if (taps == 0) continue;
+            OrderJob job{};
+            base(job, o.out + offset, taps);
+            job.tiled = 0;
+            job.phase = 1;
+            job.src_T = o.KH * o.KW;
+            job.src_kw = o.KW;
+            job.rh = ph.rh;
+            job.rw = ph.rw;
+            job.sh = o.SH;
+            job.sw = o.SW;
+            job.th = ph.th;
+            job.tw = ph.tw;
+            job.div_tw = FastDiv(ph.tw);
+            jobs.push_back(job);
+            offset += static_cast<long long>(rows) * channels * taps;
+        }
+}
+
 int launch_weight_orders(const WeightOrder* orders, int count, hipStream_t stream) {
-    for (int first = 0; first < count; first += ORDER_BATCH) {
+    std::vector<OrderJob> jobs;
+    for (int i = 0; i < count; ++i) order_jobs(orders[i], jobs);
+    const int total = static_cast<int>(jobs.size());
+    for (int first = 0; first < total; first += ORDER_BATCH) {
         OrderBatch batch{};
-        batch.count = std::min(ORDER_BATCH, count - first);
+        batch.count = std::min(ORDER_BATCH, total - first);
         int blocks = 0;
         for (int i = 0; i < batch.count; ++i) {
-            const WeightOrder& o = orders[first + i];
-            OrderJob& job = batch.job[i];
-            const int rows = o.flip ? o.CI : o.CO, channels = o.flip ? o.CO : o.CI;
-            job.w = o.w;
-            job.out = o.out;
-            job.O = rows;
-            job.C = channels;
-            job.T = o.taps;
-            job.chunked = implicit_chunked(channels) ? 1 : 0;
-            job.flip = o.flip;
-            job.total = rows * channels * o.taps;
-            job.div_row = FastDiv(channels * o.taps);
-            job.div_t = FastDiv(o.taps);
-            job.tiled = job.chunked && o.taps <= TILE_TAPS ? 1 : 0;
-            job.div_panel = FastDiv(32 * o.taps);
-            job.div_run = FastDiv((o.flip ? TILE_ROWS : 32) * o.taps);
-            job.div_chunks = FastDiv(std::max(1, channels / CHANNEL_CHUNK));
+            const OrderJob& job = batch.job[i] = jobs[first + i];
             batch.first_block[i] = blocks;
-            blocks += static_cast<int>(job.tiled ? blocks_for(rows, TILE_ROWS) * (channels / CHANNEL_CHUNK)
+            blocks += static_cast<int>(job.tiled ? blocks_for(job.O, TILE_ROWS) * (job.C / CHANNEL_CHUNK)
                                                  : blocks_for(job.total, 256));
         }
         batch.first_block[batch.count] = blocks;
@@ -849,7 +919,7 @@ int conv_implicit_forward(const ConvGeometry& g, const float* x, const float* w,
     const ConvGather gather = gather_of(x, g.CI, g.H, g.W, g.KH, g.KW, g.SH, g.SW, g.PH, g.PW, g.N, g.OH, g.OW);
     if (gather.chunked) {
         if (!prepared) {
-            const WeightOrder order{w, wt, g.CO, g.CI, g.KH * g.KW, 0};
+            const WeightOrder order{w, wt, g.CO, g.CI, g.KH, g.KW, 0};
             MFH_TRY(launch_weight_orders(&order, 1, stream));
         }
         w = wt;
@@ -885,7 +955,7 @@ int conv_implicit_dgrad(const ConvGeometry& g, const float* dy, const float* w, 
     GemmPlan plan;
     MFH_TRY(implicit_plan(false, implicit_chunked(g.CO), engine, M, N, K, workspace, workspace_floats, &plan));
     if (!prepared) {
-        const WeightOrder order{w, wflip, g.CO, g.CI, khw, 1};
+        const WeightOrder order{w, wflip, g.CO, g.CI, g.KH, g.KW, 1};
         MFH_TRY(launch_weight_orders(&order, 1, stream));
     }
     // dy as the source of a stride-1 convolution with padding KH-1-PH whose output grid is H x W.
@@ -896,6 +966,61 @@ int conv_implicit_dgrad(const ConvGeometry& g, const float* dy, const float* w, 
     e.segment_stride = static_cast<long long>(g.CI) * g.H * g.W;
     e.accumulate = accumulate;
     return run_implicit(false, plan, wflip, K, M, N, K, gather, dx, g.H * g.W, e, workspace, stream);
+}
+
+int conv_implicit_dgrad_phases(const ConvGeometry& g, const float* dy, const float* w, float* wphase, bool prepared,
+                               float* dx, bool accumulate, int engine, float* workspace,
+                               std::int64_t workspace_floats, hipStream_t stream) {
+    if (!prepared) {
+        const WeightOrder order{w, wphase, g.CO, g.CI, g.KH, g.KW, 1, g.SH, g.SW, g.PH, g.PW};
+        MFH_TRY(launch_weight_orders(&order, 1, stream));
+    }
+    bool gaps = false;    // input positions that no tap reaches (a phase without taps)
+    int with_taps = 0;    // phases that have taps
+    for (int a = 0; a < g.SH; ++a)
+        for (int b = 0; b < g.SW; ++b) {
+            const DgradPhase ph = dgrad_phase(g, a, b);
+            gaps = gaps || (ph.th * ph.tw == 0 && ph.hp > 0 && ph.wp > 0);
+            with_taps += ph.th * ph.tw > 0 ? 1 : 0;
+        }
+    // When phase (0, 0) alone has taps (a 1x1 kernel without padding), its product zeroes the rest
+    // of each cell itself; other gaps are cleared by a fill first.
+    const bool cells = gaps && !accumulate && with_taps == 1 && dgrad_phase(g, 0, 0).th * dgrad_phase(g, 0, 0).tw > 0;
+    if (gaps && !accumulate && !cells) {
+        MFH_TRY(launch_fill_zero(dx, static_cast<std::int64_t>(g.N) * g.CI * g.H * g.W, stream));
+        accumulate = true;
+    }
+    long long offset = 0;
+    for (int a = 0; a < g.SH; ++a)
+        for (int b = 0; b < g.SW; ++b) {
+            const DgradPhase ph = dgrad_phase(g, a, b);
+            const int taps = ph.th * ph.tw;
+            if (taps == 0) continue;
+            const float* sub = wphase + offset;
+            offset += static_cast<long long>(g.CI) * g.CO * taps;
+            if (ph.hp == 0 || ph.wp == 0) continue;
+            const int M = g.CI, N = g.N * ph.hp * ph.wp, K = g.CO * taps;
+            GemmPlan plan;
+            MFH_TRY(implicit_plan(false, implicit_chunked(g.CO), engine, M, N, K, workspace, workspace_floats, &plan));
+            const ConvGather gather =
+                gather_of(dy, g.CO, g.OH, g.OW, ph.th, ph.tw, 1, 1, ph.pad_h, ph.pad_w, g.N, ph.hp, ph.wp);
+            GemmEpilogue e;
+            e.segment = ph.hp * ph.wp;
+            e.segment_stride = static_cast<long long>(g.CI) * g.H * g.W;
+            e.accumulate = accumulate;
+            e.lattice_w = ph.wp;
+            e.lattice_row = g.SH * g.W;
+            e.lattice_col = g.SW;
+            e.lattice_offset = a * g.W + b;
+            if (cells) {
+                e.cell_h = g.SH;
+                e.cell_w = g.SW;
+                e.plane_h = g.H;
+                e.plane_w = g.W;
+            }
+            MFH_TRY(run_implicit(false, plan, sub, K, M, N, K, gather, dx, g.H * g.W, e, workspace, stream));
+        }
+    return OK;
 }
 
 int launch_row_sums(const float* src, double* partial, int rows, int length, hipStream_t stream) {

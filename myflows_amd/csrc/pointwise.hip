@@ -1,5 +1,5 @@
-// Elementwise kernels around the convolution path: ReLU forward/backward and a multi-tensor Adam
-// step.
+// Elementwise kernels around the convolution path: ReLU forward/backward, a zero fill and a
+// multi-tensor Adam step.
 //
 // Adam applies, per element and with every operation rounded to float32 in this order (no
 // contraction, IEEE division and square root):
@@ -27,6 +27,11 @@ __global__ __launch_bounds__(EW_THREADS) void relu_forward_kernel(const float* _
     if (i >= count) return;
     const float v = x[i];
     y[i] = v < 0.0f ? 0.0f : v;  // NaN stays NaN
+}
+
+__global__ __launch_bounds__(EW_THREADS) void fill_zero_kernel(float* __restrict__ p, long long count) {
+    const long long i = static_cast<long long>(blockIdx.x) * EW_THREADS + threadIdx.x;
+    if (i < count) p[i] = 0.0f;
 }
 
 template <bool LEAKY>
@@ -99,6 +104,12 @@ int launch_relu_forward(const float* x, float* y, std::int64_t count, hipStream_
     if (count == 0) return OK;
     relu_forward_kernel<<<blocks_for(count, EW_THREADS), EW_THREADS, 0, stream>>>(x, y, count);
     return MFH_CHECK_LAUNCH("relu_forward", stream);
+}
+
+int launch_fill_zero(float* p, std::int64_t count, hipStream_t stream) {
+    if (count == 0) return OK;
+    fill_zero_kernel<<<blocks_for(count, EW_THREADS), EW_THREADS, 0, stream>>>(p, count);
+    return MFH_CHECK_LAUNCH("fill_zero", stream);
 }
 
 int launch_relu_backward(const float* x, const float* g, float* out, std::int64_t count, float alpha, bool add,

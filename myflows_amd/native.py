@@ -395,14 +395,19 @@ def implicit_chunked(channels):
 
 def conv_weight_orders(requests):
     """The kernels of several convolutions in the orders the implicit products read them, from one
-    launch: requests = [(weight (CO, CI, KH, KW), flip)], flip 0 for the forward (pass the result
-    to conv2d_forward as weight_order), 1 for the stride-1 dX (conv2d_backward's weight_flip).
+    launch: requests = [(weight (CO, CI, KH, KW), flip)] or [(weight, flip, stride, padding)], flip 0
+    for the forward (pass the result to conv2d_forward as weight_order), 1 for the dX
+    (conv2d_backward's weight_flip); a strided dX order (the phase sub-kernels) depends on the
+    convolution's stride and padding, which default to (1, 1) and (0, 0).
     Returns one flat float32 tensor per request."""
     requests = list(requests)
     if not requests:
         return []
     weights, outs, dims = [], [], []
-    for weight, flip in requests:
+    for request in requests:
+        weight, flip = request[0], request[1]
+        stride = _pair(request[2], "stride", 1) if len(request) > 2 else (1, 1)
+        padding = _pair(request[3], "padding", 0) if len(request) > 3 else (0, 0)
         weight = _device_f32(weight, "weight")
         if weight.ndim != 4:
             raise ValueError("weight must have shape (CO, CI, KH, KW)")
@@ -411,12 +416,17 @@ def conv_weight_orders(requests):
         out = torch.empty(weight.numel(), dtype=torch.float32, device=weight.device)
         weights.append(weight)
         outs.append(out)
-        dims.extend((*(int(v) for v in weight.shape), int(flip)))
+        dims.extend((*(int(v) for v in weight.shape), int(flip), *stride, *padding))
     count = len(requests)
     _call("mfh_conv_weight_orders", (ctypes.c_uint64 * count)(*(w.data_ptr() for w in weights)),
           (ctypes.c_uint64 * count)(*(o.data_ptr() for o in outs)), (ctypes.c_int * len(dims))(*dims), count,
           _stream())
     return outs
+
+
+def strided_dx_phases(kh, kw):
+    """Whether conv2d_backward's automatic choice runs a strided dX as phase products (1x1 kernels)."""
+    return int(kh) * int(kw) == 1
 
 
 def _weight_order_buffer(order, weight, name):
@@ -471,14 +481,19 @@ def conv2d_forward(x, weight, bias=None, *, stride=(1, 1), padding=(0, 0), activ
 
 def conv2d_backward(x, weight, grad_y, cols, *, stride=(1, 1), padding=(0, 0), need_bias_grad=True,
                     need_input_grad=True, need_weight_grad=True, activation=None, alpha=0.0, output=None,
-                    engine="mfma", recompute_cols=False, algorithm=None, weight_flip=None, input_grad=None):
+                    engine="mfma", recompute_cols=False, algorithm=None, weight_flip=None, input_grad=None,
+                    strided_dx="auto"):
     """(dx, dw, db), None for each gradient not requested; a fused activation gates grad_y through
     output. algorithm "im2col" computes dW from the forward's cols (recomputed from x when
     recompute_cols); "implicit" gathers them from x inside the GEMM. Without an algorithm, a call
     that passes cols (and does not recompute them) takes "im2col", any other the default.
-    Implicit only: weight_flip is this kernel from conv_weight_orders(flip 1) for a stride-1 dX;
-    input_grad is a gradient of x already there, to which dX is added in place (it is then the
-    returned dx)."""
+    Implicit only: weight_flip is this kernel from conv_weight_orders(flip 1, with this stride and
+    padding) for the dX; input_grad is a gradient of x already there, to which dX is added in place
+    (it is then the returned dx); strided_dx chooses how a strided convolution's dX runs: "phases"
+    (one stride-1 implicit product per output phase, written to its lattice of dx), "columns" (the
+    per-image column gradient GEMM and col2im) or "auto": phases for a 1x1 kernel (a single phase
+    product), columns otherwise (measured on MI355X: the phases of a 3x3 kernel are small-K
+    products whose launches and split-K reductions cost more than the column path)."""
     engine = _engine_code(engine)
     if algorithm is None and cols is not None and not recompute_cols:
         algorithm = "im2col"
@@ -489,8 +504,11 @@ def conv2d_backward(x, weight, grad_y, cols, *, stride=(1, 1), padding=(0, 0), n
     if tuple(grad_y.shape) != g.out_shape:
         raise ValueError("grad_y does not have the convolution's output shape")
     if algorithm == "implicit":
+        if strided_dx not in ("auto", "phases", "columns"):
+            raise ValueError('strided_dx must be "auto", "phases" or "columns"')
+        phases = strided_dx == "phases" or (strided_dx == "auto" and strided_dx_phases(g.kh, g.kw))
         return _conv2d_backward_implicit(x, weight, grad_y, g, need_bias_grad, need_input_grad, need_weight_grad,
-                                         act, alpha, output, engine, weight_flip, input_grad)
+                                         act, alpha, output, engine, weight_flip, input_grad, phases)
     if weight_flip is not None or input_grad is not None:
         raise ValueError("weight_flip and input_grad apply to the implicit algorithm only")
     if need_weight_grad:
@@ -527,7 +545,7 @@ def conv2d_backward(x, weight, grad_y, cols, *, stride=(1, 1), padding=(0, 0), n
 
 
 def _conv2d_backward_implicit(x, weight, grad_y, g, need_bias_grad, need_input_grad, need_weight_grad, act, alpha,
-                              output, engine, weight_flip=None, input_grad=None):
+                              output, engine, weight_flip=None, input_grad=None, phases=True):
     gate = None
     if act:
         if output is None:
@@ -554,15 +572,18 @@ def _conv2d_backward_implicit(x, weight, grad_y, g, need_bias_grad, need_input_g
         else:
             dx = torch.empty_like(x)
     wflip = None
-    if need_input_grad and unit_stride:
+    through_orders = unit_stride or phases  # dX through the (phase) dX orders, else columns + col2im
+    if need_input_grad and through_orders:
         if weight_flip is not None:
             wflip, flags = _weight_order_buffer(weight_flip, weight, "weight_flip"), flags | CONV_WFLIP_READY
         else:
             wflip = empty(g.ci * g.co * g.kh * g.kw)
-    grad_cols = empty(g.m * g.k) if need_input_grad and not unit_stride else None
+    elif weight_flip is not None:
+        raise ValueError("weight_flip applies to a dX through the dX orders")
+    grad_cols = empty(g.m * g.k) if need_input_grad and not through_orders else None
     partial = empty(max(g.n, BIAS_PARTIAL_ROWS) * g.co, dtype=torch.float64) if need_bias_grad else None
     db = empty(g.co) if need_bias_grad else None
-    passes = (("dw",) if need_weight_grad else ()) + (("dx",) if need_input_grad and unit_stride else ())
+    passes = (("dw",) if need_weight_grad else ()) + (("dx",) if need_input_grad and through_orders else ())
     workspace, floats = _implicit_workspace(g, *passes)
     _call("mfh_conv_backward_implicit", x.data_ptr(), weight.data_ptr(), grad_y.data_ptr(), _addr(gate),
           _addr(gated), _addr(dw), _addr(dx), _addr(wflip), _addr(grad_cols), _addr(partial), _addr(db),

@@ -98,9 +98,12 @@ class Conv2D_Op(GradientOp):
             if kernel.ndim != 4 or not native.implicit_chunked(kernel.shape[1]):
                 return []
             return [(kernel, 0)]
-        if self._saved is None or not self.parents[0].requires_grad or self.stride != (1, 1):
+        if self._saved is None or not self.parents[0].requires_grad:
             return []
-        return [(self._saved[1], 1)]
+        kernel = self._saved[1]
+        if self.stride != (1, 1) and (kernel.ndim != 4 or not native.strided_dx_phases(*kernel.shape[2:])):
+            return []  # that dX runs through the column gradient, which reads the kernel in place
+        return [(kernel, 1, self.stride, self.padding)]
 
     def take_weight_orders(self, phase, tensors):
         kernel = self.parents[1].value if phase == "forward" else self._saved[1]

@@ -292,26 +292,110 @@ def test_batched_weight_orders_match_the_permutation():
         np.testing.assert_array_equal(host(out), host(permuted_kernel(w, flip)), err_msg=f"{tuple(w.shape)} {flip}")
 
 
+def phase_orders(w, stride, padding):
+    """The strided dX order by plain tensor slicing: for each phase (a, b), a-major, the taps
+    kh = (a + PH) % SH + SH * t, kw = (b + PW) % SW + SW * u of the kernel, flipped and transposed
+    as the stride-1 dX order of that sub-kernel."""
+    kh, kw = w.shape[2:]
+    parts = []
+    for a in range(stride[0]):
+        for b in range(stride[1]):
+            rows = list(range((a + padding[0]) % stride[0], kh, stride[0]))
+            cols = list(range((b + padding[1]) % stride[1], kw, stride[1]))
+            if rows and cols:
+                parts.append(permuted_kernel(w[:, :, rows][:, :, :, cols].contiguous(), 1))
+    return torch.cat(parts)
+
+
+STRIDED = (("s2", (64, 32, 3, 3), (2, 2), (1, 1)), ("s2ds", (128, 64, 1, 1), (2, 2), (0, 0)),
+           ("s3", (32, 5, 4, 5), (3, 2), (2, 1)), ("s2p0", (7, 3, 2, 3), (2, 2), (0, 0)),
+           ("stem", (64, 3, 7, 7), (2, 2), (3, 3)))
+
+
+def test_strided_dx_orders_are_the_phase_sub_kernels():
+    """conv_weight_orders with flip 1 and a stride above 1 writes, back to back, the flipped and
+    transposed sub-kernel of each dX phase (chunked when CO is a multiple of 32), bit for bit."""
+    g = torch.Generator().manual_seed(13)
+    weights = [torch.randn(shape, generator=g).cuda() for _, shape, _, _ in STRIDED]
+    made = native.conv_weight_orders([(w, 1, s, p) for w, (_, _, s, p) in zip(weights, STRIDED)])
+    for w, out, (name, _, s, p) in zip(weights, made, STRIDED):
+        np.testing.assert_array_equal(host(out), host(phase_orders(w, s, p)), err_msg=name)
+
+
+@pytest.mark.parametrize("case", CONV_CASES[1:] + (RESNET_CASES[2], RESNET_CASES[3], RESNET_CASES[0],
+                                                   ("s3", (2, 32, 13, 11), (32, 32, 4, 5), (3, 2), (2, 1)),
+                                                   ("ds_even", (2, 32, 8, 10), (64, 32, 1, 1), (2, 2), (0, 0)),
+                                                   ("ds_pad", (1, 32, 7, 9), (32, 32, 1, 1), (2, 2), (1, 0))),
+                         ids=lambda c: c[0])
+def test_strided_dx_phases_equal_the_column_path_on_integer_data(case):
+    """The phase products and the column-gradient path give the same dX (and the FP64 loops') bit
+    for bit on integer data, written fresh and added to an existing gradient; positions that no
+    tap reaches (a 1x1 stride-2 kernel) are zero."""
+    _, x_shape, w_shape, stride, padding = case
+    print("phases", case[0], flush=True)
+    rng = np.random.default_rng(19)
+    x = rng.integers(-2, 3, size=x_shape).astype(np.float32)
+    w = rng.integers(-2, 3, size=w_shape).astype(np.float32)
+    n, co, oh, ow = (x_shape[0], w_shape[0], *rp.out_size(x_shape[2], x_shape[3], w_shape[2:], stride, padding))
+    dy = rng.integers(-2, 3, size=(n, co, oh, ow)).astype(np.float32)
+    ref_dx, _ = naive.conv_backward(x.astype(np.float64), w.astype(np.float64), dy.astype(np.float64), stride, padding)
+    results = {}
+    for path in ("phases", "columns"):
+        dx, _, _ = native.conv2d_backward(gpu(x), gpu(w), gpu(dy), None, stride=stride, padding=padding,
+                                          algorithm="implicit", need_weight_grad=False, need_bias_grad=False,
+                                          strided_dx=path)
+        np.testing.assert_array_equal(host(dx), ref_dx, err_msg=path)
+        existing = gpu(rng.integers(-2, 3, size=x_shape).astype(np.float32))
+        expected = host(existing) + ref_dx
+        native.conv2d_backward(gpu(x), gpu(w), gpu(dy), None, stride=stride, padding=padding, algorithm="implicit",
+                               need_weight_grad=False, need_bias_grad=False, strided_dx=path, input_grad=existing)
+        np.testing.assert_array_equal(host(existing), expected, err_msg=f"{path} accumulate")
+
+
+@pytest.mark.parametrize("shape,stride,padding", (((2, 64, 29, 39), (2, 2), (0, 0)), ((2, 64, 8, 10), (2, 2), (0, 0)),
+                                                   ((1, 32, 7, 9), (2, 2), (1, 0)), ((1, 32, 10, 7), (3, 2), (0, 0))))
+def test_strided_1x1_dx_writes_every_position(shape, stride, padding):
+    """A strided 1x1 dX into a buffer full of NaN: the phase product (with the cell zeros of its
+    epilogue, or after a fill when its phase is not the first) leaves no position unwritten."""
+    print("1x1 strided", shape, stride, padding, flush=True)
+    rng = np.random.default_rng(29)
+    x = rng.integers(-2, 3, size=shape).astype(np.float32)
+    w = rng.integers(-2, 3, size=(64, shape[1], 1, 1)).astype(np.float32)
+    g = native.ConvGeometry.of(shape, w.shape, stride, padding)
+    dy = rng.integers(-2, 3, size=g.out_shape).astype(np.float32)
+    ref_dx, _ = naive.conv_backward(x.astype(np.float64), w.astype(np.float64), dy.astype(np.float64), stride, padding)
+    lib, s = native._library(), torch.cuda.current_stream().cuda_stream
+    wg, dyg = gpu(w), gpu(dy)
+    (order,) = native.conv_weight_orders([(wg, 1, stride, padding)])
+    dx = torch.full(shape, float("nan"), device="cuda")
+    workspace = torch.empty(1 << 22, device="cuda")
+    native._raise_for(lib.mfh_conv_backward_implicit(
+        gpu(x).data_ptr(), wg.data_ptr(), dyg.data_ptr(), 0, 0, 0, dx.data_ptr(), order.data_ptr(), 0, 0, 0,
+        *g.c_args(), 0, 0.0, 1, 1, native.CONV_WFLIP_READY, workspace.data_ptr(), workspace.numel(), s), lib)
+    np.testing.assert_array_equal(host(dx), ref_dx)
+
+
 @pytest.mark.parametrize("case", (RESNET_CASES[1], RESNET_CASES[2], RESNET_CASES[3], RESNET_CASES[4],
                                   RESNET_CASES[5], PERFORMANCE_CASES[0]), ids=lambda c: c[0])
 def test_prepared_orders_and_in_place_dx_give_the_same_bits(case):
-    """A forward that reads a prepared kernel order, a stride-1 dX that reads a prepared flipped
-    kernel and a dX added in place to an existing gradient give exactly the results of the plain
-    calls (the in-place add is the same float32 addition as a separate one)."""
+    """A forward that reads a prepared kernel order, a dX that reads a prepared dX order (the
+    flipped kernel, or for a stride above 1 its phase sub-kernels) and a dX added in place to an
+    existing gradient give exactly the results of the plain calls (the in-place add is the same
+    float32 addition as a separate one)."""
     print("prepared", case[0], flush=True)
     x, w, b, dy = (gpu(a) for a in conv_fixture(case))
     stride, padding = case[3], case[4]
     plain_y, _ = native.conv2d_forward(x, w, b, stride=stride, padding=padding, algorithm="implicit")
-    order, flip = native.conv_weight_orders([(w, 0), (w, 1)])
+    order, flip = native.conv_weight_orders([(w, 0), (w, 1, stride, padding)])
     prepared_y, _ = native.conv2d_forward(x, w, b, stride=stride, padding=padding, algorithm="implicit",
                                           weight_order=order)
     np.testing.assert_array_equal(host(prepared_y), host(plain_y))
-    dx, dw, db = native.conv2d_backward(x, w, dy, None, stride=stride, padding=padding, algorithm="implicit")
+    dx, dw, db = native.conv2d_backward(x, w, dy, None, stride=stride, padding=padding, algorithm="implicit",
+                                        strided_dx="phases")
     existing = torch.randn(x.shape, generator=torch.Generator().manual_seed(5)).cuda()
     expected = host(existing) + host(dx)
-    extra = {"weight_flip": flip} if stride == (1, 1) else {}
     dx2, dw2, db2 = native.conv2d_backward(x, w, dy, None, stride=stride, padding=padding, algorithm="implicit",
-                                           input_grad=existing, **extra)
+                                           input_grad=existing, weight_flip=flip, strided_dx="phases")
     assert dx2 is existing
     np.testing.assert_array_equal(host(dx2), expected)
     np.testing.assert_array_equal(host(dw2), host(dw))
