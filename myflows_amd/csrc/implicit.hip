@@ -263,15 +263,14 @@ struct GradRowsInPlace {
     }
 };
 
-// Y (M x pixels) = A (M x K, row-major, lda) . view (K x pixels). Split-K writes dense partials
-// (z-th slice at C + z * c_batch); otherwise the epilogue of p (segmented NCHW, bias, activation).
+// One BM x BN tile (tile_m, tile_n) of Y (M x pixels) = A (M x K, row-major, lda) . view (K x
+// pixels), K slice z. Split-K writes dense partials (z-th slice at C + z * c_batch); otherwise the
+// epilogue of p (segmented NCHW, bias, activation).
 template <int BM, int BN, int WM, int WN, bool VA, bool CHUNKED>
-__global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void conv_implicit_forward_kernel(GemmParams p,
-                                                                                          ConvGather g) {
+__device__ __forceinline__ void implicit_forward_tile(const GemmParams& p, const ConvGather& g, int tile_m, int tile_n,
+                                                      int z) {
     using S = MfmaShape<BM, BN, BK, WM, WN, false, false>;
     __shared__ __attribute__((aligned(16))) float smem[2 * S::STAGE];
-    int tile_m, tile_n, z;
-    tile_of_workgroup(tile_m, tile_n, z);
     const int tid = threadIdx.x, wave = tid / 64, lane = tid % 64;
     const int wm0 = (wave / S::WGN) * WM, wn0 = (wave % S::WGN) * WN;
     const int m0 = tile_m * BM, n0 = tile_n * BN;
@@ -294,6 +293,36 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void conv_implicit_forw
     zero_acc<S>(acc);
     mfma_k_loop<S>(smem, k_begin, k_end, fetch, store, acc, wm0, wn0, lane);
     store_acc<S>(p, C, acc, m0, n0, wm0, wn0, lane);
+}
+
+template <int BM, int BN, int WM, int WN, bool VA, bool CHUNKED>
+__global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void conv_implicit_forward_kernel(GemmParams p,
+                                                                                          ConvGather g) {
+    int tile_m, tile_n, z;
+    tile_of_workgroup(tile_m, tile_n, z);
+    implicit_forward_tile<BM, BN, WM, WN, VA, CHUNKED>(p, g, tile_m, tile_n, z);
+}
+
+// Several implicit products of one tile shape in one launch (the phases of a strided dX): product
+// j owns the workgroups [first[j], first[j + 1]), its tiles taken column-fastest; no K split.
+constexpr int GROUPED_PRODUCTS = 4;
+struct GroupedProducts {
+    GemmParams p[GROUPED_PRODUCTS];
+    ConvGather g[GROUPED_PRODUCTS];
+    int first[GROUPED_PRODUCTS + 1];
+    int tiles_n[GROUPED_PRODUCTS];
+    int count;
+};
+static_assert(sizeof(GroupedProducts) <= 4096, "the grouped products travel in the kernel arguments");
+
+template <int BM, int BN, int WM, int WN>
+__global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void conv_implicit_grouped_kernel(GroupedProducts batch) {
+    const int block = static_cast<int>(blockIdx.x);
+    int j = 0;
+    while (j + 1 < batch.count && block >= batch.first[j + 1]) ++j;
+    const int local = block - batch.first[j];
+    implicit_forward_tile<BM, BN, WM, WN, true, true>(batch.p[j], batch.g[j], local / batch.tiles_n[j],
+                                                      local % batch.tiles_n[j], 0);
 }
 
 // dW (CO x K) = dy (CO x pixels) . view^T (pixels x K), the pixel range split over z when p.split.
@@ -525,6 +554,7 @@ constexpr ConvFn forward_of() {
 }
 
 using WgradFn = void (*)(GemmParams, ConvGather, double*, float*);
+using GroupedFn = void (*)(GroupedProducts);
 
 template <int T, bool SUMS>
 constexpr WgradFn wgrad_of() {
@@ -537,6 +567,7 @@ constexpr WgradFn wgrad_of() {
 struct ConvKernels {
     ConvFn forward[TILE_COUNT][3] = {};
     WgradFn wgrad[TILE_COUNT][2] = {};
+    GroupedFn grouped[TILE_COUNT] = {};  // chunked products only, tile 6 (the strided dX phases)
     template <int T>
     void fill() {
         if constexpr (has_natural(TILE_TABLE[T])) {
@@ -562,6 +593,7 @@ struct ConvKernels {
         fill<9>();
         fill<10>();
         fill<11>();
+        grouped[6] = conv_implicit_grouped_kernel<64, 64, 32, 32>;
     }
 };
 static_assert(TILE_COUNT == 12, "ConvKernels fills every tile");
@@ -746,6 +778,31 @@ int implicit_plan(bool wgrad, bool chunked, int engine, int M, int N, int K, flo
     return OK;
 }
 
+// The output fields of an unsplit product: C (ldc) and the epilogue e.
+void set_epilogue(GemmParams& p, float* c, int ldc, const GemmEpilogue& e) {
+    p.C = c;
+    p.ldc = ldc;
+    p.bias = e.bias;
+    p.bias_mode = e.bias_mode;
+    p.act = e.act;
+    p.alpha = e.alpha;
+    p.segment = e.segment;
+    if (e.segment > 0) p.segment_div = FastDiv(e.segment);
+    p.segment_stride = e.segment_stride;
+    p.taps = e.taps;
+    if (e.taps > 0) p.taps_div = FastDiv(e.taps);
+    p.accumulate = e.accumulate ? 1 : 0;
+    p.lattice_w = e.lattice_w;
+    if (e.lattice_w > 0) p.lattice_div = FastDiv(e.lattice_w);
+    p.lattice_row = e.lattice_row;
+    p.lattice_col = e.lattice_col;
+    p.lattice_offset = e.lattice_offset;
+    p.cell_h = e.cell_h;
+    p.cell_w = e.cell_w;
+    p.plane_h = e.plane_h;
+    p.plane_w = e.plane_w;
+}
+
 // Runs one implicit product with the epilogue e (directly, or through split-K partials and the
 // FP64 slice reduction).
 int run_implicit(bool wgrad, const GemmPlan& plan, const float* a, int lda, int M, int N, int K, const ConvGather& g,
@@ -765,27 +822,7 @@ int run_implicit(bool wgrad, const GemmPlan& plan, const float* a, int lda, int 
         p.ldc = N;
         p.c_batch = static_cast<long long>(M) * N;
     } else {
-        p.C = c;
-        p.ldc = ldc;
-        p.bias = e.bias;
-        p.bias_mode = e.bias_mode;
-        p.act = e.act;
-        p.alpha = e.alpha;
-        p.segment = e.segment;
-        if (e.segment > 0) p.segment_div = FastDiv(e.segment);
-        p.segment_stride = e.segment_stride;
-        p.taps = e.taps;
-        if (e.taps > 0) p.taps_div = FastDiv(e.taps);
-        p.accumulate = e.accumulate ? 1 : 0;
-        p.lattice_w = e.lattice_w;
-        if (e.lattice_w > 0) p.lattice_div = FastDiv(e.lattice_w);
-        p.lattice_row = e.lattice_row;
-        p.lattice_col = e.lattice_col;
-        p.lattice_offset = e.lattice_offset;
-        p.cell_h = e.cell_h;
-        p.cell_w = e.cell_w;
-        p.plane_h = e.plane_h;
-        p.plane_w = e.plane_w;
+        set_epilogue(p, c, ldc, e);
     }
     const ImplicitTile& t = TILE_TABLE[plan.tile];
     const dim3 grid(blocks_for(N, t.bn), blocks_for(M, t.bm), static_cast<unsigned>(plan.slices));
@@ -989,6 +1026,67 @@ int conv_implicit_dgrad_phases(const ConvGeometry& g, const float* dy, const flo
     if (gaps && !accumulate && !cells) {
         MFH_TRY(launch_fill_zero(dx, static_cast<std::int64_t>(g.N) * g.CI * g.H * g.W, stream));
         accumulate = true;
+    }
+    if (engine == 1 && with_taps > 1 && implicit_chunked(g.CO)) {
+        // Every phase in one launch (64 x 64 tiles of four 32 x 32 waves, the fastest of the
+        // sweep on MI355X; no K split), the phase with the most taps first so that its longer
+        // tiles start first. The choice depends on the geometry only, so a dX written fresh and
+        // one added to a gradient run the same products.
+        const int tile = 6;
+        const ImplicitTile& t = TILE_TABLE[tile];
+        GroupedProducts batch{};
+        struct Entry { DgradPhase ph; long long offset; };
+        Entry entries[GROUPED_PRODUCTS];
+        int count = 0;
+        long long offset = 0;
+        bool fits = true;
+        for (int a = 0; a < g.SH; ++a)
+            for (int b = 0; b < g.SW; ++b) {
+                const DgradPhase ph = dgrad_phase(g, a, b);
+                const int taps = ph.th * ph.tw;
+                if (taps == 0) continue;
+                if (ph.hp > 0 && ph.wp > 0) {
+                    if (count == GROUPED_PRODUCTS) fits = false;
+                    else entries[count++] = Entry{ph, offset};
+                }
+                offset += static_cast<long long>(g.CI) * g.CO * taps;
+            }
+        std::stable_sort(entries, entries + (fits ? count : 0), [](const Entry& x, const Entry& y) {
+            return x.ph.th * x.ph.tw > y.ph.th * y.ph.tw;
+        });
+        std::int64_t blocks = 0;
+        for (int i = 0; fits && i < count; ++i) {
+            const DgradPhase& ph = entries[i].ph;
+            const int M = g.CI, N = g.N * ph.hp * ph.wp, K = g.CO * ph.th * ph.tw;
+            GemmParams& p = batch.p[i];
+            p.A = wphase + entries[i].offset;
+            p.lda = K;
+            p.M = M;
+            p.N = N;
+            p.K = K;
+            p.k_chunk = K;
+            GemmEpilogue e;
+            e.segment = ph.hp * ph.wp;
+            e.segment_stride = static_cast<long long>(g.CI) * g.H * g.W;
+            e.accumulate = accumulate;
+            e.lattice_w = ph.wp;
+            e.lattice_row = g.SH * g.W;
+            e.lattice_col = g.SW;
+            e.lattice_offset = ph.a * g.W + ph.b;
+            set_epilogue(p, dx, g.H * g.W, e);
+            batch.g[i] = gather_of(dy, g.CO, g.OH, g.OW, ph.th, ph.tw, 1, 1, ph.pad_h, ph.pad_w, g.N, ph.hp, ph.wp);
+            batch.tiles_n[i] = static_cast<int>(blocks_for(N, t.bn));
+            batch.first[i] = static_cast<int>(blocks);
+            blocks += static_cast<std::int64_t>(blocks_for(M, t.bm)) * batch.tiles_n[i];
+            fits = fits && aligned16(p.A) && blocks <= INDEX_LIMIT;
+        }
+        if (fits && count > 0) {
+            batch.first[count] = static_cast<int>(blocks);
+            batch.count = count;
+            hipLaunchKernelGGL(conv_kernels().grouped[tile], dim3(static_cast<unsigned>(blocks)), dim3(threads_of(t)),
+                               0, stream, batch);
+            return MFH_CHECK_LAUNCH("conv_implicit_grouped", stream);
+        }
     }
     long long offset = 0;
     for (int a = 0; a < g.SH; ++a)

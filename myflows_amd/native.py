@@ -424,9 +424,19 @@ def conv_weight_orders(requests):
     return outs
 
 
-def strided_dx_phases(kh, kw):
-    """Whether conv2d_backward's automatic choice runs a strided dX as phase products (1x1 kernels)."""
-    return int(kh) * int(kw) == 1
+# Longest phase product (CO x its taps) that the automatic choice still runs as phases.
+PHASE_MAX_K = 1024
+
+
+def strided_dx_phases(kh, kw, co, stride):
+    """Whether conv2d_backward's automatic choice runs a strided dX as phase products: a 1x1 kernel
+    (one phase product), or phases of at most PHASE_MAX_K reduction depth, which all run in one
+    launch. Measured on MI355X for ResNet18 at batch 64: the layer2 and layer3 3x3 stride-2 dX
+    (K up to 512 and 1024) take 47 and 55 us as phases against 67 and 71 us through the column
+    gradient; layer4's (K 2048, few pixels) 83 us against 67 us."""
+    sh, sw = (int(v) for v in stride)
+    longest = -(-int(kh) // sh) * -(-int(kw) // sw)
+    return int(kh) * int(kw) == 1 or int(co) * longest <= PHASE_MAX_K
 
 
 def _weight_order_buffer(order, weight, name):
@@ -506,7 +516,8 @@ def conv2d_backward(x, weight, grad_y, cols, *, stride=(1, 1), padding=(0, 0), n
     if algorithm == "implicit":
         if strided_dx not in ("auto", "phases", "columns"):
             raise ValueError('strided_dx must be "auto", "phases" or "columns"')
-        phases = strided_dx == "phases" or (strided_dx == "auto" and strided_dx_phases(g.kh, g.kw))
+        phases = strided_dx == "phases" or (strided_dx == "auto"
+                                            and strided_dx_phases(g.kh, g.kw, g.co, (g.sh, g.sw)))
         return _conv2d_backward_implicit(x, weight, grad_y, g, need_bias_grad, need_input_grad, need_weight_grad,
                                          act, alpha, output, engine, weight_flip, input_grad, phases)
     if weight_flip is not None or input_grad is not None:

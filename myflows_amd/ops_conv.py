@@ -101,7 +101,8 @@ class Conv2D_Op(GradientOp):
         if self._saved is None or not self.parents[0].requires_grad:
             return []
         kernel = self._saved[1]
-        if self.stride != (1, 1) and (kernel.ndim != 4 or not native.strided_dx_phases(*kernel.shape[2:])):
+        if self.stride != (1, 1) and (kernel.ndim != 4 or not native.strided_dx_phases(
+                kernel.shape[2], kernel.shape[3], kernel.shape[0], self.stride)):
             return []  # that dX runs through the column gradient, which reads the kernel in place
         return [(kernel, 1, self.stride, self.padding)]
 
