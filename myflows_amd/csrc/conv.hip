@@ -365,8 +365,30 @@ __global__ __launch_bounds__(256) void pool_forward_plane_kernel(const float* __
     }
 }
 
+// The gradient of input pixel (ih, iw) of staged plane pl: the dy of every window that covers the
+// pixel and whose argmax is it, added in (oh, ow) order.
+__device__ __forceinline__ float pool_pixel_grad(const float* grad, const int* where, int pl, int ih, int iw,
+                                                 int target, int OH, int OW, int KH, int KW, const FastDiv& div_sh,
+                                                 const FastDiv& div_sw) {
+    const int ohw = OH * OW;
+    const int oh_lo = ih >= KH ? div_sh.div(ih - KH) + 1 : 0;
+    const int oh_hi = min(OH - 1, div_sh.div(ih));
+    const int ow_lo = iw >= KW ? div_sw.div(iw - KW) + 1 : 0;
+    const int ow_hi = min(OW - 1, div_sw.div(iw));
+    float sum = 0.0f;
+    for (int oh = oh_lo; oh <= oh_hi; ++oh)
+        for (int ow = ow_lo; ow <= ow_hi; ++ow) {
+            const int o = pl * ohw + oh * OW + ow;
+            if (where[o] == target) sum += grad[o];
+        }
+    return sum;
+}
+
 // Max-pool backward over `per` consecutive planes per workgroup: the planes' dy and argmax are
 // staged in LDS, then every input pixel gathers the windows that cover it, in (oh, ow) order.
+// VEC4 (W a multiple of 4, dx 16-byte aligned): a thread takes four adjacent pixels of one row and
+// stores them with one 16-byte write.
+template <bool VEC4>
 __global__ __launch_bounds__(256) void pool_backward_plane_kernel(const float* __restrict__ dy,
                                                                   const int* __restrict__ argmax,
                                                                   float* __restrict__ dx, int planes, int per, int H,
@@ -386,22 +408,27 @@ __global__ __launch_bounds__(256) void pool_backward_plane_kernel(const float* _
     }
     __syncthreads();
     const long long in_base = static_cast<long long>(first_plane) * hw;
-    for (int e = threadIdx.x; e < count * hw; e += 256) {
-        int within, iw;
-        const int pl = div_hw.divmod(e, within);
-        const int ih = div_w.divmod(within, iw);
-        const int oh_lo = ih >= KH ? div_sh.div(ih - KH) + 1 : 0;
-        const int oh_hi = min(OH - 1, div_sh.div(ih));
-        const int ow_lo = iw >= KW ? div_sw.div(iw - KW) + 1 : 0;
-        const int ow_hi = min(OW - 1, div_sw.div(iw));
-        const int target = static_cast<int>(in_base + e);
-        float sum = 0.0f;
-        for (int oh = oh_lo; oh <= oh_hi; ++oh)
-            for (int ow = ow_lo; ow <= ow_hi; ++ow) {
-                const int o = pl * ohw + oh * OW + ow;
-                if (where[o] == target) sum += grad[o];
-            }
-        dx[in_base + e] = sum;
+    if constexpr (VEC4) {
+        for (int e = 4 * threadIdx.x; e < count * hw; e += 4 * 256) {
+            int within, iw;
+            const int pl = div_hw.divmod(e, within);
+            const int ih = div_w.divmod(within, iw);
+            const int target = static_cast<int>(in_base + e);
+            float4 v;
+            v.x = pool_pixel_grad(grad, where, pl, ih, iw, target, OH, OW, KH, KW, div_sh, div_sw);
+            v.y = pool_pixel_grad(grad, where, pl, ih, iw + 1, target + 1, OH, OW, KH, KW, div_sh, div_sw);
+            v.z = pool_pixel_grad(grad, where, pl, ih, iw + 2, target + 2, OH, OW, KH, KW, div_sh, div_sw);
+            v.w = pool_pixel_grad(grad, where, pl, ih, iw + 3, target + 3, OH, OW, KH, KW, div_sh, div_sw);
+            *reinterpret_cast<float4*>(dx + in_base + e) = v;
+        }
+    } else {
+        for (int e = threadIdx.x; e < count * hw; e += 256) {
+            int within, iw;
+            const int pl = div_hw.divmod(e, within);
+            const int ih = div_w.divmod(within, iw);
+            dx[in_base + e] = pool_pixel_grad(grad, where, pl, ih, iw, static_cast<int>(in_base + e), OH, OW, KH, KW,
+                                              div_sh, div_sw);
+        }
     }
 }
 
@@ -509,7 +536,9 @@ int launch_pool_backward(const float* dy, const int* argmax, float* dx, int N, i
     if (per > 0) {
         const int planes = N * C;
         const size_t lds = static_cast<size_t>(per) * OH * OW * 2 * sizeof(float);
-        pool_backward_plane_kernel<<<blocks_for(planes, per), 256, lds, stream>>>(
+        const bool vec4 = W % 4 == 0 && (reinterpret_cast<std::uintptr_t>(dx) & 15) == 0;
+        (vec4 ? pool_backward_plane_kernel<true> : pool_backward_plane_kernel<false>)<<<blocks_for(planes, per), 256,
+                                                                                       lds, stream>>>(
             dy, argmax, dx, planes, per, H, W, OH, OW, KH, KW, FastDiv(H * W), FastDiv(W), FastDiv(SH), FastDiv(SW));
         return MFH_CHECK_LAUNCH("pool_backward_plane", stream);
     }

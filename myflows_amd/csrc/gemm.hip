@@ -403,9 +403,59 @@ int split_reduce_epilogue(const float* partial, float* c, const GemmEpilogue& e,
     return launch_split_reduce(partial, c, epilogue_params(e, M, N, ldc), slices, stream);
 }
 
+namespace {
+
+// Outputs with few columns (N <= SKINNY_N, a matrix-vector-like product such as a small fully
+// connected layer): one wave per output row; lane l adds a[row][k] * b[k][n] for k = l, l + 64, ...
+// in k order, then a fixed butterfly adds the lanes, so every output has one summation order. The
+// MFMA tiles would leave all but N of their 32 or more columns idle and spend their time in
+// prologue and epilogue.
+constexpr int SKINNY_N = 8;
+__global__ __launch_bounds__(256) void gemm_skinny_kernel(GemmParams p, int trans_a, int trans_b) {
+    const int row = static_cast<int>(blockIdx.x) * 4 + static_cast<int>(threadIdx.x) / 64, lane = threadIdx.x % 64;
+    if (row >= p.M) return;  // uniform over the wave
+    float acc[SKINNY_N];
+#pragma unroll
+    for (int n = 0; n < SKINNY_N; ++n) acc[n] = 0.0f;
+    for (int k = lane; k < p.K; k += 64) {
+        const float a = trans_a ? p.A[static_cast<long long>(k) * p.lda + row] : p.A[static_cast<long long>(row) * p.lda + k];
+#pragma unroll
+        for (int n = 0; n < SKINNY_N; ++n)
+            if (n < p.N)
+                acc[n] += a * (trans_b ? p.B[static_cast<long long>(n) * p.ldb + k] : p.B[static_cast<long long>(k) * p.ldb + n]);
+    }
+#pragma unroll
+    for (int n = 0; n < SKINNY_N; ++n)
+#pragma unroll
+        for (int offset = 32; offset > 0; offset >>= 1) acc[n] += __shfl_xor(acc[n], offset, 64);
+    if (lane != 0) return;
+#pragma unroll
+    for (int n = 0; n < SKINNY_N; ++n) {
+        if (n >= p.N) break;
+        float v = acc[n];
+        if (p.bias_mode == BIAS_COLUMN) v += p.bias[n];
+        else if (p.bias_mode == BIAS_ROW) v += p.bias[row];
+        write_output(p, p.C, row, n, activate(v, p.act, p.alpha));
+    }
+}
+
+}  // namespace
+
 int gemm_launch(int engine, hipStream_t stream, const GemmOperands& o, const GemmEpilogue& e, float* workspace,
                 std::int64_t workspace_floats) {
     const int M = o.M, N = o.N, K = o.K;
+    if (engine == 1 && o.batch == 1 && N <= SKINNY_N && e.segment == 0 && e.taps == 0 && e.lattice_w == 0) {
+        GemmParams p = epilogue_params(e, M, N, o.ldc);
+        p.A = o.a;
+        p.B = o.b;
+        p.C = o.c;
+        p.K = K;
+        p.lda = o.lda;
+        p.ldb = o.ldb;
+        p.k_chunk = K;
+        gemm_skinny_kernel<<<blocks_for(M, 4), 256, 0, stream>>>(p, o.trans_a ? 1 : 0, o.trans_b ? 1 : 0);
+        return MFH_CHECK_LAUNCH("gemm_skinny", stream);
+    }
     GemmPlan plan;
     MFH_TRY(gemm_plan_from_engine(engine, M, N, K, &plan, o.batch));
     if (o.batch > 1 || (plan.slices > 1 && (!workspace || workspace_floats < gemm_workspace_floats(plan, M, N))))

@@ -729,7 +729,9 @@ def split_reduce(partials, *, reference=False):
 
 
 def gemm(a, b, bias=None, *, trans_a=False, trans_b=False, engine="mfma", out=None, plan=None):
-    """Row-major ``op(a) @ op(b) (+ bias)`` on the MFMA engine.
+    """Row-major ``op(a) @ op(b) (+ bias)`` on the MFMA engine (the automatic plan of a product with
+    at most 8 output columns takes a one-wave-per-row kernel instead: lanes split K, a fixed
+    butterfly adds them).
 
     op(a) = a.T when trans_a (a stored K x M), op(b) = b.T when trans_b (b stored N x K); not both.
     plan=(tile, slices) forces a tile of tile_catalog() and a split-K slice count.

@@ -1,7 +1,8 @@
 """GEMM engine and teaching matmul parity on the GPU.
 
-The MFMA engine's accumulation order differs from a sequential FMA loop, so its results are checked
-against the FP64 product: every output within the worst-case bound gamma_K |A||B| (plus one
+The MFMA engine's accumulation order differs from a sequential FMA loop (and so does the
+one-wave-per-row kernel that the automatic plan takes for at most 8 output columns), so its results
+are checked against the FP64 product: every output within the worst-case bound gamma_K |A||B| (plus one
 rounding for the split-K reduction and the bias), the normwise criterion of 1e-5 of max|C|, and
 identical bits run to run. The split-K reduction is bit-exact against the FP64 loop. The teaching
 kernels keep the reference's properties (bounds, Dot2 within one ulp, the compensated modes more
@@ -18,7 +19,9 @@ from tests.fixtures import EPS32, assert_near, gamma_k
 pytestmark = pytest.mark.gpu
 
 SHAPES = ((67, 39, 45), (256, 132, 68), (300, 260, 1000), (36, 20, 3000), (16, 144, 19200), (4096, 16, 147),
-          (64, 576, 2048), (1, 1, 1), (512, 512, 512), (38400, 64, 576), (576, 64, 38400))
+          (64, 576, 2048), (1, 1, 1), (512, 512, 512), (38400, 64, 576), (576, 64, 38400),
+          # up to 8 output columns: the one-wave-per-row kernel of the automatic plan
+          (64, 2, 512), (512, 2, 64), (4096, 8, 147), (7, 5, 3000), (300, 1, 1000))
 LAYOUTS = {"NN": (False, False), "NT": (False, True), "TN": (True, False)}
 
 
