@@ -263,7 +263,7 @@ MFH_API int mfh_plane_mean(uint64_t x, uint64_t y, int64_t planes, int hw, uint6
  * Replaces GlobalAvgPool2d_Op.backward, ops/batchnorm.py:118-123 (the broadcast gradient written out). */
 MFH_API int mfh_plane_mean_backward(uint64_t dy, uint64_t dx, int64_t planes, int hw, int add, uint64_t stream);
 
-/* loss[0] = float(FP64 sum of float32 (pred - target)^2 / count) (count = 0: 0).
+/* loss[0] = float(FP64 sum of float32 (pred - target)^2 / count) (count = 0: NaN, the mean of nothing).
  * Replaces MSELoss.forward, ops/loss.py:99-106. */
 MFH_API int mfh_mse_loss(uint64_t pred, uint64_t target, uint64_t loss, int64_t count, uint64_t stream);
 

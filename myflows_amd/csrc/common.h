@@ -371,7 +371,7 @@ int launch_adam(const AdamTensor* tensors, int count, const AdamScalars& s, hipS
 int launch_plane_mean(const float* x, float* y, std::int64_t planes, int hw, hipStream_t stream);
 // dx[p * hw + i] (+)= dy[p] / float(hw)
 int launch_plane_mean_backward(const float* dy, float* dx, std::int64_t planes, int hw, bool add, hipStream_t stream);
-// loss[0] = float(FP64 sum of float32 (pred - target)^2 / count)
+// loss[0] = float(FP64 sum of float32 (pred - target)^2 / count), NaN when count is 0
 int launch_mse_loss(const float* pred, const float* target, float* loss, std::int64_t count, hipStream_t stream);
 // grad (+)= seed[0] * ((2 * (pred - target)) / float(count)), float32 in that order
 int launch_mse_grad(const float* pred, const float* target, const float* seed, float* grad, std::int64_t count,

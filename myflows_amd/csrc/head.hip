@@ -56,7 +56,9 @@ __global__ __launch_bounds__(LOSS_THREADS) void mse_loss_kernel(const float* __r
         if (static_cast<int>(threadIdx.x) < half) partial[threadIdx.x] += partial[threadIdx.x + half];
         __syncthreads();
     }
-    if (threadIdx.x == 0) loss[0] = static_cast<float>(partial[0] / static_cast<double>(count > 0 ? count : 1));
+    // The mean of no elements is NaN, as the operator's FP64 mean of an empty array.
+    if (threadIdx.x == 0)
+        loss[0] = count > 0 ? static_cast<float>(partial[0] / static_cast<double>(count)) : __builtin_nanf("");
 }
 
 __global__ __launch_bounds__(HEAD_THREADS) void mse_grad_kernel(const float* __restrict__ pred,

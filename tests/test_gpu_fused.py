@@ -202,6 +202,13 @@ def test_mse_loss_and_gradient_match_the_oracle(shape):
     np.testing.assert_array_equal(host(out), base + rp.mse_backward(pred, target))
 
 
+def test_mse_of_no_elements_is_nan_like_the_oracle():
+    empty = np.zeros((0, 2), dtype=np.float32)
+    with np.errstate(invalid="ignore", divide="ignore"), pytest.warns(RuntimeWarning):
+        ref = rp.mse_forward(empty, empty)
+    assert np.isnan(ref) and np.isnan(host(fused.mse_loss_forward(gpu(empty), gpu(empty))))
+
+
 def test_linear_bias_gradient_column_sums():
     rng = np.random.default_rng(33)
     g = rng.normal(size=(64, 2)).astype(np.float32)
