@@ -213,8 +213,8 @@ MFH_API int mfh_gemm(int engine, int trans_a, int trans_b, uint64_t a, uint64_t 
 
 /* ---- batch normalisation (+ residual add + ReLU) -------------------------------------------- */
 
-/* FP64 workspace (doubles) that mfh_bn_forward (training) and mfh_bn_backward need for an NCHW
- * tensor of N x C x HW elements; -1 on error. No reference counterpart: the reference sizes its
+/* FP64 workspace (doubles, 16-byte aligned) that mfh_bn_forward (training) and mfh_bn_backward need
+ * for an NCHW tensor of N x C x HW elements; -1 on error. No reference counterpart: the reference sizes its
  * partial buffer inline (ops/fused.py:238-243, 265-266). */
 MFH_API int64_t mfh_bn_workspace(int N, int C, int HW);
 

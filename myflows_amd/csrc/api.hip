@@ -569,6 +569,7 @@ MFH_API int mfh_bn_forward(std::uint64_t x, std::uint64_t gamma, std::uint64_t b
                 "batch-norm forward received a null buffer");
     MFH_REQUIRE(!training || (workspace && workspace_doubles >= norm_workspace_doubles(s)),
                 "batch-norm workspace is smaller than mfh_bn_workspace");
+    MFH_REQUIRE(!training || (workspace & 15) == 0, "batch-norm workspace must be 16-byte aligned");
     MFH_REQUIRE(eps >= 0.0 && momentum >= 0.0 && momentum <= 1.0, "batch-norm eps and momentum are out of range");
     NormForward f{};
     f.x = as_ptr<const float>(x);
@@ -601,6 +602,7 @@ MFH_API int mfh_bn_backward(std::uint64_t x, std::uint64_t dy, std::uint64_t gat
     MFH_REQUIRE(!residual_grad || gate, "a residual gradient comes from a fused ReLU: pass its output as gate");
     MFH_REQUIRE(workspace && workspace_doubles >= norm_workspace_doubles(s),
                 "batch-norm workspace is smaller than mfh_bn_workspace");
+    MFH_REQUIRE((workspace & 15) == 0, "batch-norm workspace must be 16-byte aligned");
     NormBackward b{};
     b.x = as_ptr<const float>(x);
     b.dy = as_ptr<const float>(dy);

@@ -138,14 +138,28 @@ __global__ __launch_bounds__(PT) void norm_partials_kernel(PartialArgs p) {
     }
 }
 
-// Sum of channel c's slice partials in slice order.
+// Sum of channel c's slice partials in slice order. The loads of SLICES_AHEAD slices are issued
+// before their additions, which still run one at a time in slice order.
+constexpr int SLICES_AHEAD = 8;
 __device__ __forceinline__ void slice_sums(const double* __restrict__ partial, int c, int slices, double& a,
                                            double& b) {
     a = 0.0;
     b = 0.0;
-    for (int s = 0; s < slices; ++s) {
-        a += partial[(static_cast<long long>(c) * slices + s) * 2];
-        b += partial[(static_cast<long long>(c) * slices + s) * 2 + 1];
+    const double* row = partial + static_cast<long long>(c) * slices * 2;
+    int s = 0;
+    for (; s + SLICES_AHEAD <= slices; s += SLICES_AHEAD) {
+        double2 v[SLICES_AHEAD];
+#pragma unroll
+        for (int u = 0; u < SLICES_AHEAD; ++u) v[u] = *reinterpret_cast<const double2*>(row + 2 * (s + u));
+#pragma unroll
+        for (int u = 0; u < SLICES_AHEAD; ++u) {
+            a += v[u].x;
+            b += v[u].y;
+        }
+    }
+    for (; s < slices; ++s) {
+        a += row[2 * s];
+        b += row[2 * s + 1];
     }
 }
 
@@ -504,7 +518,7 @@ bool aligned16(const void* q) { return (reinterpret_cast<std::uintptr_t>(q) & 15
 int norm_slices(const NormShape& s) {
     const std::int64_t positions = static_cast<std::int64_t>(s.N) * s.HW;
     if (positions <= CHANNEL_FUSED_MAX) return 1;  // one workgroup per channel, one launch per pass
-    const std::int64_t wanted = (4LL * device_cu_count() + s.C - 1) / s.C;
+    const std::int64_t wanted = (8LL * device_cu_count() + s.C - 1) / s.C;
     const std::int64_t most = std::max<std::int64_t>(1, positions / MIN_SLICE);
     return static_cast<int>(std::max<std::int64_t>(1, std::min(wanted, most)));
 }
