@@ -79,7 +79,15 @@ __global__ __launch_bounds__(HEAD_THREADS) void column_sums_kernel(const float* 
     const long long j = static_cast<long long>(blockIdx.x) * HEAD_THREADS + threadIdx.x;
     if (j >= cols) return;
     double s = 0.0;
-    for (long long r = 0; r < rows; ++r) s += static_cast<double>(src[r * cols + j]);
+    long long r = 0;
+    for (; r + 8 <= rows; r += 8) {  // eight loads in flight, added in row order
+        float v[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) v[u] = src[(r + u) * cols + j];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) s += static_cast<double>(v[u]);
+    }
+    for (; r < rows; ++r) s += static_cast<double>(src[r * cols + j]);
     out[j] = static_cast<float>(s);
 }
 

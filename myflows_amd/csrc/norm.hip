@@ -403,7 +403,7 @@ __global__ __launch_bounds__(PT) void norm_forward_channel_kernel(PartialArgs pa
     __shared__ float coef[3];
     const int c = blockIdx.x, total = pa.total, plane = p.C * p.HW;
     const double centre = static_cast<double>(p.x[c * p.HW]);
-    float xv[CHANNEL_PER];
+    float xv[CHANNEL_PER], rv[CHANNEL_PER];  // x and the residual, both loaded before the sums
     int at[CHANNEL_PER];
 #pragma unroll
     for (int i = 0; i < CHANNEL_PER; ++i) {
@@ -412,6 +412,7 @@ __global__ __launch_bounds__(PT) void norm_forward_channel_kernel(PartialArgs pa
         const int n = p.div_hw.divmod(j < total ? j : 0, hw);
         at[i] = n * plane + c * p.HW + hw;
         xv[i] = j < total ? p.x[at[i]] : 0.0f;
+        rv[i] = j < total && p.residual ? p.residual[at[i]] : 0.0f;
     }
     double a[CHAINS] = {}, b[CHAINS] = {};
 #pragma unroll
@@ -443,8 +444,7 @@ __global__ __launch_bounds__(PT) void norm_forward_channel_kernel(PartialArgs pa
 #pragma unroll
     for (int i = 0; i < CHANNEL_PER; ++i) {
         if (threadIdx.x + i * PT >= total) continue;
-        const float r = p.residual ? p.residual[at[i]] : 0.0f;
-        p.y[at[i]] = apply_value(p, xv[i], r, m_hi, m_lo, istd, g, bt);
+        p.y[at[i]] = apply_value(p, xv[i], rv[i], m_hi, m_lo, istd, g, bt);
     }
 }
 
