@@ -205,7 +205,9 @@ MFH_API int mfh_split_reduce(uint64_t partial, uint64_t c, int slices, int M, in
 
 /* C(M,N) = op(A) op(B) [+ bias(N)], row-major with leading dimensions lda/ldb/ldc. op(A) = A^T when
  * trans_a (A stored K x M), op(B) = B^T when trans_b (B stored N x K); not both. workspace may be
- * 0; with the plan's slices * M * N floats the engine splits K. bias needs ldc == N.
+ * 0; with the plan's slices * M * N floats the engine splits K. bias needs ldc == N. Engine 1 with
+ * N <= 8 runs one wave per output row (lanes split K, a fixed butterfly adds them); an explicit
+ * plan code always runs the MFMA tiles.
  * Replaces mf_gemm, native_cublas.cpp:1672-1692. */
 MFH_API int mfh_gemm(int engine, int trans_a, int trans_b, uint64_t a, uint64_t b, uint64_t bias, uint64_t c, int M,
                      int N, int K, int lda, int ldb, int ldc, uint64_t workspace, int64_t workspace_floats,
