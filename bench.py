@@ -172,7 +172,7 @@ def c3_kernels():
         native._raise_for(lib.mfh_conv_im2col(x.data_ptr(), cols.data_ptr(), *dims, stream), lib)
 
     def conv_forward():
-        native._raise_for(lib.mfh_conv_forward_implicit(x.data_ptr(), weight.data_ptr(), wt.data_ptr(), 0, 0,
+        native._raise_for(lib.mfh_conv_forward_implicit(x.data_ptr(), weight.data_ptr(), wt.data_ptr(), 0, 0, 0,
                                                         y.data_ptr(), *dims, 0, 0.0, 1, 0, 0, stream), lib)
 
     pooled = torch.empty((n, co, h // 2, w // 2), device="cuda")
@@ -235,8 +235,8 @@ C5_STEP_GFLOP = 920.2
 def c5_inference(batch=256, size=224, reps=10, warmup=3, seed=0):
     """ResNet18(output_dim=2) inference at batch 256, 3x224x224 ~ N(0, 1), eval-mode
     batch norm with running variance ~ U(0.5, 1.5) and mean ~ N(0, 0.1) (seeded), BN folded into the
-    convolutions and ReLU fused into their epilogues (apply_graph_optimizations(mode="inference"),
-    then Graph(optimize=True)). Images per second over `reps` forward passes."""
+    convolutions, ReLU and each block's residual add fused into their epilogues
+    (apply_graph_optimizations(mode="inference"), then Graph(optimize=True)). Images per second over `reps` forward passes."""
     model = mf.ResNet18(output_dim=2, initializer=mf.make_initializer(seed=seed), conv_backend="hip_native")
     rng = np.random.default_rng(seed)
     x_np = rng.standard_normal((batch, 3, size, size)).astype(np.float32)
@@ -256,10 +256,10 @@ def c5_inference(batch=256, size=224, reps=10, warmup=3, seed=0):
     torch.cuda.synchronize()
     seconds = time.perf_counter() - start
     ms = seconds * 1e3 / reps
-    return {"config": f"ResNet18 inference bs{batch} 3x{size}x{size}, BN folded, Conv+ReLU epilogues",
+    return {"config": f"ResNet18 inference bs{batch} 3x{size}x{size}, BN folded, Conv+ReLU and Conv+Add+ReLU epilogues",
             "images/s": round(batch * reps / seconds, 1), "ms_per_batch": round(ms, 3),
             "TFLOP/s": round(C5_STEP_GFLOP * batch / 256 / (ms * 1e-3) / 1e3, 2), "bn_folds": stats["bn_folds"],
-            "conv_act_fusions": graph._opt_stats["conv_act_fusions"]}
+            "conv_act_fusions": graph._opt_stats["conv_act_fusions"], "conv_add_act_fusions": stats["conv_add_act_fusions"]}
 
 
 def cpu_baseline(min_seconds=10.0, batch=2):

@@ -88,7 +88,7 @@ MFH_API int mfh_conv_backward(uint64_t weight, uint64_t dy, uint64_t y, uint64_t
                               int grid_x, int activation, float alpha, int dw_engine, int dx_engine,
                               uint64_t workspace, int64_t workspace_floats, uint64_t stream);
 
-/* Implicit-GEMM convolution forward: y (N,CO,OH,OW) = act(conv(x, weight) + bias) with the im2col
+/* Implicit-GEMM convolution forward: y (N,CO,OH,OW) = act(conv(x, weight) + bias [+ residual]) with the im2col
  * matrix gathered from x inside the GEMM's operand loads (no cols buffer). One GEMM
  * W (CO x K) . view (K x N*OH*OW) over every image, stored straight into NCHW with the bias and
  * activation in its epilogue. When CI is a multiple of 32 the features run in channel chunks of 32
@@ -97,11 +97,14 @@ MFH_API int mfh_conv_backward(uint64_t weight, uint64_t dy, uint64_t y, uint64_t
  * wt already holds it (mfh_conv_weight_orders, flip 0) and `weight` is not read (it may be 0).
  * Otherwise wt is unused and may be 0. workspace: mfh_conv_implicit_workspace(..., 0) floats let
  * it split K (0 is allowed: no split). engine: 1 (automatic plan) or 16 + tile * 128 + slices - 1
- * over the 12 tiles of the implicit products. Arguments otherwise as mfh_conv_forward.
+ * over the 12 tiles of the implicit products. residual (may be 0): an NCHW tensor of y's shape added
+ * to conv + bias before the activation, each addition rounded to float32 as separate operations
+ * would be (the fused Conv + Add + ReLU of an inference graph). Arguments otherwise as
+ * mfh_conv_forward.
  * Has no single counterpart in the reference: it replaces the im2col + gemm_rows + epilogue sequence
  * of mf_conv_forward, native_cublas.cpp:1441-1461, when the caller does not keep cols. */
 MFH_API int mfh_conv_forward_implicit(uint64_t x, uint64_t weight, uint64_t wt, int prepared, uint64_t bias,
-                                      uint64_t y, int N, int CI, int H, int W, int CO, int KH, int KW, int OH, int OW,
+                                      uint64_t residual, uint64_t y, int N, int CI, int H, int W, int CO, int KH, int KW, int OH, int OW,
                                       int SH, int SW, int PH, int PW, int activation, float alpha, int engine,
                                       uint64_t workspace, int64_t workspace_floats, uint64_t stream);
 

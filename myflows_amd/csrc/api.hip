@@ -310,7 +310,7 @@ MFH_API int mfh_conv_backward(std::uint64_t weight, std::uint64_t dy, std::uint6
 }
 
 MFH_API int mfh_conv_forward_implicit(std::uint64_t x, std::uint64_t weight, std::uint64_t wt, int prepared,
-                                      std::uint64_t bias, std::uint64_t y, int N, int CI, int H, int W, int CO, int KH,
+                                      std::uint64_t bias, std::uint64_t residual, std::uint64_t y, int N, int CI, int H, int W, int CO, int KH,
                                       int KW, int OH, int OW, int SH, int SW, int PH, int PW, int activation,
                                       float alpha, int engine, std::uint64_t workspace, std::int64_t workspace_floats,
                                       std::uint64_t stream) {
@@ -324,8 +324,9 @@ MFH_API int mfh_conv_forward_implicit(std::uint64_t x, std::uint64_t weight, std
     MFH_REQUIRE(prepared == 0 || prepared == 1, "prepared must be 0 or 1");
     MFH_REQUIRE(workspace_floats >= 0, "workspace size must be non-negative");
     return conv_implicit_forward(g, as_ptr<const float>(x), as_ptr<const float>(weight), as_ptr<float>(wt),
-                                 prepared == 1, as_ptr<const float>(bias), as_ptr<float>(y), activation, alpha, engine,
-                                 as_ptr<float>(workspace), workspace_floats, as_stream(stream));
+                                 prepared == 1, as_ptr<const float>(bias), as_ptr<const float>(residual),
+                                 as_ptr<float>(y), activation, alpha, engine, as_ptr<float>(workspace),
+                                 workspace_floats, as_stream(stream));
 }
 
 MFH_API int mfh_conv_weight_orders(const std::uint64_t* weights, const std::uint64_t* outs, const int* dims, int count,

@@ -137,6 +137,7 @@ struct GemmParams {
     int taps;                  // > 0: columns are convolution features in chunked order (see ConvGather)
     FastDiv taps_div;          // division by taps
     int accumulate;            // 1: each output is added to what C holds (C = C + result)
+    const float* residual;     // non-null: added to (product + bias) before the activation, C's layout
     // > 0: a segment is a lattice_w-wide grid of a larger plane, element (i, j) of the segment at
     // i * lattice_row + j * lattice_col + lattice_offset (the phases of a strided dX).
     int lattice_w;
@@ -181,6 +182,7 @@ struct GemmEpilogue {
     long long segment_stride = 0;
     int taps = 0;  // KH*KW when the output columns are features in chunked order; stored in natural order
     bool accumulate = false;  // C = C + result: a gradient added to one already there, in one pass
+    const float* residual = nullptr;  // act(product + bias + residual), residual laid out as C
     // Segments spread over a lattice of a larger plane (see GemmParams::lattice_w); 0: contiguous.
     int lattice_w = 0, lattice_row = 0, lattice_col = 0, lattice_offset = 0;
     int cell_h = 0, cell_w = 0, plane_h = 0, plane_w = 0;  // see GemmParams::cell_h
@@ -234,8 +236,8 @@ inline bool implicit_chunked(int C) { return C % CHANNEL_CHUNK == 0; }
 // the kernel in the order launch_weight_orders writes (flip 0): from wt, which this call fills
 // from w unless `prepared` says that it holds that order already.
 int conv_implicit_forward(const ConvGeometry& g, const float* x, const float* w, float* wt, bool prepared,
-                          const float* bias, float* y, int act, float alpha, int engine, float* workspace,
-                          std::int64_t workspace_floats, hipStream_t stream);
+                          const float* bias, const float* residual, float* y, int act, float alpha, int engine,
+                          float* workspace, std::int64_t workspace_floats, hipStream_t stream);
 // dW = dy . im2col(x), with dy read in place from NCHW. With db, the workgroups of the first
 // feature tile also sum dy over their pixel slice in FP64; an unsplit product writes db itself, a
 // split one leaves bias_partial[z * CO + co] for slice z (at most WGRAD_MAX_SLICES) and its

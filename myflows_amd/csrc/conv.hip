@@ -277,7 +277,7 @@ __global__ __launch_bounds__(256) void pool_backward_kernel(const float* __restr
     dx[idx] = sum;
 }
 
-constexpr int PLANE_FLOATS = 12288;   // floats of one workgroup's LDS plane buffer (48 KB)
+constexpr int PLANE_FLOATS = 16384;   // floats of one workgroup's LDS plane buffer (64 KB)
 constexpr int ROW_FLOATS = 12288;     // floats of the im2col row kernel's LDS input band (48 KB)
 
 // im2col of one output row (n, oh) per workgroup: the KH input rows it reads, for every channel and

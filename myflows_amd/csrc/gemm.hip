@@ -70,6 +70,7 @@ __device__ __forceinline__ void finish_output(const GemmParams& p, float* C, lon
     float v = static_cast<float>(s);
     if (p.bias_mode == BIAS_COLUMN) v += p.bias[col];
     else if (p.bias_mode == BIAS_ROW) v += p.bias[row];
+    if (p.residual) v = v + p.residual[output_offset(p, row, col)];
     write_output(p, C, row, col, activate(v, p.act, p.alpha));
 }
 
@@ -351,6 +352,7 @@ GemmParams epilogue_params(const GemmEpilogue& e, int M, int N, int ldc) {
     p.taps = e.taps;
     if (e.taps > 0) p.taps_div = FastDiv(e.taps);
     p.accumulate = e.accumulate ? 1 : 0;
+    p.residual = e.residual;
     p.lattice_w = e.lattice_w;
     if (e.lattice_w > 0) p.lattice_div = FastDiv(e.lattice_w);
     p.lattice_row = e.lattice_row;
@@ -444,7 +446,8 @@ __global__ __launch_bounds__(256) void gemm_skinny_kernel(GemmParams p, int tran
 int gemm_launch(int engine, hipStream_t stream, const GemmOperands& o, const GemmEpilogue& e, float* workspace,
                 std::int64_t workspace_floats) {
     const int M = o.M, N = o.N, K = o.K;
-    if (engine == 1 && o.batch == 1 && N <= SKINNY_N && e.segment == 0 && e.taps == 0 && e.lattice_w == 0) {
+    if (engine == 1 && o.batch == 1 && N <= SKINNY_N && e.segment == 0 && e.taps == 0 && e.lattice_w == 0 &&
+        !e.residual) {
         GemmParams p = epilogue_params(e, M, N, o.ldc);
         p.A = o.a;
         p.B = o.b;
@@ -490,6 +493,7 @@ int gemm_launch(int engine, hipStream_t stream, const GemmOperands& o, const Gem
         p.segment = 0;
         p.taps = 0;
         p.accumulate = 0;
+        p.residual = nullptr;
     } else {
         p.C = o.c;
         p.c_batch = o.c_batch;

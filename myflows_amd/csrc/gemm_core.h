@@ -285,7 +285,9 @@ __device__ __forceinline__ void store_acc(const GemmParams& p, float* __restrict
                     float v = acc[i][j][r];
                     if (p.bias_mode == BIAS_COLUMN) v += col_bias;
                     else if (p.bias_mode == BIAS_ROW) v += bias[row];
-                    float* out = C + col_offset + static_cast<long long>(row) * p.ldc;
+                    const long long offset = col_offset + static_cast<long long>(row) * p.ldc;
+                    if (p.residual) v = v + p.residual[offset];
+                    float* out = C + offset;
                     v = activate(v, p.act, p.alpha);
                     *out = p.accumulate ? *out + v : v;
                     if (p.cell_h) zero_cell(p, C, row, col);

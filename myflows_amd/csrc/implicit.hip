@@ -792,6 +792,7 @@ void set_epilogue(GemmParams& p, float* c, int ldc, const GemmEpilogue& e) {
     p.taps = e.taps;
     if (e.taps > 0) p.taps_div = FastDiv(e.taps);
     p.accumulate = e.accumulate ? 1 : 0;
+    p.residual = e.residual;
     p.lattice_w = e.lattice_w;
     if (e.lattice_w > 0) p.lattice_div = FastDiv(e.lattice_w);
     p.lattice_row = e.lattice_row;
@@ -948,8 +949,8 @@ int launch_weight_orders(const WeightOrder* orders, int count, hipStream_t strea
 }
 
 int conv_implicit_forward(const ConvGeometry& g, const float* x, const float* w, float* wt, bool prepared,
-                          const float* bias, float* y, int act, float alpha, int engine, float* workspace,
-                          std::int64_t workspace_floats, hipStream_t stream) {
+                          const float* bias, const float* residual, float* y, int act, float alpha, int engine,
+                          float* workspace, std::int64_t workspace_floats, hipStream_t stream) {
     const int M = g.CO, N = g.rows(), K = g.features();
     GemmPlan plan;
     MFH_TRY(implicit_plan(false, implicit_chunked(g.CI), engine, M, N, K, workspace, workspace_floats, &plan));
@@ -968,6 +969,7 @@ int conv_implicit_forward(const ConvGeometry& g, const float* x, const float* w,
     e.alpha = alpha;
     e.segment = g.ohw();
     e.segment_stride = static_cast<long long>(g.CO) * g.ohw();
+    e.residual = residual;
     return run_implicit(false, plan, w, K, M, N, K, gather, y, g.ohw(), e, workspace, stream);
 }
 

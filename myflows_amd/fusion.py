@@ -9,7 +9,10 @@ The passes of the reference's ``core/graph_opt.py``:
   convolution with copies of its kernel and bias scaled by gamma / sqrt(var + eps) (the model's own
   parameters are left untouched);
 * ``batchnorm_activation_groups`` (:231-257): ReLU(BN(x)) and ReLU(BN(x) + residual) whose
-  intermediates nobody else reads -> one BatchNormActivation unit.
+  intermediates nobody else reads -> one BatchNormActivation unit;
+* ``fuse_conv_add_relu`` (inference, after the BN fold; no counterpart in the reference):
+  ReLU(Conv2D_Op + residual) whose convolution and Add outputs nobody else reads -> one
+  Conv2D_AddReLU_Op, the residual add and the ReLU in the GEMM epilogue.
 
 As in the reference, ``mode="inference"`` turns on the BN fold, and activation fusion runs before
 it within one call, so a ReLU whose parent becomes a convolution only through folding is fused by a
@@ -139,14 +142,56 @@ def apply_graph_optimizations(root, *, mode="train", fold_constants=True, fuse_l
     Linear directly and has no separate MatMul + Add to fuse."""
     if fold_bn is None:
         fold_bn = str(mode).lower() == "inference"
-    stats = {"constant_folds": 0, "linear_fusions": 0, "conv_act_fusions": 0, "bn_folds": 0}
+    stats = {"constant_folds": 0, "linear_fusions": 0, "conv_act_fusions": 0, "bn_folds": 0,
+             "conv_add_act_fusions": 0}
     if fold_constants:
         root, stats["constant_folds"] = fold_constant_adds(root)
     if fuse_activations:
         root, stats["conv_act_fusions"] = fuse_conv_activation_ops(root)
     if fold_bn:
         root, stats["bn_folds"] = fold_bn_into_conv(root)
+        if fuse_activations:
+            root, stats["conv_add_act_fusions"] = fuse_conv_add_relu(root)
     return root, stats
+
+
+def fuse_conv_add_relu(root):
+    """ReLU(Add(Conv2D_Op, residual)) -> Conv2D_AddReLU_Op when the convolution and the Add have no
+    other reader (a residual block's second convolution once its BN is folded). For graphs that take
+    no gradient: the fused operator has no backward."""
+    from .ops_basic import Add, ReLU
+    from .ops_conv import Conv2D_AddReLU_Op, Conv2D_Op
+
+    fused = 0
+    for node in topological_order(root):
+        if type(node) is not ReLU or len(node.parents) != 1:
+            continue
+        add = node.parents[0]
+        if type(add) is not Add or len(add.parents) != 2 or add.children != [node]:
+            continue
+        pick = None
+        for k in (0, 1):
+            conv, residual = add.parents[k], add.parents[1 - k]
+            if type(conv) is Conv2D_Op and conv.children == [add] and residual is not conv:
+                pick = (conv, residual)
+                break
+        if pick is None:
+            continue
+        conv, residual = pick
+        bias = conv.parents[2] if len(conv.parents) == 3 else None
+        replacement = Conv2D_AddReLU_Op(conv.parents[0], conv.parents[1], residual, stride=conv.stride,
+                                        padding=conv.padding, bias=bias, backend=conv.backend,
+                                        recompute_im2col=conv.recompute_im2col)
+        if node is root:
+            root = replacement
+        replace_node(node, replacement)
+        for stale in (add, conv):  # the replaced nodes leave their parents' children lists
+            for parent in stale.parents:
+                if stale in parent.children:
+                    parent.children.remove(stale)
+            stale.children = []
+        fused += 1
+    return root, fused
 
 
 def batchnorm_activation_groups(nodes):

@@ -76,7 +76,7 @@ _SIGNATURES = {
     "mfh_conv_im2col": ("i", "pp" + _CONV + "p"),
     "mfh_conv_forward": ("i", "pppppp" + _CONV + "ifipqp"),
     "mfh_conv_backward": ("i", "pppppppppp" + _CONV + "iifiipqp"),
-    "mfh_conv_forward_implicit": ("i", "pppipp" + _CONV + "ifipqp"),
+    "mfh_conv_forward_implicit": ("i", "pppippp" + _CONV + "ifipqp"),
     "mfh_conv_weight_orders": ("i", "UUPip"),
     "mfh_conv_implicit_workspace": ("q", _CONV + "i"),
     "mfh_conv_backward_implicit": ("i", "ppppppppppp" + _CONV + "ifiiipqp"),
@@ -447,12 +447,14 @@ def _weight_order_buffer(order, weight, name):
 
 
 def conv2d_forward(x, weight, bias=None, *, stride=(1, 1), padding=(0, 0), activation=None, alpha=0.0,
-                   engine="mfma", algorithm=None, weight_order=None):
+                   engine="mfma", algorithm=None, weight_order=None, residual=None):
     """(y, cols): the contiguous NCHW output with bias and activation applied, and the im2col
     columns of x that conv2d_backward needs for dW. With algorithm "implicit" (the default) the GEMM
     gathers the columns from x itself and cols is None; "im2col" writes and returns them.
     weight_order: this kernel from conv_weight_orders(flip 0), which the implicit product then reads
-    instead of reordering the kernel itself."""
+    instead of reordering the kernel itself. residual (implicit only): a tensor of y's shape added
+    to conv + bias before the activation, act((conv + bias) + residual), each step one float32
+    rounding as in separate Add and activation operators."""
     engine = _engine_code(engine)
     algorithm = _conv_algorithm(algorithm)
     x, weight = _device_f32(x, "x"), _device_f32(weight, "weight")
@@ -464,6 +466,12 @@ def conv2d_forward(x, weight, bias=None, *, stride=(1, 1), padding=(0, 0), activ
     act, alpha = _activation_code(activation, alpha)
     device = x.device
     y = torch.empty(g.out_shape, dtype=torch.float32, device=device)
+    if residual is not None:
+        if algorithm != "implicit":
+            raise ValueError("a residual is added by the implicit algorithm's epilogue only")
+        residual = _device_f32(residual, "residual")
+        if tuple(residual.shape) != g.out_shape:
+            raise ValueError("residual must have the convolution's output shape")
     if algorithm == "implicit":
         workspace, floats = _implicit_workspace(g, "forward")
         prepared = 0
@@ -474,7 +482,7 @@ def conv2d_forward(x, weight, bias=None, *, stride=(1, 1), padding=(0, 0), activ
             else:
                 wt = torch.empty_like(weight)
         _call("mfh_conv_forward_implicit", x.data_ptr(), weight.data_ptr(), _addr(wt), prepared, _addr(bias),
-              y.data_ptr(), *g.c_args(), act, alpha, engine, _addr(workspace), floats, _stream())
+              _addr(residual), y.data_ptr(), *g.c_args(), act, alpha, engine, _addr(workspace), floats, _stream())
         return y, None
     cols = torch.empty((g.m, g.k), dtype=torch.float32, device=device)
     rows = None

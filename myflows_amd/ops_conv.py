@@ -183,6 +183,40 @@ class Conv2D_ReLU_Op(Conv2D_Op):
     fused_activation = "relu"
 
 
+class Conv2D_AddReLU_Op(Conv2D_Op):
+    """ReLU(Conv2D(+bias) + residual) with the residual add and the ReLU in the GEMM epilogue: the
+    same float32 operations, in the same order, as the separate Conv2D, Add and ReLU nodes. Formed
+    by the inference graph rewrite (``fusion.fuse_conv_add_relu``) for graphs that take no gradient,
+    so it has no backward. Parents: x, kernel, [bias], residual."""
+
+    fused_activation = "relu"
+
+    def __init__(self, x, kernel, residual, **kwargs):
+        super().__init__(x, kernel, **kwargs)
+        self.parents.append(residual)
+        if self not in residual.children:
+            residual.children.append(self)
+
+    def forward(self, x_val, kernel_val, *rest):
+        bias_val, residual_val = (rest[0], rest[1]) if self.bias is not None else (None, rest[0])
+        self.actual_backend = _resolve_backend(self.backend, x_val, kernel_val, bias_val, residual_val)
+        self._orders.pop("backward", None)
+        order = self._order_for("forward", kernel_val)
+        extra = {"weight_order": order} if order is not None else {}
+        self.value, _ = native.conv2d_forward(
+            x_val, kernel_val, bias_val, stride=self.stride, padding=self.padding, activation="relu",
+            engine=NATIVE_BACKENDS[self.actual_backend], algorithm="implicit", residual=residual_val, **extra)
+        self._activation_fused = True
+        self._saved = None
+
+    def weight_orders(self, phase):
+        return super().weight_orders(phase) if phase == "forward" else []
+
+    def backward(self):
+        raise RuntimeError("Conv2D_AddReLU_Op is an inference fusion and has no backward; build the graph "
+                           "without apply_graph_optimizations(mode='inference') to train it")
+
+
 class Conv2D_LeakyReLU_Op(Conv2D_Op):
     """Conv2D(+bias) then LeakyReLU. Fused only for alpha > 0 (then y > 0 exactly where the
     pre-activation is > 0, so the output alone can gate the backward); otherwise applied after."""

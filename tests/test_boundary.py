@@ -213,6 +213,24 @@ def test_graph_rewrites_on_cpu():
         graph = mf.Graph(out, optimize=True)
         names = sorted(g.name for g in graph._bn_groups.values())
         assert names == ["BatchNormAddReLU", "BatchNormReLU"]
+
+        # Inference: both BNs and the shortcut's fold, then ReLU(conv2 + shortcut) becomes one node
+        # whose last parent is the shortcut; a second optimising Graph fuses conv1's ReLU.
+        block = mf.BasicBlock(4, 8, stride=2, conv_backend="hip_native")
+        for bn in (block.bn1, block.bn2, block.downsample_bn):
+            bn.eval()
+        out = block(mf.Variable(torch.zeros((1, 4, 8, 8)), requires_grad=False))
+        root, stats = mf.apply_graph_optimizations(out, mode="inference", fold_constants=False)
+        assert stats["bn_folds"] == 3 and stats["conv_add_act_fusions"] == 1
+        assert type(root) is mf.Conv2D_AddReLU_Op and len(root.parents) == 4
+        residual = root.parents[3]
+        assert type(residual) is mf.Conv2D_Op and residual.children == [root] and residual.stride == (2, 2)
+        graph = mf.Graph(root, optimize=True)
+        assert graph._opt_stats["conv_act_fusions"] == 1
+        assert sorted(type(n).__name__ for n in graph.nodes if isinstance(n, mf.Conv2D_Op)) == [
+            "Conv2D_AddReLU_Op", "Conv2D_Op", "Conv2D_ReLU_Op"]
+        with pytest.raises(RuntimeError, match="no backward"):
+            root.backward()
     finally:
         if torch.cuda.is_available():
             mf.set_device("cuda")

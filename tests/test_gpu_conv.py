@@ -468,7 +468,7 @@ def test_every_implicit_tile_is_exact_on_integer_data(case):
         for slices in (1, 3, 24):
             code = native.PLAN_BASE + tile * native.PLAN_SLICES + slices - 1
             native._raise_for(lib.mfh_conv_forward_implicit(
-                xg.data_ptr(), wg.data_ptr(), order.data_ptr(), 1, 0, y.data_ptr(), *g.c_args(), 0, 0.0, code,
+                xg.data_ptr(), wg.data_ptr(), order.data_ptr(), 1, 0, 0, y.data_ptr(), *g.c_args(), 0, 0.0, code,
                 workspace.data_ptr(), workspace.numel(), stream), lib)
             native._raise_for(lib.mfh_conv_backward_implicit(
                 xg.data_ptr(), wg.data_ptr(), dyg.data_ptr(), 0, 0, 0, dx.data_ptr(), flip.data_ptr(), 0, 0, 0,

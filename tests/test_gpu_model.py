@@ -208,7 +208,7 @@ def test_resnet18_inference_with_bn_folding_and_conv_relu_epilogue():
     x_np, t_np = oracle_resnet.synthetic_batch(batch, size, size, seed=0)
     out = model(mf.Variable(gpu(x_np), requires_grad=False))
     root, stats = mf.apply_graph_optimizations(out, mode="inference", fold_constants=False)
-    assert stats["bn_folds"] == 20
+    assert stats["bn_folds"] == 20 and stats["conv_add_act_fusions"] == 8  # conv2 + shortcut + ReLU
     graph = mf.Graph(root, optimize=True)
     assert graph._opt_stats["conv_act_fusions"] == 9  # stem + conv1 of each block
     graph.forward()
@@ -219,6 +219,34 @@ def test_resnet18_inference_with_bn_folding_and_conv_relu_epilogue():
     _, _, out32 = oracle_resnet.forward_backward(params32, {k: (m.copy(), v.copy()) for k, (m, v) in running32.items()},
                                                  x_np, t_np, training=False)
     assert normwise(got, out64) <= max(4 * normwise(out32, out64), 1e-5)
+
+
+def test_conv_add_relu_epilogue_equals_separate_add_and_relu_bit_for_bit():
+    """The inference graph with ReLU(conv2 + shortcut) in the GEMM epilogue against the same folded
+    graph with Add and ReLU as separate nodes: one float32 addition and one ReLU per element in both,
+    so the outputs agree bit for bit (ResNet18 at base width 16, all four stages)."""
+    outputs = []
+    for fuse in (True, False):
+        model = mf.ResNet18(output_dim=2, base_width=16, initializer=mf.make_initializer(seed=3),
+                            conv_backend="hip_native")
+        rng = np.random.default_rng(9)
+        for bn in [model.stem_bn] + [bn for block in model.blocks() for bn in
+                                     (block.bn1, block.bn2, *((block.downsample_bn,) if block.downsample else ()))]:
+            bn.running_mean.copy_(gpu(rng.normal(0, 0.1, bn.num_features).astype(np.float32)))
+            bn.running_var.copy_(gpu(rng.uniform(0.5, 1.5, bn.num_features).astype(np.float32)))
+        model.eval()
+        x = mf.Variable(gpu(np.random.default_rng(1).standard_normal((3, 3, 48, 40)).astype(np.float32)),
+                        requires_grad=False)
+        root, stats = mf.apply_graph_optimizations(model(x), mode="inference", fold_constants=False,
+                                                   fuse_activations=fuse)
+        assert stats["conv_add_act_fusions"] == (8 if fuse else 0)
+        graph = mf.Graph(root, optimize=True)
+        adds = [n for n in graph.nodes if isinstance(n, mf.Conv2D_AddReLU_Op)]
+        assert len(adds) == (8 if fuse else 0)
+        graph.forward()
+        graph.forward()  # a second pass reads the kernel orders batched by the Graph
+        outputs.append(host(graph.target_node.value))
+    assert np.array_equal(outputs[0], outputs[1])
 
 
 def test_batched_kernel_orders_and_in_place_dx_reproduce_the_per_call_path(monkeypatch):
