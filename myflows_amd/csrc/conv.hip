@@ -325,6 +325,8 @@ __global__ __launch_bounds__(256) void im2col_row_kernel(const float* __restrict
     }
 }
 
+constexpr int STAGE_AHEAD = 4;  // global loads per thread in flight while planes are staged in LDS
+
 // Max-pool forward over `per` consecutive (n, c) planes per workgroup, each staged whole in LDS with
 // coalesced reads; the window rule is pool_forward_kernel's.
 __global__ __launch_bounds__(256) void pool_forward_plane_kernel(const float* __restrict__ x, float* __restrict__ y,
@@ -337,11 +339,31 @@ __global__ __launch_bounds__(256) void pool_forward_plane_kernel(const float* __
     const int hw = H * W, ohw = OH * OW;
     const long long base = static_cast<long long>(first_plane) * hw;
     const int elems = count * hw;
+    // The copy keeps STAGE_AHEAD loads per thread in flight: at most three 49 KB planes fit a CU's
+    // LDS, too few waves to cover HBM latency one load at a time.
     if (vec) {  // x is 16-byte aligned and H*W % 4 == 0: every plane starts aligned, copy in float4s
         const float4* src = reinterpret_cast<const float4*>(x + base);
-        for (int q = threadIdx.x; q < elems / 4; q += 256) reinterpret_cast<float4*>(tile)[q] = src[q];
+        float4* dst = reinterpret_cast<float4*>(tile);
+        const int quads = elems / 4;
+        int q = threadIdx.x;
+        for (; q + (STAGE_AHEAD - 1) * 256 < quads; q += STAGE_AHEAD * 256) {
+            float4 v[STAGE_AHEAD];
+#pragma unroll
+            for (int u = 0; u < STAGE_AHEAD; ++u) v[u] = src[q + u * 256];
+#pragma unroll
+            for (int u = 0; u < STAGE_AHEAD; ++u) dst[q + u * 256] = v[u];
+        }
+        for (; q < quads; q += 256) dst[q] = src[q];
     } else {
-        for (int e = threadIdx.x; e < elems; e += 256) tile[e] = x[base + e];
+        int e = threadIdx.x;
+        for (; e + (STAGE_AHEAD - 1) * 256 < elems; e += STAGE_AHEAD * 256) {
+            float v[STAGE_AHEAD];
+#pragma unroll
+            for (int u = 0; u < STAGE_AHEAD; ++u) v[u] = x[base + e + u * 256];
+#pragma unroll
+            for (int u = 0; u < STAGE_AHEAD; ++u) tile[e + u * 256] = v[u];
+        }
+        for (; e < elems; e += 256) tile[e] = x[base + e];
     }
     __syncthreads();
     for (int o = threadIdx.x; o < count * ohw; o += 256) {
@@ -402,7 +424,23 @@ __global__ __launch_bounds__(256) void pool_backward_plane_kernel(const float* _
     float* grad = staged;
     int* where = reinterpret_cast<int*>(staged + per * ohw);
     const long long out_base = static_cast<long long>(first_plane) * ohw;
-    for (int o = threadIdx.x; o < count * ohw; o += 256) {
+    const int staged_count = count * ohw;
+    int o = threadIdx.x;
+    for (; o + (STAGE_AHEAD - 1) * 256 < staged_count; o += STAGE_AHEAD * 256) {
+        float g[STAGE_AHEAD];
+        int a[STAGE_AHEAD];
+#pragma unroll
+        for (int u = 0; u < STAGE_AHEAD; ++u) {
+            g[u] = dy[out_base + o + u * 256];
+            a[u] = argmax[out_base + o + u * 256];
+        }
+#pragma unroll
+        for (int u = 0; u < STAGE_AHEAD; ++u) {
+            grad[o + u * 256] = g[u];
+            where[o + u * 256] = a[u];
+        }
+    }
+    for (; o < staged_count; o += 256) {
         grad[o] = dy[out_base + o];
         where[o] = argmax[out_base + o];
     }
