@@ -99,7 +99,8 @@ MFH_API int mfh_conv_backward(uint64_t weight, uint64_t dy, uint64_t y, uint64_t
  * it split K (0 is allowed: no split). engine: 1 (automatic plan) or 16 + tile * 128 + slices - 1
  * over the 12 tiles of the implicit products. residual (may be 0): an NCHW tensor of y's shape added
  * to conv + bias before the activation, each addition rounded to float32 as separate operations
- * would be (the fused Conv + Add + ReLU of an inference graph). Arguments otherwise as
+ * would be (the fused Conv + Add + ReLU of an inference graph); it must not overlap y (the call
+ * rejects residual == y). Arguments otherwise as
  * mfh_conv_forward.
  * Has no single counterpart in the reference: it replaces the im2col + gemm_rows + epilogue sequence
  * of mf_conv_forward, native_cublas.cpp:1441-1461, when the caller does not keep cols. */

@@ -323,6 +323,7 @@ MFH_API int mfh_conv_forward_implicit(std::uint64_t x, std::uint64_t weight, std
     MFH_REQUIRE(wt || !implicit_chunked(CI), "the implicit forward needs the reordered-kernel buffer wt");
     MFH_REQUIRE(prepared == 0 || prepared == 1, "prepared must be 0 or 1");
     MFH_REQUIRE(workspace_floats >= 0, "workspace size must be non-negative");
+    MFH_REQUIRE(residual != y || residual == 0, "the residual must not be the output buffer");
     return conv_implicit_forward(g, as_ptr<const float>(x), as_ptr<const float>(weight), as_ptr<float>(wt),
                                  prepared == 1, as_ptr<const float>(bias), as_ptr<const float>(residual),
                                  as_ptr<float>(y), activation, alpha, engine, as_ptr<float>(workspace),

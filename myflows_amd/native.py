@@ -472,6 +472,8 @@ def conv2d_forward(x, weight, bias=None, *, stride=(1, 1), padding=(0, 0), activ
         residual = _device_f32(residual, "residual")
         if tuple(residual.shape) != g.out_shape:
             raise ValueError("residual must have the convolution's output shape")
+        if residual.device != device:
+            raise ValueError("residual must be on x's device")
     if algorithm == "implicit":
         workspace, floats = _implicit_workspace(g, "forward")
         prepared = 0

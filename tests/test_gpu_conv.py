@@ -485,3 +485,39 @@ def test_every_implicit_tile_is_exact_on_integer_data(case):
             native._raise_for(status, lib)
             np.testing.assert_array_equal(host(dw), ref_dw, err_msg=f"dW tile {tile} slices {slices}")
             np.testing.assert_array_equal(host(db), ref_db, err_msg=f"db tile {tile} slices {slices}")
+
+
+@pytest.mark.parametrize("shape,kernel,stride,padding", [
+    ((2, 64, 9, 11), (64, 64, 3, 3), 1, 1),     # chunked features, unsplit
+    ((3, 3, 20, 18), (16, 3, 7, 7), 2, 3),      # natural-order stem-like gather
+    ((4, 512, 4, 5), (512, 512, 3, 3), 1, 1),   # layer4-like: split K, residual in the slice reduction
+])
+def test_residual_epilogue_equals_separate_add_and_relu(shape, kernel, stride, padding):
+    """act((conv + bias) + residual) from the epilogue against the same convolution without the
+    residual, then a float32 add and ReLU: bit for bit, split and unsplit plans alike."""
+    rng = np.random.default_rng(11)
+    stride, padding = (stride, stride), (padding, padding)
+    x = gpu(rng.standard_normal(shape).astype(np.float32))
+    w = gpu((rng.standard_normal(kernel) * (2.0 / np.prod(kernel[1:])) ** 0.5).astype(np.float32))
+    b = gpu(rng.standard_normal(kernel[0]).astype(np.float32))
+    plain, _ = native.conv2d_forward(x, w, b, stride=stride, padding=padding, algorithm="implicit")
+    residual = gpu(rng.standard_normal(tuple(plain.shape)).astype(np.float32))
+    fused, _ = native.conv2d_forward(x, w, b, stride=stride, padding=padding, activation="relu",
+                                     algorithm="implicit", residual=residual)
+    torch.cuda.synchronize()
+    assert torch.equal(fused, torch.relu(plain + residual))
+    with pytest.raises(ValueError, match="output shape"):
+        native.conv2d_forward(x, w, b, stride=stride, padding=padding, algorithm="implicit", residual=residual[:1])
+    with pytest.raises(ValueError, match="implicit"):
+        native.conv2d_forward(x, w, b, stride=stride, padding=padding, algorithm="im2col", residual=residual)
+
+
+def test_residual_may_not_be_the_output():
+    x = gpu(np.ones((1, 4, 6, 6), np.float32))
+    w = gpu(np.ones((4, 4, 3, 3), np.float32))
+    y = torch.zeros((1, 4, 6, 6), device="cuda")
+    lib = native._library()
+    dims = (1, 4, 6, 6, 4, 3, 3, 6, 6, 1, 1, 1, 1)
+    status = lib.mfh_conv_forward_implicit(x.data_ptr(), w.data_ptr(), 0, 0, 0, y.data_ptr(), y.data_ptr(), *dims,
+                                           1, 0.0, 1, 0, 0, torch.cuda.current_stream().cuda_stream)
+    assert status != 0 and "residual" in lib.mfh_last_error().decode()
