@@ -231,6 +231,23 @@ def test_graph_rewrites_on_cpu():
             "Conv2D_AddReLU_Op", "Conv2D_Op", "Conv2D_ReLU_Op"]
         with pytest.raises(RuntimeError, match="no backward"):
             root.backward()
+
+        # No rewrite when the convolution or the sum has another reader, or the activation is not ReLU.
+        x = mf.Variable(torch.zeros((1, 3, 8, 8)), requires_grad=False)
+        shortcut = mf.Variable(torch.zeros((1, 4, 8, 8)), requires_grad=False)
+        conv = mf.Conv2D(3, 4, 3, padding=1, fuse_activation=False, initializer=mf.make_initializer(seed=2),
+                         backend="hip_native")
+        c = conv(x)
+        total = mf.Add(mf.ReLU(mf.Add(c, shortcut)), c)  # c read twice
+        _, stats = mf.fusion.fuse_conv_add_relu(total)
+        assert stats == 0
+        s = mf.Add(conv(x), shortcut)
+        root, stats = mf.fusion.fuse_conv_add_relu(mf.Add(mf.ReLU(s), s))  # the sum read twice
+        assert stats == 0
+        root, stats = mf.fusion.fuse_conv_add_relu(mf.LeakyReLU(mf.Add(conv(x), shortcut), alpha=0.1))
+        assert stats == 0 and type(root) is mf.LeakyReLU
+        root, stats = mf.fusion.fuse_conv_add_relu(mf.ReLU(mf.Add(shortcut, conv(x))))  # either operand order
+        assert stats == 1 and type(root) is mf.Conv2D_AddReLU_Op and root.parents[-1] is shortcut
     finally:
         if torch.cuda.is_available():
             mf.set_device("cuda")
