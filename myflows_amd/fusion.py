@@ -181,7 +181,8 @@ def fuse_conv_add_relu(root):
         bias = conv.parents[2] if len(conv.parents) == 3 else None
         replacement = Conv2D_AddReLU_Op(conv.parents[0], conv.parents[1], residual, stride=conv.stride,
                                         padding=conv.padding, bias=bias, backend=conv.backend,
-                                        recompute_im2col=conv.recompute_im2col)
+                                        recompute_im2col=conv.recompute_im2col,
+                                        residual_first=add.parents[0] is residual)
         if node is root:
             root = replacement
         replace_node(node, replacement)

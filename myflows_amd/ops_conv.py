@@ -15,6 +15,7 @@ import os
 import torch
 
 from . import native
+from .device import get_device
 from .graph import GradientOp
 
 NATIVE_BACKENDS = {"hip_native": "mfma", "cuda_native_register": "mfma"}
@@ -28,9 +29,11 @@ def _backend_name(backend):
 
 
 def _resolve_backend(backend, *arrays):
-    """The backend that runs now (``auto`` -> hip_native), after checking that every array is a GPU
-    tensor on the current device."""
+    """The backend that runs now (``auto`` -> hip_native), after checking that the active device is
+    the GPU (``set_device``) and that every array is a GPU tensor on the current device."""
     chosen = "hip_native" if backend == "auto" else backend
+    if get_device() != "cuda":
+        raise ValueError(f"backend={chosen} is incompatible with device={get_device()}")
     current = torch.cuda.current_device() if torch.cuda.is_available() else None
     for value in arrays:
         if value is None:
@@ -187,18 +190,52 @@ class Conv2D_AddReLU_Op(Conv2D_Op):
     """ReLU(Conv2D(+bias) + residual) with the residual add and the ReLU in the GEMM epilogue: the
     same float32 operations, in the same order, as the separate Conv2D, Add and ReLU nodes. Formed
     by the inference graph rewrite (``fusion.fuse_conv_add_relu``) for graphs that take no gradient,
-    so it has no backward. Parents: x, kernel, [bias], residual."""
+    so it has no backward. Parents: x, kernel, [bias], residual. ``residual_first`` records that the
+    replaced Add took the residual as its first operand.
+
+    The epilogue reads a residual laid out as the output. Any other residual value (one that the Add
+    would broadcast, such as a per-channel vector, or promote, such as float64, or one on another
+    device) takes the separate operations instead: the convolution, the Add's broadcast sum in its
+    operand order, then the ReLU operator, with the results and errors the unfused nodes give."""
 
     fused_activation = "relu"
 
-    def __init__(self, x, kernel, residual, **kwargs):
+    def __init__(self, x, kernel, residual, *, residual_first=False, **kwargs):
         super().__init__(x, kernel, **kwargs)
+        self.residual_first = bool(residual_first)
         self.parents.append(residual)
         if self not in residual.children:
             residual.children.append(self)
 
+    def _unfused(self, x_val, kernel_val, bias_val, residual_val):
+        from . import fused
+        from .ops_basic import _gpu_only
+
+        self.actual_backend = _resolve_backend(self.backend, x_val, kernel_val, bias_val)
+        self._orders.pop("backward", None)
+        order = self._order_for("forward", kernel_val)
+        extra = {"weight_order": order} if order is not None else {}
+        conv, _ = native.conv2d_forward(x_val, kernel_val, bias_val, stride=self.stride, padding=self.padding,
+                                        engine=NATIVE_BACKENDS[self.actual_backend], **extra)
+        a, b = (residual_val, conv) if self.residual_first else (conv, residual_val)
+        if a.ndim == 4 and b.ndim == 1:  # Add's per-channel bias form
+            b = b.reshape(1, -1, 1, 1)
+        total = a + b
+        _gpu_only(total, "ReLU")
+        self.value = fused.relu_forward(total)
+        self._activation_fused = False
+        self._saved = None
+
     def forward(self, x_val, kernel_val, *rest):
         bias_val, residual_val = (rest[0], rest[1]) if self.bias is not None else (None, rest[0])
+        fits = (isinstance(residual_val, torch.Tensor) and isinstance(x_val, torch.Tensor)
+                and residual_val.dtype == torch.float32 and residual_val.device == x_val.device
+                and kernel_val.ndim == 4 and x_val.ndim == 4
+                and tuple(residual_val.shape) == native.ConvGeometry.of(
+                    tuple(x_val.shape), tuple(kernel_val.shape), self.stride, self.padding).out_shape)
+        if not fits:
+            self._unfused(x_val, kernel_val, bias_val, residual_val)
+            return
         self.actual_backend = _resolve_backend(self.backend, x_val, kernel_val, bias_val, residual_val)
         self._orders.pop("backward", None)
         order = self._order_for("forward", kernel_val)

@@ -51,57 +51,77 @@ class BatchNorm2d_Op(GradientOp):
 
 
 class BatchNormActivation:
-    """One execution unit for ReLU(BN(x) [+ residual]) that keeps the logical BN / Add / ReLU nodes
-    addressable: the forward writes only the ReLU node's value, the backward gates by it and hands
-    the gated gradient to the residual branch. A residual that needs broadcasting runs unfused."""
+    """The chain BN -> [Add(BN, residual)] -> ReLU of a Graph run as one execution unit.
+
+    Contract with the executor (``graph.Graph``): the unit takes the place of the chain's last node,
+    ``output`` (the ReLU), in the forward and backward orders; the executor skips the chain's other
+    nodes (``hidden``), hands ``forward`` the values of ``parents`` (x, gamma, beta and, with an Add,
+    the residual) and calls ``backward`` once ``output.grad`` is set. Afterwards ``output`` and the
+    parents hold what the separate nodes would have given them.
+
+    Route of a pass, chosen per forward:
+      * fused: one libmfhip pass for BN, the residual add and the ReLU (the hidden nodes' values are
+        never formed and are left empty), and one backward pass that gates dy by the output and
+        writes the residual's gradient beside the BN gradients;
+      * chained: a residual that the Add would broadcast or promote (another shape or dtype) runs
+        the chain's own nodes one after the other, forward and backward.
+    """
 
     def __init__(self, bn, add, output, residual):
         self.bn, self.add, self.output, self.residual = bn, add, output, residual
-        self.hidden = (bn,) if add is None else (bn, add)
-        self.parents = list(bn.parents) + ([residual] if residual is not None else [])
+        self.chain = (bn, output) if add is None else (bn, add, output)
+        self.hidden = self.chain[:-1]
+        self.parents = list(bn.parents) + ([] if residual is None else [residual])
         self.name = "BatchNormReLU" if add is None else "BatchNormAddReLU"
-        self._unfused = False
+        self.chained = False  # the route of the last forward
+        self._stats = None    # (mean, inv_std, training) of the last fused forward, when BN needs gradients
+
+    @staticmethod
+    def _fusable(x, residual):
+        return residual is None or (tuple(residual.shape) == tuple(x.shape) and residual.dtype == x.dtype)
 
     def forward(self, x, gamma, beta, residual=None):
-        bn = self.bn
-        if tuple(gamma.shape) != (x.shape[1],) or beta.shape != gamma.shape:
+        if tuple(gamma.shape) != (x.shape[1],) or tuple(beta.shape) != tuple(gamma.shape):
             raise ValueError("gamma/beta shape must be (C,)")
-        self._unfused = residual is not None and (residual.shape != x.shape or residual.dtype != x.dtype)
-        if self._unfused:
-            bn.forward(x, gamma, beta)
-            self.add.forward(*(p.value for p in self.add.parents))
-            self.output.forward(self.add.value)
+        self.chained = not self._fusable(x, residual)
+        if self.chained:
+            for node in self.chain:
+                node.forward(*(parent.value for parent in node.parents))
             return
-        self.training = bn.training
-        self.output.value, mean, inv_std = fused.batchnorm2d_forward(
-            x, gamma, beta, bn.running_mean, bn.running_var, momentum=bn.momentum, eps=bn.eps,
-            training=self.training, unbiased_running_var=bn.unbiased_running_var, relu=True, residual=residual)
+        bn = self.bn
+        y, mean, inv_std = fused.batchnorm2d_forward(
+            x, gamma, beta, bn.running_mean, bn.running_var, momentum=bn.momentum, eps=bn.eps, training=bn.training,
+            unbiased_running_var=bn.unbiased_running_var, relu=True, residual=residual)
+        self.output.value = y
         for node in self.hidden:
             node.value = None
-        self._stats = (mean, inv_std) if bn.requires_grad else None
+        self._stats = (mean, inv_std, bn.training) if bn.requires_grad else None
 
     def backward(self):
-        bn = self.bn
-        if self._unfused:
-            self.output.backward()
-            self.add.backward()
-            if bn.requires_grad:
-                bn.backward()
+        if self.chained:
+            for node in reversed(self.chain):
+                if node.requires_grad and node.grad is not None:
+                    node.backward()
             for node in self.hidden:
                 node.grad = None
             return
-        buffers = [p.grad_buffer() if p.requires_grad else (None, False) for p in self.parents]
-        residual_grad, add_residual = buffers[3] if self.residual is not None else (None, False)
-        if self._stats is None:  # only the residual branch needs a gradient
-            if residual_grad is not None:
-                gated = torch.where(self.output.value > 0, self.output.grad, torch.zeros_like(self.output.grad))
-                residual_grad.add_(gated) if add_residual else residual_grad.copy_(gated)
+        dy, gate = self.output.grad, self.output.value
+        wants_residual = self.residual is not None and self.residual.requires_grad
+        if self._stats is None:
+            # BN needs no gradient: the residual's is dy where the ReLU passed its input.
+            if wants_residual:
+                self.residual.accumulate_grad(torch.where(gate > 0, dy, torch.zeros_like(dy)), owned=True)
             return
+        mean, inv_std, training = self._stats
+        x_node, gamma_node, beta_node = self.bn.parents
+        target = {role: node.grad_buffer() if node.requires_grad else (None, False)
+                  for role, node in zip(("x", "gamma", "beta"), (x_node, gamma_node, beta_node))}
+        residual_grad, add_residual = self.residual.grad_buffer() if wants_residual else (None, False)
         fused.batchnorm2d_backward(
-            bn.parents[0].value, self.output.grad, bn.parents[1].value, *self._stats, training=self.training,
-            x_grad=buffers[0][0], gamma_grad=buffers[1][0], beta_grad=buffers[2][0],
-            accumulate=tuple(add for _, add in buffers[:3]), gate=self.output.value, residual_grad=residual_grad,
-            add_residual=add_residual)
+            x_node.value, dy, gamma_node.value, mean, inv_std, training=training, x_grad=target["x"][0],
+            gamma_grad=target["gamma"][0], beta_grad=target["beta"][0],
+            accumulate=(target["x"][1], target["gamma"][1], target["beta"][1]), gate=gate,
+            residual_grad=residual_grad, add_residual=add_residual)
 
 
 class GlobalAvgPool2d_Op(GradientOp):

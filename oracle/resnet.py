@@ -88,9 +88,10 @@ class _Tape:
             self.grads[name] = np.array(value, dtype=self.dtype, copy=True)
 
 
-def forward_backward(params, running, x, target, training=True, need_input_grad=False):
+def forward_backward(params, running, x, target, training=True, need_input_grad=False, backward=True):
     """One forward + backward pass in the dtype of x (float32 is the reference path; float64 gives
-    the high-precision comparison point). Returns (loss, grads by parameter name, output)."""
+    the high-precision comparison point). Returns (loss, grads by parameter name, output); with
+    backward=False the pass stops after the loss (grads empty)."""
     dtype = x.dtype
     tape = _Tape(dtype)
     acts = {}
@@ -134,6 +135,8 @@ def forward_backward(params, running, x, target, training=True, need_input_grad=
     tape.ops.append(("gap", "gap", h))
     acts["fc"] = rp.linear_forward(acts["gap"], params["fc.W"], params["fc.b"])
     loss = rp.mse_forward(acts["fc"], target)
+    if not backward:
+        return loss, {}, acts["fc"]
 
     grad = {"fc": rp.mse_backward(acts["fc"], target, dtype.type(1.0)).astype(dtype)}
 

@@ -248,6 +248,9 @@ def test_graph_rewrites_on_cpu():
         assert stats == 0 and type(root) is mf.LeakyReLU
         root, stats = mf.fusion.fuse_conv_add_relu(mf.ReLU(mf.Add(shortcut, conv(x))))  # either operand order
         assert stats == 1 and type(root) is mf.Conv2D_AddReLU_Op and root.parents[-1] is shortcut
+        assert root.residual_first  # the node keeps the Add's operand order for its unfused fallback
+        root, stats = mf.fusion.fuse_conv_add_relu(mf.ReLU(mf.Add(conv(x), shortcut)))
+        assert stats == 1 and not root.residual_first
     finally:
         if torch.cuda.is_available():
             mf.set_device("cuda")

@@ -506,6 +506,24 @@ def test_residual_epilogue_equals_separate_add_and_relu(shape, kernel, stride, p
                                      algorithm="implicit", residual=residual)
     torch.cuda.synchronize()
     assert torch.equal(fused, torch.relu(plain + residual))
+    # The same through explicit plan codes (64 x 64 tile of four 32 x 32 waves), unsplit and split
+    # three ways, so that the residual is read both by the product's epilogue and by the split-K
+    # reduction that finishes the split plan.
+    g = native.ConvGeometry.of(shape, kernel, stride, padding)
+    lib, stream = native._library(), torch.cuda.current_stream().cuda_stream
+    wt = torch.empty_like(w)
+    workspace = torch.empty(3 * g.co * g.m, device="cuda")
+    for slices in (1, 3):
+        code = native.PLAN_BASE + 6 * native.PLAN_SLICES + slices - 1
+        outputs = []
+        for extra, act in ((0, 0), (residual.data_ptr(), 1)):
+            out = torch.full(g.out_shape, float("nan"), device="cuda")
+            native._raise_for(lib.mfh_conv_forward_implicit(
+                x.data_ptr(), w.data_ptr(), wt.data_ptr(), 0, b.data_ptr(), extra, out.data_ptr(), *g.c_args(), act,
+                0.0, code, workspace.data_ptr(), workspace.numel(), stream), lib)
+            outputs.append(out)
+        torch.cuda.synchronize()
+        assert torch.equal(outputs[1], torch.relu(outputs[0] + residual)), f"slices {slices}"
     with pytest.raises(ValueError, match="output shape"):
         native.conv2d_forward(x, w, b, stride=stride, padding=padding, algorithm="implicit", residual=residual[:1])
     with pytest.raises(ValueError, match="implicit"):
@@ -521,3 +539,69 @@ def test_residual_may_not_be_the_output():
     status = lib.mfh_conv_forward_implicit(x.data_ptr(), w.data_ptr(), 0, 0, 0, y.data_ptr(), y.data_ptr(), *dims,
                                            1, 0.0, 1, 0, 0, torch.cuda.current_stream().cuda_stream)
     assert status != 0 and "residual" in lib.mfh_last_error().decode()
+
+
+# Convolutions whose implicit products hit every entry of the measured-plan table of the implicit
+# products (csrc/implicit.hip, MEASURED_PLANS: key orientation, M, N, K): ResNet18's batch-64
+# convolutions at 3 x 120 x 160 (forward, dW, and the stride-1 dX, which shares its forward's key) and
+# its batch-256 224 x 224 inference forwards. Passes that have no measured entry run their automatic
+# plans and are checked too.
+PLAN_GEOMETRIES = (
+    ("bs64-stem", (64, 3, 120, 160), (64, 3, 7, 7), 2, 3, ("forward", "dw")),
+    ("bs64-layer1", (64, 64, 29, 39), (64, 64, 3, 3), 1, 1, ("forward", "dx", "dw")),
+    ("bs64-layer2.0-conv1", (64, 64, 29, 39), (128, 64, 3, 3), 2, 1, ("forward", "dx", "dw")),
+    ("bs64-layer2-3x3", (64, 128, 15, 20), (128, 128, 3, 3), 1, 1, ("forward", "dx", "dw")),
+    ("bs64-layer2-1x1", (64, 64, 29, 39), (128, 64, 1, 1), 2, 0, ("forward", "dx", "dw")),
+    ("bs64-layer3.0-conv1", (64, 128, 15, 20), (256, 128, 3, 3), 2, 1, ("forward", "dx", "dw")),
+    ("bs64-layer3-3x3", (64, 256, 8, 10), (256, 256, 3, 3), 1, 1, ("forward", "dx", "dw")),
+    ("bs64-layer3-1x1", (64, 128, 15, 20), (256, 128, 1, 1), 2, 0, ("forward", "dx", "dw")),
+    ("bs64-layer4.0-conv1", (64, 256, 8, 10), (512, 256, 3, 3), 2, 1, ("forward", "dx", "dw")),
+    ("bs64-layer4-3x3", (64, 512, 4, 5), (512, 512, 3, 3), 1, 1, ("forward", "dx", "dw")),
+    ("bs256-stem", (256, 3, 224, 224), (64, 3, 7, 7), 2, 3, ("forward",)),
+    ("bs256-layer1", (256, 64, 55, 55), (64, 64, 3, 3), 1, 1, ("forward",)),
+    ("bs256-layer2.0-conv1", (256, 64, 55, 55), (128, 64, 3, 3), 2, 1, ("forward",)),
+    ("bs256-layer2-3x3", (256, 128, 28, 28), (128, 128, 3, 3), 1, 1, ("forward",)),
+    ("bs256-layer2-1x1", (256, 64, 55, 55), (128, 64, 1, 1), 2, 0, ("forward",)),
+    ("bs256-layer3.0-conv1", (256, 128, 28, 28), (256, 128, 3, 3), 2, 1, ("forward",)),
+    ("bs256-layer3-3x3", (256, 256, 14, 14), (256, 256, 3, 3), 1, 1, ("forward",)),
+    ("bs256-layer3-1x1", (256, 128, 28, 28), (256, 128, 1, 1), 2, 0, ("forward",)),
+    ("bs256-layer4.0-conv1", (256, 256, 14, 14), (512, 256, 3, 3), 2, 1, ("forward",)),
+    ("bs256-layer4-3x3", (256, 512, 7, 7), (512, 512, 3, 3), 1, 1, ("forward",)),
+)
+
+
+@pytest.mark.parametrize("geometry", PLAN_GEOMETRIES, ids=lambda g: g[0])
+def test_measured_plans_are_exact_on_integer_data(geometry):
+    """Each convolution at its full size under the automatic plan (so the measured plan of its
+    shape, split-K and grouped reductions included) on integer data in [-2, 2], where every float32
+    partial sum is exact: the forward and dX of the first, middle and last image (an output image
+    depends on its own input image only) and dW and db over the whole batch equal the FP64
+    convolution bit for bit."""
+    name, x_shape, w_shape, stride, padding, passes = geometry
+    print("measured plan", name, passes, flush=True)
+    stride, padding = (stride, stride), (padding, padding)
+    rng = np.random.default_rng(29)
+    x = rng.integers(-2, 3, size=x_shape).astype(np.float32)
+    w = rng.integers(-2, 3, size=w_shape).astype(np.float32)
+    g = native.ConvGeometry.of(x_shape, w_shape, stride, padding)
+    picks = sorted({0, x_shape[0] // 2, x_shape[0] - 1})
+    x64, w64 = torch.from_numpy(x).double(), torch.from_numpy(w).double()
+    xg, wg = gpu(x), gpu(w)
+    y, _ = native.conv2d_forward(xg, wg, None, stride=stride, padding=padding, algorithm="implicit")
+    ref_y = torch.nn.functional.conv2d(x64[picks], w64, stride=stride, padding=padding).numpy()
+    np.testing.assert_array_equal(host(y[picks]), ref_y, err_msg=f"{name} forward")
+    del y
+    if "dx" not in passes and "dw" not in passes:
+        return
+    dy = rng.integers(-2, 3, size=g.out_shape).astype(np.float32)
+    dx, dw, db = native.conv2d_backward(xg, wg, gpu(dy), None, stride=stride, padding=padding, algorithm="implicit",
+                                        need_input_grad="dx" in passes, need_weight_grad="dw" in passes)
+    dy64 = torch.from_numpy(dy).double()
+    if "dx" in passes:
+        ref_dx = torch.nn.grad.conv2d_input((len(picks),) + tuple(x_shape[1:]), w64, dy64[picks], stride=stride,
+                                            padding=padding).numpy()
+        np.testing.assert_array_equal(host(dx[picks]), ref_dx, err_msg=f"{name} dX")
+    if "dw" in passes:
+        ref_dw = torch.nn.grad.conv2d_weight(x64, tuple(w_shape), dy64, stride=stride, padding=padding).numpy()
+        np.testing.assert_array_equal(host(dw), ref_dw, err_msg=f"{name} dW")
+    np.testing.assert_array_equal(host(db), dy64.sum(dim=(0, 2, 3)).numpy(), err_msg=f"{name} db")

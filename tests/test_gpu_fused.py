@@ -270,3 +270,116 @@ def test_adam_rejects_overlapping_tensors():
     with pytest.raises(ValueError):
         fused.adam_update_many([(p, p, p[:8], p[8:], 1e-3, 0.0, 1)], beta1=0.9, beta2=0.999, eps=1e-8,
                                grad_scale=1.0)
+
+
+# --- the reference's own edge cases (tests/test_fused_ops.py) --------------------------------------
+def _adam_history(grads, lr=1e-3):
+    """theta after each of the steps of mf.Adam fed `grads` one update at a time (acc_no = 1)."""
+    import myflows_amd as mf
+
+    node = mf.Variable(gpu(np.linspace(-1, 1, grads[0].size, dtype=np.float32).reshape(grads[0].shape)),
+                       trainable=True)
+
+    class OneParameter:
+        nodes = (node,)
+
+    opt = mf.Adam(OneParameter(), learning_rate=lr)
+    history = []
+    for g in grads:
+        opt.acc_gradient = {node: gpu(g)}
+        opt.acc_no = 1
+        opt._update()
+        history.append(host(node.value).copy())
+    return history
+
+
+def test_adam_follows_the_textbook_recurrence_over_four_steps():
+    """tests/test_fused_ops.py:162-177: four steps against the FP64 textbook Adam, within 4 eps32
+    (normwise), and the first step moves every coordinate by lr."""
+    rng = np.random.default_rng(3)
+    grads = [rng.standard_normal((5, 7)).astype(np.float32) for _ in range(4)]
+    history = _adam_history(grads)
+    start = np.linspace(-1, 1, 35, dtype=np.float32).reshape(5, 7)
+    theta, m, v = start.astype(np.float64), np.zeros((5, 7)), np.zeros((5, 7))
+    for t, g in enumerate(grads, 1):
+        g = g.astype(np.float64)
+        m = 0.9 * m + 0.1 * g
+        v = 0.999 * v + 0.001 * g * g
+        theta = theta - 1e-3 * (m / (1 - 0.9 ** t)) / (np.sqrt(v / (1 - 0.999 ** t)) + 1e-8)
+        assert_near(history[t - 1], theta, 4 * np.finfo(np.float32).eps, f"step {t}")
+    np.testing.assert_allclose(np.abs(history[0] - start), 1e-3, rtol=1e-3)
+
+
+def test_adam_averages_the_gradient_over_the_accumulation_count():
+    """tests/test_fused_ops.py:187-205: a gradient summed over acc_no = 2 steps gives exactly the
+    update of its average taken as one step."""
+    import myflows_amd as mf
+
+    node = mf.Variable(torch.zeros(3, device="cuda"), trainable=True)
+
+    class OneParameter:
+        nodes = (node,)
+
+    averaged, summed = mf.Adam(OneParameter(), learning_rate=0.1), mf.Adam(OneParameter(), learning_rate=0.1)
+    averaged.acc_gradient, averaged.acc_no = {node: gpu(np.array([2.0, -4.0, 6.0], np.float32))}, 2
+    averaged._update()
+    first = host(node.value).copy()
+    node.value = torch.zeros(3, device="cuda")
+    summed.acc_gradient, summed.acc_no = {node: gpu(np.array([1.0, -2.0, 3.0], np.float32))}, 1
+    summed._update()
+    np.testing.assert_array_equal(first, host(node.value))
+    assert np.all(first != 0)
+
+
+def _bn_fp64(x, dy, gamma, beta, eps, training, rm, rv):
+    x, dy, gamma, beta = (a.astype(np.float64) for a in (x, dy, gamma, beta))
+    axes = (0, 2, 3)
+    mean = x.mean(axis=axes) if training else rm.astype(np.float64)
+    var = x.var(axis=axes) if training else rv.astype(np.float64)
+    inv = 1.0 / np.sqrt(var + eps)
+    ch = lambda a: a.reshape(1, -1, 1, 1)
+    xhat = (x - ch(mean)) * ch(inv)
+    dbeta, dgamma = dy.sum(axis=axes), (dy * xhat).sum(axis=axes)
+    m = x.shape[0] * x.shape[2] * x.shape[3]
+    dx = ch(gamma * inv) * (dy - ch(dbeta / m) - xhat * ch(dgamma / m)) if training else dy * ch(gamma * inv)
+    return xhat * ch(gamma) + ch(beta), dx, dgamma, dbeta, mean, var
+
+
+@pytest.mark.parametrize("shape,offset,scale", [((4, 3, 5, 7), 0.0, 1.0), ((2, 40, 9, 11), 0.0, 1.0),
+                                                ((1, 2, 1, 1), 0.0, 1.0), ((8, 4, 6, 6), 1000.0, 0.01),
+                                                ((64, 64, 29, 39), 1000.0, 0.01)], ids=str)
+def test_batchnorm_operator_against_fp64_including_a_large_mean(shape, offset, scale):
+    """tests/test_fused_ops.py:51-101 on the operator: y within 8 eps32, dx 64, dgamma 4, dbeta 2
+    (normwise) of the FP64 batch norm, running statistics within 4 eps32, in training and eval mode;
+    with mean 1e3 and std 1e-2 a float32 one-pass variance would lose every digit (the last case is
+    the bs64 layer1 shape, which takes the two-launch path with several slices per channel)."""
+    import myflows_amd as mf
+
+    eps32 = np.finfo(np.float32).eps
+    rng = np.random.default_rng(1)
+    x = (offset + scale * rng.standard_normal(shape)).astype(np.float32)
+    dy = rng.standard_normal(shape).astype(np.float32)
+    c = shape[1]
+    gamma = rng.uniform(0.5, 1.5, c).astype(np.float32)
+    beta = rng.standard_normal(c).astype(np.float32)
+    for training in (True, False):
+        rm = (offset + 0.1 * rng.standard_normal(c)).astype(np.float32)
+        rv = rng.uniform(0.5, 2.0, c).astype(np.float32) * np.float32(scale ** 2)
+        running_mean, running_var = gpu(rm.copy()), gpu(rv.copy())
+        nodes = [mf.Variable(gpu(a), trainable=True) for a in (x, gamma, beta)]
+        op = mf.BatchNorm2d_Op(*nodes, running_mean, running_var, momentum=0.1, eps=1e-5, training=training)
+        op.forward(*(n.value for n in nodes))
+        op.grad = gpu(dy)
+        op.backward()
+        y, dx, dgamma, dbeta, mean, var = _bn_fp64(x, dy, gamma, beta, 1e-5, training, rm, rv)
+        label = f"training={training}"
+        assert op.value.dtype == torch.float32
+        assert_near(host(op.value), y, 8 * eps32, f"y {label}")
+        assert_near(host(nodes[0].grad), dx, 64 * eps32, f"dx {label}")
+        assert_near(host(nodes[1].grad), dgamma, 4 * eps32, f"dgamma {label}")
+        assert_near(host(nodes[2].grad), dbeta, 2 * eps32, f"dbeta {label}")
+        if training:
+            assert_near(host(running_mean), 0.9 * rm.astype(np.float64) + 0.1 * mean, 4 * eps32, "running_mean")
+            assert_near(host(running_var), 0.9 * rv.astype(np.float64) + 0.1 * var, 4 * eps32, "running_var")
+        else:
+            np.testing.assert_array_equal(host(running_mean), rm)

@@ -61,6 +61,25 @@ def test_engine_error_bound_and_determinism(shape, layout):
     assert_near(host(got), exact + bias, 1e-5 if k <= 4096 else 2e-5, "C")
 
 
+@pytest.mark.parametrize("size,layout", [(1024, "NN"), (2048, "NN"), (4096, "NN"), (4096, "NT"), (4096, "TN")],
+                         ids=lambda v: str(v))
+def test_config2_square_products_at_their_stated_sizes(size, layout):
+    """Config 2's square GEMMs at full size (the 4096^3 NN product is the roofline figure's, on the
+    256 x 128 tile), with config 2's inputs (A then B, N(0, 1), seed 0): every output within
+    gamma_K |A||B| of the FP64 product, 1e-5 of max|C| normwise, the same bits on a second launch."""
+    trans_a, trans_b = LAYOUTS[layout]
+    print("config 2 gemm", size, layout, native.gemm_plan(size, size, size), flush=True)
+    rng = np.random.default_rng(0)
+    a, b, exact, magnitude = operands(rng, size, size, size, trans_a, trans_b)
+    da, db = gpu(a), gpu(b)
+    got = native.gemm(da, db, trans_a=trans_a, trans_b=trans_b)
+    assert torch.equal(got, native.gemm(da, db, trans_a=trans_a, trans_b=trans_b))
+    result = host(got).astype(np.float64)
+    error = np.abs(result - exact)
+    assert np.all(error <= gamma_k(size) * magnitude + EPS32 * np.abs(exact) + 1e-30), f"max error {error.max():.3e}"
+    assert_near(result, exact, 1e-5, "C")
+
+
 def test_misaligned_operands_take_the_scalar_loads():
     rng = np.random.default_rng(4)
     for (m, n, k) in ((300, 260, 100), (67, 39, 45)):

@@ -1,0 +1,229 @@
+"""Graph-level behaviour of the hip_native backend on the GPU, after the reference's
+tests/test_cuda_graph_integration.py:
+
+* a graph re-run after its input's batch and spatial size change (:65-78), here also with an
+  optimising ResNet graph whose plans, kernel orders and workspaces were cached at the first size;
+* backward after the active device changed is refused with a ValueError (:80-88);
+* the fusion rewrites keep the explicit backend of the convolution they replace (:90-102);
+* 100 training steps of the reference's locked stage-1 CNN (examples/stage1_cnn.py:15-49) against the
+  NumPy float32 restatement of the same network and optimiser (:104-130). CrossEntropy is not on this
+  path, so the loss is the MSE against one-hot targets; the criteria are the reference's: gradients
+  and updated values of the first 3 steps within atol 1e-4 / rtol 1e-3, the final loss as well, and
+  every float tensor float32 throughout.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+import myflows_amd as mf
+from myflows_amd import native
+from oracle import naive, reference_path as rp
+from tests.fixtures import assert_near
+
+pytestmark = pytest.mark.gpu
+
+
+def gpu(a):
+    return torch.as_tensor(np.ascontiguousarray(a), device="cuda")
+
+
+def host(t):
+    torch.cuda.synchronize()
+    return t.detach().cpu().numpy()
+
+
+class SumAll(mf.Node):
+    """A plain Node (not a GradientOp): its backward adds into a parent gradient the executor zeroes."""
+
+    def forward(self, value):
+        self.value = value.sum()
+
+    def backward(self):
+        self.parents[0].grad += self.grad
+
+
+def test_graph_reruns_after_batch_and_spatial_size_changes():
+    """Conv 3x3 (pad 1) -> MaxPool 3x3 / 1 -> sum: the pool context follows the new shape and the
+    gradients match the FP64 loops at every size."""
+    x = mf.Variable(torch.ones((1, 1, 5, 7), device="cuda"))
+    w_np = np.random.default_rng(3).standard_normal((2, 1, 3, 3)).astype(np.float32)
+    w = mf.Variable(gpu(w_np), trainable=True)
+    conv = mf.Conv2D_Op(x, w, padding=1, backend="hip_native")
+    pool = mf.MaxPool2d_Op(conv, 3, 1, backend="hip_native")
+    graph = mf.Graph(SumAll(pool))
+    rng = np.random.default_rng(4)
+    for shape in ((1, 1, 5, 7), (3, 1, 8, 6), (2, 1, 4, 5)):
+        x_np = rng.standard_normal(shape).astype(np.float32)
+        x.value = gpu(x_np)
+        graph.forward()
+        graph.backward()
+        assert tuple(x.grad.shape) == shape
+        assert pool._context.input_shape == tuple(conv.value.shape)
+        assert tuple(pool.value.shape) == (shape[0], 2, shape[2] - 2, shape[3] - 2)
+        y64 = naive.conv_forward(x_np.astype(np.float64), w_np.astype(np.float64), (1, 1), (1, 1))
+        pooled, argmax = rp.maxpool2d_native_forward(host(conv.value), (3, 3), (1, 1))
+        np.testing.assert_array_equal(host(pool.value), pooled)
+        assert_near(host(conv.value), y64, 1e-5, f"y {shape}")
+        dy = rp.maxpool2d_native_backward(np.ones(pooled.shape, np.float32), argmax, y64.shape)
+        dx64, dw64 = naive.conv_backward(x_np.astype(np.float64), w_np.astype(np.float64), dy.astype(np.float64),
+                                         (1, 1), (1, 1))
+        assert_near(host(x.grad), dx64, 1e-5, f"dx {shape}")
+        assert_near(host(w.grad), dw64, 1e-5, f"dw {shape}")
+
+
+def _resnet_graph(x_np, t_np):
+    model = mf.ResNet18(output_dim=2, base_width=16, initializer=mf.make_initializer(seed=6),
+                        conv_backend="hip_native")
+    x = mf.Variable(gpu(x_np), requires_grad=False)
+    t = mf.Variable(gpu(t_np), requires_grad=False)
+    out = model(x)
+    return model, mf.Graph(mf.MSELoss(out, t), optimize=True), out, x, t
+
+
+def test_optimised_resnet_graph_follows_a_shape_change():
+    """An optimising ResNet graph (batched kernel orders, fused BN units, cached plans and
+    workspaces) run at 2 x 64 x 64, then re-run at 3 x 48 x 40 through the same nodes, gives
+    exactly what a graph built at the second shape gives."""
+    rng = np.random.default_rng(8)
+    first = (rng.standard_normal((2, 3, 64, 64)).astype(np.float32), rng.uniform(-1, 1, (2, 2)).astype(np.float32))
+    second = (rng.standard_normal((3, 3, 48, 40)).astype(np.float32), rng.uniform(-1, 1, (3, 2)).astype(np.float32))
+    model, graph, out, x, t = _resnet_graph(*first)
+    graph.forward()
+    graph.backward()
+    x.value, t.value = gpu(second[0]), gpu(second[1])
+    graph.forward()
+    graph.backward()
+    reused = [host(out.value)] + [host(p.grad) for p in model.params]
+    model2, graph2, out2, _, _ = _resnet_graph(*second)
+    graph2.forward()
+    graph2.backward()
+    fresh = [host(out2.value)] + [host(p.grad) for p in model2.params]
+    assert reused[0].shape == (3, 2)
+    for a, b in zip(reused, fresh):
+        np.testing.assert_array_equal(a, b)
+
+
+def test_backward_rejects_a_device_change():
+    x = mf.Variable(torch.ones((1, 1, 4, 4), device="cuda"))
+    w = mf.Variable(torch.ones((1, 1, 3, 3), device="cuda"))
+    op = mf.Conv2D_Op(x, w, backend="hip_native")
+    mf.Graph(op).forward()
+    op.grad = torch.ones_like(op.value)
+    try:
+        mf.set_device("cpu")
+        with pytest.raises(ValueError, match="device=cpu"):
+            op.backward()
+    finally:
+        mf.set_device("cuda")
+
+
+@pytest.mark.parametrize("optimize,fuse_layer,activation,backend", [
+    (False, True, mf.ReLU, "cuda_native_register"),
+    (True, False, mf.ReLU, "hip_native"),
+    (True, False, mf.LeakyReLU, "cuda_native_register"),
+])
+def test_fusion_keeps_the_explicit_backend(optimize, fuse_layer, activation, backend):
+    x = mf.Variable(torch.ones((1, 1, 4, 4), device="cuda"))
+    conv = mf.Conv2D(1, 2, backend=backend, activation=activation, fuse_activation=fuse_layer,
+                     initializer=mf.make_initializer(seed=1))
+    graph = mf.Graph(SumAll(conv(x)), optimize=optimize)
+    graph.forward()
+    graph.backward()
+    conv_nodes = [n for n in graph.nodes if isinstance(n, mf.Conv2D_Op)]
+    assert len(conv_nodes) == 1
+    assert conv_nodes[0].actual_backend == backend
+    fused = fuse_layer or optimize
+    expected = {mf.ReLU: mf.Conv2D_ReLU_Op, mf.LeakyReLU: mf.Conv2D_LeakyReLU_Op}[activation] if fused else mf.Conv2D_Op
+    assert type(conv_nodes[0]) is expected
+
+
+# --- the stage-1 CNN (examples/stage1_cnn.py:15-49) -------------------------------------------
+def stage1_dataset(seed=0):
+    """32 images 1 x 8 x 8: class 0 has bright columns 1-2, class 1 bright rows 1-2."""
+    rng = np.random.default_rng(seed)
+    x = rng.normal(0, 0.05, (32, 1, 8, 8)).astype(np.float32)
+    y = np.arange(32, dtype=np.int64) % 2
+    x[y == 0, :, :, 1:3] += 1
+    x[y == 1, :, 1:3, :] += 1
+    return x, y
+
+
+def build_stage1(seed=0):
+    x_np, y_np = stage1_dataset(seed)
+    onehot = np.eye(2, dtype=np.float32)[y_np]
+    x = mf.Variable(gpu(x_np), requires_grad=False, name="images")
+    t = mf.Variable(gpu(onehot), requires_grad=False, name="targets")
+    init = mf.make_initializer(seed=seed)
+    conv = mf.Conv2D(1, 4, kernel_size=3, padding=1, fuse_activation=False, initializer=init, backend="hip_native")
+    pool = mf.MaxPool2d(2, 2, backend="hip_native")
+    fc1 = mf.Dense(64, 16, activation=mf.ReLU, initializer=init, backend="hip_native")
+    fc2 = mf.Dense(16, 2, initializer=init, backend="hip_native")
+    logits = fc2(fc1(mf.Flatten()(pool(mf.ReLU(conv(x))))))
+    loss = mf.MSELoss(logits, t)
+    graph = mf.Graph(loss, optimize=False)
+    return {"graph": graph, "opt": mf.Adam(graph, learning_rate=0.01), "loss": loss, "logits": logits,
+            "params": conv.params + fc1.params + fc2.params, "labels": y_np, "x": x_np, "t": onehot}
+
+
+def numpy_stage1_step(p, x, t):
+    """Forward + backward of the same network on the NumPy reference path (float32); returns (loss,
+    grads in parameter order, logits)."""
+    k, kb, w1, b1, w2, b2 = p
+    c, cols = rp.conv2d_forward(x, k, kb, (1, 1), (1, 1))
+    r = np.maximum(np.float32(0), c)
+    pooled, mask, padded = rp.maxpool2d_forward(r, (2, 2), (2, 2))
+    flat = pooled.reshape(32, -1)
+    z1 = rp.linear_forward(flat, w1, b1)
+    h1 = np.maximum(np.float32(0), z1)
+    logits = rp.linear_forward(h1, w2, b2)
+    loss = rp.mse_forward(logits, t)
+    g = rp.mse_backward(logits, t, np.float32(1.0)).astype(np.float32)
+    dh1, dw2, db2 = rp.linear_backward(h1, w2, b2.shape, g)
+    dz1 = rp.relu_backward(z1, dh1)
+    dflat, dw1, db1 = rp.linear_backward(flat, w1, b1.shape, dz1)
+    dr = rp.maxpool2d_backward(dflat.reshape(pooled.shape), mask, padded, (2, 2), (2, 2))
+    dc = rp.relu_backward(c, dr)
+    _, dk, dkb = rp.conv2d_backward(x, k, dc, cols, (1, 1), (1, 1), need_input_grad=False)
+    return loss, [dk, dkb, dw1, db1, dw2, db2], logits
+
+
+def assert_all_float32(model):
+    for node in model["graph"].nodes:
+        for name in ("value", "grad"):
+            value = getattr(node, name)
+            if isinstance(value, torch.Tensor):
+                assert value.dtype == torch.float32, f"{node.name}.{name} is {value.dtype}"
+    opt = model["opt"]
+    for state in (opt.acc_gradient, opt.v, opt.s):
+        for value in state.values():
+            assert value.dtype == torch.float32
+
+
+def test_stage1_cnn_trains_for_100_steps_on_the_reference_trajectory():
+    model = build_stage1()
+    params = [host(p.value).copy() for p in model["params"]]
+    moments = [(np.zeros_like(p), np.zeros_like(p)) for p in params]
+    close = dict(atol=1e-4, rtol=1e-3)
+    for step in range(1, 101):
+        model["opt"].one_step()
+        assert_all_float32(model)
+        loss, grads, _ = numpy_stage1_step(params, model["x"], model["t"])
+        if step <= 3:
+            for node, g in zip(model["params"], grads):
+                np.testing.assert_allclose(host(node.grad), g.reshape(node.value.shape), **close,
+                                           err_msg=f"gradient of {node.name} at step {step}")
+        model["opt"].update()
+        assert_all_float32(model)
+        for p, g, (m, v) in zip(params, grads, moments):
+            rp.adam_update(p, g.reshape(p.shape), m, v, lr=0.01, beta1=0.9, beta2=0.999, eps=1e-8, step=step)
+        if step <= 3:
+            for node, p in zip(model["params"], params):
+                np.testing.assert_allclose(host(node.value), p, **close, err_msg=f"{node.name} after step {step}")
+    model["graph"].forward()
+    assert_all_float32(model)
+    loss_ref, _, logits_ref = numpy_stage1_step(params, model["x"], model["t"])
+    logits = host(model["logits"].value)
+    assert np.mean(logits.argmax(1) == model["labels"]) >= 0.95
+    assert np.mean(logits_ref.argmax(1) == model["labels"]) >= 0.95
+    np.testing.assert_allclose(float(host(model["loss"].value)), float(loss_ref), **close)

@@ -173,6 +173,33 @@ def test_adam_first_step_closed_form():
     np.testing.assert_allclose(v, 0.001 * g * g, rtol=1e-5)
 
 
+def test_adam_recurrence_over_four_steps_matches_the_textbook_and_torch():
+    """The moment recurrences from step 2 on (tests/test_fused_ops.py:162-177 of the reference): four
+    steps of the oracle's float32 Adam against the FP64 textbook recurrence within 4 eps32
+    (normwise), and against torch.optim.Adam (float64) with the same gradients. A dropped (1 - beta)
+    factor, a moment not carried over or a bias correction of the wrong step fails one of them."""
+    rng = np.random.default_rng(3)
+    grads = [rng.standard_normal((5, 7)).astype(np.float32) for _ in range(4)]
+    start = np.linspace(-1, 1, 35, dtype=np.float32).reshape(5, 7)
+    p, m, v = start.copy(), np.zeros((5, 7), np.float32), np.zeros((5, 7), np.float32)
+    theta, m64, v64 = start.astype(np.float64), np.zeros((5, 7)), np.zeros((5, 7))
+    t_param = torch.tensor(start.astype(np.float64), requires_grad=True)
+    t_opt = torch.optim.Adam([t_param], lr=1e-3, betas=(0.9, 0.999), eps=1e-8)
+    eps32 = np.finfo(np.float32).eps
+    for step, g in enumerate(grads, 1):
+        rp.adam_update(p, g, m, v, lr=1e-3, beta1=0.9, beta2=0.999, eps=1e-8, step=step)
+        g64 = g.astype(np.float64)
+        m64 = 0.9 * m64 + 0.1 * g64
+        v64 = 0.999 * v64 + 0.001 * g64 * g64
+        theta = theta - 1e-3 * (m64 / (1 - 0.9 ** step)) / (np.sqrt(v64 / (1 - 0.999 ** step)) + 1e-8)
+        t_param.grad = torch.tensor(g64)
+        t_opt.step()
+        assert np.abs(p - theta).max() <= 4 * eps32 * np.abs(theta).max(), step
+        np.testing.assert_allclose(p, t_param.detach().numpy(), rtol=0, atol=4 * eps32)
+        np.testing.assert_allclose(m, m64, rtol=1e-6, atol=1e-7)
+        np.testing.assert_allclose(v, v64, rtol=1e-5, atol=1e-9)
+
+
 def test_linear_and_mse_match_torch():
     rng = np.random.default_rng(1)
     x = rng.normal(size=(7, 5)).astype(np.float32)
