@@ -5,7 +5,8 @@
  * kernels of ops/fused.py behind the same calling conventions:
  *
  *   - every device buffer is a uint64_t device address owned by the caller (PyTorch here, CuPy in
- *     the reference); the library never allocates device memory;
+ *     the reference); the library never allocates device memory (its one device array, the fixed
+ *     scratch of mfh_gemm_noalloc, is part of the loaded code object);
  *   - a null optional pointer means "not requested";
  *   - dimensions are int, the stream is a uint64_t hipStream_t handle (0 = null stream);
  *   - launches are asynchronous on that stream; nothing synchronises unless debug sync is on
@@ -216,6 +217,21 @@ MFH_API int mfh_split_reduce(uint64_t partial, uint64_t c, int slices, int M, in
 MFH_API int mfh_gemm(int engine, int trans_a, int trans_b, uint64_t a, uint64_t b, uint64_t bias, uint64_t c, int M,
                      int N, int K, int lda, int ldb, int ldc, uint64_t workspace, int64_t workspace_floats,
                      uint64_t stream);
+
+/* Floats of the static split-K scratch of mfh_gemm_noalloc (32 MiB per GPU). */
+#define MFH_GEMM_NOALLOC_SCRATCH_FLOATS 8388608
+
+/* mfh_gemm without a workspace argument, for callers that cannot allocate device memory (code under
+ * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc): the split-K partials go
+ * to a fixed device array inside the library (MFH_GEMM_NOALLOC_SCRATCH_FLOATS floats per GPU, held
+ * until the process ends). The call allocates nothing. A plan whose slices * M * N exceeds the
+ * scratch is rejected with status 2 (the plan is the one mfh_gemm would run given a large enough
+ * workspace: engine 1's automatic plan, or an explicit code). Every call on a GPU shares that GPU's
+ * scratch: calls that overlap in time on one GPU (on other streams or threads) race. Results are
+ * bitwise those of mfh_gemm with the same engine and a workspace of the plan's size.
+ * No counterpart in the reference (its mf_gemm always takes the caller's workspace). */
+MFH_API int mfh_gemm_noalloc(int engine, int trans_a, int trans_b, uint64_t a, uint64_t b, uint64_t bias, uint64_t c,
+                             int M, int N, int K, int lda, int ldb, int ldc, uint64_t stream);
 
 /* ---- batch normalisation (+ residual add + ReLU) -------------------------------------------- */
 

@@ -20,6 +20,8 @@ struct LibraryState {
     int device = -1;
     int cus = 0;
     std::string info = "{}";
+    // Device address of `scratch` on each device that mfh_init has set up (index: device id).
+    std::vector<float*> scratch_address;
 };
 
 LibraryState& state() {
@@ -28,6 +30,25 @@ LibraryState& state() {
 }
 
 thread_local std::string error_text;
+
+// The split-K workspace of mfh_gemm_noalloc: a fixed array in device memory, one copy per GPU that
+// the library runs on, held until the process ends. Host code never passes its name to a kernel
+// (on the host the name is only a stand-in); it uses the device address that mfh_init looks up
+// with hipGetSymbolAddress. Every mfh_gemm_noalloc call on a GPU shares that GPU's copy, so calls
+// that overlap in time on one GPU (other streams, other threads) race. A split-K slice writes its
+// whole M x N partial before the reduction reads it, so nothing in it needs to start at zero.
+__device__ __align__(256) float scratch[MFH_GEMM_NOALLOC_SCRATCH_FLOATS];
+
+// Looks up this device's address of `scratch` (the current device must be `device`).
+int set_up_scratch(LibraryState& s, int device) {
+    void* address = nullptr;
+    const hipError_t rc = hipGetSymbolAddress(&address, HIP_SYMBOL(scratch));
+    if (rc != hipSuccess)
+        return MFH_FAIL(ERR_INIT, std::string("hipGetSymbolAddress(scratch): ") + hipGetErrorString(rc));
+    if (static_cast<int>(s.scratch_address.size()) <= device) s.scratch_address.resize(device + 1, nullptr);
+    s.scratch_address[device] = static_cast<float*>(address);
+    return OK;
+}
 
 template <typename T>
 T* as_ptr(std::uint64_t address) {
@@ -171,6 +192,7 @@ MFH_API int mfh_init(void) {
     if (arch.rfind("gfx950", 0) != 0)
         return MFH_FAIL(ERR_INIT, "libmfhip is built for gfx950 only; the current device is " + arch);
     MFH_TRY(probe_code_object());
+    MFH_TRY(set_up_scratch(s, device));
     const char* flag = std::getenv("MFHIP_SYNC");
     if (flag && flag[0] && flag[0] != '0') s.sync_each_launch = true;
     int runtime = 0;
@@ -550,6 +572,24 @@ MFH_API int mfh_gemm(int engine, int trans_a, int trans_b, std::uint64_t a, std:
     e.bias = as_ptr<const float>(bias);
     e.bias_mode = bias ? BIAS_COLUMN : BIAS_NONE;
     return gemm_launch(engine, as_stream(stream), o, e, as_ptr<float>(workspace), workspace_floats);
+}
+
+MFH_API int mfh_gemm_noalloc(int engine, int trans_a, int trans_b, std::uint64_t a, std::uint64_t b,
+                             std::uint64_t bias, std::uint64_t c, int M, int N, int K, int lda, int ldb, int ldc,
+                             std::uint64_t stream) {
+    MFH_TRY(require_ready());
+    MFH_TRY(validate_engine(engine));
+    MFH_REQUIRE(M > 0 && N > 0 && K > 0, "GEMM dimensions must be positive");
+    const std::int64_t needed = gemm_launch_workspace(engine, M, N, K);
+    if (needed < 0) return MFH_FAIL(ERR_ARG, "unknown GEMM engine or plan code");
+    if (needed > MFH_GEMM_NOALLOC_SCRATCH_FLOATS)
+        return MFH_FAIL(ERR_ARG, "mfh_gemm_noalloc: this plan's split-K workspace needs " + std::to_string(needed) +
+                                     " floats, more than the " + std::to_string(MFH_GEMM_NOALLOC_SCRATCH_FLOATS) +
+                                     " of the static scratch; use fewer K slices or mfh_gemm with a workspace");
+    float* workspace = state().scratch_address[state().device];
+    return mfh_gemm(engine, trans_a, trans_b, a, b, bias, c, M, N, K, lda, ldb, ldc,
+                    static_cast<std::uint64_t>(reinterpret_cast<std::uintptr_t>(workspace)),
+                    MFH_GEMM_NOALLOC_SCRATCH_FLOATS, stream);
 }
 
 MFH_API std::int64_t mfh_bn_workspace(int N, int C, int HW) {

@@ -197,6 +197,10 @@ struct GemmEpilogue {
 // plan's slices * M * N floats.
 int gemm_launch(int engine, hipStream_t stream, const GemmOperands& operands, const GemmEpilogue& epilogue,
                 float* workspace, std::int64_t workspace_floats);
+// Workspace floats gemm_launch uses for one problem with a plain epilogue (bias per column at
+// most) when it is given all it asks for: the plan's slices * M * N, or 0 (no split, or an output
+// of at most 8 columns under the automatic plan, which takes the one-wave-per-row kernel).
+std::int64_t gemm_launch_workspace(int engine, int M, int N, int K);
 int split_reduce(const float* partial, float* c, int slices, int M, int N, int ldc, bool reference,
                  hipStream_t stream);
 // The FP64 slice-order reduction of split-K partials (slices x M x N, dense) followed by the

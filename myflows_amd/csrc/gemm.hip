@@ -441,13 +441,25 @@ __global__ __launch_bounds__(256) void gemm_skinny_kernel(GemmParams p, int tran
     }
 }
 
+// Whether gemm_launch runs the problem on gemm_skinny_kernel.
+bool takes_skinny(int engine, int batch, int N, const GemmEpilogue& e) {
+    return engine == 1 && batch == 1 && N <= SKINNY_N && e.segment == 0 && e.taps == 0 && e.lattice_w == 0 &&
+           !e.residual;
+}
+
 }  // namespace
+
+std::int64_t gemm_launch_workspace(int engine, int M, int N, int K) {
+    if (takes_skinny(engine, 1, N, GemmEpilogue{})) return 0;
+    GemmPlan plan;
+    if (gemm_plan_from_engine(engine, M, N, K, &plan) != OK) return -1;
+    return gemm_workspace_floats(plan, M, N);
+}
 
 int gemm_launch(int engine, hipStream_t stream, const GemmOperands& o, const GemmEpilogue& e, float* workspace,
                 std::int64_t workspace_floats) {
     const int M = o.M, N = o.N, K = o.K;
-    if (engine == 1 && o.batch == 1 && N <= SKINNY_N && e.segment == 0 && e.taps == 0 && e.lattice_w == 0 &&
-        !e.residual) {
+    if (takes_skinny(engine, o.batch, N, e)) {
         GemmParams p = epilogue_params(e, M, N, o.ldc);
         p.A = o.a;
         p.B = o.b;

@@ -89,6 +89,7 @@ _SIGNATURES = {
     "mfh_gemm_workspace": ("q", "iii"),
     "mfh_split_reduce": ("i", "pp" + "iiiii" + "p"),
     "mfh_gemm": ("i", "iiipppp" + "iiiiii" + "pqp"),
+    "mfh_gemm_noalloc": ("i", "iiipppp" + "iiiiii" + "p"),
     "mfh_bn_workspace": ("q", "iii"),
     "mfh_bn_forward": ("i", "ppppppppppq" + "iiiii" + "ddd" + "p"),
     "mfh_bn_backward": ("i", "pppppppppppq" + "iii" + "iiiii" + "p"),
