@@ -23,6 +23,8 @@
 // mapping, so an unsplit product adds each output's K terms in the same order whatever the tile.
 #pragma once
 
+#include <type_traits>
+
 #include "common.h"
 
 namespace mfh {
@@ -182,8 +184,9 @@ __device__ __forceinline__ void zero_acc(v16f (&acc)[S::TM][S::TN]) {
 
 // One stage of MFMAs on the LDS tiles As / Bs (see the operand mapping above).
 // KK0 / KK1 select a part of the stage (groups of four k per lane half), for a loop that puts
-// other work between the parts.
-template <class S, int KK0 = 0, int KK1 = S::HALF>
+// other work between the parts. RESTART: the part's first MFMA takes a zero accumulator input, so
+// the accumulators start over with this stage (their earlier contents are discarded).
+template <class S, int KK0 = 0, int KK1 = S::HALF, bool RESTART = false>
 __device__ __forceinline__ void mfma_stage(const float* As, const float* Bs, v16f (&acc)[S::TM][S::TN], int wm0,
                                            int wn0, int lane) {
     constexpr int HALF = S::HALF, LDA_S = S::LDA_S, LDB_S = S::LDB_S;
@@ -212,7 +215,10 @@ __device__ __forceinline__ void mfma_stage(const float* As, const float* Bs, v16
         for (int i = 0; i < S::TM; ++i)
 #pragma unroll
             for (int j = 0; j < S::TN; ++j) {
-                acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[i].x, b[j].x, acc[i][j], 0, 0, 0);
+                if (RESTART && kk == KK0)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[i].x, b[j].x, v16f{}, 0, 0, 0);
+                else
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[i].x, b[j].x, acc[i][j], 0, 0, 0);
                 acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[i].y, b[j].y, acc[i][j], 0, 0, 0);
                 acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[i].z, b[j].z, acc[i][j], 0, 0, 0);
                 acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[i].w, b[j].w, acc[i][j], 0, 0, 0);
@@ -230,11 +236,58 @@ __device__ __forceinline__ void mfma_stage(const float* As, const float* Bs, v16
 //                   stage's MFMAs: 3-5 % on the dW products, whose stores carry gathered operands.
 enum StageOrder : int { STAGE_PLAIN = 0, STAGE_PRIORITY = 1, STAGE_MID_STORE = 2 };
 
+// What a K loop does with the accumulators after each stage's MFMAs: nothing (the FP32 chain runs
+// on over the whole K range), or StageSums below (restarts = whether each stage starts its
+// accumulators from zero).
+struct KeepChain {
+    static constexpr bool restarts = false;
+    template <class Acc>
+    __device__ __forceinline__ void operator()(Acc&) const {}
+};
+
+// Stage sums: each stage's BK terms are summed on the matrix cores into accumulators that start
+// from zero, and the stage sums are then added to totals of type T, so an output's rounding chain
+// on the matrix cores is one stage long instead of the whole K range: a two-level sum, whose error
+// grows like sqrt(BK * K + K^2 / BK) unit roundoffs instead of K for one chain (T = float), or like
+// sqrt(BK * K) (T = double, at twice the registers). rounded() gives the totals as float. The drain
+// of stage t runs at the start of stage t + 1, after the barrier, when the stage's MFMAs are done.
+template <class S, class T = double>
+struct StageSums {
+    static constexpr bool restarts = true;
+    T total[S::TM][S::TN][16];
+    __device__ __forceinline__ StageSums() {
+#pragma unroll
+        for (int i = 0; i < S::TM; ++i)
+#pragma unroll
+            for (int j = 0; j < S::TN; ++j)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) total[i][j][r] = T(0);
+    }
+    __device__ __forceinline__ void operator()(v16f (&acc)[S::TM][S::TN]) {
+#pragma unroll
+        for (int i = 0; i < S::TM; ++i)
+#pragma unroll
+            for (int j = 0; j < S::TN; ++j)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) total[i][j][r] += static_cast<T>(acc[i][j][r]);
+    }
+    __device__ __forceinline__ void rounded(v16f (&acc)[S::TM][S::TN]) const {
+#pragma unroll
+        for (int i = 0; i < S::TM; ++i)
+#pragma unroll
+            for (int j = 0; j < S::TN; ++j)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) acc[i][j][r] = static_cast<float>(total[i][j][r]);
+    }
+};
+
 // The K loop over [k_begin, k_end) in BK stages. fetch(kt) issues the global reads of the stage
-// starting at kt; store(a_lds, b_lds) writes the fetched registers into one LDS stage buffer.
-template <class S, int ORDER = STAGE_PLAIN, class Fetch, class Store>
+// starting at kt; store(a_lds, b_lds) writes the fetched registers into one LDS stage buffer;
+// drain(acc) runs after each stage's MFMAs (KeepChain or StageSums).
+template <class S, int ORDER = STAGE_PLAIN, class Fetch, class Store, class Drain = KeepChain>
 __device__ __forceinline__ void mfma_k_loop(float* smem, int k_begin, int k_end, Fetch&& fetch, Store&& store,
-                                            v16f (&acc)[S::TM][S::TN], int wm0, int wn0, int lane) {
+                                            v16f (&acc)[S::TM][S::TN], int wm0, int wn0, int lane,
+                                            Drain&& drain = Drain{}) {
     constexpr int BK = S::BK;
     const int stages = k_end > k_begin ? (k_end - k_begin + BK - 1) / BK : 0;
     if (stages > 0) {
@@ -245,21 +298,25 @@ __device__ __forceinline__ void mfma_k_loop(float* smem, int k_begin, int k_end,
     for (int t = 0; t < stages; ++t) {
         const bool more = t + 1 < stages;
         if (more) fetch(k_begin + (t + 1) * BK);
+        // The previous stage's sums: its MFMAs have completed while the wave waited at the barrier.
+        if (t > 0) drain(acc);
         const float* As = smem + (t & 1) * S::STAGE;
         float* next = smem + ((t + 1) & 1) * S::STAGE;
+        constexpr bool RESTART = std::decay_t<Drain>::restarts;
         if constexpr (ORDER == STAGE_MID_STORE && S::HALF >= 8) {
             constexpr int MID = S::HALF / 8 * 4;
-            mfma_stage<S, 0, MID>(As, As + S::A_SIZE, acc, wm0, wn0, lane);
+            mfma_stage<S, 0, MID, RESTART>(As, As + S::A_SIZE, acc, wm0, wn0, lane);
             if (more) store(next, next + S::A_SIZE);
             mfma_stage<S, MID, S::HALF>(As, As + S::A_SIZE, acc, wm0, wn0, lane);
         } else {
             if constexpr (ORDER == STAGE_PRIORITY) __builtin_amdgcn_s_setprio(1);
-            mfma_stage<S>(As, As + S::A_SIZE, acc, wm0, wn0, lane);
+            mfma_stage<S, 0, S::HALF, RESTART>(As, As + S::A_SIZE, acc, wm0, wn0, lane);
             if (more) store(next, next + S::A_SIZE);
             if constexpr (ORDER == STAGE_PRIORITY) __builtin_amdgcn_s_setprio(0);
         }
         __syncthreads();
     }
+    if (stages > 0) drain(acc);
 }
 
 // Epilogue: bias (per output column or per output row), the activation, then the store of the

@@ -291,7 +291,13 @@ __device__ __forceinline__ void implicit_forward_tile(const GemmParams& p, const
     };
     v16f acc[S::TM][S::TN];
     zero_acc<S>(acc);
-    mfma_k_loop<S>(smem, k_begin, k_end, fetch, store, acc, wm0, wn0, lane);
+    // Two-level FP32 sum: 32-term stage sums on the matrix cores, added in FP32. Measured on the
+    // batch-64 ResNet18 products, it brings the normwise error of the forward and dX products 4-7x
+    // below one 576-4608-term chain (below the NumPy float32 path's) for 2 % of their time; FP64
+    // totals were 3x more accurate still but cost 7 % (registers: one workgroup less per CU).
+    StageSums<S, float> sums;
+    mfma_k_loop<S>(smem, k_begin, k_end, fetch, store, acc, wm0, wn0, lane, sums);
+    sums.rounded(acc);
     store_acc<S>(p, C, acc, m0, n0, wm0, wn0, lane);
 }
 

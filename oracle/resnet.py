@@ -88,10 +88,18 @@ class _Tape:
             self.grads[name] = np.array(value, dtype=self.dtype, copy=True)
 
 
-def forward_backward(params, running, x, target, training=True, need_input_grad=False, backward=True):
+def forward_backward(params, running, x, target, training=True, need_input_grad=False, backward=True,
+                     decisions=None, record=None):
     """One forward + backward pass in the dtype of x (float32 is the reference path; float64 gives
     the high-precision comparison point). Returns (loss, grads by parameter name, output); with
-    backward=False the pass stops after the loss (grads empty)."""
+    backward=False the pass stops after the loss (grads empty).
+
+    The pass's discrete decisions are each ReLU's mask (input > 0, keyed by the ReLU's name:
+    "stem_relu", "<block>.relu1", "<block>.out") and the stem max-pool's window choices ("pool",
+    a one-hot mask over each window). ``record`` (a dict) receives them; ``decisions`` (the same
+    form) imposes them instead of deciding from this pass's own values, so that two passes that
+    took different branches at near-ties can be compared on their rounding alone. ``record`` also
+    receives each decision's input ("<name>/input")."""
     dtype = x.dtype
     tape = _Tape(dtype)
     acts = {}
@@ -112,13 +120,29 @@ def forward_backward(params, running, x, target, training=True, need_input_grad=
         return name
 
     def relu(src, name):
-        acts[name] = np.maximum(0, acts[src])
-        tape.ops.append(("relu", name, src))
+        if record is not None:
+            record[name] = acts[src] > 0
+            record[name + "/input"] = acts[src]
+        if decisions is None:
+            acts[name] = np.maximum(0, acts[src])
+            mask = None
+        else:
+            mask = decisions[name]
+            acts[name] = np.where(mask, acts[src], dtype.type(0))
+        tape.ops.append(("relu", name, src, mask))
         return name
 
     acts["x"] = x
     h = relu(bn(conv("x", "stem", 2, 3), "stem_bn"), "stem_relu")
     y, mask, padded = rp.maxpool2d_forward(acts[h], (3, 3), (2, 2))
+    if record is not None:
+        record["pool"] = mask
+        record["pool/input"] = acts[h]
+    if decisions is not None:
+        mask = decisions["pool"]
+        n, c = acts[h].shape[:2]
+        patches = rp.im2col(acts[h], (3, 3), (2, 2), (0, 0)).reshape(n, -1, c, 9).transpose(0, 2, 1, 3)
+        y = np.take_along_axis(patches, mask.argmax(axis=-1)[..., None], axis=-1)[..., 0].reshape(y.shape)
     acts["pool"] = y
     tape.ops.append(("pool", "pool", h, mask, padded))
     h = "pool"
@@ -158,7 +182,8 @@ def forward_backward(params, running, x, target, training=True, need_input_grad=
         if kind == "gap":
             push(src, rp.gap_backward(g, acts[src].shape))
         elif kind == "relu":
-            push(src, rp.relu_backward(acts[src], g))
+            mask = op[3]
+            push(src, rp.relu_backward(acts[src], g) if mask is None else np.where(mask, g, dtype.type(0)))
         elif kind == "add":
             push(src, g)
             push(op[3], g)

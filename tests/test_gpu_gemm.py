@@ -80,6 +80,24 @@ def test_config2_square_products_at_their_stated_sizes(size, layout):
     assert_near(result, exact, 1e-5, "C")
 
 
+@pytest.mark.parametrize("shape", ((1024, 1024, 1024), (256, 256, 4096), (38400, 64, 576)), ids=str)
+def test_engine_is_no_less_accurate_than_one_fma_chain_per_output(shape):
+    """The reference's FP32 GEMM (its register engine) adds each output's K products in one FMA
+    chain; the teaching kernel "basic" with fp32 accumulation does exactly that. The MFMA engine's
+    normwise error against the FP64 product stays within 1.25x that chain's on the same inputs
+    (config 2's inputs, A then B ~ N(0, 1), seed 0)."""
+    m, n, k = shape
+    rng = np.random.default_rng(0)
+    a, b, exact, _ = operands(rng, m, n, k, False, False)
+    da, db = gpu(a), gpu(b)
+    engine = host(native.gemm(da, db)).astype(np.float64)
+    chain = host(native.matmul(da, db, variant="basic", accumulate="fp32")).astype(np.float64)
+    scale = np.abs(exact).max()
+    err_engine, err_chain = np.abs(engine - exact).max() / scale, np.abs(chain - exact).max() / scale
+    print("engine / one chain", shape, err_engine, err_chain, err_engine / err_chain, flush=True)
+    assert err_engine <= 1.25 * err_chain
+
+
 def test_misaligned_operands_take_the_scalar_loads():
     rng = np.random.default_rng(4)
     for (m, n, k) in ((300, 260, 100), (67, 39, 45)):

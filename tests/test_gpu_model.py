@@ -1,10 +1,13 @@
 """End-to-end parity on the GPU through the Variable/Graph API on the hip_native backend: Linear,
-the C3 convolution + pooling configuration, the ResNet18 training step (C1 shape, both graph modes),
-and ResNet18 inference with BN folding and the Conv+ReLU epilogue (a small C5).
+the C3 convolution + pooling configuration, the ResNet18 training step (C1 shape, both graph modes,
+and C4 at batch 64), and ResNet18 inference with BN folding and the Conv+ReLU and Conv+Add+ReLU
+epilogues (a small C5, and C5 at batch 256, 224 x 224).
 
-Model-level tolerance, "no worse than the reference FP32 path": against the same step computed in
-float64 by the oracle, the GPU's normwise error stays within 4x the NumPy float32 path's own error
-plus 1e-5 of the tensor's scale.
+Model-level tolerance, "no worse than the reference FP32 path": against the same pass computed in
+float64 by the oracle, the GPU's error is at most the NumPy float32 path's own error plus a floor
+of about one float32 ulp; a training step is compared with the GPU's ReLU and max-pool decisions
+imposed on both oracle passes, after checking that the decisions that differ from FP64 are
+near-ties (see test_resnet18_training_step_matches_numpy_reference).
 """
 
 import json
@@ -108,12 +111,68 @@ def build_resnet(batch, height, width, base_width=64, seed=0, optimize=False):
     return model, mf.Graph(loss, optimize=optimize), out, loss, x_np, t_np
 
 
+def gpu_decisions(graph, base_width):
+    """The discrete decisions of the GPU's forward in the oracle's form: each ReLU's mask (output > 0,
+    the same as input > 0) by the oracle's ReLU names, and the stem max-pool's choice in each window
+    (from its int32 argmax) as a one-hot mask."""
+    relus = [node for node in graph.nodes if type(node) is mf.ReLU]
+    names = ["stem_relu"] + [f"{spec[0]}.{part}" for spec in oracle_resnet.block_specs(base_width)
+                             for part in ("relu1", "out")]
+    assert len(relus) == len(names)
+    decisions = {name: host(node.value) > 0 for name, node in zip(names, relus)}
+    context = next(node for node in graph.nodes if isinstance(node, mf.MaxPool2d_Op))._context
+    n, c, h, w = context.input_shape
+    oh, ow = context.output_shape[2:]
+    argmax = host(context.argmax).astype(np.int64)
+    kh = (argmax // w) % h - 2 * np.arange(oh)[:, None]
+    kw = argmax % w - 2 * np.arange(ow)[None, :]
+    mask = np.zeros((n, c, oh * ow, 9), bool)
+    np.put_along_axis(mask, (kh * 3 + kw).reshape(n, c, oh * ow)[..., None], True, axis=-1)
+    decisions["pool"] = mask
+    return decisions
+
+
+def decision_flips(decisions, record, tie=1e-5):
+    """Where the GPU's decisions differ from the FP64 pass's: (count, worst distance of a flipped
+    decision from a tie, relative to the largest input of its ReLU / pool)."""
+    count, worst = 0, 0.0
+    for name, mask in decisions.items():
+        flipped = mask != record[name]
+        if not flipped.any():
+            continue
+        values = record[name + "/input"]
+        scale = np.abs(values).max()
+        if name == "pool":
+            n, c = values.shape[:2]
+            patches = rp.im2col(values, (3, 3), (2, 2), (0, 0)).reshape(n, -1, c, 9).transpose(0, 2, 1, 3)
+            chosen_gpu = np.take_along_axis(patches, mask.argmax(-1)[..., None], -1)[..., 0]
+            chosen_64 = np.take_along_axis(patches, record[name].argmax(-1)[..., None], -1)[..., 0]
+            windows = flipped.any(-1)
+            count += int(windows.sum())
+            worst = max(worst, float(np.abs(chosen_64 - chosen_gpu)[windows].max() / scale))
+        else:
+            count += int(flipped.sum())
+            worst = max(worst, float(np.abs(values[flipped]).max() / scale))
+    return count, worst
+
+
 @pytest.mark.parametrize("batch,height,width,base_width,optimize",
                          [(2, 120, 160, 64, False), (2, 120, 160, 64, True), (4, 64, 64, 16, True),
                           (64, 120, 160, 64, True)],
                          ids=("C1-bs2-120x160", "C1-bs2-120x160-fused-units", "small-fused-units",
                               "C4-bs64-120x160-fused-units"))
 def test_resnet18_training_step_matches_numpy_reference(batch, height, width, base_width, optimize):
+    """One training step against the oracle, "no worse than the reference FP32 path". A ReLU mask or
+    max-pool choice is a discontinuity: where a pre-activation lies within rounding of zero (or two
+    window values within rounding of each other), the GPU, the NumPy float32 path and FP64 may
+    branch differently, and one such flip moves a gradient by a whole term rather than by rounding
+    (at batch 64 the GPU and FP64 differ in 14 of ~10^8 decisions, all within 6e-7 of a tie). So
+    the step is compared in two parts:
+      * every decision the GPU took that differs from the FP64 pass's is a near-tie (its input within
+        1e-5 of its ReLU's / pool's largest input), and the loss agrees;
+      * with the GPU's decisions imposed on the FP64 and the NumPy float32 passes, the GPU's error of
+        the output and of every gradient is at most the NumPy path's, plus a floor of about one
+        float32 ulp (written below)."""
     print("resnet step", batch, height, width, base_width, optimize, flush=True)
     model, graph, out, loss, x_np, t_np = build_resnet(batch, height, width, base_width, optimize=optimize)
     if optimize:
@@ -122,29 +181,41 @@ def test_resnet18_training_step_matches_numpy_reference(batch, height, width, ba
     opt.one_step()
     grads = [host(p.grad) for p in model.params]
     gpu_out, gpu_loss = host(out.value), float(host(loss.value))
+    decisions = gpu_decisions(graph, base_width)
     opt.update()
     updated = [host(p.value) for p in model.params]
 
     params32, running32 = oracle_resnet.init_params(base_width=base_width, seed=0)
     params64, running64 = oracle_resnet.as_dtype(params32, running32, np.float64)
-    _, grads32, out32 = oracle_resnet.forward_backward(params32, running32, x_np, t_np)
-    loss64, grads64, out64 = oracle_resnet.forward_backward(params64, running64, x_np.astype(np.float64),
-                                                            t_np.astype(np.float64))
+    x64, t64 = x_np.astype(np.float64), t_np.astype(np.float64)
+    record = {}
+    loss64, _, out64 = oracle_resnet.forward_backward(params64, oracle_resnet.as_dtype(params32, running32,
+                                                      np.float64)[1], x64, t64, record=record, backward=False)
+    flips, tie = decision_flips(decisions, record)
+    del record
+    assert tie <= 1e-5, f"a decision differs from FP64 away from a tie ({flips} flips, worst {tie:.2e})"
     assert abs(gpu_loss - loss64) <= 1e-4 * abs(loss64)
-    ratios = {"output": normwise(gpu_out, out64) / max(normwise(out32, out64), 1e-30)}
-    floor = 1e-5 * max(np.abs(g).max() for g in grads64.values())
+    _, grads64, out64 = oracle_resnet.forward_backward(params64, running64, x64, t64, decisions=decisions)
+    _, grads32, out32 = oracle_resnet.forward_backward(params32, running32, x_np, t_np, decisions=decisions)
+    ratios = {"output": (normwise(gpu_out, out64) / max(normwise(out32, out64), 1e-30), 0, 0, 0)}
+    largest = max(np.abs(g).max() for g in grads64.values())
+    for name, g in zip(params32, grads):
+        ref = grads64[name]
+        eg, en = float(np.abs(g - ref).max()), float(np.abs(grads32[name] - ref).max())
+        ratios[name] = (eg / max(en, 1e-30), eg, en, float(np.abs(ref).max()))
+    print("ERROR_RATIOS", json.dumps({"case": [batch, height, width, base_width, optimize], "flips": flips,
+                                      "worst_tie": tie, "largest": float(largest),
+                                      "worst": sorted(ratios.items(), key=lambda kv: -kv[1][0])[:10],
+                                      "median": float(np.median([v[0] for v in ratios.values()]))}), flush=True)
+    assert normwise(gpu_out, out64) <= normwise(out32, out64) + 1e-7
     for name, g in zip(params32, grads):
         ref = grads64[name]
         err_gpu, err_numpy = np.abs(g - ref).max(), np.abs(grads32[name] - ref).max()
-        ratios[name] = float(err_gpu / max(err_numpy, 1e-30))
-    print("ERROR_RATIOS", json.dumps({"case": [batch, height, width, base_width, optimize],
-                                      "worst": sorted(ratios.items(), key=lambda kv: -kv[1])[:8],
-                                      "median": float(np.median(list(ratios.values())))}), flush=True)
-    assert normwise(gpu_out, out64) <= max(4 * normwise(out32, out64), 1e-5)
-    for name, g in zip(params32, grads):
-        ref = grads64[name]
-        err_gpu, err_numpy = np.abs(g - ref).max(), np.abs(grads32[name] - ref).max()
-        assert err_gpu <= 4 * err_numpy + 1e-5 * np.abs(ref).max() + floor, (name, err_gpu, err_numpy)
+        # The floor: 1e-6 of the tensor's scale (a few float32 ulps), and 1e-7 of the largest gradient,
+        # the rounding noise of a convolution bias ahead of a train-mode batch norm, whose exact
+        # gradient is zero (the norm removes the channel mean), so that any float32 path computes it
+        # as cancellation noise of its dy terms.
+        assert err_gpu <= err_numpy + 1e-6 * np.abs(ref).max() + 1e-7 * largest, (name, err_gpu, err_numpy)
     # The reference's Adam step applied to the GPU's gradients reproduces the GPU update bit for bit.
     for name, p_new, g in zip(params32, updated, grads):
         p = params32[name].copy()
@@ -231,7 +302,7 @@ def test_resnet18_inference_with_bn_folding_and_conv_relu_epilogue():
     _, _, out32 = oracle_resnet.forward_backward(params32, {k: (m.copy(), v.copy()) for k, (m, v) in running32.items()},
                                                  x_np, t_np, training=False)
     print("ERROR_RATIOS", json.dumps({"case": "small C5", "output": normwise(got, out64) / normwise(out32, out64)}))
-    assert normwise(got, out64) <= max(4 * normwise(out32, out64), 1e-5)
+    assert normwise(got, out64) <= normwise(out32, out64) + 1e-7
 
 
 def _c5_model(seed=0):
@@ -257,7 +328,8 @@ def test_config5_inference_at_batch_256_and_224x224():
     """Config 5 at its stated size: the folded, fused bs256 224 x 224 pass (the measured bs256 plans,
     the Conv+ReLU and Conv+Add+ReLU epilogues). Eval-mode outputs are per image, so images 0, 85,
     170 and 255 are checked against the oracle's eval forward of those images alone (FP64), within
-    4x the NumPy float32 path's own error."""
+    the NumPy float32 path's own error (a forward pass: a ReLU that flips at a near-tie moves the
+    output only by the near-zero value it gates)."""
     print("config 5 full size", flush=True)
     model, params32, running32, x_np = _c5_model()
     out = model(mf.Variable(gpu(x_np), requires_grad=False))
@@ -275,7 +347,7 @@ def test_config5_inference_at_batch_256_and_224x224():
     _, _, out32 = oracle_resnet.forward_backward(params32, running32, sample, target, training=False, backward=False)
     print("ERROR_RATIOS", json.dumps({"case": "C5 bs256 224", "output": normwise(got[picks], out64) /
                                       normwise(out32, out64)}), flush=True)
-    assert normwise(got[picks], out64) <= max(4 * normwise(out32, out64), 1e-5)
+    assert normwise(got[picks], out64) <= normwise(out32, out64) + 1e-7
 
 
 def test_conv_add_relu_epilogue_equals_separate_add_and_relu_bit_for_bit():

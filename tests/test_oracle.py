@@ -265,3 +265,27 @@ def test_resnet_param_order_and_count():
     names = list(params)
     assert names[0] == "stem.weight" and names[-2:] == ["fc.W", "fc.b"]
     assert names.index("layer2.0.down.weight") > names.index("layer2.0.conv2.weight")
+
+
+def test_resnet_oracle_follows_imposed_decisions():
+    """The decisions a pass records, imposed on the same pass, reproduce it bit for bit; flipping one
+    ReLU mask entry changes the gradient only through that entry's term."""
+    params, running = oracle_resnet.init_params(base_width=8, seed=1)
+    x, t = oracle_resnet.synthetic_batch(2, 32, 40, seed=1)
+    record = {}
+    loss, grads, out = oracle_resnet.forward_backward(params, {k: (m.copy(), v.copy()) for k, (m, v) in running.items()},
+                                               x, t, record=record)
+    decisions = {k: v for k, v in record.items() if not k.endswith("/input")}
+    loss2, grads2, out2 = oracle_resnet.forward_backward(params, {k: (m.copy(), v.copy()) for k, (m, v) in running.items()},
+                                                  x, t, decisions=decisions)
+    assert loss2 == loss and np.array_equal(out2, out)
+    for name in grads:
+        np.testing.assert_array_equal(grads2[name], grads[name], err_msg=name)
+    flipped = dict(decisions)
+    mask = flipped["layer4.1.out"].copy()
+    mask.flat[0] = not mask.flat[0]
+    flipped["layer4.1.out"] = mask
+    _, grads3, _ = oracle_resnet.forward_backward(params, {k: (m.copy(), v.copy()) for k, (m, v) in running.items()},
+                                           x, t, decisions=flipped)
+    assert not np.array_equal(grads3["fc.W"], grads["fc.W"])
+
