@@ -705,13 +705,15 @@ GemmPlan wgrad_plan(int M, int N, int K) {
 }
 
 // Measured plans: products whose best tile and split, in a sweep of every tile and split on MI355X,
-// beat the automatic plan below by at least 2 % (ResNet18's batch-64 convolutions at 3x120x160).
+// beat the automatic plan below by at least 2 % (ResNet18's batch-64 convolutions at 3x120x160, and
+// its batch-256 inference forwards at 224x224). The forward-orientation entries were re-measured for
+// the two-level stage sums, whose extra registers cost tiles 8, 10 and 11 a resident workgroup.
 // Key: orientation (0 forward / dX, 1 dW), M, N, K; value: tile and requested K split.
 struct MeasuredPlan {
     int wgrad, M, N, K, tile, requested;
 };
 constexpr MeasuredPlan MEASURED_PLANS[] = {
-    {0, 64, 307200, 147, 8, 1},    // stem forward
+    {0, 64, 307200, 147, 6, 1},    // stem forward
     {0, 128, 19200, 576, 11, 1},   // layer2.0 conv1 forward (stride 2)
     {0, 128, 19200, 1152, 11, 1},  // layer2 3x3 forward and dX
     {0, 128, 19200, 64, 11, 1},    // layer2 1x1 downsample forward
@@ -721,16 +723,16 @@ constexpr MeasuredPlan MEASURED_PLANS[] = {
     {0, 512, 1280, 2304, 9, 6},    // layer4.0 conv1 forward
     {0, 512, 1280, 4608, 9, 6},    // layer4 3x3 forward and dX
     // ResNet18 inference forward, batch 256 at 224 x 224 (split 1 where within 1 % of the best)
-    {0, 64, 3211264, 147, 8, 1},   // stem
+    {0, 64, 3211264, 147, 6, 1},   // stem
     {0, 64, 774400, 576, 8, 1},    // layer1 3x3 (55 x 55 after the stem's unpadded 3 x 3 / 2 pool)
-    {0, 128, 200704, 576, 11, 1},  // layer2.0 conv1 (stride 2)
-    {0, 128, 200704, 1152, 8, 1},  // layer2 3x3
-    {0, 128, 200704, 64, 8, 1},    // layer2 1x1 downsample
+    {0, 128, 200704, 576, 9, 1},   // layer2.0 conv1 (stride 2)
+    {0, 128, 200704, 1152, 9, 1},  // layer2 3x3
+    {0, 128, 200704, 64, 6, 1},    // layer2 1x1 downsample
     {0, 256, 50176, 1152, 9, 1},   // layer3.0 conv1
-    {0, 256, 50176, 2304, 10, 3},  // layer3 3x3
-    {0, 256, 50176, 128, 8, 1},    // layer3 1x1 downsample
-    {0, 512, 12544, 2304, 10, 3},  // layer4.0 conv1
-    {0, 512, 12544, 4608, 10, 3},  // layer4 3x3
+    {0, 256, 50176, 2304, 6, 1},   // layer3 3x3
+    {0, 256, 50176, 128, 6, 1},    // layer3 1x1 downsample
+    {0, 512, 12544, 2304, 9, 4},   // layer4.0 conv1
+    {0, 512, 12544, 4608, 9, 4},   // layer4 3x3
     {1, 64, 147, 307200, 6, 256},  // stem dW (more slices than the dW rule makes: its gathers need the waves)
     {1, 64, 576, 72384, 8, 96},    // layer1 dW
     {1, 128, 576, 19200, 10, 48},  // layer2.0 conv1 dW
