@@ -19,9 +19,14 @@
  * Kernels index buffers with int32 offsets; entry points reject problems whose buffers exceed
  * 2^31 - 1 elements.
  *
- * GEMM engine codes (engine arguments): 1 = the FP32 MFMA engine with its automatic tile and
- * split-K plan; 16 + tile * 128 + (slices - 1) = an explicit plan (tile index of
- * mfh_gemm_tile_info, 1..128 K slices). The reference's engine 0 (cuBLAS) does not exist here.
+ * GEMM engine codes (engine arguments), with the reference's arithmetic: 1 = the FP32 MFMA engine
+ * with its automatic tile and split-K plan; 16 + n * 32 + (slices - 1) = the reference's named tile n
+ * (0 128x128, 1 128x64, 2 256x32, 3 64x128, 4 32x256; 1..32 K slices), run on this library's tile of
+ * the same role (128x128, 256x64, 128x32, 64x128, 32x128); 1024 + tile * 128 + (slices - 1) = tile
+ * `tile` of this library's catalogue (mfh_gemm_tile_info), 1..128 K slices. Extended codes index the
+ * catalogue of the library that decodes them, so they carry over between builds by tile name only.
+ * The reference's engine 0 (cuBLAS) does not exist here. (The implicit convolution entry points have
+ * their own plan codes: 16 + tile * 128 + (slices - 1) over the 12 implicit tiles.)
  */
 #ifndef MFHIP_H
 #define MFHIP_H
@@ -193,6 +198,11 @@ MFH_API int mfh_matmul(int variant, int tile, int accumulate, uint64_t a, uint64
  * (values[2..3] are the wave tile where the reference reports the thread tile). */
 MFH_API int mfh_gemm_tile_count(void);
 MFH_API int mfh_gemm_tile_info(int index, int* values);
+
+/* LDS stages a tile's main loop keeps in flight: 2 for every tile (double-buffered operand tiles),
+ * or -1 for an unknown tile. Replaces mf_gemm_tile_stages, native_cublas.cpp:1627-1633 (whose
+ * 0 meant register double buffering and 2-4 a cp.async pipeline). */
+MFH_API int mfh_gemm_tile_stages(int index);
 
 /* Automatic tile and split-K slice count for C(M,N) over K.
  * Replaces mf_gemm_plan, native_cublas.cpp:1635-1643. */

@@ -510,6 +510,14 @@ MFH_API int mfh_gemm_tile_info(int index, int* values) {
     return OK;
 }
 
+MFH_API int mfh_gemm_tile_stages(int index) {
+    if (index < 0 || index >= gemm_tile_count()) {
+        MFH_FAIL(ERR_ARG, "unknown GEMM tile");
+        return -1;
+    }
+    return 2;
+}
+
 MFH_API int mfh_gemm_plan(int M, int N, int K, int* tile, int* slices) {
     MFH_TRY(require_ready());
     MFH_REQUIRE(M > 0 && N > 0 && K > 0, "GEMM dimensions must be positive");

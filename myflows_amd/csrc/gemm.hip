@@ -21,9 +21,19 @@ namespace {
 
 constexpr const GemmTile* TILES = GEMM_TILES;
 constexpr int NUM_TILES = GEMM_TILE_COUNT;
-constexpr int PLAN_BASE = 16;     // engine codes >= PLAN_BASE name a tile and a slice count
-constexpr int MAX_SLICES = 128;   // slices per explicit plan code
+constexpr int MAX_SLICES = 128;   // slices of the automatic planner
 constexpr int MIN_CHUNK = 256;    // smallest K slice the automatic planner makes
+
+// Explicit GEMM plan codes, with the reference's arithmetic (ops/cuda_native/native_cublas.cpp:
+// 1264-1269, 1335-1344; native.py:298-309):
+//   NAMED_BASE + n * NAMED_SLICES + (slices - 1), slices <= 32: the reference's named tile n
+//     (128x128, 128x64, 256x32, 64x128, 32x256), run on this catalogue's tile for the same role
+//     (NAMED_TILE_OF: general, N <= 64, N <= 32, M <= 64, M <= 32 outputs);
+//   EXTENDED_BASE + i * EXTENDED_SLICES + (slices - 1), slices <= 128: tile i of this catalogue
+//     (mfh_gemm_tile_info), as the reference's extended codes index its own catalogue.
+constexpr int NAMED_BASE = 16, NAMED_SLICES = 32, NAMED_COUNT = 5;
+constexpr int EXTENDED_BASE = 1024, EXTENDED_SLICES = 128;
+constexpr int NAMED_TILE_OF[NAMED_COUNT] = {0, 1, 4, 2, 5};
 
 template <int BM, int BN, int BK, int WM, int WN, bool TA, bool TB, bool VA, bool VB>
 __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void gemm_mfma_kernel(GemmParams p) {
@@ -313,7 +323,8 @@ GemmPlan gemm_auto_plan(int M, int N, int K, int batch, unsigned tiles) {
 }
 
 bool gemm_engine_valid(int engine) {
-    return engine == 1 || (engine >= PLAN_BASE && engine < PLAN_BASE + NUM_TILES * MAX_SLICES);
+    return engine == 1 || (engine >= NAMED_BASE && engine < NAMED_BASE + NAMED_COUNT * NAMED_SLICES) ||
+           (engine >= EXTENDED_BASE && engine < EXTENDED_BASE + NUM_TILES * EXTENDED_SLICES);
 }
 
 int gemm_plan_from_engine(int engine, int M, int N, int K, GemmPlan* plan, int batch) {
@@ -322,8 +333,10 @@ int gemm_plan_from_engine(int engine, int M, int N, int K, GemmPlan* plan, int b
         *plan = gemm_auto_plan(M, N, K, batch);
         return OK;
     }
-    const int code = engine - PLAN_BASE;
-    const int tile = code / MAX_SLICES, requested = code % MAX_SLICES + 1;
+    const bool named = engine < EXTENDED_BASE;
+    const int code = engine - (named ? NAMED_BASE : EXTENDED_BASE);
+    const int per_tile = named ? NAMED_SLICES : EXTENDED_SLICES;
+    const int tile = named ? NAMED_TILE_OF[code / per_tile] : code / per_tile, requested = code % per_tile + 1;
     const int bk = TILES[tile].bk;
     const std::int64_t rounded = ((static_cast<std::int64_t>(K) + requested - 1) / requested + bk - 1) / bk * bk;
     const int chunk = static_cast<int>(std::min<std::int64_t>(K, rounded));

@@ -36,7 +36,17 @@ GEMM_ENGINES = {"mfma": 1, "register": 1}
 MATMUL_VARIANTS = {"basic": 0, "tiled": 1, "shared": 2, "register": 4}
 MATMUL_ACCUMULATION = {"fp32": 0, "kahan": 1, "dot2": 2}
 ACTIVATION_CODES = {None: 0, "relu": 1, "leaky_relu": 2}
-PLAN_BASE, PLAN_SLICES = 16, 128       # explicit plan code = PLAN_BASE + tile * PLAN_SLICES + slices - 1
+# Explicit GEMM plan codes, with the reference's arithmetic (native.py:298-309 there): the reference's
+# named tiles (its GEMM_TILES) take NAMED_PLAN_BASE + index * NAMED_PLAN_SLICES + slices - 1 (at most 32
+# slices) and run on this library's tile of the same role; every tile of this library's catalogue
+# takes EXTENDED_PLAN_BASE + index * EXTENDED_PLAN_SLICES + slices - 1 (at most 128).
+NAMED_TILES = ("128x128", "128x64", "256x32", "64x128", "32x256")
+NAMED_TILE_OF = {"128x128": "128x128", "128x64": "256x64", "256x32": "128x32", "64x128": "64x128", "32x256": "32x128"}
+NAMED_PLAN_BASE, NAMED_PLAN_SLICES = 16, 32
+EXTENDED_PLAN_BASE, EXTENDED_PLAN_SLICES = 1024, 128
+# Plan codes of the implicit convolution products (their own 12 tiles): IMPLICIT_PLAN_BASE + tile *
+# IMPLICIT_PLAN_SLICES + slices - 1.
+IMPLICIT_PLAN_BASE, IMPLICIT_PLAN_SLICES = 16, 128
 CONV_GRAD_TILE = 64                    # pixels per tile of the transposed-gradient kernel
 ROWS_PATH_MAX_PIXELS = 0               # conv forward through a rows GEMM + epilogue below this OH*OW
 # How convolutions form their GEMM operand: "implicit" gathers the im2col view inside the GEMM's
@@ -85,6 +95,7 @@ _SIGNATURES = {
     "mfh_matmul": ("i", "iiipppp" + "iii" + "p"),
     "mfh_gemm_tile_count": ("i", ""),
     "mfh_gemm_tile_info": ("i", "iP"),
+    "mfh_gemm_tile_stages": ("i", "i"),
     "mfh_gemm_plan": ("i", "iiiPP"),
     "mfh_gemm_workspace": ("q", "iii"),
     "mfh_split_reduce": ("i", "pp" + "iiiii" + "p"),
@@ -280,6 +291,8 @@ def tile_catalog():
     for index in range(lib.mfh_gemm_tile_count()):
         values = (ctypes.c_int * 5)()
         _raise_for(lib.mfh_gemm_tile_info(index, values), lib)
+        if lib.mfh_gemm_tile_stages(index) < 0:
+            _raise_for(2, lib)
         bm, bn, wm, wn, bk = values
         catalog[f"{bm}x{bn}"] = (index, bm, bn, wm, wn, bk)
     return catalog
@@ -287,12 +300,17 @@ def tile_catalog():
 
 @lru_cache(maxsize=2048)
 def _plan_code(tile, requested):
-    """Engine code of an explicit plan: a catalogue tile and a requested split-K slice count."""
-    if type(requested) is not int or not 1 <= requested <= PLAN_SLICES:
-        raise ValueError(f"the split count must be an integer in [1, {PLAN_SLICES}]")
+    """Engine code of an explicit plan: a tile and a requested split-K slice count. A name of the
+    reference's named tiles with at most 32 slices takes its named code (run on this library's tile
+    of the same role, NAMED_TILE_OF); a name of this library's catalogue takes its extended code."""
+    if type(requested) is not int or not 1 <= requested <= EXTENDED_PLAN_SLICES:
+        raise ValueError(f"the split count must be an integer in [1, {EXTENDED_PLAN_SLICES}]")
+    if tile in NAMED_TILES and requested <= NAMED_PLAN_SLICES:
+        return NAMED_PLAN_BASE + NAMED_TILES.index(tile) * NAMED_PLAN_SLICES + requested - 1
     if tile not in tile_catalog():
-        raise ValueError(f"unknown tile {tile!r}; the catalogue has {sorted(tile_catalog())}")
-    return PLAN_BASE + tile_catalog()[tile][0] * PLAN_SLICES + requested - 1
+        raise ValueError(f"unknown tile {tile!r}; the catalogue has {sorted(tile_catalog())}"
+                         + (f" (named tiles take at most {NAMED_PLAN_SLICES} slices)" if tile in NAMED_TILES else ""))
+    return EXTENDED_PLAN_BASE + tile_catalog()[tile][0] * EXTENDED_PLAN_SLICES + requested - 1
 
 
 def _slices(k, requested, bk=16):
@@ -302,10 +320,21 @@ def _slices(k, requested, bk=16):
     return -(-k // chunk)
 
 
+def _explicit_tile(code):
+    """(catalogue tile name, requested slices) of an explicit GEMM plan code."""
+    if NAMED_PLAN_BASE <= code < NAMED_PLAN_BASE + len(NAMED_TILES) * NAMED_PLAN_SLICES:
+        named, part = divmod(code - NAMED_PLAN_BASE, NAMED_PLAN_SLICES)
+        return NAMED_TILE_OF[NAMED_TILES[named]], part + 1
+    index, part = divmod(code - EXTENDED_PLAN_BASE, EXTENDED_PLAN_SLICES)
+    if code < EXTENDED_PLAN_BASE or index >= len(tile_catalog()):
+        raise ValueError(f"unknown GEMM plan code {code}")
+    return list(tile_catalog())[index], part + 1
+
+
 def _explicit_split(code):
     """(requested slices, BK) of an explicit plan code."""
-    tile_index, part = divmod(code - PLAN_BASE, PLAN_SLICES)
-    return part + 1, list(tile_catalog().values())[tile_index][-1]
+    tile, requested = _explicit_tile(code)
+    return requested, tile_catalog()[tile][-1]
 
 
 def _engine_for(engine, layout, m, n, k):

@@ -59,11 +59,25 @@ def test_adam_table_layout_matches_the_header(tmp_path):
 def test_tile_catalogue_and_plan_codes():
     catalogue = native.tile_catalog()
     assert catalogue["128x128"][0] == 0 and all(entry[-1] == 16 for entry in catalogue.values())
-    assert native._plan_code("128x128", 1) == native.PLAN_BASE
-    assert native._plan_code("256x64", 3) == native.PLAN_BASE + native.PLAN_SLICES + 2
-    for bad in (("7x7", 1), ("128x128", 0), ("128x128", native.PLAN_SLICES + 1), ("128x128", 2.0)):
+    # The reference's code arithmetic (native.py:298-309 there): its named tiles take
+    # 16 + index * 32 + slices - 1 (run here on the tile of the same role), catalogue tiles
+    # 1024 + index * 128 + slices - 1.
+    assert native._plan_code("128x128", 1) == 16 and native._plan_code("128x64", 4) == 16 + 32 + 3
+    assert native._plan_code("32x256", 32) == 16 + 4 * 32 + 31
+    assert native._plan_code("256x64", 3) == 1024 + 128 + 2
+    assert native._plan_code("128x128", 33) == 1024 + 32
+    assert native._explicit_tile(16 + 32 + 3) == ("256x64", 4)    # the reference's 128x64, N <= 64
+    assert native._explicit_tile(16 + 2 * 32) == ("128x32", 1)    # 256x32, N <= 32
+    assert native._explicit_tile(16 + 3 * 32 + 7) == ("64x128", 8)
+    assert native._explicit_tile(16 + 4 * 32) == ("32x128", 1)    # 32x256, M <= 32
+    assert native._explicit_tile(1024 + 6 * 128 + 1) == ("256x128", 2)
+    assert all(native.NAMED_TILE_OF[name] in catalogue for name in native.NAMED_TILES)
+    for bad in (("7x7", 1), ("128x128", 0), ("128x128", native.EXTENDED_PLAN_SLICES + 1), ("128x128", 2.0),
+                ("128x64", 33)):
         with pytest.raises(ValueError):
             native._plan_code(*bad)
+    with pytest.raises(ValueError):
+        native._explicit_tile(1024 + len(catalogue) * 128)
     # requested slices -> slices made, with BK-aligned chunks
     assert [native._slices(k, r, 16) for k, r in ((3000, 5), (100, 7), (10, 4), (4096, 1))] == [5, 7, 1, 1]
 

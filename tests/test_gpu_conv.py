@@ -466,7 +466,7 @@ def test_every_implicit_tile_is_exact_on_integer_data(case):
     workspace = torch.empty(1 << 24, device="cuda")
     for tile in range(IMPLICIT_TILES):
         for slices in (1, 3, 24):
-            code = native.PLAN_BASE + tile * native.PLAN_SLICES + slices - 1
+            code = native.IMPLICIT_PLAN_BASE + tile * native.IMPLICIT_PLAN_SLICES + slices - 1
             native._raise_for(lib.mfh_conv_forward_implicit(
                 xg.data_ptr(), wg.data_ptr(), order.data_ptr(), 1, 0, 0, y.data_ptr(), *g.c_args(), 0, 0.0, code,
                 workspace.data_ptr(), workspace.numel(), stream), lib)
@@ -514,7 +514,7 @@ def test_residual_epilogue_equals_separate_add_and_relu(shape, kernel, stride, p
     wt = torch.empty_like(w)
     workspace = torch.empty(3 * g.co * g.m, device="cuda")
     for slices in (1, 3):
-        code = native.PLAN_BASE + 6 * native.PLAN_SLICES + slices - 1
+        code = native.IMPLICIT_PLAN_BASE + 6 * native.IMPLICIT_PLAN_SLICES + slices - 1
         outputs = []
         for extra, act in ((0, 0), (residual.data_ptr(), 1)):
             out = torch.full(g.out_shape, float("nan"), device="cuda")

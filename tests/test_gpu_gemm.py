@@ -163,6 +163,23 @@ def test_split_gemm_is_the_fp64_reduction_of_its_chunks(plan):
     assert host(got).tobytes() == host(expected).tobytes()
 
 
+def test_reference_plan_codes_run_on_the_tile_of_the_same_role():
+    """A named plan of the reference (its 128x64 tile, 4 slices) runs on this library's 256x64 tile with
+    the same split, bit for bit the extended code of that tile; the raw codes give the same bits."""
+    rng = np.random.default_rng(41)
+    a, b = gpu(rng.standard_normal((300, 700)).astype(np.float32)), gpu(rng.standard_normal((700, 60)).astype(np.float32))
+    named = native.gemm(a, b, plan=("128x64", 4))
+    assert torch.equal(named, native.gemm(a, b, plan=("256x64", 4)))
+    lib, out = native._library(), torch.empty_like(named)
+    workspace = torch.empty(4 * 300 * 60, device="cuda")
+    for code in (16 + 32 + 3, 1024 + 128 + 3):
+        native._raise_for(lib.mfh_gemm(code, 0, 0, a.data_ptr(), b.data_ptr(), 0, out.data_ptr(), 300, 60, 700, 700, 60,
+                                       60, workspace.data_ptr(), workspace.numel(), torch.cuda.current_stream().cuda_stream), lib)
+        assert torch.equal(out, named)
+    assert [lib.mfh_gemm_tile_stages(i) for i in range(lib.mfh_gemm_tile_count())] == [2] * lib.mfh_gemm_tile_count()
+    assert lib.mfh_gemm_tile_stages(lib.mfh_gemm_tile_count()) == -1
+
+
 def teaching_kernels():
     for variant in ("basic", "tiled", "shared", "register"):
         for tile in ((32,) if variant in ("basic", "register") else (16, 32)):
