@@ -12,7 +12,9 @@ over the timed steps.
 "GEMM TFLOP/s vs FP32 peak"): algorithmic 2*M*N*K flop per launch divided by the average launch
 time measured with HIP events on the launch stream, against the 157.3 TFLOP/s FP32 matrix peak.
 ``cpu_baseline`` is the NumPy restatement of the reference CPU path (oracle/resnet.py) timed on this
-host on a bounded sample: full forward + backward + Adam steps of ResNet18 at batch 2 (config 1).
+host on a bounded sample: full forward + backward + Adam steps of ResNet18 at batch 2 (config 1);
+``cpu_reference_ops`` puts the same NumPy path's config 2 GEMMs (GFLOP/s) and config 3 convolution
+and max-pool operators (ms each) beside the GPU figures, with the cores and BLAS used.
 The other configurations are reported beside the headline: ``c2_gemms`` (the standalone GEMMs of
 config 2 against the FP32 matrix peak), ``c3_kernels`` (config 3's im2col and max-pool kernels
 against the HBM peak, its convolution against the matrix peak) and ``c5_inference`` (config 5,
@@ -208,10 +210,83 @@ def c3_kernels():
         us = _event_time_us(fn)
         gbs = nbytes / (us * 1e-6) / 1e9
         out[name] = {"us": round(us, 2), "bytes": nbytes, "GB/s": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 3)}
-    us = _event_time_us(conv_forward)
-    tflops = 2.0 * m * co * k / (us * 1e-6) / 1e12
-    out["conv_forward_implicit"] = {"us": round(us, 2), "TFLOP/s": round(tflops, 2),
-                                    "frac": round(tflops / FP32_MFMA_PEAK_TFLOPS, 3)}
+    dy = torch.randn((n, co, h, w), generator=g).cuda()
+    dxb = torch.empty_like(x)
+    dw = torch.empty_like(weight)
+    db = torch.empty(co, device="cuda")
+    wflip = native.conv_weight_orders([(weight, 1)])[0]
+    partial = torch.empty(max(n, native.BIAS_PARTIAL_ROWS) * co, dtype=torch.float64, device="cuda")
+    workspace = torch.empty(max(lib.mfh_conv_implicit_workspace(*dims, p) for p in (1, 2)) + 4, device="cuda")
+
+    def conv_dx():
+        native._raise_for(lib.mfh_conv_backward_implicit(
+            0, weight.data_ptr(), dy.data_ptr(), 0, 0, 0, dxb.data_ptr(), wflip.data_ptr(), 0, 0, 0, *dims, 0, 0.0,
+            1, 1, native.CONV_WFLIP_READY, workspace.data_ptr(), workspace.numel(), stream), lib)
+
+    def conv_dw():
+        native._raise_for(lib.mfh_conv_backward_implicit(
+            x.data_ptr(), weight.data_ptr(), dy.data_ptr(), 0, 0, dw.data_ptr(), 0, 0, 0, partial.data_ptr(),
+            db.data_ptr(), *dims, 0, 0.0, 1, 1, 0, workspace.data_ptr(), workspace.numel(), stream), lib)
+
+    for name, fn in (("conv_forward_implicit", conv_forward), ("conv_dx_implicit", conv_dx),
+                     ("conv_dw_implicit", conv_dw)):
+        us = _event_time_us(fn)
+        tflops = 2.0 * m * co * k / (us * 1e-6) / 1e12
+        out[name] = {"us": round(us, 2), "TFLOP/s": round(tflops, 2), "frac": round(tflops / FP32_MFMA_PEAK_TFLOPS, 3)}
+    return out
+
+
+def _median_seconds(fn, runs):
+    fn()  # warm-up
+    times = []
+    for _ in range(runs):
+        start = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - start)
+    return float(np.median(times))
+
+
+def _blas_name():
+    try:
+        info = np.show_config(mode="dicts")
+        return info.get("Build Dependencies", {}).get("blas", {}).get("name", "unknown")
+    except Exception:  # noqa: BLE001 - only a label
+        return "unknown"
+
+
+def cpu_reference_ops(runs=5):
+    """The reference's NumPy path beside the GPU figures of configs 2 and 3, on this host's cores:
+    float32 NumPy GEMMs (A, B ~ N(0, 1) seed 0) and config 3's convolution (im2col + GEMM forward,
+    dX through col2im, dW, FP64 db) and max-pool (window max with first-index mask, masked
+    scatter), each the median of `runs` runs after a warm-up."""
+    from oracle import reference_path as rp
+
+    out = {"cores": _CORES, "numpy": np.__version__, "blas": _blas_name(), "runs": runs, "c2_gemms": {}, "c3_ops_ms": {}}
+    rng = np.random.default_rng(0)
+    cases = [(f"{n}^3", n, n, n, False) for n in (512, 1024, 2048, 4096)]
+    cases += [("im2col 38400x64x576", 38400, 64, 576, False), ("dW A^T B 576x64 over 38400", 576, 64, 38400, True)]
+    for name, m, n, k, trans_a in cases:
+        a = rng.standard_normal((k, m) if trans_a else (m, k)).astype(np.float32)
+        b = rng.standard_normal((k, n)).astype(np.float32)
+        seconds = _median_seconds(lambda: (a.T if trans_a else a) @ b, runs if m * n * k <= 2048 ** 3 else 3)
+        out["c2_gemms"][name] = {"ms": round(seconds * 1e3, 3), "GFLOP/s": round(2.0 * m * n * k / seconds / 1e9, 1)}
+    x = rng.standard_normal((32, 64, 30, 40)).astype(np.float32)
+    w = (rng.standard_normal((64, 64, 3, 3)) * np.sqrt(2.0 / 576)).astype(np.float32)
+    b = np.zeros(64, np.float32)
+    y, cols = rp.conv2d_forward(x, w, b, (1, 1), (1, 1))
+    dy = rng.standard_normal(y.shape).astype(np.float32)
+    ops = out["c3_ops_ms"]
+    ops["conv_forward"] = _median_seconds(lambda: rp.conv2d_forward(x, w, b, (1, 1), (1, 1)), runs) * 1e3
+    ops["conv_dx"] = _median_seconds(lambda: rp.conv2d_backward(
+        x, w, dy, cols, (1, 1), (1, 1), need_weight_grad=False, need_bias_grad=False), runs) * 1e3
+    ops["conv_dw_db"] = _median_seconds(lambda: rp.conv2d_backward(
+        x, w, dy, cols, (1, 1), (1, 1), need_input_grad=False), runs) * 1e3
+    pooled, mask, padded = rp.maxpool2d_forward(y, (2, 2), (2, 2))
+    dp = rng.standard_normal(pooled.shape).astype(np.float32)
+    ops["pool_forward"] = _median_seconds(lambda: rp.maxpool2d_forward(y, (2, 2), (2, 2)), runs) * 1e3
+    ops["pool_backward"] = _median_seconds(lambda: rp.maxpool2d_backward(dp, mask, padded, (2, 2), (2, 2)), runs) * 1e3
+    for key in ops:
+        ops[key] = round(ops[key], 3)
     return out
 
 
@@ -288,12 +363,7 @@ def cpu_baseline(min_seconds=10.0, batch=2):
         elapsed = time.perf_counter() - start
         if elapsed >= min_seconds and steps >= 2:
             break
-    blas = "unknown"
-    try:
-        info = np.show_config(mode="dicts")
-        blas = info.get("Build Dependencies", {}).get("blas", {}).get("name", "unknown")
-    except Exception:  # noqa: BLE001 - only a label
-        pass
+    blas = _blas_name()
     return {"value": round(batch * steps / elapsed, 3), "unit": "images/s", "cores": _CORES, "kind": "port",
             "sample": f"{steps} ResNet18 train steps (fwd+bwd+Adam) at batch {batch}, 3x120x160, NumPy "
                       f"{np.__version__} ({blas}, {_CORES} threads), {elapsed:.1f} s"}
@@ -337,6 +407,7 @@ def main():
     }
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline()
+        result["cpu_reference_ops"] = cpu_reference_ops()
     print(json.dumps(result), flush=True)
     return 0
 
