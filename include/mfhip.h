@@ -58,6 +58,13 @@ MFH_API const char* mfh_info(void);
  * Replaces mf_set_debug_sync, native_cublas.cpp:1421-1423. */
 MFH_API void mfh_set_debug_sync(int enabled);
 
+/* Stream order: nothing issued on `waiting` after this call starts before all the work issued so
+ * far on `signalling` has finished (an event recorded on one, waited for by the other; the host
+ * does not block). Both are streams of the current device; the same stream twice is a no-op.
+ * No counterpart in the reference, whose operators run on one stream: for callers that issue work
+ * on a second stream, such as the dW products of a backward pass beside its dX products. */
+MFH_API int mfh_stream_wait(uint64_t waiting, uint64_t signalling);
+
 /* ---- convolution ---------------------------------------------------------------------------- */
 
 /* cols (N*OH*OW, CI*KH*KW) = im2col(x), zero outside the padded input.
@@ -170,6 +177,23 @@ MFH_API int mfh_conv_backward_implicit(uint64_t x, uint64_t weight, uint64_t dy,
                                        int OW, int SH, int SW, int PH, int PW, int activation, float alpha,
                                        int dw_engine, int dx_engine, int flags, uint64_t workspace,
                                        int64_t workspace_floats, uint64_t stream);
+
+/* mfh_conv_backward_implicit with the dW product (and db) on a second stream: dw_stream is first
+ * ordered after the work issued so far on `stream` (after the gating of dy, with a fused
+ * activation), the dW and db launches go to dw_stream and the dX launches to `stream`, so the two
+ * run side by side. The workspace holds the dW part (its first dw_workspace_floats, at least
+ * mfh_conv_implicit_workspace pass 1) followed by the dX part (at least pass 2). dw and db are
+ * complete once `stream` has been ordered after dw_stream (mfh_stream_wait(stream, dw_stream));
+ * every buffer must stay allocated until then. The results are bitwise those of the one-stream call.
+ * No counterpart in the reference (one stream per call): for a backward pass that runs the
+ * convolutions' dW products beside their dX products. */
+MFH_API int mfh_conv_backward_implicit_streams(uint64_t x, uint64_t weight, uint64_t dy, uint64_t y, uint64_t gated,
+                                               uint64_t dw, uint64_t dx, uint64_t wflip, uint64_t grad_cols,
+                                               uint64_t partial, uint64_t db, int N, int CI, int H, int W, int CO,
+                                               int KH, int KW, int OH, int OW, int SH, int SW, int PH, int PW,
+                                               int activation, float alpha, int dw_engine, int dx_engine, int flags,
+                                               uint64_t workspace, int64_t dw_workspace_floats,
+                                               int64_t workspace_floats, uint64_t stream, uint64_t dw_stream);
 
 /* ---- max pooling ---------------------------------------------------------------------------- */
 

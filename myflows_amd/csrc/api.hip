@@ -22,7 +22,12 @@ struct LibraryState {
     std::string info = "{}";
     // Device address of `scratch` on each device that mfh_init has set up (index: device id).
     std::vector<float*> scratch_address;
+    // Events of mfh_stream_wait, used in turn (a wait holds on to the record it was issued after).
+    std::vector<hipEvent_t> order_events;
+    unsigned next_order_event = 0;
 };
+
+constexpr int ORDER_EVENTS = 16;
 
 LibraryState& state() {
     static LibraryState s;
@@ -56,6 +61,20 @@ T* as_ptr(std::uint64_t address) {
 }
 
 hipStream_t as_stream(std::uint64_t handle) { return reinterpret_cast<hipStream_t>(static_cast<std::uintptr_t>(handle)); }
+
+// Nothing issued on `waiting` from now on starts before the work issued so far on `signalling` has
+// finished: an event of the ring recorded on one stream and waited for by the other.
+int order_after(hipStream_t waiting, hipStream_t signalling) {
+    if (waiting == signalling) return OK;
+    LibraryState& s = state();
+    std::lock_guard<std::mutex> guard(s.lock);
+    hipEvent_t event = s.order_events[s.next_order_event++ % s.order_events.size()];
+    hipError_t rc = hipEventRecord(event, signalling);
+    if (rc != hipSuccess) return MFH_FAIL(ERR_HIP, std::string("hipEventRecord: ") + hipGetErrorString(rc));
+    rc = hipStreamWaitEvent(waiting, event, 0);
+    if (rc != hipSuccess) return MFH_FAIL(ERR_HIP, std::string("hipStreamWaitEvent: ") + hipGetErrorString(rc));
+    return OK;
+}
 
 int require_ready() {
     LibraryState& s = state();
@@ -143,6 +162,65 @@ int column_gradient(int engine, const ConvGeometry& g, const float* weight, cons
     return gemm_launch(engine, stream, o, GemmEpilogue{}, nullptr, 0);
 }
 
+// The products of mfh_conv_backward_implicit: dW (and db) on dw_stream with the workspace
+// [ws_dw, ws_dw + dw_floats), dX on `stream` with [ws_dx, ws_dx + dx_floats). With two streams the
+// dW stream is first ordered after `stream` (after the gating of dy, when an activation is fused).
+int conv_backward_implicit(std::uint64_t x, std::uint64_t weight, std::uint64_t dy, std::uint64_t y,
+                           std::uint64_t gated, std::uint64_t dw, std::uint64_t dx, std::uint64_t wflip,
+                           std::uint64_t grad_cols, std::uint64_t partial, std::uint64_t db, const ConvGeometry& g,
+                           int activation, float alpha, int dw_engine, int dx_engine, int flags, float* ws_dw,
+                           std::int64_t dw_floats, float* ws_dx, std::int64_t dx_floats, hipStream_t s,
+                           hipStream_t dw_s) {
+    MFH_TRY(validate(g));
+    MFH_TRY(validate_activation(activation, alpha));
+    const bool gated_dy = activation != ACT_NONE;
+    const bool unit_stride = g.SH == 1 && g.SW == 1;
+    // dW and dX given wflip are implicit products (a strided dX as its phase products); a strided dX
+    // given grad_cols is a dense GEMM into the column gradient and col2im.
+    const bool phases = !unit_stride && wflip != 0;
+    MFH_REQUIRE(implicit_engine_valid(dw_engine), "unknown implicit convolution engine or plan code");
+    if (unit_stride || phases) MFH_REQUIRE(implicit_engine_valid(dx_engine), "unknown implicit convolution engine or plan code");
+    else MFH_TRY(validate_engine(dx_engine));
+    const bool prepared = (flags & MFH_CONV_WFLIP_READY) != 0, accumulate = (flags & MFH_CONV_ACCUMULATE_DX) != 0;
+    MFH_REQUIRE((flags & ~(MFH_CONV_WFLIP_READY | MFH_CONV_ACCUMULATE_DX)) == 0, "unknown conv backward flags");
+    MFH_REQUIRE(dy && (weight || ((unit_stride || phases) && prepared)), "conv backward needs weight and dy");
+    MFH_REQUIRE(!gated_dy || (y && gated), "a fused activation needs the forward output and the gated buffer");
+    MFH_REQUIRE((partial == 0) == (db == 0), "partial and db must be given together");
+    MFH_REQUIRE(!dw || x, "dW needs x");
+    MFH_REQUIRE(!dx || wflip != 0 || (!unit_stride && grad_cols != 0),
+                "dX needs wflip (any stride) or grad_cols (strides above 1)");
+    MFH_REQUIRE(dw_floats >= 0 && dx_floats >= 0, "workspace size must be non-negative");
+    const float* grad = as_ptr<const float>(dy);
+    const std::int64_t count = static_cast<std::int64_t>(g.N) * g.CO * g.ohw();
+    if (gated_dy) {
+        MFH_TRY(launch_relu_backward(as_ptr<const float>(y), grad, as_ptr<float>(gated), count,
+                                     activation == ACT_LEAKY_RELU ? alpha : 0.0f, false, s));
+        grad = as_ptr<const float>(gated);
+    }
+    double* bias_rows = as_ptr<double>(partial);
+    if (dw || db) MFH_TRY(order_after(dw_s, s));
+    if (dw) {
+        // db rides on the dW product: its first feature tile sums dy over each pixel slice, and
+        // the split-K reduction (or the product itself, when unsplit) finishes it.
+        MFH_TRY(conv_implicit_wgrad(g, as_ptr<const float>(x), grad, as_ptr<float>(dw), bias_rows, as_ptr<float>(db),
+                                    dw_engine, ws_dw, dw_floats, dw_s));
+    } else if (db) {
+        MFH_TRY(launch_row_sums(grad, bias_rows, g.N * g.CO, g.ohw(), dw_s));
+        MFH_TRY(launch_reduce_partials(bias_rows, as_ptr<float>(db), g.N, g.CO, dw_s));
+    }
+    if (!dx) return OK;
+    if (unit_stride)
+        return conv_implicit_dgrad(g, grad, as_ptr<const float>(weight), as_ptr<float>(wflip), prepared,
+                                   as_ptr<float>(dx), accumulate, dx_engine, ws_dx, dx_floats, s);
+    if (phases)
+        return conv_implicit_dgrad_phases(g, grad, as_ptr<const float>(weight), as_ptr<float>(wflip), prepared,
+                                          as_ptr<float>(dx), accumulate, dx_engine, ws_dx, dx_floats, s);
+    bool per_image = false;
+    MFH_TRY(column_gradient(dx_engine, g, as_ptr<const float>(weight), grad, nullptr, as_ptr<float>(grad_cols),
+                            &per_image, s));
+    return launch_col2im_t(as_ptr<const float>(grad_cols), as_ptr<float>(dx), g, per_image, accumulate, s);
+}
+
 }  // namespace
 
 int fail(int status, const char* file, int line, const std::string& what) {
@@ -193,6 +271,12 @@ MFH_API int mfh_init(void) {
         return MFH_FAIL(ERR_INIT, "libmfhip is built for gfx950 only; the current device is " + arch);
     MFH_TRY(probe_code_object());
     MFH_TRY(set_up_scratch(s, device));
+    for (int i = static_cast<int>(s.order_events.size()); i < ORDER_EVENTS; ++i) {
+        hipEvent_t event = nullptr;
+        rc = hipEventCreateWithFlags(&event, hipEventDisableTiming);
+        if (rc != hipSuccess) return MFH_FAIL(ERR_INIT, std::string("hipEventCreateWithFlags: ") + hipGetErrorString(rc));
+        s.order_events.push_back(event);
+    }
     const char* flag = std::getenv("MFHIP_SYNC");
     if (flag && flag[0] && flag[0] != '0') s.sync_each_launch = true;
     int runtime = 0;
@@ -209,6 +293,11 @@ MFH_API int mfh_init(void) {
     s.info = text;
     s.ready = true;
     return OK;
+}
+
+MFH_API int mfh_stream_wait(std::uint64_t waiting, std::uint64_t signalling) {
+    MFH_TRY(require_ready());
+    return order_after(as_stream(waiting), as_stream(signalling));
 }
 
 MFH_API int mfh_conv_im2col(std::uint64_t x, std::uint64_t cols, int N, int CI, int H, int W, int CO, int KH, int KW,
@@ -392,55 +481,27 @@ MFH_API int mfh_conv_backward_implicit(std::uint64_t x, std::uint64_t weight, st
                                        std::uint64_t workspace, std::int64_t workspace_floats, std::uint64_t stream) {
     MFH_TRY(require_ready());
     const ConvGeometry g{N, CI, H, W, CO, KH, KW, OH, OW, SH, SW, PH, PW};
-    MFH_TRY(validate(g));
-    MFH_TRY(validate_activation(activation, alpha));
-    const bool gated_dy = activation != ACT_NONE;
-    const bool unit_stride = SH == 1 && SW == 1;
-    // dW and dX given wflip are implicit products (a strided dX as its phase products); a strided dX
-    // given grad_cols is a dense GEMM into the column gradient and col2im.
-    const bool phases = !unit_stride && wflip != 0;
-    MFH_REQUIRE(implicit_engine_valid(dw_engine), "unknown implicit convolution engine or plan code");
-    if (unit_stride || phases) MFH_REQUIRE(implicit_engine_valid(dx_engine), "unknown implicit convolution engine or plan code");
-    else MFH_TRY(validate_engine(dx_engine));
-    const bool prepared = (flags & MFH_CONV_WFLIP_READY) != 0, accumulate = (flags & MFH_CONV_ACCUMULATE_DX) != 0;
-    MFH_REQUIRE((flags & ~(MFH_CONV_WFLIP_READY | MFH_CONV_ACCUMULATE_DX)) == 0, "unknown conv backward flags");
-    MFH_REQUIRE(dy && (weight || ((unit_stride || phases) && prepared)), "conv backward needs weight and dy");
-    MFH_REQUIRE(!gated_dy || (y && gated), "a fused activation needs the forward output and the gated buffer");
-    MFH_REQUIRE((partial == 0) == (db == 0), "partial and db must be given together");
-    MFH_REQUIRE(!dw || x, "dW needs x");
-    MFH_REQUIRE(!dx || wflip != 0 || (!unit_stride && grad_cols != 0),
-                "dX needs wflip (any stride) or grad_cols (strides above 1)");
-    MFH_REQUIRE(workspace_floats >= 0, "workspace size must be non-negative");
-    const hipStream_t s = as_stream(stream);
-    const float* grad = as_ptr<const float>(dy);
-    const std::int64_t count = static_cast<std::int64_t>(N) * CO * g.ohw();
-    if (gated_dy) {
-        MFH_TRY(launch_relu_backward(as_ptr<const float>(y), grad, as_ptr<float>(gated), count,
-                                     activation == ACT_LEAKY_RELU ? alpha : 0.0f, false, s));
-        grad = as_ptr<const float>(gated);
-    }
     float* ws = as_ptr<float>(workspace);
-    double* bias_rows = as_ptr<double>(partial);
-    if (dw) {
-        // db rides on the dW product: its first feature tile sums dy over each pixel slice, and
-        // the split-K reduction (or the product itself, when unsplit) finishes it.
-        MFH_TRY(conv_implicit_wgrad(g, as_ptr<const float>(x), grad, as_ptr<float>(dw), bias_rows, as_ptr<float>(db),
-                                    dw_engine, ws, workspace_floats, s));
-    } else if (db) {
-        MFH_TRY(launch_row_sums(grad, bias_rows, N * CO, g.ohw(), s));
-        MFH_TRY(launch_reduce_partials(bias_rows, as_ptr<float>(db), N, CO, s));
-    }
-    if (!dx) return OK;
-    if (unit_stride)
-        return conv_implicit_dgrad(g, grad, as_ptr<const float>(weight), as_ptr<float>(wflip), prepared,
-                                   as_ptr<float>(dx), accumulate, dx_engine, ws, workspace_floats, s);
-    if (phases)
-        return conv_implicit_dgrad_phases(g, grad, as_ptr<const float>(weight), as_ptr<float>(wflip), prepared,
-                                          as_ptr<float>(dx), accumulate, dx_engine, ws, workspace_floats, s);
-    bool per_image = false;
-    MFH_TRY(column_gradient(dx_engine, g, as_ptr<const float>(weight), grad, nullptr, as_ptr<float>(grad_cols),
-                            &per_image, s));
-    return launch_col2im_t(as_ptr<const float>(grad_cols), as_ptr<float>(dx), g, per_image, accumulate, s);
+    return conv_backward_implicit(x, weight, dy, y, gated, dw, dx, wflip, grad_cols, partial, db, g, activation, alpha,
+                                  dw_engine, dx_engine, flags, ws, workspace_floats, ws, workspace_floats,
+                                  as_stream(stream), as_stream(stream));
+}
+
+MFH_API int mfh_conv_backward_implicit_streams(
+    std::uint64_t x, std::uint64_t weight, std::uint64_t dy, std::uint64_t y, std::uint64_t gated, std::uint64_t dw,
+    std::uint64_t dx, std::uint64_t wflip, std::uint64_t grad_cols, std::uint64_t partial, std::uint64_t db, int N,
+    int CI, int H, int W, int CO, int KH, int KW, int OH, int OW, int SH, int SW, int PH, int PW, int activation,
+    float alpha, int dw_engine, int dx_engine, int flags, std::uint64_t workspace, std::int64_t dw_workspace_floats,
+    std::int64_t workspace_floats, std::uint64_t stream, std::uint64_t dw_stream) {
+    MFH_TRY(require_ready());
+    const ConvGeometry g{N, CI, H, W, CO, KH, KW, OH, OW, SH, SW, PH, PW};
+    MFH_REQUIRE(dw_workspace_floats >= 0 && dw_workspace_floats <= workspace_floats,
+                "the dW part of the workspace must lie within it");
+    float* ws = as_ptr<float>(workspace);
+    float* ws_dx = ws ? ws + dw_workspace_floats : nullptr;
+    return conv_backward_implicit(x, weight, dy, y, gated, dw, dx, wflip, grad_cols, partial, db, g, activation, alpha,
+                                  dw_engine, dx_engine, flags, ws, dw_workspace_floats, ws_dx,
+                                  workspace_floats - dw_workspace_floats, as_stream(stream), as_stream(dw_stream));
 }
 
 MFH_API int mfh_pool_forward(std::uint64_t x, std::uint64_t y, std::uint64_t argmax, int N, int C, int H, int W,

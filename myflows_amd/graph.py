@@ -13,7 +13,8 @@ Keeps the semantics of the reference's ``core/node.py:5-123`` and ``core/graph.p
   intermediates) an execution plan of which nodes need gradients; ``forward()`` in order,
   ``backward()`` in reverse seeded with ones; intermediate gradients are released as soon as their
   node has consumed them. Before each pass, the kernel reorders that the pass's implicit-GEMM
-  convolutions read are made by one native launch for all of them (``weight_orders``).
+  convolutions read are made by one native launch for all of them (``weight_orders``), and the
+  convolutions' dW products run on a second stream beside their dX products (``streams.py``).
 """
 
 from __future__ import annotations
@@ -21,6 +22,8 @@ from __future__ import annotations
 from dataclasses import dataclass
 
 import torch
+
+from . import streams
 
 
 class Node:
@@ -188,6 +191,9 @@ class Graph:
         if self._opt_stats is not None:
             self._opt_stats["bn_activation_fusions"] = len(self._bn_groups)
         self.profiler = None
+        # Whether backward() runs the convolutions' dW products on the weight-gradient stream
+        # (streams.py) beside their dX products; the gradients are the same either way.
+        self.overlap_weight_grads = True
         self._leaves = tuple(node for node in self.nodes if not node.parents)
         self._retained = set()
         self._plans = {}
@@ -264,19 +270,21 @@ class Graph:
         self.target_node.grad = torch.ones_like(seed) if loss_scale == 1.0 else torch.full_like(seed, loss_scale)
         profiler = self.profiler
         served = _prepare_weight_orders((unit for unit, _ in plan.backward_units), "backward")
-        for unit, output in plan.backward_units:
-            if output.grad is None:
-                continue
-            for parent in plan.pre_clear.get(unit, ()):
-                if parent.grad is None:  # a plain Node may add into parent.grad directly
-                    parent.clear_grad()
-            retained = output.grad if output in self._retained else None
-            if profiler is None:
-                unit.backward()
-            else:
-                with profiler.node(unit, "backward"):
+        overlap = self.overlap_weight_grads and isinstance(seed, torch.Tensor) and seed.is_cuda
+        with streams.weight_grad_overlap(overlap):
+            for unit, output in plan.backward_units:
+                if output.grad is None:
+                    continue
+                for parent in plan.pre_clear.get(unit, ()):
+                    if parent.grad is None:  # a plain Node may add into parent.grad directly
+                        parent.clear_grad()
+                retained = output.grad if output in self._retained else None
+                if profiler is None:
                     unit.backward()
-            output.grad = retained  # release the consumed intermediate gradient unless retained
+                else:
+                    with profiler.node(unit, "backward"):
+                        unit.backward()
+                output.grad = retained  # release the consumed intermediate gradient unless retained
         for unit in served:
             unit.drop_weight_orders("backward")
         for node in plan.keep:

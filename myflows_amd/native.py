@@ -83,6 +83,7 @@ _SIGNATURES = {
     "mfh_last_error": ("s", ""),
     "mfh_info": ("s", ""),
     "mfh_set_debug_sync": ("-", "i"),
+    "mfh_stream_wait": ("i", "pp"),
     "mfh_conv_im2col": ("i", "pp" + _CONV + "p"),
     "mfh_conv_forward": ("i", "pppppp" + _CONV + "ifipqp"),
     "mfh_conv_backward": ("i", "pppppppppp" + _CONV + "iifiipqp"),
@@ -90,6 +91,7 @@ _SIGNATURES = {
     "mfh_conv_weight_orders": ("i", "UUPip"),
     "mfh_conv_implicit_workspace": ("q", _CONV + "i"),
     "mfh_conv_backward_implicit": ("i", "ppppppppppp" + _CONV + "ifiiipqp"),
+    "mfh_conv_backward_implicit_streams": ("i", "ppppppppppp" + _CONV + "ifiiipqqpp"),
     "mfh_pool_forward": ("i", "ppp" + "i" * 10 + "p"),
     "mfh_pool_backward": ("i", "ppp" + "i" * 10 + "p"),
     "mfh_matmul": ("i", "iiipppp" + "iii" + "p"),
@@ -164,7 +166,27 @@ def _addr(tensor):
 
 
 def _stream():
-    return torch.cuda.current_stream().cuda_stream
+    """The raw handle (hipStream_t) of the current stream on the current device. torch's own
+    accessor is taken directly: torch.cuda.current_stream() costs several microseconds of Python
+    per call, paid for every launch."""
+    return _raw_stream(_current_device())
+
+
+try:
+    _raw_stream, _current_device = torch._C._cuda_getCurrentRawStream, torch._C._cuda_getDevice
+except AttributeError:  # another torch build: the public accessors
+    _raw_stream = lambda device: torch.cuda.current_stream(device).cuda_stream  # noqa: E731
+    _current_device = torch.cuda.current_device
+
+
+def current_device_index():
+    return _current_device()
+
+
+def stream_wait(waiting, signalling):
+    """Raw stream `waiting` runs nothing issued after this call before the work issued so far on
+    raw stream `signalling` has finished (mfh_stream_wait)."""
+    _call("mfh_stream_wait", waiting, signalling)
 
 
 def is_available():
@@ -532,7 +554,7 @@ def conv2d_forward(x, weight, bias=None, *, stride=(1, 1), padding=(0, 0), activ
 def conv2d_backward(x, weight, grad_y, cols, *, stride=(1, 1), padding=(0, 0), need_bias_grad=True,
                     need_input_grad=True, need_weight_grad=True, activation=None, alpha=0.0, output=None,
                     engine="mfma", recompute_cols=False, algorithm=None, weight_flip=None, input_grad=None,
-                    strided_dx="auto"):
+                    strided_dx="auto", dw_stream=None, hold=None):
     """(dx, dw, db), None for each gradient not requested; a fused activation gates grad_y through
     output. algorithm "im2col" computes dW from the forward's cols (recomputed from x when
     recompute_cols); "implicit" gathers them from x inside the GEMM. Without an algorithm, a call
@@ -543,7 +565,12 @@ def conv2d_backward(x, weight, grad_y, cols, *, stride=(1, 1), padding=(0, 0), n
     (one stride-1 implicit product per output phase, written to its lattice of dx), "columns" (the
     per-image column gradient GEMM and col2im) or "auto": phases for a 1x1 kernel (a single phase
     product), columns otherwise (measured on MI355X: the phases of a 3x3 kernel are small-K
-    products whose launches and split-K reductions cost more than the column path)."""
+    products whose launches and split-K reductions cost more than the column path).
+    Implicit only: dw_stream (a raw stream handle of the current device) runs the dW and db
+    products beside the dX product on the current stream (mfh_conv_backward_implicit_streams); dw
+    and db are complete once the current stream has been ordered after dw_stream (stream_wait). The
+    tensors are allocated on the current stream, so such a caller also passes a list as hold, which
+    receives every tensor the call reads or writes, and keeps them until that ordering."""
     engine = _engine_code(engine)
     if algorithm is None and cols is not None and not recompute_cols:
         algorithm = "im2col"
@@ -559,9 +586,9 @@ def conv2d_backward(x, weight, grad_y, cols, *, stride=(1, 1), padding=(0, 0), n
         phases = strided_dx == "phases" or (strided_dx == "auto"
                                             and strided_dx_phases(g.kh, g.kw, g.co, (g.sh, g.sw)))
         return _conv2d_backward_implicit(x, weight, grad_y, g, need_bias_grad, need_input_grad, need_weight_grad,
-                                         act, alpha, output, engine, weight_flip, input_grad, phases)
-    if weight_flip is not None or input_grad is not None:
-        raise ValueError("weight_flip and input_grad apply to the implicit algorithm only")
+                                         act, alpha, output, engine, weight_flip, input_grad, phases, dw_stream, hold)
+    if weight_flip is not None or input_grad is not None or dw_stream is not None or hold is not None:
+        raise ValueError("weight_flip, input_grad, dw_stream and hold apply to the implicit algorithm only")
     if need_weight_grad:
         cols = (conv2d_im2col(x, tuple(weight.shape), stride=stride, padding=padding) if recompute_cols
                 else _device_f32(cols, "cols"))
@@ -596,7 +623,10 @@ def conv2d_backward(x, weight, grad_y, cols, *, stride=(1, 1), padding=(0, 0), n
 
 
 def _conv2d_backward_implicit(x, weight, grad_y, g, need_bias_grad, need_input_grad, need_weight_grad, act, alpha,
-                              output, engine, weight_flip=None, input_grad=None, phases=True):
+                              output, engine, weight_flip=None, input_grad=None, phases=True, dw_stream=None,
+                              hold=None):
+    if dw_stream is not None and hold is None:
+        raise ValueError("a dW product on another stream needs a hold list for the call's tensors")
     gate = None
     if act:
         if output is None:
@@ -635,10 +665,22 @@ def _conv2d_backward_implicit(x, weight, grad_y, g, need_bias_grad, need_input_g
     partial = empty(max(g.n, BIAS_PARTIAL_ROWS) * g.co, dtype=torch.float64) if need_bias_grad else None
     db = empty(g.co) if need_bias_grad else None
     passes = (("dw",) if need_weight_grad else ()) + (("dx",) if need_input_grad and through_orders else ())
-    workspace, floats = _implicit_workspace(g, *passes)
-    _call("mfh_conv_backward_implicit", x.data_ptr(), weight.data_ptr(), grad_y.data_ptr(), _addr(gate),
-          _addr(gated), _addr(dw), _addr(dx), _addr(wflip), _addr(grad_cols), _addr(partial), _addr(db),
-          *g.c_args(), act, alpha, engine, engine, flags, _addr(workspace), floats, _stream())
+    pointers = (x.data_ptr(), weight.data_ptr(), grad_y.data_ptr(), _addr(gate), _addr(gated), _addr(dw), _addr(dx),
+                _addr(wflip), _addr(grad_cols), _addr(partial), _addr(db), *g.c_args(), act, alpha, engine, engine,
+                flags)
+    if dw_stream is None:
+        workspace, floats = _implicit_workspace(g, *passes)
+        _call("mfh_conv_backward_implicit", *pointers, _addr(workspace), floats, _stream())
+    else:  # the dW and dX products run at the same time: one workspace part each
+        dw_floats = _implicit_workspace_floats(g, "dw") if need_weight_grad else 0
+        dx_floats = _implicit_workspace_floats(g, "dx") if "dx" in passes else 0
+        floats = dw_floats + dx_floats
+        workspace = torch.empty(floats, dtype=torch.float32, device="cuda") if floats else None
+        _call("mfh_conv_backward_implicit_streams", *pointers, _addr(workspace), dw_floats, floats, _stream(),
+              dw_stream)
+    if hold is not None:
+        hold.extend(t for t in (x, weight, grad_y, gate, gated, dw, dx, wflip, grad_cols, partial, db, workspace)
+                    if t is not None)
     return dx, dw, db
 
 

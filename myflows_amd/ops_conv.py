@@ -14,7 +14,7 @@ import os
 
 import torch
 
-from . import native
+from . import native, streams
 from .device import get_device
 from .graph import GradientOp
 
@@ -34,7 +34,7 @@ def _resolve_backend(backend, *arrays):
     chosen = "hip_native" if backend == "auto" else backend
     if get_device() != "cuda":
         raise ValueError(f"backend={chosen} is incompatible with device={get_device()}")
-    current = torch.cuda.current_device() if torch.cuda.is_available() else None
+    current = native.current_device_index()
     for value in arrays:
         if value is None:
             continue
@@ -167,12 +167,28 @@ class Conv2D_Op(GradientOp):
             target = self._grad_target(x_node, x_val) if need_x else None
             if target is not None:  # dX is added to the gradient x already has, in the same pass
                 extra["input_grad"] = target
-        grads = native.conv2d_backward(
-            x_val, kernel_val, self.grad, cols, stride=self.stride, padding=self.padding, need_bias_grad=need_b,
-            need_weight_grad=need_w, need_input_grad=need_x,
-            activation=self.fused_activation if self._activation_fused else None, alpha=self._activation_alpha(),
-            output=self.value, engine=NATIVE_BACKENDS[self.actual_backend], recompute_cols=self.recompute_im2col,
-            **({"algorithm": "implicit"} if implicit else {}), **extra)
+        engine = NATIVE_BACKENDS[self.actual_backend]
+        session = streams.active()
+        if implicit and (need_w or need_b) and session is not None and session.usable():
+            # dW and db on the weight-gradient stream, dX on this one (the same products and plans as
+            # the one-stream call below)
+            side, hold = session.fork()
+            grads = native.conv2d_backward(
+                x_val, kernel_val, self.grad, None, stride=self.stride, padding=self.padding,
+                need_bias_grad=need_b, need_weight_grad=need_w, need_input_grad=need_x,
+                activation=self.fused_activation if self._activation_fused else None,
+                alpha=self._activation_alpha(), output=self.value, engine=engine, algorithm="implicit",
+                dw_stream=side, hold=hold, **extra)
+            if any(grad is not None and parent.grad is not None
+                   for parent, grad in zip(self.parents[1:], grads[1:])):
+                session.join()  # an existing gradient is added to on this stream
+        else:
+            grads = native.conv2d_backward(
+                x_val, kernel_val, self.grad, cols, stride=self.stride, padding=self.padding,
+                need_bias_grad=need_b, need_weight_grad=need_w, need_input_grad=need_x,
+                activation=self.fused_activation if self._activation_fused else None,
+                alpha=self._activation_alpha(), output=self.value, engine=engine,
+                recompute_cols=self.recompute_im2col, **({"algorithm": "implicit"} if implicit else {}), **extra)
         for parent, grad in zip(self.parents, grads):
             if grad is None or ("input_grad" in extra and parent is x_node):
                 continue

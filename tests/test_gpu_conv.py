@@ -605,3 +605,40 @@ def test_measured_plans_are_exact_on_integer_data(geometry):
         ref_dw = torch.nn.grad.conv2d_weight(x64, tuple(w_shape), dy64, stride=stride, padding=padding).numpy()
         np.testing.assert_array_equal(host(dw), ref_dw, err_msg=f"{name} dW")
     np.testing.assert_array_equal(host(db), dy64.sum(dim=(0, 2, 3)).numpy(), err_msg=f"{name} db")
+
+
+@pytest.mark.parametrize("shape,kernel,stride,padding,activation,in_place", [
+    ((4, 64, 15, 20), (64, 64, 3, 3), 1, 1, "relu", False),   # gated dy, stride-1 dX
+    ((4, 64, 15, 20), (128, 64, 3, 3), 2, 1, None, False),    # strided 3x3: column-gradient dX
+    ((4, 64, 15, 20), (128, 64, 1, 1), 2, 0, None, True),     # strided 1x1: phase dX, added in place
+    ((8, 512, 4, 5), (512, 512, 3, 3), 1, 1, None, True),     # split-K dW and dX at once
+    ((3, 3, 20, 18), (16, 3, 7, 7), 2, 3, None, False),       # natural-order stem gather
+])
+def test_weight_gradient_stream_call_gives_the_one_stream_bits(shape, kernel, stride, padding, activation,
+                                                               in_place):
+    """mfh_conv_backward_implicit_streams (dW and db on a second stream, dX on the current one)
+    against the one-stream call: dX, dW and db bit for bit once the current stream is ordered after
+    the second one; every buffer of the call is handed to the hold list."""
+    rng = np.random.default_rng(23)
+    x = gpu(rng.standard_normal(shape).astype(np.float32))
+    w = gpu((rng.standard_normal(kernel) * (2.0 / np.prod(kernel[1:])) ** 0.5).astype(np.float32))
+    b = gpu(rng.standard_normal(kernel[0]).astype(np.float32))
+    stride, padding = (stride, stride), (padding, padding)
+    y, _ = native.conv2d_forward(x, w, b, stride=stride, padding=padding, activation=activation,
+                                 algorithm="implicit")
+    dy = gpu(rng.standard_normal(tuple(y.shape)).astype(np.float32))
+    base = gpu(rng.standard_normal(shape).astype(np.float32))
+    side = torch.cuda.Stream()
+    results = []
+    for two_streams in (False, True):
+        extra = {"input_grad": base.clone()} if in_place else {}
+        hold = [] if two_streams else None
+        options = {"dw_stream": side.cuda_stream, "hold": hold} if two_streams else {}
+        grads = native.conv2d_backward(x, w, dy, None, stride=stride, padding=padding, activation=activation,
+                                       output=y, algorithm="implicit", **options, **extra)
+        if two_streams:
+            native.stream_wait(native._stream(), side.cuda_stream)
+            assert len(hold) >= 5 and all(isinstance(t, torch.Tensor) for t in hold)
+        results.append([host(g) for g in grads])
+    for got, want, name in zip(results[1], results[0], ("dx", "dw", "db")):
+        np.testing.assert_array_equal(got, want, err_msg=name)

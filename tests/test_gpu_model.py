@@ -249,6 +249,41 @@ def test_resnet18_two_steps_are_deterministic():
         np.testing.assert_array_equal(a, b)
 
 
+def test_weight_gradient_stream_gives_the_single_stream_gradients_bit_for_bit(monkeypatch):
+    """Graph.backward with the convolutions' dW products on the weight-gradient stream (the
+    default) against the same passes on one stream: the same bits for every gradient and every
+    updated parameter over two Adam steps at batch 8, and the stream is left joined and idle."""
+    from myflows_amd import streams
+
+    forks = []
+    original = streams.WeightGradSession.fork
+
+    def counting(self):
+        forks.append(1)
+        return original(self)
+
+    monkeypatch.setattr(streams.WeightGradSession, "fork", counting)
+    runs = []
+    for overlap in (False, True):
+        forks.clear()
+        model, graph, _, _, _, _ = build_resnet(8, 64, 80, base_width=16, optimize=True)
+        graph.overlap_weight_grads = overlap
+        opt = mf.Adam(graph, learning_rate=1e-3)
+        grads = []
+        for _ in range(2):
+            opt.one_step()
+            grads.append([host(p.grad) for p in model.params])
+            opt.update()
+        runs.append((grads, [host(p.value) for p in model.params], len(forks)))
+        assert streams.active() is None
+    assert runs[0][2] == 0 and runs[1][2] == 2 * 20  # ResNet18's 20 convolutions, two passes
+    for step_a, step_b in zip(runs[0][0], runs[1][0]):
+        for a, b in zip(step_a, step_b):
+            np.testing.assert_array_equal(a, b)
+    for a, b in zip(runs[0][1], runs[1][1]):
+        np.testing.assert_array_equal(a, b)
+
+
 def test_shared_weight_on_two_branches_accumulates():
     rng = np.random.default_rng(9)
     x_np = rng.standard_normal((2, 3, 10, 12)).astype(np.float32)
