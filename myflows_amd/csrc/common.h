@@ -228,7 +228,11 @@ struct ConvGather {
     int hw, chw;   // H * W, C * H * W
     int chunked;
     FastDiv div_ohw, div_ow, div_khkw, div_kw;
+    long long src_floats;  // N * C * H * W: the extent of src that the buffer loads may read
 };
+// The chunked implicit products read their operands with buffer loads, whose byte offsets are 32-bit:
+// each operand tensor they read must hold at most this many floats.
+constexpr std::int64_t BUFFER_LIMIT_FLOATS = 2147483647 / 4;
 constexpr int IMPLICIT_FORWARD = 0, IMPLICIT_WGRAD = 1, IMPLICIT_DGRAD = 2;
 // Split-K workspace floats of one pass of the implicit convolution under the automatic plan.
 std::int64_t implicit_workspace_floats(const ConvGeometry& g, int pass);

@@ -96,6 +96,65 @@ struct TileLoader {
     }
 };
 
+// Buffer loads (the raw buffer instructions of CDNA): a 128-bit resource in SGPRs holds the base
+// address and the byte extent of one tensor; each load adds a per-lane byte offset (VGPR) and a
+// wave-uniform one (SGPR). A lane whose offset lies past the extent reads zero without touching
+// memory, so a gather marks its out-of-image lanes with BUFFER_OOB instead of branching around the
+// load, and the address arithmetic that is the same for the whole wave stays in scalar registers.
+// The extent must fit in 31 bits (BUFFER_LIMIT_FLOATS); BUFFER_OOB then lies beyond every extent,
+// also after a wave-uniform offset inside the extent is added to it.
+constexpr unsigned BUFFER_OOB = 0x80000000u;
+constexpr int BUFFER_CONFIG = 0x00020000;  // resource word 3 for gfx9-family raw buffers (stride 0)
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_of(const float* base, long long floats) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(base), static_cast<short>(0),
+                                             static_cast<int>(floats * 4), BUFFER_CONFIG);
+}
+
+__device__ __forceinline__ float buffer_load(__amdgpu_buffer_rsrc_t r, unsigned lane_bytes, int wave_bytes) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, lane_bytes, wave_bytes, 0));
+}
+
+__device__ __forceinline__ float4 buffer_load4(__amdgpu_buffer_rsrc_t r, unsigned lane_bytes, int wave_bytes) {
+    return __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(r, lane_bytes, wave_bytes, 0));
+}
+
+// A ROWS x COLS tile of a row-major matrix (rows of length ld, `rows` of them) whose COLS columns
+// [col0, col0 + COLS) lie inside every row: float4 buffer loads, the column offset wave-uniform;
+// rows past the end read zero. COLS a multiple of 4, ld a multiple of 4, base 16-byte aligned.
+template <int ROWS, int COLS, int THREADS>
+struct BufferRowTile {
+    static constexpr int VCOLS = COLS / 4, ELEMS = ROWS * VCOLS;
+    static constexpr int PER_THREAD = (ELEMS + THREADS - 1) / THREADS;
+    __amdgpu_buffer_rsrc_t rsrc;
+    unsigned lane_bytes[PER_THREAD];
+    float4 v[PER_THREAD];
+
+    __device__ __forceinline__ void init(const float* base, int ld, int rows, int row0, int tid) {
+        rsrc = buffer_of(base, static_cast<long long>(rows) * ld);
+#pragma unroll
+        for (int i = 0; i < PER_THREAD; ++i) {
+            const int f = tid + i * THREADS;
+            const int row = row0 + f / VCOLS;
+            lane_bytes[i] = f < ELEMS && row < rows ? static_cast<unsigned>(row * ld + f % VCOLS * 4) * 4u : BUFFER_OOB;
+        }
+    }
+
+    __device__ __forceinline__ void load(int col0) {
+#pragma unroll
+        for (int i = 0; i < PER_THREAD; ++i) v[i] = buffer_load4(rsrc, lane_bytes[i], col0 * 4);
+    }
+
+    template <int LD>
+    __device__ __forceinline__ void store(float* lds, int tid) const {
+#pragma unroll
+        for (int i = 0; i < PER_THREAD; ++i) {
+            const int f = tid + i * THREADS;
+            if (f < ELEMS) *reinterpret_cast<float4*>(lds + f / VCOLS * LD + f % VCOLS * 4) = v[i];
+        }
+    }
+};
+
 __device__ __forceinline__ float activate(float v, int act, float alpha) {
     if (act == ACT_RELU) return v < 0.0f ? 0.0f : v;  // NaN stays NaN
     if (act == ACT_LEAKY_RELU) return v > 0.0f ? v : alpha * v;

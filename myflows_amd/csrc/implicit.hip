@@ -89,17 +89,24 @@ struct GatherFeatureRows {
 };
 
 // The same tile in chunked feature order: stage kt covers channels [c0, c0 + 32) at one tap. The
-// tap is uniform over the stage, so a wave may span two rows (BN a multiple of 32).
+// tap is uniform over the stage, so a wave may span two rows (BN a multiple of 32). The loads are
+// buffer loads: a lane's offset is its pixel's window origin plus the stage's (uniform) channel
+// chunk and tap, or BUFFER_OOB when the tap falls outside the image, and the PER channels of a
+// thread are a uniform stride apart. A stage then costs a handful of vector instructions besides
+// its loads, and the loads need no branches (the matrix cores and the vector ALU of a SIMD do not
+// run at the same time, so every vector instruction of the loop is time the MFMAs lose).
 template <int BN, int THREADS>
 struct GatherChunkRows {
     static_assert(BN % 32 == 0 && THREADS % BN == 0, "whole rows per thread group");
     static constexpr int RSTEP = THREADS / BN, PER = BK / RSTEP;
     static_assert(BK == CHANNEL_CHUNK && BK % RSTEP == 0, "one stage is one channel chunk");
-    int origin, ih0, iw0;
+    __amdgpu_buffer_rsrc_t rsrc;
+    int origin, ih0, iw0;  // origin: offset of channel tid / BN at window position (0, 0) (may be negative)
     bool valid;
     float v[PER];
 
     __device__ __forceinline__ void init(const ConvGather& g, int n0, int tid) {
+        rsrc = buffer_of(g.src, g.src_floats);
         const int q = n0 + tid % BN;
         valid = q < g.pixels;
         int rem, ow;
@@ -107,7 +114,7 @@ struct GatherChunkRows {
         const int oh = g.div_ow.divmod(rem, ow);
         ih0 = oh * g.SH - g.PH;
         iw0 = ow * g.SW - g.PW;
-        origin = n * g.chw + ih0 * g.W + iw0;
+        origin = n * g.chw + (tid / BN) * g.hw + ih0 * g.W + iw0;
     }
 
     __device__ __forceinline__ void load(const ConvGather& g, int kt, int k_end, int tid) {
@@ -117,15 +124,11 @@ struct GatherChunkRows {
         const int ih = ih0 + kh, iw = iw0 + kw;
         const bool ok = valid && kt < k_end && static_cast<unsigned>(ih) < static_cast<unsigned>(g.H) &&
                         static_cast<unsigned>(iw) < static_cast<unsigned>(g.W);
-        const int offset = origin + (chunk * CHANNEL_CHUNK + tid / BN) * g.hw + kh * g.W + kw;
-        const int step = RSTEP * g.hw;
-        if (ok) {
+        const int uniform = chunk * CHANNEL_CHUNK * g.hw + kh * g.W + kw;
+        const unsigned lane_bytes = ok ? static_cast<unsigned>(origin + uniform) * 4u : BUFFER_OOB;
+        const int step_bytes = RSTEP * g.hw * 4;
 #pragma unroll
-            for (int i = 0; i < PER; ++i) v[i] = g.src[offset + i * step];
-        } else {
-#pragma unroll
-            for (int i = 0; i < PER; ++i) v[i] = 0.0f;
-        }
+        for (int i = 0; i < PER; ++i) v[i] = buffer_load(rsrc, lane_bytes, i * step_bytes);
     }
 
     template <int LD>
@@ -278,11 +281,14 @@ __device__ __forceinline__ void implicit_forward_tile(const GemmParams& p, const
     const int k_end = p.split ? min(p.K, k_begin + p.k_chunk) : p.K;
     float* __restrict__ C = p.C + (p.split ? z * p.c_batch : 0);
 
-    TileLoader<BM, BK, S::THREADS, VA> la;
+    // Chunked products (K a multiple of BK) read the kernel order with buffer loads too.
+    std::conditional_t<CHUNKED, BufferRowTile<BM, BK, S::THREADS>, TileLoader<BM, BK, S::THREADS, VA>> la;
     std::conditional_t<CHUNKED, GatherChunkRows<BN, S::THREADS>, GatherFeatureRows<BN, S::THREADS>> lb;
+    if constexpr (CHUNKED) la.init(p.A, p.lda, p.M, m0, tid);
     lb.init(g, n0, tid);
     auto fetch = [&](int kt) {
-        la.load(p.A, p.lda, m0, p.M, kt, k_end, tid);
+        if constexpr (CHUNKED) la.load(kt);
+        else la.load(p.A, p.lda, m0, p.M, kt, k_end, tid);
         lb.load(g, kt, k_end, tid);
     };
     auto store = [&](float* a_lds, float* b_lds) {
@@ -635,6 +641,7 @@ ConvGather gather_of(const float* src, int C, int H, int W, int KH, int KW, int 
     g.OW = OW;
     g.pixels = N * OH * OW;
     g.features = C * KH * KW;
+    g.src_floats = static_cast<long long>(N) * C * H * W;
     g.hw = H * W;
     g.chw = C * H * W;
     g.chunked = implicit_chunked(C) ? 1 : 0;
@@ -823,6 +830,12 @@ void set_epilogue(GemmParams& p, float* c, int ldc, const GemmEpilogue& e) {
     p.plane_w = e.plane_w;
 }
 
+// Whether the operands of a chunked forward-orientation product fit the buffer loads' 31-bit
+// byte extents: the gathered source and the M x lda kernel order.
+bool buffer_extents_fit(const ConvGather& g, int M, int lda) {
+    return g.src_floats <= BUFFER_LIMIT_FLOATS && static_cast<std::int64_t>(M) * lda <= BUFFER_LIMIT_FLOATS;
+}
+
 // Runs one implicit product with the epilogue e (directly, or through split-K partials and the
 // FP64 slice reduction).
 int run_implicit(bool wgrad, const GemmPlan& plan, const float* a, int lda, int M, int N, int K, const ConvGather& g,
@@ -850,6 +863,8 @@ int run_implicit(bool wgrad, const GemmPlan& plan, const float* a, int lda, int 
     const bool vec_a = K % 4 == 0 && lda % 4 == 0 && aligned16(a);
     const int variant = g.chunked ? 2 : vec_a ? 1 : 0;
     if (!wgrad && g.chunked && !vec_a) return MFH_FAIL(ERR_ARG, "the reordered kernel buffer must be 16-byte aligned");
+    if (!wgrad && g.chunked && !buffer_extents_fit(g, M, lda))
+        return MFH_FAIL(ERR_ARG, "a chunked implicit convolution reads tensors of at most 2 GiB");
     if (wgrad)
         hipLaunchKernelGGL(conv_kernels().wgrad[plan.tile][row_out ? 1 : 0], grid, block, 0, stream, p, g, row_sums,
                            row_out);
@@ -1099,7 +1114,7 @@ int conv_implicit_dgrad_phases(const ConvGeometry& g, const float* dy, const flo
             batch.tiles_n[i] = static_cast<int>(blocks_for(N, t.bn));
             batch.first[i] = static_cast<int>(blocks);
             blocks += static_cast<std::int64_t>(blocks_for(M, t.bm)) * batch.tiles_n[i];
-            fits = fits && aligned16(p.A) && blocks <= INDEX_LIMIT;
+            fits = fits && aligned16(p.A) && blocks <= INDEX_LIMIT && buffer_extents_fit(batch.g[i], M, K);
         }
         if (fits && count > 0) {
             batch.first[count] = static_cast<int>(blocks);
