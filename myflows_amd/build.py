@@ -28,6 +28,12 @@ HIP_FLAGS = ["-O3", "-std=c++17", "-fPIC", f"--offload-arch={ARCH}", "-fvisibili
              "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops", "-Wno-unused-command-line-argument"]
 
 
+# Extra flags per translation unit. The implicit convolutions keep their MFMA accumulators in
+# ordinary VGPRs: their per-stage FP32 sums then read them without v_accvgpr_read copies (measured
+# on MI355X: the batch-64 layer1 products 3 % faster, the same bits).
+UNIT_FLAGS = {"implicit.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
+
+
 class BuildError(RuntimeError):
     pass
 
@@ -72,7 +78,7 @@ def build(verbose=False):
         for source in sources():
             obj = Path(work) / (source.stem + ".o")
             objects.append(obj)
-            commands.append([hipcc, *HIP_FLAGS, "-c", str(source), "-o", str(obj)])
+            commands.append([hipcc, *HIP_FLAGS, *UNIT_FLAGS.get(source.name, []), "-c", str(source), "-o", str(obj)])
         workers = max(1, min(len(commands), int(os.environ.get("MAX_JOBS", os.cpu_count() or 1))))
         with ThreadPoolExecutor(max_workers=workers) as pool:
             for command, _ in zip(commands, pool.map(_run, commands)):

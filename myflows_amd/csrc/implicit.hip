@@ -216,6 +216,56 @@ struct GatherPixelColumns {
     }
 };
 
+// The same tile in chunked feature order. The tile's BN feature rows are BN / 32 groups of 32
+// channels at one (chunk, tap); thread r of a pixel column (R = THREADS / BK_WG of them) takes group
+// r % G and the channels r / G + i * (R / G) of it, so the PER features of a thread share a tap: one
+// bounds test per stage, then PER buffer loads a uniform channel stride apart (out-of-image lanes
+// read zero), where the natural order tests every feature and branches around every load.
+template <int BN, int THREADS>
+struct GatherTapColumns {
+    static constexpr int R = THREADS / BK_WG, G = BN / 32, SPAN = R / G, PER = 32 / SPAN;
+    static_assert(BN % 32 == 0 && R % G == 0 && 32 % SPAN == 0, "a pixel column's threads split the groups evenly");
+    __amdgpu_buffer_rsrc_t rsrc;
+    int offset, kh, kw, row0;  // offset: element offset of the thread's first channel at tap (kh, kw)
+
+    __device__ __forceinline__ void init(const ConvGather& g, int n0, int tid) {
+        rsrc = buffer_of(g.src, g.src_floats);
+        const int r = tid / BK_WG, group = r % G, sub = r / G;
+        row0 = group * 32 + sub;
+        const int k = n0 + group * 32;  // the group's first feature
+        if (k < g.features) {
+            int tap;
+            const int chunk = g.div_khkw.divmod(k / CHANNEL_CHUNK, tap);
+            kh = g.div_kw.divmod(tap, kw);
+            offset = (chunk * CHANNEL_CHUNK + sub) * g.hw + kh * g.W + kw;
+        } else {  // past the last feature: every pixel is out of bounds
+            kh = FAR;
+            kw = 0;
+            offset = 0;
+        }
+    }
+
+    float v[PER];
+
+    __device__ __forceinline__ void load(const ConvGather& g, const PixelAt& at) {
+        const int ih = at.ih0 + kh, iw = at.iw0 + kw;
+        const bool ok = at.valid && static_cast<unsigned>(ih) < static_cast<unsigned>(g.H) &&
+                        static_cast<unsigned>(iw) < static_cast<unsigned>(g.W);
+        const unsigned lane =
+            ok ? static_cast<unsigned>(at.n * g.chw + at.ih0 * g.W + at.iw0 + offset) * 4u : BUFFER_OOB;
+        const int step_bytes = SPAN * g.hw * 4;
+#pragma unroll
+        for (int i = 0; i < PER; ++i) v[i] = buffer_load(rsrc, lane, i * step_bytes);
+    }
+
+    template <int LD>
+    __device__ __forceinline__ void store(float* lds, int tid) const {
+        const int col = tid % BK_WG;
+#pragma unroll
+        for (int i = 0; i < PER; ++i) lds[(row0 + i * SPAN) * LD + col] = v[i];
+    }
+};
+
 // dW's A operand: dy read in place, A[co][q] = dy[n, co, p] for pixel q = (n, p), as a BM x BK_WG
 // k-contiguous tile (rows = output channels, columns = the same pixels as the gathered tile).
 template <int BM, int THREADS>
@@ -340,7 +390,7 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void conv_implicit_grou
 // dW (CO x K) = dy (CO x pixels) . view^T (pixels x K), the pixel range split over z when p.split.
 // SUMS: the workgroups of feature tile 0 also sum each dy row over their pixel range in FP64, the
 // conv bias gradient: db[co] directly when unsplit, else sums[z * CO + co] for the reduction.
-template <int BM, int BN, int WM, int WN, bool SUMS>
+template <int BM, int BN, int WM, int WN, bool SUMS, bool CHUNKED>
 __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void conv_implicit_wgrad_kernel(GemmParams p, ConvGather g,
                                                                                         double* sums, float* db) {
     using S = MfmaShape<BM, BN, BK_WG, WM, WN, false, true>;
@@ -357,7 +407,7 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void conv_implicit_wgra
 
     using RowLoader = GradRowsInPlace<BM, S::THREADS>;
     RowLoader la;
-    GatherPixelColumns<BN, S::THREADS> lb;
+    std::conditional_t<CHUNKED, GatherTapColumns<BN, S::THREADS>, GatherPixelColumns<BN, S::THREADS>> lb;
     lb.init(g, n0, tid);
     const bool summing = SUMS && tile_n == 0;
     double row_sums[RowLoader::PER];
@@ -568,17 +618,17 @@ constexpr ConvFn forward_of() {
 using WgradFn = void (*)(GemmParams, ConvGather, double*, float*);
 using GroupedFn = void (*)(GroupedProducts);
 
-template <int T, bool SUMS>
+template <int T, bool SUMS, bool CHUNKED>
 constexpr WgradFn wgrad_of() {
     constexpr ImplicitTile t = TILE_TABLE[T];
-    return conv_implicit_wgrad_kernel<t.bm, t.bn, t.wm, t.wn, SUMS>;
+    return conv_implicit_wgrad_kernel<t.bm, t.bn, t.wm, t.wn, SUMS, CHUNKED>;
 }
 
 // forward[tile][0 | 1 | 2]: natural feature order with scalar / float4 A loads, chunked order;
-// wgrad[tile][0 | 1]: without / with the FP64 row sums of dy.
+// wgrad[tile][0 | 1][0 | 1]: without / with the FP64 row sums of dy; natural / chunked feature order.
 struct ConvKernels {
     ConvFn forward[TILE_COUNT][3] = {};
-    WgradFn wgrad[TILE_COUNT][2] = {};
+    WgradFn wgrad[TILE_COUNT][2][2] = {};
     GroupedFn grouped[TILE_COUNT] = {};  // chunked products only, tile 6 (the strided dX phases)
     template <int T>
     void fill() {
@@ -588,8 +638,10 @@ struct ConvKernels {
         }
         forward[T][2] = forward_of<T, true, true>();
         if constexpr (has_wgrad(TILE_TABLE[T])) {
-            wgrad[T][0] = wgrad_of<T, false>();
-            wgrad[T][1] = wgrad_of<T, true>();
+            wgrad[T][0][0] = wgrad_of<T, false, false>();
+            wgrad[T][1][0] = wgrad_of<T, true, false>();
+            wgrad[T][0][1] = wgrad_of<T, false, true>();
+            wgrad[T][1][1] = wgrad_of<T, true, true>();
         }
     }
     ConvKernels() {
@@ -831,7 +883,8 @@ void set_epilogue(GemmParams& p, float* c, int ldc, const GemmEpilogue& e) {
 }
 
 // Whether the operands of a chunked forward-orientation product fit the buffer loads' 31-bit
-// byte extents: the gathered source and the M x lda kernel order.
+// byte extents: the gathered source and the M x lda kernel order (a chunked dW product gathers
+// its source with buffer loads too).
 bool buffer_extents_fit(const ConvGather& g, int M, int lda) {
     return g.src_floats <= BUFFER_LIMIT_FLOATS && static_cast<std::int64_t>(M) * lda <= BUFFER_LIMIT_FLOATS;
 }
@@ -863,10 +916,11 @@ int run_implicit(bool wgrad, const GemmPlan& plan, const float* a, int lda, int 
     const bool vec_a = K % 4 == 0 && lda % 4 == 0 && aligned16(a);
     const int variant = g.chunked ? 2 : vec_a ? 1 : 0;
     if (!wgrad && g.chunked && !vec_a) return MFH_FAIL(ERR_ARG, "the reordered kernel buffer must be 16-byte aligned");
-    if (!wgrad && g.chunked && !buffer_extents_fit(g, M, lda))
+    if (g.chunked && (wgrad ? g.src_floats > BUFFER_LIMIT_FLOATS : !buffer_extents_fit(g, M, lda)))
         return MFH_FAIL(ERR_ARG, "a chunked implicit convolution reads tensors of at most 2 GiB");
     if (wgrad)
-        hipLaunchKernelGGL(conv_kernels().wgrad[plan.tile][row_out ? 1 : 0], grid, block, 0, stream, p, g, row_sums,
+        hipLaunchKernelGGL(conv_kernels().wgrad[plan.tile][row_out ? 1 : 0][g.chunked ? 1 : 0], grid, block, 0, stream,
+                           p, g, row_sums,
                            row_out);
     else
         hipLaunchKernelGGL(conv_kernels().forward[plan.tile][variant], grid, block, 0, stream, p, g);
