@@ -7,6 +7,7 @@ The public names mirror the reference package (``Variable``, ``Graph``, ``Conv2D
 """
 
 from . import fused, native
+from .capture import CapturedStep
 from .device import cuda_available, get_device, set_device
 from .fusion import apply_graph_optimizations
 from .graph import GradientOp, Graph, Node, Variable
@@ -20,7 +21,8 @@ from .optim import MBGD, Adam, Optimizer
 from .resnet import BasicBlock, BatchNorm2d, GlobalAvgPool2d, ResNet18
 
 __all__ = [
-    "Adam", "Add", "BACKENDS", "BasicBlock", "BatchNorm2d", "BatchNorm2d_Op", "BatchNormActivation", "Conv2D",
+    "Adam", "Add", "BACKENDS", "BasicBlock", "BatchNorm2d", "BatchNorm2d_Op", "BatchNormActivation",
+    "CapturedStep", "Conv2D",
     "Conv2D_AddReLU_Op", "Conv2D_LeakyReLU_Op", "Conv2D_Op", "Conv2D_ReLU_Op", "Dense", "Flatten", "Flatten_Op",
     "GlobalAvgPool2d", "GlobalAvgPool2d_Op", "GradientOp", "Graph", "LINEAR_BACKENDS", "Layer", "LeakyReLU", "Linear", "MBGD",
     "MSELoss", "MaxPool2d", "MaxPool2d_Op", "NATIVE_BACKENDS", "Node", "Optimizer", "ReLU", "ResNet18", "Variable",

@@ -276,8 +276,10 @@ __global__ __launch_bounds__(APPLY_THREADS) void norm_apply_kernel(ApplyArgs p) 
         __syncthreads();
         const int lo_e = max(e0, first * p.HW), hi_e = min(min(p.total, e0 + APPLY_SPAN), (last + 1) * p.HW);
         for (int e = lo_e + threadIdx.x * VEC; e < hi_e; e += APPLY_THREADS * VEC) {
-            const int i = p.div_hw.div(e) - first;  // all VEC elements share a plane (HW % VEC == 0)
-            const float m_hi = coef[0][i], m_lo = coef[1][i], istd = coef[2][i], g = coef[3][i], b = coef[4][i];
+            // The VEC elements' planes: i, then i + 1 from the element at `next` on (when H*W is
+            // not a multiple of VEC a float4 may cross into the next plane).
+            const int i = p.div_hw.div(e) - first;
+            const int next = (first + i + 1) * p.HW - e;
             float xv[VEC], rv[VEC] = {}, out[VEC];
             if constexpr (VEC == 4) {
                 const float4 x4 = *reinterpret_cast<const float4*>(p.x + e);
@@ -291,7 +293,10 @@ __global__ __launch_bounds__(APPLY_THREADS) void norm_apply_kernel(ApplyArgs p) 
                 if (p.residual) rv[0] = p.residual[e];
             }
 #pragma unroll
-            for (int u = 0; u < VEC; ++u) out[u] = apply_value(p, xv[u], rv[u], m_hi, m_lo, istd, g, b);
+            for (int u = 0; u < VEC; ++u) {
+                const int j = u < next ? i : i + 1;
+                out[u] = apply_value(p, xv[u], rv[u], coef[0][j], coef[1][j], coef[2][j], coef[3][j], coef[4][j]);
+            }
             if constexpr (VEC == 4) *reinterpret_cast<float4*>(p.y + e) = make_float4(out[0], out[1], out[2], out[3]);
             else p.y[e] = out[0];
         }
@@ -357,8 +362,8 @@ __global__ __launch_bounds__(APPLY_THREADS) void norm_dx_kernel(DxArgs p) {
         if (p.dx) {
             const int lo_e = max(e0, first * p.HW), hi_e = min(min(p.total, e0 + APPLY_SPAN), (last + 1) * p.HW);
             for (int e = lo_e + threadIdx.x * VEC; e < hi_e; e += APPLY_THREADS * VEC) {
-                const int i = p.div_hw.div(e) - first;
-                const float a = coef[0][i], k1 = coef[1][i], k2 = coef[2][i], m_hi = coef[3][i], m_lo = coef[4][i];
+                const int i = p.div_hw.div(e) - first;  // planes i and i + 1, as in norm_apply
+                const int next = (first + i + 1) * p.HW - e;
                 float xv[VEC], gv[VEC], tv[VEC] = {}, prev[VEC] = {};
                 if constexpr (VEC == 4) {
                     const float4 x4 = *reinterpret_cast<const float4*>(p.x + e);
@@ -381,7 +386,11 @@ __global__ __launch_bounds__(APPLY_THREADS) void norm_dx_kernel(DxArgs p) {
                 }
                 float out[VEC];
 #pragma unroll
-                for (int u = 0; u < VEC; ++u) out[u] = dx_value(p, xv[u], gv[u], tv[u], prev[u], a, k1, k2, m_hi, m_lo);
+                for (int u = 0; u < VEC; ++u) {
+                    const int j = u < next ? i : i + 1;
+                    out[u] = dx_value(p, xv[u], gv[u], tv[u], prev[u], coef[0][j], coef[1][j], coef[2][j], coef[3][j],
+                                      coef[4][j]);
+                }
                 if constexpr (VEC == 4)
                     *reinterpret_cast<float4*>(p.dx + e) = make_float4(out[0], out[1], out[2], out[3]);
                 else p.dx[e] = out[0];
@@ -513,6 +522,14 @@ int run_partials(int mode, const NormShape& s, const PartialArgs& args, hipStrea
 
 bool aligned16(const void* q) { return (reinterpret_cast<std::uintptr_t>(q) & 15) == 0; }
 
+// Whether the element passes can take float4s: every workgroup's span starts on a multiple of 4
+// (APPLY_SPAN is one) and is one round of planes (so its first element is the span's), and the
+// tensor's length is a multiple of 4. A float4 then lies in one plane or crosses into the next.
+bool vec4_spans(const NormShape& s) {
+    const std::int64_t total = static_cast<std::int64_t>(s.N) * s.C * s.HW;
+    return total % 4 == 0 && (s.HW % 4 == 0 || APPLY_SPAN / s.HW + 2 <= MAX_PLANES);
+}
+
 }  // namespace
 
 int norm_slices(const NormShape& s) {
@@ -562,7 +579,7 @@ int norm_forward(const NormShape& s, const NormForward& f, hipStream_t stream) {
     a.var_scale = f.var_scale;
     a.div_hw = FastDiv(s.HW);
     a.div_c = FastDiv(s.C);
-    const bool vec = s.HW % 4 == 0 && aligned16(f.x) && aligned16(f.y) && (!f.residual || aligned16(f.residual));
+    const bool vec = vec4_spans(s) && aligned16(f.x) && aligned16(f.y) && (!f.residual || aligned16(f.residual));
     if (f.training && slices == 1) {
         norm_forward_channel_kernel<<<s.C, PT, 0, stream>>>(args, a);
         return MFH_CHECK_LAUNCH("norm_forward_channel", stream);
@@ -617,7 +634,7 @@ int norm_backward(const NormShape& s, const NormBackward& b, hipStream_t stream)
     d.count = static_cast<double>(s.N) * s.HW;
     d.div_hw = FastDiv(s.HW);
     d.div_c = FastDiv(s.C);
-    const bool vec = s.HW % 4 == 0 && aligned16(b.x) && aligned16(b.dy) && (!b.gate || aligned16(b.gate)) &&
+    const bool vec = vec4_spans(s) && aligned16(b.x) && aligned16(b.dy) && (!b.gate || aligned16(b.gate)) &&
                      (!b.x_grad || aligned16(b.x_grad));
     if (fused) {
         norm_backward_channel_kernel<<<s.C, PT, 0, stream>>>(args, d);

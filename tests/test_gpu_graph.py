@@ -227,3 +227,60 @@ def test_stage1_cnn_trains_for_100_steps_on_the_reference_trajectory():
     assert np.mean(logits.argmax(1) == model["labels"]) >= 0.95
     assert np.mean(logits_ref.argmax(1) == model["labels"]) >= 0.95
     np.testing.assert_allclose(float(host(model["loss"].value)), float(loss_ref), **close)
+
+
+def _resnet_step(batch, seed=0):
+    model = mf.ResNet18(output_dim=2, base_width=16, initializer=mf.make_initializer(seed=seed),
+                        conv_backend="hip_native")
+    rng = np.random.default_rng(seed)
+    x = mf.Variable(gpu(rng.standard_normal((batch, 3, 48, 64)).astype(np.float32)), requires_grad=False)
+    t = mf.Variable(gpu(rng.uniform(-1, 1, (batch, 2)).astype(np.float32)), requires_grad=False)
+    loss = mf.MSELoss(model(x), t)
+    return mf.Adam(mf.Graph(loss, optimize=True), learning_rate=1e-3), loss, x, model
+
+
+def test_captured_step_replays_the_eager_step_bit_for_bit():
+    """CapturedStep (forward and backward recorded once as a HIP graph, both streams of the backward
+    in the recording) against the same network run eagerly: the loss and every parameter equal bit
+    for bit after each of four Adam steps, with eager work and a host synchronisation between the
+    replays and a new input batch copied in before the third."""
+    eager, loss_e, x_e, model_e = _resnet_step(2)
+    captured, loss_c, x_c, model_c = _resnet_step(2)
+    step = mf.CapturedStep(captured, warmup=2)
+    for _ in range(2):  # the recording's warm-up passes, which also move the BN running statistics
+        eager.graph.forward()
+        eager.graph.backward()
+    fresh = gpu(np.random.default_rng(9).standard_normal(tuple(x_e.value.shape)).astype(np.float32))
+    for k in range(4):
+        if k == 2:
+            x_e.value = fresh.clone()
+            x_c.value.copy_(fresh)
+        eager.one_step()
+        eager.update()
+        step.one_step()
+        step.update()
+        assert np.array_equal(host(loss_e.value), host(loss_c.value)), f"loss differs at step {k}"
+        for a, b in zip(model_e.params, model_c.params):
+            assert torch.equal(a.value, b.value), f"a parameter differs at step {k}"
+        torch.randn(8, device="cuda").sum().item()
+    assert step.replays == 4
+
+
+def test_captured_step_accumulates_gradients_over_several_replays():
+    """Two one_step() calls before update(): the captured step hands Adam the sum of both passes'
+    gradients, as the eager optimiser does (the recorded buffers are copied before the second replay
+    overwrites them)."""
+    eager, _, _, model_e = _resnet_step(2, seed=1)
+    captured, _, _, model_c = _resnet_step(2, seed=1)
+    step = mf.CapturedStep(captured, warmup=1)
+    eager.graph.forward()
+    eager.graph.backward()
+    for _ in range(2):
+        eager.one_step()
+        step.one_step()
+    for a, b in zip(model_e.params, model_c.params):
+        assert torch.equal(eager.acc_gradient[a], captured.acc_gradient[b])
+    eager.update()
+    step.update()
+    for a, b in zip(model_e.params, model_c.params):
+        assert torch.equal(a.value, b.value)
