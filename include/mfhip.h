@@ -297,6 +297,32 @@ MFH_API int mfh_bn_backward(uint64_t x, uint64_t dy, uint64_t gate, uint64_t gam
                             uint64_t workspace, int64_t workspace_doubles, int N, int C, int HW, int training,
                             int add_x, int add_gamma, int add_beta, int add_residual, uint64_t stream);
 
+/* Batch norm + ReLU + max-pool (KH x KW window, stride SH x SW, no padding) as one unit, for a
+ * network stem: the ReLU output is never stored. Returns 1 when the fused kernels take this shape
+ * (their LDS staging of a plane fits), else 0.
+ * No counterpart in the reference (there, BatchNormActivation's output feeds MaxPool2d_Op):
+ * it spares the ReLU output's HBM round trip and the max-pool's passes. */
+MFH_API int mfh_bn_relu_pool_supported(int N, int C, int H, int W, int KH, int KW, int SH, int SW);
+
+/* mfh_bn_forward with relu (no residual) followed by mfh_pool_forward on its output: pooled and
+ * argmax (N, C, OH, OW) with OH = (H - KH) / SH + 1, argmax the int32 flat index into the
+ * N x C x H x W tensor. mean / inv_std / running statistics and workspace as mfh_bn_forward.
+ * The same bits as those two calls. */
+MFH_API int mfh_bn_relu_pool_forward(uint64_t x, uint64_t gamma, uint64_t beta, uint64_t running_mean,
+                                     uint64_t running_var, uint64_t pooled, uint64_t argmax, uint64_t mean,
+                                     uint64_t inv_std, uint64_t workspace, int64_t workspace_doubles, int N, int C,
+                                     int H, int W, int KH, int KW, int SH, int SW, int training, double momentum,
+                                     double eps, double var_scale, uint64_t stream);
+
+/* The unit's backward from the pooled gradient: mfh_pool_backward into the ReLU output's gradient,
+ * gated by the ReLU (recomputed from x, mean, inv_std, gamma and beta), then mfh_bn_backward, with
+ * the same bits and add_* flags; nothing of the ReLU output's size is written but x_grad. */
+MFH_API int mfh_bn_relu_pool_backward(uint64_t x, uint64_t pooled_grad, uint64_t argmax, uint64_t gamma,
+                                      uint64_t beta, uint64_t mean, uint64_t inv_std, uint64_t x_grad,
+                                      uint64_t gamma_grad, uint64_t beta_grad, uint64_t workspace,
+                                      int64_t workspace_doubles, int N, int C, int H, int W, int KH, int KW, int SH,
+                                      int SW, int training, int add_x, int add_gamma, int add_beta, uint64_t stream);
+
 /* ---- activations and the optimiser ---------------------------------------------------------- */
 
 /* y = max(0, x) over count elements (NaN stays NaN).

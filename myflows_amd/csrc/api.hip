@@ -734,6 +734,94 @@ MFH_API int mfh_bn_backward(std::uint64_t x, std::uint64_t dy, std::uint64_t gat
     return norm_backward(s, b, as_stream(stream));
 }
 
+namespace {
+
+// The unit's shapes: a training or eval batch norm over N x C x H x W, then a KH x KW / (SH, SW)
+// max-pool without padding.
+int pool_unit_shapes(int N, int C, int H, int W, int KH, int KW, int SH, int SW, NormShape* s, PoolDims* d) {
+    MFH_REQUIRE(N > 0 && C > 0 && H > 0 && W > 0, "batch-norm + max-pool dimensions must be positive");
+    MFH_REQUIRE(KH > 0 && KW > 0 && SH > 0 && SW > 0 && KH <= H && KW <= W,
+                "max-pool window and stride must be positive and the window inside the input");
+    MFH_REQUIRE(fits_index(static_cast<std::int64_t>(N) * C * H * W), "tensor exceeds int32 element offsets");
+    *s = NormShape{N, C, H * W};
+    *d = PoolDims{H, W, (H - KH) / SH + 1, (W - KW) / SW + 1, KH, KW, SH, SW};
+    return validate_norm(*s);
+}
+
+}  // namespace
+
+MFH_API int mfh_bn_relu_pool_supported(int N, int C, int H, int W, int KH, int KW, int SH, int SW) {
+    NormShape s;
+    PoolDims d;
+    if (require_ready() != OK || pool_unit_shapes(N, C, H, W, KH, KW, SH, SW, &s, &d) != OK) return 0;
+    return norm_pool_supported(s, d) ? 1 : 0;
+}
+
+MFH_API int mfh_bn_relu_pool_forward(std::uint64_t x, std::uint64_t gamma, std::uint64_t beta,
+                                     std::uint64_t running_mean, std::uint64_t running_var, std::uint64_t pooled,
+                                     std::uint64_t argmax, std::uint64_t mean, std::uint64_t inv_std,
+                                     std::uint64_t workspace, std::int64_t workspace_doubles, int N, int C, int H, int W,
+                                     int KH, int KW, int SH, int SW, int training, double momentum, double eps,
+                                     double var_scale, std::uint64_t stream) {
+    MFH_TRY(require_ready());
+    NormShape s;
+    PoolDims d;
+    MFH_TRY(pool_unit_shapes(N, C, H, W, KH, KW, SH, SW, &s, &d));
+    MFH_REQUIRE(x && gamma && beta && running_mean && running_var && pooled && argmax && mean && inv_std,
+                "batch-norm + max-pool forward received a null buffer");
+    MFH_REQUIRE(!training || (workspace && workspace_doubles >= norm_workspace_doubles(s)),
+                "batch-norm workspace is smaller than mfh_bn_workspace");
+    MFH_REQUIRE(!training || (workspace & 15) == 0, "batch-norm workspace must be 16-byte aligned");
+    MFH_REQUIRE(eps >= 0.0 && momentum >= 0.0 && momentum <= 1.0, "batch-norm eps and momentum are out of range");
+    NormForward f{};
+    f.x = as_ptr<const float>(x);
+    f.gamma = as_ptr<const float>(gamma);
+    f.beta = as_ptr<const float>(beta);
+    f.running_mean = as_ptr<float>(running_mean);
+    f.running_var = as_ptr<float>(running_var);
+    f.mean = as_ptr<float>(mean);
+    f.inv_std = as_ptr<float>(inv_std);
+    f.partial = as_ptr<double>(workspace);
+    f.training = training != 0;
+    f.relu = true;
+    f.momentum = momentum;
+    f.eps = eps;
+    f.var_scale = var_scale;
+    return norm_relu_pool_forward(s, f, d, as_ptr<float>(pooled), as_ptr<int>(argmax), as_stream(stream));
+}
+
+MFH_API int mfh_bn_relu_pool_backward(std::uint64_t x, std::uint64_t pooled_grad, std::uint64_t argmax,
+                                      std::uint64_t gamma, std::uint64_t beta, std::uint64_t mean,
+                                      std::uint64_t inv_std, std::uint64_t x_grad, std::uint64_t gamma_grad,
+                                      std::uint64_t beta_grad, std::uint64_t workspace, std::int64_t workspace_doubles,
+                                      int N, int C, int H, int W, int KH, int KW, int SH, int SW, int training,
+                                      int add_x, int add_gamma, int add_beta, std::uint64_t stream) {
+    MFH_TRY(require_ready());
+    NormShape s;
+    PoolDims d;
+    MFH_TRY(pool_unit_shapes(N, C, H, W, KH, KW, SH, SW, &s, &d));
+    MFH_REQUIRE(x && pooled_grad && argmax && gamma && beta && mean && inv_std,
+                "batch-norm + max-pool backward received a null buffer");
+    MFH_REQUIRE(workspace && workspace_doubles >= norm_workspace_doubles(s),
+                "batch-norm workspace is smaller than mfh_bn_workspace");
+    MFH_REQUIRE((workspace & 15) == 0, "batch-norm workspace must be 16-byte aligned");
+    NormBackward b{};
+    b.x = as_ptr<const float>(x);
+    b.gamma = as_ptr<const float>(gamma);
+    b.mean = as_ptr<const float>(mean);
+    b.inv_std = as_ptr<const float>(inv_std);
+    b.x_grad = as_ptr<float>(x_grad);
+    b.gamma_grad = as_ptr<float>(gamma_grad);
+    b.beta_grad = as_ptr<float>(beta_grad);
+    b.partial = as_ptr<double>(workspace);
+    b.training = training != 0;
+    b.add_x = add_x != 0;
+    b.add_gamma = add_gamma != 0;
+    b.add_beta = add_beta != 0;
+    return norm_relu_pool_backward(s, b, d, as_ptr<const float>(pooled_grad), as_ptr<const int>(argmax),
+                                   as_ptr<const float>(beta), as_stream(stream));
+}
+
 MFH_API int mfh_relu_forward(std::uint64_t x, std::uint64_t y, std::int64_t count, std::uint64_t stream) {
     MFH_TRY(require_ready());
     MFH_REQUIRE(count >= 0, "element count must be non-negative");

@@ -354,6 +354,19 @@ struct NormBackward {
 };
 int norm_backward(const NormShape& s, const NormBackward& b, hipStream_t stream);
 
+// Batch norm + ReLU + max-pool (no padding) as one unit; the ReLU output is never stored. The
+// forward writes the pooled values and their int32 flat argmax into the N x C x H x W tensor, the
+// backward takes the pooled gradient and that argmax (NormBackward's dy, gate and residual fields
+// are unused). Same bits as norm_forward with relu, the max-pool, and their backward passes.
+struct PoolDims {
+    int H, W, OH, OW, KH, KW, SH, SW;
+};
+bool norm_pool_supported(const NormShape& s, const PoolDims& d);
+int norm_relu_pool_forward(const NormShape& s, const NormForward& f, const PoolDims& d, float* pooled, int* argmax,
+                           hipStream_t stream);
+int norm_relu_pool_backward(const NormShape& s, const NormBackward& b, const PoolDims& d, const float* pooled_grad,
+                            const int* argmax, const float* beta, hipStream_t stream);
+
 // ---- pointwise.hip ----------------------------------------------------------------------------
 int launch_relu_forward(const float* x, float* y, std::int64_t count, hipStream_t stream);
 // p[0 .. count) = 0 (a kernel, not a memset, so that it may sit in a captured graph)

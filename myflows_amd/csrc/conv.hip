@@ -11,6 +11,7 @@
 
 #include "common.h"
 #include "fastdiv.h"
+#include "pool_rules.h"
 
 namespace mfh {
 namespace {
@@ -371,39 +372,12 @@ __global__ __launch_bounds__(256) void pool_forward_plane_kernel(const float* __
         const int pl = div_ohw.divmod(o, within);
         const int oh = div_ow.divmod(within, ow);
         const int first = pl * hw + oh * SH * W + ow * SW;  // LDS index of the window's first element
-        int best = first;
-        float value = tile[first];
-        for (int kh = 0; kh < KH; ++kh)
-            for (int kw = 0; kw < KW; ++kw) {
-                const float v = tile[first + kh * W + kw];
-                if (v > value || v != v) {
-                    value = v;
-                    best = first + kh * W + kw;
-                }
-            }
+        int best;
+        const float value = window_max(tile, first, W, KH, KW, best);
         const long long out = static_cast<long long>(first_plane) * ohw + o;
         y[out] = value;
         argmax[out] = static_cast<int>(base + best);
     }
-}
-
-// The gradient of input pixel (ih, iw) of staged plane pl: the dy of every window that covers the
-// pixel and whose argmax is it, added in (oh, ow) order.
-__device__ __forceinline__ float pool_pixel_grad(const float* grad, const int* where, int pl, int ih, int iw,
-                                                 int target, int OH, int OW, int KH, int KW, const FastDiv& div_sh,
-                                                 const FastDiv& div_sw) {
-    const int ohw = OH * OW;
-    const int oh_lo = ih >= KH ? div_sh.div(ih - KH) + 1 : 0;
-    const int oh_hi = min(OH - 1, div_sh.div(ih));
-    const int ow_lo = iw >= KW ? div_sw.div(iw - KW) + 1 : 0;
-    const int ow_hi = min(OW - 1, div_sw.div(iw));
-    float sum = 0.0f;
-    for (int oh = oh_lo; oh <= oh_hi; ++oh)
-        for (int ow = ow_lo; ow <= ow_hi; ++ow) {
-            const int o = pl * ohw + oh * OW + ow;
-            if (where[o] == target) sum += grad[o];
-        }
-    return sum;
 }
 
 // Max-pool backward over `per` consecutive planes per workgroup: the planes' dy and argmax are

@@ -22,6 +22,7 @@
 // sums, the finalisation and the element pass in a row, with the arithmetic of the two-launch path.
 #include "common.h"
 #include "fastdiv.h"
+#include "pool_rules.h"
 
 namespace mfh {
 namespace {
@@ -42,6 +43,7 @@ struct PartialArgs {
     const float* dy;
     const float* gate;
     const float* mean;
+    const float* inv_std;  // the forward's, for a gate recomputed from x (norm_partials_pool_kernel)
     float* residual_grad;
     double* partial;
     int C, HW, total, chunk;
@@ -237,13 +239,21 @@ __device__ __forceinline__ void store_statistics(const ApplyArgs& p, int c, cons
     }
 }
 
+// (((x - hi) - lo) * inv_std) * gamma + beta, rounded per operation.
+__device__ __forceinline__ float affine_value(float x, float m_hi, float m_lo, float istd, float g, float b) {
+#pragma clang fp contract(off)
+    return (((x - m_hi) - m_lo) * istd) * g + b;
+}
+
+__device__ __forceinline__ float relu_value(float v) { return v < 0.0f ? 0.0f : v; }  // NaN stays NaN
+
 // y = (((x - hi) - lo) * inv_std) * gamma + beta [+ residual] [ReLU], rounded per operation.
 __device__ __forceinline__ float apply_value(const ApplyArgs& p, float x, float r, float m_hi, float m_lo, float istd,
                                              float g, float b) {
 #pragma clang fp contract(off)
-    float v = (((x - m_hi) - m_lo) * istd) * g + b;
+    float v = affine_value(x, m_hi, m_lo, istd, g, b);
     if (p.residual) v = v + r;
-    if (p.relu) v = v < 0.0f ? 0.0f : v;  // NaN stays NaN
+    if (p.relu) v = relu_value(v);
     return v;
 }
 
@@ -326,12 +336,18 @@ __device__ __forceinline__ void store_param_grads(const DxArgs& p, int c, const 
     if (p.beta_grad) p.beta_grad[c] = p.add_beta ? p.beta_grad[c] + static_cast<float>(sdy) : static_cast<float>(sdy);
 }
 
-__device__ __forceinline__ float dx_value(const DxArgs& p, float x, float dy, float gate, float prev, float a, float k1,
-                                          float k2, float m_hi, float m_lo) {
+// dx of one element from its (already gated) output gradient g.
+__device__ __forceinline__ float dx_of_gated(const DxArgs& p, float x, float g, float prev, float a, float k1, float k2,
+                                             float m_hi, float m_lo) {
 #pragma clang fp contract(off)
-    const float g = p.gate && !(gate > 0.0f) ? 0.0f : dy;
     const float v = p.training ? a * ((g - k1) - ((x - m_hi) - m_lo) * k2) : a * g;
     return p.add ? prev + v : v;
+}
+
+__device__ __forceinline__ float dx_value(const DxArgs& p, float x, float dy, float gate, float prev, float a, float k1,
+                                          float k2, float m_hi, float m_lo) {
+    const float g = p.gate && !(gate > 0.0f) ? 0.0f : dy;
+    return dx_of_gated(p, x, g, prev, a, k1, k2, m_hi, m_lo);
 }
 
 // norm_dx with dgamma / dbeta and the dx coefficients finalised in the workgroup.
@@ -513,6 +529,197 @@ __global__ __launch_bounds__(PT) void norm_backward_channel_kernel(PartialArgs p
     }
 }
 
+// ---- Batch norm + ReLU + max-pool as one unit (a stem: conv -> BN -> ReLU -> max-pool) ----------
+// The ReLU output y is never stored. Forward: after norm_partials<STATS>, one workgroup per (n, c)
+// plane normalises the plane into LDS with norm_apply's arithmetic and pools it there with the
+// pooling kernels' window rule (argmax = flat index into the N x C x H x W tensor y would be).
+// Backward: the pooled gradient and argmax of the planes a workgroup covers are staged in LDS; each
+// element's gradient is the pooling backward's sum (pool_pixel_grad), gated by ReLU(BN(x)) > 0
+// recomputed from x with the forward's coefficients (the same float operations as the stored y).
+// The partial sums run over the slices and chains of norm_partials<GRADS> and the dx pass uses
+// norm_dx's arithmetic, so the unit gives the bits of the separate BN+ReLU and max-pool passes.
+struct PoolShape {
+    int H, W, OH, OW, KH, KW, SH, SW;
+    FastDiv div_ow, div_w, div_sh, div_sw;
+};
+
+struct PoolGrad {
+    const float* dy;    // (N, C, OH, OW) gradient of the pooled output
+    const int* argmax;  // (N, C, OH, OW) flat indices into x's shape
+    const float* gamma;
+    const float* beta;
+};
+
+constexpr int POOL_STAGE_FLOATS = 16384;  // LDS floats a fused workgroup may stage (64 KB)
+
+// Stages planes [n_lo, n_lo + count) of channel c: their pooled gradient, then their argmax.
+__device__ __forceinline__ void stage_pool_grads(const PoolGrad& g, int C, int c, int ohw, int n_lo, int count,
+                                                 float* grad, int* where) {
+    const int total = count * ohw;
+    for (int k = threadIdx.x; k < total; k += blockDim.x) {
+        const int n = n_lo + k / ohw, o = k - (k / ohw) * ohw;
+        const long long at = (static_cast<long long>(n) * C + c) * ohw + o;
+        grad[k] = g.dy[at];
+        where[k] = g.argmax[at];
+    }
+}
+
+// Forward: one workgroup per plane pl = n * C + c; y of the plane in LDS, then the pooled plane.
+__global__ __launch_bounds__(APPLY_THREADS) void norm_apply_pool_kernel(ApplyArgs p, PoolShape q, float* __restrict__ pooled,
+                                                                      int* __restrict__ argmax, int vec) {
+#pragma clang fp contract(off)
+    extern __shared__ float plane_y[];  // H * W floats
+    __shared__ float coef[3];
+    const int pl = blockIdx.x;
+    int c;
+    p.div_c.divmod(pl, c);
+    if (threadIdx.x == 0) {
+        double sum = 0.0, sq = 0.0;
+        if (p.training) slice_sums(p.partial, c, p.slices, sum, sq);
+        const ApplyCoef k = apply_coef(p, c, sum, sq);
+        coef[0] = k.hi;
+        coef[1] = k.lo;
+        coef[2] = k.istd;
+        if (pl < p.C) store_statistics(p, c, k);  // image 0's plane: once per channel
+    }
+    __syncthreads();
+    const float m_hi = coef[0], m_lo = coef[1], istd = coef[2], g = p.gamma[c], b = p.beta[c];
+    const long long base = static_cast<long long>(pl) * p.HW;
+    if (vec) {  // H*W % 4 == 0 and x 16-byte aligned
+        for (int e = 4 * threadIdx.x; e < p.HW; e += 4 * APPLY_THREADS) {
+            const float4 x4 = *reinterpret_cast<const float4*>(p.x + base + e);
+            plane_y[e] = relu_value(affine_value(x4.x, m_hi, m_lo, istd, g, b));
+            plane_y[e + 1] = relu_value(affine_value(x4.y, m_hi, m_lo, istd, g, b));
+            plane_y[e + 2] = relu_value(affine_value(x4.z, m_hi, m_lo, istd, g, b));
+            plane_y[e + 3] = relu_value(affine_value(x4.w, m_hi, m_lo, istd, g, b));
+        }
+    } else {
+        for (int e = threadIdx.x; e < p.HW; e += APPLY_THREADS)
+            plane_y[e] = relu_value(affine_value(p.x[base + e], m_hi, m_lo, istd, g, b));
+    }
+    __syncthreads();
+    const int ohw = q.OH * q.OW;
+    for (int o = threadIdx.x; o < ohw; o += APPLY_THREADS) {
+        int ow;
+        const int oh = q.div_ow.divmod(o, ow);
+        int best;
+        const float v = window_max(plane_y, oh * q.SH * q.W + ow * q.SW, q.W, q.KH, q.KW, best);
+        const long long out = static_cast<long long>(pl) * ohw + o;
+        pooled[out] = v;
+        argmax[out] = static_cast<int>(base + best);
+    }
+}
+
+// The gated gradient of element (n, hw) of channel c, whose flat index is `at`: its pooling gradient
+// from the staged planes (n relative to the first staged plane), zero where ReLU(BN(x)) <= 0.
+__device__ __forceinline__ float pooled_grad(const float* grad, const int* where, int n_rel, int hw, int at, float x,
+                                             const PoolShape& q, float m_hi, float m_lo, float istd, float gm,
+                                             float bt) {
+    int iw;
+    const int ih = q.div_w.divmod(hw, iw);
+    const float y = relu_value(affine_value(x, m_hi, m_lo, istd, gm, bt));
+    if (!(y > 0.0f)) return 0.0f;
+    return pool_pixel_grad(grad, where, n_rel, ih, iw, at, q.OH, q.OW, q.KH, q.KW, q.div_sh, q.div_sw);
+}
+
+// Backward partial sums: workgroup (s, c) covers slice s of channel c, as norm_partials<GRADS>.
+__global__ __launch_bounds__(PT) void norm_partials_pool_kernel(PartialArgs p, PoolShape q, PoolGrad pg) {
+    extern __shared__ float staged[];
+    const int s = blockIdx.x, c = blockIdx.y, slices = gridDim.x;
+    const int j0 = s * p.chunk, j1 = min(p.total, j0 + p.chunk);
+    const int ohw = q.OH * q.OW;
+    const int n_lo = j0 < j1 ? p.div_hw.div(j0) : 0;
+    const int count = j0 < j1 ? p.div_hw.div(j1 - 1) - n_lo + 1 : 0;
+    float* grad = staged;
+    int* where = reinterpret_cast<int*>(staged + count * ohw);
+    stage_pool_grads(pg, p.C, c, ohw, n_lo, count, grad, where);
+    __syncthreads();
+    const int plane = p.C * p.HW;
+    const float m_hi = p.mean[c], m_lo = p.mean[p.C + c], istd = p.inv_std[c], gm = pg.gamma[c], bt = pg.beta[c];
+    const double centre = static_cast<double>(m_hi) + static_cast<double>(m_lo);
+    double a[CHAINS] = {}, b[CHAINS] = {};
+    for (int base = j0 + threadIdx.x; base < j1; base += CHAINS * PT) {
+        float xv[CHAINS], gv[CHAINS];
+#pragma unroll
+        for (int u = 0; u < CHAINS; ++u) {
+            const int j = base + u * PT;
+            int hw;
+            const int n = p.div_hw.divmod(j < j1 ? j : j0, hw);
+            const int at = n * plane + c * p.HW + hw;
+            xv[u] = j < j1 ? p.x[at] : 0.0f;
+            gv[u] = j < j1 ? pooled_grad(grad, where, n - n_lo, hw, at, xv[u], q, m_hi, m_lo, istd, gm, bt) : 0.0f;
+        }
+#pragma unroll
+        for (int u = 0; u < CHAINS; ++u) {
+            if (base + u * PT >= j1) continue;
+            const double d = static_cast<double>(xv[u]) - centre;
+            a[u] += static_cast<double>(gv[u]);
+            b[u] = fma(static_cast<double>(gv[u]), d, b[u]);
+        }
+    }
+    double sa = a[0], sb = b[0];
+#pragma unroll
+    for (int u = 1; u < CHAINS; ++u) {
+        sa += a[u];
+        sb += b[u];
+    }
+    workgroup_sum(sa, sb);
+    if (threadIdx.x == 0) {
+        p.partial[(static_cast<long long>(c) * slices + s) * 2] = sa;
+        p.partial[(static_cast<long long>(c) * slices + s) * 2 + 1] = sb;
+    }
+}
+
+// Backward dx: one workgroup per plane pl = n * C + c, as norm_dx with the pooled gradient staged.
+__global__ __launch_bounds__(APPLY_THREADS) void norm_dx_pool_kernel(DxArgs p, PoolShape q, PoolGrad pg, int vec) {
+#pragma clang fp contract(off)
+    extern __shared__ float staged[];
+    __shared__ float coef[3];
+    const int pl = blockIdx.x;
+    int c;
+    const int n = p.div_c.divmod(pl, c);
+    const int ohw = q.OH * q.OW;
+    float* grad = staged;
+    int* where = reinterpret_cast<int*>(staged + ohw);
+    stage_pool_grads(pg, p.C, c, ohw, n, 1, grad, where);
+    if (threadIdx.x == 0) {
+        double sdy = 0.0, sdyx = 0.0;
+        if (p.sums) slice_sums(p.partial, c, p.slices, sdy, sdyx);
+        const DxCoef k = dx_coef(p, c, sdy, sdyx);
+        coef[0] = k.a;
+        coef[1] = k.k1;
+        coef[2] = k.k2;
+        if (pl < p.C) store_param_grads(p, c, k, sdy);
+    }
+    __syncthreads();
+    if (!p.dx) return;
+    const float ka = coef[0], k1 = coef[1], k2 = coef[2], m_hi = p.mean[c], m_lo = p.mean[p.C + c];
+    const float istd = p.inv_std[c], gm = pg.gamma[c], bt = pg.beta[c];
+    const int base = pl * p.HW;
+    if (vec) {  // W % 4 == 0, x and dx 16-byte aligned: four adjacent pixels of one row
+        for (int e = 4 * threadIdx.x; e < p.HW; e += 4 * APPLY_THREADS) {
+            const float4 x4 = *reinterpret_cast<const float4*>(p.x + base + e);
+            const float xs[4] = {x4.x, x4.y, x4.z, x4.w};
+            float4 prev = make_float4(0.f, 0.f, 0.f, 0.f);
+            if (p.add) prev = *reinterpret_cast<const float4*>(p.dx + base + e);
+            const float ps[4] = {prev.x, prev.y, prev.z, prev.w};
+            float out[4];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const float gv = pooled_grad(grad, where, 0, e + u, base + e + u, xs[u], q, m_hi, m_lo, istd, gm, bt);
+                out[u] = dx_of_gated(p, xs[u], gv, ps[u], ka, k1, k2, m_hi, m_lo);
+            }
+            *reinterpret_cast<float4*>(p.dx + base + e) = make_float4(out[0], out[1], out[2], out[3]);
+        }
+    } else {
+        for (int e = threadIdx.x; e < p.HW; e += APPLY_THREADS) {
+            const float x = p.x[base + e];
+            const float gv = pooled_grad(grad, where, 0, e, base + e, x, q, m_hi, m_lo, istd, gm, bt);
+            p.dx[base + e] = dx_of_gated(p, x, gv, p.add ? p.dx[base + e] : 0.0f, ka, k1, k2, m_hi, m_lo);
+        }
+    }
+}
+
 int run_partials(int mode, const NormShape& s, const PartialArgs& args, hipStream_t stream) {
     const dim3 grid(norm_slices(s), s.C);
     if (mode == STATS) norm_partials_kernel<STATS><<<grid, PT, 0, stream>>>(args);
@@ -589,6 +796,132 @@ int norm_forward(const NormShape& s, const NormForward& f, hipStream_t stream) {
     if (vec) norm_apply_kernel<4><<<blocks, APPLY_THREADS, 0, stream>>>(a);
     else norm_apply_kernel<1><<<blocks, APPLY_THREADS, 0, stream>>>(a);
     return MFH_CHECK_LAUNCH("norm_apply", stream);
+}
+
+namespace {
+
+PoolShape pool_shape_of(const PoolDims& d) {
+    PoolShape q{};
+    q.H = d.H;
+    q.W = d.W;
+    q.OH = d.OH;
+    q.OW = d.OW;
+    q.KH = d.KH;
+    q.KW = d.KW;
+    q.SH = d.SH;
+    q.SW = d.SW;
+    q.div_ow = FastDiv(d.OW);
+    q.div_w = FastDiv(d.W);
+    q.div_sh = FastDiv(d.SH);
+    q.div_sw = FastDiv(d.SW);
+    return q;
+}
+
+// Most planes one partial-sum slice of `chunk` positions overlaps.
+int planes_per_slice(const NormShape& s) {
+    const std::int64_t total = static_cast<std::int64_t>(s.N) * s.HW;
+    const int slices = norm_slices(s);
+    const std::int64_t chunk = (total + slices - 1) / slices;
+    return static_cast<int>(std::min<std::int64_t>(s.N, (chunk - 1) / s.HW + 2));
+}
+
+}  // namespace
+
+bool norm_pool_supported(const NormShape& s, const PoolDims& d) {
+    const std::int64_t ohw = static_cast<std::int64_t>(d.OH) * d.OW;
+    return d.H * d.W == s.HW && s.HW <= POOL_STAGE_FLOATS && 2 * ohw <= POOL_STAGE_FLOATS &&
+           2 * ohw * planes_per_slice(s) <= POOL_STAGE_FLOATS;
+}
+
+int norm_relu_pool_forward(const NormShape& s, const NormForward& f, const PoolDims& d, float* pooled, int* argmax,
+                           hipStream_t stream) {
+    if (!norm_pool_supported(s, d)) return MFH_FAIL(ERR_ARG, "batch-norm + max-pool planes exceed the fused kernels' LDS");
+    const int slices = norm_slices(s);
+    PartialArgs args{};
+    args.x = f.x;
+    args.partial = f.partial;
+    args.C = s.C;
+    args.HW = s.HW;
+    args.total = s.N * s.HW;
+    args.chunk = (args.total + slices - 1) / slices;
+    args.div_hw = FastDiv(s.HW);
+    ApplyArgs a{};
+    a.x = f.x;
+    a.gamma = f.gamma;
+    a.beta = f.beta;
+    a.mean = f.mean;
+    a.inv_std = f.inv_std;
+    a.running_mean = f.running_mean;
+    a.running_var = f.running_var;
+    a.partial = f.partial;
+    a.total = s.N * s.C * s.HW;
+    a.C = s.C;
+    a.HW = s.HW;
+    a.slices = slices;
+    a.training = f.training ? 1 : 0;
+    a.relu = 1;
+    a.count = static_cast<double>(s.N) * s.HW;
+    a.momentum = f.momentum;
+    a.eps = f.eps;
+    a.var_scale = f.var_scale;
+    a.div_hw = FastDiv(s.HW);
+    a.div_c = FastDiv(s.C);
+    if (f.training) MFH_TRY(run_partials(STATS, s, args, stream));
+    const int vec = s.HW % 4 == 0 && aligned16(f.x) ? 1 : 0;
+    norm_apply_pool_kernel<<<static_cast<unsigned>(s.N * s.C), APPLY_THREADS, s.HW * sizeof(float), stream>>>(
+        a, pool_shape_of(d), pooled, argmax, vec);
+    return MFH_CHECK_LAUNCH("norm_apply_pool", stream);
+}
+
+int norm_relu_pool_backward(const NormShape& s, const NormBackward& b, const PoolDims& d, const float* pooled_grad,
+                            const int* argmax, const float* beta, hipStream_t stream) {
+    if (!norm_pool_supported(s, d)) return MFH_FAIL(ERR_ARG, "batch-norm + max-pool planes exceed the fused kernels' LDS");
+    const int slices = norm_slices(s);
+    const bool sums = b.gamma_grad || b.beta_grad || (b.training && b.x_grad);
+    const PoolShape q = pool_shape_of(d);
+    const PoolGrad pg{pooled_grad, argmax, b.gamma, beta};
+    const int ohw = d.OH * d.OW;
+    if (sums) {
+        PartialArgs args{};
+        args.x = b.x;
+        args.mean = b.mean;
+        args.inv_std = b.inv_std;
+        args.partial = b.partial;
+        args.C = s.C;
+        args.HW = s.HW;
+        args.total = s.N * s.HW;
+        args.chunk = (args.total + slices - 1) / slices;
+        args.div_hw = FastDiv(s.HW);
+        const size_t lds = static_cast<size_t>(planes_per_slice(s)) * ohw * 2 * sizeof(float);
+        norm_partials_pool_kernel<<<dim3(slices, s.C), PT, lds, stream>>>(args, q, pg);
+        MFH_TRY(MFH_CHECK_LAUNCH("norm_partials_pool", stream));
+    }
+    if (!b.x_grad && !sums) return OK;
+    DxArgs dx{};
+    dx.x = b.x;
+    dx.gamma = b.gamma;
+    dx.mean = b.mean;
+    dx.inv_std = b.inv_std;
+    dx.dx = b.x_grad;
+    dx.gamma_grad = b.gamma_grad;
+    dx.beta_grad = b.beta_grad;
+    dx.partial = b.partial;
+    dx.total = s.N * s.C * s.HW;
+    dx.C = s.C;
+    dx.HW = s.HW;
+    dx.slices = slices;
+    dx.training = b.training ? 1 : 0;
+    dx.add = b.add_x ? 1 : 0;
+    dx.add_gamma = b.add_gamma ? 1 : 0;
+    dx.add_beta = b.add_beta ? 1 : 0;
+    dx.sums = sums ? 1 : 0;
+    dx.count = static_cast<double>(s.N) * s.HW;
+    dx.div_hw = FastDiv(s.HW);
+    dx.div_c = FastDiv(s.C);
+    const int vec = s.HW % 4 == 0 && aligned16(b.x) && (!b.x_grad || aligned16(b.x_grad)) ? 1 : 0;
+    norm_dx_pool_kernel<<<static_cast<unsigned>(s.N * s.C), APPLY_THREADS, static_cast<size_t>(ohw) * 2 * sizeof(float),
+                          stream>>>(dx, q, pg, vec);
+    return MFH_CHECK_LAUNCH("norm_dx_pool", stream);
 }
 
 int norm_backward(const NormShape& s, const NormBackward& b, hipStream_t stream) {

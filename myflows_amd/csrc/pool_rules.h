@@ -1,0 +1,47 @@
+// The max-pool window rules, shared by the pooling kernels (conv.hip) and the batch-norm kernels
+// that pool their own output (norm.hip), so that both give the same values, indices and gradients.
+#pragma once
+
+#include "common.h"
+#include "fastdiv.h"
+
+namespace mfh {
+
+// Window maximum over a KH x KW window of a plane staged in LDS (row length W), starting at LDS
+// index `first`: the first element wins ties, a NaN wins over every number (the first NaN once one
+// is found). `best` receives the LDS index of the winner. Follows native_cublas.cpp:360-376.
+__device__ __forceinline__ float window_max(const float* tile, int first, int W, int KH, int KW, int& best) {
+    best = first;
+    float value = tile[first];
+    for (int kh = 0; kh < KH; ++kh)
+        for (int kw = 0; kw < KW; ++kw) {
+            const float v = tile[first + kh * W + kw];
+            if (v > value || v != v) {
+                value = v;
+                best = first + kh * W + kw;
+            }
+        }
+    return value;
+}
+
+// The gradient of input pixel (ih, iw) of staged plane pl: the dy of every window that covers the
+// pixel and whose argmax (a flat index, `target` for this pixel) is it, added in (oh, ow) order.
+// Follows native_cublas.cpp:378-393.
+__device__ __forceinline__ float pool_pixel_grad(const float* grad, const int* where, int pl, int ih, int iw,
+                                                 int target, int OH, int OW, int KH, int KW, const FastDiv& div_sh,
+                                                 const FastDiv& div_sw) {
+    const int ohw = OH * OW;
+    const int oh_lo = ih >= KH ? div_sh.div(ih - KH) + 1 : 0;
+    const int oh_hi = min(OH - 1, div_sh.div(ih));
+    const int ow_lo = iw >= KW ? div_sw.div(iw - KW) + 1 : 0;
+    const int ow_hi = min(OW - 1, div_sw.div(iw));
+    float sum = 0.0f;
+    for (int oh = oh_lo; oh <= oh_hi; ++oh)
+        for (int ow = ow_lo; ow <= ow_hi; ++ow) {
+            const int o = pl * ohw + oh * OW + ow;
+            if (where[o] == target) sum += grad[o];
+        }
+    return sum;
+}
+
+}  // namespace mfh

@@ -129,6 +129,85 @@ def batchnorm2d_backward(x, dy, gamma, mean, inv_std, *, training, x_grad, gamma
                  int(bool(training)), add_x, add_gamma, add_beta, int(bool(add_residual)), native._stream())
 
 
+def _pool_window(x, kernel_size, stride):
+    kh, kw = (int(v) for v in kernel_size)
+    sh, sw = (int(v) for v in stride)
+    n, c, h, w = (int(v) for v in x.shape)
+    if min(kh, kw, sh, sw) <= 0 or kh > h or kw > w:
+        raise ValueError("max-pool window and stride must be positive and the window inside the input")
+    return kh, kw, sh, sw, (h - kh) // sh + 1, (w - kw) // sw + 1
+
+
+def batchnorm_relu_pool_supported(shape, kernel_size, stride):
+    """Whether batchnorm2d_relu_pool_forward/backward take an NCHW input of this shape and this pool
+    window (their LDS staging of one plane fits)."""
+    n, c, h, w = (int(v) for v in shape)
+    kh, kw = (int(v) for v in kernel_size)
+    sh, sw = (int(v) for v in stride)
+    return bool(native._library().mfh_bn_relu_pool_supported(n, c, h, w, kh, kw, sh, sw))
+
+
+def batchnorm2d_relu_pool_forward(x, gamma, beta, running_mean, running_var, *, momentum, eps, training,
+                                  kernel_size, stride, unbiased_running_var=False):
+    """(pooled, argmax, mean, inv_std): batchnorm2d_forward(..., relu=True) followed by a max-pool
+    without padding, in two launches that never store the ReLU output. argmax is the int32 flat index
+    into x's shape (as maxpool2d_forward's into its input). Bit for bit the separate passes."""
+    x = _f32(x, "x")
+    n, c, hw = _bn_shape(x)
+    gamma, beta = _channel_vector(gamma, c, "gamma"), _channel_vector(beta, c, "beta")
+    for name, stat in (("running_mean", running_mean), ("running_var", running_var)):
+        if not (isinstance(stat, torch.Tensor) and stat.dtype == torch.float32 and stat.is_cuda
+                and stat.is_contiguous() and tuple(stat.shape) == (c,)):
+            raise ValueError(f"{name} must be a contiguous float32 GPU tensor of shape (C,)")
+    kh, kw, sh, sw, oh, ow = _pool_window(x, kernel_size, stride)
+    count = n * hw
+    var_scale = count / (count - 1) if unbiased_running_var and count > 1 else 1.0
+    pooled = torch.empty((n, c, oh, ow), dtype=torch.float32, device=x.device)
+    argmax = torch.empty((n, c, oh, ow), dtype=torch.int32, device=x.device)
+    mean = torch.empty((2, c), dtype=torch.float32, device=x.device)
+    inv_std = torch.empty((c,), dtype=torch.float32, device=x.device)
+    doubles = _bn_workspace_doubles(n, c, hw) if training else 0
+    workspace = torch.empty(doubles, dtype=torch.float64, device=x.device) if doubles else None
+    native._call("mfh_bn_relu_pool_forward", x.data_ptr(), gamma.data_ptr(), beta.data_ptr(),
+                 running_mean.data_ptr(), running_var.data_ptr(), pooled.data_ptr(), argmax.data_ptr(),
+                 mean.data_ptr(), inv_std.data_ptr(), native._addr(workspace), doubles, n, c, int(x.shape[2]),
+                 int(x.shape[3]), kh, kw, sh, sw, int(bool(training)), float(momentum), float(eps), float(var_scale),
+                 native._stream())
+    return pooled, argmax, mean, inv_std
+
+
+def batchnorm2d_relu_pool_backward(x, pooled_grad, argmax, gamma, beta, mean, inv_std, *, training, kernel_size,
+                                   stride, x_grad, gamma_grad, beta_grad, accumulate=(True, True, True)):
+    """Gradients of batchnorm2d_relu_pool_forward from the pooled output's gradient: the max-pool
+    backward, the ReLU gate (recomputed from x) and batchnorm2d_backward in two launches, written (or
+    added, per ``accumulate``) into x_grad, gamma_grad and beta_grad."""
+    x, pooled_grad = _f32(x, "x"), _f32(pooled_grad, "pooled_grad")
+    n, c, hw = _bn_shape(x)
+    kh, kw, sh, sw, oh, ow = _pool_window(x, kernel_size, stride)
+    if tuple(pooled_grad.shape) != (n, c, oh, ow):
+        raise ValueError("pooled_grad must have the pooled output's shape")
+    if not (isinstance(argmax, torch.Tensor) and argmax.dtype == torch.int32 and argmax.is_cuda
+            and argmax.is_contiguous() and argmax.shape == pooled_grad.shape):
+        raise ValueError("argmax must be the contiguous int32 GPU tensor from batchnorm2d_relu_pool_forward")
+    gamma, beta = _channel_vector(gamma, c, "gamma"), _channel_vector(beta, c, "beta")
+    mean, inv_std = _f32(mean, "mean"), _channel_vector(inv_std, c, "inv_std")
+    if tuple(mean.shape) != (2, c):
+        raise ValueError("mean must be the (2, C) pair from batchnorm2d_relu_pool_forward")
+    x_grad = _gradient_buffer(x_grad, x, "x_grad")
+    gamma_grad = _gradient_buffer(gamma_grad, gamma, "gamma_grad")
+    beta_grad = _gradient_buffer(beta_grad, gamma, "beta_grad")
+    if x_grad is None and gamma_grad is None and beta_grad is None:
+        return
+    doubles = _bn_workspace_doubles(n, c, hw)
+    workspace = torch.empty(doubles, dtype=torch.float64, device=x.device)
+    add_x, add_gamma, add_beta = (int(bool(a)) for a in accumulate)
+    native._call("mfh_bn_relu_pool_backward", x.data_ptr(), pooled_grad.data_ptr(), argmax.data_ptr(),
+                 gamma.data_ptr(), beta.data_ptr(), mean.data_ptr(), inv_std.data_ptr(), native._addr(x_grad),
+                 native._addr(gamma_grad), native._addr(beta_grad), workspace.data_ptr(), doubles, n, c,
+                 int(x.shape[2]), int(x.shape[3]), kh, kw, sh, sw, int(bool(training)), add_x, add_gamma, add_beta,
+                 native._stream())
+
+
 def relu_forward(x):
     """max(0, x) (NaN stays NaN)."""
     x = _f32(x, "x")

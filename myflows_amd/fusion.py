@@ -9,7 +9,8 @@ The passes of the reference's ``core/graph_opt.py``:
   convolution with copies of its kernel and bias scaled by gamma / sqrt(var + eps) (the model's own
   parameters are left untouched);
 * ``batchnorm_activation_groups`` (:231-257): ReLU(BN(x)) and ReLU(BN(x) + residual) whose
-  intermediates nobody else reads -> one BatchNormActivation unit;
+  intermediates nobody else reads -> one BatchNormActivation unit; MaxPool(ReLU(BN(x))) whose ReLU
+  output only the max-pool reads -> one BatchNormReLUPool unit (no counterpart in the reference);
 * ``fuse_conv_add_relu`` (inference, after the BN fold; no counterpart in the reference):
   ReLU(Conv2D_Op + residual) whose convolution and Add outputs nobody else reads -> one
   Conv2D_AddReLU_Op, the residual add and the ReLU in the GEMM epilogue.
@@ -196,25 +197,40 @@ def fuse_conv_add_relu(root):
 
 
 def batchnorm_activation_groups(nodes):
-    """{ReLU node: BatchNormActivation} for the BN(+Add)+ReLU chains whose BN and Add outputs (and BN
-    parameters and running statistics) no other node uses."""
+    """{output node: unit} for the BN(+Add)+ReLU chains whose BN and Add outputs (and BN parameters
+    and running statistics) no other node uses (BatchNormActivation, keyed by the ReLU), and for the
+    BN+ReLU chains read only by an unpadded max-pool (BatchNormReLUPool, keyed by the max-pool: the
+    ReLU output then never reaches memory)."""
     from .ops_basic import Add, ReLU
-    from .ops_norm import BatchNorm2d_Op, BatchNormActivation
+    from .ops_conv import MaxPool2d_Op
+    from .ops_norm import BatchNorm2d_Op, BatchNormActivation, BatchNormReLUPool
 
     readers = Counter(p for n in nodes for p in n.parents)
     stat_owners = Counter(id(n.running_mean) for n in nodes if type(n) is BatchNorm2d_Op)
+
+    def private(bn):
+        return (type(bn) is BatchNorm2d_Op and readers[bn] == 1 and stat_owners[id(bn.running_mean)] == 1
+                and all(readers[p] == 1 for p in bn.parents[1:]))
+
     groups = {}
+    pooled = set()
+    for pool in nodes:
+        if type(pool) is not MaxPool2d_Op or pool.padding != (0, 0):
+            continue
+        relu = pool.parents[0]
+        if type(relu) is not ReLU or readers[relu] != 1 or not private(relu.parents[0]):
+            continue
+        groups[pool] = BatchNormReLUPool(relu.parents[0], relu, pool)
+        pooled.add(relu)
     for relu in nodes:
-        if type(relu) is not ReLU:
+        if type(relu) is not ReLU or relu in pooled:
             continue
         parent = relu.parents[0]
         add = parent if type(parent) is Add else None
         if add is not None and readers[add] != 1:
             continue
         for bn in (add.parents if add is not None else (parent,)):
-            private = (type(bn) is BatchNorm2d_Op and readers[bn] == 1 and stat_owners[id(bn.running_mean)] == 1
-                       and all(readers[p] == 1 for p in bn.parents[1:]))
-            if not private:
+            if not private(bn):
                 continue
             residual = None if add is None else next((p for p in add.parents if p is not bn), None)
             if residual in bn.parents:

@@ -106,6 +106,9 @@ _SIGNATURES = {
     "mfh_bn_workspace": ("q", "iii"),
     "mfh_bn_forward": ("i", "ppppppppppq" + "iiiii" + "ddd" + "p"),
     "mfh_bn_backward": ("i", "pppppppppppq" + "iii" + "iiiii" + "p"),
+    "mfh_bn_relu_pool_supported": ("i", "iiiiiiii"),
+    "mfh_bn_relu_pool_forward": ("i", "pppppppppp" + "q" + "iiiiiiii" + "i" + "ddd" + "p"),
+    "mfh_bn_relu_pool_backward": ("i", "pppppppppp" + "pq" + "iiiiiiii" + "iiii" + "p"),
     "mfh_relu_forward": ("i", "ppqp"),
     "mfh_relu_backward": ("i", "pppqfip"),
     "mfh_adam_step": ("i", "ti" + "ffffff" + "p"),

@@ -4,15 +4,18 @@ Operator API of the reference's ``ops/batchnorm.py``: ``BatchNorm2d_Op`` (:7-60)
 ``BatchNormActivation`` (:63-107) and ``GlobalAvgPool2d_Op`` (:110-123). The arithmetic is that of
 ``fused.batchnorm2d_forward`` / ``batchnorm2d_backward`` (libmfhip): FP64 statistics, the mean kept
 as a float hi + lo pair, x_hat recomputed from x in the backward instead of being stored.
+``BatchNormReLUPool`` (BN, ReLU and an unpadded max-pool as one unit) has no counterpart in the
+reference; it gives the separate nodes' bits.
 """
 
 from __future__ import annotations
 
 import torch
 
-from . import fused
+from . import fused, native
 from .fused import on_libmfhip as _on_libmfhip
 from .graph import GradientOp
+from .ops_conv import _resolve_backend
 
 
 class BatchNorm2d_Op(GradientOp):
@@ -122,6 +125,79 @@ class BatchNormActivation:
             gamma_grad=target["gamma"][0], beta_grad=target["beta"][0],
             accumulate=(target["x"][1], target["gamma"][1], target["beta"][1]), gate=gate,
             residual_grad=residual_grad, add_residual=add_residual)
+
+
+class BatchNormReLUPool:
+    """The chain BN -> ReLU -> MaxPool2d of a Graph (a network stem) run as one execution unit.
+
+    Contract with the executor (``graph.Graph``), as ``BatchNormActivation``'s: the unit takes the
+    place of the chain's last node, ``output`` (the max-pool), the executor skips ``hidden`` (the BN
+    and the ReLU), hands ``forward`` the values of ``parents`` (x, gamma, beta) and calls
+    ``backward`` once ``output.grad`` is set.
+
+    Route of a pass, chosen per forward:
+      * fused: libmfhip's BN + ReLU + max-pool launches. The ReLU output is never formed (the
+        hidden nodes' values stay empty): the forward pools the normalised planes in LDS, and the
+        backward takes the pooled gradient to x, gamma and beta, recomputing the ReLU gate from x.
+        Bit for bit the separate nodes' results;
+      * chained: the chain's own nodes one after the other, for a padded max-pool or a shape the
+        fused kernels do not take.
+    """
+
+    def __init__(self, bn, relu, pool):
+        self.bn, self.relu, self.output = bn, relu, pool
+        self.chain = (bn, relu, pool)
+        self.hidden = (bn, relu)
+        self.parents = list(bn.parents)
+        self.name = "BatchNormReLUPool"
+        self.chained = False  # the route of the last forward
+        self._saved = None    # (argmax, mean, inv_std, training) of the last fused forward, when BN needs gradients
+
+    def _fusable(self, x):
+        pool = self.output
+        return (isinstance(x, torch.Tensor) and x.ndim == 4 and _on_libmfhip(x) and pool.padding == (0, 0)
+                and fused.batchnorm_relu_pool_supported(x.shape, pool.kernel_size, pool.stride))
+
+    def forward(self, x, gamma, beta):
+        if tuple(gamma.shape) != (x.shape[1],) or tuple(beta.shape) != tuple(gamma.shape):
+            raise ValueError("gamma/beta shape must be (C,)")
+        self.chained = not self._fusable(x)
+        if self.chained:
+            for node in self.chain:
+                node.forward(*(parent.value for parent in node.parents))
+            return
+        bn, pool = self.bn, self.output
+        pool.actual_backend = _resolve_backend(pool.backend, x)
+        pooled, argmax, mean, inv_std = fused.batchnorm2d_relu_pool_forward(
+            x, gamma, beta, bn.running_mean, bn.running_var, momentum=bn.momentum, eps=bn.eps, training=bn.training,
+            kernel_size=pool.kernel_size, stride=pool.stride, unbiased_running_var=bn.unbiased_running_var)
+        pool.value = pooled
+        # The max-pool node keeps the forward state it would have had (its window choices).
+        pool._context = native.NativePoolContext(tuple(x.shape), tuple(pooled.shape), pool.kernel_size, pool.stride,
+                                                 argmax, x.device.index) if pool.requires_grad else None
+        for node in self.hidden:
+            node.value = None
+        self._saved = (argmax, mean, inv_std, bn.training) if bn.requires_grad else None
+
+    def backward(self):
+        if self.chained:
+            for node in reversed(self.chain):
+                if node.requires_grad and node.grad is not None:
+                    node.backward()
+            for node in self.hidden:
+                node.grad = None
+            return
+        if self._saved is None:
+            return
+        argmax, mean, inv_std, training = self._saved
+        pool = self.output
+        x_node, gamma_node, beta_node = self.bn.parents
+        target = [node.grad_buffer() if node.requires_grad else (None, False)
+                  for node in (x_node, gamma_node, beta_node)]
+        fused.batchnorm2d_relu_pool_backward(
+            x_node.value, pool.grad, argmax, gamma_node.value, beta_node.value, mean, inv_std, training=training,
+            kernel_size=pool.kernel_size, stride=pool.stride, x_grad=target[0][0], gamma_grad=target[1][0],
+            beta_grad=target[2][0], accumulate=tuple(add for _, add in target))
 
 
 class GlobalAvgPool2d_Op(GradientOp):

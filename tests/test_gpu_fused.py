@@ -15,7 +15,7 @@ import numpy as np
 import pytest
 import torch
 
-from myflows_amd import fused
+from myflows_amd import fused, native
 from oracle import reference_path as rp
 from tests.fixtures import assert_near
 
@@ -383,3 +383,77 @@ def test_batchnorm_operator_against_fp64_including_a_large_mean(shape, offset, s
             assert_near(host(running_var), 0.9 * rv.astype(np.float64) + 0.1 * var, 4 * eps32, "running_var")
         else:
             np.testing.assert_array_equal(host(running_mean), rm)
+
+
+# ---- batch norm + ReLU + max-pool as one unit --------------------------------------------------
+POOL_UNIT_CASES = (
+    ((64, 8, 60, 80), (3, 3), (2, 2)),   # the ResNet18 stem's shape at a quarter of its channels; float4 paths
+    ((3, 5, 9, 11), (2, 2), (2, 2)),     # odd planes: scalar paths, one slice per channel
+    ((16, 4, 31, 33), (3, 3), (1, 1)),   # overlapping windows, several slices that cut planes
+    ((2, 3, 7, 8), (7, 8), (1, 1)),      # one window per plane
+)
+
+
+def _separate_bn_relu_pool(x, gamma, beta, rm, rv, kernel, stride, training):
+    y, mean, inv_std = fused.batchnorm2d_forward(x, gamma, beta, rm, rv, momentum=0.1, eps=1e-5,
+                                                 training=training, relu=True)
+    pooled, context = native.maxpool2d_forward(y, kernel_size=kernel, stride=stride)
+    return y, pooled, context, mean, inv_std
+
+
+@pytest.mark.parametrize("shape,kernel,stride", POOL_UNIT_CASES, ids=str)
+@pytest.mark.parametrize("training", (True, False))
+@pytest.mark.parametrize("integer", (False, True), ids=("normal", "ties"))
+def test_batchnorm_relu_pool_unit_equals_the_separate_passes(shape, kernel, stride, training, integer):
+    """batchnorm2d_relu_pool_forward / _backward against batchnorm2d_forward(relu) + max-pool forward
+    and max-pool backward + batchnorm2d_backward(gate=y): pooled values, argmax, statistics, running
+    statistics and every gradient equal bit for bit (integer-valued inputs make ties and zero ReLU
+    outputs common; the gradients are added into existing ones on a second call)."""
+    x, gamma, beta, rm, rv, rng = bn_inputs(shape, 21)
+    if integer:
+        x = rng.integers(-3, 4, size=shape).astype(np.float32)
+    xg, gg, bg = gpu(x), gpu(gamma), gpu(beta)
+    rm1, rv1, rm2, rv2 = gpu(rm), gpu(rv), gpu(rm), gpu(rv)
+    y, pooled, context, mean, inv_std = _separate_bn_relu_pool(xg, gg, bg, rm1, rv1, kernel, stride, training)
+    pooled_u, argmax_u, mean_u, inv_std_u = fused.batchnorm2d_relu_pool_forward(
+        xg, gg, bg, rm2, rv2, momentum=0.1, eps=1e-5, training=training, kernel_size=kernel, stride=stride)
+    for a, b in ((pooled, pooled_u), (context.argmax, argmax_u), (mean, mean_u), (inv_std, inv_std_u),
+                 (rm1, rm2), (rv1, rv2)):
+        assert torch.equal(a, b)
+    dp = gpu(rng.standard_normal(tuple(pooled.shape)).astype(np.float32))
+    dy = native.maxpool2d_backward(dp, context)
+    outs = []
+    for unit in (False, True):
+        grads = [torch.zeros_like(xg), torch.zeros_like(gg), torch.zeros_like(gg)]
+        for _ in range(2):  # the second call adds into the first's gradients
+            if unit:
+                fused.batchnorm2d_relu_pool_backward(
+                    xg, dp, argmax_u, gg, bg, mean_u, inv_std_u, training=training, kernel_size=kernel,
+                    stride=stride, x_grad=grads[0], gamma_grad=grads[1], beta_grad=grads[2])
+            else:
+                fused.batchnorm2d_backward(xg, dy, gg, mean, inv_std, training=training, x_grad=grads[0],
+                                           gamma_grad=grads[1], beta_grad=grads[2], gate=y)
+        outs.append([host(g) for g in grads])
+    for a, b in zip(*outs):
+        np.testing.assert_array_equal(a, b)
+
+
+def test_batchnorm_relu_pool_unit_with_nan_inputs():
+    """A NaN in x propagates through BN and ReLU (NaN stays NaN) and wins its pooling windows, in
+    the unit as in the separate passes; its gradient gate is closed (NaN > 0 is false)."""
+    x, gamma, beta, rm, rv, rng = bn_inputs((2, 3, 9, 12), 5)
+    x[0, 1, 4, 5] = np.nan
+    xg, gg, bg = gpu(x), gpu(gamma), gpu(beta)
+    _, pooled, context, _, _ = _separate_bn_relu_pool(xg, gg, bg, gpu(rm), gpu(rv), (3, 3), (2, 2), False)
+    pooled_u, argmax_u, _, _ = fused.batchnorm2d_relu_pool_forward(
+        xg, gg, bg, gpu(rm), gpu(rv), momentum=0.1, eps=1e-5, training=False, kernel_size=(3, 3), stride=(2, 2))
+    assert torch.isnan(pooled_u).any()
+    np.testing.assert_array_equal(host(pooled), host(pooled_u))
+    assert torch.equal(context.argmax, argmax_u)
+
+
+def test_batchnorm_relu_pool_unit_rejects_planes_beyond_its_lds():
+    """A plane too large for the fused kernels' LDS staging is refused by the support query (the
+    Graph unit then runs the separate nodes)."""
+    assert fused.batchnorm_relu_pool_supported((2, 4, 60, 80), (3, 3), (2, 2))
+    assert not fused.batchnorm_relu_pool_supported((1, 1, 200, 200), (3, 3), (2, 2))

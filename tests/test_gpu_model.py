@@ -111,6 +111,19 @@ def build_resnet(batch, height, width, base_width=64, seed=0, optimize=False):
     return model, mf.Graph(loss, optimize=optimize), out, loss, x_np, t_np
 
 
+def relu_output(relu):
+    """A ReLU node's output; for the stem's ReLU inside a BatchNormReLUPool unit (never stored), the
+    separate BN+ReLU pass over the same input, which gives the unit's bits (running statistics left
+    untouched)."""
+    if relu.value is not None:
+        return relu.value
+    bn = relu.parents[0]
+    x, gamma, beta = (p.value for p in bn.parents)
+    y, _, _ = mf.fused.batchnorm2d_forward(x, gamma, beta, bn.running_mean.clone(), bn.running_var.clone(),
+                                           momentum=bn.momentum, eps=bn.eps, training=bn.training, relu=True)
+    return y
+
+
 def gpu_decisions(graph, base_width):
     """The discrete decisions of the GPU's forward in the oracle's form: each ReLU's mask (output > 0,
     the same as input > 0) by the oracle's ReLU names, and the stem max-pool's choice in each window
@@ -119,7 +132,7 @@ def gpu_decisions(graph, base_width):
     names = ["stem_relu"] + [f"{spec[0]}.{part}" for spec in oracle_resnet.block_specs(base_width)
                              for part in ("relu1", "out")]
     assert len(relus) == len(names)
-    decisions = {name: host(node.value) > 0 for name, node in zip(names, relus)}
+    decisions = {name: host(relu_output(node)) > 0 for name, node in zip(names, relus)}
     context = next(node for node in graph.nodes if isinstance(node, mf.MaxPool2d_Op))._context
     n, c, h, w = context.input_shape
     oh, ow = context.output_shape[2:]
