@@ -4,9 +4,10 @@ Workload: one ResNet18(output_dim=2) training step with Adam
 Variable/Graph API, every convolution, the stem max-pool, the fc Linear, batch norm, ReLU and Adam
 on libmfhip; batch 64, input 3x120x160 ~ N(0, 1), targets ~ U(-1, 1), MSE loss, Kaiming weights
 from seed 0 (synthetic data, random-init weights of the reference architecture). The graph is built
-with Graph(optimize=True), which runs BN+ReLU and BN+Add+ReLU as single units (--plain-graph keeps
-them as separate nodes, as the reference's own training task does). ``value`` is images per second
-over the timed steps.
+with Graph(optimize=True), which runs BN+ReLU, BN+Add+ReLU and the stem's BN+ReLU+max-pool as single
+units (--plain-graph keeps them as separate nodes, as the reference's own training task does); each
+backward convolution runs its dW product on a second stream beside its dX (--single-stream keeps
+one stream). ``value`` is images per second over the timed steps.
 
 ``roofline`` is the FP32 MFMA GEMM engine on the 4096^3 GEMM of BASELINE config 2 (the metric's
 "GEMM TFLOP/s vs FP32 peak"): algorithmic 2*M*N*K flop per launch divided by the average launch
@@ -18,14 +19,18 @@ and max-pool operators (ms each) beside the GPU figures, with the cores and BLAS
 The other configurations are reported beside the headline: ``c2_gemms`` (the standalone GEMMs of
 config 2 against the FP32 matrix peak), ``c3_kernels`` (config 3's im2col and max-pool kernels
 against the HBM peak, its convolution against the matrix peak) and ``c5_inference`` (config 5,
-ResNet18 inference at batch 256, 224x224, with BN folded into the convolutions).
+ResNet18 inference at batch 256, 224x224, with BN folded into the convolutions) and
+``step_bandwidth_kernels`` (the step's batch-norm, max-pool, split-K reduction, kernel reorder and
+Adam kernels at their step shapes against the HBM peak).
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline] [--plain-graph]
+                       [--single-stream] [--step-only]
 """
 
 from __future__ import annotations
 
 import argparse
+import ctypes
 import json
 import os
 import sys
@@ -236,6 +241,124 @@ def c3_kernels():
     return out
 
 
+def _bandwidth_entry(us, nbytes):
+    gbs = nbytes / (us * 1e-6) / 1e9
+    return {"us": round(us, 2), "bytes": int(nbytes), "GB/s": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 3)}
+
+
+def step_bandwidth_kernels():
+    """The bandwidth-bound kernels of the bs64 training step at their step shapes, each against the
+    8 TB/s HBM peak. Bytes are algorithmic (each required tensor read or write once), so a pass that
+    reads a tensor twice shows it as a lower fraction. Batch norm: the two-launch path (partial sums,
+    then the element pass) at layer1 and layer2, the one-launch channel kernels at layer3, the stem's
+    BN+ReLU+max-pool unit; the stem-shaped max-pool kernels; a split-K reduction (layer4 forward,
+    6 slices); the batched forward kernel reorders of all 20 convolutions; Adam over all 62
+    parameter tensors."""
+    lib = native._library()
+    stream = torch.cuda.current_stream().cuda_stream
+    g = torch.Generator().manual_seed(0)
+    out = {"config": "ResNet18 bs64 3x120x160 step shapes", "peak_GB/s": HBM_PEAK_GBS}
+
+    def bn_case(name, n, c, h, w, residual):
+        x = (torch.randn((n, c, h, w), generator=g) * 2 + 0.5).cuda()
+        r = torch.randn((n, c, h, w), generator=g).cuda() if residual else None
+        gamma, beta = torch.ones(c, device="cuda"), torch.zeros(c, device="cuda")
+        rm, rv = torch.zeros(c, device="cuda"), torch.ones(c, device="cuda")
+        y, dx, dy = torch.empty_like(x), torch.empty_like(x), torch.randn((n, c, h, w), generator=g).cuda()
+        rg = torch.empty_like(x) if residual else None
+        mean, istd = torch.empty((2, c), device="cuda"), torch.empty(c, device="cuda")
+        dg, db = torch.empty(c, device="cuda"), torch.empty(c, device="cuda")
+        doubles = lib.mfh_bn_workspace(n, c, h * w)
+        ws = torch.empty(doubles + 2, dtype=torch.float64, device="cuda")
+
+        def forward():
+            native._raise_for(lib.mfh_bn_forward(
+                x.data_ptr(), gamma.data_ptr(), beta.data_ptr(), rm.data_ptr(), rv.data_ptr(), native._addr(r),
+                y.data_ptr(), mean.data_ptr(), istd.data_ptr(), ws.data_ptr(), doubles, n, c, h * w, 1, 1, 0.1,
+                1e-5, 1.0, stream), lib)
+
+        def backward():
+            native._raise_for(lib.mfh_bn_backward(
+                x.data_ptr(), dy.data_ptr(), y.data_ptr(), gamma.data_ptr(), mean.data_ptr(), istd.data_ptr(),
+                dx.data_ptr(), dg.data_ptr(), db.data_ptr(), native._addr(rg), ws.data_ptr(), doubles, n, c, h * w,
+                1, 0, 0, 0, 0, stream), lib)
+
+        forward()
+        elems = 4 * n * c * h * w
+        out[f"bn_forward_{name}"] = _bandwidth_entry(_event_time_us(forward), elems * (3 if residual else 2))
+        out[f"bn_backward_{name}"] = _bandwidth_entry(_event_time_us(backward), elems * (5 if residual else 4))
+
+    bn_case("layer1_two_launch", 64, 64, 29, 39, False)
+    bn_case("layer2_two_launch_residual", 64, 128, 15, 20, True)
+    bn_case("layer3_one_launch_residual", 64, 256, 8, 10, True)
+
+    # The stem: BN + ReLU + 3x3/2 max-pool as one unit, and the plain max-pool kernels at its shape.
+    n, c, h, w, oh, ow = 64, 64, 60, 80, 29, 39
+    x = torch.randn((n, c, h, w), generator=g).cuda()
+    gamma, beta = torch.ones(c, device="cuda"), torch.zeros(c, device="cuda")
+    rm, rv = torch.zeros(c, device="cuda"), torch.ones(c, device="cuda")
+    pooled, argmax = torch.empty((n, c, oh, ow), device="cuda"), torch.empty((n, c, oh, ow), dtype=torch.int32,
+                                                                            device="cuda")
+    mean, istd = torch.empty((2, c), device="cuda"), torch.empty(c, device="cuda")
+    dg, db, dx = torch.empty(c, device="cuda"), torch.empty(c, device="cuda"), torch.empty_like(x)
+    dp = torch.randn((n, c, oh, ow), generator=g).cuda()
+    doubles = lib.mfh_bn_workspace(n, c, h * w)
+    ws = torch.empty(doubles + 2, dtype=torch.float64, device="cuda")
+    dims = (n, c, h, w, 3, 3, 2, 2)
+
+    def unit_forward():
+        native._raise_for(lib.mfh_bn_relu_pool_forward(
+            x.data_ptr(), gamma.data_ptr(), beta.data_ptr(), rm.data_ptr(), rv.data_ptr(), pooled.data_ptr(),
+            argmax.data_ptr(), mean.data_ptr(), istd.data_ptr(), ws.data_ptr(), doubles, *dims, 1, 0.1, 1e-5, 1.0,
+            stream), lib)
+
+    def unit_backward():
+        native._raise_for(lib.mfh_bn_relu_pool_backward(
+            x.data_ptr(), dp.data_ptr(), argmax.data_ptr(), gamma.data_ptr(), beta.data_ptr(), mean.data_ptr(),
+            istd.data_ptr(), dx.data_ptr(), dg.data_ptr(), db.data_ptr(), ws.data_ptr(), doubles, *dims, 1, 0, 0, 0,
+            stream), lib)
+
+    unit_forward()
+    big, small = 4 * n * c * h * w, 4 * n * c * oh * ow
+    out["bn_relu_pool_forward_stem"] = _bandwidth_entry(_event_time_us(unit_forward), big + 2 * small)
+    out["bn_relu_pool_backward_stem"] = _bandwidth_entry(_event_time_us(unit_backward), 2 * big + 2 * small)
+    pool_dims = (n, c, h, w, oh, ow, 3, 3, 2, 2)
+    out["pool_forward_stem"] = _bandwidth_entry(_event_time_us(lambda: native._raise_for(lib.mfh_pool_forward(
+        x.data_ptr(), pooled.data_ptr(), argmax.data_ptr(), *pool_dims, stream), lib)), big + 2 * small)
+    out["pool_backward_stem"] = _bandwidth_entry(_event_time_us(lambda: native._raise_for(lib.mfh_pool_backward(
+        dp.data_ptr(), argmax.data_ptr(), dx.data_ptr(), *pool_dims, stream), lib)), big + 2 * small)
+
+    # Split-K reduction of the layer4 3x3 forward product (512 x 1280 outputs, 6 slices).
+    s, m, nn = 6, 512, 1280
+    partial = torch.randn((s, m, nn), generator=g).cuda()
+    cm = torch.empty((m, nn), device="cuda")
+    out["split_reduce_layer4_forward"] = _bandwidth_entry(_event_time_us(lambda: native._raise_for(
+        lib.mfh_split_reduce(partial.data_ptr(), cm.data_ptr(), s, m, nn, nn, 0, stream), lib)), 4 * (s + 1) * m * nn)
+
+    # The forward kernel reorders of all of ResNet18's convolutions in one batched call.
+    model = mf.ResNet18(output_dim=2, initializer=mf.make_initializer(seed=0), conv_backend="hip_native")
+    kernels = [p.value for p in model.params if p.value.ndim == 4]
+    outs = [torch.empty_like(k) for k in kernels]
+    wdims = []
+    for k in kernels:
+        wdims += [*k.shape, 0, 1, 1, 0, 0]
+    w_ptrs = (ctypes.c_uint64 * len(kernels))(*[k.data_ptr() for k in kernels])
+    o_ptrs = (ctypes.c_uint64 * len(kernels))(*[o.data_ptr() for o in outs])
+    d_arr = (ctypes.c_int * len(wdims))(*wdims)
+    floats = sum(k.numel() for k in kernels)
+    out["weight_order_all_convs"] = _bandwidth_entry(_event_time_us(lambda: native._raise_for(
+        lib.mfh_conv_weight_orders(w_ptrs, o_ptrs, d_arr, len(kernels), stream), lib)), 8 * floats)
+
+    # Adam over every parameter tensor (read p, g, m, v; write p, m, v).
+    # The tensor table is built once, so the timed calls are the native launches alone.
+    params = [p.value for p in model.params]
+    held = [(p, torch.randn_like(p) * 1e-3, torch.zeros_like(p), torch.zeros_like(p)) for p in params]  # kept alive
+    rows = [mf.fused._adam_row(p, grad, m, v, 1e-3, 0.0, 1, 0.9, 0.999) for p, grad, m, v in held]
+    out["adam_all_params"] = _bandwidth_entry(_event_time_us(lambda: mf.fused._adam_launch(
+        rows, 0.9, 0.999, 1e-8, 1.0)), 28 * sum(p.numel() for p in params))
+    return out
+
+
 def _median_seconds(fn, runs):
     fn()  # warm-up
     times = []
@@ -376,6 +499,10 @@ def main():
     parser.add_argument("--warmup", type=int, default=3)
     parser.add_argument("--batch", type=int, default=64)
     parser.add_argument("--no-cpu-baseline", action="store_true")
+    parser.add_argument("--step-only", action="store_true",
+                        help="time the training step alone (no roofline, config 2/3/5 or bandwidth legs), for profiling")
+    parser.add_argument("--single-stream", action="store_true",
+                        help="run each backward's dW products on the current stream (no weight-gradient stream)")
     parser.add_argument("--plain-graph", action="store_true",
                         help="Graph(optimize=False): BN, Add and ReLU as separate nodes (the reference task's graph)")
     args = parser.parse_args()
@@ -388,9 +515,15 @@ def main():
     torch.cuda.set_device(0)
     native._library()
     opt, _ = build_step(args.batch, 120, 160, optimize=not args.plain_graph)
+    opt.graph.overlap_weight_grads = not args.single_stream
     seconds = time_steps(opt, args.steps, args.warmup)
     ms_per_step = seconds * 1e3 / args.steps
     images_per_s = args.batch * args.steps / seconds
+    if args.step_only:
+        print(json.dumps({"metric": METRIC, "value": round(images_per_s, 2), "unit": "images/s", "n_gpus": 1,
+                          "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms_per_step, 3),
+                          "single_stream": args.single_stream, "step_only": True}), flush=True)
+        return 0
     roofline = gemm_roofline()
     result = {
         "metric": METRIC, "value": round(images_per_s, 2), "unit": "images/s", "n_gpus": 1, "steps": args.steps,
@@ -398,12 +531,15 @@ def main():
         "vs_baseline": None, "dtype": "f32", "data": "synthetic",
         "config": {"workload": "ResNet18(output_dim=2) train step (fwd+bwd+Adam), hip_native backend",
                    "global_batch": args.batch, "input": [3, 120, 160], "loss": "MSE",
-                   "graph": "optimize=False" if args.plain_graph else "optimize=True (BN+ReLU, BN+Add+ReLU units)"},
+                   "graph": "optimize=False" if args.plain_graph else
+                   "optimize=True (BN+ReLU, BN+Add+ReLU and stem BN+ReLU+max-pool units)",
+                   "backward_streams": 1 if args.single_stream else 2},
         "step_tflops": round(STEP_GFLOP * args.batch / 64 / (ms_per_step * 1e-3) / 1e3, 2),
         "roofline": roofline,
         "c2_gemms": c2_gemms(),
         "c3_kernels": c3_kernels(),
         "c5_inference": c5_inference(),
+        "step_bandwidth_kernels": step_bandwidth_kernels(),
     }
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline()

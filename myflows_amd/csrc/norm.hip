@@ -817,12 +817,17 @@ PoolShape pool_shape_of(const PoolDims& d) {
     return q;
 }
 
-// Most planes one partial-sum slice of `chunk` positions overlaps.
+// Most planes that one partial-sum slice (of norm_partials' chunk of positions) overlaps.
 int planes_per_slice(const NormShape& s) {
     const std::int64_t total = static_cast<std::int64_t>(s.N) * s.HW;
     const int slices = norm_slices(s);
     const std::int64_t chunk = (total + slices - 1) / slices;
-    return static_cast<int>(std::min<std::int64_t>(s.N, (chunk - 1) / s.HW + 2));
+    std::int64_t most = 0;
+    for (std::int64_t j0 = 0; j0 < total; j0 += chunk) {
+        const std::int64_t j1 = std::min(total, j0 + chunk);
+        most = std::max(most, (j1 - 1) / s.HW - j0 / s.HW + 1);
+    }
+    return static_cast<int>(most);
 }
 
 }  // namespace
