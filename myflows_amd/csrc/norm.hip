@@ -27,7 +27,10 @@
 namespace mfh {
 namespace {
 
-constexpr int PT = 256;           // threads per partial-sum workgroup
+constexpr int PT = 256;           // threads per partial-sum workgroup (WIDE_PT for a one-slice channel of
+                                  // at least WIDE_MIN positions, that one workgroup sums alone)
+constexpr int WIDE_PT = 1024;
+constexpr int WIDE_MIN = 4096;
 constexpr int CHAINS = 4;         // independent load / add chains per thread in the partial sums
 constexpr int MIN_SLICE = 2048;   // fewest positions a slice covers
 constexpr int APPLY_THREADS = 256;
@@ -53,8 +56,9 @@ struct PartialArgs {
 
 // Sum of (a, b) over the workgroup: a fixed xor-butterfly inside each wave64, then the wave sums in
 // wave order. The result is valid in thread 0.
+template <int T>
 __device__ __forceinline__ void workgroup_sum(double& a, double& b) {
-    __shared__ double wave_a[PT / 64], wave_b[PT / 64];
+    __shared__ double wave_a[T / 64], wave_b[T / 64];
 #pragma unroll
     for (int offset = 32; offset > 0; offset >>= 1) {
         a += __shfl_xor(a, offset, 64);
@@ -70,17 +74,17 @@ __device__ __forceinline__ void workgroup_sum(double& a, double& b) {
         a = wave_a[0];
         b = wave_b[0];
 #pragma unroll
-        for (int w = 1; w < PT / 64; ++w) {
+        for (int w = 1; w < T / 64; ++w) {
             a += wave_a[w];
             b += wave_b[w];
         }
     }
 }
 
-// Workgroup (s, c) sums slice s of channel c. Each thread runs CHAINS interleaved chains (positions
-// j, j + PT, j + 2 PT, j + 3 PT, then the next 4 PT), so CHAINS loads are in flight at a time; the
-// chains are added in chain order at the end. The sums are valid in thread 0.
-template <int MODE>
+// Workgroup (s, c) of T threads sums slice s of channel c. Each thread runs CHAINS interleaved
+// chains (positions j, j + T, j + 2 T, j + 3 T, then the next 4 T), so CHAINS loads are in flight at
+// a time; the chains are added in chain order at the end. The sums are valid in thread 0.
+template <int MODE, int T>
 __device__ __forceinline__ void channel_partial(const PartialArgs& p, int c, int s, double& sa, double& sb) {
     const int j0 = s * p.chunk, j1 = min(p.total, j0 + p.chunk);
     const int plane = p.C * p.HW;
@@ -88,12 +92,12 @@ __device__ __forceinline__ void channel_partial(const PartialArgs& p, int c, int
     const double centre = MODE == STATS ? static_cast<double>(p.x[c * p.HW])
                                         : static_cast<double>(p.mean[c]) + static_cast<double>(p.mean[p.C + c]);
     double a[CHAINS] = {}, b[CHAINS] = {};
-    for (int base = j0 + threadIdx.x; base < j1; base += CHAINS * PT) {
+    for (int base = j0 + threadIdx.x; base < j1; base += CHAINS * T) {
         float xv[CHAINS], gv[CHAINS];
         int at[CHAINS];
 #pragma unroll
         for (int u = 0; u < CHAINS; ++u) {
-            const int j = base + u * PT;
+            const int j = base + u * T;
             int hw;
             const int n = p.div_hw.divmod(j < j1 ? j : j0, hw);
             at[u] = n * plane + c * p.HW + hw;
@@ -106,7 +110,7 @@ __device__ __forceinline__ void channel_partial(const PartialArgs& p, int c, int
         }
 #pragma unroll
         for (int u = 0; u < CHAINS; ++u) {
-            if (base + u * PT >= j1) continue;
+            if (base + u * T >= j1) continue;
             const double d = static_cast<double>(xv[u]) - centre;
             if constexpr (MODE == STATS) {
                 a[u] += d;
@@ -126,14 +130,14 @@ __device__ __forceinline__ void channel_partial(const PartialArgs& p, int c, int
         sa += a[u];
         sb += b[u];
     }
-    workgroup_sum(sa, sb);
+    workgroup_sum<T>(sa, sb);
 }
 
-template <int MODE>
-__global__ __launch_bounds__(PT) void norm_partials_kernel(PartialArgs p) {
+template <int MODE, int T>
+__global__ __launch_bounds__(T) void norm_partials_kernel(PartialArgs p) {
     const int s = blockIdx.x, c = blockIdx.y, slices = gridDim.x;
     double sa, sb;
-    channel_partial<MODE>(p, c, s, sa, sb);
+    channel_partial<MODE, T>(p, c, s, sa, sb);
     if (threadIdx.x == 0) {
         p.partial[(static_cast<long long>(c) * slices + s) * 2] = sa;
         p.partial[(static_cast<long long>(c) * slices + s) * 2 + 1] = sb;
@@ -418,13 +422,13 @@ __global__ __launch_bounds__(APPLY_THREADS) void norm_dx_kernel(DxArgs p) {
 
 // One workgroup per channel when a channel is a single slice (at most CHANNEL_FUSED_MAX positions):
 // the partial-sum pass, the finalisation and the element pass of norm_apply (forward) or norm_dx
-// (backward) in one launch. Thread t holds the channel's positions j = t + i * PT (i < CHANNEL_PER)
+// (backward) in one launch. Thread t holds the channel's positions j = t + i * T (i < CHANNEL_FUSED_MAX / T)
 // in registers, loaded once, and adds them into the same four chains in the same order as
 // channel_partial, so the results are the bits of the two-launch path. Position j is
 // (n, hw) = (j / HW, j % HW).
-constexpr int CHANNEL_PER = CHANNEL_FUSED_MAX / PT;
-
-__global__ __launch_bounds__(PT) void norm_forward_channel_kernel(PartialArgs pa, ApplyArgs p) {
+template <int T>
+__global__ __launch_bounds__(T) void norm_forward_channel_kernel(PartialArgs pa, ApplyArgs p) {
+    constexpr int CHANNEL_PER = CHANNEL_FUSED_MAX / T;
     __shared__ float coef[3];
     const int c = blockIdx.x, total = pa.total, plane = p.C * p.HW;
     const double centre = static_cast<double>(p.x[c * p.HW]);
@@ -432,7 +436,7 @@ __global__ __launch_bounds__(PT) void norm_forward_channel_kernel(PartialArgs pa
     int at[CHANNEL_PER];
 #pragma unroll
     for (int i = 0; i < CHANNEL_PER; ++i) {
-        const int j = threadIdx.x + i * PT;
+        const int j = threadIdx.x + i * T;
         int hw;
         const int n = p.div_hw.divmod(j < total ? j : 0, hw);
         at[i] = n * plane + c * p.HW + hw;
@@ -442,7 +446,7 @@ __global__ __launch_bounds__(PT) void norm_forward_channel_kernel(PartialArgs pa
     double a[CHAINS] = {}, b[CHAINS] = {};
 #pragma unroll
     for (int i = 0; i < CHANNEL_PER; ++i) {
-        if (threadIdx.x + i * PT >= total) continue;
+        if (threadIdx.x + i * T >= total) continue;
         const double d = static_cast<double>(xv[i]) - centre;
         a[i % CHAINS] += d;
         b[i % CHAINS] = fma(d, d, b[i % CHAINS]);
@@ -453,7 +457,7 @@ __global__ __launch_bounds__(PT) void norm_forward_channel_kernel(PartialArgs pa
         sa += a[u];
         sb += b[u];
     }
-    workgroup_sum(sa, sb);
+    workgroup_sum<T>(sa, sb);
     if (threadIdx.x == 0) {
         double sum = 0.0, sq = 0.0;  // the one-slice slice_sums
         sum += sa;
@@ -468,12 +472,14 @@ __global__ __launch_bounds__(PT) void norm_forward_channel_kernel(PartialArgs pa
     const float m_hi = coef[0], m_lo = coef[1], istd = coef[2], g = p.gamma[c], bt = p.beta[c];
 #pragma unroll
     for (int i = 0; i < CHANNEL_PER; ++i) {
-        if (threadIdx.x + i * PT >= total) continue;
+        if (threadIdx.x + i * T >= total) continue;
         p.y[at[i]] = apply_value(p, xv[i], rv[i], m_hi, m_lo, istd, g, bt);
     }
 }
 
-__global__ __launch_bounds__(PT) void norm_backward_channel_kernel(PartialArgs pa, DxArgs p) {
+template <int T>
+__global__ __launch_bounds__(T) void norm_backward_channel_kernel(PartialArgs pa, DxArgs p) {
+    constexpr int CHANNEL_PER = CHANNEL_FUSED_MAX / T;
     __shared__ float coef[3];
     const int c = blockIdx.x, total = pa.total, plane = p.C * p.HW;
     const double centre = static_cast<double>(p.mean[c]) + static_cast<double>(p.mean[p.C + c]);
@@ -481,7 +487,7 @@ __global__ __launch_bounds__(PT) void norm_backward_channel_kernel(PartialArgs p
     int at[CHANNEL_PER];
 #pragma unroll
     for (int i = 0; i < CHANNEL_PER; ++i) {
-        const int j = threadIdx.x + i * PT;
+        const int j = threadIdx.x + i * T;
         int hw;
         const int n = p.div_hw.divmod(j < total ? j : 0, hw);
         at[i] = n * plane + c * p.HW + hw;
@@ -493,7 +499,7 @@ __global__ __launch_bounds__(PT) void norm_backward_channel_kernel(PartialArgs p
     double a[CHAINS] = {}, b[CHAINS] = {};
 #pragma unroll
     for (int i = 0; i < CHANNEL_PER; ++i) {
-        if (threadIdx.x + i * PT >= total) continue;
+        if (threadIdx.x + i * T >= total) continue;
         const float gv = p.gate && !(tv[i] > 0.0f) ? 0.0f : dv[i];
         if (pa.residual_grad)
             pa.residual_grad[at[i]] = pa.add_residual ? pa.residual_grad[at[i]] + gv : gv;
@@ -507,7 +513,7 @@ __global__ __launch_bounds__(PT) void norm_backward_channel_kernel(PartialArgs p
         sa += a[u];
         sb += b[u];
     }
-    workgroup_sum(sa, sb);
+    workgroup_sum<T>(sa, sb);
     if (threadIdx.x == 0) {
         double sdy = 0.0, sdyx = 0.0;  // the one-slice slice_sums
         sdy += sa;
@@ -523,7 +529,7 @@ __global__ __launch_bounds__(PT) void norm_backward_channel_kernel(PartialArgs p
     const float ka = coef[0], k1 = coef[1], k2 = coef[2], m_hi = p.mean[c], m_lo = p.mean[p.C + c];
 #pragma unroll
     for (int i = 0; i < CHANNEL_PER; ++i) {
-        if (threadIdx.x + i * PT >= total) continue;
+        if (threadIdx.x + i * T >= total) continue;
         const float prev = p.add ? p.dx[at[i]] : 0.0f;
         p.dx[at[i]] = dx_value(p, xv[i], dv[i], tv[i], prev, ka, k1, k2, m_hi, m_lo);
     }
@@ -623,7 +629,8 @@ __device__ __forceinline__ float pooled_grad(const float* grad, const int* where
 }
 
 // Backward partial sums: workgroup (s, c) covers slice s of channel c, as norm_partials<GRADS>.
-__global__ __launch_bounds__(PT) void norm_partials_pool_kernel(PartialArgs p, PoolShape q, PoolGrad pg) {
+template <int T>
+__global__ __launch_bounds__(T) void norm_partials_pool_kernel(PartialArgs p, PoolShape q, PoolGrad pg) {
     extern __shared__ float staged[];
     const int s = blockIdx.x, c = blockIdx.y, slices = gridDim.x;
     const int j0 = s * p.chunk, j1 = min(p.total, j0 + p.chunk);
@@ -638,11 +645,11 @@ __global__ __launch_bounds__(PT) void norm_partials_pool_kernel(PartialArgs p, P
     const float m_hi = p.mean[c], m_lo = p.mean[p.C + c], istd = p.inv_std[c], gm = pg.gamma[c], bt = pg.beta[c];
     const double centre = static_cast<double>(m_hi) + static_cast<double>(m_lo);
     double a[CHAINS] = {}, b[CHAINS] = {};
-    for (int base = j0 + threadIdx.x; base < j1; base += CHAINS * PT) {
+    for (int base = j0 + threadIdx.x; base < j1; base += CHAINS * T) {
         float xv[CHAINS], gv[CHAINS];
 #pragma unroll
         for (int u = 0; u < CHAINS; ++u) {
-            const int j = base + u * PT;
+            const int j = base + u * T;
             int hw;
             const int n = p.div_hw.divmod(j < j1 ? j : j0, hw);
             const int at = n * plane + c * p.HW + hw;
@@ -651,7 +658,7 @@ __global__ __launch_bounds__(PT) void norm_partials_pool_kernel(PartialArgs p, P
         }
 #pragma unroll
         for (int u = 0; u < CHAINS; ++u) {
-            if (base + u * PT >= j1) continue;
+            if (base + u * T >= j1) continue;
             const double d = static_cast<double>(xv[u]) - centre;
             a[u] += static_cast<double>(gv[u]);
             b[u] = fma(static_cast<double>(gv[u]), d, b[u]);
@@ -663,7 +670,7 @@ __global__ __launch_bounds__(PT) void norm_partials_pool_kernel(PartialArgs p, P
         sa += a[u];
         sb += b[u];
     }
-    workgroup_sum(sa, sb);
+    workgroup_sum<T>(sa, sb);
     if (threadIdx.x == 0) {
         p.partial[(static_cast<long long>(c) * slices + s) * 2] = sa;
         p.partial[(static_cast<long long>(c) * slices + s) * 2 + 1] = sb;
@@ -720,10 +727,25 @@ __global__ __launch_bounds__(APPLY_THREADS) void norm_dx_pool_kernel(DxArgs p, P
     }
 }
 
+// Whether a pass sums each channel with WIDE_PT threads: a one-slice channel of at least WIDE_MIN
+// positions (one workgroup per channel then has too few to keep 256 threads' loads in flight; on
+// MI355X layer3's 5120 positions take 6 / 8 us per forward / backward pass at 1024 threads against
+// 9 / 16.5 at 256). The partial-sum pass and the one-launch channel kernels decide alike, so they
+// sum in the same order.
+bool wide_sums(const NormShape& s) {
+    return norm_slices(s) == 1 && static_cast<std::int64_t>(s.N) * s.HW >= WIDE_MIN;
+}
+
 int run_partials(int mode, const NormShape& s, const PartialArgs& args, hipStream_t stream) {
     const dim3 grid(norm_slices(s), s.C);
-    if (mode == STATS) norm_partials_kernel<STATS><<<grid, PT, 0, stream>>>(args);
-    else norm_partials_kernel<GRADS><<<grid, PT, 0, stream>>>(args);
+    const bool wide = wide_sums(s);
+    if (mode == STATS) {
+        if (wide) norm_partials_kernel<STATS, WIDE_PT><<<grid, WIDE_PT, 0, stream>>>(args);
+        else norm_partials_kernel<STATS, PT><<<grid, PT, 0, stream>>>(args);
+    } else {
+        if (wide) norm_partials_kernel<GRADS, WIDE_PT><<<grid, WIDE_PT, 0, stream>>>(args);
+        else norm_partials_kernel<GRADS, PT><<<grid, PT, 0, stream>>>(args);
+    }
     return MFH_CHECK_LAUNCH(mode == STATS ? "norm_partials<stats>" : "norm_partials<grads>", stream);
 }
 
@@ -788,7 +810,8 @@ int norm_forward(const NormShape& s, const NormForward& f, hipStream_t stream) {
     a.div_c = FastDiv(s.C);
     const bool vec = vec4_spans(s) && aligned16(f.x) && aligned16(f.y) && (!f.residual || aligned16(f.residual));
     if (f.training && slices == 1) {
-        norm_forward_channel_kernel<<<s.C, PT, 0, stream>>>(args, a);
+        if (wide_sums(s)) norm_forward_channel_kernel<WIDE_PT><<<s.C, WIDE_PT, 0, stream>>>(args, a);
+        else norm_forward_channel_kernel<PT><<<s.C, PT, 0, stream>>>(args, a);
         return MFH_CHECK_LAUNCH("norm_forward_channel", stream);
     }
     if (f.training) MFH_TRY(run_partials(STATS, s, args, stream));
@@ -898,7 +921,8 @@ int norm_relu_pool_backward(const NormShape& s, const NormBackward& b, const Poo
         args.chunk = (args.total + slices - 1) / slices;
         args.div_hw = FastDiv(s.HW);
         const size_t lds = static_cast<size_t>(planes_per_slice(s)) * ohw * 2 * sizeof(float);
-        norm_partials_pool_kernel<<<dim3(slices, s.C), PT, lds, stream>>>(args, q, pg);
+        if (wide_sums(s)) norm_partials_pool_kernel<WIDE_PT><<<dim3(slices, s.C), WIDE_PT, lds, stream>>>(args, q, pg);
+        else norm_partials_pool_kernel<PT><<<dim3(slices, s.C), PT, lds, stream>>>(args, q, pg);
         MFH_TRY(MFH_CHECK_LAUNCH("norm_partials_pool", stream));
     }
     if (!b.x_grad && !sums) return OK;
@@ -975,7 +999,8 @@ int norm_backward(const NormShape& s, const NormBackward& b, hipStream_t stream)
     const bool vec = vec4_spans(s) && aligned16(b.x) && aligned16(b.dy) && (!b.gate || aligned16(b.gate)) &&
                      (!b.x_grad || aligned16(b.x_grad));
     if (fused) {
-        norm_backward_channel_kernel<<<s.C, PT, 0, stream>>>(args, d);
+        if (wide_sums(s)) norm_backward_channel_kernel<WIDE_PT><<<s.C, WIDE_PT, 0, stream>>>(args, d);
+        else norm_backward_channel_kernel<PT><<<s.C, PT, 0, stream>>>(args, d);
         return MFH_CHECK_LAUNCH("norm_backward_channel", stream);
     }
     const unsigned blocks = blocks_for(total, APPLY_SPAN);
