@@ -389,7 +389,7 @@ def test_batchnorm_operator_against_fp64_including_a_large_mean(shape, offset, s
 POOL_UNIT_CASES = (
     ((64, 8, 60, 80), (3, 3), (2, 2)),   # the ResNet18 stem's shape at a quarter of its channels; float4 paths
     ((3, 5, 9, 11), (2, 2), (2, 2)),     # odd planes: scalar paths, one slice per channel
-    ((16, 4, 31, 33), (3, 3), (1, 1)),   # overlapping windows, several slices that cut planes
+    ((24, 4, 31, 33), (3, 3), (1, 1)),   # overlapping windows, several slices that cut planes
     ((2, 3, 7, 8), (7, 8), (1, 1)),      # one window per plane
 )
 
