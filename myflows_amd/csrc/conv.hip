@@ -426,12 +426,8 @@ __global__ __launch_bounds__(256) void pool_backward_plane_kernel(const float* _
             const int pl = div_hw.divmod(e, within);
             const int ih = div_w.divmod(within, iw);
             const int target = static_cast<int>(in_base + e);
-            float4 v;
-            v.x = pool_pixel_grad(grad, where, pl, ih, iw, target, OH, OW, KH, KW, div_sh, div_sw);
-            v.y = pool_pixel_grad(grad, where, pl, ih, iw + 1, target + 1, OH, OW, KH, KW, div_sh, div_sw);
-            v.z = pool_pixel_grad(grad, where, pl, ih, iw + 2, target + 2, OH, OW, KH, KW, div_sh, div_sw);
-            v.w = pool_pixel_grad(grad, where, pl, ih, iw + 3, target + 3, OH, OW, KH, KW, div_sh, div_sw);
-            *reinterpret_cast<float4*>(dx + in_base + e) = v;
+            *reinterpret_cast<float4*>(dx + in_base + e) =
+                pool_quad_grad(grad, where, pl, ih, iw, target, OH, OW, KH, KW, div_sh, div_sw);
         }
     } else {
         for (int e = threadIdx.x; e < count * hw; e += 256) {

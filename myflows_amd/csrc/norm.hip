@@ -710,11 +710,15 @@ __global__ __launch_bounds__(APPLY_THREADS) void norm_dx_pool_kernel(DxArgs p, P
             float4 prev = make_float4(0.f, 0.f, 0.f, 0.f);
             if (p.add) prev = *reinterpret_cast<const float4*>(p.dx + base + e);
             const float ps[4] = {prev.x, prev.y, prev.z, prev.w};
+            int iw;
+            const int ih = q.div_w.divmod(e, iw);
+            const float4 g4 = pool_quad_grad(grad, where, 0, ih, iw, base + e, q.OH, q.OW, q.KH, q.KW, q.div_sh, q.div_sw);
+            const float gs[4] = {g4.x, g4.y, g4.z, g4.w};
             float out[4];
 #pragma unroll
             for (int u = 0; u < 4; ++u) {
-                const float gv = pooled_grad(grad, where, 0, e + u, base + e + u, xs[u], q, m_hi, m_lo, istd, gm, bt);
-                out[u] = dx_of_gated(p, xs[u], gv, ps[u], ka, k1, k2, m_hi, m_lo);
+                const float y = relu_value(affine_value(xs[u], m_hi, m_lo, istd, gm, bt));
+                out[u] = dx_of_gated(p, xs[u], y > 0.0f ? gs[u] : 0.0f, ps[u], ka, k1, k2, m_hi, m_lo);
             }
             *reinterpret_cast<float4*>(p.dx + base + e) = make_float4(out[0], out[1], out[2], out[3]);
         }
@@ -947,7 +951,7 @@ int norm_relu_pool_backward(const NormShape& s, const NormBackward& b, const Poo
     dx.count = static_cast<double>(s.N) * s.HW;
     dx.div_hw = FastDiv(s.HW);
     dx.div_c = FastDiv(s.C);
-    const int vec = s.HW % 4 == 0 && aligned16(b.x) && (!b.x_grad || aligned16(b.x_grad)) ? 1 : 0;
+    const int vec = d.W % 4 == 0 && aligned16(b.x) && (!b.x_grad || aligned16(b.x_grad)) ? 1 : 0;
     norm_dx_pool_kernel<<<static_cast<unsigned>(s.N * s.C), APPLY_THREADS, static_cast<size_t>(ohw) * 2 * sizeof(float),
                           stream>>>(dx, q, pg, vec);
     return MFH_CHECK_LAUNCH("norm_dx_pool", stream);

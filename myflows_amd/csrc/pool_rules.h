@@ -44,4 +44,32 @@ __device__ __forceinline__ float pool_pixel_grad(const float* grad, const int* w
     return sum;
 }
 
+// The gradients of four adjacent pixels (ih, iw .. iw + 3) of one row of staged plane pl, the first
+// at flat index `target`: each window that covers any of them is visited once, in (oh, ow) order,
+// and adds its dy to the one of the four pixels its argmax names (if any). Per pixel that is the
+// windows of pool_pixel_grad in the same order, so the four sums are its bits; the window range
+// and the LDS reads are shared by the four pixels.
+__device__ __forceinline__ float4 pool_quad_grad(const float* grad, const int* where, int pl, int ih, int iw,
+                                                 int target, int OH, int OW, int KH, int KW, const FastDiv& div_sh,
+                                                 const FastDiv& div_sw) {
+    const int ohw = OH * OW;
+    const int oh_lo = ih >= KH ? div_sh.div(ih - KH) + 1 : 0;
+    const int oh_hi = min(OH - 1, div_sh.div(ih));
+    const int ow_lo = iw >= KW ? div_sw.div(iw - KW) + 1 : 0;
+    const int ow_hi = min(OW - 1, div_sw.div(iw + 3));
+    float sum[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (int oh = oh_lo; oh <= oh_hi; ++oh)
+        for (int ow = ow_lo; ow <= ow_hi; ++ow) {
+            const int o = pl * ohw + oh * OW + ow;
+            const unsigned u = static_cast<unsigned>(where[o] - target);
+            if (u < 4u) {
+                const float g = grad[o];
+#pragma unroll
+                for (int k = 0; k < 4; ++k)
+                    if (u == static_cast<unsigned>(k)) sum[k] += g;
+            }
+        }
+    return make_float4(sum[0], sum[1], sum[2], sum[3]);
+}
+
 }  // namespace mfh
