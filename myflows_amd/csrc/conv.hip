@@ -280,31 +280,52 @@ __global__ __launch_bounds__(256) void pool_backward_kernel(const float* __restr
 
 constexpr int PLANE_FLOATS = 16384;   // floats of one workgroup's LDS plane buffer (64 KB)
 constexpr int ROW_FLOATS = 12288;     // floats of the im2col row kernel's LDS input band (48 KB)
+constexpr int ROW_AHEAD = 8;          // the row kernel's global loads per thread in flight while it stages
+
+// Workgroups are handed to the 8 XCDs of an MI355X round-robin by id, and each XCD has its own L2.
+// Renumbering workgroup b of `total` gives XCD x one contiguous run of logical ids, so that the
+// workgroups one XCD runs together are neighbours and meet in its L2 on the data they share.
+__device__ __forceinline__ int xcd_contiguous(int b, int total) {
+    constexpr int XCDS = 8;
+    const int xcd = b % XCDS, position = b / XCDS;
+    const int base = total / XCDS, extra = total % XCDS;
+    return xcd * base + min(xcd, extra) + position;
+}
 
 // im2col of one output row (n, oh) per workgroup: the KH input rows it reads, for every channel and
-// with the padding columns and rows as zeros, are staged in LDS with coalesced reads; then the
+// with padding rows as zeros, are staged in LDS with coalesced reads (padding columns are not
+// staged: they read as zero, which keeps the band at 30 KB for 64 channels of 40); then the
 // OW x K block of cols that this row owns (contiguous in memory) is written in order, four features
 // per 16-byte store when K % 4 == 0.
 template <bool VEC>
 __global__ __launch_bounds__(256) void im2col_row_kernel(const float* __restrict__ x, float* __restrict__ cols,
                                                          int CI, int H, int W, int KH, int KW, int OH, int OW, int SH,
                                                          int SW, int PH, int PW, FastDiv div_k, FastDiv div_khkw,
-                                                         FastDiv div_kw, FastDiv div_wp, FastDiv div_oh) {
-    extern __shared__ float band[];  // CI * KH * (W + 2 PW) floats
+                                                         FastDiv div_kw, FastDiv div_w, FastDiv div_oh) {
+    extern __shared__ float band[];  // CI * KH * W floats
     int oh;
-    const int n = div_oh.divmod(blockIdx.x, oh);
-    const int WP = W + 2 * PW;
-    const int entries = CI * KH * WP;
+    // Neighbouring output rows read KH - SH input rows in common: one XCD takes a run of them.
+    const int n = div_oh.divmod(xcd_contiguous(blockIdx.x, gridDim.x), oh);
+    const int entries = CI * KH * W;
     const float* image = x + static_cast<long long>(n) * CI * H * W;
-    for (int e = threadIdx.x; e < entries; e += 256) {
+    auto input = [&](int e) {
         int col;
-        const int r = div_wp.divmod(e, col);  // r = ci * KH + kh
-        int kh;
-        const int ci = r / KH;
-        kh = r - ci * KH;
-        const int ih = oh * SH - PH + kh, iw = col - PW;
-        band[e] = (ih >= 0 && ih < H && iw >= 0 && iw < W) ? image[(ci * H + ih) * W + iw] : 0.0f;
+        const int r = div_w.divmod(e, col);  // r = ci * KH + kh
+        const int ci = r / KH, kh = r - ci * KH;
+        const int ih = oh * SH - PH + kh;
+        return ih >= 0 && ih < H ? image[(ci * H + ih) * W + col] : 0.0f;
+    };
+    // ROW_AHEAD loads per thread in flight: one at a time, the band's ~30 loads per thread would
+    // each wait out the full memory latency.
+    int e = threadIdx.x;
+    for (; e + (ROW_AHEAD - 1) * 256 < entries; e += ROW_AHEAD * 256) {
+        float v[ROW_AHEAD];
+#pragma unroll
+        for (int u = 0; u < ROW_AHEAD; ++u) v[u] = input(e + u * 256);
+#pragma unroll
+        for (int u = 0; u < ROW_AHEAD; ++u) band[e + u * 256] = v[u];
     }
+    for (; e < entries; e += 256) band[e] = input(e);
     __syncthreads();
     const int K = CI * KH * KW;
     const int count = OW * K;
@@ -316,7 +337,8 @@ __global__ __launch_bounds__(256) void im2col_row_kernel(const float* __restrict
         const int ci = div_khkw.divmod(f, tap);
         int kw;
         const int kh = div_kw.divmod(tap, kw);
-        return band[(ci * KH + kh) * WP + ow * SW + kw];
+        const int iw = ow * SW - PW + kw;
+        return static_cast<unsigned>(iw) < static_cast<unsigned>(W) ? band[(ci * KH + kh) * W + iw] : 0.0f;
     };
     if constexpr (VEC) {
         for (int j = threadIdx.x * 4; j < count; j += 256 * 4)
@@ -445,18 +467,18 @@ __global__ __launch_bounds__(256) void pool_backward_plane_kernel(const float* _
 int launch_im2col(const float* x, float* cols, const ConvGeometry& g, hipStream_t stream) {
     const int K = g.features();
     const int total = g.rows() * K;
-    const int band = g.CI * g.KH * (g.W + 2 * g.PW);
+    const int band = g.CI * g.KH * g.W;
     if (band <= ROW_FLOATS && static_cast<long long>(g.N) * g.OH <= INDEX_LIMIT) {
         const bool vec = K % 4 == 0 && (reinterpret_cast<std::uintptr_t>(cols) & 15) == 0;
         const unsigned blocks = static_cast<unsigned>(g.N * g.OH);
-        const FastDiv dk(K), dkk(g.KH * g.KW), dkw(g.KW), dwp(g.W + 2 * g.PW), doh(g.OH);
+        const FastDiv dk(K), dkk(g.KH * g.KW), dkw(g.KW), dw(g.W), doh(g.OH);
         const size_t lds = static_cast<size_t>(band) * sizeof(float);
         if (vec)
             im2col_row_kernel<true><<<blocks, 256, lds, stream>>>(x, cols, g.CI, g.H, g.W, g.KH, g.KW, g.OH, g.OW, g.SH,
-                                                                  g.SW, g.PH, g.PW, dk, dkk, dkw, dwp, doh);
+                                                                  g.SW, g.PH, g.PW, dk, dkk, dkw, dw, doh);
         else
             im2col_row_kernel<false><<<blocks, 256, lds, stream>>>(x, cols, g.CI, g.H, g.W, g.KH, g.KW, g.OH, g.OW,
-                                                                   g.SH, g.SW, g.PH, g.PW, dk, dkk, dkw, dwp, doh);
+                                                                   g.SH, g.SW, g.PH, g.PW, dk, dkk, dkw, dw, doh);
         return MFH_CHECK_LAUNCH("im2col_row", stream);
     }
     if (K % 4 == 0 && (reinterpret_cast<std::uintptr_t>(cols) & 15) == 0) {
