@@ -36,17 +36,22 @@ def _bn_workspace_doubles(n, c, hw):
     return doubles
 
 
-def _bn_shape(x):
-    if x.ndim != 4:
+@lru_cache(maxsize=256)
+def _bn_dims(shape):
+    if len(shape) != 4:
         raise ValueError("batch norm expects an NCHW tensor")
-    n, c, h, w = (int(v) for v in x.shape)
+    n, c, h, w = (int(v) for v in shape)
     native._within_int32(x=n * c * h * w)
     return n, c, h * w
 
 
+def _bn_shape(x):
+    return _bn_dims(x.shape)
+
+
 def _channel_vector(value, c, name):
     value = _f32(value, name)
-    if tuple(value.shape) != (c,):
+    if value.shape != (c,):
         raise ValueError(f"{name} must have shape (C,)")
     return value
 
@@ -76,7 +81,7 @@ def batchnorm2d_forward(x, gamma, beta, running_mean, running_var, *, momentum, 
     mean = torch.empty((2, c), dtype=torch.float32, device=x.device)
     inv_std = torch.empty((c,), dtype=torch.float32, device=x.device)
     doubles = _bn_workspace_doubles(n, c, hw) if training else 0
-    workspace = torch.empty(doubles, dtype=torch.float64, device=x.device) if doubles else None
+    workspace = native.stream_workspace(doubles, torch.float64) if doubles else None
     native._call("mfh_bn_forward", x.data_ptr(), gamma.data_ptr(), beta.data_ptr(), running_mean.data_ptr(),
                  running_var.data_ptr(), native._addr(residual), y.data_ptr(), mean.data_ptr(), inv_std.data_ptr(),
                  native._addr(workspace), doubles, n, c, hw, int(bool(training)), int(bool(relu)), float(momentum),
@@ -121,7 +126,7 @@ def batchnorm2d_backward(x, dy, gamma, mean, inv_std, *, training, x_grad, gamma
     if x_grad is None and gamma_grad is None and beta_grad is None and residual_grad is None:
         return
     doubles = _bn_workspace_doubles(n, c, hw)
-    workspace = torch.empty(doubles, dtype=torch.float64, device=x.device)
+    workspace = native.stream_workspace(doubles, torch.float64)
     add_x, add_gamma, add_beta = (int(bool(a)) for a in accumulate)
     native._call("mfh_bn_backward", x.data_ptr(), dy.data_ptr(), native._addr(gate), gamma.data_ptr(),
                  mean.data_ptr(), inv_std.data_ptr(), native._addr(x_grad), native._addr(gamma_grad),
@@ -167,7 +172,7 @@ def batchnorm2d_relu_pool_forward(x, gamma, beta, running_mean, running_var, *, 
     mean = torch.empty((2, c), dtype=torch.float32, device=x.device)
     inv_std = torch.empty((c,), dtype=torch.float32, device=x.device)
     doubles = _bn_workspace_doubles(n, c, hw) if training else 0
-    workspace = torch.empty(doubles, dtype=torch.float64, device=x.device) if doubles else None
+    workspace = native.stream_workspace(doubles, torch.float64) if doubles else None
     native._call("mfh_bn_relu_pool_forward", x.data_ptr(), gamma.data_ptr(), beta.data_ptr(),
                  running_mean.data_ptr(), running_var.data_ptr(), pooled.data_ptr(), argmax.data_ptr(),
                  mean.data_ptr(), inv_std.data_ptr(), native._addr(workspace), doubles, n, c, int(x.shape[2]),
@@ -199,7 +204,7 @@ def batchnorm2d_relu_pool_backward(x, pooled_grad, argmax, gamma, beta, mean, in
     if x_grad is None and gamma_grad is None and beta_grad is None:
         return
     doubles = _bn_workspace_doubles(n, c, hw)
-    workspace = torch.empty(doubles, dtype=torch.float64, device=x.device)
+    workspace = native.stream_workspace(doubles, torch.float64)
     add_x, add_gamma, add_beta = (int(bool(a)) for a in accumulate)
     native._call("mfh_bn_relu_pool_backward", x.data_ptr(), pooled_grad.data_ptr(), argmax.data_ptr(),
                  gamma.data_ptr(), beta.data_ptr(), mean.data_ptr(), inv_std.data_ptr(), native._addr(x_grad),
@@ -335,15 +340,66 @@ def adam_update(param, grad, m, v, *, lr, beta1, beta2, eps, step, grad_scale=1.
     _adam_launch([_adam_row(param, grad, m, v, lr, weight_decay, step, beta1, beta2)], beta1, beta2, eps, grad_scale)
 
 
-def adam_update_many(updates, *, beta1, beta2, eps, grad_scale):
-    """Adam for (param, grad, m, v, lr, decay, step) tuples in one multi-tensor launch per 16 tensors.
+class _AdamTable:
+    """The parameter side of the last multi-tensor Adam launch: the (param, m, v) tensors, checked
+    once (float32 GPU, contiguous, same shape, no two overlapping), and a row table holding their
+    pointers. A training loop hands the same tensors back every step, and then only the gradients
+    (new tensors each step) are checked and written into the table. The tensors are held, so their
+    ids stay theirs while the table is kept."""
 
-    The tensors must not overlap one another (each parameter is read and written once).
-    """
+    def __init__(self):
+        self.key = None
+        self.held = None
+        self.shapes = None
+        self.table = None
+
+
+_ADAM_TABLE = _AdamTable()
+
+
+def _adam_param_key(updates):
+    return tuple((id(p), id(m), id(v), p.data_ptr(), m.data_ptr(), v.data_ptr()) for p, g, m, v, *_ in updates)
+
+
+def _adam_table_for(updates, beta1, beta2):
+    """The cached row table for these (param, m, v) tensors, rebuilt (with every check) when they
+    change."""
+    cache = _ADAM_TABLE
+    key = _adam_param_key(updates)
+    if cache.key == key:
+        return cache
     rows = [_adam_row(p, g, m, v, lr, decay, step, beta1, beta2) for p, g, m, v, lr, decay, step in updates]
     spans = sorted((t.data_ptr(), t.data_ptr() + 4 * t.numel()) for p, g, m, v, *_ in updates for t in (p, m, v)
                    if t.numel())
     for (_, end), (start, _) in zip(spans, spans[1:]):
         if start < end:
             raise ValueError("adam_update_many needs non-overlapping parameters and moments")
-    _adam_launch(rows, beta1, beta2, eps, grad_scale)
+    cache.key = key
+    cache.held = [(p, m, v) for p, g, m, v, *_ in updates]
+    cache.shapes = [p.shape for p, *_ in updates]
+    cache.table = (native.AdamTensor * len(rows))(*rows)
+    return cache
+
+
+def adam_update_many(updates, *, beta1, beta2, eps, grad_scale):
+    """Adam for (param, grad, m, v, lr, decay, step) tuples in one multi-tensor launch per 16 tensors.
+
+    The tensors must not overlap one another (each parameter is read and written once).
+    """
+    updates = list(updates)
+    if not updates:
+        return
+    cache = _adam_table_for(updates, beta1, beta2)
+    table = cache.table
+    f32 = torch.float32
+    for i, ((p, g, m, v, lr, decay, step), shape) in enumerate(zip(updates, cache.shapes)):
+        if not (isinstance(g, torch.Tensor) and g.dtype is f32 and g.is_cuda and g.is_contiguous()
+                and g.shape == shape):
+            raise ValueError("Adam updates contiguous tensors of the parameter's shape in place")
+        row = table[i]
+        # The scalars are formed in double precision and rounded once to float32 by the fields.
+        row.grad = g.data_ptr()
+        row.lr, row.weight_decay = float(lr), float(decay)
+        row.bias_correction1, row.bias_correction2 = 1.0 - beta1 ** step, 1.0 - beta2 ** step
+    native._call("mfh_adam_step", table, len(updates), float(grad_scale), float(beta1), 1.0 - beta1, float(beta2),
+                 1.0 - beta2, float(eps), native._stream())

@@ -215,10 +215,13 @@ def set_debug_sync(enabled=True):
 # ---------------------------------------------------------------------------------------------
 # argument checks shared by the entry points
 # ---------------------------------------------------------------------------------------------
+_F32 = torch.float32
+
+
 def _device_f32(value, name):
-    if not isinstance(value, torch.Tensor) or value.dtype != torch.float32 or value.device.type != "cuda":
+    if not (isinstance(value, torch.Tensor) and value.dtype is _F32 and value.is_cuda):
         raise TypeError(f"{name} must be a float32 torch tensor on the GPU")
-    return value.contiguous()
+    return value if value.is_contiguous() else value.contiguous()
 
 
 def _within_int32(**counts):
@@ -270,6 +273,15 @@ class ConvGeometry:
 
     @classmethod
     def of(cls, x_shape, weight_shape, stride, padding):
+        """The checked geometry; one shared instance per (shapes, stride, padding), since a network
+        asks for the same few geometries at every step."""
+        try:
+            return _conv_geometry(x_shape, weight_shape, stride, padding)
+        except TypeError:  # an unhashable stride or padding (a list): not cached
+            return cls._checked(x_shape, weight_shape, stride, padding)
+
+    @classmethod
+    def _checked(cls, x_shape, weight_shape, stride, padding):
         if len(x_shape) != 4 or len(weight_shape) != 4 or x_shape[1] != weight_shape[1]:
             raise ValueError("x and weight must be NCHW and OIHW with the same input channels")
         (sh, sw), (ph, pw) = _pair(stride, "stride", 1), _pair(padding, "padding", 0)
@@ -303,6 +315,11 @@ class ConvGeometry:
     def c_args(self):
         return (self.n, self.ci, self.h, self.w, self.co, self.kh, self.kw, self.oh, self.ow, self.sh, self.sw,
                 self.ph, self.pw)
+
+
+@lru_cache(maxsize=1024)
+def _conv_geometry(x_shape, weight_shape, stride, padding):
+    return ConvGeometry._checked(x_shape, weight_shape, stride, padding)
 
 
 # ---------------------------------------------------------------------------------------------
@@ -428,19 +445,40 @@ def _conv_algorithm(algorithm):
     return algorithm
 
 
-@lru_cache(maxsize=1024)
 def _implicit_workspace_floats(g, pass_name):
-    floats = _library().mfh_conv_implicit_workspace(*g.c_args(), IMPLICIT_PASSES[pass_name])
-    if floats < 0:
-        _raise_for(2, _library())
+    # Kept with the (shared) geometry instance: hashing a geometry costs more than the lookup.
+    memo = g.__dict__.setdefault("_workspace_floats", {})
+    floats = memo.get(pass_name)
+    if floats is None:
+        floats = _library().mfh_conv_implicit_workspace(*g.c_args(), IMPLICIT_PASSES[pass_name])
+        if floats < 0:
+            _raise_for(2, _library())
+        memo[pass_name] = floats
     return floats
+
+
+_STREAM_WORKSPACES = {}
+
+
+def stream_workspace(count, dtype=torch.float32):
+    """A scratch tensor of at least `count` elements for a call issued on the current stream, kept
+    per (device, stream, dtype) and handed to every such call: calls on one stream run one after the
+    other, so two of them never use it at the same time. A larger request replaces it (the old block
+    goes back to torch's allocator on the same stream). The calls a training step makes would
+    otherwise allocate and free one per launch."""
+    key = (_current_device(), _stream(), dtype)
+    held = _STREAM_WORKSPACES.get(key)
+    if held is None or held.numel() < count:
+        held = torch.empty(count, dtype=dtype, device="cuda")
+        _STREAM_WORKSPACES[key] = held
+    return held
 
 
 def _implicit_workspace(g, *passes):
     floats = max((_implicit_workspace_floats(g, p) for p in passes), default=0)
     if not floats:
         return None, 0
-    return torch.empty(floats, dtype=torch.float32, device="cuda"), floats
+    return stream_workspace(floats), floats
 
 
 def implicit_chunked(channels):
@@ -517,7 +555,7 @@ def conv2d_forward(x, weight, bias=None, *, stride=(1, 1), padding=(0, 0), activ
         bias = _device_f32(bias, "bias")
         if tuple(bias.shape) != (weight.shape[0],):
             raise ValueError("bias must have shape (out_channels,)")
-    g = ConvGeometry.of(tuple(x.shape), tuple(weight.shape), stride, padding)
+    g = ConvGeometry.of(x.shape, weight.shape, stride, padding)
     act, alpha = _activation_code(activation, alpha)
     device = x.device
     y = torch.empty(g.out_shape, dtype=torch.float32, device=device)
@@ -579,7 +617,7 @@ def conv2d_backward(x, weight, grad_y, cols, *, stride=(1, 1), padding=(0, 0), n
         algorithm = "im2col"
     algorithm = _conv_algorithm(algorithm)
     x, weight, grad_y = _device_f32(x, "x"), _device_f32(weight, "weight"), _device_f32(grad_y, "grad_y")
-    g = ConvGeometry.of(tuple(x.shape), tuple(weight.shape), stride, padding)
+    g = ConvGeometry.of(x.shape, weight.shape, stride, padding)
     act, alpha = _activation_code(activation, alpha)
     if tuple(grad_y.shape) != g.out_shape:
         raise ValueError("grad_y does not have the convolution's output shape")

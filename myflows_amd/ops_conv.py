@@ -40,9 +40,9 @@ def _resolve_backend(backend, *arrays):
             continue
         if not isinstance(value, torch.Tensor):
             raise TypeError("operator arrays must be torch tensors on the active device")
-        if value.device.type != "cuda":
+        if not value.is_cuda:
             raise ValueError(f"backend={chosen} is incompatible with device=cpu")
-        if value.device.index != current:
+        if value.get_device() != current:
             raise ValueError("operator arrays must be on the current GPU")
     return chosen
 
@@ -128,9 +128,9 @@ class Conv2D_Op(GradientOp):
     def _grad_target(node, like):
         """node's gradient as an in-place dX target (contiguous float32 of x's shape), else None."""
         grad = node.grad
-        if (isinstance(grad, torch.Tensor) and grad.dtype == torch.float32 and grad.shape == like.shape
-                and grad.is_contiguous() and grad.device == like.device):
-            return node.grad_buffer()[0]
+        if (isinstance(grad, torch.Tensor) and grad.dtype is torch.float32 and grad.shape == like.shape
+                and grad.is_contiguous() and grad.get_device() == like.get_device()):
+            return grad
         return None
 
     def forward(self, x_val, kernel_val, bias_val=None):

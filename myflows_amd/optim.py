@@ -99,19 +99,18 @@ class Adam(Optimizer):
         self.t += 1
         scale = 1.0 if self.acc_no in (0, 1) else 1.0 / self.acc_no
         batch = []
+        acc, moments, steps, lr = self.acc_gradient, self.s, self.parameter_steps, self.learning_rate
         for node in self.graph.nodes:
-            if not (isinstance(node, Variable) and node.trainable):
+            gradient = acc.get(node)
+            if gradient is None or not (isinstance(node, Variable) and node.trainable):
                 continue
-            gradient = self.acc_gradient.get(node)
-            if gradient is None:
-                continue
-            if node not in self.s:
+            if node not in moments:
                 self.v[node] = torch.zeros_like(node.value)
-                self.s[node] = torch.zeros_like(node.value)
-                self.parameter_steps[node] = 0
-            step = self.parameter_steps.get(node, self.t - 1) + 1
-            self.parameter_steps[node] = step
-            batch.append((node.value, gradient, self.v[node], self.s[node], self.learning_rate, 0.0, step))
+                moments[node] = torch.zeros_like(node.value)
+                steps[node] = 0
+            step = steps.get(node, self.t - 1) + 1
+            steps[node] = step
+            batch.append((node.value, gradient, self.v[node], moments[node], lr, 0.0, step))
         if self.multi_tensor:
             adam_update_many(batch, beta1=self.beta_1, beta2=self.beta_2, eps=self.eps, grad_scale=scale)
         else:
