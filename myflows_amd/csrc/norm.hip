@@ -20,6 +20,8 @@
 // When a channel has at most CHANNEL_FUSED_MAX positions it is a single slice, and each pass is one
 // launch of one workgroup per channel (norm_forward_channel / norm_backward_channel): the partial
 // sums, the finalisation and the element pass in a row, with the arithmetic of the two-launch path.
+#include <initializer_list>
+
 #include "common.h"
 #include "fastdiv.h"
 #include "pool_rules.h"
@@ -34,7 +36,7 @@ constexpr int WIDE_MIN = 4096;
 constexpr int CHAINS = 4;         // independent load / add chains per thread in the partial sums
 constexpr int MIN_SLICE = 2048;   // fewest positions a slice covers
 constexpr int APPLY_THREADS = 256;
-constexpr int APPLY_ELEMS = 4;    // elements per thread in norm_apply / norm_dx
+constexpr int APPLY_ELEMS = 16;   // elements per thread in norm_apply / norm_dx
 constexpr int APPLY_SPAN = APPLY_THREADS * APPLY_ELEMS;
 constexpr int MAX_PLANES = 128;   // (n, c) planes a workgroup finalises at once; more are taken in rounds
 constexpr int CHANNEL_FUSED_MAX = 8192;  // positions per channel up to which a pass is one launch
@@ -52,7 +54,27 @@ struct PartialArgs {
     int C, HW, total, chunk;
     FastDiv div_hw;
     int add_residual;
+    int vec;  // quads may be moved as float4s: every tensor of the pass is 16-byte aligned
 };
+
+// Four consecutive floats at v[at .. at + 3], as one 16-byte access when `vec`.
+__device__ __forceinline__ void load_quad(const float* v, int at, int vec, float (&out)[4]) {
+    if (vec) {
+        const float4 t = *reinterpret_cast<const float4*>(v + at);
+        out[0] = t.x; out[1] = t.y; out[2] = t.z; out[3] = t.w;
+    } else {
+#pragma unroll
+        for (int u = 0; u < 4; ++u) out[u] = v[at + u];
+    }
+}
+__device__ __forceinline__ void store_quad(float* v, int at, int vec, const float (&in)[4]) {
+    if (vec) {
+        *reinterpret_cast<float4*>(v + at) = make_float4(in[0], in[1], in[2], in[3]);
+    } else {
+#pragma unroll
+        for (int u = 0; u < 4; ++u) v[at + u] = in[u];
+    }
+}
 
 // Sum of (a, b) over the workgroup: a fixed xor-butterfly inside each wave64, then the wave sums in
 // wave order. The result is valid in thread 0.
@@ -81,10 +103,25 @@ __device__ __forceinline__ void workgroup_sum(double& a, double& b) {
     }
 }
 
-// Workgroup (s, c) of T threads sums slice s of channel c. Each thread runs CHAINS interleaved
-// chains (positions j, j + T, j + 2 T, j + 3 T, then the next 4 T), so CHAINS loads are in flight at
-// a time; the chains are added in chain order at the end. The sums are valid in thread 0.
-template <int MODE, int T>
+// The gated gradient of four positions: dy, zero where the fused ReLU's output is not positive.
+__device__ __forceinline__ void gated_quad(const PartialArgs& p, int at, float (&g)[4]) {
+    load_quad(p.dy, at, p.vec, g);
+    if (p.gate) {
+        float t[4];
+        load_quad(p.gate, at, p.vec, t);
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+            if (!(t[u] > 0.0f)) g[u] = 0.0f;
+    }
+}
+
+// Workgroup (s, c) of T threads sums slice s of channel c, in CHAINS = 4 chains per thread that are
+// added in chain order at the end; the sums are valid in thread 0.
+//   * QUAD (H*W a multiple of 4; the slice bounds are then multiples of 4 too): thread t takes the
+//     quads of positions [j, j + 4) at j = j0 + 4 (t + i T), i = 0, 1, ..., chain u the u-th
+//     position of each; a quad lies in one plane, so it is one 16-byte load per tensor.
+//   * otherwise: positions j, j + T, j + 2 T, j + 3 T (chains 0-3), then the next 4 T.
+template <int MODE, int T, bool QUAD>
 __device__ __forceinline__ void channel_partial(const PartialArgs& p, int c, int s, double& sa, double& sb) {
     const int j0 = s * p.chunk, j1 = min(p.total, j0 + p.chunk);
     const int plane = p.C * p.HW;
@@ -92,7 +129,49 @@ __device__ __forceinline__ void channel_partial(const PartialArgs& p, int c, int
     const double centre = MODE == STATS ? static_cast<double>(p.x[c * p.HW])
                                         : static_cast<double>(p.mean[c]) + static_cast<double>(p.mean[p.C + c]);
     double a[CHAINS] = {}, b[CHAINS] = {};
-    for (int base = j0 + threadIdx.x; base < j1; base += CHAINS * T) {
+    if constexpr (QUAD) {
+        // Two quads per iteration, both loaded before either is summed.
+        for (int base = j0 + 4 * threadIdx.x; base < j1; base += 8 * T) {
+            float xv[2][4] = {}, gv[2][4] = {};
+            int at[2];
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                const int j = base + h * 4 * T;
+                int hw;
+                const int n = p.div_hw.divmod(j < j1 ? j : j0, hw);
+                at[h] = n * plane + c * p.HW + hw;
+                if (j < j1) {
+                    load_quad(p.x, at[h], p.vec, xv[h]);
+                    if constexpr (MODE == GRADS) gated_quad(p, at[h], gv[h]);
+                }
+            }
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                if (base + h * 4 * T >= j1) continue;
+                if constexpr (MODE == GRADS) {
+                    if (p.residual_grad) {
+                        float r[4] = {};
+                        if (p.add_residual) load_quad(p.residual_grad, at[h], p.vec, r);
+#pragma unroll
+                        for (int u = 0; u < 4; ++u) r[u] = p.add_residual ? r[u] + gv[h][u] : gv[h][u];
+                        store_quad(p.residual_grad, at[h], p.vec, r);
+                    }
+                }
+#pragma unroll
+                for (int u = 0; u < 4; ++u) {
+                    const double d = static_cast<double>(xv[h][u]) - centre;
+                    if constexpr (MODE == STATS) {
+                        a[u] += d;
+                        b[u] = fma(d, d, b[u]);
+                    } else {
+                        a[u] += static_cast<double>(gv[h][u]);
+                        b[u] = fma(static_cast<double>(gv[h][u]), d, b[u]);
+                    }
+                }
+            }
+        }
+    }
+    for (int base = j0 + threadIdx.x; !QUAD && base < j1; base += CHAINS * T) {
         float xv[CHAINS], gv[CHAINS];
         int at[CHAINS];
 #pragma unroll
@@ -133,11 +212,11 @@ __device__ __forceinline__ void channel_partial(const PartialArgs& p, int c, int
     workgroup_sum<T>(sa, sb);
 }
 
-template <int MODE, int T>
+template <int MODE, int T, bool QUAD>
 __global__ __launch_bounds__(T) void norm_partials_kernel(PartialArgs p) {
     const int s = blockIdx.x, c = blockIdx.y, slices = gridDim.x;
     double sa, sb;
-    channel_partial<MODE, T>(p, c, s, sa, sb);
+    channel_partial<MODE, T, QUAD>(p, c, s, sa, sb);
     if (threadIdx.x == 0) {
         p.partial[(static_cast<long long>(c) * slices + s) * 2] = sa;
         p.partial[(static_cast<long long>(c) * slices + s) * 2 + 1] = sb;
@@ -289,27 +368,40 @@ __global__ __launch_bounds__(APPLY_THREADS) void norm_apply_kernel(ApplyArgs p) 
         }
         __syncthreads();
         const int lo_e = max(e0, first * p.HW), hi_e = min(min(p.total, e0 + APPLY_SPAN), (last + 1) * p.HW);
-        for (int e = lo_e + threadIdx.x * VEC; e < hi_e; e += APPLY_THREADS * VEC) {
+        // A thread's ITER groups of VEC elements, APPLY_THREADS * VEC apart: every load is issued
+        // before the first store (the stores could alias the loads for the compiler).
+        constexpr int ITER = APPLY_ELEMS / VEC;
+        float xv[ITER][VEC], rv[ITER][VEC] = {};
+#pragma unroll
+        for (int b = 0; b < ITER; ++b) {
+            const int e = lo_e + (b * APPLY_THREADS + threadIdx.x) * VEC;
+            if (e >= hi_e) continue;
+            if constexpr (VEC == 4) {
+                const float4 x4 = *reinterpret_cast<const float4*>(p.x + e);
+                xv[b][0] = x4.x; xv[b][1] = x4.y; xv[b][2] = x4.z; xv[b][3] = x4.w;
+                if (p.residual) {
+                    const float4 r4 = *reinterpret_cast<const float4*>(p.residual + e);
+                    rv[b][0] = r4.x; rv[b][1] = r4.y; rv[b][2] = r4.z; rv[b][3] = r4.w;
+                }
+            } else {
+                xv[b][0] = p.x[e];
+                if (p.residual) rv[b][0] = p.residual[e];
+            }
+        }
+#pragma unroll
+        for (int b = 0; b < ITER; ++b) {
+            const int e = lo_e + (b * APPLY_THREADS + threadIdx.x) * VEC;
+            if (e >= hi_e) continue;
             // The VEC elements' planes: i, then i + 1 from the element at `next` on (when H*W is
             // not a multiple of VEC a float4 may cross into the next plane).
             const int i = p.div_hw.div(e) - first;
             const int next = (first + i + 1) * p.HW - e;
-            float xv[VEC], rv[VEC] = {}, out[VEC];
-            if constexpr (VEC == 4) {
-                const float4 x4 = *reinterpret_cast<const float4*>(p.x + e);
-                xv[0] = x4.x; xv[1] = x4.y; xv[2] = x4.z; xv[3] = x4.w;
-                if (p.residual) {
-                    const float4 r4 = *reinterpret_cast<const float4*>(p.residual + e);
-                    rv[0] = r4.x; rv[1] = r4.y; rv[2] = r4.z; rv[3] = r4.w;
-                }
-            } else {
-                xv[0] = p.x[e];
-                if (p.residual) rv[0] = p.residual[e];
-            }
+            float out[VEC];
 #pragma unroll
             for (int u = 0; u < VEC; ++u) {
                 const int j = u < next ? i : i + 1;
-                out[u] = apply_value(p, xv[u], rv[u], coef[0][j], coef[1][j], coef[2][j], coef[3][j], coef[4][j]);
+                out[u] = apply_value(p, xv[b][u], rv[b][u], coef[0][j], coef[1][j], coef[2][j], coef[3][j],
+                                     coef[4][j]);
             }
             if constexpr (VEC == 4) *reinterpret_cast<float4*>(p.y + e) = make_float4(out[0], out[1], out[2], out[3]);
             else p.y[e] = out[0];
@@ -381,35 +473,44 @@ __global__ __launch_bounds__(APPLY_THREADS) void norm_dx_kernel(DxArgs p) {
         __syncthreads();
         if (p.dx) {
             const int lo_e = max(e0, first * p.HW), hi_e = min(min(p.total, e0 + APPLY_SPAN), (last + 1) * p.HW);
-            for (int e = lo_e + threadIdx.x * VEC; e < hi_e; e += APPLY_THREADS * VEC) {
-                const int i = p.div_hw.div(e) - first;  // planes i and i + 1, as in norm_apply
-                const int next = (first + i + 1) * p.HW - e;
-                float xv[VEC], gv[VEC], tv[VEC] = {}, prev[VEC] = {};
+            constexpr int ITER = APPLY_ELEMS / VEC;  // loads first, as in norm_apply
+            float xv[ITER][VEC], gv[ITER][VEC], tv[ITER][VEC] = {}, prev[ITER][VEC] = {};
+#pragma unroll
+            for (int b = 0; b < ITER; ++b) {
+                const int e = lo_e + (b * APPLY_THREADS + threadIdx.x) * VEC;
+                if (e >= hi_e) continue;
                 if constexpr (VEC == 4) {
                     const float4 x4 = *reinterpret_cast<const float4*>(p.x + e);
                     const float4 d4 = *reinterpret_cast<const float4*>(p.dy + e);
-                    xv[0] = x4.x; xv[1] = x4.y; xv[2] = x4.z; xv[3] = x4.w;
-                    gv[0] = d4.x; gv[1] = d4.y; gv[2] = d4.z; gv[3] = d4.w;
+                    xv[b][0] = x4.x; xv[b][1] = x4.y; xv[b][2] = x4.z; xv[b][3] = x4.w;
+                    gv[b][0] = d4.x; gv[b][1] = d4.y; gv[b][2] = d4.z; gv[b][3] = d4.w;
                     if (p.gate) {
                         const float4 t4 = *reinterpret_cast<const float4*>(p.gate + e);
-                        tv[0] = t4.x; tv[1] = t4.y; tv[2] = t4.z; tv[3] = t4.w;
+                        tv[b][0] = t4.x; tv[b][1] = t4.y; tv[b][2] = t4.z; tv[b][3] = t4.w;
                     }
                     if (p.add) {
                         const float4 o4 = *reinterpret_cast<const float4*>(p.dx + e);
-                        prev[0] = o4.x; prev[1] = o4.y; prev[2] = o4.z; prev[3] = o4.w;
+                        prev[b][0] = o4.x; prev[b][1] = o4.y; prev[b][2] = o4.z; prev[b][3] = o4.w;
                     }
                 } else {
-                    xv[0] = p.x[e];
-                    gv[0] = p.dy[e];
-                    if (p.gate) tv[0] = p.gate[e];
-                    if (p.add) prev[0] = p.dx[e];
+                    xv[b][0] = p.x[e];
+                    gv[b][0] = p.dy[e];
+                    if (p.gate) tv[b][0] = p.gate[e];
+                    if (p.add) prev[b][0] = p.dx[e];
                 }
+            }
+#pragma unroll
+            for (int b = 0; b < ITER; ++b) {
+                const int e = lo_e + (b * APPLY_THREADS + threadIdx.x) * VEC;
+                if (e >= hi_e) continue;
+                const int i = p.div_hw.div(e) - first;  // planes i and i + 1, as in norm_apply
+                const int next = (first + i + 1) * p.HW - e;
                 float out[VEC];
 #pragma unroll
                 for (int u = 0; u < VEC; ++u) {
                     const int j = u < next ? i : i + 1;
-                    out[u] = dx_value(p, xv[u], gv[u], tv[u], prev[u], coef[0][j], coef[1][j], coef[2][j], coef[3][j],
-                                      coef[4][j]);
+                    out[u] = dx_value(p, xv[b][u], gv[b][u], tv[b][u], prev[b][u], coef[0][j], coef[1][j], coef[2][j],
+                                      coef[3][j], coef[4][j]);
                 }
                 if constexpr (VEC == 4)
                     *reinterpret_cast<float4*>(p.dx + e) = make_float4(out[0], out[1], out[2], out[3]);
@@ -422,34 +523,62 @@ __global__ __launch_bounds__(APPLY_THREADS) void norm_dx_kernel(DxArgs p) {
 
 // One workgroup per channel when a channel is a single slice (at most CHANNEL_FUSED_MAX positions):
 // the partial-sum pass, the finalisation and the element pass of norm_apply (forward) or norm_dx
-// (backward) in one launch. Thread t holds the channel's positions j = t + i * T (i < CHANNEL_FUSED_MAX / T)
-// in registers, loaded once, and adds them into the same four chains in the same order as
-// channel_partial, so the results are the bits of the two-launch path. Position j is
-// (n, hw) = (j / HW, j % HW).
-template <int T>
+// (backward) in one launch. Thread t holds its positions of the channel in registers, loaded once,
+// and adds them into the same four chains in the same order as channel_partial, so the results are
+// the bits of the two-launch path: QUAD, the quads j = 4 (t + i T) + u (chain u); otherwise
+// j = t + i T (chain i % 4). Position j is (n, hw) = (j / HW, j % HW).
+template <int T, bool QUAD>
+struct ChannelSlots {
+    static constexpr int PER = CHANNEL_FUSED_MAX / T;  // positions per thread
+    static constexpr int GROUPS = QUAD ? PER / 4 : PER;
+    static constexpr int WIDTH = QUAD ? 4 : 1;
+    // First position of group i of this thread.
+    static __device__ __forceinline__ int first(int i) { return QUAD ? 4 * (threadIdx.x + i * T) : threadIdx.x + i * T; }
+    // Chain of position u of group i.
+    static __device__ __forceinline__ int chain(int i, int u) { return QUAD ? u : i % CHAINS; }
+};
+
+template <int W>
+__device__ __forceinline__ void load_group(const float* v, int at, int vec, float (&out)[W]) {
+    if constexpr (W == 4) load_quad(v, at, vec, out);
+    else out[0] = v[at];
+}
+template <int W>
+__device__ __forceinline__ void store_group(float* v, int at, int vec, const float (&in)[W]) {
+    if constexpr (W == 4) store_quad(v, at, vec, in);
+    else v[at] = in[0];
+}
+
+template <int T, bool QUAD>
 __global__ __launch_bounds__(T) void norm_forward_channel_kernel(PartialArgs pa, ApplyArgs p) {
-    constexpr int CHANNEL_PER = CHANNEL_FUSED_MAX / T;
+    using S = ChannelSlots<T, QUAD>;
+    constexpr int G = S::GROUPS, W = S::WIDTH;
     __shared__ float coef[3];
     const int c = blockIdx.x, total = pa.total, plane = p.C * p.HW;
     const double centre = static_cast<double>(p.x[c * p.HW]);
-    float xv[CHANNEL_PER], rv[CHANNEL_PER];  // x and the residual, both loaded before the sums
-    int at[CHANNEL_PER];
+    float xv[G][W] = {}, rv[G][W] = {};  // x and the residual, both loaded before the sums
+    int at[G];
 #pragma unroll
-    for (int i = 0; i < CHANNEL_PER; ++i) {
-        const int j = threadIdx.x + i * T;
+    for (int i = 0; i < G; ++i) {
+        const int j = S::first(i);
         int hw;
         const int n = p.div_hw.divmod(j < total ? j : 0, hw);
         at[i] = n * plane + c * p.HW + hw;
-        xv[i] = j < total ? p.x[at[i]] : 0.0f;
-        rv[i] = j < total && p.residual ? p.residual[at[i]] : 0.0f;
+        if (j < total) {
+            load_group<W>(p.x, at[i], pa.vec, xv[i]);
+            if (p.residual) load_group<W>(p.residual, at[i], pa.vec, rv[i]);
+        }
     }
     double a[CHAINS] = {}, b[CHAINS] = {};
 #pragma unroll
-    for (int i = 0; i < CHANNEL_PER; ++i) {
-        if (threadIdx.x + i * T >= total) continue;
-        const double d = static_cast<double>(xv[i]) - centre;
-        a[i % CHAINS] += d;
-        b[i % CHAINS] = fma(d, d, b[i % CHAINS]);
+    for (int i = 0; i < G; ++i) {
+        if (S::first(i) >= total) continue;
+#pragma unroll
+        for (int u = 0; u < W; ++u) {
+            const double d = static_cast<double>(xv[i][u]) - centre;
+            a[S::chain(i, u)] += d;
+            b[S::chain(i, u)] = fma(d, d, b[S::chain(i, u)]);
+        }
     }
     double sa = a[0], sb = b[0];
 #pragma unroll
@@ -471,41 +600,56 @@ __global__ __launch_bounds__(T) void norm_forward_channel_kernel(PartialArgs pa,
     __syncthreads();
     const float m_hi = coef[0], m_lo = coef[1], istd = coef[2], g = p.gamma[c], bt = p.beta[c];
 #pragma unroll
-    for (int i = 0; i < CHANNEL_PER; ++i) {
-        if (threadIdx.x + i * T >= total) continue;
-        p.y[at[i]] = apply_value(p, xv[i], rv[i], m_hi, m_lo, istd, g, bt);
+    for (int i = 0; i < G; ++i) {
+        if (S::first(i) >= total) continue;
+        float out[W];
+#pragma unroll
+        for (int u = 0; u < W; ++u) out[u] = apply_value(p, xv[i][u], rv[i][u], m_hi, m_lo, istd, g, bt);
+        store_group<W>(p.y, at[i], pa.vec, out);
     }
 }
 
-template <int T>
+template <int T, bool QUAD>
 __global__ __launch_bounds__(T) void norm_backward_channel_kernel(PartialArgs pa, DxArgs p) {
-    constexpr int CHANNEL_PER = CHANNEL_FUSED_MAX / T;
+    using S = ChannelSlots<T, QUAD>;
+    constexpr int G = S::GROUPS, W = S::WIDTH;
     __shared__ float coef[3];
     const int c = blockIdx.x, total = pa.total, plane = p.C * p.HW;
     const double centre = static_cast<double>(p.mean[c]) + static_cast<double>(p.mean[p.C + c]);
-    float xv[CHANNEL_PER], dv[CHANNEL_PER], tv[CHANNEL_PER];
-    int at[CHANNEL_PER];
+    float xv[G][W] = {}, dv[G][W] = {}, tv[G][W] = {};
+    int at[G];
 #pragma unroll
-    for (int i = 0; i < CHANNEL_PER; ++i) {
-        const int j = threadIdx.x + i * T;
+    for (int i = 0; i < G; ++i) {
+        const int j = S::first(i);
         int hw;
         const int n = p.div_hw.divmod(j < total ? j : 0, hw);
         at[i] = n * plane + c * p.HW + hw;
-        const bool in = j < total;
-        xv[i] = in ? p.x[at[i]] : 0.0f;
-        dv[i] = in ? p.dy[at[i]] : 0.0f;
-        tv[i] = in && p.gate ? p.gate[at[i]] : 0.0f;
+        if (j < total) {
+            load_group<W>(p.x, at[i], pa.vec, xv[i]);
+            load_group<W>(p.dy, at[i], pa.vec, dv[i]);
+            if (p.gate) load_group<W>(p.gate, at[i], pa.vec, tv[i]);
+        }
     }
     double a[CHAINS] = {}, b[CHAINS] = {};
 #pragma unroll
-    for (int i = 0; i < CHANNEL_PER; ++i) {
-        if (threadIdx.x + i * T >= total) continue;
-        const float gv = p.gate && !(tv[i] > 0.0f) ? 0.0f : dv[i];
-        if (pa.residual_grad)
-            pa.residual_grad[at[i]] = pa.add_residual ? pa.residual_grad[at[i]] + gv : gv;
-        const double d = static_cast<double>(xv[i]) - centre;
-        a[i % CHAINS] += static_cast<double>(gv);
-        b[i % CHAINS] = fma(static_cast<double>(gv), d, b[i % CHAINS]);
+    for (int i = 0; i < G; ++i) {
+        if (S::first(i) >= total) continue;
+        float gv[W];
+#pragma unroll
+        for (int u = 0; u < W; ++u) gv[u] = p.gate && !(tv[i][u] > 0.0f) ? 0.0f : dv[i][u];
+        if (pa.residual_grad) {
+            float r[W] = {};
+            if (pa.add_residual) load_group<W>(pa.residual_grad, at[i], pa.vec, r);
+#pragma unroll
+            for (int u = 0; u < W; ++u) r[u] = pa.add_residual ? r[u] + gv[u] : gv[u];
+            store_group<W>(pa.residual_grad, at[i], pa.vec, r);
+        }
+#pragma unroll
+        for (int u = 0; u < W; ++u) {
+            const double d = static_cast<double>(xv[i][u]) - centre;
+            a[S::chain(i, u)] += static_cast<double>(gv[u]);
+            b[S::chain(i, u)] = fma(static_cast<double>(gv[u]), d, b[S::chain(i, u)]);
+        }
     }
     double sa = a[0], sb = b[0];
 #pragma unroll
@@ -528,10 +672,13 @@ __global__ __launch_bounds__(T) void norm_backward_channel_kernel(PartialArgs pa
     if (!p.dx) return;
     const float ka = coef[0], k1 = coef[1], k2 = coef[2], m_hi = p.mean[c], m_lo = p.mean[p.C + c];
 #pragma unroll
-    for (int i = 0; i < CHANNEL_PER; ++i) {
-        if (threadIdx.x + i * T >= total) continue;
-        const float prev = p.add ? p.dx[at[i]] : 0.0f;
-        p.dx[at[i]] = dx_value(p, xv[i], dv[i], tv[i], prev, ka, k1, k2, m_hi, m_lo);
+    for (int i = 0; i < G; ++i) {
+        if (S::first(i) >= total) continue;
+        float prev[W] = {}, out[W];
+        if (p.add) load_group<W>(p.dx, at[i], pa.vec, prev);
+#pragma unroll
+        for (int u = 0; u < W; ++u) out[u] = dx_value(p, xv[i][u], dv[i][u], tv[i][u], prev[u], ka, k1, k2, m_hi, m_lo);
+        store_group<W>(p.dx, at[i], pa.vec, out);
     }
 }
 
@@ -628,9 +775,31 @@ __device__ __forceinline__ float pooled_grad(const float* grad, const int* where
     return pool_pixel_grad(grad, where, n_rel, ih, iw, at, q.OH, q.OW, q.KH, q.KW, q.div_sh, q.div_sw);
 }
 
-// Backward partial sums: workgroup (s, c) covers slice s of channel c, as norm_partials<GRADS>.
-template <int T>
-__global__ __launch_bounds__(T) void norm_partials_pool_kernel(PartialArgs p, PoolShape q, PoolGrad pg) {
+// The gated gradients of the quad of positions hw .. hw + 3 (one plane row when `rows`, i.e. W a
+// multiple of 4: the covering windows are then scanned once for the four) of staged plane n_rel,
+// first flat index `at`.
+__device__ __forceinline__ void pooled_quad(const float* grad, const int* where, int n_rel, int hw, int at,
+                                            const float (&x)[4], const PoolShape& q, float m_hi, float m_lo,
+                                            float istd, float gm, float bt, bool rows, float (&g)[4]) {
+    if (rows) {
+        int iw;
+        const int ih = q.div_w.divmod(hw, iw);
+        const float4 g4 = pool_quad_grad(grad, where, n_rel, ih, iw, at, q.OH, q.OW, q.KH, q.KW, q.div_sh, q.div_sw);
+        g[0] = g4.x; g[1] = g4.y; g[2] = g4.z; g[3] = g4.w;
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+            if (!(relu_value(affine_value(x[u], m_hi, m_lo, istd, gm, bt)) > 0.0f)) g[u] = 0.0f;
+    } else {
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+            g[u] = pooled_grad(grad, where, n_rel, hw + u, at + u, x[u], q, m_hi, m_lo, istd, gm, bt);
+    }
+}
+
+// Backward partial sums: workgroup (s, c) covers slice s of channel c, in the order of
+// norm_partials<GRADS> (quads when QUAD).
+template <int T, bool QUAD>
+__global__ __launch_bounds__(T) void norm_partials_pool_kernel(PartialArgs p, PoolShape q, PoolGrad pg, int rows) {
     extern __shared__ float staged[];
     const int s = blockIdx.x, c = blockIdx.y, slices = gridDim.x;
     const int j0 = s * p.chunk, j1 = min(p.total, j0 + p.chunk);
@@ -645,7 +814,32 @@ __global__ __launch_bounds__(T) void norm_partials_pool_kernel(PartialArgs p, Po
     const float m_hi = p.mean[c], m_lo = p.mean[p.C + c], istd = p.inv_std[c], gm = pg.gamma[c], bt = pg.beta[c];
     const double centre = static_cast<double>(m_hi) + static_cast<double>(m_lo);
     double a[CHAINS] = {}, b[CHAINS] = {};
-    for (int base = j0 + threadIdx.x; base < j1; base += CHAINS * T) {
+    if constexpr (QUAD) {
+        for (int base = j0 + 4 * threadIdx.x; base < j1; base += 8 * T) {
+            float xv[2][4] = {}, gv[2][4] = {};
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                const int j = base + h * 4 * T;
+                if (j >= j1) continue;
+                int hw;
+                const int n = p.div_hw.divmod(j, hw);
+                const int at = n * plane + c * p.HW + hw;
+                load_quad(p.x, at, p.vec, xv[h]);
+                pooled_quad(grad, where, n - n_lo, hw, at, xv[h], q, m_hi, m_lo, istd, gm, bt, rows != 0, gv[h]);
+            }
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                if (base + h * 4 * T >= j1) continue;
+#pragma unroll
+                for (int u = 0; u < 4; ++u) {
+                    const double d = static_cast<double>(xv[h][u]) - centre;
+                    a[u] += static_cast<double>(gv[h][u]);
+                    b[u] = fma(static_cast<double>(gv[h][u]), d, b[u]);
+                }
+            }
+        }
+    }
+    for (int base = j0 + threadIdx.x; !QUAD && base < j1; base += CHAINS * T) {
         float xv[CHAINS], gv[CHAINS];
 #pragma unroll
         for (int u = 0; u < CHAINS; ++u) {
@@ -740,20 +934,41 @@ bool wide_sums(const NormShape& s) {
     return norm_slices(s) == 1 && static_cast<std::int64_t>(s.N) * s.HW >= WIDE_MIN;
 }
 
-int run_partials(int mode, const NormShape& s, const PartialArgs& args, hipStream_t stream) {
-    const dim3 grid(norm_slices(s), s.C);
-    const bool wide = wide_sums(s);
-    if (mode == STATS) {
-        if (wide) norm_partials_kernel<STATS, WIDE_PT><<<grid, WIDE_PT, 0, stream>>>(args);
-        else norm_partials_kernel<STATS, PT><<<grid, PT, 0, stream>>>(args);
-    } else {
-        if (wide) norm_partials_kernel<GRADS, WIDE_PT><<<grid, WIDE_PT, 0, stream>>>(args);
-        else norm_partials_kernel<GRADS, PT><<<grid, PT, 0, stream>>>(args);
-    }
-    return MFH_CHECK_LAUNCH(mode == STATS ? "norm_partials<stats>" : "norm_partials<grads>", stream);
+bool aligned16(const void* q) { return (reinterpret_cast<std::uintptr_t>(q) & 15) == 0; }
+
+// Whether a channel's positions are summed in quads (channel_partial): H*W a multiple of 4. It depends
+// on the shape only, so every pass over a shape sums in the same order.
+bool quad_order(const NormShape& s) { return s.HW % 4 == 0; }
+
+// Positions per partial-sum slice: a multiple of 4 in quad order, so that a quad lies in one slice.
+int slice_chunk(const NormShape& s, int slices) {
+    const std::int64_t total = static_cast<std::int64_t>(s.N) * s.HW;
+    std::int64_t chunk = (total + slices - 1) / slices;
+    if (quad_order(s)) chunk = (chunk + 3) / 4 * 4;
+    return static_cast<int>(chunk);
 }
 
-bool aligned16(const void* q) { return (reinterpret_cast<std::uintptr_t>(q) & 15) == 0; }
+// The float4 flag of a pass: all of its tensors 16-byte aligned (quad order only).
+int quad_vec(const NormShape& s, std::initializer_list<const void*> tensors) {
+    if (!quad_order(s)) return 0;
+    for (const void* t : tensors)
+        if (t && !aligned16(t)) return 0;
+    return 1;
+}
+
+template <int MODE, bool QUAD>
+void launch_partials(const NormShape& s, const PartialArgs& args, hipStream_t stream) {
+    const dim3 grid(norm_slices(s), s.C);
+    if (wide_sums(s)) norm_partials_kernel<MODE, WIDE_PT, QUAD><<<grid, WIDE_PT, 0, stream>>>(args);
+    else norm_partials_kernel<MODE, PT, QUAD><<<grid, PT, 0, stream>>>(args);
+}
+
+int run_partials(int mode, const NormShape& s, const PartialArgs& args, hipStream_t stream) {
+    const bool quad = quad_order(s);
+    if (mode == STATS) (quad ? launch_partials<STATS, true> : launch_partials<STATS, false>)(s, args, stream);
+    else (quad ? launch_partials<GRADS, true> : launch_partials<GRADS, false>)(s, args, stream);
+    return MFH_CHECK_LAUNCH(mode == STATS ? "norm_partials<stats>" : "norm_partials<grads>", stream);
+}
 
 // Whether the element passes can take float4s: every workgroup's span starts on a multiple of 4
 // (APPLY_SPAN is one) and is one round of planes (so its first element is the span's), and the
@@ -787,8 +1002,9 @@ int norm_forward(const NormShape& s, const NormForward& f, hipStream_t stream) {
     args.C = s.C;
     args.HW = s.HW;
     args.total = s.N * s.HW;
-    args.chunk = (args.total + slices - 1) / slices;
+    args.chunk = slice_chunk(s, slices);
     args.div_hw = FastDiv(s.HW);
+    args.vec = quad_vec(s, {f.x, f.y, f.residual});
     ApplyArgs a{};
     a.x = f.x;
     a.gamma = f.gamma;
@@ -814,8 +1030,14 @@ int norm_forward(const NormShape& s, const NormForward& f, hipStream_t stream) {
     a.div_c = FastDiv(s.C);
     const bool vec = vec4_spans(s) && aligned16(f.x) && aligned16(f.y) && (!f.residual || aligned16(f.residual));
     if (f.training && slices == 1) {
-        if (wide_sums(s)) norm_forward_channel_kernel<WIDE_PT><<<s.C, WIDE_PT, 0, stream>>>(args, a);
-        else norm_forward_channel_kernel<PT><<<s.C, PT, 0, stream>>>(args, a);
+        const bool wide = wide_sums(s);
+        if (quad_order(s)) {
+            if (wide) norm_forward_channel_kernel<WIDE_PT, true><<<s.C, WIDE_PT, 0, stream>>>(args, a);
+            else norm_forward_channel_kernel<PT, true><<<s.C, PT, 0, stream>>>(args, a);
+        } else {
+            if (wide) norm_forward_channel_kernel<WIDE_PT, false><<<s.C, WIDE_PT, 0, stream>>>(args, a);
+            else norm_forward_channel_kernel<PT, false><<<s.C, PT, 0, stream>>>(args, a);
+        }
         return MFH_CHECK_LAUNCH("norm_forward_channel", stream);
     }
     if (f.training) MFH_TRY(run_partials(STATS, s, args, stream));
@@ -848,7 +1070,7 @@ PoolShape pool_shape_of(const PoolDims& d) {
 int planes_per_slice(const NormShape& s) {
     const std::int64_t total = static_cast<std::int64_t>(s.N) * s.HW;
     const int slices = norm_slices(s);
-    const std::int64_t chunk = (total + slices - 1) / slices;
+    const std::int64_t chunk = slice_chunk(s, slices);
     std::int64_t most = 0;
     for (std::int64_t j0 = 0; j0 < total; j0 += chunk) {
         const std::int64_t j1 = std::min(total, j0 + chunk);
@@ -875,8 +1097,9 @@ int norm_relu_pool_forward(const NormShape& s, const NormForward& f, const PoolD
     args.C = s.C;
     args.HW = s.HW;
     args.total = s.N * s.HW;
-    args.chunk = (args.total + slices - 1) / slices;
+    args.chunk = slice_chunk(s, slices);
     args.div_hw = FastDiv(s.HW);
+    args.vec = quad_vec(s, {f.x});
     ApplyArgs a{};
     a.x = f.x;
     a.gamma = f.gamma;
@@ -922,11 +1145,20 @@ int norm_relu_pool_backward(const NormShape& s, const NormBackward& b, const Poo
         args.C = s.C;
         args.HW = s.HW;
         args.total = s.N * s.HW;
-        args.chunk = (args.total + slices - 1) / slices;
+        args.chunk = slice_chunk(s, slices);
         args.div_hw = FastDiv(s.HW);
         const size_t lds = static_cast<size_t>(planes_per_slice(s)) * ohw * 2 * sizeof(float);
-        if (wide_sums(s)) norm_partials_pool_kernel<WIDE_PT><<<dim3(slices, s.C), WIDE_PT, lds, stream>>>(args, q, pg);
-        else norm_partials_pool_kernel<PT><<<dim3(slices, s.C), PT, lds, stream>>>(args, q, pg);
+        args.vec = quad_vec(s, {b.x});
+        const int rows = d.W % 4 == 0 ? 1 : 0;
+        const bool wide = wide_sums(s);
+        const dim3 grid(slices, s.C);
+        if (quad_order(s)) {
+            if (wide) norm_partials_pool_kernel<WIDE_PT, true><<<grid, WIDE_PT, lds, stream>>>(args, q, pg, rows);
+            else norm_partials_pool_kernel<PT, true><<<grid, PT, lds, stream>>>(args, q, pg, rows);
+        } else {
+            if (wide) norm_partials_pool_kernel<WIDE_PT, false><<<grid, WIDE_PT, lds, stream>>>(args, q, pg, rows);
+            else norm_partials_pool_kernel<PT, false><<<grid, PT, lds, stream>>>(args, q, pg, rows);
+        }
         MFH_TRY(MFH_CHECK_LAUNCH("norm_partials_pool", stream));
     }
     if (!b.x_grad && !sums) return OK;
@@ -972,8 +1204,9 @@ int norm_backward(const NormShape& s, const NormBackward& b, hipStream_t stream)
     args.C = s.C;
     args.HW = s.HW;
     args.total = s.N * s.HW;
-    args.chunk = (args.total + slices - 1) / slices;
+    args.chunk = slice_chunk(s, slices);
     args.div_hw = FastDiv(s.HW);
+    args.vec = quad_vec(s, {b.x, b.dy, b.gate, b.residual_grad, b.x_grad});
     const bool fused = sums && slices == 1;
     if ((sums || b.residual_grad) && !fused) MFH_TRY(run_partials(GRADS, s, args, stream));
     if (!b.x_grad && !sums) return OK;
@@ -1003,8 +1236,14 @@ int norm_backward(const NormShape& s, const NormBackward& b, hipStream_t stream)
     const bool vec = vec4_spans(s) && aligned16(b.x) && aligned16(b.dy) && (!b.gate || aligned16(b.gate)) &&
                      (!b.x_grad || aligned16(b.x_grad));
     if (fused) {
-        if (wide_sums(s)) norm_backward_channel_kernel<WIDE_PT><<<s.C, WIDE_PT, 0, stream>>>(args, d);
-        else norm_backward_channel_kernel<PT><<<s.C, PT, 0, stream>>>(args, d);
+        const bool wide = wide_sums(s);
+        if (quad_order(s)) {
+            if (wide) norm_backward_channel_kernel<WIDE_PT, true><<<s.C, WIDE_PT, 0, stream>>>(args, d);
+            else norm_backward_channel_kernel<PT, true><<<s.C, PT, 0, stream>>>(args, d);
+        } else {
+            if (wide) norm_backward_channel_kernel<WIDE_PT, false><<<s.C, WIDE_PT, 0, stream>>>(args, d);
+            else norm_backward_channel_kernel<PT, false><<<s.C, PT, 0, stream>>>(args, d);
+        }
         return MFH_CHECK_LAUNCH("norm_backward_channel", stream);
     }
     const unsigned blocks = blocks_for(total, APPLY_SPAN);
