@@ -378,6 +378,50 @@ __device__ __forceinline__ void mfma_k_loop(float* smem, int k_begin, int k_end,
     if (stages > 0) drain(acc);
 }
 
+// The K loop with the global reads two stages ahead: the reads of stage t + 2 are issued when stage
+// t starts, into one of two register slots, so a stage's reads have two stages of MFMAs to arrive
+// before they are stored to LDS (at the end of stage t + 1) instead of one. fetch(slot, kt) and
+// store(slot, a_lds, b_lds) take the slot as std::integral_constant<int, 0 or 1>: stage t uses slot
+// t % 2 and LDS buffer t % 2. The MFMAs, their operands and their order are mfma_k_loop's
+// (STAGE_PLAIN), so the results are its bits. fetch is issued for every stage, also for the two past
+// the end (kt >= k_end), so that the compiler sees the same loads in flight on every path and waits
+// for exactly one stage's: a loader must read nothing (or stay in bounds) there, as the buffer
+// loaders do, whose out-of-range lanes read zero.
+template <class S, class Fetch, class Store, class Drain = KeepChain>
+__device__ __forceinline__ void mfma_k_loop_ahead(float* smem, int k_begin, int k_end, Fetch&& fetch, Store&& store,
+                                                  v16f (&acc)[S::TM][S::TN], int wm0, int wn0, int lane,
+                                                  Drain&& drain = Drain{}) {
+    constexpr int BK = S::BK;
+    using Slot0 = std::integral_constant<int, 0>;
+    using Slot1 = std::integral_constant<int, 1>;
+    const int stages = k_end > k_begin ? (k_end - k_begin + BK - 1) / BK : 0;
+    if (stages > 0) {
+        fetch(Slot0{}, k_begin);
+        fetch(Slot1{}, k_begin + BK);
+        store(Slot0{}, smem, smem + S::A_SIZE);
+    }
+    __syncthreads();
+    constexpr bool RESTART = std::decay_t<Drain>::restarts;
+    // Stage t of slot T: fetch stage t + 2 into slot T, the MFMAs of LDS buffer T, then stage t + 1
+    // (slot 1 - T) into LDS buffer 1 - T.
+    auto stage = [&](auto slot, int t) {
+        constexpr int T = decltype(slot)::value;
+        using Other = std::integral_constant<int, 1 - T>;
+        fetch(slot, k_begin + (t + 2) * BK);
+        if (t > 0) drain(acc);
+        const float* As = smem + T * S::STAGE;
+        float* next = smem + (1 - T) * S::STAGE;
+        mfma_stage<S, 0, S::HALF, RESTART>(As, As + S::A_SIZE, acc, wm0, wn0, lane);
+        if (t + 1 < stages) store(Other{}, next, next + S::A_SIZE);
+        __syncthreads();
+    };
+    for (int t = 0; t < stages; t += 2) {
+        stage(Slot0{}, t);
+        if (t + 1 < stages) stage(Slot1{}, t + 1);
+    }
+    if (stages > 0) drain(acc);
+}
+
 // Epilogue: bias (per output column or per output row), the activation, then the store of the
 // wave's accumulators into C (dense or segmented, see output_offset), added to what C holds when
 // p.accumulate.

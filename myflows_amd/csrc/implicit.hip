@@ -331,20 +331,17 @@ __device__ __forceinline__ void implicit_forward_tile(const GemmParams& p, const
     const int k_end = p.split ? min(p.K, k_begin + p.k_chunk) : p.K;
     float* __restrict__ C = p.C + (p.split ? z * p.c_batch : 0);
 
-    // Chunked products (K a multiple of BK) read the kernel order with buffer loads too.
-    std::conditional_t<CHUNKED, BufferRowTile<BM, BK, S::THREADS>, TileLoader<BM, BK, S::THREADS, VA>> la;
-    std::conditional_t<CHUNKED, GatherChunkRows<BN, S::THREADS>, GatherFeatureRows<BN, S::THREADS>> lb;
-    if constexpr (CHUNKED) la.init(p.A, p.lda, p.M, m0, tid);
-    lb.init(g, n0, tid);
-    auto fetch = [&](int kt) {
-        if constexpr (CHUNKED) la.load(kt);
-        else la.load(p.A, p.lda, m0, p.M, kt, k_end, tid);
-        lb.load(g, kt, k_end, tid);
-    };
-    auto store = [&](float* a_lds, float* b_lds) {
-        la.template store<S::LDA_S>(a_lds, tid);
-        lb.template store<S::LDB_S>(b_lds, tid);
-    };
+    // Chunked products (K a multiple of BK) read the kernel order with buffer loads too, two stages
+    // ahead (two register slots of loaders).
+    using LoadA = std::conditional_t<CHUNKED, BufferRowTile<BM, BK, S::THREADS>, TileLoader<BM, BK, S::THREADS, VA>>;
+    using LoadB = std::conditional_t<CHUNKED, GatherChunkRows<BN, S::THREADS>, GatherFeatureRows<BN, S::THREADS>>;
+    LoadA la[CHUNKED ? 2 : 1];
+    LoadB lb[CHUNKED ? 2 : 1];
+#pragma unroll
+    for (int i = 0; i < (CHUNKED ? 2 : 1); ++i) {
+        if constexpr (CHUNKED) la[i].init(p.A, p.lda, p.M, m0, tid);
+        lb[i].init(g, n0, tid);
+    }
     v16f acc[S::TM][S::TN];
     zero_acc<S>(acc);
     // Two-level FP32 sum: 32-term stage sums on the matrix cores, added in FP32. Measured on the
@@ -352,7 +349,27 @@ __device__ __forceinline__ void implicit_forward_tile(const GemmParams& p, const
     // below one 576-4608-term chain (below the NumPy float32 path's) for 2 % of their time; FP64
     // totals were 3x more accurate still but cost 7 % (registers: one workgroup less per CU).
     StageSums<S, float> sums;
-    mfma_k_loop<S>(smem, k_begin, k_end, fetch, store, acc, wm0, wn0, lane, sums);
+    if constexpr (CHUNKED) {
+        auto fetch = [&](auto slot, int kt) {
+            la[decltype(slot)::value].load(kt);
+            lb[decltype(slot)::value].load(g, kt, k_end, tid);
+        };
+        auto store = [&](auto slot, float* a_lds, float* b_lds) {
+            la[decltype(slot)::value].template store<S::LDA_S>(a_lds, tid);
+            lb[decltype(slot)::value].template store<S::LDB_S>(b_lds, tid);
+        };
+        mfma_k_loop_ahead<S>(smem, k_begin, k_end, fetch, store, acc, wm0, wn0, lane, sums);
+    } else {
+        auto fetch = [&](int kt) {
+            la[0].load(p.A, p.lda, m0, p.M, kt, k_end, tid);
+            lb[0].load(g, kt, k_end, tid);
+        };
+        auto store = [&](float* a_lds, float* b_lds) {
+            la[0].template store<S::LDA_S>(a_lds, tid);
+            lb[0].template store<S::LDB_S>(b_lds, tid);
+        };
+        mfma_k_loop<S>(smem, k_begin, k_end, fetch, store, acc, wm0, wn0, lane, sums);
+    }
     sums.rounded(acc);
     store_acc<S>(p, C, acc, m0, n0, wm0, wn0, lane);
 }
