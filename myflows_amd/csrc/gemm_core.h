@@ -382,12 +382,12 @@ __device__ __forceinline__ void mfma_k_loop(float* smem, int k_begin, int k_end,
 // t starts, into one of two register slots, so a stage's reads have two stages of MFMAs to arrive
 // before they are stored to LDS (at the end of stage t + 1) instead of one. fetch(slot, kt) and
 // store(slot, a_lds, b_lds) take the slot as std::integral_constant<int, 0 or 1>: stage t uses slot
-// t % 2 and LDS buffer t % 2. The MFMAs, their operands and their order are mfma_k_loop's
-// (STAGE_PLAIN), so the results are its bits. fetch is issued for every stage, also for the two past
+// t % 2 and LDS buffer t % 2. The MFMAs, their operands and their order are mfma_k_loop's (with
+// ORDER STAGE_PLAIN or STAGE_MID_STORE), so the results are its bits. fetch is issued for every stage, also for the two past
 // the end (kt >= k_end), so that the compiler sees the same loads in flight on every path and waits
 // for exactly one stage's: a loader must read nothing (or stay in bounds) there, as the buffer
 // loaders do, whose out-of-range lanes read zero.
-template <class S, class Fetch, class Store, class Drain = KeepChain>
+template <class S, int ORDER = STAGE_PLAIN, class Fetch, class Store, class Drain = KeepChain>
 __device__ __forceinline__ void mfma_k_loop_ahead(float* smem, int k_begin, int k_end, Fetch&& fetch, Store&& store,
                                                   v16f (&acc)[S::TM][S::TN], int wm0, int wn0, int lane,
                                                   Drain&& drain = Drain{}) {
@@ -411,8 +411,15 @@ __device__ __forceinline__ void mfma_k_loop_ahead(float* smem, int k_begin, int 
         if (t > 0) drain(acc);
         const float* As = smem + T * S::STAGE;
         float* next = smem + (1 - T) * S::STAGE;
-        mfma_stage<S, 0, S::HALF, RESTART>(As, As + S::A_SIZE, acc, wm0, wn0, lane);
-        if (t + 1 < stages) store(Other{}, next, next + S::A_SIZE);
+        if constexpr (ORDER == STAGE_MID_STORE && S::HALF >= 8) {
+            constexpr int MID = S::HALF / 8 * 4;
+            mfma_stage<S, 0, MID, RESTART>(As, As + S::A_SIZE, acc, wm0, wn0, lane);
+            if (t + 1 < stages) store(Other{}, next, next + S::A_SIZE);
+            mfma_stage<S, MID, S::HALF>(As, As + S::A_SIZE, acc, wm0, wn0, lane);
+        } else {
+            mfma_stage<S, 0, S::HALF, RESTART>(As, As + S::A_SIZE, acc, wm0, wn0, lane);
+            if (t + 1 < stages) store(Other{}, next, next + S::A_SIZE);
+        }
         __syncthreads();
     };
     for (int t = 0; t < stages; t += 2) {

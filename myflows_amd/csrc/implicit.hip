@@ -422,32 +422,44 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void conv_implicit_wgra
     float* __restrict__ C = p.C + (p.split ? z * p.c_batch : 0);
     const int ohw = g.OH * g.OW;
 
+    // Chunked products read two stages ahead (two register slots of loaders).
+    constexpr int SLOTS = CHUNKED ? 2 : 1;
     using RowLoader = GradRowsInPlace<BM, S::THREADS>;
-    RowLoader la;
-    std::conditional_t<CHUNKED, GatherTapColumns<BN, S::THREADS>, GatherPixelColumns<BN, S::THREADS>> lb;
-    lb.init(g, n0, tid);
+    RowLoader la[SLOTS];
+    std::conditional_t<CHUNKED, GatherTapColumns<BN, S::THREADS>, GatherPixelColumns<BN, S::THREADS>> lb[SLOTS];
+#pragma unroll
+    for (int i = 0; i < SLOTS; ++i) lb[i].init(g, n0, tid);
     const bool summing = SUMS && tile_n == 0;
     double row_sums[RowLoader::PER];
 #pragma unroll
     for (int i = 0; i < RowLoader::PER; ++i) row_sums[i] = 0.0;
-    auto fetch = [&](int kt) {
+    auto fetch_slot = [&](int slot, int kt) {
         const PixelAt at = pixel_at(g, kt + tid % BK_WG, k_end);
-        la.load(p.A, p.M, ohw, m0, at, tid);
-        lb.load(g, at);
+        la[slot].load(p.A, p.M, ohw, m0, at, tid);
+        lb[slot].load(g, at);
     };
-    auto store = [&](float* a_lds, float* b_lds) {
-        la.template store<S::LDA_S>(a_lds, tid);
-        lb.template store<S::LDB_S>(b_lds, tid);
+    auto store_slot = [&](int slot, float* a_lds, float* b_lds) {
+        la[slot].template store<S::LDA_S>(a_lds, tid);
+        lb[slot].template store<S::LDB_S>(b_lds, tid);
         if constexpr (SUMS)
-            if (summing) la.add_to(row_sums);
+            if (summing) la[slot].add_to(row_sums);
     };
     v16f acc[S::TM][S::TN];
     zero_acc<S>(acc);
-    mfma_k_loop<S, STAGE_MID_STORE>(smem, k_begin, k_end, fetch, store, acc, wm0, wn0, lane);
+    if constexpr (CHUNKED) {
+        mfma_k_loop_ahead<S, STAGE_MID_STORE>(
+            smem, k_begin, k_end, [&](auto slot, int kt) { fetch_slot(decltype(slot)::value, kt); },
+            [&](auto slot, float* a_lds, float* b_lds) { store_slot(decltype(slot)::value, a_lds, b_lds); }, acc, wm0,
+            wn0, lane);
+    } else {
+        mfma_k_loop<S, STAGE_MID_STORE>(
+            smem, k_begin, k_end, [&](int kt) { fetch_slot(0, kt); },
+            [&](float* a_lds, float* b_lds) { store_slot(0, a_lds, b_lds); }, acc, wm0, wn0, lane);
+    }
     store_acc<S>(p, C, acc, m0, n0, wm0, wn0, lane);
     if constexpr (SUMS)
         if (summing)
-            la.store_sums(row_sums, sums + static_cast<long long>(z) * p.M, p.split ? nullptr : db, p.M, m0, tid);
+            la[0].store_sums(row_sums, sums + static_cast<long long>(z) * p.M, p.split ? nullptr : db, p.M, m0, tid);
 }
 
 // The kernel as the A operand of an implicit product: out[o][k] for O rows and features k over C
