@@ -434,6 +434,63 @@ def test_stem_weight_gradient_at_batch_64_is_exact_on_integer_data():
     np.testing.assert_array_equal(host(db), rows.sum(axis=1))
 
 
+def _stem_reference(x, w, stride, padding):
+    """FP64 convolution through explicit windows (no im2col code of the library)."""
+    kh, kw = w.shape[2:]
+    padded = np.pad(x.astype(np.float64), ((0, 0), (0, 0), (padding[0],) * 2, (padding[1],) * 2))
+    windows = np.lib.stride_tricks.sliding_window_view(padded, (kh, kw), axis=(2, 3))
+    windows = windows[:, :, ::stride[0], ::stride[1]]
+    n, c, oh, ow = windows.shape[:4]
+    cols = windows.transpose(0, 2, 3, 1, 4, 5).reshape(n * oh * ow, c * kh * kw)
+    out = cols @ w.astype(np.float64).reshape(w.shape[0], -1).T
+    return out.reshape(n, oh, ow, -1).transpose(0, 3, 1, 2)
+
+
+@pytest.mark.parametrize("shape,kernel,stride,padding,co", [
+    ((64, 3, 120, 160), (7, 7), (2, 2), (3, 3), 64),   # the ResNet18 stem at batch 64
+    ((3, 3, 33, 47), (7, 5), (1, 1), (2, 2), 70),      # five taps per row, two channel tiles
+    ((2, 3, 17, 29), (7, 8), (2, 3), (0, 4), 16),      # eight taps, uneven strides
+])
+def test_stem_forward_is_exact_on_integer_data(shape, kernel, stride, padding, co):
+    """Stem-shaped forwards (3 input channels, a 7-row window of 5-8 taps, the natural feature
+    order of the implicit product) on integer data, where every float32 sum is exact: y equals the
+    FP64 convolution bit for bit, with bias and ReLU applied as the implicit epilogue does (bias
+    after the sum, then the activation)."""
+    print("stem forward", shape, kernel, stride, padding, co, flush=True)
+    rng = np.random.default_rng(31)
+    x = rng.integers(-2, 3, size=shape).astype(np.float32)
+    w = rng.integers(-2, 3, size=(co, 3, *kernel)).astype(np.float32)
+    bias = rng.integers(-3, 4, size=co).astype(np.float32)
+    ref = _stem_reference(x, w, stride, padding)
+    y, _ = native.conv2d_forward(gpu(x), gpu(w), stride=stride, padding=padding, algorithm="implicit")
+    np.testing.assert_array_equal(host(y), ref)
+    y, _ = native.conv2d_forward(gpu(x), gpu(w), gpu(bias), stride=stride, padding=padding, activation="relu",
+                                 algorithm="implicit")
+    np.testing.assert_array_equal(host(y), np.maximum(ref + bias.reshape(1, -1, 1, 1), 0.0))
+
+
+def test_stem_forward_keeps_an_inf_out_of_windows_that_do_not_cover_it():
+    """An Inf in the input reaches exactly the outputs whose windows cover it (as Inf, or NaN where
+    the weight on it is zero): a gather that read a pixel beside a window, even under a zero weight,
+    would turn that output into NaN."""
+    print("stem inf", flush=True)
+    rng = np.random.default_rng(5)
+    x = rng.integers(-2, 3, size=(1, 3, 20, 24)).astype(np.float32)
+    w = rng.integers(-2, 3, size=(8, 3, 7, 7)).astype(np.float32)
+    x[0, 1, 9, 12] = np.inf
+    y = host(native.conv2d_forward(gpu(x), gpu(w), stride=(2, 2), padding=(3, 3), algorithm="implicit")[0])
+    covered = np.zeros(y.shape[2:], dtype=bool)
+    for oh in range(y.shape[2]):
+        for ow in range(y.shape[3]):
+            covered[oh, ow] = 0 <= 9 - (2 * oh - 3) < 7 and 0 <= 12 - (2 * ow - 3) < 7
+    assert covered.any() and (~covered).any()
+    assert np.isfinite(y[:, :, ~covered]).all() and not np.isfinite(y[:, :, covered]).any()
+    # Inf (nonzero weight) or NaN (zero weight) where the window covers the Inf, as in FP64.
+    with np.errstate(invalid="ignore"):
+        ref = _stem_reference(x, w, (2, 2), (3, 3))
+    np.testing.assert_array_equal(y, ref)
+
+
 IMPLICIT_TILES = 12  # tiles of the implicit products (plan code 16 + tile * 128 + slices - 1)
 
 
