@@ -795,7 +795,8 @@ GemmPlan wgrad_plan(int M, int N, int K) {
 // Measured plans: products whose best tile and split, in a sweep of every tile and split on MI355X,
 // beat the automatic plan below by at least 2 % (ResNet18's batch-64 convolutions at 3x120x160, and
 // its batch-256 inference forwards at 224x224). The forward-orientation entries were re-measured for
-// the two-level stage sums, whose extra registers cost tiles 8, 10 and 11 a resident workgroup.
+// the two-level stage sums, whose extra registers cost tiles 8, 10 and 11 a resident workgroup; the
+// dW entries for the reads two stages ahead.
 // Key: orientation (0 forward / dX, 1 dW), M, N, K; value: tile and requested K split.
 struct MeasuredPlan {
     int wgrad, M, N, K, tile, requested;
@@ -823,11 +824,14 @@ constexpr MeasuredPlan MEASURED_PLANS[] = {
     {0, 512, 12544, 4608, 9, 4},   // layer4 3x3
     {1, 64, 147, 307200, 6, 256},  // stem dW (more slices than the dW rule makes: its gathers need the waves)
     {1, 64, 576, 72384, 8, 96},    // layer1 dW
-    {1, 128, 576, 19200, 10, 48},  // layer2.0 conv1 dW
-    {1, 128, 1152, 19200, 10, 48}, // layer2 3x3 dW
+    {1, 128, 576, 19200, 8, 48},   // layer2.0 conv1 dW
+    {1, 128, 1152, 19200, 8, 24},  // layer2 3x3 dW
     {1, 128, 64, 19200, 6, 128},   // layer2 1x1 downsample dW
-    {1, 256, 1152, 5120, 9, 32},   // layer3.0 conv1 dW
-    {1, 512, 2304, 1280, 9, 8},    // layer4.0 conv1 dW
+    {1, 256, 1152, 5120, 6, 24},   // layer3.0 conv1 dW
+    {1, 256, 2304, 5120, 8, 16},   // layer3 3x3 dW
+    {1, 256, 128, 5120, 6, 32},    // layer3 1x1 downsample dW
+    {1, 512, 2304, 1280, 8, 8},    // layer4.0 conv1 dW
+    {1, 512, 256, 1280, 6, 8},     // layer4 1x1 downsample dW
     {1, 512, 4608, 1280, 8, 8},    // layer4 3x3 dW
 };
 

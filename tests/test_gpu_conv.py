@@ -614,6 +614,7 @@ PLAN_GEOMETRIES = (
     ("bs64-layer3-1x1", (64, 128, 15, 20), (256, 128, 1, 1), 2, 0, ("forward", "dx", "dw")),
     ("bs64-layer4.0-conv1", (64, 256, 8, 10), (512, 256, 3, 3), 2, 1, ("forward", "dx", "dw")),
     ("bs64-layer4-3x3", (64, 512, 4, 5), (512, 512, 3, 3), 1, 1, ("forward", "dx", "dw")),
+    ("bs64-layer4-1x1", (64, 256, 8, 10), (512, 256, 1, 1), 2, 0, ("forward", "dx", "dw")),
     ("bs256-stem", (256, 3, 224, 224), (64, 3, 7, 7), 2, 3, ("forward",)),
     ("bs256-layer1", (256, 64, 55, 55), (64, 64, 3, 3), 1, 1, ("forward",)),
     ("bs256-layer2.0-conv1", (256, 64, 55, 55), (128, 64, 3, 3), 2, 1, ("forward",)),
