@@ -515,7 +515,7 @@ def main():
     torch.cuda.set_device(0)
     native._library()
     opt, _ = build_step(args.batch, 120, 160, optimize=not args.plain_graph)
-    opt.graph.overlap_weight_grads = not args.single_stream
+    opt.graph.overlap_weight_grads = opt.graph.overlap_branches = not args.single_stream
     seconds = time_steps(opt, args.steps, args.warmup)
     ms_per_step = seconds * 1e3 / args.steps
     images_per_s = args.batch * args.steps / seconds

@@ -167,6 +167,13 @@ class _Plan:
     pre_clear: dict         # non-GradientOp unit -> its parents that need a zero gradient first
     keep: tuple             # nodes whose gradient survives backward (leaves, retained nodes)
     groups: frozenset       # fused groups in use
+    forward_steps: tuple    # forward_units with shortcut branches on the side stream: (unit, step kind)
+
+
+# Kinds of a forward step: a unit on the current stream, the fork of a branch (the side stream waits
+# for the current one), a unit of that branch (issued on the side stream), the join before the
+# branch's consumer (the current stream waits for the side stream).
+MAIN, FORK, SIDE, JOIN = 0, 1, 2, 3
 
 
 class Graph:
@@ -194,6 +201,9 @@ class Graph:
         # Whether backward() runs the convolutions' dW products on the weight-gradient stream
         # (streams.py) beside their dX products; the gradients are the same either way.
         self.overlap_weight_grads = True
+        # Whether forward() runs convolution + batch-norm shortcut branches (a ResNet downsample) on
+        # the side stream beside the main path; the values are the same either way.
+        self.overlap_branches = True
         self._leaves = tuple(node for node in self.nodes if not node.parents)
         self._retained = set()
         self._plans = {}
@@ -223,7 +233,49 @@ class Graph:
         pre_clear = {n: tuple(p for p in n.parents if needs[p]) for n in propagating if not isinstance(n, GradientOp)}
         keep = tuple(n for n in self.nodes if needs[n] and (not n.parents or n in self._retained))
         return _Plan(tuple(needs.items()), frozenset(n for n, need in needs.items() if need), forward_units,
-                     backward_units, pre_clear, keep, frozenset(groups))
+                     backward_units, pre_clear, keep, frozenset(groups),
+                     self._forward_steps(forward_units, groups))
+
+    def _forward_steps(self, forward_units, groups):
+        """forward_units with every convolution + batch-norm shortcut (a ResNet downsample: a Conv2D
+        whose only consumer is a BatchNorm2d whose only consumer is the residual Add of a fused
+        BN+Add+ReLU unit) moved up to just after the unit that makes the convolution's input and
+        issued on the side stream, so that it runs beside the main path's convolutions; the fused
+        unit waits for it. Each node still runs after its parents and before its consumers."""
+        from .ops_conv import Conv2D_Op
+        from .ops_norm import BatchNorm2d_Op, BatchNormActivation
+        consumers = {}
+        for node in self.nodes:
+            for parent in node.parents:
+                consumers.setdefault(parent, set()).add(node)
+        units = list(forward_units)
+        producer = {}
+        for unit in units:
+            producer[getattr(unit, "output", unit)] = unit
+        branches = []
+        for consumer in units:
+            if not isinstance(consumer, BatchNormActivation) or consumer.residual is None or consumer.add is None:
+                continue
+            bn = consumer.residual
+            conv = bn.parents[0] if isinstance(bn, BatchNorm2d_Op) else None
+            if (not isinstance(conv, Conv2D_Op) or bn not in units or conv not in units
+                    or consumers.get(bn) != {consumer.add} or consumers.get(conv) != {bn}
+                    or any(p.parents for p in conv.parents[1:] + bn.parents[1:])):
+                continue
+            branches.append((conv, bn, consumer))
+        if not branches:
+            return tuple((unit, MAIN) for unit in units)
+        for conv, bn, _ in branches:
+            units.remove(conv)
+            units.remove(bn)
+        steps = [(unit, MAIN) for unit in units]
+        for conv, bn, consumer in branches:
+            anchor = producer.get(conv.parents[0])
+            at = 0 if anchor is None else next(i for i, (u, _) in enumerate(steps) if u is anchor) + 1
+            steps[at:at] = [(None, FORK), (conv, SIDE), (bn, SIDE)]
+            join = next(i for i, (u, _) in enumerate(steps) if u is consumer)
+            steps.insert(join, (None, JOIN))
+        return tuple(steps)
 
     def _plan(self):
         flags = tuple(leaf.requires_grad for leaf in self._leaves)
@@ -245,17 +297,53 @@ class Graph:
         self._forward_plan = plan
         profiler = self.profiler
         served = _prepare_weight_orders((u for u in plan.forward_units if u.parents), "forward")
-        for unit in plan.forward_units:
+        if profiler is None and self.overlap_branches:
+            self._run_steps(plan.forward_steps)
+        else:
+            for unit in plan.forward_units:
+                if not unit.parents:
+                    continue
+                inputs = [p.value for p in unit.parents]
+                if profiler is None:
+                    unit.forward(*inputs)
+                else:
+                    with profiler.node(unit, "forward"):
+                        unit.forward(*inputs)
+        for unit in served:
+            unit.drop_weight_orders("forward")
+
+    @staticmethod
+    def _run_steps(steps):
+        """Run forward steps (see _forward_steps). A branch takes the side stream only when its input
+        is a GPU tensor; otherwise its units run in place, in the same order."""
+        from . import native
+        side = main = None
+        for unit, kind in steps:
+            if kind == FORK:
+                side = main = None
+                continue
+            if kind == JOIN:
+                if side is not None:
+                    native.stream_wait(main, side)
+                side = main = None
+                continue
             if not unit.parents:
                 continue
             inputs = [p.value for p in unit.parents]
-            if profiler is None:
-                unit.forward(*inputs)
-            else:
-                with profiler.node(unit, "forward"):
-                    unit.forward(*inputs)
-        for unit in served:
-            unit.drop_weight_orders("forward")
+            if kind == SIDE:
+                if side is None and main is None:
+                    x = inputs[0]
+                    if isinstance(x, torch.Tensor) and x.is_cuda:
+                        main = native._stream()
+                        side = streams.side_stream(native.current_device_index()).cuda_stream
+                        native.stream_wait(side, main)
+                    else:
+                        main = False  # no side stream for this branch
+                if side is not None:
+                    with native.launch_stream(side):
+                        unit.forward(*inputs)
+                    continue
+            unit.forward(*inputs)
 
     def backward(self, loss_scale=1.0):
         plan = self._plan()

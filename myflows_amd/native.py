@@ -16,9 +16,11 @@ There is no fallback: without the library or a GPU every entry point raises.
 
 from __future__ import annotations
 
+import contextlib
 import ctypes
 import json
 import os
+import threading
 from dataclasses import dataclass
 from functools import lru_cache
 
@@ -168,11 +170,30 @@ def _addr(tensor):
     return 0 if tensor is None else tensor.data_ptr()
 
 
+_launch = threading.local()
+
+
 def _stream():
-    """The raw handle (hipStream_t) of the current stream on the current device. torch's own
-    accessor is taken directly: torch.cuda.current_stream() costs several microseconds of Python
-    per call, paid for every launch."""
-    return _raw_stream(_current_device())
+    """The raw handle (hipStream_t) the library's calls are issued on: the one set by launch_stream,
+    else the current stream on the current device. torch's own accessor is taken directly:
+    torch.cuda.current_stream() costs several microseconds of Python per call, paid for every
+    launch."""
+    override = getattr(_launch, "stream", None)
+    return override if override is not None else _raw_stream(_current_device())
+
+
+@contextlib.contextmanager
+def launch_stream(handle):
+    """Issue the library calls made in the block (on this thread) on raw stream `handle` instead of
+    the current stream. Tensors are still allocated on the current stream: the caller orders
+    `handle` after the current stream's work on them (stream_wait) and the current stream after
+    `handle` before that memory is read or freed there."""
+    previous = getattr(_launch, "stream", None)
+    _launch.stream = handle
+    try:
+        yield
+    finally:
+        _launch.stream = previous
 
 
 try:

@@ -263,33 +263,45 @@ def test_resnet18_two_steps_are_deterministic():
 
 
 def test_weight_gradient_stream_gives_the_single_stream_gradients_bit_for_bit(monkeypatch):
-    """Graph.backward with the convolutions' dW products on the weight-gradient stream (the
-    default) against the same passes on one stream: the same bits for every gradient and every
-    updated parameter over two Adam steps at batch 8, and the stream is left joined and idle."""
-    from myflows_amd import streams
+    """Graph.backward with the convolutions' dW products on the weight-gradient stream and
+    Graph.forward with the downsample shortcuts on the side stream (the defaults) against the same
+    passes on one stream: the same bits for every output, gradient and updated parameter over two
+    Adam steps at batch 8, and the stream is left joined and idle."""
+    from myflows_amd import native, streams
 
-    forks = []
+    forks, side_launches = [], []
     original = streams.WeightGradSession.fork
+    original_launch = native.launch_stream
 
     def counting(self):
         forks.append(1)
         return original(self)
 
+    def counting_launch(handle):
+        side_launches.append(handle)
+        return original_launch(handle)
+
     monkeypatch.setattr(streams.WeightGradSession, "fork", counting)
+    monkeypatch.setattr(native, "launch_stream", counting_launch)
     runs = []
     for overlap in (False, True):
         forks.clear()
+        side_launches.clear()
         model, graph, _, _, _, _ = build_resnet(8, 64, 80, base_width=16, optimize=True)
-        graph.overlap_weight_grads = overlap
+        graph.overlap_weight_grads = graph.overlap_branches = overlap
         opt = mf.Adam(graph, learning_rate=1e-3)
-        grads = []
+        grads, outputs = [], []
         for _ in range(2):
             opt.one_step()
+            outputs.append(host(graph.target_node.value))
             grads.append([host(p.grad) for p in model.params])
             opt.update()
-        runs.append((grads, [host(p.value) for p in model.params], len(forks)))
+        runs.append((grads, [host(p.value) for p in model.params], len(forks), len(side_launches), outputs))
         assert streams.active() is None
     assert runs[0][2] == 0 and runs[1][2] == 2 * 20  # ResNet18's 20 convolutions, two passes
+    assert runs[0][3] == 0 and runs[1][3] == 2 * 3 * 2  # three downsample conv + BN shortcuts, two passes
+    for a, b in zip(runs[0][4], runs[1][4]):
+        np.testing.assert_array_equal(a, b)
     for step_a, step_b in zip(runs[0][0], runs[1][0]):
         for a, b in zip(step_a, step_b):
             np.testing.assert_array_equal(a, b)
