@@ -268,3 +268,59 @@ def test_graph_rewrites_on_cpu():
     finally:
         if torch.cuda.is_available():
             mf.set_device("cuda")
+
+
+def test_forward_steps_put_downsample_shortcuts_beside_the_main_path():
+    """Graph._forward_steps (no device work): a BasicBlock with a downsample takes its 1x1 conv and
+    BN onto the side stream right after the block input is made and joins before the fused
+    BN+Add+ReLU; every unit still runs after its parents; a block without a downsample, or a
+    shortcut BN with a second consumer, keeps one stream."""
+    from myflows_amd import graph as G
+
+    def steps_of(root):
+        graph = mf.Graph(root, optimize=True)
+        return [(u, k) for u, k in graph._plan().forward_steps if u is None or u.parents]
+
+    def check_order(steps):
+        done = set()
+        for unit, _ in steps:
+            if unit is None:
+                continue
+            for parent in unit.parents:
+                producer_known = not parent.parents or parent in done
+                assert producer_known, f"{unit.name} runs before its parent {parent.name}"
+            done.add(getattr(unit, "output", unit))
+            done.update(getattr(unit, "hidden", ()))
+
+    mf.set_device("cpu")
+    try:
+        x = mf.Variable(torch.zeros((1, 4, 8, 8)), requires_grad=False)
+        stem = mf.ReLU(mf.BatchNorm2d(4)(mf.Conv2D(4, 4, 3, padding=1, fuse_activation=False,
+                                                   backend="hip_native")(x)))
+        block = mf.BasicBlock(4, 8, stride=2, conv_backend="hip_native")
+        steps = steps_of(block(stem))
+        kinds = [k for _, k in steps]
+        assert kinds.count(G.FORK) == 1 and kinds.count(G.JOIN) == 1 and kinds.count(G.SIDE) == 2
+        fork, join = kinds.index(G.FORK), kinds.index(G.JOIN)
+        side = [u for u, k in steps if k == G.SIDE]
+        assert [type(u).__name__ for u in side] == ["Conv2D_Op", "BatchNorm2d_Op"]
+        assert steps[fork - 1][0].name == "BatchNormReLU"  # right after the block input is made
+        assert steps[join + 1][0].name == "BatchNormAddReLU"  # the fused unit that reads the shortcut
+        assert all(k == G.MAIN for _, k in steps[fork + 3:join])  # the main path between them
+        check_order(steps)
+
+        plain = mf.BasicBlock(8, 8, stride=1, conv_backend="hip_native")
+        steps = steps_of(plain(mf.Variable(torch.zeros((1, 8, 4, 4)), requires_grad=False)))
+        assert all(k == G.MAIN for _, k in steps)
+
+        conv = mf.Conv2D(4, 8, 1, stride=2, fuse_activation=False, backend="hip_native")
+        bn = mf.BatchNorm2d(8)
+        shortcut = bn(conv(stem))
+        main = mf.BatchNorm2d(8)(mf.Conv2D(4, 8, 3, stride=2, padding=1, fuse_activation=False,
+                                            backend="hip_native")(stem))
+        out = mf.Add(mf.ReLU(mf.Add(main, shortcut)), shortcut)  # the shortcut BN has two consumers
+        steps = steps_of(out)
+        assert all(k == G.MAIN for _, k in steps)
+    finally:
+        if torch.cuda.is_available():
+            mf.set_device("cuda")
