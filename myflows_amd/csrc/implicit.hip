@@ -92,16 +92,20 @@ struct GatherFeatureRows {
 // tap is uniform over the stage, so a wave may span two rows (BN a multiple of 32). The loads are
 // buffer loads: a lane's offset is its pixel's window origin plus the stage's (uniform) channel
 // chunk and tap, or BUFFER_OOB when the tap falls outside the image, and the PER channels of a
-// thread are a uniform stride apart. A stage then costs a handful of vector instructions besides
-// its loads, and the loads need no branches (the matrix cores and the vector ALU of a SIMD do not
-// run at the same time, so every vector instruction of the loop is time the MFMAs lose).
+// thread (a contiguous run of the chunk) are one plane apart. A stage then costs a handful of vector
+// instructions besides its loads, and the loads need no branches (the matrix cores and the vector
+// ALU of a SIMD do not run at the same time, so every vector instruction of the loop is time the
+// MFMAs lose). The tile is stored pixel-major ([BN][BK + 4]): a thread writes its channel run with
+// 16-byte stores, and the MFMA loop reads four channels of a pixel with one 16-byte read, as it
+// reads the kernel operand.
 template <int BN, int THREADS>
 struct GatherChunkRows {
     static_assert(BN % 32 == 0 && THREADS % BN == 0, "whole rows per thread group");
     static constexpr int RSTEP = THREADS / BN, PER = BK / RSTEP;
-    static_assert(BK == CHANNEL_CHUNK && BK % RSTEP == 0, "one stage is one channel chunk");
+    static_assert(BK == CHANNEL_CHUNK && BK % RSTEP == 0 && PER % 4 == 0,
+                  "one stage is one channel chunk, in runs of whole float4s per thread");
     __amdgpu_buffer_rsrc_t rsrc;
-    int origin, ih0, iw0;  // origin: offset of channel tid / BN at window position (0, 0) (may be negative)
+    int origin, ih0, iw0;  // origin: offset of channel (tid / BN) * PER at window position (0, 0) (may be negative)
     bool valid;
     float v[PER];
 
@@ -114,7 +118,7 @@ struct GatherChunkRows {
         const int oh = g.div_ow.divmod(rem, ow);
         ih0 = oh * g.SH - g.PH;
         iw0 = ow * g.SW - g.PW;
-        origin = n * g.chw + (tid / BN) * g.hw + ih0 * g.W + iw0;
+        origin = n * g.chw + (tid / BN) * PER * g.hw + ih0 * g.W + iw0;
     }
 
     __device__ __forceinline__ void load(const ConvGather& g, int kt, int k_end, int tid) {
@@ -126,16 +130,17 @@ struct GatherChunkRows {
                         static_cast<unsigned>(iw) < static_cast<unsigned>(g.W);
         const int uniform = chunk * CHANNEL_CHUNK * g.hw + kh * g.W + kw;
         const unsigned lane_bytes = ok ? static_cast<unsigned>(origin + uniform) * 4u : BUFFER_OOB;
-        const int step_bytes = RSTEP * g.hw * 4;
+        const int step_bytes = g.hw * 4;
 #pragma unroll
         for (int i = 0; i < PER; ++i) v[i] = buffer_load(rsrc, lane_bytes, i * step_bytes);
     }
 
     template <int LD>
     __device__ __forceinline__ void store(float* lds, int tid) const {
-        const int r0 = tid / BN, col = tid % BN;
+        float* row = lds + (tid % BN) * LD + (tid / BN) * PER;
 #pragma unroll
-        for (int i = 0; i < PER; ++i) lds[(r0 + i * RSTEP) * LD + col] = v[i];
+        for (int q = 0; q < PER / 4; ++q)
+            *reinterpret_cast<float4*>(row + 4 * q) = make_float4(v[4 * q], v[4 * q + 1], v[4 * q + 2], v[4 * q + 3]);
     }
 };
 
@@ -322,7 +327,8 @@ struct GradRowsInPlace {
 template <int BM, int BN, int WM, int WN, bool VA, bool CHUNKED>
 __device__ __forceinline__ void implicit_forward_tile(const GemmParams& p, const ConvGather& g, int tile_m, int tile_n,
                                                       int z) {
-    using S = MfmaShape<BM, BN, BK, WM, WN, false, false>;
+    // The chunked gather stores its tile pixel-major (TB), the natural-order one feature-major.
+    using S = MfmaShape<BM, BN, BK, WM, WN, false, CHUNKED>;
     __shared__ __attribute__((aligned(16))) float smem[2 * S::STAGE];
     const int tid = threadIdx.x, wave = tid / 64, lane = tid % 64;
     const int wm0 = (wave / S::WGN) * WM, wn0 = (wave % S::WGN) * WN;
