@@ -169,7 +169,10 @@ class Conv2D_Op(GradientOp):
                 extra["input_grad"] = target
         engine = NATIVE_BACKENDS[self.actual_backend]
         session = streams.active()
-        if implicit and (need_w or need_b) and session is not None and session.usable():
+        # A product with no dX beside it (a frozen input, such as a network's first convolution)
+        # stays on this stream: there it runs beside the dW products already queued on the side
+        # stream instead of after them.
+        if implicit and need_x and (need_w or need_b) and session is not None and session.usable():
             # dW and db on the weight-gradient stream, dX on this one (the same products and plans as
             # the one-stream call below)
             side, hold = session.fork()
