@@ -397,21 +397,22 @@ __global__ __launch_bounds__(256) void pool_forward_plane_kernel(const float* __
         int best;
         const float value = window_max(tile, first, W, KH, KW, best);
         const long long out = static_cast<long long>(first_plane) * ohw + o;
-        y[out] = value;
-        argmax[out] = static_cast<int>(base + best);
+        __builtin_nontemporal_store(value, y + out);
+        __builtin_nontemporal_store(static_cast<int>(base + best), argmax + out);
     }
 }
 
 // Max-pool backward over `per` consecutive planes per workgroup: the planes' dy and argmax are
 // staged in LDS, then every input pixel gathers the windows that cover it, in (oh, ow) order.
-// VEC4 (W a multiple of 4, dx 16-byte aligned): a thread takes four adjacent pixels of one row and
-// stores them with one 16-byte write.
+// div_plane and div_row divide by the units of a plane and of a row: pixels (H*W, W), or under VEC4
+// (W a multiple of 4, dx 16-byte aligned) blocks of two rows by four columns ((H+1)/2 * W/4, W/4),
+// whose gradients a thread forms together and writes with two non-temporal 16-byte stores.
 template <bool VEC4>
 __global__ __launch_bounds__(256) void pool_backward_plane_kernel(const float* __restrict__ dy,
                                                                   const int* __restrict__ argmax,
                                                                   float* __restrict__ dx, int planes, int per, int H,
                                                                   int W, int OH, int OW, int KH, int KW,
-                                                                  FastDiv div_hw, FastDiv div_w, FastDiv div_sh,
+                                                                  FastDiv div_plane, FastDiv div_row, FastDiv div_sh,
                                                                   FastDiv div_sw) {
     extern __shared__ float staged[];  // per * OH * OW floats of dy, then as many int32 argmax
     const int first_plane = blockIdx.x * per;
@@ -443,19 +444,24 @@ __global__ __launch_bounds__(256) void pool_backward_plane_kernel(const float* _
     __syncthreads();
     const long long in_base = static_cast<long long>(first_plane) * hw;
     if constexpr (VEC4) {
-        for (int e = 4 * threadIdx.x; e < count * hw; e += 4 * 256) {
-            int within, iw;
-            const int pl = div_hw.divmod(e, within);
-            const int ih = div_w.divmod(within, iw);
-            const int target = static_cast<int>(in_base + e);
-            *reinterpret_cast<float4*>(dx + in_base + e) =
-                pool_quad_grad(grad, where, pl, ih, iw, target, OH, OW, KH, KW, div_sh, div_sw);
+        const int blocks = count * static_cast<int>(div_plane.d);
+        for (int b = threadIdx.x; b < blocks; b += 256) {
+            int within, col;
+            const int pl = div_plane.divmod(b, within);
+            const int ih = 2 * div_row.divmod(within, col);
+            const int iw = 4 * col;
+            const int rows = min(2, H - ih);
+            const int target = static_cast<int>(in_base) + pl * hw + ih * W + iw;
+            float sum[2][4];
+            pool_rows_grad<2>(grad, where, pl, ih, rows, iw, target, W, OH, OW, KH, KW, div_sh, div_sw, sum);
+            store_streaming4(dx + target, sum[0][0], sum[0][1], sum[0][2], sum[0][3]);
+            if (rows > 1) store_streaming4(dx + target + W, sum[1][0], sum[1][1], sum[1][2], sum[1][3]);
         }
     } else {
         for (int e = threadIdx.x; e < count * hw; e += 256) {
             int within, iw;
-            const int pl = div_hw.divmod(e, within);
-            const int ih = div_w.divmod(within, iw);
+            const int pl = div_plane.divmod(e, within);
+            const int ih = div_row.divmod(within, iw);
             dx[in_base + e] = pool_pixel_grad(grad, where, pl, ih, iw, static_cast<int>(in_base + e), OH, OW, KH, KW,
                                               div_sh, div_sw);
         }
@@ -567,9 +573,11 @@ int launch_pool_backward(const float* dy, const int* argmax, float* dx, int N, i
         const int planes = N * C;
         const size_t lds = static_cast<size_t>(per) * OH * OW * 2 * sizeof(float);
         const bool vec4 = W % 4 == 0 && (reinterpret_cast<std::uintptr_t>(dx) & 15) == 0;
+        const int per_row = vec4 ? W / 4 : W, per_plane = vec4 ? (H + 1) / 2 * per_row : H * W;
         (vec4 ? pool_backward_plane_kernel<true> : pool_backward_plane_kernel<false>)<<<blocks_for(planes, per), 256,
                                                                                        lds, stream>>>(
-            dy, argmax, dx, planes, per, H, W, OH, OW, KH, KW, FastDiv(H * W), FastDiv(W), FastDiv(SH), FastDiv(SW));
+            dy, argmax, dx, planes, per, H, W, OH, OW, KH, KW, FastDiv(per_plane), FastDiv(per_row), FastDiv(SH),
+            FastDiv(SW));
         return MFH_CHECK_LAUNCH("pool_backward_plane", stream);
     }
     pool_backward_kernel<<<blocks_for(total, 256), 256, 0, stream>>>(dy, argmax, dx, total, FastDiv(W), FastDiv(H),

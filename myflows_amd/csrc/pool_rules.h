@@ -72,4 +72,48 @@ __device__ __forceinline__ float4 pool_quad_grad(const float* grad, const int* w
     return make_float4(sum[0], sum[1], sum[2], sum[3]);
 }
 
+// A 16-byte store marked non-temporal: the line goes out to memory without displacing what the
+// caches hold for the rest of the kernel (a pass's output that the pass itself never reads).
+__device__ __forceinline__ void store_streaming4(float* p, float a, float b, float c, float d) {
+    typedef float v4f __attribute__((ext_vector_type(4)));
+    const v4f v = {a, b, c, d};
+    __builtin_nontemporal_store(v, reinterpret_cast<v4f*>(p));
+}
+
+// The gradients of a block of `rows` (at most R) rows by four columns of staged plane pl: rows ih ..
+// ih + rows - 1, columns iw .. iw + 3, pixel (ih, iw) at flat index `target`. Every window that covers
+// any of them is visited once, in (oh, ow) order; a window whose argmax names a pixel of the block
+// covers that pixel, so per pixel the visits that add are pool_pixel_grad's windows in its order and
+// the sums are its bits. Rows ih and ih + 1 of a 3x3 stride-2 pool share two of their three window
+// rows, so a two-row block reads 6 windows for 8 pixels where two quads read 9.
+template <int R>
+__device__ __forceinline__ void pool_rows_grad(const float* grad, const int* where, int pl, int ih, int rows, int iw,
+                                               int target, int W, int OH, int OW, int KH, int KW,
+                                               const FastDiv& div_sh, const FastDiv& div_sw, float (&sum)[R][4]) {
+    const int ohw = OH * OW;
+    const int oh_lo = ih >= KH ? div_sh.div(ih - KH) + 1 : 0;
+    const int oh_hi = min(OH - 1, div_sh.div(ih + rows - 1));
+    const int ow_lo = iw >= KW ? div_sw.div(iw - KW) + 1 : 0;
+    const int ow_hi = min(OW - 1, div_sw.div(iw + 3));
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+        for (int k = 0; k < 4; ++k) sum[r][k] = 0.0f;
+    for (int oh = oh_lo; oh <= oh_hi; ++oh)
+        for (int ow = ow_lo; ow <= ow_hi; ++ow) {
+            const int o = pl * ohw + oh * OW + ow;
+            const int d = where[o] - target;
+            const float g = grad[o];
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+                const unsigned u = static_cast<unsigned>(d - r * W);
+                if (u < 4u) {
+#pragma unroll
+                    for (int k = 0; k < 4; ++k)
+                        if (u == static_cast<unsigned>(k)) sum[r][k] += g;
+                }
+            }
+        }
+}
+
 }  // namespace mfh
