@@ -25,7 +25,8 @@ def host(t):
 
 @pytest.mark.parametrize("shape,kernel,stride,padding", POOL_CASES + (
     ((4, 8, 60, 80), (3, 3), (2, 2), (0, 0)), ((2, 4, 30, 40), (2, 2), (2, 2), (0, 0)),
-    ((2, 3, 9, 9), (3, 3), (1, 1), (1, 1))))
+    ((2, 3, 9, 9), (3, 3), (1, 1), (1, 1)),
+    ((3, 5, 13, 16), (3, 3), (2, 2), (0, 0))))  # two-row backward blocks: odd H, nine planes per workgroup
 def test_pool_bit_exact_with_ties_padding_and_overlap(shape, kernel, stride, padding):
     print("pool", shape, kernel, stride, padding, flush=True)
     rng = np.random.default_rng(7)
