@@ -122,6 +122,18 @@ MFH_API int mfh_conv_forward_implicit(uint64_t x, uint64_t weight, uint64_t wt, 
                                       int SH, int SW, int PH, int PW, int activation, float alpha, int engine,
                                       uint64_t workspace, int64_t workspace_floats, uint64_t stream);
 
+/* mfh_conv_forward_implicit without residual or activation, for a caller that forms y itself:
+ * when the product's plan splits K (over the caller's workspace), the product's slices are left in
+ * the workspace unreduced (slices x CO x N*OH*OW floats) and *slices receives their count; y is then
+ * not written (mfh_bn_forward_split forms it, adding bias (optional, per output channel), and
+ * stores it). Otherwise y is written as by
+ * mfh_conv_forward_implicit and *slices is 1. No counterpart in the reference: the fused graph's
+ * Conv + BN pairs use it. */
+MFH_API int mfh_conv_forward_implicit_deferred(uint64_t x, uint64_t weight, uint64_t wt, int prepared, uint64_t bias,
+                                               uint64_t y, int N, int CI, int H, int W, int CO, int KH, int KW, int OH, int OW,
+                                               int SH, int SW, int PH, int PW, int engine, uint64_t workspace,
+                                               int64_t workspace_floats, int* slices, uint64_t stream);
+
 /* The kernels of several convolutions in the orders the implicit products read them, in one
  * launch for up to 32 orders (more take more launches). Kernel i is weights[i] (CO, CI, KH, KW)
  * with dims[9i .. 9i+8] = CO, CI, KH, KW, flip, SH, SW, PH, PW; outs[i] receives CO*CI*KH*KW
@@ -285,6 +297,19 @@ MFH_API int mfh_bn_forward(uint64_t x, uint64_t gamma, uint64_t beta, uint64_t r
                            uint64_t residual, uint64_t y, uint64_t mean, uint64_t inv_std, uint64_t workspace,
                            int64_t workspace_doubles, int N, int C, int HW, int training, int relu, double momentum,
                            double eps, double var_scale, uint64_t stream);
+
+/* Training mfh_bn_forward of a convolution output that mfh_conv_forward_implicit_deferred left as
+ * `slices` FP32 split-K slices (partial: slices x C x N*HW floats, channel c's position
+ * n * HW + hw of slice z at partial[(z * C + c) * N * HW + n * HW + hw]). x is formed first, each
+ * element the FP64 sum of its slices in slice order rounded once, plus bias[c] (optional) in
+ * float32 (the bits of mfh_conv_forward_implicit's own slice reduction), and stored into x; then y, mean, inv_std and the running statistics are those of
+ * mfh_bn_forward on that x, in one launch. Only for shapes whose channels are normalised in one
+ * launch (N * HW at most 8192); others return status 2. No counterpart in the reference (its
+ * convolution and batch norm are separate operators): the fused graph's Conv + BN pairs use it. */
+MFH_API int mfh_bn_forward_split(uint64_t partial, int slices, uint64_t bias, uint64_t x, uint64_t gamma, uint64_t beta,
+                                 uint64_t running_mean, uint64_t running_var, uint64_t residual, uint64_t y,
+                                 uint64_t mean, uint64_t inv_std, int N, int C, int HW, int relu, double momentum,
+                                 double eps, double var_scale, uint64_t stream);
 
 /* Gradients of mfh_bn_forward. g = dy, or dy where gate > 0 and 0 elsewhere when gate (the fused
  * ReLU's output) is given; residual_grad (optional, needs gate) receives g. dgamma / dbeta are

@@ -441,6 +441,24 @@ MFH_API int mfh_conv_forward_implicit(std::uint64_t x, std::uint64_t weight, std
                                  workspace_floats, as_stream(stream));
 }
 
+MFH_API int mfh_conv_forward_implicit_deferred(std::uint64_t x, std::uint64_t weight, std::uint64_t wt, int prepared,
+                                               std::uint64_t bias, std::uint64_t y, int N, int CI, int H, int W, int CO, int KH, int KW,
+                                               int OH, int OW, int SH, int SW, int PH, int PW, int engine,
+                                               std::uint64_t workspace, std::int64_t workspace_floats,
+                                               int* slices, std::uint64_t stream) {
+    MFH_TRY(require_ready());
+    const ConvGeometry g{N, CI, H, W, CO, KH, KW, OH, OW, SH, SW, PH, PW};
+    MFH_TRY(validate(g));
+    MFH_REQUIRE(implicit_engine_valid(engine), "unknown implicit convolution engine or plan code");
+    MFH_REQUIRE(x && y && slices && (weight || (prepared && wt)), "conv forward received a null buffer");
+    MFH_REQUIRE(wt || !implicit_chunked(CI), "the implicit forward needs the reordered-kernel buffer wt");
+    MFH_REQUIRE(prepared == 0 || prepared == 1, "prepared must be 0 or 1");
+    MFH_REQUIRE(workspace_floats >= 0, "workspace size must be non-negative");
+    return conv_implicit_forward(g, as_ptr<const float>(x), as_ptr<const float>(weight), as_ptr<float>(wt),
+                                 prepared == 1, as_ptr<const float>(bias), nullptr, as_ptr<float>(y), ACT_NONE, 0.0f, engine,
+                                 as_ptr<float>(workspace), workspace_floats, as_stream(stream), slices);
+}
+
 MFH_API int mfh_conv_weight_orders(const std::uint64_t* weights, const std::uint64_t* outs, const int* dims, int count,
                                    std::uint64_t stream) {
     MFH_TRY(require_ready());
@@ -699,6 +717,39 @@ MFH_API int mfh_bn_forward(std::uint64_t x, std::uint64_t gamma, std::uint64_t b
     f.eps = eps;
     f.var_scale = var_scale;
     return norm_forward(s, f, as_stream(stream));
+}
+
+MFH_API int mfh_bn_forward_split(std::uint64_t partial, int slices, std::uint64_t bias, std::uint64_t x,
+                                 std::uint64_t gamma,
+                                 std::uint64_t beta, std::uint64_t running_mean, std::uint64_t running_var,
+                                 std::uint64_t residual, std::uint64_t y, std::uint64_t mean, std::uint64_t inv_std,
+                                 int N, int C, int HW, int relu, double momentum, double eps, double var_scale,
+                                 std::uint64_t stream) {
+    MFH_TRY(require_ready());
+    const NormShape s{N, C, HW};
+    MFH_TRY(validate_norm(s));
+    MFH_REQUIRE(partial && x && gamma && beta && running_mean && running_var && y && mean && inv_std,
+                "batch-norm forward received a null buffer");
+    MFH_REQUIRE(slices >= 1, "slices must be positive");
+    MFH_REQUIRE(static_cast<std::int64_t>(slices) * N * C * HW <= INDEX_LIMIT, "the slices exceed the int32 index range");
+    MFH_REQUIRE(eps >= 0.0 && momentum >= 0.0 && momentum <= 1.0, "batch-norm eps and momentum are out of range");
+    NormForward f{};
+    f.x = as_ptr<const float>(x);
+    f.gamma = as_ptr<const float>(gamma);
+    f.beta = as_ptr<const float>(beta);
+    f.running_mean = as_ptr<float>(running_mean);
+    f.running_var = as_ptr<float>(running_var);
+    f.residual = as_ptr<const float>(residual);
+    f.y = as_ptr<float>(y);
+    f.mean = as_ptr<float>(mean);
+    f.inv_std = as_ptr<float>(inv_std);
+    f.training = true;
+    f.relu = relu != 0;
+    f.momentum = momentum;
+    f.eps = eps;
+    f.var_scale = var_scale;
+    return norm_forward_split(s, f, as_ptr<const float>(partial), slices, as_ptr<const float>(bias), as_ptr<float>(x),
+                              as_stream(stream));
 }
 
 MFH_API int mfh_bn_backward(std::uint64_t x, std::uint64_t dy, std::uint64_t gate, std::uint64_t gamma,

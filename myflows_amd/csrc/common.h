@@ -245,7 +245,8 @@ inline bool implicit_chunked(int C) { return C % CHANNEL_CHUNK == 0; }
 // from w unless `prepared` says that it holds that order already.
 int conv_implicit_forward(const ConvGeometry& g, const float* x, const float* w, float* wt, bool prepared,
                           const float* bias, const float* residual, float* y, int act, float alpha, int engine,
-                          float* workspace, std::int64_t workspace_floats, hipStream_t stream);
+                          float* workspace, std::int64_t workspace_floats, hipStream_t stream,
+                          int* deferred = nullptr);
 // dW = dy . im2col(x), with dy read in place from NCHW. With db, the workgroups of the first
 // feature tile also sum dy over their pixel slice in FP64; an unsplit product writes db itself, a
 // split one leaves bias_partial[z * CO + co] for slice z (at most WGRAD_MAX_SLICES) and its
@@ -337,6 +338,11 @@ struct NormForward {
     double momentum, eps, var_scale;
 };
 int norm_forward(const NormShape& s, const NormForward& f, hipStream_t stream);
+// Training forward of a one-launch shape whose x is formed first from `slices` split-K slices of a
+// convolution product (partial: slices x C x N*HW floats) plus the convolution's bias (optional),
+// and stored into x.
+int norm_forward_split(const NormShape& s, const NormForward& f, const float* partial, int slices, const float* bias,
+                       float* x, hipStream_t stream);
 
 struct NormBackward {
     const float* x;

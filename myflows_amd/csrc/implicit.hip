@@ -932,7 +932,7 @@ bool buffer_extents_fit(const ConvGather& g, int M, int lda) {
 // FP64 slice reduction).
 int run_implicit(bool wgrad, const GemmPlan& plan, const float* a, int lda, int M, int N, int K, const ConvGather& g,
                  float* c, int ldc, GemmEpilogue e, float* workspace, hipStream_t stream,
-                 double* row_sums = nullptr, float* row_out = nullptr) {
+                 double* row_sums = nullptr, float* row_out = nullptr, bool defer_reduce = false) {
     const bool split = plan.slices > 1;
     GemmParams p{};
     p.A = a;
@@ -964,7 +964,7 @@ int run_implicit(bool wgrad, const GemmPlan& plan, const float* a, int lda, int 
     else
         hipLaunchKernelGGL(conv_kernels().forward[plan.tile][variant], grid, block, 0, stream, p, g);
     MFH_TRY(MFH_CHECK_LAUNCH(wgrad ? "conv_implicit_wgrad" : "conv_implicit_forward", stream));
-    if (!split) return OK;
+    if (!split || defer_reduce) return OK;
     if (row_out) {  // the row sums' slice partials are finished by the same reduction launch
         e.row_partial = row_sums;
         e.row_out = row_out;
@@ -1077,7 +1077,7 @@ int launch_weight_orders(const WeightOrder* orders, int count, hipStream_t strea
 
 int conv_implicit_forward(const ConvGeometry& g, const float* x, const float* w, float* wt, bool prepared,
                           const float* bias, const float* residual, float* y, int act, float alpha, int engine,
-                          float* workspace, std::int64_t workspace_floats, hipStream_t stream) {
+                          float* workspace, std::int64_t workspace_floats, hipStream_t stream, int* deferred) {
     const int M = g.CO, N = g.rows(), K = g.features();
     GemmPlan plan;
     MFH_TRY(implicit_plan(false, implicit_chunked(g.CI), engine, M, N, K, workspace, workspace_floats, &plan));
@@ -1097,7 +1097,12 @@ int conv_implicit_forward(const ConvGeometry& g, const float* x, const float* w,
     e.segment = g.ohw();
     e.segment_stride = static_cast<long long>(g.CO) * g.ohw();
     e.residual = residual;
-    return run_implicit(false, plan, w, K, M, N, K, gather, y, g.ohw(), e, workspace, stream);
+    // A split product without residual or activation may leave its slices in the workspace for the
+    // caller to reduce and add the bias to (the slice count goes to *deferred; 1 when y was written
+    // here).
+    const bool defer = deferred && plan.slices > 1 && !residual && act == ACT_NONE;
+    if (deferred) *deferred = defer ? plan.slices : 1;
+    return run_implicit(false, plan, w, K, M, N, K, gather, y, g.ohw(), e, workspace, stream, nullptr, nullptr, defer);
 }
 
 int conv_implicit_wgrad(const ConvGeometry& g, const float* x, const float* dy, float* dw, double* bias_partial,

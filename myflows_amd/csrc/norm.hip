@@ -549,13 +549,58 @@ __device__ __forceinline__ void store_group(float* v, int at, int vec, const flo
     else v[at] = in[0];
 }
 
-template <int T, bool QUAD>
-__global__ __launch_bounds__(T) void norm_forward_channel_kernel(PartialArgs pa, ApplyArgs p) {
+// A convolution output not yet formed: the FP32 split-K slices of its product, slice z holding
+// channel c's position j (= n * HW + hw) at partial[z * slice_floats + c * (N * HW) + j]. A
+// position's value is their FP64 sum in slice order, rounded once, plus the channel's bias in
+// FP32: the product's own slice reduction (gemm.hip split_reduce_vec4_kernel, finish_output), so x
+// gets the same bits.
+struct SplitSource {
+    const float* partial;
+    long long slice_floats;
+    int slices;
+    const float* bias;  // per channel, optional
+    float* x;           // where the formed convolution output is stored
+};
+
+template <int W>
+__device__ __forceinline__ void split_group(const SplitSource& src, int c, long long at, int vec, float (&out)[W]) {
+    double sum[W] = {};
+    if (W == 4 && vec) {
+        for (int z = 0; z < src.slices; ++z) {
+            const float4 t = *reinterpret_cast<const float4*>(src.partial + z * src.slice_floats + at);
+            const float v[4] = {t.x, t.y, t.z, t.w};
+#pragma unroll
+            for (int u = 0; u < W; ++u) sum[u] += static_cast<double>(v[u]);
+        }
+    } else {
+        for (int z = 0; z < src.slices; ++z)
+#pragma unroll
+            for (int u = 0; u < W; ++u) sum[u] += static_cast<double>(src.partial[z * src.slice_floats + at + u]);
+    }
+    const float b = src.bias ? src.bias[c] : 0.0f;
+#pragma unroll
+    for (int u = 0; u < W; ++u) {
+        out[u] = static_cast<float>(sum[u]);
+        if (src.bias) out[u] += b;
+    }
+}
+
+// SPLIT: x is formed from src first (and stored), then normalised as below, in one launch.
+template <int T, bool QUAD, bool SPLIT = false>
+__global__ __launch_bounds__(T) void norm_forward_channel_kernel(PartialArgs pa, ApplyArgs p, SplitSource src) {
     using S = ChannelSlots<T, QUAD>;
     constexpr int G = S::GROUPS, W = S::WIDTH;
     __shared__ float coef[3];
     const int c = blockIdx.x, total = pa.total, plane = p.C * p.HW;
-    const double centre = static_cast<double>(p.x[c * p.HW]);
+    const long long channel = static_cast<long long>(c) * total;  // channel c's first position in a slice
+    double centre;
+    if constexpr (SPLIT) {
+        float first[1];
+        split_group<1>(src, c, channel, 0, first);
+        centre = static_cast<double>(first[0]);
+    } else {
+        centre = static_cast<double>(p.x[c * p.HW]);
+    }
     float xv[G][W] = {}, rv[G][W] = {};  // x and the residual, both loaded before the sums
     int at[G];
 #pragma unroll
@@ -565,9 +610,15 @@ __global__ __launch_bounds__(T) void norm_forward_channel_kernel(PartialArgs pa,
         const int n = p.div_hw.divmod(j < total ? j : 0, hw);
         at[i] = n * plane + c * p.HW + hw;
         if (j < total) {
-            load_group<W>(p.x, at[i], pa.vec, xv[i]);
+            if constexpr (SPLIT) split_group<W>(src, c, channel + j, pa.vec, xv[i]);
+            else load_group<W>(p.x, at[i], pa.vec, xv[i]);
             if (p.residual) load_group<W>(p.residual, at[i], pa.vec, rv[i]);
         }
+    }
+    if constexpr (SPLIT) {
+#pragma unroll
+        for (int i = 0; i < G; ++i)
+            if (S::first(i) < total) store_group<W>(src.x, at[i], pa.vec, xv[i]);
     }
     double a[CHAINS] = {}, b[CHAINS] = {};
 #pragma unroll
@@ -963,6 +1014,19 @@ void launch_partials(const NormShape& s, const PartialArgs& args, hipStream_t st
     else norm_partials_kernel<MODE, PT, QUAD><<<grid, PT, 0, stream>>>(args);
 }
 
+template <bool SPLIT>
+void launch_forward_channel(const NormShape& s, const PartialArgs& args, const ApplyArgs& a, const SplitSource& src,
+                            hipStream_t stream) {
+    const bool wide = wide_sums(s);
+    if (quad_order(s)) {
+        if (wide) norm_forward_channel_kernel<WIDE_PT, true, SPLIT><<<s.C, WIDE_PT, 0, stream>>>(args, a, src);
+        else norm_forward_channel_kernel<PT, true, SPLIT><<<s.C, PT, 0, stream>>>(args, a, src);
+    } else {
+        if (wide) norm_forward_channel_kernel<WIDE_PT, false, SPLIT><<<s.C, WIDE_PT, 0, stream>>>(args, a, src);
+        else norm_forward_channel_kernel<PT, false, SPLIT><<<s.C, PT, 0, stream>>>(args, a, src);
+    }
+}
+
 int run_partials(int mode, const NormShape& s, const PartialArgs& args, hipStream_t stream) {
     const bool quad = quad_order(s);
     if (mode == STATS) (quad ? launch_partials<STATS, true> : launch_partials<STATS, false>)(s, args, stream);
@@ -993,10 +1057,10 @@ std::int64_t norm_workspace_doubles(const NormShape& s) {
     return 2LL * s.C * norm_slices(s);
 }
 
-int norm_forward(const NormShape& s, const NormForward& f, hipStream_t stream) {
+// The arguments of the forward kernels of one batch-norm pass.
+static void forward_args(const NormShape& s, const NormForward& f, int slices, PartialArgs& args, ApplyArgs& a) {
     const int total = s.N * s.C * s.HW;
-    const int slices = norm_slices(s);
-    PartialArgs args{};
+    args = PartialArgs{};
     args.x = f.x;
     args.partial = f.partial;
     args.C = s.C;
@@ -1005,7 +1069,7 @@ int norm_forward(const NormShape& s, const NormForward& f, hipStream_t stream) {
     args.chunk = slice_chunk(s, slices);
     args.div_hw = FastDiv(s.HW);
     args.vec = quad_vec(s, {f.x, f.y, f.residual});
-    ApplyArgs a{};
+    a = ApplyArgs{};
     a.x = f.x;
     a.gamma = f.gamma;
     a.beta = f.beta;
@@ -1028,16 +1092,17 @@ int norm_forward(const NormShape& s, const NormForward& f, hipStream_t stream) {
     a.var_scale = f.var_scale;
     a.div_hw = FastDiv(s.HW);
     a.div_c = FastDiv(s.C);
+}
+
+int norm_forward(const NormShape& s, const NormForward& f, hipStream_t stream) {
+    const int total = s.N * s.C * s.HW;
+    const int slices = norm_slices(s);
+    PartialArgs args;
+    ApplyArgs a;
+    forward_args(s, f, slices, args, a);
     const bool vec = vec4_spans(s) && aligned16(f.x) && aligned16(f.y) && (!f.residual || aligned16(f.residual));
     if (f.training && slices == 1) {
-        const bool wide = wide_sums(s);
-        if (quad_order(s)) {
-            if (wide) norm_forward_channel_kernel<WIDE_PT, true><<<s.C, WIDE_PT, 0, stream>>>(args, a);
-            else norm_forward_channel_kernel<PT, true><<<s.C, PT, 0, stream>>>(args, a);
-        } else {
-            if (wide) norm_forward_channel_kernel<WIDE_PT, false><<<s.C, WIDE_PT, 0, stream>>>(args, a);
-            else norm_forward_channel_kernel<PT, false><<<s.C, PT, 0, stream>>>(args, a);
-        }
+        launch_forward_channel<false>(s, args, a, SplitSource{}, stream);
         return MFH_CHECK_LAUNCH("norm_forward_channel", stream);
     }
     if (f.training) MFH_TRY(run_partials(STATS, s, args, stream));
@@ -1045,6 +1110,20 @@ int norm_forward(const NormShape& s, const NormForward& f, hipStream_t stream) {
     if (vec) norm_apply_kernel<4><<<blocks, APPLY_THREADS, 0, stream>>>(a);
     else norm_apply_kernel<1><<<blocks, APPLY_THREADS, 0, stream>>>(a);
     return MFH_CHECK_LAUNCH("norm_apply", stream);
+}
+
+int norm_forward_split(const NormShape& s, const NormForward& f, const float* partial, int slices, const float* bias,
+                       float* x, hipStream_t stream) {
+    if (!f.training || norm_slices(s) != 1)
+        return MFH_FAIL(ERR_ARG, "forming x inside batch norm needs a training pass of one launch per channel "
+                                 "(N*H*W at most 8192); reduce the slices first (mfh_split_reduce)");
+    PartialArgs args;
+    ApplyArgs a;
+    forward_args(s, f, 1, args, a);
+    args.vec = quad_vec(s, {x, f.y, f.residual, partial});
+    const SplitSource src{partial, static_cast<long long>(s.C) * s.N * s.HW, slices, bias, x};
+    launch_forward_channel<true>(s, args, a, src, stream);
+    return MFH_CHECK_LAUNCH("norm_forward_channel<split>", stream);
 }
 
 namespace {

@@ -56,6 +56,11 @@ def _channel_vector(value, c, name):
     return value
 
 
+# Positions per channel (N * H * W) up to which a training batch norm normalises a channel in one
+# launch, and so can also form a deferred convolution output (mfh_bn_forward_split).
+SPLIT_FORM_MAX_POSITIONS = 8192
+
+
 def batchnorm2d_forward(x, gamma, beta, running_mean, running_var, *, momentum, eps, training,
                         unbiased_running_var=False, relu=False, residual=None):
     """(y, mean, inv_std); updates running_mean / running_var in place when training.
@@ -80,6 +85,16 @@ def batchnorm2d_forward(x, gamma, beta, running_mean, running_var, *, momentum, 
     y = torch.empty_like(x)
     mean = torch.empty((2, c), dtype=torch.float32, device=x.device)
     inv_std = torch.empty((c,), dtype=torch.float32, device=x.device)
+    split = native.take_pending_split(x)
+    if split is not None:  # x is a convolution output still in split-K slices: form it here
+        if not training or count > SPLIT_FORM_MAX_POSITIONS:
+            raise RuntimeError("a deferred convolution output reached a batch norm that cannot form it")
+        partial, slices, bias = split
+        native._call("mfh_bn_forward_split", partial.data_ptr(), slices, native._addr(bias), x.data_ptr(), gamma.data_ptr(),
+                     beta.data_ptr(), running_mean.data_ptr(), running_var.data_ptr(), native._addr(residual),
+                     y.data_ptr(), mean.data_ptr(), inv_std.data_ptr(), n, c, hw, int(bool(relu)), float(momentum),
+                     float(eps), float(var_scale), native._stream())
+        return y, mean, inv_std
     doubles = _bn_workspace_doubles(n, c, hw) if training else 0
     workspace = native.stream_workspace(doubles, torch.float64) if doubles else None
     native._call("mfh_bn_forward", x.data_ptr(), gamma.data_ptr(), beta.data_ptr(), running_mean.data_ptr(),
@@ -158,6 +173,8 @@ def batchnorm2d_relu_pool_forward(x, gamma, beta, running_mean, running_var, *, 
     without padding, in two launches that never store the ReLU output. argmax is the int32 flat index
     into x's shape (as maxpool2d_forward's into its input). Bit for bit the separate passes."""
     x = _f32(x, "x")
+    if native.take_pending_split(x) is not None:
+        raise RuntimeError("a deferred convolution output reached a unit that cannot form it")
     n, c, hw = _bn_shape(x)
     gamma, beta = _channel_vector(gamma, c, "gamma"), _channel_vector(beta, c, "beta")
     for name, stat in (("running_mean", running_mean), ("running_var", running_var)):

@@ -168,6 +168,7 @@ class _Plan:
     keep: tuple             # nodes whose gradient survives backward (leaves, retained nodes)
     groups: frozenset       # fused groups in use
     forward_steps: tuple    # forward_units with shortcut branches on the side stream: (unit, step kind)
+    deferred: dict          # convolution -> the batch norm, its only consumer, that may form its output
 
 
 # Kinds of a forward step: a unit on the current stream, the fork of a branch (the side stream waits
@@ -234,7 +235,30 @@ class Graph:
         keep = tuple(n for n in self.nodes if needs[n] and (not n.parents or n in self._retained))
         return _Plan(tuple(needs.items()), frozenset(n for n, need in needs.items() if need), forward_units,
                      backward_units, pre_clear, keep, frozenset(groups),
-                     self._forward_steps(forward_units, groups))
+                     self._forward_steps(forward_units, groups), self._deferred_splits(groups))
+
+    def _deferred_splits(self, groups):
+        """Plain convolutions (no fused activation) whose only consumer is a batch norm
+        that runs alone or as the BN of a BN(+Add)+ReLU unit: a training batch norm of few enough
+        positions forms such a convolution's output from the product's split-K slices itself
+        (Conv2D_Op.forward, fused.batchnorm2d_forward)."""
+        from .ops_conv import Conv2D_Op
+        from .ops_norm import BatchNorm2d_Op, BatchNormActivation
+        consumers = {}
+        for node in self.nodes:
+            for parent in node.parents:
+                consumers.setdefault(parent, set()).add(node)
+        in_unit = {g.bn: g for g in groups.values()}
+        pairs = {}
+        for node in self.nodes:
+            if type(node) is not Conv2D_Op or node is self.target_node:
+                continue
+            users = consumers.get(node, ())
+            bn = next(iter(users)) if len(users) == 1 else None
+            if (isinstance(bn, BatchNorm2d_Op) and bn.parents[0] is node and node not in self._retained
+                    and (bn not in in_unit or isinstance(in_unit[bn], BatchNormActivation))):
+                pairs[node] = bn
+        return pairs
 
     def _forward_steps(self, forward_units, groups):
         """forward_units with every convolution + batch-norm shortcut (a ResNet downsample: a Conv2D
@@ -289,6 +313,8 @@ class Graph:
                     node.requires_grad = need
                 if not need:
                     node.grad = None
+                if hasattr(node, "_defer_bn"):
+                    node._defer_bn = plan.deferred.get(node)
             Graph._installed = plan
         return plan
 

@@ -90,6 +90,7 @@ _SIGNATURES = {
     "mfh_conv_forward": ("i", "pppppp" + _CONV + "ifipqp"),
     "mfh_conv_backward": ("i", "pppppppppp" + _CONV + "iifiipqp"),
     "mfh_conv_forward_implicit": ("i", "pppippp" + _CONV + "ifipqp"),
+    "mfh_conv_forward_implicit_deferred": ("i", "pppipp" + _CONV + "ipqPp"),
     "mfh_conv_weight_orders": ("i", "UUPip"),
     "mfh_conv_implicit_workspace": ("q", _CONV + "i"),
     "mfh_conv_backward_implicit": ("i", "ppppppppppp" + _CONV + "ifiiipqp"),
@@ -107,6 +108,7 @@ _SIGNATURES = {
     "mfh_gemm_noalloc": ("i", "iiipppp" + "iiiiii" + "p"),
     "mfh_bn_workspace": ("q", "iii"),
     "mfh_bn_forward": ("i", "ppppppppppq" + "iiiii" + "ddd" + "p"),
+    "mfh_bn_forward_split": ("i", "pip" + "p" * 9 + "iiii" + "ddd" + "p"),
     "mfh_bn_backward": ("i", "pppppppppppq" + "iii" + "iiiii" + "p"),
     "mfh_bn_relu_pool_supported": ("i", "iiiiiiii"),
     "mfh_bn_relu_pool_forward": ("i", "pppppppppp" + "q" + "iiiiiiii" + "i" + "ddd" + "p"),
@@ -611,6 +613,58 @@ def conv2d_forward(x, weight, bias=None, *, stride=(1, 1), padding=(0, 0), activ
     _call("mfh_conv_forward", x.data_ptr(), weight.data_ptr(), _addr(bias), cols.data_ptr(), _addr(rows),
           y.data_ptr(), *g.c_args(), act, alpha, engine, _addr(workspace), floats, _stream())
     return y, cols
+
+
+# Convolution outputs whose split-K slices still wait in their stream's workspace (see
+# conv2d_forward_deferred): id(y) -> (y, workspace, slices, bias).
+_PENDING_SPLITS = {}
+
+
+def conv2d_forward_deferred(x, weight, bias=None, *, stride=(1, 1), padding=(0, 0), engine="mfma", weight_order=None,
+                            max_positions=0):
+    """conv2d_forward (implicit, no residual or activation) for a caller that forms y itself:
+    when the output has at most max_positions positions per channel (N * OH * OW) and the product's
+    plan splits K, y is returned unwritten and its slices stay in this stream's convolution
+    workspace, registered for take_pending_split(y); the next batch-norm forward of y
+    (fused.batchnorm2d_forward) must form y before this stream runs another convolution. Otherwise
+    y is complete, as from conv2d_forward."""
+    x, weight = _device_f32(x, "x"), _device_f32(weight, "weight")
+    g = ConvGeometry.of(x.shape, weight.shape, stride, padding)
+    n, _, oh, ow = g.out_shape
+    if n * oh * ow > max_positions:
+        return conv2d_forward(x, weight, bias, stride=stride, padding=padding, engine=engine, algorithm="implicit",
+                              weight_order=weight_order)[0]
+    if bias is not None:
+        bias = _device_f32(bias, "bias")
+        if tuple(bias.shape) != (weight.shape[0],):
+            raise ValueError("bias must have shape (out_channels,)")
+    engine = _engine_code(engine)
+    y = torch.empty(g.out_shape, dtype=torch.float32, device=x.device)
+    workspace, floats = _implicit_workspace(g, "forward")
+    prepared, wt = 0, None
+    if implicit_chunked(g.ci):
+        if weight_order is not None:
+            wt, prepared = _weight_order_buffer(weight_order, weight, "weight_order"), 1
+        else:
+            wt = torch.empty_like(weight)
+    slices = ctypes.c_int(1)
+    _call("mfh_conv_forward_implicit_deferred", x.data_ptr(), weight.data_ptr(), _addr(wt), prepared, _addr(bias),
+          y.data_ptr(),
+          *g.c_args(), engine, _addr(workspace), floats, ctypes.byref(slices), _stream())
+    if slices.value > 1:
+        _PENDING_SPLITS[id(y)] = (y, workspace, slices.value, bias)
+    return y
+
+
+def take_pending_split(y):
+    """(workspace, slices, bias) of a convolution output left unformed by conv2d_forward_deferred, or None;
+    the caller then forms y."""
+    entry = _PENDING_SPLITS.pop(id(y), None)
+    if entry is None:
+        return None
+    if entry[0] is not y:  # a stale entry of a freed tensor whose id was reused
+        return None
+    return entry[1:]
 
 
 def conv2d_backward(x, weight, grad_y, cols, *, stride=(1, 1), padding=(0, 0), need_bias_grad=True,

@@ -14,7 +14,7 @@ import os
 
 import torch
 
-from . import native, streams
+from . import fused, native, streams
 from .device import get_device
 from .graph import GradientOp
 
@@ -66,6 +66,7 @@ class Conv2D_Op(GradientOp):
     """
 
     fused_activation = None  # "relu" / "leaky_relu" in the fused subclasses
+    _defer_bn = None  # set by a Graph: the training batch norm that is this node's only consumer
 
     def __init__(self, x, kernel, stride=1, padding=0, groups=1, dilation=1, bias=None, backend="auto",
                  recompute_im2col=None):
@@ -140,10 +141,19 @@ class Conv2D_Op(GradientOp):
         self._orders.pop("backward", None)
         order = self._order_for("forward", kernel_val)
         extra = {"weight_order": order} if order is not None else {}
-        self.value, cols = native.conv2d_forward(
-            x_val, kernel_val, bias_val, stride=self.stride, padding=self.padding,
-            activation=self.fused_activation, alpha=self._activation_alpha(),
-            engine=NATIVE_BACKENDS[self.actual_backend], **extra)
+        bn = self._defer_bn
+        if bn is not None and bn.training and self.fused_activation is None and self._implicit():
+            # The one consumer is a training batch norm, which can form this output from the
+            # product's split-K slices (and the bias) itself: one launch less, the same bits.
+            self.value, cols = native.conv2d_forward_deferred(
+                x_val, kernel_val, bias_val, stride=self.stride, padding=self.padding,
+                engine=NATIVE_BACKENDS[self.actual_backend], max_positions=fused.SPLIT_FORM_MAX_POSITIONS,
+                **extra), None
+        else:
+            self.value, cols = native.conv2d_forward(
+                x_val, kernel_val, bias_val, stride=self.stride, padding=self.padding,
+                activation=self.fused_activation, alpha=self._activation_alpha(),
+                engine=NATIVE_BACKENDS[self.actual_backend], **extra)
         self._activation_fused = self.fused_activation is not None
         keep_cols = self.parents[1].requires_grad and not self.recompute_im2col
         self._saved = (x_val, kernel_val, cols if keep_cols else None) if self.requires_grad else None

@@ -457,3 +457,74 @@ def test_batchnorm_relu_pool_unit_rejects_planes_beyond_its_lds():
     Graph unit then runs the separate nodes)."""
     assert fused.batchnorm_relu_pool_supported((2, 4, 60, 80), (3, 3), (2, 2))
     assert not fused.batchnorm_relu_pool_supported((1, 1, 200, 200), (3, 3), (2, 2))
+
+
+@pytest.mark.parametrize("x_shape,w_shape,stride,residual", [
+    ((64, 256, 8, 10), (512, 256, 3, 3), 2, False),   # layer4.0 conv1 at batch 64: 6 slices
+    ((64, 512, 4, 5), (512, 512, 3, 3), 1, True),     # layer4 3x3, the BN with a residual: 6 slices
+    ((64, 128, 15, 20), (256, 128, 3, 3), 2, False),  # layer3.0 conv1: 3 slices, 1024 threads per channel
+], ids=("layer4-down", "layer4-residual", "layer3-down"))
+def test_batch_norm_forms_a_deferred_convolution_output_bit_for_bit(x_shape, w_shape, stride, residual):
+    """A split convolution product whose output the training batch norm forms (FP64 slice sums,
+    the bias, then the statistics and y in one launch) against the product's own slice reduction
+    followed by the batch norm: x, y, the statistics and the running statistics bit for bit."""
+    print("deferred", x_shape, w_shape, flush=True)
+    rng = np.random.default_rng(23)
+    x = gpu(rng.standard_normal(x_shape).astype(np.float32))
+    w = gpu((rng.standard_normal(w_shape) * (2.0 / np.prod(w_shape[1:])) ** 0.5).astype(np.float32))
+    b = gpu(rng.standard_normal(w_shape[0]).astype(np.float32))
+    c = w_shape[0]
+    gamma, beta = gpu(rng.uniform(0.5, 1.5, c).astype(np.float32)), gpu(rng.standard_normal(c).astype(np.float32))
+    conv = dict(stride=(stride, stride), padding=(1, 1))
+    ref_x, _ = native.conv2d_forward(x, w, b, **conv)
+    r = gpu(rng.standard_normal(tuple(ref_x.shape)).astype(np.float32)) if residual else None
+    stats = [(torch.zeros(c, device="cuda"), torch.ones(c, device="cuda")) for _ in range(2)]
+    bn = dict(momentum=0.1, eps=1e-5, training=True, relu=True, residual=r)
+    ref = fused.batchnorm2d_forward(ref_x, gamma, beta, *stats[0], **bn)
+    formed = native.conv2d_forward_deferred(x, w, b, max_positions=fused.SPLIT_FORM_MAX_POSITIONS, **conv)
+    assert id(formed) in native._PENDING_SPLITS  # the plan splits K: the batch norm forms the output
+    out = fused.batchnorm2d_forward(formed, gamma, beta, *stats[1], **bn)
+    assert id(formed) not in native._PENDING_SPLITS
+    for name, a, e in [("x", formed, ref_x), ("y", out[0], ref[0]), ("mean", out[1], ref[1]),
+                       ("inv_std", out[2], ref[2]), ("running_mean", stats[1][0], stats[0][0]),
+                       ("running_var", stats[1][1], stats[0][1])]:
+        np.testing.assert_array_equal(host(a), host(e), err_msg=name)
+
+
+def test_resnet_step_with_deferred_split_outputs_matches_the_plain_step():
+    """ResNet18 at batch 64, 3x120x160 (the bench step): the Graph lets the training batch norms
+    of layer3 and layer4 form their split convolutions' outputs; one forward and backward with and
+    without that give the same loss, output and gradients bit for bit."""
+    import myflows_amd as mf
+    from myflows_amd import ops_conv
+    from tests.test_gpu_model import build_resnet
+    print("deferred step", flush=True)
+    formed = []
+    take = native.take_pending_split
+
+    def counting(y):
+        entry = take(y)
+        formed.append(entry is not None)
+        return entry
+
+    runs = []
+    for defer in (True, False):
+        model, graph, out, loss, _, _ = build_resnet(64, 120, 160, optimize=True)
+        graph.forward()  # installs the plan (and its Conv + BN pairs)
+        convs = [n for n in graph.nodes if type(n) is ops_conv.Conv2D_Op]
+        assert sum(n._defer_bn is not None for n in convs) == 19
+        if not defer:
+            for n in convs:
+                n._defer_bn = None
+        native.take_pending_split = counting
+        try:
+            graph.forward()
+        finally:
+            native.take_pending_split = take
+        graph.backward()
+        runs.append([host(loss.value), host(out.value)] + [host(p.grad) for p in model.params])
+        if defer:
+            assert sum(formed) == 8  # layer3's and layer4's split 3x3 products
+        formed.clear()
+    for a, b in zip(*runs):
+        np.testing.assert_array_equal(a, b)
