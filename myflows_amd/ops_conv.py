@@ -142,7 +142,11 @@ class Conv2D_Op(GradientOp):
         order = self._order_for("forward", kernel_val)
         extra = {"weight_order": order} if order is not None else {}
         bn = self._defer_bn
-        if bn is not None and bn.training and self.fused_activation is None and self._implicit():
+        defer = bn is not None and bn.training and self.fused_activation is None and self._implicit()
+        if defer:  # at most as many positions per channel as the batch norm can form in one launch
+            n, _, oh, ow = native.ConvGeometry.of(x_val.shape, kernel_val.shape, self.stride, self.padding).out_shape
+            defer = n * oh * ow <= fused.SPLIT_FORM_MAX_POSITIONS
+        if defer:
             # The one consumer is a training batch norm, which can form this output from the
             # product's split-K slices (and the bias) itself: one launch less, the same bits.
             self.value, cols = native.conv2d_forward_deferred(
