@@ -17,7 +17,7 @@ from .ops_basic import LINEAR_BACKENDS, Add, LeakyReLU, Linear, MSELoss, ReLU
 from .ops_conv import (BACKENDS, NATIVE_BACKENDS, Conv2D_AddReLU_Op, Conv2D_LeakyReLU_Op, Conv2D_Op, Conv2D_ReLU_Op,
                        Flatten_Op, MaxPool2d_Op)
 from .ops_norm import BatchNorm2d_Op, BatchNormActivation, BatchNormReLUPool, GlobalAvgPool2d_Op
-from .optim import MBGD, Adam, Optimizer
+from .optim import MBGD, Adam, Optimizer, ParameterGroups
 from .resnet import BasicBlock, BatchNorm2d, GlobalAvgPool2d, ResNet18
 
 __all__ = [
@@ -25,7 +25,7 @@ __all__ = [
     "BatchNormReLUPool", "CapturedStep", "Conv2D",
     "Conv2D_AddReLU_Op", "Conv2D_LeakyReLU_Op", "Conv2D_Op", "Conv2D_ReLU_Op", "Dense", "Flatten", "Flatten_Op",
     "GlobalAvgPool2d", "GlobalAvgPool2d_Op", "GradientOp", "Graph", "LINEAR_BACKENDS", "Layer", "LeakyReLU", "Linear", "MBGD",
-    "MSELoss", "MaxPool2d", "MaxPool2d_Op", "NATIVE_BACKENDS", "Node", "Optimizer", "ReLU", "ResNet18", "Variable",
+    "MSELoss", "MaxPool2d", "MaxPool2d_Op", "NATIVE_BACKENDS", "Node", "Optimizer", "ParameterGroups", "ReLU", "ResNet18", "Variable",
     "apply_graph_optimizations", "cuda_available", "fused", "get_device", "make_initializer", "native",
     "set_device",
 ]

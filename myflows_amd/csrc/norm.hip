@@ -1049,7 +1049,9 @@ int norm_slices(const NormShape& s) {
     if (positions <= CHANNEL_FUSED_MAX) return 1;  // one workgroup per channel, one launch per pass
     const std::int64_t wanted = (8LL * device_cu_count() + s.C - 1) / s.C;
     const std::int64_t most = std::max<std::int64_t>(1, positions / MIN_SLICE);
-    return static_cast<int>(std::max<std::int64_t>(1, std::min(wanted, most)));
+    // At least two slices: one slice means the one-launch channel kernels, which hold at most
+    // CHANNEL_FUSED_MAX positions (a wide layer, C >= 8 * CUs, would otherwise get one).
+    return static_cast<int>(std::max<std::int64_t>(2, std::min(wanted, most)));
 }
 
 std::int64_t norm_workspace_doubles(const NormShape& s) {

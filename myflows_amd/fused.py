@@ -336,10 +336,6 @@ def column_sums(grad):
 
 def _adam_row(param, grad, m, v, lr, decay, step, beta1, beta2):
     # The scalars are formed in double precision and rounded once to float32 by the c_float fields.
-    tensors = [_f32(t, name) for t, name in ((param, "param"), (grad, "grad"), (m, "m"), (v, "v"))]
-    for t, original in zip(tensors, (param, grad, m, v)):
-        if t.data_ptr() != original.data_ptr() or t.shape != param.shape:
-            raise ValueError("Adam updates contiguous tensors of the parameter's shape in place")
     return native.AdamTensor(param.data_ptr(), grad.data_ptr(), m.data_ptr(), v.data_ptr(), param.numel(),
                              float(lr), float(decay), 1.0 - beta1 ** step, 1.0 - beta2 ** step)
 
@@ -353,8 +349,16 @@ def _adam_launch(rows, beta1, beta2, eps, grad_scale):
 
 
 def adam_update(param, grad, m, v, *, lr, beta1, beta2, eps, step, grad_scale=1.0, weight_decay=0.0):
-    """One Adam step (zero-initialised moments, bias-corrected) applied in place."""
-    _adam_launch([_adam_row(param, grad, m, v, lr, weight_decay, step, beta1, beta2)], beta1, beta2, eps, grad_scale)
+    """One Adam step (zero-initialised moments, bias-corrected) applied in place. param, m and v are
+    float32 GPU tensors of one shape; a strided one is updated through a contiguous copy that is
+    written back, and a strided gradient is read through a contiguous copy."""
+    tensors = [_f32(t, name) for t, name in ((param, "param"), (grad, "grad"), (m, "m"), (v, "v"))]
+    if any(t.shape != param.shape for t in tensors):
+        raise ValueError("Adam updates tensors of the parameter's shape")
+    _adam_launch([_adam_row(*tensors, lr, weight_decay, step, beta1, beta2)], beta1, beta2, eps, grad_scale)
+    for original, updated in ((param, tensors[0]), (m, tensors[2]), (v, tensors[3])):
+        if updated is not original:
+            original.copy_(updated)
 
 
 class _AdamTable:
@@ -368,6 +372,7 @@ class _AdamTable:
         self.key = None
         self.held = None
         self.shapes = None
+        self.owners = None  # ids of the param / moment tensors and of the tensors they view
         self.table = None
 
 
@@ -378,45 +383,71 @@ def _adam_param_key(updates):
     return tuple((id(p), id(m), id(v), p.data_ptr(), m.data_ptr(), v.data_ptr()) for p, g, m, v, *_ in updates)
 
 
+def _multi_adam_fits(updates):
+    """Whether one multi-tensor launch can update these (param, grad, m, v, ...) tuples: every
+    param, m and v a contiguous float32 GPU tensor of its parameter's shape, and none of them
+    overlapping another (the launch reads and writes each element once, in no set order). Otherwise
+    the updates run one tensor after another, as the reference's multi-tensor Adam does
+    (ops/fused.py:579-606)."""
+    f32 = torch.float32
+    spans = []
+    for p, g, m, v, *_ in updates:
+        for t in (p, m, v):
+            if not (isinstance(t, torch.Tensor) and t.dtype is f32 and t.is_cuda and t.is_contiguous()
+                    and t.shape == p.shape):
+                return False
+            if t.numel():
+                spans.append((t.data_ptr(), t.data_ptr() + 4 * t.numel()))
+    spans.sort()
+    return all(start >= end for (_, end), (start, _) in zip(spans, spans[1:]))
+
+
 def _adam_table_for(updates, beta1, beta2):
     """The cached row table for these (param, m, v) tensors, rebuilt (with every check) when they
-    change."""
+    change; None when they cannot share one launch (_multi_adam_fits)."""
     cache = _ADAM_TABLE
     key = _adam_param_key(updates)
     if cache.key == key:
         return cache
-    rows = [_adam_row(p, g, m, v, lr, decay, step, beta1, beta2) for p, g, m, v, lr, decay, step in updates]
-    spans = sorted((t.data_ptr(), t.data_ptr() + 4 * t.numel()) for p, g, m, v, *_ in updates for t in (p, m, v)
-                   if t.numel())
-    for (_, end), (start, _) in zip(spans, spans[1:]):
-        if start < end:
-            raise ValueError("adam_update_many needs non-overlapping parameters and moments")
+    if not _multi_adam_fits(updates):
+        return None
+    rows = [_adam_row(p, p, m, v, lr, decay, step, beta1, beta2) for p, g, m, v, lr, decay, step in updates]
     cache.key = key
     cache.held = [(p, m, v) for p, g, m, v, *_ in updates]
     cache.shapes = [p.shape for p, *_ in updates]
+    cache.owners = {id(t if t._base is None else t._base) for held in cache.held for t in held}
     cache.table = (native.AdamTensor * len(rows))(*rows)
     return cache
 
 
 def adam_update_many(updates, *, beta1, beta2, eps, grad_scale):
-    """Adam for (param, grad, m, v, lr, decay, step) tuples in one multi-tensor launch per 16 tensors.
+    """Adam for (param, grad, m, v, lr, decay, step) tuples in one multi-tensor launch per 48 tensors.
 
-    The tensors must not overlap one another (each parameter is read and written once).
+    Tensors that one launch cannot take (a strided or overlapping param or moment, a strided
+    gradient, a gradient that shares memory with a param or moment) are updated one after another
+    with adam_update instead, in the order given.
     """
     updates = list(updates)
     if not updates:
         return
     cache = _adam_table_for(updates, beta1, beta2)
-    table = cache.table
-    f32 = torch.float32
-    for i, ((p, g, m, v, lr, decay, step), shape) in enumerate(zip(updates, cache.shapes)):
-        if not (isinstance(g, torch.Tensor) and g.dtype is f32 and g.is_cuda and g.is_contiguous()
-                and g.shape == shape):
-            raise ValueError("Adam updates contiguous tensors of the parameter's shape in place")
-        row = table[i]
-        # The scalars are formed in double precision and rounded once to float32 by the fields.
-        row.grad = g.data_ptr()
-        row.lr, row.weight_decay = float(lr), float(decay)
-        row.bias_correction1, row.bias_correction2 = 1.0 - beta1 ** step, 1.0 - beta2 ** step
+    if cache is not None:
+        table, owners = cache.table, cache.owners
+        f32 = torch.float32
+        for i, ((p, g, m, v, lr, decay, step), shape) in enumerate(zip(updates, cache.shapes)):
+            if not (isinstance(g, torch.Tensor) and g.dtype is f32 and g.is_cuda and g.is_contiguous()
+                    and g.shape == shape and id(g if g._base is None else g._base) not in owners):
+                cache = None
+                break
+            row = table[i]
+            # The scalars are formed in double precision and rounded once to float32 by the fields.
+            row.grad = g.data_ptr()
+            row.lr, row.weight_decay = float(lr), float(decay)
+            row.bias_correction1, row.bias_correction2 = 1.0 - beta1 ** step, 1.0 - beta2 ** step
+    if cache is None:
+        for p, g, m, v, lr, decay, step in updates:
+            adam_update(p, g, m, v, lr=lr, beta1=beta1, beta2=beta2, eps=eps, step=step, grad_scale=grad_scale,
+                        weight_decay=decay)
+        return
     native._call("mfh_adam_step", table, len(updates), float(grad_scale), float(beta1), 1.0 - beta1, float(beta2),
                  1.0 - beta2, float(eps), native._stream())

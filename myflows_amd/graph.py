@@ -157,6 +157,20 @@ def _prepare_weight_orders(units, phase):
     return tuple(unit for unit, _ in pending)
 
 
+def _next_on_stream(steps):
+    """For a sequence of (unit, kind) forward steps: unit -> the next unit issued on the same stream
+    (MAIN units on the current stream, SIDE units on the side stream)."""
+    after, last = {}, {}
+    for unit, kind in steps:
+        if kind in (FORK, JOIN) or unit is None or not unit.parents:
+            continue
+        stream = SIDE if kind == SIDE else MAIN
+        if stream in last:
+            after[last[stream]] = unit
+        last[stream] = unit
+    return after
+
+
 @dataclass(frozen=True)
 class _Plan:
     """What one combination of leaf flags and retained nodes asks of a graph."""
@@ -168,7 +182,8 @@ class _Plan:
     keep: tuple             # nodes whose gradient survives backward (leaves, retained nodes)
     groups: frozenset       # fused groups in use
     forward_steps: tuple    # forward_units with shortcut branches on the side stream: (unit, step kind)
-    deferred: dict          # convolution -> the batch norm, its only consumer, that may form its output
+    deferred: tuple         # per forward order (one stream, branches on the side stream): convolution ->
+                            # the batch norm, its only consumer and next on its stream, that may form its output
 
 
 # Kinds of a forward step: a unit on the current stream, the fork of a branch (the side stream waits
@@ -181,6 +196,7 @@ class Graph:
     """Forward and backward over the subgraph that produces ``target_node``."""
 
     _installed = None  # the plan whose per-node flags are written into the (possibly shared) nodes
+    _deferred_installed = None  # (plan, forward order) whose deferred pairs the nodes hold
 
     def __init__(self, target_node, optimize=False, fold_constants=False, fuse_linear=True, fuse_activations=True):
         self._opt_stats = None
@@ -207,8 +223,17 @@ class Graph:
         self.overlap_branches = True
         self._leaves = tuple(node for node in self.nodes if not node.parents)
         self._retained = set()
+        self._materialize = False
         self._plans = {}
         self._forward_plan = None
+
+    def materialize_intermediates(self, enabled=True):
+        """Run the fused units' nodes one by one from the next forward on (while enabled), so that
+        the batch-norm and residual-add values a fused unit never forms are there to inspect; the
+        results are the same bits either way."""
+        if self._materialize != bool(enabled):
+            self._materialize = bool(enabled)
+            self._plans.clear()
 
     def retain_grad(self, *nodes):
         """Keep the gradients of these intermediates (or differentiable leaves) after backward."""
@@ -227,21 +252,27 @@ class Graph:
                 needs[node] = from_parents or node in self._retained
                 if from_parents:
                     propagating.append(node)
-        groups = {out: g for out, g in self._bn_groups.items() if self._retained.isdisjoint(g.hidden)}
+        groups = {} if self._materialize else {
+            out: g for out, g in self._bn_groups.items() if self._retained.isdisjoint(g.hidden)}
         hidden = {node for g in groups.values() for node in g.hidden}
         forward_units = tuple(groups.get(n, n) for n in self.nodes if n not in hidden)
         backward_units = tuple((groups.get(n, n), n) for n in reversed(propagating) if n not in hidden)
         pre_clear = {n: tuple(p for p in n.parents if needs[p]) for n in propagating if not isinstance(n, GradientOp)}
         keep = tuple(n for n in self.nodes if needs[n] and (not n.parents or n in self._retained))
+        forward_steps = self._forward_steps(forward_units, groups)
         return _Plan(tuple(needs.items()), frozenset(n for n, need in needs.items() if need), forward_units,
-                     backward_units, pre_clear, keep, frozenset(groups),
-                     self._forward_steps(forward_units, groups), self._deferred_splits(groups))
+                     backward_units, pre_clear, keep, frozenset(groups), forward_steps,
+                     self._deferred_splits(groups, forward_units, forward_steps))
 
-    def _deferred_splits(self, groups):
+    def _deferred_splits(self, groups, forward_units, forward_steps):
         """Plain convolutions (no fused activation) whose only consumer is a batch norm
         that runs alone or as the BN of a BN(+Add)+ReLU unit: a training batch norm of few enough
         positions forms such a convolution's output from the product's split-K slices itself
-        (Conv2D_Op.forward, fused.batchnorm2d_forward)."""
+        (Conv2D_Op.forward, fused.batchnorm2d_forward). The slices wait in the stream's convolution
+        workspace, so a pair is kept only when the batch norm's unit is the next unit issued on the
+        convolution's stream, and no other product on that stream runs between. Returns the pairs
+        of each forward order: (forward_units on one stream, forward_steps with the shortcut
+        branches on the side stream)."""
         from .ops_conv import Conv2D_Op
         from .ops_norm import BatchNorm2d_Op, BatchNormActivation
         consumers = {}
@@ -258,7 +289,12 @@ class Graph:
             if (isinstance(bn, BatchNorm2d_Op) and bn.parents[0] is node and node not in self._retained
                     and (bn not in in_unit or isinstance(in_unit[bn], BatchNormActivation))):
                 pairs[node] = bn
-        return pairs
+        if not pairs:
+            return {}, {}
+        unit_of = {g.bn: g for g in groups.values()}
+        orders = (_next_on_stream((unit, MAIN) for unit in forward_units), _next_on_stream(forward_steps))
+        return tuple({conv: bn for conv, bn in pairs.items() if after.get(conv) is unit_of.get(bn, bn)}
+                     for after in orders)
 
     def _forward_steps(self, forward_units, groups):
         """forward_units with every convolution + batch-norm shortcut (a ResNet downsample: a Conv2D
@@ -313,17 +349,31 @@ class Graph:
                     node.requires_grad = need
                 if not need:
                     node.grad = None
-                if hasattr(node, "_defer_bn"):
-                    node._defer_bn = plan.deferred.get(node)
             Graph._installed = plan
         return plan
+
+    def _install_deferred(self, plan, overlapped):
+        """Write the deferred convolution -> batch norm pairs of this plan's forward order into the
+        convolution nodes (which another graph or order may have set otherwise)."""
+        key = (plan, overlapped)
+        if Graph._deferred_installed == key:
+            return
+        pairs = plan.deferred[1 if overlapped else 0]
+        for node, _ in plan.needs:
+            if hasattr(node, "_defer_bn"):
+                node._defer_bn = pairs.get(node)
+        Graph._deferred_installed = key
 
     def forward(self):
         plan = self._plan()
         self._forward_plan = plan
         profiler = self.profiler
+        overlapped = profiler is None and self.overlap_branches
+        from . import native
+        native.drop_pending_splits()  # outputs a failed earlier forward left unformed
+        self._install_deferred(plan, overlapped)
         served = _prepare_weight_orders((u for u in plan.forward_units if u.parents), "forward")
-        if profiler is None and self.overlap_branches:
+        if overlapped:
             self._run_steps(plan.forward_steps)
         else:
             for unit in plan.forward_units:

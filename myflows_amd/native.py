@@ -491,10 +491,16 @@ def stream_workspace(count, dtype=torch.float32):
     otherwise allocate and free one per launch."""
     key = (_current_device(), _stream(), dtype)
     held = _STREAM_WORKSPACES.get(key)
-    if held is None or held.numel() < count:
+    if held is None or held.numel() < count or (_PENDING_SPLITS and _holds_pending_split(held)):
+        # A block whose split-K slices still wait for their batch norm is never handed out again:
+        # this call takes a fresh one (the pending entry keeps the old block until it is formed).
         held = torch.empty(count, dtype=dtype, device="cuda")
         _STREAM_WORKSPACES[key] = held
     return held
+
+
+def _holds_pending_split(block):
+    return any(entry[1] is block for entry in _PENDING_SPLITS.values())
 
 
 def _implicit_workspace(g, *passes):
@@ -507,6 +513,30 @@ def _implicit_workspace(g, *passes):
 def implicit_chunked(channels):
     """Whether an implicit product over this many channels reads them in chunks of CHANNEL_CHUNK."""
     return int(channels) % CHANNEL_CHUNK == 0
+
+
+# Floats of the largest tensor a chunked implicit product reads: its buffer loads take 32-bit byte
+# offsets (2 GiB).
+BUFFER_LIMIT_FLOATS = (2 ** 31 - 1) // 4
+
+
+def implicit_fits(g):
+    """Whether every implicit product of this convolution (forward, dW, dX) can read its tensors:
+    a chunked product reads x, dy and the kernel orders with buffer loads of at most
+    BUFFER_LIMIT_FLOATS floats. The geometry's own int32 limits leave only large 1x1-like
+    convolutions outside; those take the im2col algorithm by default."""
+    if not (implicit_chunked(g.ci) or implicit_chunked(g.co)):
+        return True
+    return max(g.n * g.ci * g.h * g.w, g.m * g.co, g.co * g.k) <= BUFFER_LIMIT_FLOATS
+
+
+def _default_algorithm_for(g, algorithm):
+    """The algorithm a call runs: the one asked for, else the default, which is im2col for a
+    convolution whose tensors the implicit products cannot read (implicit_fits)."""
+    if algorithm is not None:
+        return _conv_algorithm(algorithm)
+    algorithm = default_conv_algorithm()
+    return algorithm if algorithm != "implicit" or implicit_fits(g) else "im2col"
 
 
 def conv_weight_orders(requests):
@@ -566,19 +596,23 @@ def conv2d_forward(x, weight, bias=None, *, stride=(1, 1), padding=(0, 0), activ
                    engine="mfma", algorithm=None, weight_order=None, residual=None):
     """(y, cols): the contiguous NCHW output with bias and activation applied, and the im2col
     columns of x that conv2d_backward needs for dW. With algorithm "implicit" (the default) the GEMM
-    gathers the columns from x itself and cols is None; "im2col" writes and returns them.
+    gathers the columns from x itself and cols is None; "im2col" writes and returns them. Without an
+    algorithm, a convolution whose tensors the implicit products cannot read (implicit_fits) takes
+    "im2col".
     weight_order: this kernel from conv_weight_orders(flip 0), which the implicit product then reads
     instead of reordering the kernel itself. residual (implicit only): a tensor of y's shape added
     to conv + bias before the activation, act((conv + bias) + residual), each step one float32
     rounding as in separate Add and activation operators."""
     engine = _engine_code(engine)
-    algorithm = _conv_algorithm(algorithm)
+    if algorithm is not None:
+        algorithm = _conv_algorithm(algorithm)
     x, weight = _device_f32(x, "x"), _device_f32(weight, "weight")
     if bias is not None:
         bias = _device_f32(bias, "bias")
         if tuple(bias.shape) != (weight.shape[0],):
             raise ValueError("bias must have shape (out_channels,)")
     g = ConvGeometry.of(x.shape, weight.shape, stride, padding)
+    algorithm = _default_algorithm_for(g, algorithm)
     act, alpha = _activation_code(activation, alpha)
     device = x.device
     y = torch.empty(g.out_shape, dtype=torch.float32, device=device)
@@ -656,6 +690,13 @@ def conv2d_forward_deferred(x, weight, bias=None, *, stride=(1, 1), padding=(0, 
     return y
 
 
+def drop_pending_splits():
+    """Forget every output left unformed by conv2d_forward_deferred (their batch norms never ran,
+    e.g. an earlier forward raised between the product and the batch norm); the outputs stay
+    unwritten and their workspace blocks go back to the allocator."""
+    _PENDING_SPLITS.clear()
+
+
 def take_pending_split(y):
     """(workspace, slices, bias) of a convolution output left unformed by conv2d_forward_deferred, or None;
     the caller then forms y."""
@@ -674,7 +715,8 @@ def conv2d_backward(x, weight, grad_y, cols, *, stride=(1, 1), padding=(0, 0), n
     """(dx, dw, db), None for each gradient not requested; a fused activation gates grad_y through
     output. algorithm "im2col" computes dW from the forward's cols (recomputed from x when
     recompute_cols); "implicit" gathers them from x inside the GEMM. Without an algorithm, a call
-    that passes cols (and does not recompute them) takes "im2col", any other the default.
+    that passes cols (and does not recompute them) takes "im2col", any other the default (im2col,
+    recomputing cols, where implicit_fits says the implicit products cannot read the tensors).
     Implicit only: weight_flip is this kernel from conv_weight_orders(flip 1, with this stride and
     padding) for the dX; input_grad is a gradient of x already there, to which dX is added in place
     (it is then the returned dx); strided_dx chooses how a strided convolution's dX runs: "phases"
@@ -690,9 +732,13 @@ def conv2d_backward(x, weight, grad_y, cols, *, stride=(1, 1), padding=(0, 0), n
     engine = _engine_code(engine)
     if algorithm is None and cols is not None and not recompute_cols:
         algorithm = "im2col"
-    algorithm = _conv_algorithm(algorithm)
+    if algorithm is not None:
+        algorithm = _conv_algorithm(algorithm)
     x, weight, grad_y = _device_f32(x, "x"), _device_f32(weight, "weight"), _device_f32(grad_y, "grad_y")
     g = ConvGeometry.of(x.shape, weight.shape, stride, padding)
+    if algorithm is None:
+        algorithm = _default_algorithm_for(g, None)
+        recompute_cols = recompute_cols or (algorithm == "im2col" and cols is None)
     act, alpha = _activation_code(activation, alpha)
     if tuple(grad_y.shape) != g.out_shape:
         raise ValueError("grad_y does not have the convolution's output shape")

@@ -88,8 +88,15 @@ class Conv2D_Op(GradientOp):
     def _activation_alpha(self):
         return 0.0
 
-    def _implicit(self):
-        return native.default_conv_algorithm() == "implicit"
+    def _implicit(self, geometry=None):
+        """Whether this node's products take the implicit algorithm: the default one, for a
+        convolution whose tensors it can read (native.implicit_fits; checked once the geometry is
+        known, and the forward's choice holds for the backward)."""
+        if native.default_conv_algorithm() != "implicit":
+            return False
+        if geometry is not None:
+            return native.implicit_fits(geometry)
+        return getattr(self, "_implicit_ran", True)
 
     def weight_orders(self, phase):
         """The kernel reorders this node's next forward ("forward") or backward ("backward") pass
@@ -141,10 +148,12 @@ class Conv2D_Op(GradientOp):
         self._orders.pop("backward", None)
         order = self._order_for("forward", kernel_val)
         extra = {"weight_order": order} if order is not None else {}
+        geometry = native.ConvGeometry.of(x_val.shape, kernel_val.shape, self.stride, self.padding)
+        self._implicit_ran = self._implicit(geometry)
         bn = self._defer_bn
-        defer = bn is not None and bn.training and self.fused_activation is None and self._implicit()
+        defer = bn is not None and bn.training and self.fused_activation is None and self._implicit_ran
         if defer:  # at most as many positions per channel as the batch norm can form in one launch
-            n, _, oh, ow = native.ConvGeometry.of(x_val.shape, kernel_val.shape, self.stride, self.padding).out_shape
+            n, _, oh, ow = geometry.out_shape
             defer = n * oh * ow <= fused.SPLIT_FORM_MAX_POSITIONS
         if defer:
             # The one consumer is a training batch norm, which can form this output from the
@@ -263,9 +272,10 @@ class Conv2D_AddReLU_Op(Conv2D_Op):
         bias_val, residual_val = (rest[0], rest[1]) if self.bias is not None else (None, rest[0])
         fits = (isinstance(residual_val, torch.Tensor) and isinstance(x_val, torch.Tensor)
                 and residual_val.dtype == torch.float32 and residual_val.device == x_val.device
-                and kernel_val.ndim == 4 and x_val.ndim == 4
-                and tuple(residual_val.shape) == native.ConvGeometry.of(
-                    tuple(x_val.shape), tuple(kernel_val.shape), self.stride, self.padding).out_shape)
+                and kernel_val.ndim == 4 and x_val.ndim == 4)
+        if fits:  # the residual is read by the implicit product's epilogue
+            geometry = native.ConvGeometry.of(tuple(x_val.shape), tuple(kernel_val.shape), self.stride, self.padding)
+            fits = tuple(residual_val.shape) == geometry.out_shape and native.implicit_fits(geometry)
         if not fits:
             self._unfused(x_val, kernel_val, bias_val, residual_val)
             return

@@ -700,3 +700,36 @@ def test_weight_gradient_stream_call_gives_the_one_stream_bits(shape, kernel, st
         results.append([host(g) for g in grads])
     for got, want, name in zip(results[1], results[0], ("dx", "dw", "db")):
         np.testing.assert_array_equal(got, want, err_msg=name)
+
+
+def test_a_convolution_beyond_the_buffer_loads_takes_the_im2col_algorithm():
+    """A 1x1 convolution over 32 channels whose input holds more floats than a chunked implicit
+    product's buffer loads address (2 GiB) but whose columns fit the geometry's int32 limits: the
+    default algorithm is then im2col (forward returns cols), the explicit implicit call is refused
+    with status 2, and the forward, dX and dW are exact on integer data (FP64 on the GPU as the
+    reference; a 1x1 convolution's rows are independent, so a crop run by the implicit product
+    checks the forward too)."""
+    shape, w_shape = (1, 32, 4100, 4100), (32, 32, 1, 1)
+    g = native.ConvGeometry.of(shape, w_shape, (1, 1), (0, 0))
+    assert not native.implicit_fits(g) and native.implicit_fits(native.ConvGeometry.of(
+        (1, 32, 64, 4100), w_shape, (1, 1), (0, 0)))
+    print("beyond buffer loads", shape, flush=True)
+    gen = torch.Generator(device="cuda").manual_seed(37)
+    x = torch.randint(-1, 2, shape, generator=gen, device="cuda").float()
+    w = torch.randint(-2, 3, w_shape, generator=gen, device="cuda").float()
+    dy = torch.randint(-1, 2, shape, generator=gen, device="cuda").float()
+    with pytest.raises(native.NativeHipError):
+        native.conv2d_forward(x, w, algorithm="implicit")
+    y, cols = native.conv2d_forward(x, w)
+    assert cols is not None
+    crop, _ = native.conv2d_forward(x[:, :, :64].contiguous(), w, algorithm="implicit")
+    assert torch.equal(y[:, :, :64], crop)
+    w2 = w.reshape(32, 32).double()
+    expected = (w2 @ x.reshape(32, -1).double()).reshape(shape)
+    assert torch.equal(y.double(), expected)
+    del expected, crop
+    dx, dw, db = native.conv2d_backward(x, w, dy, None, need_bias_grad=True)
+    dyf = dy.reshape(32, -1).double()
+    assert torch.equal(dw.reshape(32, 32).double(), dyf @ x.reshape(32, -1).double().T)
+    assert torch.equal(db.double(), dyf.sum(dim=1))
+    assert torch.equal(dx.double(), (w2.T @ dyf).reshape(shape))

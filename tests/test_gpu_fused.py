@@ -265,11 +265,83 @@ def test_adam_over_more_tensors_than_one_launch_takes():
         np.testing.assert_array_equal(host(dv), v)
 
 
-def test_adam_rejects_overlapping_tensors():
-    p = torch.zeros(16, device="cuda")
-    with pytest.raises(ValueError):
-        fused.adam_update_many([(p, p, p[:8], p[8:], 1e-3, 0.0, 1)], beta1=0.9, beta2=0.999, eps=1e-8,
-                               grad_scale=1.0)
+def test_adam_falls_back_to_one_tensor_at_a_time_for_overlapping_or_strided_tensors():
+    """tests/test_multi_adam.py:45-51: parameters that overlap another update's, and a strided
+    gradient, cannot share one multi-tensor launch; the updates then run one tensor after another
+    in the order given, which the oracle repeats on NumPy views of the same arrays."""
+    arr = np.arange(20, dtype=np.float32) / 7
+    dev = gpu(arr)
+
+    def update(p, g):
+        return p, g, torch.zeros_like(p), torch.zeros_like(p), 0.01, 0.0, 1
+
+    overlapping = [update(dev[:10], dev[10:]), update(dev[5:15], gpu(arr[:10] + 1))]
+    strided = [update(gpu(arr[:10]), gpu(arr)[::2])]
+    assert not fused._multi_adam_fits(overlapping)
+    for updates in (overlapping, strided):
+        calls = []
+        call = native._call
+        native._call = lambda name, *args: (calls.append(name), call(name, *args))[1]
+        try:
+            fused.adam_update_many(updates, beta1=0.9, beta2=0.999, eps=1e-8, grad_scale=1.0)
+        finally:
+            native._call = call
+        assert calls == ["mfh_adam_step"] * len(updates)
+    ref = arr.copy()
+    for p, g in ((ref[:10], ref[10:].copy()), (ref[5:15], arr[:10] + 1)):
+        rp.adam_update(p, g, np.zeros(10, np.float32), np.zeros(10, np.float32), lr=0.01, beta1=0.9, beta2=0.999,
+                       eps=1e-8, step=1)
+    np.testing.assert_array_equal(host(dev), ref)
+    p_ref = arr[:10].copy()
+    rp.adam_update(p_ref, arr[::2].copy(), np.zeros(10, np.float32), np.zeros(10, np.float32), lr=0.01, beta1=0.9,
+                   beta2=0.999, eps=1e-8, step=1)
+    np.testing.assert_array_equal(host(strided[0][0]), p_ref)
+
+
+def test_adam_groups_partial_steps_and_accumulation_are_bitwise_equal_in_one_launch():
+    """tests/test_multi_adam.py:19-43: parameter groups (a rate multiplier; an absolute rate with
+    weight decay), a parameter frozen for the first two updates, a parameter without a gradient at
+    each update and accumulation counts 1-3: the multi-tensor optimiser (one launch per update) and
+    the per-tensor one give the same parameters, moments and per-parameter steps bit for bit."""
+    import myflows_amd as mf
+
+    def trajectory(multi):
+        rng = np.random.default_rng(7)
+        nodes = [mf.Variable(gpu(rng.normal(size=n).astype(np.float32)), trainable=True)
+                 for n in (1, 255, 256, 257, 8195)]
+        groups = [{"name": "head", "params": nodes[:2], "lr_mult": .3},
+                  {"name": "trunk", "params": nodes[2:], "lr": .002, "weight_decay": .001}]
+
+        class Nodes:
+            pass
+        graph = Nodes()
+        graph.nodes = nodes
+        opt = mf.Adam(graph, learning_rate=.001, param_groups=groups, multi_tensor=multi)
+        assert opt.group_learning_rates() == {"head": .001 * .3, "trunk": .002}
+        for step in range(7):
+            nodes[2].trainable = step >= 2
+            opt.acc_no = 1 + step % 3
+            for i, node in enumerate(nodes):
+                g = rng.normal(size=node.value.shape).astype(np.float32)
+                if i != step % 5:
+                    opt.acc_gradient[node] = gpu(g)
+            opt.update()
+        return [(host(n.value), host(opt.v[n]), host(opt.s[n]), opt.parameter_steps[n]) for n in nodes]
+
+    calls = []
+    call = native._call
+    native._call = lambda name, *args: (calls.append(name), call(name, *args))[1]
+    try:
+        batched = trajectory(True)
+    finally:
+        native._call = call
+    assert calls.count("mfh_adam_step") == 7
+    expected = trajectory(False)
+    for left, right in zip(expected, batched):
+        assert left[-1] == right[-1]
+        for a, b in zip(left[:3], right[:3]):
+            np.testing.assert_array_equal(a, b)
+    assert [s for *_, s in batched] == [5, 5, 4, 6, 6]
 
 
 # --- the reference's own edge cases (tests/test_fused_ops.py) --------------------------------------
@@ -528,3 +600,84 @@ def test_resnet_step_with_deferred_split_outputs_matches_the_plain_step():
         formed.clear()
     for a, b in zip(*runs):
         np.testing.assert_array_equal(a, b)
+
+
+def test_a_product_between_a_deferred_output_and_its_batch_norm_leaves_the_slices_alone():
+    """A deferred product's slices wait in its stream's convolution workspace: another split product
+    issued on that stream before the batch norm takes a fresh workspace block (the pending one is
+    never handed out), so the batch norm still forms the first output with the plain path's bits."""
+    print("deferred then another split product", flush=True)
+    rng = np.random.default_rng(29)
+    x = gpu(rng.standard_normal((64, 512, 4, 5)).astype(np.float32))
+    w = gpu((rng.standard_normal((512, 512, 3, 3)) * 0.02).astype(np.float32))
+    b = gpu(rng.standard_normal(512).astype(np.float32))
+    x2 = gpu(rng.standard_normal((64, 256, 8, 10)).astype(np.float32))
+    w2 = gpu((rng.standard_normal((512, 256, 3, 3)) * 0.03).astype(np.float32))
+    gamma, beta = gpu(rng.uniform(0.5, 1.5, 512).astype(np.float32)), gpu(rng.standard_normal(512).astype(np.float32))
+    conv = dict(stride=(1, 1), padding=(1, 1))
+    ref_x, _ = native.conv2d_forward(x, w, b, **conv)
+    ref_x2, _ = native.conv2d_forward(x2, w2, None, stride=(2, 2), padding=(1, 1))
+    stats = [(torch.zeros(512, device="cuda"), torch.ones(512, device="cuda")) for _ in range(2)]
+    bn = dict(momentum=0.1, eps=1e-5, training=True, relu=True)
+    ref = fused.batchnorm2d_forward(ref_x, gamma, beta, *stats[0], **bn)
+    formed = native.conv2d_forward_deferred(x, w, b, max_positions=fused.SPLIT_FORM_MAX_POSITIONS, **conv)
+    assert id(formed) in native._PENDING_SPLITS
+    between, _ = native.conv2d_forward(x2, w2, None, stride=(2, 2), padding=(1, 1))  # splits K too
+    out = fused.batchnorm2d_forward(formed, gamma, beta, *stats[1], **bn)
+    np.testing.assert_array_equal(host(between), host(ref_x2))
+    for name, a, e in [("x", formed, ref_x), ("y", out[0], ref[0]), ("mean", out[1], ref[1])]:
+        np.testing.assert_array_equal(host(a), host(e), err_msg=name)
+
+
+def test_single_stream_step_with_deferred_outputs_matches_the_plain_step_where_the_downsample_splits():
+    """ResNet18 at batch 16, 3x120x160, on one stream (overlap_branches=False: the order a profiler
+    or the single-stream bench runs): the downsample products of layer3/layer4 split K and run
+    between a block's second convolution and its batch norm, so the Graph pairs only convolutions
+    whose batch norm is the next unit on their stream. Loss, output and every gradient equal the
+    step without deferred outputs bit for bit, and so does the two-stream step."""
+    from myflows_amd import ops_conv
+    from tests.test_gpu_model import build_resnet
+    print("single-stream deferred step bs16", flush=True)
+    runs = []
+    for overlap, defer in ((False, True), (False, False), (True, True)):
+        model, graph, out, loss, _, _ = build_resnet(16, 120, 160, optimize=True)
+        graph.overlap_branches = overlap
+        graph.forward()  # installs the plan and its pairs for this order
+        convs = [n for n in graph.nodes if type(n) is ops_conv.Conv2D_Op]
+        assert sum(n._defer_bn is not None for n in convs) == (19 if overlap else 16)
+        if not defer:
+            for n in convs:
+                n._defer_bn = None
+        graph.forward()
+        graph.backward()
+        assert not native._PENDING_SPLITS
+        runs.append([host(loss.value), host(out.value)] + [host(p.grad) for p in model.params])
+    for other in runs[1:]:
+        for a, b in zip(runs[0], other):
+            np.testing.assert_array_equal(a, b)
+
+
+@pytest.mark.parametrize("shape", [(4, 2048, 56, 56), (256, 2048, 7, 7)], ids=str)
+def test_batchnorm_of_a_wide_layer_with_many_positions_against_fp64(shape):
+    """C >= 8 * CUs channels with more positions per channel than the one-launch channel kernels
+    hold (8192): the pass splits each channel into slices (two launches) and every position is
+    normalised: y and dx against the FP64 batch norm, as the operator test bounds them."""
+    import myflows_amd as mf
+    print("wide batch norm", shape, flush=True)
+    eps32 = np.finfo(np.float32).eps
+    rng = np.random.default_rng(31)
+    x = rng.normal(0.5, 2.0, shape).astype(np.float32)
+    dy = rng.standard_normal(shape).astype(np.float32)
+    c = shape[1]
+    gamma, beta = rng.uniform(0.5, 1.5, c).astype(np.float32), rng.standard_normal(c).astype(np.float32)
+    nodes = [mf.Variable(gpu(a), trainable=True) for a in (x, gamma, beta)]
+    rm, rv = np.zeros(c, np.float32), np.ones(c, np.float32)
+    op = mf.BatchNorm2d_Op(*nodes, gpu(rm), gpu(rv), momentum=0.1, eps=1e-5, training=True)
+    op.forward(*(n.value for n in nodes))
+    op.grad = gpu(dy)
+    op.backward()
+    y, dx, dgamma, dbeta, _, _ = _bn_fp64(x, dy, gamma, beta, 1e-5, True, rm, rv)
+    assert_near(host(op.value), y, 8 * eps32, "y")
+    assert_near(host(nodes[0].grad), dx, 64 * eps32, "dx")
+    assert_near(host(nodes[1].grad), dgamma, 4 * eps32, "dgamma")
+    assert_near(host(nodes[2].grad), dbeta, 2 * eps32, "dbeta")
