@@ -87,6 +87,20 @@ def build_step(batch, height, width, seed=0, optimize=True):
     return mf.Adam(graph, learning_rate=1e-3), loss
 
 
+def host_issue_ms(step, runs=5):
+    """Median host time to issue one training step (replay or eager pass, then Adam) onto an idle
+    GPU: the call returns before the GPU has finished, so this is what the host needs per step."""
+    times = []
+    for _ in range(runs):
+        torch.cuda.synchronize()
+        start = time.perf_counter()
+        step.one_step()
+        step.update()
+        times.append((time.perf_counter() - start) * 1e3)
+    torch.cuda.synchronize()
+    return round(float(np.median(times)), 3)
+
+
 def time_steps(opt, steps, warmup):
     for _ in range(warmup):
         opt.one_step()
@@ -505,6 +519,9 @@ def main():
                         help="run each backward's dW products on the current stream (no weight-gradient stream)")
     parser.add_argument("--plain-graph", action="store_true",
                         help="Graph(optimize=False): BN, Add and ReLU as separate nodes (the reference task's graph)")
+    parser.add_argument("--eager", action="store_true",
+                        help="issue every step from Python (Graph.forward/backward) instead of replaying the "
+                             "library program recorded from one such step (RecordedStep)")
     args = parser.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU: this build runs no multi-GPU path (use --gpus 1)", file=sys.stderr)
@@ -516,13 +533,17 @@ def main():
     native._library()
     opt, _ = build_step(args.batch, 120, 160, optimize=not args.plain_graph)
     opt.graph.overlap_weight_grads = opt.graph.overlap_branches = not args.single_stream
-    seconds = time_steps(opt, args.steps, args.warmup)
+    step = opt if args.eager else mf.RecordedStep(opt, warmup=2)
+    seconds = time_steps(step, args.steps, args.warmup)
     ms_per_step = seconds * 1e3 / args.steps
     images_per_s = args.batch * args.steps / seconds
+    issue_ms = host_issue_ms(step)
+    issue = "eager" if args.eager else "recorded program"
     if args.step_only:
         print(json.dumps({"metric": METRIC, "value": round(images_per_s, 2), "unit": "images/s", "n_gpus": 1,
                           "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms_per_step, 3),
-                          "single_stream": args.single_stream, "step_only": True}), flush=True)
+                          "single_stream": args.single_stream, "step_issue": issue,
+                          "host_issue_ms_per_step": issue_ms, "step_only": True}), flush=True)
         return 0
     roofline = gemm_roofline()
     result = {
@@ -533,7 +554,8 @@ def main():
                    "global_batch": args.batch, "input": [3, 120, 160], "loss": "MSE",
                    "graph": "optimize=False" if args.plain_graph else
                    "optimize=True (BN+ReLU, BN+Add+ReLU and stem BN+ReLU+max-pool units)",
-                   "backward_streams": 1 if args.single_stream else 2},
+                   "backward_streams": 1 if args.single_stream else 2, "step_issue": issue},
+        "host_issue_ms_per_step": issue_ms,
         "step_tflops": round(STEP_GFLOP * args.batch / 64 / (ms_per_step * 1e-3) / 1e3, 2),
         "roofline": roofline,
         "c2_gemms": c2_gemms(),

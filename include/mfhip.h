@@ -65,6 +65,33 @@ MFH_API void mfh_set_debug_sync(int enabled);
  * on a second stream, such as the dW products of a backward pass beside its dX products. */
 MFH_API int mfh_stream_wait(uint64_t waiting, uint64_t signalling);
 
+/* ---- recorded programs ---------------------------------------------------------------------- */
+
+/* Start recording, on the calling thread, every kernel launch and stream ordering the library
+ * issues from now on (they still run as usual) into a program, until mfh_program_end. Status 2 when
+ * this thread already records one.
+ * No counterpart in the reference: for a caller that issues the same sequence of library calls
+ * (a training step) again and again and whose host time would otherwise bound it. */
+MFH_API int mfh_program_begin(void);
+
+/* Stop recording: *program receives a handle to the recorded steps and *launches (when not null)
+ * the number of kernel launches among them. The handle stays valid until mfh_program_free. */
+MFH_API int mfh_program_end(uint64_t* program, int64_t* launches);
+
+/* Issue the recorded steps again, in their order and on their streams: the same kernels with the
+ * same arguments and buffers, without the host work that chose them. The caller keeps every buffer
+ * and stream of the recording alive, and refreshes inputs in place; work that other libraries did
+ * during the recording is not part of the program. Status 3 names the step whose launch failed. */
+MFH_API int mfh_program_run(uint64_t program);
+
+/* Release a program handle from mfh_program_end. */
+MFH_API void mfh_program_free(uint64_t program);
+
+/* p[0 .. count) = value (float32), on `stream`. No counterpart in the reference (whose graph seeds
+ * its backward with xp.ones): the seed of a backward pass as a library launch, so that a recorded
+ * program makes it too. */
+MFH_API int mfh_fill(uint64_t p, int64_t count, float value, uint64_t stream);
+
 /* ---- convolution ---------------------------------------------------------------------------- */
 
 /* cols (N*OH*OW, CI*KH*KW) = im2col(x), zero outside the padded input.

@@ -7,7 +7,7 @@ The public names mirror the reference package (``Variable``, ``Graph``, ``Conv2D
 """
 
 from . import fused, native
-from .capture import CapturedStep
+from .capture import CapturedStep, RecordedStep
 from .device import cuda_available, get_device, set_device
 from .fusion import apply_graph_optimizations
 from .graph import GradientOp, Graph, Node, Variable
@@ -25,7 +25,8 @@ __all__ = [
     "BatchNormReLUPool", "CapturedStep", "Conv2D",
     "Conv2D_AddReLU_Op", "Conv2D_LeakyReLU_Op", "Conv2D_Op", "Conv2D_ReLU_Op", "Dense", "Flatten", "Flatten_Op",
     "GlobalAvgPool2d", "GlobalAvgPool2d_Op", "GradientOp", "Graph", "LINEAR_BACKENDS", "Layer", "LeakyReLU", "Linear", "MBGD",
-    "MSELoss", "MaxPool2d", "MaxPool2d_Op", "NATIVE_BACKENDS", "Node", "Optimizer", "ParameterGroups", "ReLU", "ResNet18", "Variable",
+    "MSELoss", "MaxPool2d", "MaxPool2d_Op", "NATIVE_BACKENDS", "Node", "Optimizer", "ParameterGroups",
+    "RecordedStep", "ReLU", "ResNet18", "Variable",
     "apply_graph_optimizations", "cuda_available", "fused", "get_device", "make_initializer", "native",
     "set_device",
 ]

@@ -30,41 +30,26 @@ import torch
 from .graph import Graph
 
 
-class CapturedStep:
-    """``one_step()`` of an optimiser (forward, backward and gradient accumulation) as one HIP graph
-    replay. ``warmup`` eager passes run first (on a side stream, as stream capture requires), so
-    that plans, weight orders and workspaces exist before the recording."""
+class _ReplayedStep:
+    """The optimiser side of a replayed step: the recorded gradient buffers of the trainable leaves
+    (refreshed by every replay) go to ``acc_gradient`` as the eager ``one_step`` would put them."""
 
-    def __init__(self, optimizer, warmup=2):
+    def __init__(self, optimizer):
         self.optimizer = optimizer
         graph = optimizer.graph
         if not isinstance(graph, Graph):
-            raise TypeError("CapturedStep needs an optimiser over a Graph")
+            raise TypeError(f"{type(self).__name__} needs an optimiser over a Graph")
         device = graph.target_node.value.device if graph.target_node.value is not None else None
         if not torch.cuda.is_available() or (device is not None and device.type != "cuda"):
-            raise RuntimeError("CapturedStep records HIP work and needs the graph on a GPU")
-        side = torch.cuda.Stream()
-        side.wait_stream(torch.cuda.current_stream())
-        with torch.cuda.stream(side):
-            for _ in range(max(1, int(warmup))):
-                graph.forward()
-                graph.backward()
-        torch.cuda.current_stream().wait_stream(side)
-        torch.cuda.synchronize()
-        self.hip_graph = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(self.hip_graph):
-            graph.forward()
-            graph.backward()
-        # The recorded gradient buffers of the trainable leaves, refreshed by every replay.
-        self.gradients = {node: node.grad for node in graph.nodes
-                          if node.trainable is True and node.grad is not None}
+            raise RuntimeError(f"{type(self).__name__} records HIP work and needs the graph on a GPU")
         self.replays = 0
 
+    def _keep_gradients(self):
+        graph = self.optimizer.graph
+        self.gradients = {node: node.grad for node in graph.nodes if node.trainable is True and node.grad is not None}
+
     def forward_backward(self):
-        """Replay the recorded forward and backward pass (the outputs and gradients are updated in
-        place)."""
-        self.hip_graph.replay()
-        self.replays += 1
+        raise NotImplementedError
 
     def one_step(self):
         """The optimiser's ``one_step``: replay, then add the gradients into ``acc_gradient``.
@@ -88,3 +73,82 @@ class CapturedStep:
 
     def update(self):
         self.optimizer.update()
+
+
+class CapturedStep(_ReplayedStep):
+    """``one_step()`` of an optimiser (forward, backward and gradient accumulation) as one HIP graph
+    replay. ``warmup`` eager passes run first (on a side stream, as stream capture requires), so
+    that plans, weight orders and workspaces exist before the recording."""
+
+    def __init__(self, optimizer, warmup=2):
+        super().__init__(optimizer)
+        graph = optimizer.graph
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            for _ in range(max(1, int(warmup))):
+                graph.forward()
+                graph.backward()
+        torch.cuda.current_stream().wait_stream(side)
+        torch.cuda.synchronize()
+        self.hip_graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(self.hip_graph):
+            graph.forward()
+            graph.backward()
+        self._keep_gradients()
+
+    def forward_backward(self):
+        """Replay the recorded forward and backward pass (the outputs and gradients are updated in
+        place)."""
+        self.hip_graph.replay()
+        self.replays += 1
+
+
+class RecordedStep(_ReplayedStep):
+    """``one_step()`` of an optimiser as a libmfhip program: one ctypes call that issues the
+    forward and backward pass's kernel launches and stream orderings again, from C, as the eager
+    pass issued them (on the same streams, so the weight-gradient stream still runs beside the dX
+    products).
+
+    ``warmup`` eager passes run first, so that plans, weight orders and workspaces exist; then one
+    more eager pass runs while the library records it (mfh_program_begin / mfh_program_end), with
+    every tensor it allocates in a private memory pool: the blocks of the pass's temporaries stay
+    reserved for the replays, which write them in the recorded order. Every GPU write of the pass
+    is a library launch (the backward's seed too), so the program is the whole pass. The same rules
+    as for ``CapturedStep`` hold: fixed shapes and leaf flags, inputs refreshed in place, outputs and
+    gradients overwritten by each replay, the optimiser update eager."""
+
+    def __init__(self, optimizer, warmup=2):
+        from . import native
+        super().__init__(optimizer)
+        graph = optimizer.graph
+        for _ in range(max(0, int(warmup))):
+            graph.forward()
+            graph.backward()
+        self.pool = torch.cuda.MemPool()
+        self.program = None
+        with torch.cuda.use_mem_pool(self.pool):
+            native.program_begin()
+            try:
+                graph.forward()
+                graph.backward()
+            finally:
+                self.program, self.launches = native.program_end()
+        self._native = native
+        self._keep_gradients()
+
+    def forward_backward(self):
+        """Issue the recorded forward and backward pass again (outputs and gradients in place)."""
+        self._native.program_run(self.program)
+        self.replays += 1
+
+    def close(self):
+        if self.program:
+            self._native.program_free(self.program)
+            self.program = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass

@@ -35,6 +35,7 @@ LibraryState& state() {
 }
 
 thread_local std::string error_text;
+thread_local Program* recording_program = nullptr;
 
 // The split-K workspace of mfh_gemm_noalloc: a fixed array in device memory, one copy per GPU that
 // the library runs on, held until the process ends. Host code never passes its name to a kernel
@@ -62,10 +63,24 @@ T* as_ptr(std::uint64_t address) {
 
 hipStream_t as_stream(std::uint64_t handle) { return reinterpret_cast<hipStream_t>(static_cast<std::uintptr_t>(handle)); }
 
+int issue_order(hipStream_t waiting, hipStream_t signalling);
+
+// A stream ordering of a recorded program (issued again, with the ring's next event, on replay).
+struct OrderStep final : ProgramStep {
+    hipStream_t waiting, signalling;
+    OrderStep(hipStream_t w, hipStream_t s) : waiting(w), signalling(s) {}
+    hipError_t issue() override { return issue_order(waiting, signalling) == OK ? hipSuccess : hipErrorUnknown; }
+};
+
 // Nothing issued on `waiting` from now on starts before the work issued so far on `signalling` has
 // finished: an event of the ring recorded on one stream and waited for by the other.
 int order_after(hipStream_t waiting, hipStream_t signalling) {
     if (waiting == signalling) return OK;
+    if (Program* program = recording()) program->steps.push_back(std::make_unique<OrderStep>(waiting, signalling));
+    return issue_order(waiting, signalling);
+}
+
+int issue_order(hipStream_t waiting, hipStream_t signalling) {
     LibraryState& s = state();
     std::lock_guard<std::mutex> guard(s.lock);
     hipEvent_t event = s.order_events[s.next_order_event++ % s.order_events.size()];
@@ -243,6 +258,8 @@ int after_launch(const char* kernel, hipStream_t stream, const char* file, int l
 bool debug_sync_enabled() { return state().sync_each_launch; }
 int device_cu_count() { return state().cus; }
 
+Program*& recording() { return recording_program; }
+
 }  // namespace mfh
 
 using namespace mfh;
@@ -298,6 +315,52 @@ MFH_API int mfh_init(void) {
 MFH_API int mfh_stream_wait(std::uint64_t waiting, std::uint64_t signalling) {
     MFH_TRY(require_ready());
     return order_after(as_stream(waiting), as_stream(signalling));
+}
+
+MFH_API int mfh_program_begin(void) {
+    MFH_TRY(require_ready());
+    MFH_REQUIRE(recording() == nullptr, "a program is already being recorded on this thread");
+    recording() = new Program();
+    return OK;
+}
+
+MFH_API int mfh_program_end(std::uint64_t* program, std::int64_t* launches) {
+    Program* recorded = recording();
+    MFH_REQUIRE(recorded != nullptr, "no program is being recorded on this thread");
+    recording() = nullptr;
+    if (!program) {
+        delete recorded;
+        return MFH_FAIL(ERR_ARG, "mfh_program_end needs somewhere to put the program");
+    }
+    *program = static_cast<std::uint64_t>(reinterpret_cast<std::uintptr_t>(recorded));
+    if (launches) *launches = static_cast<std::int64_t>(recorded->launches);
+    return OK;
+}
+
+MFH_API int mfh_program_run(std::uint64_t program) {
+    MFH_TRY(require_ready());
+    MFH_REQUIRE(program != 0, "mfh_program_run received a null program");
+    MFH_REQUIRE(recording() == nullptr, "a program cannot be replayed while one is being recorded");
+    Program* p = as_ptr<Program>(program);
+    for (std::size_t i = 0; i < p->steps.size(); ++i) {
+        const hipError_t rc = p->steps[i]->issue();
+        if (rc != hipSuccess)
+            return MFH_FAIL(ERR_HIP, "program step " + std::to_string(i) + ": " + hipGetErrorString(rc));
+    }
+    if (state().sync_each_launch) {
+        const hipError_t rc = hipDeviceSynchronize();
+        if (rc != hipSuccess) return MFH_FAIL(ERR_HIP, std::string("program: ") + hipGetErrorString(rc));
+    }
+    return OK;
+}
+
+MFH_API void mfh_program_free(std::uint64_t program) { delete as_ptr<Program>(program); }
+
+MFH_API int mfh_fill(std::uint64_t p, std::int64_t count, float value, std::uint64_t stream) {
+    MFH_TRY(require_ready());
+    MFH_REQUIRE(count >= 0 && fits_index(count), "fill count must be non-negative and within int32 indexing");
+    MFH_REQUIRE(p || count == 0, "fill received a null buffer");
+    return launch_fill(as_ptr<float>(p), static_cast<int>(count), value, as_stream(stream));
 }
 
 MFH_API int mfh_conv_im2col(std::uint64_t x, std::uint64_t cols, int N, int CI, int H, int W, int CO, int KH, int KW,

@@ -10,6 +10,7 @@
 #include <string>
 
 #include "fastdiv.h"
+#include "launch.h"
 
 namespace mfh {
 
@@ -376,6 +377,7 @@ int norm_relu_pool_backward(const NormShape& s, const NormBackward& b, const Poo
 // ---- pointwise.hip ----------------------------------------------------------------------------
 int launch_relu_forward(const float* x, float* y, std::int64_t count, hipStream_t stream);
 // p[0 .. count) = 0 (a kernel, not a memset, so that it may sit in a captured graph)
+int launch_fill(float* p, std::int64_t count, float value, hipStream_t stream);
 int launch_fill_zero(float* p, std::int64_t count, hipStream_t stream);
 // out (+)= x > 0 ? g : alpha * g   (alpha = 0 for ReLU)
 int launch_relu_backward(const float* x, const float* g, float* out, std::int64_t count, float alpha, bool add,

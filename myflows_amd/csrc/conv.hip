@@ -480,21 +480,20 @@ int launch_im2col(const float* x, float* cols, const ConvGeometry& g, hipStream_
         const FastDiv dk(K), dkk(g.KH * g.KW), dkw(g.KW), dw(g.W), doh(g.OH);
         const size_t lds = static_cast<size_t>(band) * sizeof(float);
         if (vec)
-            im2col_row_kernel<true><<<blocks, 256, lds, stream>>>(x, cols, g.CI, g.H, g.W, g.KH, g.KW, g.OH, g.OW, g.SH,
+            launch(im2col_row_kernel<true>, blocks, 256, lds, stream, x, cols, g.CI, g.H, g.W, g.KH, g.KW, g.OH, g.OW, g.SH,
                                                                   g.SW, g.PH, g.PW, dk, dkk, dkw, dw, doh);
         else
-            im2col_row_kernel<false><<<blocks, 256, lds, stream>>>(x, cols, g.CI, g.H, g.W, g.KH, g.KW, g.OH, g.OW,
+            launch(im2col_row_kernel<false>, blocks, 256, lds, stream, x, cols, g.CI, g.H, g.W, g.KH, g.KW, g.OH, g.OW,
                                                                    g.SH, g.SW, g.PH, g.PW, dk, dkk, dkw, dw, doh);
         return MFH_CHECK_LAUNCH("im2col_row", stream);
     }
     if (K % 4 == 0 && (reinterpret_cast<std::uintptr_t>(cols) & 15) == 0) {
         const int quads = total / 4;
-        im2col_vec4_kernel<<<blocks_for(quads, 256), 256, 0, stream>>>(
-            x, cols, quads, FastDiv(K), FastDiv(g.KW), FastDiv(g.KH), FastDiv(g.OW), FastDiv(g.OH), g.CI, g.KH, g.KW,
+        launch(im2col_vec4_kernel, blocks_for(quads, 256), 256, 0, stream, x, cols, quads, FastDiv(K), FastDiv(g.KW), FastDiv(g.KH), FastDiv(g.OW), FastDiv(g.OH), g.CI, g.KH, g.KW,
             g.H, g.W, g.SH, g.SW, g.PH, g.PW);
         return MFH_CHECK_LAUNCH("im2col_vec4", stream);
     }
-    im2col_kernel<<<blocks_for(total, 256), 256, 0, stream>>>(x, cols, total, FastDiv(K), FastDiv(g.KW),
+    launch(im2col_kernel, blocks_for(total, 256), 256, 0, stream, x, cols, total, FastDiv(K), FastDiv(g.KW),
                                                                 FastDiv(g.KH), FastDiv(g.OW), FastDiv(g.OH), g.CI,
                                                                 g.H, g.W, g.SH, g.SW, g.PH, g.PW);
     return MFH_CHECK_LAUNCH("im2col", stream);
@@ -506,7 +505,7 @@ int launch_col2im_t(const float* gcT, float* dx, const ConvGeometry& g, bool per
     const long long ohw = g.ohw();
     const long long f_stride = per_image ? ohw : static_cast<long long>(g.rows());
     const long long n_stride = per_image ? ohw * g.features() : ohw;
-    col2im_t_kernel<<<blocks_for(total, 256), 256, 0, stream>>>(gcT, dx, total, FastDiv(g.W), FastDiv(g.H),
+    launch(col2im_t_kernel, blocks_for(total, 256), 256, 0, stream, gcT, dx, total, FastDiv(g.W), FastDiv(g.H),
                                                                   FastDiv(g.CI), g.CI, g.KH, g.KW, g.OH, g.OW, g.SH,
                                                                   g.SW, FastDiv(g.SH), FastDiv(g.SW), g.PH, g.PW,
                                                                   f_stride, n_stride, accumulate ? 1 : 0);
@@ -516,7 +515,7 @@ int launch_col2im_t(const float* gcT, float* dx, const ConvGeometry& g, bool per
 int launch_conv_epilogue(const float* rows, const float* bias, float* y, int N, int OHW, int CO, int act,
                          float alpha, hipStream_t stream) {
     const dim3 grid(blocks_for(OHW, TILE), blocks_for(CO, TILE), N), block(TILE, TROWS);
-    conv_epilogue_kernel<<<grid, block, 0, stream>>>(rows, bias, y, OHW, CO, act, alpha);
+    launch(conv_epilogue_kernel, grid, block, 0, stream, rows, bias, y, OHW, CO, act, alpha);
     return MFH_CHECK_LAUNCH("conv_epilogue", stream);
 }
 
@@ -525,18 +524,18 @@ int conv_grad_tile() { return TILE; }
 int launch_conv_grad_rows(const float* dy, const float* y, float* dyT, double* partial, int N, int OHW, int CO,
                           int grid_x, int act, float alpha, hipStream_t stream) {
     const dim3 grid(grid_x, blocks_for(CO, TILE), N), block(TILE, TROWS);
-    conv_grad_rows_kernel<<<grid, block, 0, stream>>>(dy, y, dyT, partial, OHW, CO, act, alpha);
+    launch(conv_grad_rows_kernel, grid, block, 0, stream, dy, y, dyT, partial, OHW, CO, act, alpha);
     return MFH_CHECK_LAUNCH("conv_grad_rows", stream);
 }
 
 int launch_reduce_partials(const double* partial, float* out, int count, int width, hipStream_t stream) {
-    reduce_partials_kernel<<<blocks_for(width, RP_COLS), RP_COLS * RP_LANES, 0, stream>>>(partial, out, count, width);
+    launch(reduce_partials_kernel, blocks_for(width, RP_COLS), RP_COLS * RP_LANES, 0, stream, partial, out, count, width);
     return MFH_CHECK_LAUNCH("reduce_partials", stream);
 }
 
 int launch_add_bias(float* rows, const float* bias, int M, int N, hipStream_t stream) {
     const int total = M * N;
-    add_bias_kernel<<<blocks_for(total, 256), 256, 0, stream>>>(rows, bias, total, FastDiv(N));
+    launch(add_bias_kernel, blocks_for(total, 256), 256, 0, stream, rows, bias, total, FastDiv(N));
     return MFH_CHECK_LAUNCH("add_bias", stream);
 }
 
@@ -554,12 +553,11 @@ int launch_pool_forward(const float* x, float* y, int* argmax, int N, int C, int
     if (per > 0) {
         const int planes = N * C;
         const size_t lds = static_cast<size_t>(per) * H * W * sizeof(float);
-        pool_forward_plane_kernel<<<blocks_for(planes, per), 256, lds, stream>>>(
-            x, y, argmax, planes, per, H, W, OH, OW, KH, KW, SH, SW, FastDiv(OH * OW), FastDiv(OW),
+        launch(pool_forward_plane_kernel, blocks_for(planes, per), 256, lds, stream, x, y, argmax, planes, per, H, W, OH, OW, KH, KW, SH, SW, FastDiv(OH * OW), FastDiv(OW),
             (H * W) % 4 == 0 && (reinterpret_cast<std::uintptr_t>(x) & 15) == 0 ? 1 : 0);
         return MFH_CHECK_LAUNCH("pool_forward_plane", stream);
     }
-    pool_forward_kernel<<<blocks_for(total, 256), 256, 0, stream>>>(x, y, argmax, total, FastDiv(OW), FastDiv(OH), H,
+    launch(pool_forward_kernel, blocks_for(total, 256), 256, 0, stream, x, y, argmax, total, FastDiv(OW), FastDiv(OH), H,
                                                                       W, KH, KW, SH, SW);
     return MFH_CHECK_LAUNCH("pool_forward", stream);
 }
@@ -574,13 +572,12 @@ int launch_pool_backward(const float* dy, const int* argmax, float* dx, int N, i
         const size_t lds = static_cast<size_t>(per) * OH * OW * 2 * sizeof(float);
         const bool vec4 = W % 4 == 0 && (reinterpret_cast<std::uintptr_t>(dx) & 15) == 0;
         const int per_row = vec4 ? W / 4 : W, per_plane = vec4 ? (H + 1) / 2 * per_row : H * W;
-        (vec4 ? pool_backward_plane_kernel<true> : pool_backward_plane_kernel<false>)<<<blocks_for(planes, per), 256,
-                                                                                       lds, stream>>>(
-            dy, argmax, dx, planes, per, H, W, OH, OW, KH, KW, FastDiv(per_plane), FastDiv(per_row), FastDiv(SH),
+        launch((vec4 ? pool_backward_plane_kernel<true> : pool_backward_plane_kernel<false>), blocks_for(planes, per), 256,
+                                                                                       lds, stream, dy, argmax, dx, planes, per, H, W, OH, OW, KH, KW, FastDiv(per_plane), FastDiv(per_row), FastDiv(SH),
             FastDiv(SW));
         return MFH_CHECK_LAUNCH("pool_backward_plane", stream);
     }
-    pool_backward_kernel<<<blocks_for(total, 256), 256, 0, stream>>>(dy, argmax, dx, total, FastDiv(W), FastDiv(H),
+    launch(pool_backward_kernel, blocks_for(total, 256), 256, 0, stream, dy, argmax, dx, total, FastDiv(W), FastDiv(H),
                                                                        OH, OW, KH, KW, FastDiv(SH), FastDiv(SW));
     return MFH_CHECK_LAUNCH("pool_backward", stream);
 }

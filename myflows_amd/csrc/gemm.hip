@@ -386,11 +386,11 @@ int launch_split_reduce(const float* partial, float* c, GemmParams p, int slices
     p.row_slices = slices;
     if (outputs % 4 == 0 && aligned16(partial)) {
         const std::int64_t threads = std::max<std::int64_t>(outputs / 4, 64LL * p.row_count);
-        split_reduce_vec4_kernel<<<blocks_for(threads, 256), 256, 0, stream>>>(partial, c, p, slices);
+        launch(split_reduce_vec4_kernel, blocks_for(threads, 256), 256, 0, stream, partial, c, p, slices);
         return MFH_CHECK_LAUNCH("split_reduce_vec4", stream);
     }
     const std::int64_t threads = std::max<std::int64_t>(outputs, 64LL * p.row_count);
-    split_reduce_kernel<<<blocks_for(threads, 256), 256, 0, stream>>>(partial, c, p, slices);
+    launch(split_reduce_kernel, blocks_for(threads, 256), 256, 0, stream, partial, c, p, slices);
     return MFH_CHECK_LAUNCH("split_reduce", stream);
 }
 
@@ -409,7 +409,7 @@ int split_reduce_grouped(const float* partial, float* c, const GemmEpilogue& e, 
     if (outputs % 4 != 0 || !aligned16(partial)) return launch_split_reduce(partial, c, p, slices, stream);
     const std::int64_t blocks = std::max<std::int64_t>(blocks_for(outputs / 4, GROUP_QUADS),
                                                        blocks_for(64LL * p.row_count, REDUCE_GROUPS * GROUP_QUADS));
-    split_reduce_grouped_kernel<<<blocks, REDUCE_GROUPS * GROUP_QUADS, 0, stream>>>(partial, c, p, slices);
+    launch(split_reduce_grouped_kernel, blocks, REDUCE_GROUPS * GROUP_QUADS, 0, stream, partial, c, p, slices);
     return MFH_CHECK_LAUNCH("split_reduce_grouped", stream);
 }
 
@@ -481,7 +481,7 @@ int gemm_launch(int engine, hipStream_t stream, const GemmOperands& o, const Gem
         p.lda = o.lda;
         p.ldb = o.ldb;
         p.k_chunk = K;
-        gemm_skinny_kernel<<<blocks_for(M, 4), 256, 0, stream>>>(p, o.trans_a ? 1 : 0, o.trans_b ? 1 : 0);
+        launch(gemm_skinny_kernel, blocks_for(M, 4), 256, 0, stream, p, o.trans_a ? 1 : 0, o.trans_b ? 1 : 0);
         return MFH_CHECK_LAUNCH("gemm_skinny", stream);
     }
     GemmPlan plan;
@@ -528,7 +528,7 @@ int gemm_launch(int engine, hipStream_t stream, const GemmOperands& o, const Gem
     const int layout = (o.trans_a ? 2 : 0) + (o.trans_b ? 1 : 0);  // NN, NT, TN, TT
     const GemmFn fn = kernel_table().fn[plan.tile][layout * 4 + (vec_a ? 2 : 0) + (vec_b ? 1 : 0)];
     const dim3 grid(blocks_for(N, tile.bn), blocks_for(M, tile.bm), static_cast<unsigned>(planes));
-    hipLaunchKernelGGL(fn, grid, dim3(threads_of(tile)), 0, stream, p);
+    launch(fn, grid, dim3(threads_of(tile)), 0, stream, p);
     MFH_TRY(MFH_CHECK_LAUNCH("gemm_mfma", stream));
     if (!split) return OK;
     return launch_split_reduce(workspace, o.c, epilogue_params(e, M, N, o.ldc), plan.slices, stream);

@@ -95,20 +95,20 @@ __global__ __launch_bounds__(HEAD_THREADS) void column_sums_kernel(const float* 
 
 int launch_plane_mean(const float* x, float* y, std::int64_t planes, int hw, hipStream_t stream) {
     if (planes == 0) return OK;
-    plane_mean_kernel<<<blocks_for(planes, HEAD_THREADS), HEAD_THREADS, 0, stream>>>(x, y, planes, hw);
+    launch(plane_mean_kernel, blocks_for(planes, HEAD_THREADS), HEAD_THREADS, 0, stream, x, y, planes, hw);
     return MFH_CHECK_LAUNCH("plane_mean", stream);
 }
 
 int launch_plane_mean_backward(const float* dy, float* dx, std::int64_t planes, int hw, bool add, hipStream_t stream) {
     const std::int64_t count = planes * hw;
     if (count == 0) return OK;
-    plane_mean_backward_kernel<<<blocks_for(count, HEAD_THREADS), HEAD_THREADS, 0, stream>>>(dy, dx, count, hw,
+    launch(plane_mean_backward_kernel, blocks_for(count, HEAD_THREADS), HEAD_THREADS, 0, stream, dy, dx, count, hw,
                                                                                            add ? 1 : 0);
     return MFH_CHECK_LAUNCH("plane_mean_backward", stream);
 }
 
 int launch_mse_loss(const float* pred, const float* target, float* loss, std::int64_t count, hipStream_t stream) {
-    mse_loss_kernel<<<1, LOSS_THREADS, 0, stream>>>(pred, target, loss, count);
+    launch(mse_loss_kernel, 1, LOSS_THREADS, 0, stream, pred, target, loss, count);
     return MFH_CHECK_LAUNCH("mse_loss", stream);
 }
 
@@ -116,14 +116,14 @@ int launch_mse_grad(const float* pred, const float* target, const float* seed, f
                     bool add, hipStream_t stream) {
     if (count == 0) return OK;
     const float divisor = static_cast<float>(count > 0 ? count : 1);
-    mse_grad_kernel<<<blocks_for(count, HEAD_THREADS), HEAD_THREADS, 0, stream>>>(pred, target, seed, grad, count,
+    launch(mse_grad_kernel, blocks_for(count, HEAD_THREADS), HEAD_THREADS, 0, stream, pred, target, seed, grad, count,
                                                                                 divisor, add ? 1 : 0);
     return MFH_CHECK_LAUNCH("mse_grad", stream);
 }
 
 int launch_column_sums(const float* src, float* out, std::int64_t rows, std::int64_t cols, hipStream_t stream) {
     if (cols == 0) return OK;
-    column_sums_kernel<<<blocks_for(cols, HEAD_THREADS), HEAD_THREADS, 0, stream>>>(src, out, rows, cols);
+    launch(column_sums_kernel, blocks_for(cols, HEAD_THREADS), HEAD_THREADS, 0, stream, src, out, rows, cols);
     return MFH_CHECK_LAUNCH("column_sums", stream);
 }
 

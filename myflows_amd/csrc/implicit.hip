@@ -958,11 +958,11 @@ int run_implicit(bool wgrad, const GemmPlan& plan, const float* a, int lda, int 
     if (g.chunked && (wgrad ? g.src_floats > BUFFER_LIMIT_FLOATS : !buffer_extents_fit(g, M, lda)))
         return MFH_FAIL(ERR_ARG, "a chunked implicit convolution reads tensors of at most 2 GiB");
     if (wgrad)
-        hipLaunchKernelGGL(conv_kernels().wgrad[plan.tile][row_out ? 1 : 0][g.chunked ? 1 : 0], grid, block, 0, stream,
+        launch(conv_kernels().wgrad[plan.tile][row_out ? 1 : 0][g.chunked ? 1 : 0], grid, block, 0, stream,
                            p, g, row_sums,
                            row_out);
     else
-        hipLaunchKernelGGL(conv_kernels().forward[plan.tile][variant], grid, block, 0, stream, p, g);
+        launch(conv_kernels().forward[plan.tile][variant], grid, block, 0, stream, p, g);
     MFH_TRY(MFH_CHECK_LAUNCH(wgrad ? "conv_implicit_wgrad" : "conv_implicit_forward", stream));
     if (!split || defer_reduce) return OK;
     if (row_out) {  // the row sums' slice partials are finished by the same reduction launch
@@ -1069,7 +1069,7 @@ int launch_weight_orders(const WeightOrder* orders, int count, hipStream_t strea
         }
         batch.first_block[batch.count] = blocks;
         if (blocks == 0) continue;
-        weight_order_kernel<<<blocks, 256, 0, stream>>>(batch);
+        launch(weight_order_kernel, blocks, 256, 0, stream, batch);
         MFH_TRY(MFH_CHECK_LAUNCH("weight_order", stream));
     }
     return OK;
@@ -1217,7 +1217,7 @@ int conv_implicit_dgrad_phases(const ConvGeometry& g, const float* dy, const flo
         if (fits && count > 0) {
             batch.first[count] = static_cast<int>(blocks);
             batch.count = count;
-            hipLaunchKernelGGL(conv_kernels().grouped[tile], dim3(static_cast<unsigned>(blocks)), dim3(threads_of(t)),
+            launch(conv_kernels().grouped[tile], dim3(static_cast<unsigned>(blocks)), dim3(threads_of(t)),
                                0, stream, batch);
             return MFH_CHECK_LAUNCH("conv_implicit_grouped", stream);
         }
@@ -1256,7 +1256,7 @@ int conv_implicit_dgrad_phases(const ConvGeometry& g, const float* dy, const flo
 }
 
 int launch_row_sums(const float* src, double* partial, int rows, int length, hipStream_t stream) {
-    row_sums_kernel<<<blocks_for(rows, 4), 256, 0, stream>>>(src, partial, rows, length);
+    launch(row_sums_kernel, blocks_for(rows, 4), 256, 0, stream, src, partial, rows, length);
     return MFH_CHECK_LAUNCH("row_sums", stream);
 }
 

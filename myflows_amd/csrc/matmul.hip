@@ -171,24 +171,24 @@ template <int MODE>
 int launch_mode(int variant, int tile, const float* a, const float* b, float* c, int M, int N, int K,
                 hipStream_t stream) {
     if (variant == 0) {
-        matmul_per_output<MODE><<<blocks_for(static_cast<std::int64_t>(M) * N, 256), 256, 0, stream>>>(a, b, c, M, N,
+        launch(matmul_per_output<MODE>, blocks_for(static_cast<std::int64_t>(M) * N, 256), 256, 0, stream, a, b, c, M, N,
                                                                                                        K);
         return MFH_CHECK_LAUNCH("matmul_per_output", stream);
     }
     if (variant == 4) {
         if (blocks_for(M, 64) > GRID_YZ_LIMIT) return MFH_FAIL(ERR_ARG, "matmul rows exceed the grid limit");
-        matmul_register<MODE><<<dim3(blocks_for(N, 64), blocks_for(M, 64)), 256, 0, stream>>>(a, b, c, M, N, K);
+        launch(matmul_register<MODE>, dim3(blocks_for(N, 64), blocks_for(M, 64)), 256, 0, stream, a, b, c, M, N, K);
         return MFH_CHECK_LAUNCH("matmul_register", stream);
     }
     if (blocks_for(M, tile) > GRID_YZ_LIMIT) return MFH_FAIL(ERR_ARG, "matmul rows exceed the grid limit");
     const dim3 grid(blocks_for(N, tile), blocks_for(M, tile)), block(tile, tile);
     if (variant == 1) {
-        if (tile == 16) matmul_tiled<16, MODE><<<grid, block, 0, stream>>>(a, b, c, M, N, K);
-        else matmul_tiled<32, MODE><<<grid, block, 0, stream>>>(a, b, c, M, N, K);
+        if (tile == 16) launch(matmul_tiled<16, MODE>, grid, block, 0, stream, a, b, c, M, N, K);
+        else launch(matmul_tiled<32, MODE>, grid, block, 0, stream, a, b, c, M, N, K);
         return MFH_CHECK_LAUNCH("matmul_tiled", stream);
     }
-    if (tile == 16) matmul_lds<16, MODE><<<grid, block, 0, stream>>>(a, b, c, M, N, K);
-    else matmul_lds<32, MODE><<<grid, block, 0, stream>>>(a, b, c, M, N, K);
+    if (tile == 16) launch(matmul_lds<16, MODE>, grid, block, 0, stream, a, b, c, M, N, K);
+    else launch(matmul_lds<32, MODE>, grid, block, 0, stream, a, b, c, M, N, K);
     return MFH_CHECK_LAUNCH("matmul_lds", stream);
 }
 

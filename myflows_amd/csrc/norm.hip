@@ -1010,8 +1010,8 @@ int quad_vec(const NormShape& s, std::initializer_list<const void*> tensors) {
 template <int MODE, bool QUAD>
 void launch_partials(const NormShape& s, const PartialArgs& args, hipStream_t stream) {
     const dim3 grid(norm_slices(s), s.C);
-    if (wide_sums(s)) norm_partials_kernel<MODE, WIDE_PT, QUAD><<<grid, WIDE_PT, 0, stream>>>(args);
-    else norm_partials_kernel<MODE, PT, QUAD><<<grid, PT, 0, stream>>>(args);
+    if (wide_sums(s)) launch(norm_partials_kernel<MODE, WIDE_PT, QUAD>, grid, WIDE_PT, 0, stream, args);
+    else launch(norm_partials_kernel<MODE, PT, QUAD>, grid, PT, 0, stream, args);
 }
 
 template <bool SPLIT>
@@ -1019,11 +1019,11 @@ void launch_forward_channel(const NormShape& s, const PartialArgs& args, const A
                             hipStream_t stream) {
     const bool wide = wide_sums(s);
     if (quad_order(s)) {
-        if (wide) norm_forward_channel_kernel<WIDE_PT, true, SPLIT><<<s.C, WIDE_PT, 0, stream>>>(args, a, src);
-        else norm_forward_channel_kernel<PT, true, SPLIT><<<s.C, PT, 0, stream>>>(args, a, src);
+        if (wide) launch(norm_forward_channel_kernel<WIDE_PT, true, SPLIT>, s.C, WIDE_PT, 0, stream, args, a, src);
+        else launch(norm_forward_channel_kernel<PT, true, SPLIT>, s.C, PT, 0, stream, args, a, src);
     } else {
-        if (wide) norm_forward_channel_kernel<WIDE_PT, false, SPLIT><<<s.C, WIDE_PT, 0, stream>>>(args, a, src);
-        else norm_forward_channel_kernel<PT, false, SPLIT><<<s.C, PT, 0, stream>>>(args, a, src);
+        if (wide) launch(norm_forward_channel_kernel<WIDE_PT, false, SPLIT>, s.C, WIDE_PT, 0, stream, args, a, src);
+        else launch(norm_forward_channel_kernel<PT, false, SPLIT>, s.C, PT, 0, stream, args, a, src);
     }
 }
 
@@ -1109,8 +1109,8 @@ int norm_forward(const NormShape& s, const NormForward& f, hipStream_t stream) {
     }
     if (f.training) MFH_TRY(run_partials(STATS, s, args, stream));
     const unsigned blocks = blocks_for(total, APPLY_SPAN);
-    if (vec) norm_apply_kernel<4><<<blocks, APPLY_THREADS, 0, stream>>>(a);
-    else norm_apply_kernel<1><<<blocks, APPLY_THREADS, 0, stream>>>(a);
+    if (vec) launch(norm_apply_kernel<4>, blocks, APPLY_THREADS, 0, stream, a);
+    else launch(norm_apply_kernel<1>, blocks, APPLY_THREADS, 0, stream, a);
     return MFH_CHECK_LAUNCH("norm_apply", stream);
 }
 
@@ -1204,8 +1204,7 @@ int norm_relu_pool_forward(const NormShape& s, const NormForward& f, const PoolD
     a.div_c = FastDiv(s.C);
     if (f.training) MFH_TRY(run_partials(STATS, s, args, stream));
     const int vec = s.HW % 4 == 0 && aligned16(f.x) ? 1 : 0;
-    norm_apply_pool_kernel<<<static_cast<unsigned>(s.N * s.C), APPLY_THREADS, s.HW * sizeof(float), stream>>>(
-        a, pool_shape_of(d), pooled, argmax, vec);
+    launch(norm_apply_pool_kernel, static_cast<unsigned>(s.N * s.C), APPLY_THREADS, s.HW * sizeof(float), stream, a, pool_shape_of(d), pooled, argmax, vec);
     return MFH_CHECK_LAUNCH("norm_apply_pool", stream);
 }
 
@@ -1234,11 +1233,11 @@ int norm_relu_pool_backward(const NormShape& s, const NormBackward& b, const Poo
         const bool wide = wide_sums(s);
         const dim3 grid(slices, s.C);
         if (quad_order(s)) {
-            if (wide) norm_partials_pool_kernel<WIDE_PT, true><<<grid, WIDE_PT, lds, stream>>>(args, q, pg, rows);
-            else norm_partials_pool_kernel<PT, true><<<grid, PT, lds, stream>>>(args, q, pg, rows);
+            if (wide) launch(norm_partials_pool_kernel<WIDE_PT, true>, grid, WIDE_PT, lds, stream, args, q, pg, rows);
+            else launch(norm_partials_pool_kernel<PT, true>, grid, PT, lds, stream, args, q, pg, rows);
         } else {
-            if (wide) norm_partials_pool_kernel<WIDE_PT, false><<<grid, WIDE_PT, lds, stream>>>(args, q, pg, rows);
-            else norm_partials_pool_kernel<PT, false><<<grid, PT, lds, stream>>>(args, q, pg, rows);
+            if (wide) launch(norm_partials_pool_kernel<WIDE_PT, false>, grid, WIDE_PT, lds, stream, args, q, pg, rows);
+            else launch(norm_partials_pool_kernel<PT, false>, grid, PT, lds, stream, args, q, pg, rows);
         }
         MFH_TRY(MFH_CHECK_LAUNCH("norm_partials_pool", stream));
     }
@@ -1265,8 +1264,8 @@ int norm_relu_pool_backward(const NormShape& s, const NormBackward& b, const Poo
     dx.div_hw = FastDiv(s.HW);
     dx.div_c = FastDiv(s.C);
     const int vec = d.W % 4 == 0 && aligned16(b.x) && (!b.x_grad || aligned16(b.x_grad)) ? 1 : 0;
-    norm_dx_pool_kernel<<<static_cast<unsigned>(s.N * s.C), APPLY_THREADS, static_cast<size_t>(ohw) * 2 * sizeof(float),
-                          stream>>>(dx, q, pg, vec);
+    launch(norm_dx_pool_kernel, static_cast<unsigned>(s.N * s.C), APPLY_THREADS, static_cast<size_t>(ohw) * 2 * sizeof(float),
+                          stream, dx, q, pg, vec);
     return MFH_CHECK_LAUNCH("norm_dx_pool", stream);
 }
 
@@ -1319,17 +1318,17 @@ int norm_backward(const NormShape& s, const NormBackward& b, hipStream_t stream)
     if (fused) {
         const bool wide = wide_sums(s);
         if (quad_order(s)) {
-            if (wide) norm_backward_channel_kernel<WIDE_PT, true><<<s.C, WIDE_PT, 0, stream>>>(args, d);
-            else norm_backward_channel_kernel<PT, true><<<s.C, PT, 0, stream>>>(args, d);
+            if (wide) launch(norm_backward_channel_kernel<WIDE_PT, true>, s.C, WIDE_PT, 0, stream, args, d);
+            else launch(norm_backward_channel_kernel<PT, true>, s.C, PT, 0, stream, args, d);
         } else {
-            if (wide) norm_backward_channel_kernel<WIDE_PT, false><<<s.C, WIDE_PT, 0, stream>>>(args, d);
-            else norm_backward_channel_kernel<PT, false><<<s.C, PT, 0, stream>>>(args, d);
+            if (wide) launch(norm_backward_channel_kernel<WIDE_PT, false>, s.C, WIDE_PT, 0, stream, args, d);
+            else launch(norm_backward_channel_kernel<PT, false>, s.C, PT, 0, stream, args, d);
         }
         return MFH_CHECK_LAUNCH("norm_backward_channel", stream);
     }
     const unsigned blocks = blocks_for(total, APPLY_SPAN);
-    if (vec) norm_dx_kernel<4><<<blocks, APPLY_THREADS, 0, stream>>>(d);
-    else norm_dx_kernel<1><<<blocks, APPLY_THREADS, 0, stream>>>(d);
+    if (vec) launch(norm_dx_kernel<4>, blocks, APPLY_THREADS, 0, stream, d);
+    else launch(norm_dx_kernel<1>, blocks, APPLY_THREADS, 0, stream, d);
     return MFH_CHECK_LAUNCH("norm_dx", stream);
 }
 

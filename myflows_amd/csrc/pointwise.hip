@@ -29,9 +29,9 @@ __global__ __launch_bounds__(EW_THREADS) void relu_forward_kernel(const float* _
     y[i] = v < 0.0f ? 0.0f : v;  // NaN stays NaN
 }
 
-__global__ __launch_bounds__(EW_THREADS) void fill_zero_kernel(float* __restrict__ p, long long count) {
+__global__ __launch_bounds__(EW_THREADS) void fill_kernel(float* __restrict__ p, long long count, float value) {
     const long long i = static_cast<long long>(blockIdx.x) * EW_THREADS + threadIdx.x;
-    if (i < count) p[i] = 0.0f;
+    if (i < count) p[i] = value;
 }
 
 template <bool LEAKY>
@@ -102,22 +102,24 @@ bool aligned16(const void* q) { return (reinterpret_cast<std::uintptr_t>(q) & 15
 
 int launch_relu_forward(const float* x, float* y, std::int64_t count, hipStream_t stream) {
     if (count == 0) return OK;
-    relu_forward_kernel<<<blocks_for(count, EW_THREADS), EW_THREADS, 0, stream>>>(x, y, count);
+    launch(relu_forward_kernel, blocks_for(count, EW_THREADS), EW_THREADS, 0, stream, x, y, count);
     return MFH_CHECK_LAUNCH("relu_forward", stream);
 }
 
-int launch_fill_zero(float* p, std::int64_t count, hipStream_t stream) {
+int launch_fill(float* p, std::int64_t count, float value, hipStream_t stream) {
     if (count == 0) return OK;
-    fill_zero_kernel<<<blocks_for(count, EW_THREADS), EW_THREADS, 0, stream>>>(p, count);
-    return MFH_CHECK_LAUNCH("fill_zero", stream);
+    launch(fill_kernel, blocks_for(count, EW_THREADS), EW_THREADS, 0, stream, p, count, value);
+    return MFH_CHECK_LAUNCH("fill", stream);
 }
+
+int launch_fill_zero(float* p, std::int64_t count, hipStream_t stream) { return launch_fill(p, count, 0.0f, stream); }
 
 int launch_relu_backward(const float* x, const float* g, float* out, std::int64_t count, float alpha, bool add,
                          hipStream_t stream) {
     if (count == 0) return OK;
     const unsigned blocks = blocks_for(count, EW_THREADS);
-    if (alpha != 0.0f) relu_backward_kernel<true><<<blocks, EW_THREADS, 0, stream>>>(x, g, out, count, alpha, add);
-    else relu_backward_kernel<false><<<blocks, EW_THREADS, 0, stream>>>(x, g, out, count, alpha, add);
+    if (alpha != 0.0f) launch(relu_backward_kernel<true>, blocks, EW_THREADS, 0, stream, x, g, out, count, alpha, add);
+    else launch(relu_backward_kernel<false>, blocks, EW_THREADS, 0, stream, x, g, out, count, alpha, add);
     return MFH_CHECK_LAUNCH("relu_backward", stream);
 }
 
@@ -137,7 +139,7 @@ int launch_adam(const AdamTensor* tensors, int count, const AdamScalars& s, hipS
         }
         group.first_block[group.count] = blocks;
         if (blocks == 0) continue;
-        adam_kernel<<<blocks, EW_THREADS, 0, stream>>>(group, s);
+        launch(adam_kernel, blocks, EW_THREADS, 0, stream, group, s);
         MFH_TRY(MFH_CHECK_LAUNCH("adam", stream));
     }
     return OK;

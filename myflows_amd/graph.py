@@ -431,7 +431,13 @@ class Graph:
         for node in plan.active:
             node.grad = None
         seed = self.target_node.value
-        self.target_node.grad = torch.ones_like(seed) if loss_scale == 1.0 else torch.full_like(seed, loss_scale)
+        if isinstance(seed, torch.Tensor) and seed.is_cuda and seed.dtype == torch.float32:
+            from . import native  # a library launch, so that a recorded program seeds its backward too
+            self.target_node.grad = native.fill_(torch.empty_like(seed, memory_format=torch.contiguous_format),
+                                                 loss_scale)
+        else:
+            self.target_node.grad = (torch.ones_like(seed) if loss_scale == 1.0
+                                     else torch.full_like(seed, loss_scale))
         profiler = self.profiler
         served = _prepare_weight_orders((unit for unit, _ in plan.backward_units), "backward")
         overlap = self.overlap_weight_grads and isinstance(seed, torch.Tensor) and seed.is_cuda

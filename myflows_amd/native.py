@@ -74,10 +74,11 @@ class AdamTensor(ctypes.Structure):
 
 
 # Argument codes: p device pointer / stream (uint64), i int32, q int64, f float, d double,
-# t pointer to an AdamTensor table, P pointer to int32 (host array), U pointer to uint64 (host array).
+# t pointer to an AdamTensor table, P pointer to int32 (host array), U pointer to uint64 (host array),
+# L pointer to int64.
 _CTYPE = {"p": ctypes.c_uint64, "i": ctypes.c_int, "q": ctypes.c_int64, "f": ctypes.c_float, "d": ctypes.c_double,
           "t": ctypes.POINTER(AdamTensor), "P": ctypes.POINTER(ctypes.c_int), "s": ctypes.c_char_p, "-": None,
-          "U": ctypes.POINTER(ctypes.c_uint64)}
+          "U": ctypes.POINTER(ctypes.c_uint64), "L": ctypes.POINTER(ctypes.c_int64)}
 _CONV = "i" * 13
 # symbol: (result code, argument codes); mirrors include/mfhip.h.
 _SIGNATURES = {
@@ -86,6 +87,11 @@ _SIGNATURES = {
     "mfh_info": ("s", ""),
     "mfh_set_debug_sync": ("-", "i"),
     "mfh_stream_wait": ("i", "pp"),
+    "mfh_program_begin": ("i", ""),
+    "mfh_program_end": ("i", "UL"),
+    "mfh_program_run": ("i", "p"),
+    "mfh_program_free": ("-", "p"),
+    "mfh_fill": ("i", "pqfp"),
     "mfh_conv_im2col": ("i", "pp" + _CONV + "p"),
     "mfh_conv_forward": ("i", "pppppp" + _CONV + "ifipqp"),
     "mfh_conv_backward": ("i", "pppppppppp" + _CONV + "iifiipqp"),
@@ -213,6 +219,36 @@ def stream_wait(waiting, signalling):
     """Raw stream `waiting` runs nothing issued after this call before the work issued so far on
     raw stream `signalling` has finished (mfh_stream_wait)."""
     _call("mfh_stream_wait", waiting, signalling)
+
+
+def fill_(tensor, value):
+    """tensor[...] = value (a contiguous float32 GPU tensor), as one library launch on the current
+    stream (mfh_fill)."""
+    tensor = _device_f32(tensor, "tensor")
+    _call("mfh_fill", tensor.data_ptr(), tensor.numel(), float(value), _stream())
+    return tensor
+
+
+def program_begin():
+    """Record every launch and stream ordering the library issues on this thread from now on into a
+    program (mfh_program_begin); program_end returns it."""
+    _call("mfh_program_begin")
+
+
+def program_end():
+    """(handle, kernel launches) of the program recorded since program_begin."""
+    handle, launches = ctypes.c_uint64(0), ctypes.c_int64(0)
+    _call("mfh_program_end", ctypes.byref(handle), ctypes.byref(launches))
+    return handle.value, launches.value
+
+
+def program_run(handle):
+    """Issue a recorded program again (mfh_program_run)."""
+    _call("mfh_program_run", handle)
+
+
+def program_free(handle):
+    _library().mfh_program_free(handle)
 
 
 def is_available():

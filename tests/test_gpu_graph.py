@@ -284,3 +284,57 @@ def test_captured_step_accumulates_gradients_over_several_replays():
     step.update()
     for a, b in zip(model_e.params, model_c.params):
         assert torch.equal(a.value, b.value)
+
+
+def _recorded_against_eager(batch, base_width=16, shape=(48, 64), overlap=True, steps=4):
+    """A network stepped eagerly and the same network stepped through a RecordedStep: the loss and
+    every parameter compared bit for bit after each Adam step, with eager work and a host
+    synchronisation between replays and a new input batch copied in before the third step."""
+    def build():
+        model = mf.ResNet18(output_dim=2, base_width=base_width, initializer=mf.make_initializer(seed=0),
+                            conv_backend="hip_native")
+        rng = np.random.default_rng(0)
+        x = mf.Variable(gpu(rng.standard_normal((batch, 3) + shape).astype(np.float32)), requires_grad=False)
+        t = mf.Variable(gpu(rng.uniform(-1, 1, (batch, 2)).astype(np.float32)), requires_grad=False)
+        loss = mf.MSELoss(model(x), t)
+        graph = mf.Graph(loss, optimize=True)
+        graph.overlap_weight_grads = graph.overlap_branches = overlap
+        return mf.Adam(graph, learning_rate=1e-3), loss, x, model
+
+    eager, loss_e, x_e, model_e = build()
+    recorded, loss_r, x_r, model_r = build()
+    step = mf.RecordedStep(recorded, warmup=2)
+    assert step.launches > 50
+    for _ in range(3):  # the warm-up passes and the recorded pass also move the BN running statistics
+        eager.graph.forward()
+        eager.graph.backward()
+    fresh = gpu(np.random.default_rng(9).standard_normal(tuple(x_e.value.shape)).astype(np.float32))
+    for k in range(steps):
+        if k == 2:
+            x_e.value = fresh.clone()
+            x_r.value.copy_(fresh)
+        eager.one_step()
+        eager.update()
+        step.one_step()
+        step.update()
+        assert np.array_equal(host(loss_e.value), host(loss_r.value)), f"loss differs at step {k}"
+        for a, b in zip(model_e.params, model_r.params):
+            assert torch.equal(a.value, b.value), f"a parameter differs at step {k}"
+        torch.randn(8, device="cuda").sum().item()
+    assert step.replays == steps
+    step.close()
+
+
+@pytest.mark.parametrize("overlap", (True, False), ids=("two-streams", "one-stream"))
+def test_recorded_step_replays_the_eager_step_bit_for_bit(overlap):
+    """RecordedStep (the library's launches and stream orderings of one forward and backward pass,
+    issued again from C) against the eager network, at batch 2 with a quarter of the widths."""
+    print("recorded step bs2", overlap, flush=True)
+    _recorded_against_eager(2, overlap=overlap)
+
+
+def test_recorded_step_at_the_bench_shape_replays_the_eager_step_bit_for_bit():
+    """The bench step (ResNet18, batch 64, 3x120x160, both streams, deferred split outputs) recorded
+    and replayed: the same loss and parameters as the eager step after each of three Adam steps."""
+    print("recorded step bs64", flush=True)
+    _recorded_against_eager(64, base_width=64, shape=(120, 160), steps=3)
