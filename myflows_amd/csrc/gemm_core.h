@@ -150,7 +150,7 @@ struct BufferRowTile {
 #pragma unroll
         for (int i = 0; i < PER_THREAD; ++i) {
             const int f = tid + i * THREADS;
-            if (f < ELEMS) *reinterpret_cast<float4*>(lds + f / VCOLS * LD + f % VCOLS * 4) = v[i];
+            if (ELEMS % THREADS == 0 || f < ELEMS) *reinterpret_cast<float4*>(lds + f / VCOLS * LD + f % VCOLS * 4) = v[i];
         }
     }
 };
@@ -384,9 +384,12 @@ __device__ __forceinline__ void mfma_k_loop(float* smem, int k_begin, int k_end,
 // store(slot, a_lds, b_lds) take the slot as std::integral_constant<int, 0 or 1>: stage t uses slot
 // t % 2 and LDS buffer t % 2. The MFMAs, their operands and their order are mfma_k_loop's (with
 // ORDER STAGE_PLAIN or STAGE_MID_STORE), so the results are its bits. fetch is issued for every stage, also for the two past
-// the end (kt >= k_end), so that the compiler sees the same loads in flight on every path and waits
-// for exactly one stage's: a loader must read nothing (or stay in bounds) there, as the buffer
-// loaders do, whose out-of-range lanes read zero.
+// the end (kt >= k_end), and store for every stage, also for the one past the end (into the LDS
+// buffer that no MFMA reads any more: every wave has passed the barrier after its last read), so
+// that the compiler sees the same loads in flight on every path and waits for exactly one stage's
+// (a conditional store makes it wait for the other slot's loads at the top of a stage): a loader
+// must read nothing (or stay in bounds) past the end, as the buffer loaders do, whose out-of-range
+// lanes read zero, and a store's side effects must not mind the zeros.
 template <class S, int ORDER = STAGE_PLAIN, class Fetch, class Store, class Drain = KeepChain>
 __device__ __forceinline__ void mfma_k_loop_ahead(float* smem, int k_begin, int k_end, Fetch&& fetch, Store&& store,
                                                   v16f (&acc)[S::TM][S::TN], int wm0, int wn0, int lane,
@@ -414,18 +417,23 @@ __device__ __forceinline__ void mfma_k_loop_ahead(float* smem, int k_begin, int 
         if constexpr (ORDER == STAGE_MID_STORE && S::HALF >= 8) {
             constexpr int MID = S::HALF / 8 * 4;
             mfma_stage<S, 0, MID, RESTART>(As, As + S::A_SIZE, acc, wm0, wn0, lane);
-            if (t + 1 < stages) store(Other{}, next, next + S::A_SIZE);
+            store(Other{}, next, next + S::A_SIZE);
             mfma_stage<S, MID, S::HALF>(As, As + S::A_SIZE, acc, wm0, wn0, lane);
         } else {
             mfma_stage<S, 0, S::HALF, RESTART>(As, As + S::A_SIZE, acc, wm0, wn0, lane);
-            if (t + 1 < stages) store(Other{}, next, next + S::A_SIZE);
+            store(Other{}, next, next + S::A_SIZE);
         }
         __syncthreads();
     };
-    for (int t = 0; t < stages; t += 2) {
+    // Pairs of stages, then an odd last one: a loop body that could skip its second stage would
+    // leave the compiler a path back to the first with that stage's loads still in flight, and it
+    // would then wait for them at the top of every pair.
+    int t = 0;
+    for (; t + 1 < stages; t += 2) {
         stage(Slot0{}, t);
-        if (t + 1 < stages) stage(Slot1{}, t + 1);
+        stage(Slot1{}, t + 1);
     }
+    if (t < stages) stage(Slot0{}, t);
     if (stages > 0) drain(acc);
 }
 

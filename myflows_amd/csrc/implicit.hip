@@ -221,56 +221,6 @@ struct GatherPixelColumns {
     }
 };
 
-// The same tile in chunked feature order. The tile's BN feature rows are BN / 32 groups of 32
-// channels at one (chunk, tap); thread r of a pixel column (R = THREADS / BK_WG of them) takes group
-// r % G and the channels r / G + i * (R / G) of it, so the PER features of a thread share a tap: one
-// bounds test per stage, then PER buffer loads a uniform channel stride apart (out-of-image lanes
-// read zero), where the natural order tests every feature and branches around every load.
-template <int BN, int THREADS>
-struct GatherTapColumns {
-    static constexpr int R = THREADS / BK_WG, G = BN / 32, SPAN = R / G, PER = 32 / SPAN;
-    static_assert(BN % 32 == 0 && R % G == 0 && 32 % SPAN == 0, "a pixel column's threads split the groups evenly");
-    __amdgpu_buffer_rsrc_t rsrc;
-    int offset, kh, kw, row0;  // offset: element offset of the thread's first channel at tap (kh, kw)
-
-    __device__ __forceinline__ void init(const ConvGather& g, int n0, int tid) {
-        rsrc = buffer_of(g.src, g.src_floats);
-        const int r = tid / BK_WG, group = r % G, sub = r / G;
-        row0 = group * 32 + sub;
-        const int k = n0 + group * 32;  // the group's first feature
-        if (k < g.features) {
-            int tap;
-            const int chunk = g.div_khkw.divmod(k / CHANNEL_CHUNK, tap);
-            kh = g.div_kw.divmod(tap, kw);
-            offset = (chunk * CHANNEL_CHUNK + sub) * g.hw + kh * g.W + kw;
-        } else {  // past the last feature: every pixel is out of bounds
-            kh = FAR;
-            kw = 0;
-            offset = 0;
-        }
-    }
-
-    float v[PER];
-
-    __device__ __forceinline__ void load(const ConvGather& g, const PixelAt& at) {
-        const int ih = at.ih0 + kh, iw = at.iw0 + kw;
-        const bool ok = at.valid && static_cast<unsigned>(ih) < static_cast<unsigned>(g.H) &&
-                        static_cast<unsigned>(iw) < static_cast<unsigned>(g.W);
-        const unsigned lane =
-            ok ? static_cast<unsigned>(at.n * g.chw + at.ih0 * g.W + at.iw0 + offset) * 4u : BUFFER_OOB;
-        const int step_bytes = SPAN * g.hw * 4;
-#pragma unroll
-        for (int i = 0; i < PER; ++i) v[i] = buffer_load(rsrc, lane, i * step_bytes);
-    }
-
-    template <int LD>
-    __device__ __forceinline__ void store(float* lds, int tid) const {
-        const int col = tid % BK_WG;
-#pragma unroll
-        for (int i = 0; i < PER; ++i) lds[(row0 + i * SPAN) * LD + col] = v[i];
-    }
-};
-
 // dW's A operand: dy read in place, A[co][q] = dy[n, co, p] for pixel q = (n, p), as a BM x BK_WG
 // k-contiguous tile (rows = output channels, columns = the same pixels as the gathered tile).
 template <int BM, int THREADS>
@@ -305,8 +255,8 @@ struct GradRowsInPlace {
     // The row sums over this workgroup's pixels: the BK_WG threads of a row (adjacent lanes)
     // combine their sums with a fixed butterfly, then the first of them stores the FP64 sum to
     // out[row], or, when the workgroup covers every pixel, its float rounding to final[row].
-    __device__ __forceinline__ void store_sums(double (&sums)[PER], double* out, float* final, int CO, int m0,
-                                               int tid) const {
+    __device__ __forceinline__ static void store_sums(double (&sums)[PER], double* out, float* final, int CO, int m0,
+                                               int tid) {
 #pragma unroll
         for (int i = 0; i < PER; ++i) {
             double s = sums[i];
@@ -410,6 +360,86 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void conv_implicit_grou
                                                       local % batch.tiles_n[j], 0);
 }
 
+// Both operand loads of one dW stage in chunked feature order: BK_WG pixels [kt, kt + BK_WG) of
+// dy's rows (A, BM x BK_WG) and of the gathered view's feature rows (B, BN x BK_WG), all with buffer
+// loads. Thread t owns pixel column kt + t % BK_WG and, with r = t / BK_WG (R threads per column),
+// the A rows r, r + R, ... The tile's BN feature rows are BN / 32 groups of 32 channels at one
+// (chunk, tap); thread r takes group r % G and the channels r / G + i * (R / G) of it, so its B_PER
+// features share a tap: one bounds test per stage, then loads a uniform channel stride apart. A
+// lane's offsets into dy and x are 32-bit and the row / channel steps wave-uniform (scalar
+// offsets), so a stage's loads need no 64-bit address arithmetic and no branches. A lane past the
+// pixel range, or whose window tap falls outside the image, reads zero.
+// Rows of A past CO read whatever lies there (rows of the next image, or zero past the tensor):
+// they only reach output rows past CO, which are never stored.
+template <int BM, int BN, int THREADS>
+struct WgradChunkStage {
+    static constexpr int R = THREADS / BK_WG, A_PER = BM / R;
+    static constexpr int G = BN / 32, SPAN = R / G, B_PER = 32 / SPAN;
+    static_assert(BM % R == 0 && BN % 32 == 0 && R % G == 0 && 32 % SPAN == 0,
+                  "a pixel column's threads split the rows and the groups evenly");
+    __amdgpu_buffer_rsrc_t dy_rsrc, x_rsrc;
+    int lo, a_row, kh, kw, b_offset, b_row0;
+    float a[A_PER], b[B_PER];
+
+    __device__ __forceinline__ void init(const ConvGather& g, const float* dy, int CO, int m0, int n0, int tid) {
+        dy_rsrc = buffer_of(dy, static_cast<long long>(g.pixels) * CO);
+        x_rsrc = buffer_of(g.src, g.src_floats);
+        lo = tid % BK_WG;
+        const int r = tid / BK_WG, group = r % G, sub = r / G;
+        a_row = m0 + r;
+        b_row0 = group * 32 + sub;
+        const int k = n0 + group * 32;  // the group's first feature
+        if (k < g.features) {
+            int tap;
+            const int chunk = g.div_khkw.divmod(k / CHANNEL_CHUNK, tap);
+            kh = g.div_kw.divmod(tap, kw);
+            b_offset = (chunk * CHANNEL_CHUNK + sub) * g.hw + kh * g.W + kw;
+        } else {  // past the last feature: every pixel is out of bounds
+            kh = FAR;
+            kw = 0;
+            b_offset = 0;
+        }
+    }
+
+    __device__ __forceinline__ void load(const ConvGather& g, int CO, int kt, int k_end) {
+        const int ohw = g.OH * g.OW;
+        const int q = kt + lo;
+        const bool valid = q < k_end;
+        int pix, ow;
+        const int n = g.div_ohw.divmod(valid ? q : 0, pix);
+        const int oh = g.div_ow.divmod(pix, ow);
+        const int ih0 = oh * g.SH - g.PH, iw0 = ow * g.SW - g.PW;
+        const int ih = ih0 + kh, iw = iw0 + kw;
+        const bool ok = valid && static_cast<unsigned>(ih) < static_cast<unsigned>(g.H) &&
+                        static_cast<unsigned>(iw) < static_cast<unsigned>(g.W);
+        // Both lane offsets first (selects, no branch around the loads), then the loads.
+        const unsigned a_at = static_cast<unsigned>((n * CO + a_row) * ohw + pix) * 4u;
+        const unsigned b_at = static_cast<unsigned>(n * g.chw + ih0 * g.W + iw0 + b_offset) * 4u;
+        const unsigned a_lane = valid ? a_at : BUFFER_OOB;
+        const unsigned b_lane = ok ? b_at : BUFFER_OOB;
+        const int a_step = R * ohw * 4, b_step = SPAN * g.hw * 4;
+#pragma unroll
+        for (int i = 0; i < A_PER; ++i) a[i] = buffer_load(dy_rsrc, a_lane, i * a_step);
+#pragma unroll
+        for (int i = 0; i < B_PER; ++i) b[i] = buffer_load(x_rsrc, b_lane, i * b_step);
+    }
+
+    template <int LDA, int LDB>
+    __device__ __forceinline__ void store(float* a_lds, float* b_lds, int tid) const {
+        const int r = tid / BK_WG;
+#pragma unroll
+        for (int i = 0; i < A_PER; ++i) a_lds[(r + i * R) * LDA + lo] = a[i];
+#pragma unroll
+        for (int i = 0; i < B_PER; ++i) b_lds[(b_row0 + i * SPAN) * LDB + lo] = b[i];
+    }
+
+    // Adds this thread's A values (0 past the pixel range) to its FP64 row sums.
+    __device__ __forceinline__ void add_to(double (&sums)[A_PER]) const {
+#pragma unroll
+        for (int i = 0; i < A_PER; ++i) sums[i] += static_cast<double>(a[i]);
+    }
+};
+
 // dW (CO x K) = dy (CO x pixels) . view^T (pixels x K), the pixel range split over z when p.split.
 // SUMS: the workgroups of feature tile 0 also sum each dy row over their pixel range in FP64, the
 // conv bias gradient: db[co] directly when unsplit, else sums[z * CO + co] for the reduction.
@@ -427,45 +457,57 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void conv_implicit_wgra
     const int k_end = p.split ? min(p.K, k_begin + p.k_chunk) : p.K;
     float* __restrict__ C = p.C + (p.split ? z * p.c_batch : 0);
     const int ohw = g.OH * g.OW;
-
-    // Chunked products read two stages ahead (two register slots of loaders).
-    constexpr int SLOTS = CHUNKED ? 2 : 1;
+    v16f acc[S::TM][S::TN];
+    zero_acc<S>(acc);
     using RowLoader = GradRowsInPlace<BM, S::THREADS>;
-    RowLoader la[SLOTS];
-    std::conditional_t<CHUNKED, GatherTapColumns<BN, S::THREADS>, GatherPixelColumns<BN, S::THREADS>> lb[SLOTS];
-#pragma unroll
-    for (int i = 0; i < SLOTS; ++i) lb[i].init(g, n0, tid);
-    const bool summing = SUMS && tile_n == 0;
     double row_sums[RowLoader::PER];
 #pragma unroll
     for (int i = 0; i < RowLoader::PER; ++i) row_sums[i] = 0.0;
-    auto fetch_slot = [&](int slot, int kt) {
-        const PixelAt at = pixel_at(g, kt + tid % BK_WG, k_end);
-        la[slot].load(p.A, p.M, ohw, m0, at, tid);
-        lb[slot].load(g, at);
-    };
-    auto store_slot = [&](int slot, float* a_lds, float* b_lds) {
-        la[slot].template store<S::LDA_S>(a_lds, tid);
-        lb[slot].template store<S::LDB_S>(b_lds, tid);
-        if constexpr (SUMS)
-            if (summing) la[slot].add_to(row_sums);
-    };
-    v16f acc[S::TM][S::TN];
-    zero_acc<S>(acc);
+    const bool summing = SUMS && tile_n == 0;
+
     if constexpr (CHUNKED) {
-        mfma_k_loop_ahead<S, STAGE_MID_STORE>(
-            smem, k_begin, k_end, [&](auto slot, int kt) { fetch_slot(decltype(slot)::value, kt); },
-            [&](auto slot, float* a_lds, float* b_lds) { store_slot(decltype(slot)::value, a_lds, b_lds); }, acc, wm0,
-            wn0, lane);
+        // Two register slots of loads, two stages ahead; the row sums as a separate loop body, so
+        // that the other feature tiles' stages carry no FP64 work.
+        using Stage = WgradChunkStage<BM, BN, S::THREADS>;
+        static_assert(Stage::A_PER == RowLoader::PER, "the row sums follow the A rows");
+        Stage st[2];
+#pragma unroll
+        for (int i = 0; i < 2; ++i) st[i].init(g, p.A, p.M, m0, n0, tid);
+        auto fetch = [&](auto slot, int kt) { st[decltype(slot)::value].load(g, p.M, kt, k_end); };
+        if (summing) {
+            auto store = [&](auto slot, float* a_lds, float* b_lds) {
+                st[decltype(slot)::value].template store<S::LDA_S, S::LDB_S>(a_lds, b_lds, tid);
+                st[decltype(slot)::value].add_to(row_sums);
+            };
+            mfma_k_loop_ahead<S, STAGE_MID_STORE>(smem, k_begin, k_end, fetch, store, acc, wm0, wn0, lane);
+        } else {
+            auto store = [&](auto slot, float* a_lds, float* b_lds) {
+                st[decltype(slot)::value].template store<S::LDA_S, S::LDB_S>(a_lds, b_lds, tid);
+            };
+            mfma_k_loop_ahead<S, STAGE_MID_STORE>(smem, k_begin, k_end, fetch, store, acc, wm0, wn0, lane);
+        }
     } else {
-        mfma_k_loop<S, STAGE_MID_STORE>(
-            smem, k_begin, k_end, [&](int kt) { fetch_slot(0, kt); },
-            [&](float* a_lds, float* b_lds) { store_slot(0, a_lds, b_lds); }, acc, wm0, wn0, lane);
+        RowLoader la;
+        GatherPixelColumns<BN, S::THREADS> lb;
+        lb.init(g, n0, tid);
+        auto fetch = [&](int kt) {
+            const PixelAt at = pixel_at(g, kt + tid % BK_WG, k_end);
+            la.load(p.A, p.M, ohw, m0, at, tid);
+            lb.load(g, at);
+        };
+        auto store = [&](float* a_lds, float* b_lds) {
+            la.template store<S::LDA_S>(a_lds, tid);
+            lb.template store<S::LDB_S>(b_lds, tid);
+            if constexpr (SUMS)
+                if (summing) la.add_to(row_sums);
+        };
+        mfma_k_loop<S, STAGE_MID_STORE>(smem, k_begin, k_end, fetch, store, acc, wm0, wn0, lane);
     }
     store_acc<S>(p, C, acc, m0, n0, wm0, wn0, lane);
     if constexpr (SUMS)
         if (summing)
-            la[0].store_sums(row_sums, sums + static_cast<long long>(z) * p.M, p.split ? nullptr : db, p.M, m0, tid);
+            RowLoader::store_sums(row_sums, sums + static_cast<long long>(z) * p.M, p.split ? nullptr : db, p.M, m0,
+                                  tid);
 }
 
 // The kernel as the A operand of an implicit product: out[o][k] for O rows and features k over C
@@ -802,7 +844,8 @@ GemmPlan wgrad_plan(int M, int N, int K) {
 // beat the automatic plan below by at least 2 % (ResNet18's batch-64 convolutions at 3x120x160, and
 // its batch-256 inference forwards at 224x224). The forward-orientation entries were re-measured for
 // the two-level stage sums, whose extra registers cost tiles 8, 10 and 11 a resident workgroup; the
-// dW entries for the reads two stages ahead.
+// dW entries for the chunked dW loads of WgradChunkStage (layer2 to layer4 moved to tile 6 with
+// fewer slices, 5-8 % faster than their previous plans).
 // Key: orientation (0 forward / dX, 1 dW), M, N, K; value: tile and requested K split.
 struct MeasuredPlan {
     int wgrad, M, N, K, tile, requested;
@@ -831,14 +874,14 @@ constexpr MeasuredPlan MEASURED_PLANS[] = {
     {1, 64, 147, 307200, 6, 256},  // stem dW (more slices than the dW rule makes: its gathers need the waves)
     {1, 64, 576, 72384, 8, 96},    // layer1 dW
     {1, 128, 576, 19200, 8, 48},   // layer2.0 conv1 dW
-    {1, 128, 1152, 19200, 8, 24},  // layer2 3x3 dW
+    {1, 128, 1152, 19200, 6, 48},  // layer2 3x3 dW
     {1, 128, 64, 19200, 6, 128},   // layer2 1x1 downsample dW
-    {1, 256, 1152, 5120, 6, 24},   // layer3.0 conv1 dW
-    {1, 256, 2304, 5120, 8, 16},   // layer3 3x3 dW
+    {1, 256, 1152, 5120, 8, 12},   // layer3.0 conv1 dW
+    {1, 256, 2304, 5120, 6, 12},   // layer3 3x3 dW
     {1, 256, 128, 5120, 6, 32},    // layer3 1x1 downsample dW
-    {1, 512, 2304, 1280, 8, 8},    // layer4.0 conv1 dW
+    {1, 512, 2304, 1280, 6, 4},    // layer4.0 conv1 dW
     {1, 512, 256, 1280, 6, 8},     // layer4 1x1 downsample dW
-    {1, 512, 4608, 1280, 8, 8},    // layer4 3x3 dW
+    {1, 512, 4608, 1280, 6, 4},    // layer4 3x3 dW
 };
 
 // The plan of a product: a measured plan when one matches, else the dW rule, else the plan of least
@@ -955,7 +998,9 @@ int run_implicit(bool wgrad, const GemmPlan& plan, const float* a, int lda, int 
     const bool vec_a = K % 4 == 0 && lda % 4 == 0 && aligned16(a);
     const int variant = g.chunked ? 2 : vec_a ? 1 : 0;
     if (!wgrad && g.chunked && !vec_a) return MFH_FAIL(ERR_ARG, "the reordered kernel buffer must be 16-byte aligned");
-    if (g.chunked && (wgrad ? g.src_floats > BUFFER_LIMIT_FLOATS : !buffer_extents_fit(g, M, lda)))
+    if (g.chunked && (wgrad ? g.src_floats > BUFFER_LIMIT_FLOATS || static_cast<std::int64_t>(g.pixels) * M >
+                                                                       BUFFER_LIMIT_FLOATS
+                            : !buffer_extents_fit(g, M, lda)))
         return MFH_FAIL(ERR_ARG, "a chunked implicit convolution reads tensors of at most 2 GiB");
     if (wgrad)
         launch(conv_kernels().wgrad[plan.tile][row_out ? 1 : 0][g.chunked ? 1 : 0], grid, block, 0, stream,

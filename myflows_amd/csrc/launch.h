@@ -68,8 +68,8 @@ void launch(void (*kernel)(Params...), dim3 grid, dim3 block, std::size_t shared
     static_assert(sizeof...(Params) == sizeof...(Args), "launch() takes one argument per kernel parameter");
     std::tuple<std::decay_t<Params>...> packed(static_cast<std::decay_t<Params>>(std::forward<Args>(args))...);
     const void* entry = reinterpret_cast<const void*>(kernel);
-    launch_packed(entry, grid, block, static_cast<unsigned>(shared), stream, packed,
-                  std::index_sequence_for<Params...>{});
+    (void)launch_packed(entry, grid, block, static_cast<unsigned>(shared), stream, packed,
+                        std::index_sequence_for<Params...>{});
     if (Program* program = recording()) {
         program->steps.push_back(std::make_unique<KernelStep<std::decay_t<Params>...>>(
             entry, grid, block, static_cast<unsigned>(shared), stream, std::move(packed)));
