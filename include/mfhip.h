@@ -184,6 +184,7 @@ MFH_API int64_t mfh_conv_implicit_workspace(int N, int CI, int H, int W, int CO,
 /* flags of mfh_conv_backward_implicit */
 #define MFH_CONV_WFLIP_READY 1   /* wflip already holds the dX order (mfh_conv_weight_orders, flip 1) */
 #define MFH_CONV_ACCUMULATE_DX 2 /* dx += the input gradient (dx holds a gradient already) */
+#define MFH_CONV_COLUMN_ORDER 4  /* a strided dX through grad_cols reads the column order in wflip */
 
 /* Backward of a convolution without cols, from x and the NCHW dy:
  *   gated (N*CO*OH*OW floats) receives dy gated by the fused activation through y; required when
@@ -201,7 +202,12 @@ MFH_API int64_t mfh_conv_implicit_workspace(int N, int CI, int H, int W, int CO,
  *          of each phase (a, b) (input positions SH*i + a, SW*j + b; the taps that reach them),
  *          each written to its lattice of dx, positions that no tap reaches set to 0; straight
  *          into NCHW dx. Strides above 1 without wflip: the per-image column gradient W^T dy_n in
- *          grad_cols (N*CI*KH*KW*OH*OW floats) and the col2im gather.
+ *          grad_cols (N*CI*KH*KW*OH*OW floats) and the col2im gather; with grad_cols and
+ *          MFH_CONV_COLUMN_ORDER (CO a multiple of 32) the column gradient is one implicit product
+ *          over every image, the dX of a 1x1 convolution from CI*KH*KW channels to CO on the OH x OW
+ *          grid, whose kernel order wflip holds (mfh_conv_weight_orders of W seen as a
+ *          CO x CI*KH*KW x 1 x 1 kernel, flip 1; filled from `weight` here unless
+ *          MFH_CONV_WFLIP_READY).
  *          With MFH_CONV_ACCUMULATE_DX, dx = dx + the gradient (one rounding, as a separate add).
  * workspace: at least the larger of mfh_conv_implicit_workspace passes 1 and 2 that are requested
  * (pass 2 covers the largest phase product of a strided dX).

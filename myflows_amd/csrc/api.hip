@@ -191,14 +191,21 @@ int conv_backward_implicit(std::uint64_t x, std::uint64_t weight, std::uint64_t 
     const bool gated_dy = activation != ACT_NONE;
     const bool unit_stride = g.SH == 1 && g.SW == 1;
     // dW and dX given wflip are implicit products (a strided dX as its phase products); a strided dX
-    // given grad_cols is a dense GEMM into the column gradient and col2im.
-    const bool phases = !unit_stride && wflip != 0;
+    // given grad_cols goes through the column gradient and col2im: one implicit product with the
+    // column order in wflip (MFH_CONV_COLUMN_ORDER), else a dense GEMM per image.
+    const bool column_order = !unit_stride && (flags & MFH_CONV_COLUMN_ORDER) != 0;
+    const bool phases = !unit_stride && wflip != 0 && !column_order;
     MFH_REQUIRE(implicit_engine_valid(dw_engine), "unknown implicit convolution engine or plan code");
-    if (unit_stride || phases) MFH_REQUIRE(implicit_engine_valid(dx_engine), "unknown implicit convolution engine or plan code");
+    if (unit_stride || phases || column_order)
+        MFH_REQUIRE(implicit_engine_valid(dx_engine), "unknown implicit convolution engine or plan code");
     else MFH_TRY(validate_engine(dx_engine));
     const bool prepared = (flags & MFH_CONV_WFLIP_READY) != 0, accumulate = (flags & MFH_CONV_ACCUMULATE_DX) != 0;
-    MFH_REQUIRE((flags & ~(MFH_CONV_WFLIP_READY | MFH_CONV_ACCUMULATE_DX)) == 0, "unknown conv backward flags");
-    MFH_REQUIRE(dy && (weight || ((unit_stride || phases) && prepared)), "conv backward needs weight and dy");
+    MFH_REQUIRE((flags & ~(MFH_CONV_WFLIP_READY | MFH_CONV_ACCUMULATE_DX | MFH_CONV_COLUMN_ORDER)) == 0,
+                "unknown conv backward flags");
+    MFH_REQUIRE(!column_order || (!dx || (wflip && grad_cols && implicit_chunked(g.CO))),
+                "the column order needs wflip, grad_cols and a multiple of 32 output channels");
+    MFH_REQUIRE(dy && (weight || ((unit_stride || phases || column_order) && prepared)),
+                "conv backward needs weight and dy");
     MFH_REQUIRE(!gated_dy || (y && gated), "a fused activation needs the forward output and the gated buffer");
     MFH_REQUIRE((partial == 0) == (db == 0), "partial and db must be given together");
     MFH_REQUIRE(!dw || x, "dW needs x");
@@ -230,6 +237,15 @@ int conv_backward_implicit(std::uint64_t x, std::uint64_t weight, std::uint64_t 
     if (phases)
         return conv_implicit_dgrad_phases(g, grad, as_ptr<const float>(weight), as_ptr<float>(wflip), prepared,
                                           as_ptr<float>(dx), accumulate, dx_engine, ws_dx, dx_floats, s);
+    if (column_order) {
+        // The column gradient gcT[n][f][p] = sum_co W[co][f] dy[n][co][p] is the dX of a 1x1
+        // convolution from CI*KH*KW channels to CO channels on the OH x OW grid: one implicit product
+        // over every image, reading dy in place, with the 1x1 kernel's dX order of W in wflip.
+        const ConvGeometry g1 = column_geometry(g);
+        MFH_TRY(conv_implicit_dgrad(g1, grad, as_ptr<const float>(weight), as_ptr<float>(wflip), prepared,
+                                    as_ptr<float>(grad_cols), false, dx_engine, ws_dx, dx_floats, s));
+        return launch_col2im_t(as_ptr<const float>(grad_cols), as_ptr<float>(dx), g, true, accumulate, s);
+    }
     bool per_image = false;
     MFH_TRY(column_gradient(dx_engine, g, as_ptr<const float>(weight), grad, nullptr, as_ptr<float>(grad_cols),
                             &per_image, s));

@@ -64,6 +64,13 @@ struct ConvGeometry {
     int features() const { return CI * KH * KW; }  // K of the im2col matrix
 };
 
+// The column gradient of a convolution's dX as a convolution: the dX of a 1x1 convolution from
+// CI*KH*KW channels to CO channels on the OH x OW output grid (whose input is the per-image column
+// gradient [n][CI*KH*KW][OH*OW]).
+inline ConvGeometry column_geometry(const ConvGeometry& g) {
+    return ConvGeometry{g.N, g.CI * g.KH * g.KW, g.OH, g.OW, g.CO, 1, 1, g.OH, g.OW, 1, 1, 0, 0};
+}
+
 // ---- conv.hip ---------------------------------------------------------------------------------
 int launch_im2col(const float* x, float* cols, const ConvGeometry& g, hipStream_t stream);
 // dx from the feature-major column gradient: gcT[n][CI*KH*KW][OH*OW] when per_image, else

@@ -1028,7 +1028,8 @@ bool implicit_engine_valid(int engine) { return engine == 1 || (engine >= 16 && 
 
 std::int64_t implicit_workspace_floats(const ConvGeometry& g, int pass) {
     if (pass == IMPLICIT_DGRAD && (g.SH > 1 || g.SW > 1)) {
-        std::int64_t most = 0;
+        // Phase products, or the column gradient's one product (MFH_CONV_COLUMN_ORDER).
+        std::int64_t most = implicit_chunked(g.CO) ? implicit_workspace_floats(column_geometry(g), pass) : 0;
         for (int a = 0; a < g.SH; ++a)
             for (int b = 0; b < g.SW; ++b) {
                 const DgradPhase ph = dgrad_phase(g, a, b);

@@ -57,7 +57,7 @@ CONV_ALGORITHMS = ("implicit", "im2col")
 IMPLICIT_PASSES = {"forward": 0, "dw": 1, "dx": 2}
 CHANNEL_CHUNK = 32        # implicit products take features in chunks of this many channels per tap
 BIAS_PARTIAL_ROWS = 256   # rows of FP64 bias partials a dW product may write (its pixel slices)
-CONV_WFLIP_READY, CONV_ACCUMULATE_DX = 1, 2  # flags of mfh_conv_backward_implicit
+CONV_WFLIP_READY, CONV_ACCUMULATE_DX, CONV_COLUMN_ORDER = 1, 2, 4  # flags of mfh_conv_backward_implicit
 _STATUS_TEXT = {1: "initialization failed", 2: "invalid argument", 3: "HIP runtime error", 5: "wrong HIP device"}
 
 
@@ -753,13 +753,13 @@ def conv2d_backward(x, weight, grad_y, cols, *, stride=(1, 1), padding=(0, 0), n
     recompute_cols); "implicit" gathers them from x inside the GEMM. Without an algorithm, a call
     that passes cols (and does not recompute them) takes "im2col", any other the default (im2col,
     recomputing cols, where implicit_fits says the implicit products cannot read the tensors).
-    Implicit only: weight_flip is this kernel from conv_weight_orders(flip 1, with this stride and
-    padding) for the dX; input_grad is a gradient of x already there, to which dX is added in place
-    (it is then the returned dx); strided_dx chooses how a strided convolution's dX runs: "phases"
-    (one stride-1 implicit product per output phase, written to its lattice of dx), "columns" (the
-    per-image column gradient GEMM and col2im) or "auto": phases for a 1x1 kernel (a single phase
-    product), columns otherwise (measured on MI355X: the phases of a 3x3 kernel are small-K
-    products whose launches and split-K reductions cost more than the column path).
+    Implicit only: weight_flip is this kernel from conv_weight_orders for the dX route taken (flip 1
+    with this stride and padding for the dX orders; for the column route, the kernel seen as a
+    (CO, CI*KH*KW, 1, 1) kernel with flip 1); input_grad is a gradient of x already there, to which
+    dX is added in place (it is then the returned dx); strided_dx chooses how a strided
+    convolution's dX runs: "phases" (one stride-1 implicit product per output phase, written to its
+    lattice of dx), "columns" (the column gradient, then col2im: one implicit product over every
+    image when CO is a multiple of 32, else a GEMM per image) or "auto" (strided_dx_phases decides).
     Implicit only: dw_stream (a raw stream handle of the current device) runs the dW and db
     products beside the dX product on the current stream (mfh_conv_backward_implicit_streams); dw
     and db are complete once the current stream has been ordered after dw_stream (stream_wait). The
@@ -852,17 +852,22 @@ def _conv2d_backward_implicit(x, weight, grad_y, g, need_bias_grad, need_input_g
             dx = torch.empty_like(x)
     wflip = None
     through_orders = unit_stride or phases  # dX through the (phase) dX orders, else columns + col2im
-    if need_input_grad and through_orders:
+    # The column gradient as one implicit product reads W through its column order (the dX order of
+    # W seen as a 1x1 kernel of CI*KH*KW channels) when dy's channels come in chunks.
+    column_order = need_input_grad and not through_orders and implicit_chunked(g.co)
+    if need_input_grad and (through_orders or column_order):
         if weight_flip is not None:
             wflip, flags = _weight_order_buffer(weight_flip, weight, "weight_flip"), flags | CONV_WFLIP_READY
         else:
             wflip = empty(g.ci * g.co * g.kh * g.kw)
+        if column_order:
+            flags |= CONV_COLUMN_ORDER
     elif weight_flip is not None:
-        raise ValueError("weight_flip applies to a dX through the dX orders")
+        raise ValueError("weight_flip applies to a dX through the dX orders or the column order")
     grad_cols = empty(g.m * g.k) if need_input_grad and not through_orders else None
     partial = empty(max(g.n, BIAS_PARTIAL_ROWS) * g.co, dtype=torch.float64) if need_bias_grad else None
     db = empty(g.co) if need_bias_grad else None
-    passes = (("dw",) if need_weight_grad else ()) + (("dx",) if need_input_grad and through_orders else ())
+    passes = (("dw",) if need_weight_grad else ()) + (("dx",) if wflip is not None else ())
     pointers = (x.data_ptr(), weight.data_ptr(), grad_y.data_ptr(), _addr(gate), _addr(gated), _addr(dw), _addr(dx),
                 _addr(wflip), _addr(grad_cols), _addr(partial), _addr(db), *g.c_args(), act, alpha, engine, engine,
                 flags)

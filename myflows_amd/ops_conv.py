@@ -114,7 +114,11 @@ class Conv2D_Op(GradientOp):
         kernel = self._saved[1]
         if self.stride != (1, 1) and (kernel.ndim != 4 or not native.strided_dx_phases(
                 kernel.shape[2], kernel.shape[3], kernel.shape[0], self.stride)):
-            return []  # that dX runs through the column gradient, which reads the kernel in place
+            # That dX runs through the column gradient: its one implicit product reads the dX order
+            # of the kernel seen as a 1x1 kernel of CI*KH*KW channels (when dy has chunked channels).
+            if kernel.ndim == 4 and native.implicit_chunked(kernel.shape[0]):
+                return [(kernel.reshape(kernel.shape[0], -1, 1, 1), 1)]
+            return []
         return [(kernel, 1, self.stride, self.padding)]
 
     def take_weight_orders(self, phase, tensors):

@@ -325,12 +325,15 @@ def test_strided_dx_orders_are_the_phase_sub_kernels():
 @pytest.mark.parametrize("case", CONV_CASES[1:] + (RESNET_CASES[2], RESNET_CASES[3], RESNET_CASES[0],
                                                    ("s3", (2, 32, 13, 11), (32, 32, 4, 5), (3, 2), (2, 1)),
                                                    ("ds_even", (2, 32, 8, 10), (64, 32, 1, 1), (2, 2), (0, 0)),
-                                                   ("ds_pad", (1, 32, 7, 9), (32, 32, 1, 1), (2, 2), (1, 0))),
+                                                   ("ds_pad", (1, 32, 7, 9), (32, 32, 1, 1), (2, 2), (1, 0)),
+                                                   ("l4down3x3", (2, 256, 8, 10), (512, 256, 3, 3), (2, 2), (1, 1))),
                          ids=lambda c: c[0])
 def test_strided_dx_phases_equal_the_column_path_on_integer_data(case):
     """The phase products and the column-gradient path give the same dX (and the FP64 loops') bit
     for bit on integer data, written fresh and added to an existing gradient; positions that no
-    tap reaches (a 1x1 stride-2 kernel) are zero."""
+    tap reaches (a 1x1 stride-2 kernel) are zero. The column path is one implicit product when the
+    output channels come in chunks of 32 (its column order made by the call, or prepared by
+    conv_weight_orders as the Graph does), a GEMM per image otherwise."""
     _, x_shape, w_shape, stride, padding = case
     print("phases", case[0], flush=True)
     rng = np.random.default_rng(19)
@@ -339,17 +342,21 @@ def test_strided_dx_phases_equal_the_column_path_on_integer_data(case):
     n, co, oh, ow = (x_shape[0], w_shape[0], *rp.out_size(x_shape[2], x_shape[3], w_shape[2:], stride, padding))
     dy = rng.integers(-2, 3, size=(n, co, oh, ow)).astype(np.float32)
     ref_dx, _ = naive.conv_backward(x.astype(np.float64), w.astype(np.float64), dy.astype(np.float64), stride, padding)
-    results = {}
-    for path in ("phases", "columns"):
+    paths = [("phases", None), ("columns", None)]
+    if w_shape[0] % 32 == 0:
+        paths.append(("columns", native.conv_weight_orders([(gpu(w).reshape(w_shape[0], -1, 1, 1), 1)])[0]))
+    for path, order in paths:
+        label = path + (" prepared order" if order is not None else "")
         dx, _, _ = native.conv2d_backward(gpu(x), gpu(w), gpu(dy), None, stride=stride, padding=padding,
                                           algorithm="implicit", need_weight_grad=False, need_bias_grad=False,
-                                          strided_dx=path)
-        np.testing.assert_array_equal(host(dx), ref_dx, err_msg=path)
+                                          strided_dx=path, weight_flip=order)
+        np.testing.assert_array_equal(host(dx), ref_dx, err_msg=label)
         existing = gpu(rng.integers(-2, 3, size=x_shape).astype(np.float32))
         expected = host(existing) + ref_dx
         native.conv2d_backward(gpu(x), gpu(w), gpu(dy), None, stride=stride, padding=padding, algorithm="implicit",
-                               need_weight_grad=False, need_bias_grad=False, strided_dx=path, input_grad=existing)
-        np.testing.assert_array_equal(host(existing), expected, err_msg=f"{path} accumulate")
+                               need_weight_grad=False, need_bias_grad=False, strided_dx=path, input_grad=existing,
+                               weight_flip=order)
+        np.testing.assert_array_equal(host(existing), expected, err_msg=f"{label} accumulate")
 
 
 @pytest.mark.parametrize("shape,stride,padding", (((2, 64, 29, 39), (2, 2), (0, 0)), ((2, 64, 8, 10), (2, 2), (0, 0)),
