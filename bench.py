@@ -222,10 +222,16 @@ def c3_kernels():
     pool_forward()
     out = {"config": "Conv2D 64->64 3x3/1/1, N=32, 30x40; MaxPool 2x2/2", "peak_GB/s": HBM_PEAK_GBS,
            "peak_TFLOP/s": FP32_MFMA_PEAK_TFLOPS}
-    bytes_im2col = 4 * (n * ci * h * w + m * k)
+    grad_cols = torch.randn((n, k, h * w), generator=g).cuda()  # feature-major, per image
+    dxc = torch.empty_like(x)
+
+    def col2im():
+        native._raise_for(lib.mfh_conv_col2im(grad_cols.data_ptr(), dxc.data_ptr(), *dims, 1, 0, stream), lib)
+
+    bytes_im2col = 4 * (n * ci * h * w + m * k)  # read x, write cols; col2im: read grad_cols, write dx
     bytes_pool = 4 * n * co * h * w + 8 * n * co * (h // 2) * (w // 2)
-    for name, fn, nbytes in (("im2col", im2col, bytes_im2col), ("pool_forward", pool_forward, bytes_pool),
-                             ("pool_backward", pool_backward, bytes_pool)):
+    for name, fn, nbytes in (("im2col", im2col, bytes_im2col), ("col2im", col2im, bytes_im2col),
+                             ("pool_forward", pool_forward, bytes_pool), ("pool_backward", pool_backward, bytes_pool)):
         us = _event_time_us(fn)
         gbs = nbytes / (us * 1e-6) / 1e9
         out[name] = {"us": round(us, 2), "bytes": nbytes, "GB/s": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 3)}

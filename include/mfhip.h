@@ -99,6 +99,17 @@ MFH_API int mfh_fill(uint64_t p, int64_t count, float value, uint64_t stream);
 MFH_API int mfh_conv_im2col(uint64_t x, uint64_t cols, int N, int CI, int H, int W, int CO, int KH, int KW, int OH,
                             int OW, int SH, int SW, int PH, int PW, uint64_t stream);
 
+/* dx (N, CI, H, W) = col2im of a feature-major column gradient: the sum, over every window position
+ * that reads an input position, of that position's column-gradient entry, in a fixed order (so the
+ * result is deterministic). grad_cols is [n][CI*KH*KW][OH*OW] when per_image, else
+ * [CI*KH*KW][N*OH*OW]; with accumulate, dx += the sums.
+ * No counterpart of its own in the reference, whose col2im (native_cublas.cpp:247-271, over the
+ * pixel-major grad_cols) runs inside mf_conv_backward_plans: for callers that form the column
+ * gradient themselves, and to time the col2im pass alone. */
+MFH_API int mfh_conv_col2im(uint64_t grad_cols, uint64_t dx, int N, int CI, int H, int W, int CO, int KH, int KW,
+                            int OH, int OW, int SH, int SW, int PH, int PW, int per_image, int accumulate,
+                            uint64_t stream);
+
 /* y (N,CO,OH,OW) = act(conv(x, weight) + bias). cols receives im2col(x) (kept by the caller for
  * dW). With rows == 0 one GEMM W cols^T over all images writes y straight into NCHW, bias and
  * activation in its epilogue (workspace: the mfh_gemm_workspace(CO, N*OH*OW, CI*KH*KW) floats that

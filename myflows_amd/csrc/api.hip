@@ -388,6 +388,19 @@ MFH_API int mfh_conv_im2col(std::uint64_t x, std::uint64_t cols, int N, int CI, 
     return launch_im2col(as_ptr<const float>(x), as_ptr<float>(cols), g, as_stream(stream));
 }
 
+MFH_API int mfh_conv_col2im(std::uint64_t grad_cols, std::uint64_t dx, int N, int CI, int H, int W, int CO, int KH,
+                            int KW, int OH, int OW, int SH, int SW, int PH, int PW, int per_image, int accumulate,
+                            std::uint64_t stream) {
+    MFH_TRY(require_ready());
+    const ConvGeometry g{N, CI, H, W, CO, KH, KW, OH, OW, SH, SW, PH, PW};
+    MFH_TRY(validate(g));
+    MFH_REQUIRE(grad_cols && dx, "col2im needs input and output buffers");
+    MFH_REQUIRE((per_image == 0 || per_image == 1) && (accumulate == 0 || accumulate == 1),
+                "per_image and accumulate must be 0 or 1");
+    return launch_col2im_t(as_ptr<const float>(grad_cols), as_ptr<float>(dx), g, per_image != 0, accumulate != 0,
+                           as_stream(stream));
+}
+
 MFH_API int mfh_conv_forward(std::uint64_t x, std::uint64_t weight, std::uint64_t bias, std::uint64_t cols,
                              std::uint64_t rows, std::uint64_t y, int N, int CI, int H, int W, int CO, int KH, int KW,
                              int OH, int OW, int SH, int SW, int PH, int PW, int activation, float alpha, int engine,

@@ -341,8 +341,30 @@ __global__ __launch_bounds__(256) void im2col_row_kernel(const float* __restrict
         return static_cast<unsigned>(iw) < static_cast<unsigned>(W) ? band[(ci * KH + kh) * W + iw] : 0.0f;
     };
     if constexpr (VEC) {
-        for (int j = threadIdx.x * 4; j < count; j += 256 * 4)
-            *reinterpret_cast<float4*>(out + j) = make_float4(value(j), value(j + 1), value(j + 2), value(j + 3));
+        // Four consecutive features of one window position per thread: (ow, first feature) and its
+        // (ci, kh, kw) are decomposed once, the other three step kw, then kh, then ci forward.
+        for (int j = threadIdx.x * 4; j < count; j += 256 * 4) {
+            int f;
+            const int ow = div_k.divmod(j, f);
+            int tap, kw;
+            int ci = div_khkw.divmod(f, tap);
+            int kh = div_kw.divmod(tap, kw);
+            const int iw0 = ow * SW - PW;
+            float v[4];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const int iw = iw0 + kw;
+                v[u] = static_cast<unsigned>(iw) < static_cast<unsigned>(W) ? band[(ci * KH + kh) * W + iw] : 0.0f;
+                if (++kw == KW) {
+                    kw = 0;
+                    if (++kh == KH) {
+                        kh = 0;
+                        ++ci;
+                    }
+                }
+            }
+            *reinterpret_cast<float4*>(out + j) = make_float4(v[0], v[1], v[2], v[3]);
+        }
     } else {
         for (int j = threadIdx.x; j < count; j += 256) out[j] = value(j);
     }

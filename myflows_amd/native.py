@@ -93,6 +93,7 @@ _SIGNATURES = {
     "mfh_program_free": ("-", "p"),
     "mfh_fill": ("i", "pqfp"),
     "mfh_conv_im2col": ("i", "pp" + _CONV + "p"),
+    "mfh_conv_col2im": ("i", "pp" + _CONV + "iip"),
     "mfh_conv_forward": ("i", "pppppp" + _CONV + "ifipqp"),
     "mfh_conv_backward": ("i", "pppppppppp" + _CONV + "iifiipqp"),
     "mfh_conv_forward_implicit": ("i", "pppippp" + _CONV + "ifipqp"),
@@ -489,6 +490,27 @@ def conv2d_im2col(x, kernel_shape, *, stride=(1, 1), padding=(0, 0)):
     cols = torch.empty((g.m, g.k), dtype=torch.float32, device=x.device)
     _call("mfh_conv_im2col", x.data_ptr(), cols.data_ptr(), *g.c_args(), _stream())
     return cols
+
+
+def conv2d_col2im(grad_cols, x_shape, kernel_shape, *, stride=(1, 1), padding=(0, 0), per_image=True, out=None,
+                  accumulate=False):
+    """dx of shape x_shape from a feature-major column gradient (mfh_conv_col2im): grad_cols holds
+    [n][CI*KH*KW][OH*OW] when per_image, else [CI*KH*KW][N*OH*OW]. With out and accumulate, the sums
+    are added to out."""
+    grad_cols = _device_f32(grad_cols, "grad_cols")
+    g = ConvGeometry.of(tuple(x_shape), tuple(kernel_shape), stride, padding)
+    if grad_cols.numel() != g.m * g.k:
+        raise ValueError("grad_cols must hold N*OH*OW*CI*KH*KW floats")
+    if out is None:
+        if accumulate:
+            raise ValueError("accumulate needs out")
+        out = torch.empty(tuple(x_shape), dtype=torch.float32, device=grad_cols.device)
+    elif not (isinstance(out, torch.Tensor) and out.dtype == torch.float32 and out.is_contiguous()
+              and tuple(out.shape) == tuple(x_shape) and out.device == grad_cols.device):
+        raise ValueError("out must be a contiguous float32 tensor of x's shape on grad_cols' device")
+    _call("mfh_conv_col2im", grad_cols.data_ptr(), out.data_ptr(), *g.c_args(), int(bool(per_image)),
+          int(bool(accumulate)), _stream())
+    return out
 
 
 def default_conv_algorithm():

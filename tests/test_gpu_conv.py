@@ -221,6 +221,18 @@ def test_im2col_and_col2im_are_bit_exact(shape, kernel, stride, padding):
                                           need_bias_grad=need_w, need_weight_grad=need_w, activation=activation,
                                           output=ones)
         np.testing.assert_array_equal(host(dx), expected)
+    # The col2im entry point alone, on both feature-major layouts, written fresh and added.
+    n, k = shape[0], grad_cols.shape[1]
+    pixel_major = grad_cols.astype(np.float32).reshape(n, oh * ow, k)
+    layouts = {True: pixel_major.transpose(0, 2, 1), False: pixel_major.transpose(2, 0, 1)}
+    for per_image, gct in layouts.items():
+        dx = native.conv2d_col2im(gpu(gct), shape, w_shape, stride=stride, padding=padding, per_image=per_image)
+        np.testing.assert_array_equal(host(dx), expected, err_msg=f"per_image={per_image}")
+        base = rng.integers(-2, 3, size=shape).astype(np.float32)
+        out = gpu(base)
+        native.conv2d_col2im(gpu(gct), shape, w_shape, stride=stride, padding=padding, per_image=per_image, out=out,
+                             accumulate=True)
+        np.testing.assert_array_equal(host(out), base + expected, err_msg=f"per_image={per_image} accumulate")
 
 
 def test_native_errors_name_the_reason():
