@@ -237,6 +237,12 @@ struct ConvGather {
     int chunked;
     FastDiv div_ohw, div_ow, div_khkw, div_kw;
     long long src_floats;  // N * C * H * W: the extent of src that the buffer loads may read
+    // Natural feature order only: when non-null, src with PH / PW zero rows / columns on each side
+    // ((H + 2 PH) x (W + 2 PW) planes of pw columns, phw floats each, padded_floats in all), which the
+    // products read without window bounds tests.
+    const float* padded;
+    int pw, phw;
+    long long padded_floats;
 };
 // The chunked implicit products read their operands with buffer loads, whose byte offsets are 32-bit:
 // each operand tensor they read must hold at most this many floats.

@@ -88,6 +88,57 @@ struct GatherFeatureRows {
     }
 };
 
+// Most features a natural-order product may have to read its padded source (the LDS table of their
+// offsets below).
+constexpr int PADDED_TABLE_MAX = 1024;
+
+// The natural-order tile read from the zero-padded copy of the source (ConvGather::padded) and stored
+// pixel-major like GatherChunkRows' ([BN][BK + 4]): thread t takes pixel n0 + t % BN and the PER
+// consecutive features (t / BN) * PER + i of the stage. The byte offset of every feature inside an
+// image's padded planes is read from a table in LDS (two 16-byte reads per stage, the same address
+// for a whole wave), so a load costs one add, with no window bounds test and no division. A feature
+// past the last (table entry BUFFER_OOB), or a pixel past the last, reads zero; both at once read
+// the tensor's first element, which only reaches an output column past the last pixel, never
+// stored.
+template <int BN, int THREADS>
+struct GatherPaddedRows {
+    static_assert(BN % 64 == 0 && THREADS % BN == 0, "each wave must read features of a single row group");
+    static constexpr int RSTEP = THREADS / BN, PER = BK / RSTEP;
+    static_assert(BK % RSTEP == 0 && PER % 4 == 0, "runs of whole float4s per thread");
+    __amdgpu_buffer_rsrc_t rsrc;
+    unsigned lane;  // byte offset of this thread's window origin in the padded source
+    float v[PER];
+
+    __device__ __forceinline__ void init(const ConvGather& g, int n0, int tid) {
+        rsrc = buffer_of(g.padded, g.padded_floats);
+        const int q = n0 + tid % BN;
+        int rem, ow;
+        const int n = g.div_ohw.divmod(q < g.pixels ? q : 0, rem);
+        const int oh = g.div_ow.divmod(rem, ow);
+        lane = q < g.pixels ? static_cast<unsigned>(n * g.C * g.phw + oh * g.SH * g.pw + ow * g.SW) * 4u : BUFFER_OOB;
+    }
+
+    __device__ __forceinline__ void load(const unsigned* table, int kt, int tid) {
+        const unsigned* at = table + kt + (tid / BN) * PER;
+#pragma unroll
+        for (int q = 0; q < PER / 4; ++q) {
+            const uint4 o = *reinterpret_cast<const uint4*>(at + 4 * q);
+            v[4 * q] = buffer_load(rsrc, lane + o.x, 0);
+            v[4 * q + 1] = buffer_load(rsrc, lane + o.y, 0);
+            v[4 * q + 2] = buffer_load(rsrc, lane + o.z, 0);
+            v[4 * q + 3] = buffer_load(rsrc, lane + o.w, 0);
+        }
+    }
+
+    template <int LD>
+    __device__ __forceinline__ void store(float* lds, int tid) const {
+        float* row = lds + (tid % BN) * LD + (tid / BN) * PER;
+#pragma unroll
+        for (int q = 0; q < PER / 4; ++q)
+            *reinterpret_cast<float4*>(row + 4 * q) = make_float4(v[4 * q], v[4 * q + 1], v[4 * q + 2], v[4 * q + 3]);
+    }
+};
+
 // The same tile in chunked feature order: stage kt covers channels [c0, c0 + 32) at one tap. The
 // tap is uniform over the stage, so a wave may span two rows (BN a multiple of 32). The loads are
 // buffer loads: a lane's offset is its pixel's window origin plus the stage's (uniform) channel
@@ -154,6 +205,17 @@ __device__ __forceinline__ void feature_of(const ConvGather& g, int k, int& c, i
         c = g.div_khkw.divmod(k, tap);
     }
     kh = g.div_kw.divmod(tap, kw);
+}
+
+// Fills the LDS table of GatherPaddedRows: entry k < K is the byte offset of feature k = (c, kh, kw)
+// inside an image's padded planes, entries K .. features_padded - 1 are BUFFER_OOB.
+template <int THREADS>
+__device__ __forceinline__ void fill_padded_table(unsigned* table, const ConvGather& g, int features_padded, int tid) {
+    for (int k = tid; k < features_padded; k += THREADS) {
+        int c = 0, kh = 0, kw = 0;
+        if (k < g.features) feature_of(g, k, c, kh, kw);
+        table[k] = k < g.features ? static_cast<unsigned>(c * g.phw + kh * g.pw + kw) * 4u : BUFFER_OOB;
+    }
 }
 
 // The decomposition of one output pixel q (dW orientation: thread t handles pixel kt + t % BK_WG).
@@ -274,11 +336,13 @@ struct GradRowsInPlace {
 // One BM x BN tile (tile_m, tile_n) of Y (M x pixels) = A (M x K, row-major, lda) . view (K x
 // pixels), K slice z. Split-K writes dense partials (z-th slice at C + z * c_batch); otherwise the
 // epilogue of p (segmented NCHW, bias, activation).
-template <int BM, int BN, int WM, int WN, bool VA, bool CHUNKED>
+template <int BM, int BN, int WM, int WN, bool VA, bool CHUNKED, bool PADDED = false>
 __device__ __forceinline__ void implicit_forward_tile(const GemmParams& p, const ConvGather& g, int tile_m, int tile_n,
                                                       int z) {
-    // The chunked gather stores its tile pixel-major (TB), the natural-order one feature-major.
-    using S = MfmaShape<BM, BN, BK, WM, WN, false, CHUNKED>;
+    // The chunked and padded gathers store their tile pixel-major (TB), the natural-order one
+    // feature-major.
+    constexpr bool AHEAD = CHUNKED || PADDED;
+    using S = MfmaShape<BM, BN, BK, WM, WN, false, AHEAD>;
     __shared__ __attribute__((aligned(16))) float smem[2 * S::STAGE];
     const int tid = threadIdx.x, wave = tid / 64, lane = tid % 64;
     const int wm0 = (wave / S::WGN) * WM, wn0 = (wave % S::WGN) * WN;
@@ -288,15 +352,23 @@ __device__ __forceinline__ void implicit_forward_tile(const GemmParams& p, const
     float* __restrict__ C = p.C + (p.split ? z * p.c_batch : 0);
 
     // Chunked products (K a multiple of BK) read the kernel order with buffer loads too, two stages
-    // ahead (two register slots of loaders).
-    using LoadA = std::conditional_t<CHUNKED, BufferRowTile<BM, BK, S::THREADS>, TileLoader<BM, BK, S::THREADS, VA>>;
-    using LoadB = std::conditional_t<CHUNKED, GatherChunkRows<BN, S::THREADS>, GatherFeatureRows<BN, S::THREADS>>;
-    LoadA la[CHUNKED ? 2 : 1];
-    LoadB lb[CHUNKED ? 2 : 1];
+    // ahead (two register slots of loaders); so do padded natural-order products, whose kernel is
+    // a copy with its rows padded to whole stages (lda a multiple of BK, zeros past K).
+    using LoadA = std::conditional_t<AHEAD, BufferRowTile<BM, BK, S::THREADS>, TileLoader<BM, BK, S::THREADS, VA>>;
+    using LoadB = std::conditional_t<CHUNKED, GatherChunkRows<BN, S::THREADS>,
+                                     std::conditional_t<PADDED, GatherPaddedRows<BN, S::THREADS>,
+                                                        GatherFeatureRows<BN, S::THREADS>>>;
+    LoadA la[AHEAD ? 2 : 1];
+    LoadB lb[AHEAD ? 2 : 1];
 #pragma unroll
-    for (int i = 0; i < (CHUNKED ? 2 : 1); ++i) {
-        if constexpr (CHUNKED) la[i].init(p.A, p.lda, p.M, m0, tid);
+    for (int i = 0; i < (AHEAD ? 2 : 1); ++i) {
+        if constexpr (AHEAD) la[i].init(p.A, p.lda, p.M, m0, tid);
         lb[i].init(g, n0, tid);
+    }
+    __shared__ unsigned table[PADDED ? PADDED_TABLE_MAX : 1];
+    if constexpr (PADDED) {
+        fill_padded_table<S::THREADS>(table, g, p.lda, tid);
+        __syncthreads();
     }
     v16f acc[S::TM][S::TN];
     zero_acc<S>(acc);
@@ -305,10 +377,11 @@ __device__ __forceinline__ void implicit_forward_tile(const GemmParams& p, const
     // below one 576-4608-term chain (below the NumPy float32 path's) for 2 % of their time; FP64
     // totals were 3x more accurate still but cost 7 % (registers: one workgroup less per CU).
     StageSums<S, float> sums;
-    if constexpr (CHUNKED) {
+    if constexpr (AHEAD) {
         auto fetch = [&](auto slot, int kt) {
             la[decltype(slot)::value].load(kt);
-            lb[decltype(slot)::value].load(g, kt, k_end, tid);
+            if constexpr (CHUNKED) lb[decltype(slot)::value].load(g, kt, k_end, tid);
+            else lb[decltype(slot)::value].load(table, kt, tid);
         };
         auto store = [&](auto slot, float* a_lds, float* b_lds) {
             la[decltype(slot)::value].template store<S::LDA_S>(a_lds, tid);
@@ -330,12 +403,12 @@ __device__ __forceinline__ void implicit_forward_tile(const GemmParams& p, const
     store_acc<S>(p, C, acc, m0, n0, wm0, wn0, lane);
 }
 
-template <int BM, int BN, int WM, int WN, bool VA, bool CHUNKED>
+template <int BM, int BN, int WM, int WN, bool VA, bool CHUNKED, bool PADDED>
 __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void conv_implicit_forward_kernel(GemmParams p,
                                                                                           ConvGather g) {
     int tile_m, tile_n, z;
     tile_of_workgroup(tile_m, tile_n, z);
-    implicit_forward_tile<BM, BN, WM, WN, VA, CHUNKED>(p, g, tile_m, tile_n, z);
+    implicit_forward_tile<BM, BN, WM, WN, VA, CHUNKED, PADDED>(p, g, tile_m, tile_n, z);
 }
 
 // Several implicit products of one tile shape in one launch (the phases of a strided dX): product
@@ -440,10 +513,74 @@ struct WgradChunkStage {
     }
 };
 
+// Both operand loads of one dW stage in natural feature order from the zero-padded source
+// (ConvGather::padded): dy's rows as in WgradChunkStage, and the thread's feature rows r, r + R, ...
+// at one byte offset each into an image's padded planes, so a load costs one add and no window
+// bounds test. A feature row past the last, or a pixel past the range, reads zero (an offset beyond
+// the extent); both at once read the tensor's first element, which only reaches an output column
+// past the last feature, never stored.
+template <int BM, int BN, int THREADS>
+struct WgradPaddedStage {
+    static constexpr int R = THREADS / BK_WG, A_PER = BM / R, B_PER = BN / R;
+    static_assert(BM % R == 0 && BN % R == 0, "a pixel column's threads split the rows evenly");
+    __amdgpu_buffer_rsrc_t dy_rsrc, x_rsrc;
+    int lo, a_row, b_row0;
+    unsigned b_offset[B_PER];
+    float a[A_PER], b[B_PER];
+
+    __device__ __forceinline__ void init(const ConvGather& g, const float* dy, int CO, int m0, int n0, int tid) {
+        dy_rsrc = buffer_of(dy, static_cast<long long>(g.pixels) * CO);
+        x_rsrc = buffer_of(g.padded, g.padded_floats);
+        lo = tid % BK_WG;
+        const int r = tid / BK_WG;
+        a_row = m0 + r;
+        b_row0 = r;
+#pragma unroll
+        for (int i = 0; i < B_PER; ++i) {
+            const int k = n0 + r + i * R;
+            int c = 0, kh = 0, kw = 0;
+            if (k < g.features) feature_of(g, k, c, kh, kw);
+            b_offset[i] = k < g.features ? static_cast<unsigned>(c * g.phw + kh * g.pw + kw) * 4u : BUFFER_OOB;
+        }
+    }
+
+    __device__ __forceinline__ void load(const ConvGather& g, int CO, int kt, int k_end) {
+        const int ohw = g.OH * g.OW;
+        const int q = kt + lo;
+        const bool valid = q < k_end;
+        int pix, ow;
+        const int n = g.div_ohw.divmod(valid ? q : 0, pix);
+        const int oh = g.div_ow.divmod(pix, ow);
+        const unsigned a_at = static_cast<unsigned>((n * CO + a_row) * ohw + pix) * 4u;
+        const unsigned b_at = static_cast<unsigned>(n * g.C * g.phw + oh * g.SH * g.pw + ow * g.SW) * 4u;
+        const unsigned a_lane = valid ? a_at : BUFFER_OOB;
+        const unsigned b_lane = valid ? b_at : BUFFER_OOB;
+        const int a_step = R * ohw * 4;
+#pragma unroll
+        for (int i = 0; i < A_PER; ++i) a[i] = buffer_load(dy_rsrc, a_lane, i * a_step);
+#pragma unroll
+        for (int i = 0; i < B_PER; ++i) b[i] = buffer_load(x_rsrc, b_lane + b_offset[i], 0);
+    }
+
+    template <int LDA, int LDB>
+    __device__ __forceinline__ void store(float* a_lds, float* b_lds, int tid) const {
+        const int r = tid / BK_WG;
+#pragma unroll
+        for (int i = 0; i < A_PER; ++i) a_lds[(r + i * R) * LDA + lo] = a[i];
+#pragma unroll
+        for (int i = 0; i < B_PER; ++i) b_lds[(b_row0 + i * R) * LDB + lo] = b[i];
+    }
+
+    __device__ __forceinline__ void add_to(double (&sums)[A_PER]) const {
+#pragma unroll
+        for (int i = 0; i < A_PER; ++i) sums[i] += static_cast<double>(a[i]);
+    }
+};
+
 // dW (CO x K) = dy (CO x pixels) . view^T (pixels x K), the pixel range split over z when p.split.
 // SUMS: the workgroups of feature tile 0 also sum each dy row over their pixel range in FP64, the
 // conv bias gradient: db[co] directly when unsplit, else sums[z * CO + co] for the reduction.
-template <int BM, int BN, int WM, int WN, bool SUMS, bool CHUNKED>
+template <int BM, int BN, int WM, int WN, bool SUMS, bool CHUNKED, bool PADDED>
 __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void conv_implicit_wgrad_kernel(GemmParams p, ConvGather g,
                                                                                         double* sums, float* db) {
     using S = MfmaShape<BM, BN, BK_WG, WM, WN, false, true>;
@@ -465,10 +602,10 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void conv_implicit_wgra
     for (int i = 0; i < RowLoader::PER; ++i) row_sums[i] = 0.0;
     const bool summing = SUMS && tile_n == 0;
 
-    if constexpr (CHUNKED) {
+    if constexpr (CHUNKED || PADDED) {
         // Two register slots of loads, two stages ahead; the row sums as a separate loop body, so
         // that the other feature tiles' stages carry no FP64 work.
-        using Stage = WgradChunkStage<BM, BN, S::THREADS>;
+        using Stage = std::conditional_t<CHUNKED, WgradChunkStage<BM, BN, S::THREADS>, WgradPaddedStage<BM, BN, S::THREADS>>;
         static_assert(Stage::A_PER == RowLoader::PER, "the row sums follow the A rows");
         Stage st[2];
 #pragma unroll
@@ -653,6 +790,34 @@ __global__ __launch_bounds__(256) void row_sums_kernel(const float* __restrict__
     if (lane == 0) partial[row] = s;
 }
 
+// dst (planes x (H + 2 PH) x (W + 2 PW)) = src (planes x H x W) with PH zero rows and PW zero
+// columns on each side; one thread per element of dst.
+// The padded operands of a natural-order product, one launch: elements [0, planes_total) are the
+// source planes with PH / PW zero rows / columns on each side ((H + 2 PH) x (W + 2 PW), pw columns),
+// the next kernel_total the forward kernel's rows (K floats of w) padded with zeros to kp columns.
+__global__ __launch_bounds__(256) void pad_operands_kernel(const float* __restrict__ src, float* __restrict__ dst,
+                                                           int planes_total, FastDiv div_pw, FastDiv div_ph, int H,
+                                                           int W, int PH, int PW, const float* __restrict__ w,
+                                                           float* __restrict__ w_dst, int kernel_total, FastDiv div_kp,
+                                                           int K) {
+    int i = blockIdx.x * 256 + threadIdx.x;
+    if (i < planes_total) {
+        int col, row;
+        const int t = div_pw.divmod(i, col);
+        const int plane = div_ph.divmod(t, row);
+        const int h = row - PH, x = col - PW;
+        dst[i] = static_cast<unsigned>(h) < static_cast<unsigned>(H) && static_cast<unsigned>(x) < static_cast<unsigned>(W)
+                     ? src[static_cast<long long>(plane) * H * W + h * W + x]
+                     : 0.0f;
+        return;
+    }
+    i -= planes_total;
+    if (i >= kernel_total) return;
+    int col;
+    const int row = div_kp.divmod(i, col);
+    w_dst[i] = col < K ? w[static_cast<long long>(row) * K + col] : 0.0f;
+}
+
 using ConvFn = void (*)(GemmParams, ConvGather);
 
 // Tile catalogue of the implicit products: block tile BM x BN, wave tile WM x WN. The 64 x 64 wave
@@ -686,32 +851,35 @@ constexpr bool has_wgrad(const ImplicitTile& t) {
     return t.bn % 64 == 0 && t.bm % (threads_of(t) / BK_WG) == 0 && t.bn % (threads_of(t) / BK_WG) == 0;
 }
 
-template <int T, bool VA, bool CHUNKED>
+template <int T, bool VA, bool CHUNKED, bool PADDED = false>
 constexpr ConvFn forward_of() {
     constexpr ImplicitTile t = TILE_TABLE[T];
-    return conv_implicit_forward_kernel<t.bm, t.bn, t.wm, t.wn, VA, CHUNKED>;
+    return conv_implicit_forward_kernel<t.bm, t.bn, t.wm, t.wn, VA, CHUNKED, PADDED>;
 }
 
 using WgradFn = void (*)(GemmParams, ConvGather, double*, float*);
 using GroupedFn = void (*)(GroupedProducts);
 
-template <int T, bool SUMS, bool CHUNKED>
+template <int T, bool SUMS, bool CHUNKED, bool PADDED = false>
 constexpr WgradFn wgrad_of() {
     constexpr ImplicitTile t = TILE_TABLE[T];
-    return conv_implicit_wgrad_kernel<t.bm, t.bn, t.wm, t.wn, SUMS, CHUNKED>;
+    return conv_implicit_wgrad_kernel<t.bm, t.bn, t.wm, t.wn, SUMS, CHUNKED, PADDED>;
 }
 
-// forward[tile][0 | 1 | 2]: natural feature order with scalar / float4 A loads, chunked order;
-// wgrad[tile][0 | 1][0 | 1]: without / with the FP64 row sums of dy; natural / chunked feature order.
+// forward[tile][0 | 1 | 2 | 3]: natural feature order with scalar / float4 A loads, chunked order,
+// natural order from the padded operands;
+// wgrad[tile][0 | 1][0 | 1 | 2]: without / with the FP64 row sums of dy; natural / chunked feature
+// order / natural order from the padded source.
 struct ConvKernels {
-    ConvFn forward[TILE_COUNT][3] = {};
-    WgradFn wgrad[TILE_COUNT][2][2] = {};
+    ConvFn forward[TILE_COUNT][4] = {};
+    WgradFn wgrad[TILE_COUNT][2][3] = {};
     GroupedFn grouped[TILE_COUNT] = {};  // chunked products only, tile 6 (the strided dX phases)
     template <int T>
     void fill() {
         if constexpr (has_natural(TILE_TABLE[T])) {
             forward[T][0] = forward_of<T, false, false>();
             forward[T][1] = forward_of<T, true, false>();
+            forward[T][3] = forward_of<T, true, false, true>();
         }
         forward[T][2] = forward_of<T, true, true>();
         if constexpr (has_wgrad(TILE_TABLE[T])) {
@@ -719,6 +887,8 @@ struct ConvKernels {
             wgrad[T][1][0] = wgrad_of<T, true, false>();
             wgrad[T][0][1] = wgrad_of<T, false, true>();
             wgrad[T][1][1] = wgrad_of<T, true, true>();
+            wgrad[T][0][2] = wgrad_of<T, false, false, true>();
+            wgrad[T][1][2] = wgrad_of<T, true, false, true>();
         }
     }
     ConvKernels() {
@@ -971,6 +1141,69 @@ bool buffer_extents_fit(const ConvGather& g, int M, int lda) {
     return g.src_floats <= BUFFER_LIMIT_FLOATS && static_cast<std::int64_t>(M) * lda <= BUFFER_LIMIT_FLOATS;
 }
 
+// Where a natural-order product's padded operands live in its workspace, past the split-K partials:
+// the zero-padded source copy ((H + 2 PH) x (W + 2 PW) planes; none for an unpadded source, read in
+// place) and, for a forward product, the kernel's rows padded with zeros to whole stages. `usable`
+// is false where the product keeps the bounds-tested gather: chunked sources, operands past the
+// buffer loads' extent, forward products with more features than the offset table holds.
+struct PaddedLayout {
+    bool usable = false;
+    std::int64_t source_at = 0, source_floats = 0, kernel_at = 0, kernel_floats = 0, total = 0;
+    int kp = 0;
+};
+
+std::int64_t aligned64(std::int64_t floats) { return (floats + 63) / 64 * 64; }
+
+PaddedLayout padded_layout(const ConvGather& g, int images, std::int64_t partial_floats, bool forward, int M) {
+    PaddedLayout l;
+    l.total = partial_floats;
+    const std::int64_t all = static_cast<std::int64_t>(images) * g.C * (g.H + 2 * g.PH) * (g.W + 2 * g.PW);
+    l.kp = (g.features + BK - 1) / BK * BK;
+    if (g.chunked || all > BUFFER_LIMIT_FLOATS) return l;
+    if (forward && (l.kp > PADDED_TABLE_MAX || static_cast<std::int64_t>(M) * l.kp > BUFFER_LIMIT_FLOATS)) return l;
+    l.usable = true;
+    l.source_at = aligned64(partial_floats);
+    l.source_floats = g.PH || g.PW ? all : 0;
+    l.kernel_at = aligned64(l.source_at + l.source_floats);
+    l.kernel_floats = forward ? static_cast<std::int64_t>(M) * l.kp : 0;
+    l.total = l.kernel_at + l.kernel_floats;
+    return l;
+}
+
+// Sets up a natural-order product to read padded operands without window bounds tests
+// (ConvGather::padded): the source itself when it has no padding, else a zero-padded copy made here
+// in the workspace; a forward product also gets its kernel with rows padded to whole stages
+// (*kernel, *kp columns). Where the layout is not usable or the workspace cannot hold it, the gather
+// keeps its bounds tests (g.padded stays null).
+int pad_operands(ConvGather& g, int images, const GemmPlan& plan, int M, int N, float* workspace,
+                 std::int64_t workspace_floats, hipStream_t stream, const float** kernel = nullptr, int* kp = nullptr) {
+    const bool forward = kernel != nullptr;
+    const PaddedLayout l =
+        padded_layout(g, images, plan.slices > 1 ? gemm_workspace_floats(plan, M, N) : 0, forward, M);
+    if (!l.usable || (l.total > 0 && (!workspace || workspace_floats < l.total))) return OK;
+    const int ph = g.H + 2 * g.PH, pw = g.W + 2 * g.PW;
+    float* source = l.source_floats ? workspace + l.source_at : nullptr;
+    float* kernel_copy = forward ? workspace + l.kernel_at : nullptr;
+    if (forward && !aligned16(kernel_copy)) return OK;  // the padded kernel is read with 16-byte loads
+    const std::int64_t work = l.source_floats + l.kernel_floats;
+    if (work > 0) {
+        launch(pad_operands_kernel, blocks_for(work, 256), 256, 0, stream, g.src, source,
+               static_cast<int>(l.source_floats), FastDiv(pw), FastDiv(ph), g.H, g.W, g.PH, g.PW,
+               forward ? *kernel : nullptr, kernel_copy, static_cast<int>(l.kernel_floats), FastDiv(l.kp),
+               g.features);
+        MFH_TRY(MFH_CHECK_LAUNCH("pad_operands", stream));
+    }
+    g.padded = source ? source : g.src;
+    g.pw = pw;
+    g.phw = ph * pw;
+    g.padded_floats = static_cast<long long>(images) * g.C * ph * pw;
+    if (forward) {
+        *kernel = kernel_copy;
+        *kp = l.kp;
+    }
+    return OK;
+}
+
 // Runs one implicit product with the epilogue e (directly, or through split-K partials and the
 // FP64 slice reduction).
 int run_implicit(bool wgrad, const GemmPlan& plan, const float* a, int lda, int M, int N, int K, const ConvGather& g,
@@ -996,14 +1229,16 @@ int run_implicit(bool wgrad, const GemmPlan& plan, const float* a, int lda, int 
     const dim3 grid(blocks_for(N, t.bn), blocks_for(M, t.bm), static_cast<unsigned>(plan.slices));
     const dim3 block(threads_of(t));
     const bool vec_a = K % 4 == 0 && lda % 4 == 0 && aligned16(a);
-    const int variant = g.chunked ? 2 : vec_a ? 1 : 0;
-    if (!wgrad && g.chunked && !vec_a) return MFH_FAIL(ERR_ARG, "the reordered kernel buffer must be 16-byte aligned");
+    const int variant = g.chunked ? 2 : g.padded ? 3 : vec_a ? 1 : 0;
+    const int order = g.chunked ? 1 : g.padded ? 2 : 0;
+    if (!wgrad && (g.chunked || g.padded) && !vec_a)
+        return MFH_FAIL(ERR_ARG, "the reordered kernel buffer must be 16-byte aligned");
     if (g.chunked && (wgrad ? g.src_floats > BUFFER_LIMIT_FLOATS || static_cast<std::int64_t>(g.pixels) * M >
                                                                        BUFFER_LIMIT_FLOATS
                             : !buffer_extents_fit(g, M, lda)))
         return MFH_FAIL(ERR_ARG, "a chunked implicit convolution reads tensors of at most 2 GiB");
     if (wgrad)
-        launch(conv_kernels().wgrad[plan.tile][row_out ? 1 : 0][g.chunked ? 1 : 0], grid, block, 0, stream,
+        launch(conv_kernels().wgrad[plan.tile][row_out ? 1 : 0][order], grid, block, 0, stream,
                            p, g, row_sums,
                            row_out);
     else
@@ -1044,9 +1279,14 @@ std::int64_t implicit_workspace_floats(const ConvGeometry& g, int pass) {
     if (pass == IMPLICIT_FORWARD) plan = implicit_auto_plan(false, g.CO, g.rows(), g.features(), implicit_chunked(g.CI));
     else if (pass == IMPLICIT_WGRAD) plan = implicit_auto_plan(true, g.CO, g.features(), g.rows(), implicit_chunked(g.CI));
     else plan = implicit_auto_plan(false, g.CI, g.N * g.H * g.W, g.CO * g.KH * g.KW, implicit_chunked(g.CO));
-    return pass == IMPLICIT_WGRAD ? gemm_workspace_floats(plan, g.CO, g.features())
-                                  : gemm_workspace_floats(plan, pass == IMPLICIT_FORWARD ? g.CO : g.CI,
-                                                          pass == IMPLICIT_FORWARD ? g.rows() : g.N * g.H * g.W);
+    const std::int64_t partials = pass == IMPLICIT_WGRAD
+                                      ? gemm_workspace_floats(plan, g.CO, g.features())
+                                      : gemm_workspace_floats(plan, pass == IMPLICIT_FORWARD ? g.CO : g.CI,
+                                                              pass == IMPLICIT_FORWARD ? g.rows() : g.N * g.H * g.W);
+    if (pass == IMPLICIT_DGRAD) return partials;
+    // The forward and dW products of a natural-order convolution also hold its padded operands.
+    const ConvGather gather = gather_of(nullptr, g.CI, g.H, g.W, g.KH, g.KW, g.SH, g.SW, g.PH, g.PW, g.N, g.OH, g.OW);
+    return padded_layout(gather, g.N, partials, pass == IMPLICIT_FORWARD, g.CO).total;
 }
 
 // The jobs of one order: one, or one per non-empty phase of a strided dX (sub-kernels back to back).
@@ -1127,7 +1367,7 @@ int conv_implicit_forward(const ConvGeometry& g, const float* x, const float* w,
     const int M = g.CO, N = g.rows(), K = g.features();
     GemmPlan plan;
     MFH_TRY(implicit_plan(false, implicit_chunked(g.CI), engine, M, N, K, workspace, workspace_floats, &plan));
-    const ConvGather gather = gather_of(x, g.CI, g.H, g.W, g.KH, g.KW, g.SH, g.SW, g.PH, g.PW, g.N, g.OH, g.OW);
+    ConvGather gather = gather_of(x, g.CI, g.H, g.W, g.KH, g.KW, g.SH, g.SW, g.PH, g.PW, g.N, g.OH, g.OW);
     if (gather.chunked) {
         if (!prepared) {
             const WeightOrder order{w, wt, g.CO, g.CI, g.KH, g.KW, 0};
@@ -1135,6 +1375,8 @@ int conv_implicit_forward(const ConvGeometry& g, const float* x, const float* w,
         }
         w = wt;
     }
+    int lda = K;
+    if (!gather.chunked) MFH_TRY(pad_operands(gather, g.N, plan, M, N, workspace, workspace_floats, stream, &w, &lda));
     GemmEpilogue e;
     e.bias = bias;
     e.bias_mode = bias ? BIAS_ROW : BIAS_NONE;
@@ -1148,7 +1390,9 @@ int conv_implicit_forward(const ConvGeometry& g, const float* x, const float* w,
     // here).
     const bool defer = deferred && plan.slices > 1 && !residual && act == ACT_NONE;
     if (deferred) *deferred = defer ? plan.slices : 1;
-    return run_implicit(false, plan, w, K, M, N, K, gather, y, g.ohw(), e, workspace, stream, nullptr, nullptr, defer);
+    // A padded product runs over the padded kernel's whole stages (features past K read zeros).
+    return run_implicit(false, plan, w, lda, M, N, gather.padded ? lda : K, gather, y, g.ohw(), e, workspace, stream,
+                        nullptr, nullptr, defer);
 }
 
 int conv_implicit_wgrad(const ConvGeometry& g, const float* x, const float* dy, float* dw, double* bias_partial,
@@ -1158,7 +1402,8 @@ int conv_implicit_wgrad(const ConvGeometry& g, const float* x, const float* dy, 
     MFH_TRY(implicit_plan(true, implicit_chunked(g.CI), engine, M, N, K, workspace, workspace_floats, &plan));
     if (db && (!bias_partial || plan.slices > WGRAD_MAX_SLICES))
         return MFH_FAIL(ERR_ARG, "the dW plan's bias partials need bias_partial rows for every pixel slice");
-    const ConvGather gather = gather_of(x, g.CI, g.H, g.W, g.KH, g.KW, g.SH, g.SW, g.PH, g.PW, g.N, g.OH, g.OW);
+    ConvGather gather = gather_of(x, g.CI, g.H, g.W, g.KH, g.KW, g.SH, g.SW, g.PH, g.PW, g.N, g.OH, g.OW);
+    MFH_TRY(pad_operands(gather, g.N, plan, M, N, workspace, workspace_floats, stream));
     GemmEpilogue e;
     if (gather.chunked) e.taps = g.KH * g.KW;
     return run_implicit(true, plan, dy, g.ohw(), M, N, K, gather, dw, N, e, workspace, stream, bias_partial, db);
