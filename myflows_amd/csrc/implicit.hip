@@ -378,10 +378,14 @@ __device__ __forceinline__ void implicit_forward_tile(const GemmParams& p, const
     // totals were 3x more accurate still but cost 7 % (registers: one workgroup less per CU).
     StageSums<S, float> sums;
     if constexpr (AHEAD) {
+        // The loop also fetches the two stages past the last (into slots no MFMA reads): the kernel
+        // operand then re-reads the last stage, since its column offset is a scalar offset, which
+        // the buffer range check does not cover (and the padded gather's table ends there).
+        const int k_last = max(k_begin, k_end - BK);
         auto fetch = [&](auto slot, int kt) {
-            la[decltype(slot)::value].load(kt);
+            la[decltype(slot)::value].load(min(kt, k_last));
             if constexpr (CHUNKED) lb[decltype(slot)::value].load(g, kt, k_end, tid);
-            else lb[decltype(slot)::value].load(table, kt, tid);
+            else lb[decltype(slot)::value].load(table, min(kt, k_last), tid);
         };
         auto store = [&](auto slot, float* a_lds, float* b_lds) {
             la[decltype(slot)::value].template store<S::LDA_S>(a_lds, tid);
@@ -442,9 +446,8 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void conv_implicit_grou
 // lane's offsets into dy and x are 32-bit and the row / channel steps wave-uniform (scalar
 // offsets), so a stage's loads need no 64-bit address arithmetic and no branches. A lane past the
 // pixel range, or whose window tap falls outside the image, reads zero.
-// Rows of A past CO read whatever lies there (rows of the next image, or zero past the tensor):
-// they only reach output rows past CO, which are never stored.
-template <int BM, int BN, int THREADS>
+// Rows of A past CO (the last row tile) read zero.
+template <int BM, int BN, int THREADS, bool CHECK_ROWS>
 struct WgradChunkStage {
     static constexpr int R = THREADS / BK_WG, A_PER = BM / R;
     static constexpr int G = BN / 32, SPAN = R / G, B_PER = 32 / SPAN;
@@ -491,10 +494,24 @@ struct WgradChunkStage {
         const unsigned a_lane = valid ? a_at : BUFFER_OOB;
         const unsigned b_lane = ok ? b_at : BUFFER_OOB;
         const int a_step = R * ohw * 4, b_step = SPAN * g.hw * 4;
-#pragma unroll
-        for (int i = 0; i < A_PER; ++i) a[i] = buffer_load(dy_rsrc, a_lane, i * a_step);
+        load_rows(CO, a_lane, a_step);
 #pragma unroll
         for (int i = 0; i < B_PER; ++i) b[i] = buffer_load(x_rsrc, b_lane, i * b_step);
+    }
+
+    // dy's rows a_row + i R at this lane's pixel (lane offset a_lane of row a_row). The row steps
+    // are scalar offsets, which the buffer range check does not cover; CHECK_ROWS (the last row
+    // tile of an output whose rows end inside it) adds them to the lane offset instead, and its
+    // rows past CO read zero.
+    __device__ __forceinline__ void load_rows(int CO, unsigned a_lane, int a_step) {
+        if constexpr (CHECK_ROWS) {
+#pragma unroll
+            for (int i = 0; i < A_PER; ++i)
+                a[i] = buffer_load(dy_rsrc, a_row + i * R < CO ? a_lane + i * a_step : BUFFER_OOB, 0);
+        } else {
+#pragma unroll
+            for (int i = 0; i < A_PER; ++i) a[i] = buffer_load(dy_rsrc, a_lane, i * a_step);
+        }
     }
 
     template <int LDA, int LDB>
@@ -519,7 +536,7 @@ struct WgradChunkStage {
 // bounds test. A feature row past the last, or a pixel past the range, reads zero (an offset beyond
 // the extent); both at once read the tensor's first element, which only reaches an output column
 // past the last feature, never stored.
-template <int BM, int BN, int THREADS>
+template <int BM, int BN, int THREADS, bool CHECK_ROWS>
 struct WgradPaddedStage {
     static constexpr int R = THREADS / BK_WG, A_PER = BM / R, B_PER = BN / R;
     static_assert(BM % R == 0 && BN % R == 0, "a pixel column's threads split the rows evenly");
@@ -556,8 +573,14 @@ struct WgradPaddedStage {
         const unsigned a_lane = valid ? a_at : BUFFER_OOB;
         const unsigned b_lane = valid ? b_at : BUFFER_OOB;
         const int a_step = R * ohw * 4;
+        if constexpr (CHECK_ROWS) {  // dy's rows as in WgradChunkStage::load_rows
 #pragma unroll
-        for (int i = 0; i < A_PER; ++i) a[i] = buffer_load(dy_rsrc, a_lane, i * a_step);
+            for (int i = 0; i < A_PER; ++i)
+                a[i] = buffer_load(dy_rsrc, a_row + i * R < CO ? a_lane + i * a_step : BUFFER_OOB, 0);
+        } else {
+#pragma unroll
+            for (int i = 0; i < A_PER; ++i) a[i] = buffer_load(dy_rsrc, a_lane, i * a_step);
+        }
 #pragma unroll
         for (int i = 0; i < B_PER; ++i) b[i] = buffer_load(x_rsrc, b_lane + b_offset[i], 0);
     }
@@ -605,24 +628,32 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void conv_implicit_wgra
     if constexpr (CHUNKED || PADDED) {
         // Two register slots of loads, two stages ahead; the row sums as a separate loop body, so
         // that the other feature tiles' stages carry no FP64 work.
-        using Stage = std::conditional_t<CHUNKED, WgradChunkStage<BM, BN, S::THREADS>, WgradPaddedStage<BM, BN, S::THREADS>>;
-        static_assert(Stage::A_PER == RowLoader::PER, "the row sums follow the A rows");
-        Stage st[2];
+        auto run = [&](auto check_rows) {
+            constexpr bool CHECK = decltype(check_rows)::value;
+            using Stage = std::conditional_t<CHUNKED, WgradChunkStage<BM, BN, S::THREADS, CHECK>,
+                                             WgradPaddedStage<BM, BN, S::THREADS, CHECK>>;
+            static_assert(Stage::A_PER == RowLoader::PER, "the row sums follow the A rows");
+            Stage st[2];
 #pragma unroll
-        for (int i = 0; i < 2; ++i) st[i].init(g, p.A, p.M, m0, n0, tid);
-        auto fetch = [&](auto slot, int kt) { st[decltype(slot)::value].load(g, p.M, kt, k_end); };
-        if (summing) {
-            auto store = [&](auto slot, float* a_lds, float* b_lds) {
-                st[decltype(slot)::value].template store<S::LDA_S, S::LDB_S>(a_lds, b_lds, tid);
-                st[decltype(slot)::value].add_to(row_sums);
-            };
-            mfma_k_loop_ahead<S, STAGE_MID_STORE>(smem, k_begin, k_end, fetch, store, acc, wm0, wn0, lane);
-        } else {
-            auto store = [&](auto slot, float* a_lds, float* b_lds) {
-                st[decltype(slot)::value].template store<S::LDA_S, S::LDB_S>(a_lds, b_lds, tid);
-            };
-            mfma_k_loop_ahead<S, STAGE_MID_STORE>(smem, k_begin, k_end, fetch, store, acc, wm0, wn0, lane);
-        }
+            for (int i = 0; i < 2; ++i) st[i].init(g, p.A, p.M, m0, n0, tid);
+            auto fetch = [&](auto slot, int kt) { st[decltype(slot)::value].load(g, p.M, kt, k_end); };
+            if (summing) {
+                auto store = [&](auto slot, float* a_lds, float* b_lds) {
+                    st[decltype(slot)::value].template store<S::LDA_S, S::LDB_S>(a_lds, b_lds, tid);
+                    st[decltype(slot)::value].add_to(row_sums);
+                };
+                mfma_k_loop_ahead<S, STAGE_MID_STORE>(smem, k_begin, k_end, fetch, store, acc, wm0, wn0, lane);
+            } else {
+                auto store = [&](auto slot, float* a_lds, float* b_lds) {
+                    st[decltype(slot)::value].template store<S::LDA_S, S::LDB_S>(a_lds, b_lds, tid);
+                };
+                mfma_k_loop_ahead<S, STAGE_MID_STORE>(smem, k_begin, k_end, fetch, store, acc, wm0, wn0, lane);
+            }
+        };
+        // Only the last row tile of an output whose rows end inside it reads dy's rows with
+        // range-checked offsets.
+        if (m0 + BM <= p.M) run(std::false_type{});
+        else run(std::true_type{});
     } else {
         RowLoader la;
         GatherPixelColumns<BN, S::THREADS> lb;
@@ -790,28 +821,46 @@ __global__ __launch_bounds__(256) void row_sums_kernel(const float* __restrict__
     if (lane == 0) partial[row] = s;
 }
 
-// dst (planes x (H + 2 PH) x (W + 2 PW)) = src (planes x H x W) with PH zero rows and PW zero
-// columns on each side; one thread per element of dst.
-// The padded operands of a natural-order product, one launch: elements [0, planes_total) are the
-// source planes with PH / PW zero rows / columns on each side ((H + 2 PH) x (W + 2 PW), pw columns),
-// the next kernel_total the forward kernel's rows (K floats of w) padded with zeros to kp columns.
+// The padded operands of a natural-order product, one launch: the first plane_blocks workgroups
+// write the source planes with PH / PW zero rows / columns on each side ((H + 2 PH) x (W + 2 PW),
+// pw columns; planes_total floats, four consecutive ones per thread, stored as one float4 when all
+// four exist), the others the forward kernel's rows (K floats of w) padded with zeros to kp columns
+// (kernel_total floats, one per thread).
 __global__ __launch_bounds__(256) void pad_operands_kernel(const float* __restrict__ src, float* __restrict__ dst,
-                                                           int planes_total, FastDiv div_pw, FastDiv div_ph, int H,
-                                                           int W, int PH, int PW, const float* __restrict__ w,
-                                                           float* __restrict__ w_dst, int kernel_total, FastDiv div_kp,
-                                                           int K) {
-    int i = blockIdx.x * 256 + threadIdx.x;
-    if (i < planes_total) {
+                                                           int planes_total, int plane_blocks, FastDiv div_pw,
+                                                           FastDiv div_ph, int H, int W, int PH, int PW,
+                                                           const float* __restrict__ w, float* __restrict__ w_dst,
+                                                           int kernel_total, FastDiv div_kp, int K) {
+    if (static_cast<int>(blockIdx.x) < plane_blocks) {
+        const int i0 = (blockIdx.x * 256 + threadIdx.x) * 4;
+        if (i0 >= planes_total) return;
+        const int pw = W + 2 * PW, ph = H + 2 * PH;
         int col, row;
-        const int t = div_pw.divmod(i, col);
-        const int plane = div_ph.divmod(t, row);
-        const int h = row - PH, x = col - PW;
-        dst[i] = static_cast<unsigned>(h) < static_cast<unsigned>(H) && static_cast<unsigned>(x) < static_cast<unsigned>(W)
-                     ? src[static_cast<long long>(plane) * H * W + h * W + x]
-                     : 0.0f;
+        const int t = div_pw.divmod(i0, col);
+        int plane = div_ph.divmod(t, row);
+        float v[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const int h = row - PH, x = col - PW;
+            const bool inside = i0 + u < planes_total && static_cast<unsigned>(h) < static_cast<unsigned>(H) &&
+                                static_cast<unsigned>(x) < static_cast<unsigned>(W);
+            v[u] = inside ? src[static_cast<long long>(plane) * H * W + h * W + x] : 0.0f;
+            if (++col == pw) {
+                col = 0;
+                if (++row == ph) {
+                    row = 0;
+                    ++plane;
+                }
+            }
+        }
+        if (i0 + 4 <= planes_total) {
+            *reinterpret_cast<float4*>(dst + i0) = make_float4(v[0], v[1], v[2], v[3]);
+        } else {
+            for (int u = 0; i0 + u < planes_total; ++u) dst[i0 + u] = v[u];
+        }
         return;
     }
-    i -= planes_total;
+    const int i = (blockIdx.x - plane_blocks) * 256 + threadIdx.x;
     if (i >= kernel_total) return;
     int col;
     const int row = div_kp.divmod(i, col);
@@ -1184,13 +1233,14 @@ int pad_operands(ConvGather& g, int images, const GemmPlan& plan, int M, int N, 
     const int ph = g.H + 2 * g.PH, pw = g.W + 2 * g.PW;
     float* source = l.source_floats ? workspace + l.source_at : nullptr;
     float* kernel_copy = forward ? workspace + l.kernel_at : nullptr;
-    if (forward && !aligned16(kernel_copy)) return OK;  // the padded kernel is read with 16-byte loads
-    const std::int64_t work = l.source_floats + l.kernel_floats;
-    if (work > 0) {
-        launch(pad_operands_kernel, blocks_for(work, 256), 256, 0, stream, g.src, source,
-               static_cast<int>(l.source_floats), FastDiv(pw), FastDiv(ph), g.H, g.W, g.PH, g.PW,
-               forward ? *kernel : nullptr, kernel_copy, static_cast<int>(l.kernel_floats), FastDiv(l.kp),
-               g.features);
+    // The padded planes are written and the padded kernel read with 16-byte accesses.
+    if ((source && !aligned16(source)) || (forward && !aligned16(kernel_copy))) return OK;
+    const int plane_blocks = blocks_for((l.source_floats + 3) / 4, 256);
+    const int blocks = plane_blocks + blocks_for(l.kernel_floats, 256);
+    if (blocks > 0) {
+        launch(pad_operands_kernel, blocks, 256, 0, stream, g.src, source, static_cast<int>(l.source_floats),
+               plane_blocks, FastDiv(pw), FastDiv(ph), g.H, g.W, g.PH, g.PW, forward ? *kernel : nullptr,
+               kernel_copy, static_cast<int>(l.kernel_floats), FastDiv(l.kp), g.features);
         MFH_TRY(MFH_CHECK_LAUNCH("pad_operands", stream));
     }
     g.padded = source ? source : g.src;
