@@ -279,8 +279,11 @@ __global__ __launch_bounds__(256) void pool_backward_kernel(const float* __restr
 }
 
 constexpr int PLANE_FLOATS = 16384;   // floats of one workgroup's LDS plane buffer (64 KB)
-constexpr int ROW_FLOATS = 12288;     // floats of the im2col row kernel's LDS input band (48 KB)
-constexpr int ROW_AHEAD = 8;          // the row kernel's global loads per thread in flight while it stages
+constexpr int ROW_AHEAD = 8;          // the span kernel's global loads per thread in flight while it stages
+constexpr long long SPAN_RUNS = 4096;  // runs of output pixels the im2col span kernel aims for
+constexpr int SPAN_AHEAD = 8;           // band floats per thread the span kernel reads ahead
+constexpr int SPAN_PER_CU = 4;          // resident span workgroups per CU
+constexpr long long SPAN_LDS_FLOATS = 16384;  // the span kernel's LDS (band and feature offsets, 64 KB)
 
 // Workgroups are handed to the 8 XCDs of an MI355X round-robin by id, and each XCD has its own L2.
 // Renumbering workgroup b of `total` gives XCD x one contiguous run of logical ids, so that the
@@ -292,81 +295,105 @@ __device__ __forceinline__ int xcd_contiguous(int b, int total) {
     return xcd * base + min(xcd, extra) + position;
 }
 
-// im2col of one output row (n, oh) per workgroup: the KH input rows it reads, for every channel and
-// with padding rows as zeros, are staged in LDS with coalesced reads (padding columns are not
-// staged: they read as zero, which keeps the band at 30 KB for 64 channels of 40); then the
-// OW x K block of cols that this row owns (contiguous in memory) is written in order, four features
-// per 16-byte store when K % 4 == 0.
+// im2col in runs of `span` output pixels (n, oh, ow0 .. ow0 + span - 1), `items` runs in all, taken
+// by a grid of resident workgroups in turn (workgroup L takes runs L, L + gridDim.x, ...). A run's
+// input band (KH rows x bw = (span - 1) * SW + KW columns for every channel, padding as zeros) is
+// staged in LDS; then the span x K block of cols that the run owns (contiguous in memory) is
+// written in order, with no bounds tests: feature f of pixel p is band[offset[f] + p * SW], the
+// offsets (ci * KH + kh) * bw + kw of the K features held in LDS too, so the writes decompose no
+// index (four features per 16-byte store when K % 4 == 0). The first SPAN_AHEAD * 256 entries of
+// the next run's band are read into registers before the current run is written, so the reads of
+// one run overlap the writes of the other.
 template <bool VEC>
-__global__ __launch_bounds__(256) void im2col_row_kernel(const float* __restrict__ x, float* __restrict__ cols,
-                                                         int CI, int H, int W, int KH, int KW, int OH, int OW, int SH,
-                                                         int SW, int PH, int PW, FastDiv div_k, FastDiv div_khkw,
-                                                         FastDiv div_kw, FastDiv div_w, FastDiv div_oh) {
-    extern __shared__ float band[];  // CI * KH * W floats
-    int oh;
-    // Neighbouring output rows read KH - SH input rows in common: one XCD takes a run of them.
-    const int n = div_oh.divmod(xcd_contiguous(blockIdx.x, gridDim.x), oh);
-    const int entries = CI * KH * W;
-    const float* image = x + static_cast<long long>(n) * CI * H * W;
-    auto input = [&](int e) {
-        int col;
-        const int r = div_w.divmod(e, col);  // r = ci * KH + kh
-        const int ci = r / KH, kh = r - ci * KH;
-        const int ih = oh * SH - PH + kh;
-        return ih >= 0 && ih < H ? image[(ci * H + ih) * W + col] : 0.0f;
-    };
-    // ROW_AHEAD loads per thread in flight: one at a time, the band's ~30 loads per thread would
-    // each wait out the full memory latency.
-    int e = threadIdx.x;
-    for (; e + (ROW_AHEAD - 1) * 256 < entries; e += ROW_AHEAD * 256) {
-        float v[ROW_AHEAD];
-#pragma unroll
-        for (int u = 0; u < ROW_AHEAD; ++u) v[u] = input(e + u * 256);
-#pragma unroll
-        for (int u = 0; u < ROW_AHEAD; ++u) band[e + u * 256] = v[u];
-    }
-    for (; e < entries; e += 256) band[e] = input(e);
-    __syncthreads();
-    const int K = CI * KH * KW;
-    const int count = OW * K;
-    float* out = cols + (static_cast<long long>(n) * OH + oh) * OW * K;
-    auto value = [&](int j) {
-        int f;
-        const int ow = div_k.divmod(j, f);
-        int tap;
+__global__ __launch_bounds__(256) void im2col_span_kernel(const float* __restrict__ x, float* __restrict__ cols,
+                                                          int CI, int H, int W, int KH, int KW, int OH, int OW, int SH,
+                                                          int SW, int PH, int PW, int span, int bw, int items,
+                                                          FastDiv div_k, FastDiv div_khkw, FastDiv div_kw,
+                                                          FastDiv div_kh, FastDiv div_bw, FastDiv div_runs,
+                                                          FastDiv div_oh) {
+    extern __shared__ float band[];  // CI * KH * bw floats, then the K feature offsets
+    const int entries = CI * KH * bw, K = CI * KH * KW;
+    int* offset = reinterpret_cast<int*>(band + entries);
+    for (int f = threadIdx.x; f < K; f += 256) {
+        int tap, kw;
         const int ci = div_khkw.divmod(f, tap);
-        int kw;
         const int kh = div_kw.divmod(tap, kw);
-        const int iw = ow * SW - PW + kw;
-        return static_cast<unsigned>(iw) < static_cast<unsigned>(W) ? band[(ci * KH + kh) * W + iw] : 0.0f;
+        offset[f] = (ci * KH + kh) * bw + kw;
+    }
+    struct Run {
+        const float* image;
+        float* out;
+        int ih0, iw0, pixels;
     };
-    if constexpr (VEC) {
-        // Four consecutive features of one window position per thread: (ow, first feature) and its
-        // (ci, kh, kw) are decomposed once, the other three step kw, then kh, then ci forward.
-        for (int j = threadIdx.x * 4; j < count; j += 256 * 4) {
-            int f;
-            const int ow = div_k.divmod(j, f);
-            int tap, kw;
-            int ci = div_khkw.divmod(f, tap);
-            int kh = div_kw.divmod(tap, kw);
-            const int iw0 = ow * SW - PW;
-            float v[4];
+    auto run_of = [&](int item) {
+        int run, oh;
+        const int n = div_oh.divmod(div_runs.divmod(item, run), oh);
+        const int ow0 = run * span;
+        return Run{x + static_cast<long long>(n) * CI * H * W, cols + ((static_cast<long long>(n) * OH + oh) * OW + ow0) * K,
+                   oh * SH - PH, ow0 * SW - PW, min(span, OW - ow0)};
+    };
+    auto input = [&](const Run& r, int e) {
+        int col, kh;
+        const int ci = div_kh.divmod(div_bw.divmod(e, col), kh);  // band row ci * KH + kh
+        const int ih = r.ih0 + kh, iw = r.iw0 + col;
+        return static_cast<unsigned>(ih) < static_cast<unsigned>(H) && static_cast<unsigned>(iw) < static_cast<unsigned>(W)
+                   ? r.image[(ci * H + ih) * W + iw]
+                   : 0.0f;
+    };
+    float ahead[SPAN_AHEAD];
+    auto read_ahead = [&](const Run& r) {
 #pragma unroll
-            for (int u = 0; u < 4; ++u) {
-                const int iw = iw0 + kw;
-                v[u] = static_cast<unsigned>(iw) < static_cast<unsigned>(W) ? band[(ci * KH + kh) * W + iw] : 0.0f;
-                if (++kw == KW) {
-                    kw = 0;
-                    if (++kh == KH) {
-                        kh = 0;
-                        ++ci;
-                    }
-                }
-            }
-            *reinterpret_cast<float4*>(out + j) = make_float4(v[0], v[1], v[2], v[3]);
+        for (int u = 0; u < SPAN_AHEAD; ++u) {
+            const int e = threadIdx.x + u * 256;
+            ahead[u] = e < entries ? input(r, e) : 0.0f;
         }
-    } else {
-        for (int j = threadIdx.x; j < count; j += 256) out[j] = value(j);
+    };
+    // Consecutive workgroups of one XCD take consecutive runs, which read input rows in common.
+    int item = xcd_contiguous(blockIdx.x, gridDim.x);
+    if (item >= items) return;
+    Run r = run_of(item);
+    read_ahead(r);
+    constexpr int STEP = VEC ? 4 * 256 : 256;  // floats of cols a workgroup writes per round
+    const int step_pixels = div_k.div(STEP), step_features = STEP - step_pixels * K;
+    for (;;) {
+#pragma unroll
+        for (int u = 0; u < SPAN_AHEAD; ++u) {
+            const int e = threadIdx.x + u * 256;
+            if (e < entries) band[e] = ahead[u];
+        }
+        for (int e = threadIdx.x + SPAN_AHEAD * 256; e < entries; e += 256) band[e] = input(r, e);
+        __syncthreads();
+        const int next_item = item + gridDim.x;
+        const bool more = next_item < items;
+        Run next{};
+        if (more) {
+            next = run_of(next_item);
+            read_ahead(next);
+        }
+        // Element j = p * K + f of the run's block; j advances by STEP, (p, f) with it.
+        const int count = r.pixels * K;
+        int j = VEC ? 4 * threadIdx.x : threadIdx.x, f;
+        int p = div_k.divmod(j, f);
+        for (; j < count; j += STEP) {
+            const int base = p * SW;
+            if constexpr (VEC) {
+                const int4 o = *reinterpret_cast<const int4*>(offset + f);
+                *reinterpret_cast<float4*>(r.out + j) =
+                    make_float4(band[o.x + base], band[o.y + base], band[o.z + base], band[o.w + base]);
+            } else {
+                r.out[j] = band[offset[f] + base];
+            }
+            f += step_features;
+            p += step_pixels;
+            if (f >= K) {
+                f -= K;
+                ++p;
+            }
+        }
+        __syncthreads();  // every read of the band is done before the next run overwrites it
+        if (!more) break;
+        item = next_item;
+        r = next;
     }
 }
 
@@ -495,19 +522,29 @@ __global__ __launch_bounds__(256) void pool_backward_plane_kernel(const float* _
 int launch_im2col(const float* x, float* cols, const ConvGeometry& g, hipStream_t stream) {
     const int K = g.features();
     const int total = g.rows() * K;
-    const int band = g.CI * g.KH * g.W;
-    if (band <= ROW_FLOATS && static_cast<long long>(g.N) * g.OH <= INDEX_LIMIT) {
+    // Runs of output pixels: several per resident workgroup (about SPAN_RUNS in all), each run's
+    // band and the feature offsets within SPAN_LDS_FLOATS.
+    const long long rows = static_cast<long long>(g.N) * g.OH;
+    int runs = static_cast<int>(std::min<long long>(g.OW, std::max<long long>(1, (SPAN_RUNS + rows - 1) / rows)));
+    int span = (g.OW + runs - 1) / runs;
+    auto band_of = [&](int s) { return static_cast<long long>(g.CI) * g.KH * ((s - 1) * g.SW + g.KW); };
+    while (span > 1 && band_of(span) + K > SPAN_LDS_FLOATS) span = (span + 1) / 2;
+    runs = (g.OW + span - 1) / span;
+    if (band_of(span) + K <= SPAN_LDS_FLOATS && rows * runs <= INDEX_LIMIT) {
         const bool vec = K % 4 == 0 && (reinterpret_cast<std::uintptr_t>(cols) & 15) == 0;
-        const unsigned blocks = static_cast<unsigned>(g.N * g.OH);
-        const FastDiv dk(K), dkk(g.KH * g.KW), dkw(g.KW), dw(g.W), doh(g.OH);
-        const size_t lds = static_cast<size_t>(band) * sizeof(float);
+        const int items = static_cast<int>(rows * runs);
+        const unsigned blocks =
+            static_cast<unsigned>(std::min<long long>(items, SPAN_PER_CU * std::max(1, device_cu_count())));
+        const int bw = (span - 1) * g.SW + g.KW;
+        const FastDiv dk(K), dkk(g.KH * g.KW), dkw(g.KW), dkh(g.KH), dbw(bw), druns(runs), doh(g.OH);
+        const size_t lds = static_cast<size_t>(band_of(span) + K) * sizeof(float);
         if (vec)
-            launch(im2col_row_kernel<true>, blocks, 256, lds, stream, x, cols, g.CI, g.H, g.W, g.KH, g.KW, g.OH, g.OW, g.SH,
-                                                                  g.SW, g.PH, g.PW, dk, dkk, dkw, dw, doh);
+            launch(im2col_span_kernel<true>, blocks, 256, lds, stream, x, cols, g.CI, g.H, g.W, g.KH, g.KW, g.OH, g.OW,
+                   g.SH, g.SW, g.PH, g.PW, span, bw, items, dk, dkk, dkw, dkh, dbw, druns, doh);
         else
-            launch(im2col_row_kernel<false>, blocks, 256, lds, stream, x, cols, g.CI, g.H, g.W, g.KH, g.KW, g.OH, g.OW,
-                                                                   g.SH, g.SW, g.PH, g.PW, dk, dkk, dkw, dw, doh);
-        return MFH_CHECK_LAUNCH("im2col_row", stream);
+            launch(im2col_span_kernel<false>, blocks, 256, lds, stream, x, cols, g.CI, g.H, g.W, g.KH, g.KW, g.OH, g.OW,
+                   g.SH, g.SW, g.PH, g.PW, span, bw, items, dk, dkk, dkw, dkh, dbw, druns, doh);
+        return MFH_CHECK_LAUNCH("im2col_span", stream);
     }
     if (K % 4 == 0 && (reinterpret_cast<std::uintptr_t>(cols) & 15) == 0) {
         const int quads = total / 4;
