@@ -76,6 +76,10 @@ __global__ __launch_bounds__(256) void im2col_vec4_kernel(const float* __restric
 // f * f_stride + n * n_stride + oh*OW + ow ([f][n*OH*OW + p] or [n][f][p]), so for a fixed (kh, kw)
 // the threads of consecutive iw read consecutive ow: the gather is coalesced. No atomics, so the
 // result is deterministic.
+// FKH, FKW, FSH, FSW > 0: the kernel for that window and stride, with every tap's read issued
+// before the sums (taps outside the image add nothing: the sum starts at +0 and never is -0, so
+// skipping a term and adding +0 give the same bits); 0: any window, read window by window.
+template <int FKH, int FKW, int FSH, int FSW>
 __global__ __launch_bounds__(256) void col2im_t_kernel(const float* __restrict__ gcT, float* __restrict__ dx,
                                                        int total, FastDiv div_w, FastDiv div_h, FastDiv div_ci,
                                                        int CI, int KH, int KW, int OH, int OW, int SH, int SW,
@@ -88,19 +92,40 @@ __global__ __launch_bounds__(256) void col2im_t_kernel(const float* __restrict__
     const int t2 = div_h.divmod(t, ih);
     const int n = div_ci.divmod(t2, ci);
     const int hp = ih + PH, wp = iw + PW;  // coordinates in the zero-padded input
-    // Windows oh with oh*SH <= hp <= oh*SH + KH - 1, likewise ow.
-    const int oh_lo = hp >= KH ? div_sh.div(hp - KH) + 1 : 0;
-    const int oh_hi = min(OH - 1, div_sh.div(hp));
-    const int ow_lo = wp >= KW ? div_sw.div(wp - KW) + 1 : 0;
-    const int ow_hi = min(OW - 1, div_sw.div(wp));
-    const float* image = gcT + n * n_stride + static_cast<long long>(ci) * KH * KW * f_stride;
     float sum = 0.0f;
-    for (int oh = oh_lo; oh <= oh_hi; ++oh) {
-        const int kh = hp - oh * SH;
-        const float* row = image + kh * KW * f_stride + oh * OW;
-        for (int ow = ow_lo; ow <= ow_hi; ++ow) {
-            const int kw = wp - ow * SW;
-            sum += row[kw * f_stride + ow];
+    if constexpr (FKH > 0) {
+        const float* image = gcT + n * n_stride + static_cast<long long>(ci) * FKH * FKW * f_stride;
+        // Taps in the order of increasing (oh, ow): kh, then kw, descending.
+        float v[FKH * FKW];
+#pragma unroll
+        for (int a = 0; a < FKH; ++a) {
+            const int kh = FKH - 1 - a, oh_s = hp - kh;  // oh * FSH
+            const int oh = oh_s / FSH;
+            const bool row_ok = oh_s >= 0 && oh_s % FSH == 0 && oh < OH;
+#pragma unroll
+            for (int b = 0; b < FKW; ++b) {
+                const int kw = FKW - 1 - b, ow_s = wp - kw;
+                const int ow = ow_s / FSW;
+                const bool ok = row_ok && ow_s >= 0 && ow_s % FSW == 0 && ow < OW;
+                v[a * FKW + b] = ok ? image[(kh * FKW + kw) * f_stride + oh * OW + ow] : 0.0f;
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < FKH * FKW; ++u) sum += v[u];
+    } else {
+        // Windows oh with oh*SH <= hp <= oh*SH + KH - 1, likewise ow.
+        const int oh_lo = hp >= KH ? div_sh.div(hp - KH) + 1 : 0;
+        const int oh_hi = min(OH - 1, div_sh.div(hp));
+        const int ow_lo = wp >= KW ? div_sw.div(wp - KW) + 1 : 0;
+        const int ow_hi = min(OW - 1, div_sw.div(wp));
+        const float* image = gcT + n * n_stride + static_cast<long long>(ci) * KH * KW * f_stride;
+        for (int oh = oh_lo; oh <= oh_hi; ++oh) {
+            const int kh = hp - oh * SH;
+            const float* row = image + kh * KW * f_stride + oh * OW;
+            for (int ow = ow_lo; ow <= ow_hi; ++ow) {
+                const int kw = wp - ow * SW;
+                sum += row[kw * f_stride + ow];
+            }
         }
     }
     dx[idx] = accumulate ? dx[idx] + sum : sum;
@@ -564,10 +589,12 @@ int launch_col2im_t(const float* gcT, float* dx, const ConvGeometry& g, bool per
     const long long ohw = g.ohw();
     const long long f_stride = per_image ? ohw : static_cast<long long>(g.rows());
     const long long n_stride = per_image ? ohw * g.features() : ohw;
-    launch(col2im_t_kernel, blocks_for(total, 256), 256, 0, stream, gcT, dx, total, FastDiv(g.W), FastDiv(g.H),
-                                                                  FastDiv(g.CI), g.CI, g.KH, g.KW, g.OH, g.OW, g.SH,
-                                                                  g.SW, FastDiv(g.SH), FastDiv(g.SW), g.PH, g.PW,
-                                                                  f_stride, n_stride, accumulate ? 1 : 0);
+    auto kernel = col2im_t_kernel<0, 0, 0, 0>;
+    if (g.KH == 3 && g.KW == 3 && g.SH == 1 && g.SW == 1) kernel = col2im_t_kernel<3, 3, 1, 1>;
+    else if (g.KH == 3 && g.KW == 3 && g.SH == 2 && g.SW == 2) kernel = col2im_t_kernel<3, 3, 2, 2>;
+    launch(kernel, blocks_for(total, 256), 256, 0, stream, gcT, dx, total, FastDiv(g.W), FastDiv(g.H), FastDiv(g.CI),
+           g.CI, g.KH, g.KW, g.OH, g.OW, g.SH, g.SW, FastDiv(g.SH), FastDiv(g.SW), g.PH, g.PW, f_stride, n_stride,
+           accumulate ? 1 : 0);
     return MFH_CHECK_LAUNCH("col2im_t", stream);
 }
 
