@@ -44,6 +44,13 @@ RESNET_CASES = (
     ("l4", (2, 512, 4, 5), (512, 512, 3, 3), (1, 1), (1, 1)),
     ("widepad", (1, 2, 5, 6), (3, 2, 1, 2), (1, 1), (1, 2)),
 )
+# Output channels that end inside a row tile: the last row tile of a chunked (co40) or padded
+# natural-order (stem20) product reads dy's rows, and the forward the kernel's rows, with
+# range-checked offsets, and its rows past CO read zero.
+PARTIAL_ROW_CASES = (
+    ("co40", (2, 64, 9, 11), (40, 64, 3, 3), (1, 1), (1, 1)),
+    ("stem20", (2, 3, 20, 24), (20, 3, 7, 7), (2, 2), (3, 3)),
+)
 
 
 @contextlib.contextmanager
@@ -172,7 +179,7 @@ def test_recomputed_columns_give_identical_gradients():
         np.testing.assert_array_equal(a, b)
 
 
-@pytest.mark.parametrize("case", CONV_CASES[1:] + RESNET_CASES, ids=lambda c: c[0])
+@pytest.mark.parametrize("case", CONV_CASES[1:] + RESNET_CASES + PARTIAL_ROW_CASES, ids=lambda c: c[0])
 def test_implicit_path_is_exact_on_integer_data(case):
     """Small integers make every product and every partial sum exact in float32, whatever the
     summation order: the implicit forward, dW and dX must then equal the FP64 loops bit for bit,
@@ -513,13 +520,14 @@ def test_stem_forward_keeps_an_inf_out_of_windows_that_do_not_cover_it():
 IMPLICIT_TILES = 12  # tiles of the implicit products (plan code 16 + tile * 128 + slices - 1)
 
 
-@pytest.mark.parametrize("case", (RESNET_CASES[1], ("l2s", (2, 128, 15, 20), (128, 128, 3, 3), (1, 1), (1, 1))),
-                         ids=lambda c: c[0])
+@pytest.mark.parametrize("case", (RESNET_CASES[1], ("l2s", (2, 128, 15, 20), (128, 128, 3, 3), (1, 1), (1, 1)),
+                                  PARTIAL_ROW_CASES[0]), ids=lambda c: c[0])
 def test_every_implicit_tile_is_exact_on_integer_data(case):
     """Each tile of the implicit catalogue (forced through its plan code, unsplit and split over K;
     the 24-way dW split takes the grouped reduction) gives the FP64 loops' forward, dX, dW and db
-    bit for bit on integer data; a tile without a dW kernel (the 96-pixel one) is refused with a
-    reason instead of launched."""
+    bit for bit on integer data; a tile without a kernel for a product (the 96-pixel one: no dW,
+    and no natural-order dX, which 40 output channels take) is refused with a reason instead of
+    launched."""
     _, x_shape, w_shape, stride, padding = case
     print("tiles", case[0], flush=True)
     rng = np.random.default_rng(17)
@@ -546,12 +554,16 @@ def test_every_implicit_tile_is_exact_on_integer_data(case):
             native._raise_for(lib.mfh_conv_forward_implicit(
                 xg.data_ptr(), wg.data_ptr(), order.data_ptr(), 1, 0, 0, y.data_ptr(), *g.c_args(), 0, 0.0, code,
                 workspace.data_ptr(), workspace.numel(), stream), lib)
-            native._raise_for(lib.mfh_conv_backward_implicit(
+            status = lib.mfh_conv_backward_implicit(
                 xg.data_ptr(), wg.data_ptr(), dyg.data_ptr(), 0, 0, 0, dx.data_ptr(), flip.data_ptr(), 0, 0, 0,
                 *g.c_args(), 0, 0.0, 1, code, native.CONV_WFLIP_READY, workspace.data_ptr(), workspace.numel(),
-                stream), lib)
+                stream)
             np.testing.assert_array_equal(host(y), ref_y, err_msg=f"forward tile {tile} slices {slices}")
-            np.testing.assert_array_equal(host(dx), ref_dx, err_msg=f"dX tile {tile} slices {slices}")
+            if tile == 11 and co % 32 != 0:
+                assert status == 2 and "no kernel" in lib.mfh_last_error().decode()
+            else:
+                native._raise_for(status, lib)
+                np.testing.assert_array_equal(host(dx), ref_dx, err_msg=f"dX tile {tile} slices {slices}")
             status = lib.mfh_conv_backward_implicit(
                 xg.data_ptr(), wg.data_ptr(), dyg.data_ptr(), 0, 0, dw.data_ptr(), 0, 0, 0, partial.data_ptr(),
                 db.data_ptr(), *g.c_args(), 0, 0.0, code, 1, 0, workspace.data_ptr(), workspace.numel(), stream)
