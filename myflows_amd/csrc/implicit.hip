@@ -95,8 +95,8 @@ constexpr int PADDED_TABLE_MAX = 1024;
 // The natural-order tile read from the zero-padded copy of the source (ConvGather::padded) and stored
 // pixel-major like GatherChunkRows' ([BN][BK + 4]): thread t takes pixel n0 + t % BN and the PER
 // consecutive features (t / BN) * PER + i of the stage. The byte offset of every feature inside an
-// image's padded planes is read from a table in LDS (two 16-byte reads per stage, the same address
-// for a whole wave), so a load costs one add, with no window bounds test and no division. A feature
+// image's padded planes is read from a table in LDS (PER / 4 16-byte reads per stage, the same
+// address for a whole wave), so a load costs one add, with no window bounds test and no division. A feature
 // past the last (table entry BUFFER_OOB), or a pixel past the last, reads zero; both at once read
 // the tensor's first element, which only reaches an output column past the last pixel, never
 // stored.
