@@ -336,9 +336,9 @@ __global__ __launch_bounds__(256) void im2col_span_kernel(const float* __restric
                                                           FastDiv div_k, FastDiv div_khkw, FastDiv div_kw,
                                                           FastDiv div_kh, FastDiv div_bw, FastDiv div_runs,
                                                           FastDiv div_oh) {
-    extern __shared__ float band[];  // CI * KH * bw floats, then the K feature offsets
+    extern __shared__ float band[];  // CI * KH * bw floats, then (16-byte aligned) the K feature offsets
     const int entries = CI * KH * bw, K = CI * KH * KW;
-    int* offset = reinterpret_cast<int*>(band + entries);
+    int* offset = reinterpret_cast<int*>(band + (entries + 3) / 4 * 4);
     for (int f = threadIdx.x; f < K; f += 256) {
         int tap, kw;
         const int ci = div_khkw.divmod(f, tap);
@@ -552,7 +552,8 @@ int launch_im2col(const float* x, float* cols, const ConvGeometry& g, hipStream_
     const long long rows = static_cast<long long>(g.N) * g.OH;
     int runs = static_cast<int>(std::min<long long>(g.OW, std::max<long long>(1, (SPAN_RUNS + rows - 1) / rows)));
     int span = (g.OW + runs - 1) / runs;
-    auto band_of = [&](int s) { return static_cast<long long>(g.CI) * g.KH * ((s - 1) * g.SW + g.KW); };
+    // LDS floats of a run of s pixels: its band, rounded up to whole 16 bytes, and the feature offsets.
+    auto band_of = [&](int s) { return (static_cast<long long>(g.CI) * g.KH * ((s - 1) * g.SW + g.KW) + 3) / 4 * 4; };
     while (span > 1 && band_of(span) + K > SPAN_LDS_FLOATS) span = (span + 1) / 2;
     runs = (g.OW + span - 1) / span;
     if (band_of(span) + K <= SPAN_LDS_FLOATS && rows * runs <= INDEX_LIMIT) {

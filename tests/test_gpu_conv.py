@@ -206,7 +206,10 @@ def test_implicit_path_is_exact_on_integer_data(case):
 @pytest.mark.parametrize("shape,kernel,stride,padding", [
     ((2, 3, 7, 9), (3, 3), (1, 1), (1, 1)), ((1, 2, 8, 9), (3, 2), (2, 3), (1, 0)),
     ((2, 3, 16, 16), (7, 7), (2, 2), (3, 3)), ((3, 5, 6, 5), (1, 1), (2, 2), (0, 0)),
-    ((2, 64, 30, 40), (3, 3), (1, 1), (1, 1)), ((2, 16, 29, 39), (3, 3), (2, 2), (1, 1))])
+    ((2, 64, 30, 40), (3, 3), (1, 1), (1, 1)), ((2, 16, 29, 39), (3, 3), (2, 2), (1, 1)),
+    # 4096 output rows take runs of a whole row (6 pixels): a 14-float input band, so the feature
+    # offsets after it start at the next 16-byte boundary (the float4 path, K = 4).
+    ((64, 2, 64, 7), (1, 2), (1, 1), (0, 0))])
 def test_im2col_and_col2im_are_bit_exact(shape, kernel, stride, padding):
     print("im2col", shape, kernel, stride, padding, flush=True)
     rng = np.random.default_rng(3)
