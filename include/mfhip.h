@@ -251,6 +251,22 @@ MFH_API int mfh_conv_backward_implicit_streams(uint64_t x, uint64_t weight, uint
                                                uint64_t workspace, int64_t dw_workspace_floats,
                                                int64_t workspace_floats, uint64_t stream, uint64_t dw_stream);
 
+/* mfh_conv_backward_implicit_streams for a caller that forms dx itself: when the convolution has
+ * stride 1, dx is written fresh (no CONV_ACCUMULATE_DX) and the dX product's plan splits K (over the
+ * dX part of the workspace, which starts dw_workspace_floats floats in), the product's slices are
+ * left there unreduced (slices x CI x N*H*W floats, laid out as mfh_bn_forward_split's partial)
+ * and *dx_slices receives their count; dx is then not written (mfh_bn_backward_split forms it and
+ * stores it). Otherwise dx is written as by mfh_conv_backward_implicit_streams and *dx_slices is 1.
+ * No counterpart in the reference: the fused graph's BN -> Conv pairs use it in the backward. */
+MFH_API int mfh_conv_backward_implicit_deferred(uint64_t x, uint64_t weight, uint64_t dy, uint64_t y, uint64_t gated,
+                                                uint64_t dw, uint64_t dx, uint64_t wflip, uint64_t grad_cols,
+                                                uint64_t partial, uint64_t db, int N, int CI, int H, int W, int CO,
+                                                int KH, int KW, int OH, int OW, int SH, int SW, int PH, int PW,
+                                                int activation, float alpha, int dw_engine, int dx_engine, int flags,
+                                                uint64_t workspace, int64_t dw_workspace_floats,
+                                                int64_t workspace_floats, int* dx_slices, uint64_t stream,
+                                                uint64_t dw_stream);
+
 /* ---- max pooling ---------------------------------------------------------------------------- */
 
 /* Max-pool without padding (the caller pads with -inf): y = window max in (kh, kw) order with the
@@ -365,6 +381,20 @@ MFH_API int mfh_bn_backward(uint64_t x, uint64_t dy, uint64_t gate, uint64_t gam
                             uint64_t x_grad, uint64_t gamma_grad, uint64_t beta_grad, uint64_t residual_grad,
                             uint64_t workspace, int64_t workspace_doubles, int N, int C, int HW, int training,
                             int add_x, int add_gamma, int add_beta, int add_residual, uint64_t stream);
+
+/* mfh_bn_backward whose dy is the dx of a convolution that mfh_conv_backward_implicit_deferred left
+ * as `slices` FP32 split-K slices (partial laid out as in mfh_bn_forward_split): dy is formed first,
+ * each element the FP64 sum of its slices in slice order rounded once (the bits of the product's
+ * own slice reduction), and stored into dy; then the gradients are those of mfh_bn_backward on that
+ * dy, in one launch. Only for passes that sum over one launch per channel (N * HW at most 8192, a
+ * gradient of gamma, beta or, in training, x asked for); others return status 2. No counterpart in
+ * the reference (its convolution and batch norm are separate operators): the fused graph's
+ * BN -> Conv pairs use it. */
+MFH_API int mfh_bn_backward_split(uint64_t partial, int slices, uint64_t x, uint64_t dy, uint64_t gate, uint64_t gamma,
+                                  uint64_t mean, uint64_t inv_std, uint64_t x_grad, uint64_t gamma_grad,
+                                  uint64_t beta_grad, uint64_t residual_grad, uint64_t workspace,
+                                  int64_t workspace_doubles, int N, int C, int HW, int training, int add_x,
+                                  int add_gamma, int add_beta, int add_residual, uint64_t stream);
 
 /* Batch norm + ReLU + max-pool (KH x KW window, stride SH x SW, no padding) as one unit, for a
  * network stem: the ReLU output is never stored. Returns 1 when the fused kernels take this shape

@@ -185,7 +185,8 @@ int conv_backward_implicit(std::uint64_t x, std::uint64_t weight, std::uint64_t 
                            std::uint64_t grad_cols, std::uint64_t partial, std::uint64_t db, const ConvGeometry& g,
                            int activation, float alpha, int dw_engine, int dx_engine, int flags, float* ws_dw,
                            std::int64_t dw_floats, float* ws_dx, std::int64_t dx_floats, hipStream_t s,
-                           hipStream_t dw_s) {
+                           hipStream_t dw_s, int* dx_slices = nullptr) {
+    if (dx_slices) *dx_slices = 1;
     MFH_TRY(validate(g));
     MFH_TRY(validate_activation(activation, alpha));
     const bool gated_dy = activation != ACT_NONE;
@@ -233,7 +234,7 @@ int conv_backward_implicit(std::uint64_t x, std::uint64_t weight, std::uint64_t 
     if (!dx) return OK;
     if (unit_stride)
         return conv_implicit_dgrad(g, grad, as_ptr<const float>(weight), as_ptr<float>(wflip), prepared,
-                                   as_ptr<float>(dx), accumulate, dx_engine, ws_dx, dx_floats, s);
+                                   as_ptr<float>(dx), accumulate, dx_engine, ws_dx, dx_floats, s, dx_slices);
     if (phases)
         return conv_implicit_dgrad_phases(g, grad, as_ptr<const float>(weight), as_ptr<float>(wflip), prepared,
                                           as_ptr<float>(dx), accumulate, dx_engine, ws_dx, dx_floats, s);
@@ -614,6 +615,26 @@ MFH_API int mfh_conv_backward_implicit_streams(
                                   workspace_floats - dw_workspace_floats, as_stream(stream), as_stream(dw_stream));
 }
 
+MFH_API int mfh_conv_backward_implicit_deferred(
+    std::uint64_t x, std::uint64_t weight, std::uint64_t dy, std::uint64_t y, std::uint64_t gated, std::uint64_t dw,
+    std::uint64_t dx, std::uint64_t wflip, std::uint64_t grad_cols, std::uint64_t partial, std::uint64_t db, int N,
+    int CI, int H, int W, int CO, int KH, int KW, int OH, int OW, int SH, int SW, int PH, int PW, int activation,
+    float alpha, int dw_engine, int dx_engine, int flags, std::uint64_t workspace, std::int64_t dw_workspace_floats,
+    std::int64_t workspace_floats, int* dx_slices, std::uint64_t stream, std::uint64_t dw_stream) {
+    MFH_TRY(require_ready());
+    MFH_REQUIRE(dx_slices, "the deferred conv backward needs the slice-count output");
+    *dx_slices = 1;
+    const ConvGeometry g{N, CI, H, W, CO, KH, KW, OH, OW, SH, SW, PH, PW};
+    MFH_REQUIRE(dw_workspace_floats >= 0 && dw_workspace_floats <= workspace_floats,
+                "the dW part of the workspace must lie within it");
+    float* ws = as_ptr<float>(workspace);
+    float* ws_dx = ws ? ws + dw_workspace_floats : nullptr;
+    return conv_backward_implicit(x, weight, dy, y, gated, dw, dx, wflip, grad_cols, partial, db, g, activation, alpha,
+                                  dw_engine, dx_engine, flags, ws, dw_workspace_floats, ws_dx,
+                                  workspace_floats - dw_workspace_floats, as_stream(stream), as_stream(dw_stream),
+                                  dx_slices);
+}
+
 MFH_API int mfh_pool_forward(std::uint64_t x, std::uint64_t y, std::uint64_t argmax, int N, int C, int H, int W,
                              int OH, int OW, int KH, int KW, int SH, int SW, std::uint64_t stream) {
     MFH_TRY(require_ready());
@@ -844,6 +865,41 @@ MFH_API int mfh_bn_forward_split(std::uint64_t partial, int slices, std::uint64_
                               as_stream(stream));
 }
 
+namespace {
+
+int bn_backward_of(std::uint64_t x, std::uint64_t dy, std::uint64_t gate, std::uint64_t gamma, std::uint64_t mean,
+                   std::uint64_t inv_std, std::uint64_t x_grad, std::uint64_t gamma_grad, std::uint64_t beta_grad,
+                   std::uint64_t residual_grad, std::uint64_t workspace, std::int64_t workspace_doubles,
+                   const NormShape& s, int training, int add_x, int add_gamma, int add_beta, int add_residual,
+                   NormBackward* b) {
+    MFH_TRY(validate_norm(s));
+    MFH_REQUIRE(x && dy && gamma && mean && inv_std, "batch-norm backward received a null buffer");
+    MFH_REQUIRE(!residual_grad || gate, "a residual gradient comes from a fused ReLU: pass its output as gate");
+    MFH_REQUIRE(workspace && workspace_doubles >= norm_workspace_doubles(s),
+                "batch-norm workspace is smaller than mfh_bn_workspace");
+    MFH_REQUIRE((workspace & 15) == 0, "batch-norm workspace must be 16-byte aligned");
+    *b = NormBackward{};
+    b->x = as_ptr<const float>(x);
+    b->dy = as_ptr<const float>(dy);
+    b->gate = as_ptr<const float>(gate);
+    b->gamma = as_ptr<const float>(gamma);
+    b->mean = as_ptr<const float>(mean);
+    b->inv_std = as_ptr<const float>(inv_std);
+    b->x_grad = as_ptr<float>(x_grad);
+    b->gamma_grad = as_ptr<float>(gamma_grad);
+    b->beta_grad = as_ptr<float>(beta_grad);
+    b->residual_grad = as_ptr<float>(residual_grad);
+    b->partial = as_ptr<double>(workspace);
+    b->training = training != 0;
+    b->add_x = add_x != 0;
+    b->add_gamma = add_gamma != 0;
+    b->add_beta = add_beta != 0;
+    b->add_residual = add_residual != 0;
+    return OK;
+}
+
+}  // namespace
+
 MFH_API int mfh_bn_backward(std::uint64_t x, std::uint64_t dy, std::uint64_t gate, std::uint64_t gamma,
                             std::uint64_t mean, std::uint64_t inv_std, std::uint64_t x_grad, std::uint64_t gamma_grad,
                             std::uint64_t beta_grad, std::uint64_t residual_grad, std::uint64_t workspace,
@@ -851,30 +907,27 @@ MFH_API int mfh_bn_backward(std::uint64_t x, std::uint64_t dy, std::uint64_t gat
                             int add_gamma, int add_beta, int add_residual, std::uint64_t stream) {
     MFH_TRY(require_ready());
     const NormShape s{N, C, HW};
-    MFH_TRY(validate_norm(s));
-    MFH_REQUIRE(x && dy && gamma && mean && inv_std, "batch-norm backward received a null buffer");
-    MFH_REQUIRE(!residual_grad || gate, "a residual gradient comes from a fused ReLU: pass its output as gate");
-    MFH_REQUIRE(workspace && workspace_doubles >= norm_workspace_doubles(s),
-                "batch-norm workspace is smaller than mfh_bn_workspace");
-    MFH_REQUIRE((workspace & 15) == 0, "batch-norm workspace must be 16-byte aligned");
-    NormBackward b{};
-    b.x = as_ptr<const float>(x);
-    b.dy = as_ptr<const float>(dy);
-    b.gate = as_ptr<const float>(gate);
-    b.gamma = as_ptr<const float>(gamma);
-    b.mean = as_ptr<const float>(mean);
-    b.inv_std = as_ptr<const float>(inv_std);
-    b.x_grad = as_ptr<float>(x_grad);
-    b.gamma_grad = as_ptr<float>(gamma_grad);
-    b.beta_grad = as_ptr<float>(beta_grad);
-    b.residual_grad = as_ptr<float>(residual_grad);
-    b.partial = as_ptr<double>(workspace);
-    b.training = training != 0;
-    b.add_x = add_x != 0;
-    b.add_gamma = add_gamma != 0;
-    b.add_beta = add_beta != 0;
-    b.add_residual = add_residual != 0;
+    NormBackward b;
+    MFH_TRY(bn_backward_of(x, dy, gate, gamma, mean, inv_std, x_grad, gamma_grad, beta_grad, residual_grad, workspace,
+                           workspace_doubles, s, training, add_x, add_gamma, add_beta, add_residual, &b));
     return norm_backward(s, b, as_stream(stream));
+}
+
+MFH_API int mfh_bn_backward_split(std::uint64_t partial, int slices, std::uint64_t x, std::uint64_t dy,
+                                  std::uint64_t gate, std::uint64_t gamma, std::uint64_t mean, std::uint64_t inv_std,
+                                  std::uint64_t x_grad, std::uint64_t gamma_grad, std::uint64_t beta_grad,
+                                  std::uint64_t residual_grad, std::uint64_t workspace, std::int64_t workspace_doubles,
+                                  int N, int C, int HW, int training, int add_x, int add_gamma, int add_beta,
+                                  int add_residual, std::uint64_t stream) {
+    MFH_TRY(require_ready());
+    const NormShape s{N, C, HW};
+    NormBackward b;
+    MFH_TRY(bn_backward_of(x, dy, gate, gamma, mean, inv_std, x_grad, gamma_grad, beta_grad, residual_grad, workspace,
+                           workspace_doubles, s, training, add_x, add_gamma, add_beta, add_residual, &b));
+    MFH_REQUIRE(partial, "batch-norm backward received a null buffer");
+    MFH_REQUIRE(slices >= 1, "slices must be positive");
+    MFH_REQUIRE(static_cast<std::int64_t>(slices) * N * C * HW <= INDEX_LIMIT, "the slices exceed the int32 index range");
+    return norm_backward_split(s, b, as_ptr<const float>(partial), slices, as_ptr<float>(dy), as_stream(stream));
 }
 
 namespace {

@@ -269,10 +269,13 @@ int conv_implicit_wgrad(const ConvGeometry& g, const float* x, const float* dy, 
                         float* db, int engine, float* workspace, std::int64_t workspace_floats, hipStream_t stream);
 // dX of a stride-1 convolution as a forward convolution of dy with the flipped kernel, read from
 // wflip (CI x CO*KH*KW floats in the order launch_weight_orders writes with flip 1), which this call
-// fills from w unless `prepared`. With accumulate, dx += the result.
+// fills from w unless `prepared`. With accumulate, dx += the result. With `deferred`, a product
+// split over K that writes dx fresh may leave its FP32 slices in the workspace for the caller to
+// reduce (slice z of CI x N*H*W floats at workspace + z * CI * N*H*W; dx unwritten): *deferred
+// receives the slice count, or 1 when dx was written here.
 int conv_implicit_dgrad(const ConvGeometry& g, const float* dy, const float* w, float* wflip, bool prepared, float* dx,
                         bool accumulate, int engine, float* workspace, std::int64_t workspace_floats,
-                        hipStream_t stream);
+                        hipStream_t stream, int* deferred = nullptr);
 // dX of a strided convolution as SH*SW phase products (see DgradPhase), each a stride-1 implicit
 // convolution of dy with its flipped sub-kernel whose epilogue writes the phase's lattice of dx.
 // The sub-kernels are read from wphase (CI*CO*KH*KW floats in the order launch_weight_orders
@@ -373,6 +376,11 @@ struct NormBackward {
     bool training, add_x, add_gamma, add_beta, add_residual;
 };
 int norm_backward(const NormShape& s, const NormBackward& b, hipStream_t stream);
+// Backward of a one-launch shape (a pass with sums) whose dy is formed first from `slices` split-K
+// slices of a convolution's dX product (partial: slices x C x N*HW floats) and stored into dy,
+// which must be b.dy.
+int norm_backward_split(const NormShape& s, const NormBackward& b, const float* partial, int slices, float* dy,
+                        hipStream_t stream);
 
 // Batch norm + ReLU + max-pool (no padding) as one unit; the ReLU output is never stored. The
 // forward writes the pooled values and their int32 flat argmax into the N x C x H x W tensor, the

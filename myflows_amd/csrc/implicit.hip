@@ -1461,7 +1461,7 @@ int conv_implicit_wgrad(const ConvGeometry& g, const float* x, const float* dy, 
 
 int conv_implicit_dgrad(const ConvGeometry& g, const float* dy, const float* w, float* wflip, bool prepared, float* dx,
                         bool accumulate, int engine, float* workspace, std::int64_t workspace_floats,
-                        hipStream_t stream) {
+                        hipStream_t stream, int* deferred) {
     const int khw = g.KH * g.KW;
     const int M = g.CI, N = g.N * g.H * g.W, K = g.CO * khw;
     GemmPlan plan;
@@ -1477,7 +1477,10 @@ int conv_implicit_dgrad(const ConvGeometry& g, const float* dy, const float* w, 
     e.segment = g.H * g.W;
     e.segment_stride = static_cast<long long>(g.CI) * g.H * g.W;
     e.accumulate = accumulate;
-    return run_implicit(false, plan, wflip, K, M, N, K, gather, dx, g.H * g.W, e, workspace, stream);
+    const bool defer = deferred && plan.slices > 1 && !accumulate;
+    if (deferred) *deferred = defer ? plan.slices : 1;
+    return run_implicit(false, plan, wflip, K, M, N, K, gather, dx, g.H * g.W, e, workspace, stream, nullptr, nullptr,
+                        defer);
 }
 
 int conv_implicit_dgrad_phases(const ConvGeometry& g, const float* dy, const float* w, float* wphase, bool prepared,

@@ -660,13 +660,16 @@ __global__ __launch_bounds__(T) void norm_forward_channel_kernel(PartialArgs pa,
     }
 }
 
-template <int T, bool QUAD>
-__global__ __launch_bounds__(T) void norm_backward_channel_kernel(PartialArgs pa, DxArgs p) {
+// SPLIT: dy is formed from src first (the split-K slices of the product whose output gradient it
+// is) and stored, then used as below, in one launch.
+template <int T, bool QUAD, bool SPLIT = false>
+__global__ __launch_bounds__(T) void norm_backward_channel_kernel(PartialArgs pa, DxArgs p, SplitSource src) {
     using S = ChannelSlots<T, QUAD>;
     constexpr int G = S::GROUPS, W = S::WIDTH;
     __shared__ float coef[3];
     const int c = blockIdx.x, total = pa.total, plane = p.C * p.HW;
     const double centre = static_cast<double>(p.mean[c]) + static_cast<double>(p.mean[p.C + c]);
+    const long long channel = static_cast<long long>(c) * total;  // channel c's first position in a slice
     float xv[G][W] = {}, dv[G][W] = {}, tv[G][W] = {};
     int at[G];
 #pragma unroll
@@ -677,9 +680,15 @@ __global__ __launch_bounds__(T) void norm_backward_channel_kernel(PartialArgs pa
         at[i] = n * plane + c * p.HW + hw;
         if (j < total) {
             load_group<W>(p.x, at[i], pa.vec, xv[i]);
-            load_group<W>(p.dy, at[i], pa.vec, dv[i]);
+            if constexpr (SPLIT) split_group<W>(src, c, channel + j, pa.vec, dv[i]);
+            else load_group<W>(p.dy, at[i], pa.vec, dv[i]);
             if (p.gate) load_group<W>(p.gate, at[i], pa.vec, tv[i]);
         }
+    }
+    if constexpr (SPLIT) {
+#pragma unroll
+        for (int i = 0; i < G; ++i)
+            if (S::first(i) < total) store_group<W>(src.x, at[i], pa.vec, dv[i]);
     }
     double a[CHAINS] = {}, b[CHAINS] = {};
 #pragma unroll
@@ -1269,11 +1278,23 @@ int norm_relu_pool_backward(const NormShape& s, const NormBackward& b, const Poo
     return MFH_CHECK_LAUNCH("norm_dx_pool", stream);
 }
 
-int norm_backward(const NormShape& s, const NormBackward& b, hipStream_t stream) {
-    const int total = s.N * s.C * s.HW;
-    const int slices = norm_slices(s);
-    const bool sums = b.gamma_grad || b.beta_grad || (b.training && b.x_grad);
-    PartialArgs args{};
+namespace {
+
+template <bool SPLIT>
+void launch_backward_channel(const NormShape& s, const PartialArgs& args, const DxArgs& d, const SplitSource& src,
+                             hipStream_t stream) {
+    const bool wide = wide_sums(s);
+    if (quad_order(s)) {
+        if (wide) launch(norm_backward_channel_kernel<WIDE_PT, true, SPLIT>, s.C, WIDE_PT, 0, stream, args, d, src);
+        else launch(norm_backward_channel_kernel<PT, true, SPLIT>, s.C, PT, 0, stream, args, d, src);
+    } else {
+        if (wide) launch(norm_backward_channel_kernel<WIDE_PT, false, SPLIT>, s.C, WIDE_PT, 0, stream, args, d, src);
+        else launch(norm_backward_channel_kernel<PT, false, SPLIT>, s.C, PT, 0, stream, args, d, src);
+    }
+}
+
+void backward_args(const NormShape& s, const NormBackward& b, int slices, bool sums, PartialArgs& args, DxArgs& d) {
+    args = PartialArgs{};
     args.x = b.x;
     args.dy = b.dy;
     args.gate = b.gate;
@@ -1287,10 +1308,7 @@ int norm_backward(const NormShape& s, const NormBackward& b, hipStream_t stream)
     args.chunk = slice_chunk(s, slices);
     args.div_hw = FastDiv(s.HW);
     args.vec = quad_vec(s, {b.x, b.dy, b.gate, b.residual_grad, b.x_grad});
-    const bool fused = sums && slices == 1;
-    if ((sums || b.residual_grad) && !fused) MFH_TRY(run_partials(GRADS, s, args, stream));
-    if (!b.x_grad && !sums) return OK;
-    DxArgs d{};
+    d = DxArgs{};
     d.x = b.x;
     d.dy = b.dy;
     d.gate = b.gate;
@@ -1301,7 +1319,7 @@ int norm_backward(const NormShape& s, const NormBackward& b, hipStream_t stream)
     d.gamma_grad = b.gamma_grad;
     d.beta_grad = b.beta_grad;
     d.partial = b.partial;
-    d.total = total;
+    d.total = s.N * s.C * s.HW;
     d.C = s.C;
     d.HW = s.HW;
     d.slices = slices;
@@ -1313,23 +1331,47 @@ int norm_backward(const NormShape& s, const NormBackward& b, hipStream_t stream)
     d.count = static_cast<double>(s.N) * s.HW;
     d.div_hw = FastDiv(s.HW);
     d.div_c = FastDiv(s.C);
+}
+
+}  // namespace
+
+int norm_backward(const NormShape& s, const NormBackward& b, hipStream_t stream) {
+    const int total = s.N * s.C * s.HW;
+    const int slices = norm_slices(s);
+    const bool sums = b.gamma_grad || b.beta_grad || (b.training && b.x_grad);
+    PartialArgs args;
+    DxArgs d;
+    backward_args(s, b, slices, sums, args, d);
+    const bool fused = sums && slices == 1;
+    if ((sums || b.residual_grad) && !fused) MFH_TRY(run_partials(GRADS, s, args, stream));
+    if (!b.x_grad && !sums) return OK;
     const bool vec = vec4_spans(s) && aligned16(b.x) && aligned16(b.dy) && (!b.gate || aligned16(b.gate)) &&
                      (!b.x_grad || aligned16(b.x_grad));
     if (fused) {
-        const bool wide = wide_sums(s);
-        if (quad_order(s)) {
-            if (wide) launch(norm_backward_channel_kernel<WIDE_PT, true>, s.C, WIDE_PT, 0, stream, args, d);
-            else launch(norm_backward_channel_kernel<PT, true>, s.C, PT, 0, stream, args, d);
-        } else {
-            if (wide) launch(norm_backward_channel_kernel<WIDE_PT, false>, s.C, WIDE_PT, 0, stream, args, d);
-            else launch(norm_backward_channel_kernel<PT, false>, s.C, PT, 0, stream, args, d);
-        }
+        launch_backward_channel<false>(s, args, d, SplitSource{}, stream);
         return MFH_CHECK_LAUNCH("norm_backward_channel", stream);
     }
     const unsigned blocks = blocks_for(total, APPLY_SPAN);
     if (vec) launch(norm_dx_kernel<4>, blocks, APPLY_THREADS, 0, stream, d);
     else launch(norm_dx_kernel<1>, blocks, APPLY_THREADS, 0, stream, d);
     return MFH_CHECK_LAUNCH("norm_dx", stream);
+}
+
+int norm_backward_split(const NormShape& s, const NormBackward& b, const float* partial, int slices, float* dy,
+                        hipStream_t stream) {
+    const bool sums = b.gamma_grad || b.beta_grad || (b.training && b.x_grad);
+    if (!sums || norm_slices(s) != 1)
+        return MFH_FAIL(ERR_ARG, "forming dy inside the batch-norm backward needs a pass that sums over one launch "
+                                 "per channel (N*H*W at most 8192, with a gradient of gamma, beta or, training, x); "
+                                 "reduce the slices first (mfh_split_reduce)");
+    if (b.dy != dy) return MFH_FAIL(ERR_ARG, "the formed dy must be the pass's dy");
+    PartialArgs args;
+    DxArgs d;
+    backward_args(s, b, 1, sums, args, d);
+    args.vec = quad_vec(s, {b.x, b.dy, b.gate, b.residual_grad, b.x_grad, partial});
+    const SplitSource src{partial, static_cast<long long>(s.C) * s.N * s.HW, slices, nullptr, dy};
+    launch_backward_channel<true>(s, args, d, src, stream);
+    return MFH_CHECK_LAUNCH("norm_backward_channel<split>", stream);
 }
 
 }  // namespace mfh

@@ -89,8 +89,8 @@ def batchnorm2d_forward(x, gamma, beta, running_mean, running_var, *, momentum, 
     if split is not None:  # x is a convolution output still in split-K slices: form it here
         if not training or count > SPLIT_FORM_MAX_POSITIONS:
             raise RuntimeError("a deferred convolution output reached a batch norm that cannot form it")
-        partial, slices, bias = split
-        native._call("mfh_bn_forward_split", partial.data_ptr(), slices, native._addr(bias), x.data_ptr(), gamma.data_ptr(),
+        partial, slices, bias, _block = split
+        native._call("mfh_bn_forward_split", partial, slices, native._addr(bias), x.data_ptr(), gamma.data_ptr(),
                      beta.data_ptr(), running_mean.data_ptr(), running_var.data_ptr(), native._addr(residual),
                      y.data_ptr(), mean.data_ptr(), inv_std.data_ptr(), n, c, hw, int(bool(relu)), float(momentum),
                      float(eps), float(var_scale), native._stream())
@@ -118,7 +118,9 @@ def batchnorm2d_backward(x, dy, gamma, mean, inv_std, *, training, x_grad, gamma
     """Write (or add, per ``accumulate``) the requested gradients into x_grad, gamma_grad and beta_grad.
 
     With ``gate`` (the output of a fused ReLU) dy counts only where gate > 0, and that gated dy is
-    also stored (or added, with add_residual) into ``residual_grad``.
+    also stored (or added, with add_residual) into ``residual_grad``. A dy that a convolution's
+    backward left in split-K slices (native.conv2d_backward with defer_dx_positions) is formed and
+    stored first, in the same launch.
     """
     x, dy = _f32(x, "x"), _f32(dy, "dy")
     n, c, hw = _bn_shape(x)
@@ -138,15 +140,24 @@ def batchnorm2d_backward(x, dy, gamma, mean, inv_std, *, training, x_grad, gamma
     elif residual_grad is not None:
         raise ValueError("a residual gradient needs the fused ReLU's output as gate")
     residual_grad = _gradient_buffer(residual_grad, x, "residual_grad")
+    split = native.take_pending_split(dy)
+    if split is not None:  # dy is a convolution's input gradient still in split-K slices: form it here
+        sums = gamma_grad is not None or beta_grad is not None or (training and x_grad is not None)
+        if not sums or n * hw > SPLIT_FORM_MAX_POSITIONS:
+            raise RuntimeError("a deferred convolution input gradient reached a batch norm that cannot form it")
     if x_grad is None and gamma_grad is None and beta_grad is None and residual_grad is None:
         return
     doubles = _bn_workspace_doubles(n, c, hw)
     workspace = native.stream_workspace(doubles, torch.float64)
     add_x, add_gamma, add_beta = (int(bool(a)) for a in accumulate)
-    native._call("mfh_bn_backward", x.data_ptr(), dy.data_ptr(), native._addr(gate), gamma.data_ptr(),
-                 mean.data_ptr(), inv_std.data_ptr(), native._addr(x_grad), native._addr(gamma_grad),
-                 native._addr(beta_grad), native._addr(residual_grad), workspace.data_ptr(), doubles, n, c, hw,
-                 int(bool(training)), add_x, add_gamma, add_beta, int(bool(add_residual)), native._stream())
+    pointers = (x.data_ptr(), dy.data_ptr(), native._addr(gate), gamma.data_ptr(), mean.data_ptr(),
+                inv_std.data_ptr(), native._addr(x_grad), native._addr(gamma_grad), native._addr(beta_grad),
+                native._addr(residual_grad), workspace.data_ptr(), doubles, n, c, hw, int(bool(training)), add_x,
+                add_gamma, add_beta, int(bool(add_residual)), native._stream())
+    if split is not None:
+        native._call("mfh_bn_backward_split", split[0], split[1], *pointers)
+    else:
+        native._call("mfh_bn_backward", *pointers)
 
 
 def _pool_window(x, kernel_size, stride):

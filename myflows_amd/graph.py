@@ -184,6 +184,8 @@ class _Plan:
     forward_steps: tuple    # forward_units with shortcut branches on the side stream: (unit, step kind)
     deferred: tuple         # per forward order (one stream, branches on the side stream): convolution ->
                             # the batch norm, its only consumer and next on its stream, that may form its output
+    deferred_dx: dict       # convolution -> the batch-norm unit, next in the backward order, whose output
+                            # is the convolution's input and has no other consumer: it may form the dX
 
 
 # Kinds of a forward step: a unit on the current stream, the fork of a branch (the side stream waits
@@ -197,6 +199,7 @@ class Graph:
 
     _installed = None  # the plan whose per-node flags are written into the (possibly shared) nodes
     _deferred_installed = None  # (plan, forward order) whose deferred pairs the nodes hold
+    _deferred_dx_installed = None  # the plan whose deferred dX pairs the nodes hold
 
     def __init__(self, target_node, optimize=False, fold_constants=False, fuse_linear=True, fuse_activations=True):
         self._opt_stats = None
@@ -262,7 +265,8 @@ class Graph:
         forward_steps = self._forward_steps(forward_units, groups)
         return _Plan(tuple(needs.items()), frozenset(n for n, need in needs.items() if need), forward_units,
                      backward_units, pre_clear, keep, frozenset(groups), forward_steps,
-                     self._deferred_splits(groups, forward_units, forward_steps))
+                     self._deferred_splits(groups, forward_units, forward_steps),
+                     self._deferred_input_grads(backward_units))
 
     def _deferred_splits(self, groups, forward_units, forward_steps):
         """Plain convolutions (no fused activation) whose only consumer is a batch norm
@@ -295,6 +299,40 @@ class Graph:
         orders = (_next_on_stream((unit, MAIN) for unit in forward_units), _next_on_stream(forward_steps))
         return tuple({conv: bn for conv, bn in pairs.items() if after.get(conv) is unit_of.get(bn, bn)}
                      for after in orders)
+
+    def _deferred_input_grads(self, backward_units):
+        """Convolutions whose input is the output of a batch norm (alone, or the end of a
+        BN(+Add)+ReLU unit) with no other consumer, that unit being the next in the backward order:
+        a training batch norm of few enough positions forms such a convolution's dX from the dX
+        product's split-K slices itself (Conv2D_Op.backward, fused.batchnorm2d_backward). The
+        gradient is then the dX alone (no other consumer adds to it) and nothing runs between the
+        product and the batch norm. A retained input keeps its gradient formed."""
+        from .ops_conv import Conv2D_Op
+        from .ops_norm import BatchNorm2d_Op, BatchNormActivation
+        consumers = {}
+        for node in self.nodes:
+            for parent in node.parents:
+                consumers.setdefault(parent, set()).add(node)
+        pairs = {}
+        for (unit, _), (after, after_output) in zip(backward_units, backward_units[1:]):
+            if not isinstance(unit, Conv2D_Op):
+                continue
+            x_node = unit.parents[0]
+            if (x_node is after_output and consumers.get(x_node) == {unit} and x_node not in self._retained
+                    and x_node is not self.target_node
+                    and (isinstance(after, BatchNormActivation) or isinstance(after, BatchNorm2d_Op))):
+                pairs[unit] = after
+        return pairs
+
+    def _install_deferred_dx(self, plan):
+        """Write this plan's deferred dX pairs into the convolution nodes (which another graph may
+        have set otherwise)."""
+        if Graph._deferred_dx_installed is plan:
+            return
+        for node, _ in plan.needs:
+            if hasattr(node, "_defer_dx"):
+                node._defer_dx = plan.deferred_dx.get(node)
+        Graph._deferred_dx_installed = plan
 
     def _forward_steps(self, forward_units, groups):
         """forward_units with every convolution + batch-norm shortcut (a ResNet downsample: a Conv2D
@@ -439,6 +477,7 @@ class Graph:
             self.target_node.grad = (torch.ones_like(seed) if loss_scale == 1.0
                                      else torch.full_like(seed, loss_scale))
         profiler = self.profiler
+        self._install_deferred_dx(plan)
         served = _prepare_weight_orders((unit for unit, _ in plan.backward_units), "backward")
         overlap = self.overlap_weight_grads and isinstance(seed, torch.Tensor) and seed.is_cuda
         with streams.weight_grad_overlap(overlap):

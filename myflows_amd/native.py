@@ -102,6 +102,7 @@ _SIGNATURES = {
     "mfh_conv_implicit_workspace": ("q", _CONV + "i"),
     "mfh_conv_backward_implicit": ("i", "ppppppppppp" + _CONV + "ifiiipqp"),
     "mfh_conv_backward_implicit_streams": ("i", "ppppppppppp" + _CONV + "ifiiipqqpp"),
+    "mfh_conv_backward_implicit_deferred": ("i", "ppppppppppp" + _CONV + "ifiiipqqPpp"),
     "mfh_pool_forward": ("i", "ppp" + "i" * 10 + "p"),
     "mfh_pool_backward": ("i", "ppp" + "i" * 10 + "p"),
     "mfh_matmul": ("i", "iiipppp" + "iii" + "p"),
@@ -117,6 +118,7 @@ _SIGNATURES = {
     "mfh_bn_forward": ("i", "ppppppppppq" + "iiiii" + "ddd" + "p"),
     "mfh_bn_forward_split": ("i", "pip" + "p" * 9 + "iiii" + "ddd" + "p"),
     "mfh_bn_backward": ("i", "pppppppppppq" + "iii" + "iiiii" + "p"),
+    "mfh_bn_backward_split": ("i", "pi" + "pppppppppppq" + "iii" + "iiiii" + "p"),
     "mfh_bn_relu_pool_supported": ("i", "iiiiiiii"),
     "mfh_bn_relu_pool_forward": ("i", "pppppppppp" + "q" + "iiiiiiii" + "i" + "ddd" + "p"),
     "mfh_bn_relu_pool_backward": ("i", "pppppppppp" + "pq" + "iiiiiiii" + "iiii" + "p"),
@@ -707,8 +709,9 @@ def conv2d_forward(x, weight, bias=None, *, stride=(1, 1), padding=(0, 0), activ
     return y, cols
 
 
-# Convolution outputs whose split-K slices still wait in their stream's workspace (see
-# conv2d_forward_deferred): id(y) -> (y, workspace, slices, bias).
+# Convolution outputs (and input gradients) whose split-K slices still wait in a workspace block
+# (see conv2d_forward_deferred, conv2d_backward's defer_dx_positions):
+# id(y) -> (y, block, slices, bias, offset of the slices in the block in floats).
 _PENDING_SPLITS = {}
 
 
@@ -744,7 +747,7 @@ def conv2d_forward_deferred(x, weight, bias=None, *, stride=(1, 1), padding=(0, 
           y.data_ptr(),
           *g.c_args(), engine, _addr(workspace), floats, ctypes.byref(slices), _stream())
     if slices.value > 1:
-        _PENDING_SPLITS[id(y)] = (y, workspace, slices.value, bias)
+        _PENDING_SPLITS[id(y)] = (y, workspace, slices.value, bias, 0)
     return y
 
 
@@ -756,20 +759,23 @@ def drop_pending_splits():
 
 
 def take_pending_split(y):
-    """(workspace, slices, bias) of a convolution output left unformed by conv2d_forward_deferred, or None;
-    the caller then forms y."""
+    """(address of the slices, slices, bias, block) of a convolution output left unformed by
+    conv2d_forward_deferred (or an input gradient left unformed by conv2d_backward with
+    defer_dx_positions; bias None), else None; the caller then forms y, holding the block (the
+    workspace tensor the slices lie in) until its launch is queued."""
     entry = _PENDING_SPLITS.pop(id(y), None)
     if entry is None:
         return None
     if entry[0] is not y:  # a stale entry of a freed tensor whose id was reused
         return None
-    return entry[1:]
+    _, block, slices, bias, offset = entry
+    return block.data_ptr() + 4 * offset, slices, bias, block
 
 
 def conv2d_backward(x, weight, grad_y, cols, *, stride=(1, 1), padding=(0, 0), need_bias_grad=True,
                     need_input_grad=True, need_weight_grad=True, activation=None, alpha=0.0, output=None,
                     engine="mfma", recompute_cols=False, algorithm=None, weight_flip=None, input_grad=None,
-                    strided_dx="auto", dw_stream=None, hold=None):
+                    strided_dx="auto", dw_stream=None, hold=None, defer_dx_positions=0):
     """(dx, dw, db), None for each gradient not requested; a fused activation gates grad_y through
     output. algorithm "im2col" computes dW from the forward's cols (recomputed from x when
     recompute_cols); "implicit" gathers them from x inside the GEMM. Without an algorithm, a call
@@ -786,7 +792,12 @@ def conv2d_backward(x, weight, grad_y, cols, *, stride=(1, 1), padding=(0, 0), n
     products beside the dX product on the current stream (mfh_conv_backward_implicit_streams); dw
     and db are complete once the current stream has been ordered after dw_stream (stream_wait). The
     tensors are allocated on the current stream, so such a caller also passes a list as hold, which
-    receives every tensor the call reads or writes, and keeps them until that ordering."""
+    receives every tensor the call reads or writes, and keeps them until that ordering.
+    Implicit only: with defer_dx_positions, a stride-1 convolution whose dx is fresh (no input_grad)
+    and has at most that many positions per channel (N * H * W) may return dx unwritten, its dX
+    product's split-K slices left in a workspace block registered for take_pending_split(dx)
+    (mfh_conv_backward_implicit_deferred); the next batch-norm backward of dx
+    (fused.batchnorm2d_backward with dy = dx) must form it. Otherwise dx is complete."""
     engine = _engine_code(engine)
     if algorithm is None and cols is not None and not recompute_cols:
         algorithm = "im2col"
@@ -806,9 +817,12 @@ def conv2d_backward(x, weight, grad_y, cols, *, stride=(1, 1), padding=(0, 0), n
         phases = strided_dx == "phases" or (strided_dx == "auto"
                                             and strided_dx_phases(g.kh, g.kw, g.co, (g.sh, g.sw)))
         return _conv2d_backward_implicit(x, weight, grad_y, g, need_bias_grad, need_input_grad, need_weight_grad,
-                                         act, alpha, output, engine, weight_flip, input_grad, phases, dw_stream, hold)
-    if weight_flip is not None or input_grad is not None or dw_stream is not None or hold is not None:
-        raise ValueError("weight_flip, input_grad, dw_stream and hold apply to the implicit algorithm only")
+                                         act, alpha, output, engine, weight_flip, input_grad, phases, dw_stream, hold,
+                                         defer_dx_positions)
+    if (weight_flip is not None or input_grad is not None or dw_stream is not None or hold is not None
+            or defer_dx_positions):
+        raise ValueError("weight_flip, input_grad, dw_stream, hold and defer_dx_positions apply to the implicit "
+                         "algorithm only")
     if need_weight_grad:
         cols = (conv2d_im2col(x, tuple(weight.shape), stride=stride, padding=padding) if recompute_cols
                 else _device_f32(cols, "cols"))
@@ -844,7 +858,7 @@ def conv2d_backward(x, weight, grad_y, cols, *, stride=(1, 1), padding=(0, 0), n
 
 def _conv2d_backward_implicit(x, weight, grad_y, g, need_bias_grad, need_input_grad, need_weight_grad, act, alpha,
                               output, engine, weight_flip=None, input_grad=None, phases=True, dw_stream=None,
-                              hold=None):
+                              hold=None, defer_dx_positions=0):
     if dw_stream is not None and hold is None:
         raise ValueError("a dW product on another stream needs a hold list for the call's tensors")
     gate = None
@@ -893,16 +907,28 @@ def _conv2d_backward_implicit(x, weight, grad_y, g, need_bias_grad, need_input_g
     pointers = (x.data_ptr(), weight.data_ptr(), grad_y.data_ptr(), _addr(gate), _addr(gated), _addr(dw), _addr(dx),
                 _addr(wflip), _addr(grad_cols), _addr(partial), _addr(db), *g.c_args(), act, alpha, engine, engine,
                 flags)
-    if dw_stream is None:
+    defer = (need_input_grad and input_grad is None and unit_stride and 0 < defer_dx_positions
+             and g.n * g.h * g.w <= defer_dx_positions)
+    if dw_stream is None and not defer:
         workspace, floats = _implicit_workspace(g, *passes)
         _call("mfh_conv_backward_implicit", *pointers, _addr(workspace), floats, _stream())
-    else:  # the dW and dX products run at the same time: one workspace part each
+    else:  # one workspace part each for the dW and dX products (which may run at the same time)
         dw_floats = _implicit_workspace_floats(g, "dw") if need_weight_grad else 0
         dx_floats = _implicit_workspace_floats(g, "dx") if "dx" in passes else 0
         floats = dw_floats + dx_floats
-        workspace = torch.empty(floats, dtype=torch.float32, device="cuda") if floats else None
-        _call("mfh_conv_backward_implicit_streams", *pointers, _addr(workspace), dw_floats, floats, _stream(),
-              dw_stream)
+        if dw_stream is None:  # one stream: the block is this stream's workspace
+            workspace = stream_workspace(floats) if floats else None
+        else:
+            workspace = torch.empty(floats, dtype=torch.float32, device="cuda") if floats else None
+        if defer:
+            slices = ctypes.c_int(1)
+            _call("mfh_conv_backward_implicit_deferred", *pointers, _addr(workspace), dw_floats, floats,
+                  ctypes.byref(slices), _stream(), _stream() if dw_stream is None else dw_stream)
+            if slices.value > 1:
+                _PENDING_SPLITS[id(dx)] = (dx, workspace, slices.value, None, dw_floats)
+        else:
+            _call("mfh_conv_backward_implicit_streams", *pointers, _addr(workspace), dw_floats, floats, _stream(),
+                  dw_stream)
     if hold is not None:
         hold.extend(t for t in (x, weight, grad_y, gate, gated, dw, dx, wflip, grad_cols, partial, db, workspace)
                     if t is not None)

@@ -67,6 +67,8 @@ class Conv2D_Op(GradientOp):
 
     fused_activation = None  # "relu" / "leaky_relu" in the fused subclasses
     _defer_bn = None  # set by a Graph: the training batch norm that is this node's only consumer
+    _defer_dx = None  # set by a Graph: the batch-norm unit after this node in the backward order that
+                      # consumes the gradient of this node's input alone
 
     def __init__(self, x, kernel, stride=1, padding=0, groups=1, dilation=1, bias=None, backend="auto",
                  recompute_im2col=None):
@@ -194,6 +196,11 @@ class Conv2D_Op(GradientOp):
             target = self._grad_target(x_node, x_val) if need_x else None
             if target is not None:  # dX is added to the gradient x already has, in the same pass
                 extra["input_grad"] = target
+            unit = self._defer_dx
+            if need_x and target is None and x_node.grad is None and unit is not None and unit.forms_input_grad():
+                # The batch norm that consumes dX next, and alone, can form it from the dX product's
+                # split-K slices itself: one launch less, the same bits.
+                extra["defer_dx_positions"] = fused.SPLIT_FORM_MAX_POSITIONS
         engine = NATIVE_BACKENDS[self.actual_backend]
         session = streams.active()
         # A product with no dX beside it (a frozen input, such as a network's first convolution)

@@ -44,6 +44,11 @@ class BatchNorm2d_Op(GradientOp):
             training=self.training, unbiased_running_var=self.unbiased_running_var)
         self._stats = (mean, inv_std) if self.requires_grad else None
 
+    def forms_input_grad(self):
+        """Whether the next backward can form its dy from a convolution's split-K dX slices (a
+        training pass that sums over the channels)."""
+        return self._stats is not None and self._training_used
+
     def backward(self):
         x_node, gamma_node, beta_node = self.parents
         buffers = [node.grad_buffer() if node.requires_grad else (None, False) for node in self.parents]
@@ -99,6 +104,11 @@ class BatchNormActivation:
         for node in self.hidden:
             node.value = None
         self._stats = (mean, inv_std, bn.training) if bn.requires_grad else None
+
+    def forms_input_grad(self):
+        """Whether the next backward can form its dy from a convolution's split-K dX slices: the
+        fused route of a training pass whose batch norm needs gradients."""
+        return not self.chained and self._stats is not None and self._stats[2]
 
     def backward(self):
         if self.chained:

@@ -324,3 +324,31 @@ def test_forward_steps_put_downsample_shortcuts_beside_the_main_path():
     finally:
         if torch.cuda.is_available():
             mf.set_device("cuda")
+
+
+def test_deferred_input_gradients_pair_a_convolution_with_the_next_batch_norm_unit_only():
+    """Graph._deferred_input_grads (no device work): in a BasicBlock the second convolution's dX
+    may be formed by the first BN+ReLU unit, the next backward unit and the only consumer of the
+    convolution's input; the first convolution (its input also feeds the residual Add) and a
+    convolution whose input is retained are not paired."""
+    mf.set_device("cpu")
+    try:
+        x = mf.Variable(torch.zeros((1, 8, 4, 4)), requires_grad=False)
+        stem = mf.ReLU(mf.BatchNorm2d(8)(mf.Conv2D(8, 8, 3, padding=1, fuse_activation=False,
+                                                   backend="hip_native")(x)))
+        block = mf.BasicBlock(8, 8, stride=1, conv_backend="hip_native")
+        out = block(stem)
+        graph = mf.Graph(out, optimize=True)
+        plan = graph._plan()
+        pairs = plan.deferred_dx
+        assert len(pairs) == 1
+        (conv, unit), = pairs.items()
+        assert unit.name == "BatchNormReLU" and conv.parents[0] is unit.output
+        position = [u for u, _ in plan.backward_units]
+        assert position.index(unit) == position.index(conv) + 1
+        assert unit.output is not stem  # the block's first unit, not the stem's (which feeds the Add too)
+        graph.retain_grad(unit.output)
+        assert not graph._plan().deferred_dx
+    finally:
+        if torch.cuda.is_available():
+            mf.set_device("cuda")

@@ -657,6 +657,89 @@ def test_single_stream_step_with_deferred_outputs_matches_the_plain_step_where_t
             np.testing.assert_array_equal(a, b)
 
 
+@pytest.mark.parametrize("x_shape,two_streams", [
+    ((64, 256, 8, 10), True),    # layer3 3x3 at batch 64, dW on the weight-gradient stream
+    ((64, 512, 4, 5), True),     # layer4 3x3
+    ((64, 512, 4, 5), False),    # layer4 3x3, one stream (dW and dX parts of one stream workspace)
+], ids=("layer3-streams", "layer4-streams", "layer4-one-stream"))
+def test_batch_norm_backward_forms_a_deferred_input_gradient_bit_for_bit(x_shape, two_streams):
+    """A stride-1 convolution backward whose dX product splits K leaves dx in slices; the next
+    batch-norm backward (BN+ReLU, training) forms dx (FP64 slice sums rounded once) and then its
+    gradients in one launch. dx, x_grad, dgamma, dbeta and the convolution's dW and db equal the
+    plain path's (the product's own slice reduction, then the batch-norm backward) bit for bit."""
+    from myflows_amd import streams
+    print("deferred dx", x_shape, "two streams" if two_streams else "one stream", flush=True)
+    rng = np.random.default_rng(31)
+    n, c, h, w = x_shape
+    # The batch norm's input and output (the convolution's input), and the convolution's kernel.
+    bn_x = gpu(rng.standard_normal(x_shape).astype(np.float32))
+    gamma, beta = gpu(rng.uniform(0.5, 1.5, c).astype(np.float32)), gpu(rng.standard_normal(c).astype(np.float32))
+    stats = (torch.zeros(c, device="cuda"), torch.ones(c, device="cuda"))
+    y, mean, inv_std = fused.batchnorm2d_forward(bn_x, gamma, beta, *stats, momentum=0.1, eps=1e-5, training=True,
+                                                 relu=True)
+    kernel = gpu((rng.standard_normal((c, c, 3, 3)) * (2.0 / (9 * c)) ** 0.5).astype(np.float32))
+    dy = gpu(rng.standard_normal(x_shape).astype(np.float32))
+    conv = dict(stride=(1, 1), padding=(1, 1), algorithm="implicit")
+    results = []
+    for defer in (False, True):
+        hold = [] if two_streams else None
+        side = streams.side_stream(0).cuda_stream if two_streams else None
+        dx, dw, db = native.conv2d_backward(y, kernel, dy, None, dw_stream=side, hold=hold,
+                                            defer_dx_positions=fused.SPLIT_FORM_MAX_POSITIONS if defer else 0, **conv)
+        if defer:
+            assert id(dx) in native._PENDING_SPLITS  # the dX plan splits K: the batch norm forms dx
+        grads = [torch.empty_like(bn_x), torch.empty_like(gamma), torch.empty_like(gamma)]
+        fused.batchnorm2d_backward(bn_x, dx, gamma, mean, inv_std, training=True, x_grad=grads[0],
+                                   gamma_grad=grads[1], beta_grad=grads[2], accumulate=(False, False, False), gate=y)
+        assert id(dx) not in native._PENDING_SPLITS
+        if two_streams:
+            native.stream_wait(native._stream(), side)
+        results.append([host(t) for t in (dx, dw, db, *grads)])
+    for name, a, e in zip(("dx", "dw", "db", "x_grad", "gamma_grad", "beta_grad"), results[1], results[0]):
+        np.testing.assert_array_equal(a, e, err_msg=name)
+
+
+def test_resnet_step_with_deferred_input_gradients_matches_the_plain_step():
+    """ResNet18 at batch 64, 3x120x160 (the bench step), both streams: the Graph lets the batch-norm
+    units of layer3 and layer4 form the split dX of the convolution they feed; one forward and
+    backward with and without that give the same loss, output and gradients bit for bit."""
+    from myflows_amd import ops_conv
+    from tests.test_gpu_model import build_resnet
+    print("deferred dx step", flush=True)
+    formed = []
+    take = native.take_pending_split
+
+    def counting(y):
+        entry = take(y)
+        formed.append(entry is not None)
+        return entry
+
+    runs = []
+    for defer in (True, False):
+        model, graph, out, loss, _, _ = build_resnet(64, 120, 160, optimize=True)
+        graph.forward()
+        graph.backward()  # installs the plan's deferred dX pairs
+        convs = [n for n in graph.nodes if type(n) is ops_conv.Conv2D_Op]
+        assert sum(n._defer_dx is not None for n in convs) == 8  # each block's second convolution
+        graph.forward()
+        if not defer:  # the plan's pairs stay installed, so the next backward keeps these
+            for n in convs:
+                n._defer_dx = None
+        native.take_pending_split = counting
+        try:
+            graph.backward()
+        finally:
+            native.take_pending_split = take
+        assert not native._PENDING_SPLITS
+        runs.append([host(loss.value), host(out.value)] + [host(p.grad) for p in model.params])
+        if defer:
+            print("dX formed by batch norms:", sum(formed), flush=True)
+            assert sum(formed) >= 1  # layer3/layer4 second convolutions whose dX plans split K
+        formed.clear()
+    for a, b in zip(*runs):
+        np.testing.assert_array_equal(a, b)
+
+
 @pytest.mark.parametrize("shape", [(4, 2048, 56, 56), (256, 2048, 7, 7)], ids=str)
 def test_batchnorm_of_a_wide_layer_with_many_positions_against_fp64(shape):
     """C >= 8 * CUs channels with more positions per channel than the one-launch channel kernels
