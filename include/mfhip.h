@@ -295,6 +295,12 @@ MFH_API int mfh_matmul(int variant, int tile, int accumulate, uint64_t a, uint64
 MFH_API int mfh_gemm_tile_count(void);
 MFH_API int mfh_gemm_tile_info(int index, int* values);
 
+/* K groups of a tile: 1, or the number of wave sets (each of (BM/WM) x (BN/WN) waves) that share
+ * the tile's K range in one workgroup, each summing its run of stages, the runs' sums then added
+ * in group order; -1 for an unknown tile. No counterpart in the reference (its tiles run one
+ * thread set per output tile); a catalogue reader names such tiles apart (e.g. "64x64k4"). */
+MFH_API int mfh_gemm_tile_groups(int index);
+
 /* LDS stages a tile's main loop keeps in flight: 2 for every tile (double-buffered operand tiles),
  * or -1 for an unknown tile. Replaces mf_gemm_tile_stages, native_cublas.cpp:1627-1633 (whose
  * 0 meant register double buffering and 2-4 a cp.async pipeline). */

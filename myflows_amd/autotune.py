@@ -5,8 +5,9 @@ per shape under MFHIP_AUTOTUNE_CACHE (default: ``myflows_amd/_gemm_plans``). The
 
 Each measurement writes ``{"identity", "layout", "shape", "candidates", "selected"}``. A file is
 used only when its identity (device name, arch, CU count, HIP runtime, library build) and shape
-match. Every tile adds each output's K terms in the same order, so all unsplit candidates must
-agree bit for bit; a disagreement raises instead of being stored.
+match. Every one-group tile adds each output's K terms in the same order, so all unsplit
+candidates of one K-group count must agree bit for bit; a disagreement raises instead of being
+stored.
 """
 
 from __future__ import annotations
@@ -115,14 +116,14 @@ def measure(layout, m, n, k, repeats=3, rounds=3, seed=197):
             for t, r, s, w in candidates(m, n, k, budget)]
     launch = lambda row: native.gemm(a, b, trans_a=trans_a, trans_b=trans_b, out=out,
                                      plan=(row["tile"], row["requested_slices"]))
-    reference_bits = None
-    for row in rows:  # correctness pass: every unsplit tile must give the same bits
+    reference_bits = {}
+    for row in rows:  # correctness pass: the unsplit tiles of one K-group count must give the same bits
         launch(row)
         if row["slices"] == 1:
-            bits = out.clone()
-            if reference_bits is None:
-                reference_bits = bits
-            elif not torch.equal(bits, reference_bits):
+            bits, groups = out.clone(), native.tile_groups(row["tile"])
+            if groups not in reference_bits:
+                reference_bits[groups] = bits
+            elif not torch.equal(bits, reference_bits[groups]):
                 raise ArithmeticError(f"unsplit tile {row['tile']} changed the summation order of {layout} {m}x{n}x{k}")
     start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     order = random.Random(2201)

@@ -702,6 +702,14 @@ MFH_API int mfh_gemm_tile_info(int index, int* values) {
     return OK;
 }
 
+MFH_API int mfh_gemm_tile_groups(int index) {
+    if (index < 0 || index >= gemm_tile_count()) {
+        MFH_FAIL(ERR_ARG, "unknown GEMM tile");
+        return -1;
+    }
+    return gemm_tile(index).kg;
+}
+
 MFH_API int mfh_gemm_tile_stages(int index) {
     if (index < 0 || index >= gemm_tile_count()) {
         MFH_FAIL(ERR_ARG, "unknown GEMM tile");

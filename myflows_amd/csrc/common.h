@@ -95,6 +95,7 @@ int probe_code_object();
 // ---- gemm.hip ---------------------------------------------------------------------------------
 struct GemmTile {
     int bm, bn, bk, wm, wn;  // block tile, reduction depth per LDS stage, wave tile
+    int kg = 1;              // K groups: sets of (BM/WM) x (BN/WN) waves that share the tile's K range
 };
 // Tile catalogue of the MFMA kernels: block tile BM x BN, stage depth BK, wave tile WM x WN
 // (multiples of 32).
@@ -107,6 +108,7 @@ inline constexpr GemmTile GEMM_TILES[] = {
     {32, 128, 16, 32, 32},   // 5: M <= 32
     {256, 128, 16, 64, 64},  // 6: large outputs, 8 waves
     {128, 256, 16, 64, 64},  // 7: large outputs, 8 waves
+    {64, 64, 16, 32, 32, 2},  // 8: small outputs: two groups of four waves share the K range
 };
 constexpr int GEMM_TILE_COUNT = sizeof(GEMM_TILES) / sizeof(GEMM_TILES[0]);
 constexpr unsigned ALL_TILES = (1u << GEMM_TILE_COUNT) - 1;

@@ -72,6 +72,84 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void gemm_mfma_kernel(G
     store_acc<S>(p, C, acc, m0, n0, wm0, wn0, lane);
 }
 
+// A tile whose K range is shared by KG groups of (BM/WM) x (BN/WN) waves (KG x the waves of
+// gemm_mfma_kernel for the same tile, so that a small output still has several waves per SIMD):
+// group g runs the stages [g * per, (g + 1) * per) of the workgroup's K range (per = the stage
+// count over KG, rounded up; stages past the end read zeros, which add exact zeros, so that every
+// group passes the same barriers) on its own double-buffered LDS stage with its global reads two
+// stages ahead, each output's terms in one FP32 chain; the groups' sums are then added in group
+// order ((g0 + g1) + g2) + ... through LDS, and group 0 writes the tile. Fixed order: bitwise
+// reproducible run to run (a grouped tile sums in another order than the one-group tiles).
+template <int BM, int BN, int BK, int WM, int WN, int KG, bool TA, bool TB, bool VA, bool VB>
+__global__ __launch_bounds__((BM / WM) * (BN / WN) * 64 * KG) void gemm_grouped_kernel(GemmParams p) {
+    using S = MfmaShape<BM, BN, BK, WM, WN, TA, TB>;
+    constexpr int PARTIAL = S::THREADS * 16 * S::TM * S::TN;  // floats of one group's accumulators
+    static_assert((KG - 1) * PARTIAL <= KG * 2 * S::STAGE, "the group sums fit in the stage buffers");
+    __shared__ __attribute__((aligned(16))) float smem[KG * 2 * S::STAGE];
+
+    int tile_m, tile_n, z;
+    tile_of_workgroup(tile_m, tile_n, z);
+    const int group = threadIdx.x / S::THREADS, tid = threadIdx.x % S::THREADS;
+    const int wave = tid / 64, lane = tid % 64;
+    const int wm0 = (wave / S::WGN) * WM, wn0 = (wave % S::WGN) * WN;
+    const int m0 = tile_m * BM, n0 = tile_n * BN;
+    const float* __restrict__ A = p.A + (p.split ? 0 : z * p.a_batch);
+    const float* __restrict__ B = p.B + (p.split ? 0 : z * p.b_batch);
+    float* __restrict__ C = p.C + z * p.c_batch;
+    const int k_begin = p.split ? z * p.k_chunk : 0;
+    const int k_end = p.split ? min(p.K, k_begin + p.k_chunk) : p.K;
+    const int M = p.M, N = p.N;
+    const int per = ((k_end - k_begin + BK - 1) / BK + KG - 1) / KG;  // stages of every group
+    const int g_begin = k_begin + group * per * BK;
+
+    using LoadA = TileLoader<TA ? BK : BM, TA ? BM : BK, S::THREADS, VA>;
+    using LoadB = TileLoader<TB ? BN : BK, TB ? BK : BN, S::THREADS, VB>;
+    LoadA la[2];
+    LoadB lb[2];
+    // Every load is bounded by k_end (reads past it give zeros), the ahead loop's fetches past the
+    // end included.
+    auto fetch = [&](auto slot, int kt) {
+        constexpr int T = decltype(slot)::value;
+        if constexpr (TA) la[T].load(A, p.lda, kt, k_end, m0, M, tid);
+        else la[T].load(A, p.lda, m0, M, kt, k_end, tid);
+        if constexpr (TB) lb[T].load(B, p.ldb, n0, N, kt, k_end, tid);
+        else lb[T].load(B, p.ldb, kt, k_end, n0, N, tid);
+    };
+    auto store = [&](auto slot, float* a_lds, float* b_lds) {
+        constexpr int T = decltype(slot)::value;
+        la[T].template store<S::LDA_S>(a_lds, tid);
+        lb[T].template store<S::LDB_S>(b_lds, tid);
+    };
+
+    v16f acc[S::TM][S::TN];
+    zero_acc<S>(acc);
+    mfma_k_loop_ahead<S, STAGE_PLAIN>(smem + group * 2 * S::STAGE, g_begin, g_begin + per * BK, fetch, store, acc,
+                                      wm0, wn0, lane);
+    // The loop ends with a barrier: every group is done with the stage buffers.
+    if (group > 0) {
+        float* mine = smem + (group - 1) * PARTIAL + tid;
+#pragma unroll
+        for (int i = 0; i < S::TM; ++i)
+#pragma unroll
+            for (int j = 0; j < S::TN; ++j)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) mine[((i * S::TN + j) * 16 + r) * S::THREADS] = acc[i][j][r];
+    }
+    __syncthreads();
+    if (group > 0) return;
+#pragma unroll
+    for (int g = 1; g < KG; ++g) {
+        const float* theirs = smem + (g - 1) * PARTIAL + tid;
+#pragma unroll
+        for (int i = 0; i < S::TM; ++i)
+#pragma unroll
+            for (int j = 0; j < S::TN; ++j)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) acc[i][j][r] += theirs[((i * S::TN + j) * 16 + r) * S::THREADS];
+    }
+    store_acc<S>(p, C, acc, m0, n0, wm0, wn0, lane);
+}
+
 // C = act((float)(((0.0 + p0) + p1) + ... + p[S-1]) [+ bias]) with the FP64 sum in slice order,
 // the bias (per column or per row) added in FP32 after the rounding, stored dense (row * ldc + col)
 // or segmented like the GEMM's own epilogue (C = C + that when p.accumulate).
@@ -215,7 +293,9 @@ constexpr int VARIANTS = 16;  // 4 layouts (NN, NT, TN, TT) x float4 loads of A 
 
 template <int T, bool TA, bool TB, bool VA, bool VB>
 constexpr GemmFn kernel_of() {
-    return gemm_mfma_kernel<TILES[T].bm, TILES[T].bn, TILES[T].bk, TILES[T].wm, TILES[T].wn, TA, TB, VA, VB>;
+    constexpr GemmTile t = TILES[T];
+    if constexpr (t.kg > 1) return gemm_grouped_kernel<t.bm, t.bn, t.bk, t.wm, t.wn, t.kg, TA, TB, VA, VB>;
+    else return gemm_mfma_kernel<t.bm, t.bn, t.bk, t.wm, t.wn, TA, TB, VA, VB>;
 }
 
 template <int T, bool TA, bool TB>
@@ -245,16 +325,17 @@ struct KernelTable {
         fill_row<5>(fn[5]);
         fill_row<6>(fn[6]);
         fill_row<7>(fn[7]);
+        fill_row<8>(fn[8]);
     }
 };
-static_assert(NUM_TILES == 8, "KernelTable lists every tile");
+static_assert(NUM_TILES == 9, "KernelTable lists every tile");
 
 const KernelTable& kernel_table() {
     static const KernelTable table;
     return table;
 }
 
-int threads_of(const GemmTile& t) { return (t.bm / t.wm) * (t.bn / t.wn) * 64; }
+int threads_of(const GemmTile& t) { return (t.bm / t.wm) * (t.bn / t.wn) * 64 * t.kg; }
 
 bool aligned16(const void* p) { return (reinterpret_cast<std::uintptr_t>(p) & 15) == 0; }
 
@@ -266,7 +347,7 @@ struct TileCost {
     int per_cu;
 };
 constexpr TileCost COST[NUM_TILES] = {
-    {1.063, 3}, {0.95, 3}, {0.85, 4}, {0.935, 6}, {0.60, 6}, {0.60, 6}, {1.02, 2}, {1.02, 2},
+    {1.063, 3}, {0.95, 3}, {0.85, 4}, {0.935, 6}, {0.60, 6}, {0.60, 6}, {1.02, 2}, {1.02, 2}, {0.93, 3},
 };
 constexpr double HIDING_HALF = 0.75;  // resident waves per SIMD at which half the latency is hidden
 constexpr int SPLITS[] = {1, 2, 3, 4, 6, 8, 12, 16, 24, 32, 48, 64, 96, 128};
@@ -282,7 +363,7 @@ double plan_cost(int tile, std::int64_t workgroups, int chunk, std::int64_t M, s
     const int cus = std::max(1, device_cu_count());
     const std::int64_t per_cu = (workgroups + cus - 1) / cus;
     const double waves_per_simd = static_cast<double>(std::min<std::int64_t>(per_cu, COST[tile].per_cu)) *
-                                  ((t.bm / t.wm) * (t.bn / t.wn)) / 4.0;
+                                  ((t.bm / t.wm) * (t.bn / t.wn) * t.kg) / 4.0;
     const double hiding = waves_per_simd / (waves_per_simd + HIDING_HALF);
     double cost = static_cast<double>(per_cu) * t.bm * t.bn * chunk / (COST[tile].efficiency * hiding);
     if (slices > 1) cost += 0.064 * 4.0 * (2.0 * slices + 1.0) * static_cast<double>(M) * N + 1.5e6;

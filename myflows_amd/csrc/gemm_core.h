@@ -20,7 +20,8 @@
 // register r. Which k a lane half (l / 32) feeds at each step is free as long as A and B agree, so
 // half h consumes k = h * BK/2 + s for s = 0 .. BK/2 - 1: a k-contiguous operand then reads four
 // consecutive k of its row with one 16-byte LDS load. Every tile uses the same BK and the same k
-// mapping, so an unsplit product adds each output's K terms in the same order whatever the tile.
+// mapping, so an unsplit product adds each output's K terms in the same order whatever the tile
+// (of one K group: a K-grouped tile, gemm.hip, adds its groups' runs of stages afterwards).
 #pragma once
 
 #include <type_traits>

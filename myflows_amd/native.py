@@ -109,6 +109,7 @@ _SIGNATURES = {
     "mfh_gemm_tile_count": ("i", ""),
     "mfh_gemm_tile_info": ("i", "iP"),
     "mfh_gemm_tile_stages": ("i", "i"),
+    "mfh_gemm_tile_groups": ("i", "i"),
     "mfh_gemm_plan": ("i", "iiiPP"),
     "mfh_gemm_workspace": ("q", "iii"),
     "mfh_split_reduce": ("i", "pp" + "iiiii" + "p"),
@@ -389,17 +390,25 @@ def _conv_geometry(x_shape, weight_shape, stride, padding):
 # ---------------------------------------------------------------------------------------------
 @lru_cache(maxsize=1)
 def tile_catalog():
-    """Tile name "BMxBN" -> (index, BM, BN, WM, WN, BK) of the MFMA engine, in native order."""
+    """Tile name -> (index, BM, BN, WM, WN, BK) of the MFMA engine, in native order. A tile is named
+    "BMxBN", or "BMxBNkG" when G groups of waves share its K range (mfh_gemm_tile_groups)."""
     lib = load_library()
     catalog = {}
     for index in range(lib.mfh_gemm_tile_count()):
         values = (ctypes.c_int * 5)()
         _raise_for(lib.mfh_gemm_tile_info(index, values), lib)
-        if lib.mfh_gemm_tile_stages(index) < 0:
+        groups = lib.mfh_gemm_tile_groups(index)
+        if lib.mfh_gemm_tile_stages(index) < 0 or groups < 1:
             _raise_for(2, lib)
         bm, bn, wm, wn, bk = values
-        catalog[f"{bm}x{bn}"] = (index, bm, bn, wm, wn, bk)
+        catalog[f"{bm}x{bn}" + (f"k{groups}" if groups > 1 else "")] = (index, bm, bn, wm, wn, bk)
     return catalog
+
+
+def tile_groups(tile):
+    """K groups of a tile of tile_catalog(): 1, or the wave sets that share its K range (each sums
+    its run of stages, the runs then added in group order: another order than the one-group tiles)."""
+    return load_library().mfh_gemm_tile_groups(tile_catalog()[tile][0])
 
 
 @lru_cache(maxsize=2048)

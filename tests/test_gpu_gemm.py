@@ -146,7 +146,8 @@ def test_split_reduce_is_the_fp64_loop_bit_for_bit(slices):
         np.testing.assert_array_equal(got.view(np.uint32)[~nan], expected.view(np.uint32)[~nan])
 
 
-@pytest.mark.parametrize("plan", (("128x128", 5), ("64x128", 11), ("64x64", 2), ("256x64", 3)), ids=str)
+@pytest.mark.parametrize("plan", (("128x128", 5), ("64x128", 11), ("64x64", 2), ("256x64", 3), ("64x64k2", 4)),
+                         ids=str)
 def test_split_gemm_is_the_fp64_reduction_of_its_chunks(plan):
     tile, requested = plan
     rng = np.random.default_rng(32)
@@ -240,12 +241,38 @@ def test_teaching_kernel_bias_and_argument_checks():
 
 @pytest.mark.parametrize("layout", LAYOUTS)
 def test_every_unsplit_tile_adds_in_the_same_order(layout):
-    """All tiles use the same stage depth and k mapping, so one-pass products are bit-identical
-    whatever the tile (and the XCD tile order)."""
+    """All one-group tiles use the same stage depth and k mapping, so one-pass products are
+    bit-identical whatever the tile (and the XCD tile order)."""
     trans_a, trans_b = LAYOUTS[layout]
     rng = np.random.default_rng(6)
     a, b, _, _ = operands(rng, 300, 260, 1000, trans_a, trans_b)
-    results = [native.gemm(gpu(a), gpu(b), trans_a=trans_a, trans_b=trans_b, plan=(tile, 1))
-               for tile in native.tile_catalog()]
+    tiles = [tile for tile in native.tile_catalog() if native.tile_groups(tile) == 1]
+    assert len(tiles) == 8
+    results = [native.gemm(gpu(a), gpu(b), trans_a=trans_a, trans_b=trans_b, plan=(tile, 1)) for tile in tiles]
     for other in results[1:]:
         assert torch.equal(results[0], other)
+
+
+@pytest.mark.parametrize("layout", LAYOUTS)
+@pytest.mark.parametrize("m,n,k", ((300, 260, 1000), (64, 64, 16), (130, 70, 37), (1024, 1024, 1024)), ids=str)
+def test_k_grouped_tile_is_the_group_order_sum_of_one_group_products(layout, m, n, k):
+    """The 64x64k2 tile splits each workgroup's stages into two runs (the first ceil(stages / 2)
+    stages, then the rest) and adds the runs' FP32 sums in order: bit for bit the one-group tile's
+    products over the two K ranges added in float32 (with a bias, added after the sum)."""
+    trans_a, trans_b = LAYOUTS[layout]
+    rng = np.random.default_rng(8)
+    a, b, _, _ = operands(rng, m, n, k, trans_a, trans_b)
+    a, b = gpu(a), gpu(b)
+    bias = gpu(rng.standard_normal(n).astype(np.float32))
+    bk = native.tile_catalog()["64x64k2"][-1]
+    assert native.tile_groups("64x64k2") == 2
+    split = -(-(-(-k // bk)) // 2) * bk  # the first run: ceil(stages / 2) stages
+    cut = lambda x, lo, hi, k_first: x[lo:hi] if k_first else x[:, lo:hi]
+    parts = [native.gemm(cut(a, lo, hi, trans_a).contiguous(), cut(b, lo, hi, not trans_b).contiguous(),
+                         trans_a=trans_a, trans_b=trans_b, plan=("64x64", 1)) for lo, hi in ((0, split), (split, k))
+             if lo < hi]
+    expected = parts[0] + parts[1] if len(parts) == 2 else parts[0]
+    got = native.gemm(a, b, trans_a=trans_a, trans_b=trans_b, plan=("64x64k2", 1))
+    assert torch.equal(got, expected)
+    got = native.gemm(a, b, bias, trans_a=trans_a, trans_b=trans_b, plan=("64x64k2", 1))
+    assert torch.equal(got, expected + bias)
