@@ -270,8 +270,9 @@ MFH_API int mfh_conv_backward_implicit_deferred(uint64_t x, uint64_t weight, uin
 /* ---- max pooling ---------------------------------------------------------------------------- */
 
 /* Max-pool without padding (the caller pads with -inf): y = window max in (kh, kw) order with the
- * first maximum winning ties and NaN taking over; argmax (int32) = flat index into x.
- * Replaces mf_pool_forward, native_cublas.cpp:1534-1547. */
+ * first maximum winning ties and NaN taking over; argmax (int32) = flat index into x, or 0 when no
+ * backward will read it (an inference pass), in which case it is not written.
+ * Replaces mf_pool_forward, native_cublas.cpp:1534-1547 (which always writes its mask). */
 MFH_API int mfh_pool_forward(uint64_t x, uint64_t y, uint64_t argmax, int N, int C, int H, int W, int OH, int OW,
                              int KH, int KW, int SH, int SW, uint64_t stream);
 

@@ -639,7 +639,7 @@ MFH_API int mfh_pool_forward(std::uint64_t x, std::uint64_t y, std::uint64_t arg
                              int OH, int OW, int KH, int KW, int SH, int SW, std::uint64_t stream) {
     MFH_TRY(require_ready());
     MFH_TRY(validate_pool(N, C, H, W, OH, OW, KH, KW, SH, SW));
-    MFH_REQUIRE(x && y && argmax, "pool forward received a null buffer");
+    MFH_REQUIRE(x && y, "pool forward received a null buffer");  // argmax is optional
     return launch_pool_forward(as_ptr<const float>(x), as_ptr<float>(y), as_ptr<int>(argmax), N, C, H, W, OH, OW, KH,
                                KW, SH, SW, as_stream(stream));
 }

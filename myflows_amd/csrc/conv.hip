@@ -253,7 +253,8 @@ __global__ __launch_bounds__(256) void add_bias_kernel(float* __restrict__ rows,
 }
 
 // Window maximum in (kh, kw) row-major order with a strict '>' (the first maximum wins ties); a NaN
-// takes over, so any NaN in the window gives a NaN output. argmax is the flat index into x.
+// takes over, so any NaN in the window gives a NaN output. argmax (optional: null when no backward
+// will read it) is the flat index into x.
 __global__ __launch_bounds__(256) void pool_forward_kernel(const float* __restrict__ x, float* __restrict__ y,
                                                            int* __restrict__ argmax, int total, FastDiv div_ow,
                                                            FastDiv div_oh, int H, int W, int KH, int KW, int SH,
@@ -277,7 +278,7 @@ __global__ __launch_bounds__(256) void pool_forward_kernel(const float* __restri
         }
     }
     y[idx] = value;
-    argmax[idx] = best;
+    if (argmax) argmax[idx] = best;
 }
 
 // dx[i] = sum of dy over the windows (visited in increasing oh, ow order) whose argmax is i.
@@ -472,7 +473,7 @@ __global__ __launch_bounds__(256) void pool_forward_plane_kernel(const float* __
         const float value = window_max(tile, first, W, KH, KW, best);
         const long long out = static_cast<long long>(first_plane) * ohw + o;
         __builtin_nontemporal_store(value, y + out);
-        __builtin_nontemporal_store(static_cast<int>(base + best), argmax + out);
+        if (argmax) __builtin_nontemporal_store(static_cast<int>(base + best), argmax + out);
     }
 }
 

@@ -153,7 +153,18 @@ def apply_graph_optimizations(root, *, mode="train", fold_constants=True, fuse_l
         root, stats["bn_folds"] = fold_bn_into_conv(root)
         if fuse_activations:
             root, stats["conv_add_act_fusions"] = fuse_conv_add_relu(root)
+        mark_inference_pools(root)
     return root, stats
+
+
+def mark_inference_pools(root):
+    """Max-pools of an inference graph (batch norms folded) do not store their window indices: no
+    backward reads them (MaxPool2d_Op.backward then raises)."""
+    from .ops_conv import MaxPool2d_Op
+
+    for node in topological_order(root):
+        if isinstance(node, MaxPool2d_Op):
+            node.inference = True
 
 
 def fuse_conv_add_relu(root):

@@ -962,9 +962,10 @@ class NativePoolContext:
         return (n, c, h, w, self.output_shape[2], self.output_shape[3], *self.kernel_size, *self.stride)
 
 
-def maxpool2d_forward(x, *, kernel_size=(2, 2), stride=(2, 2)):
+def maxpool2d_forward(x, *, kernel_size=(2, 2), stride=(2, 2), with_argmax=True):
     """(y, context) of a max-pool without padding: window maximum (first index wins ties, NaN wins)
-    and its flat int32 index into x."""
+    and its flat int32 index into x. Without with_argmax (a pass no backward follows) the index is
+    not written and the context cannot take a backward."""
     x = _device_f32(x, "x")
     if x.ndim != 4:
         raise ValueError("x must be an NCHW tensor")
@@ -975,9 +976,9 @@ def maxpool2d_forward(x, *, kernel_size=(2, 2), stride=(2, 2)):
         raise ValueError("the pooling window does not fit in the input")
     _within_int32(input=n * c * h * w)
     y = torch.empty((n, c, oh, ow), dtype=torch.float32, device=x.device)
-    argmax = torch.empty((n, c, oh, ow), dtype=torch.int32, device=x.device)
+    argmax = torch.empty((n, c, oh, ow), dtype=torch.int32, device=x.device) if with_argmax else None
     context = NativePoolContext((n, c, h, w), (n, c, oh, ow), kernel, step, argmax, x.device.index)
-    _call("mfh_pool_forward", x.data_ptr(), y.data_ptr(), argmax.data_ptr(), *context.c_args(), _stream())
+    _call("mfh_pool_forward", x.data_ptr(), y.data_ptr(), _addr(argmax), *context.c_args(), _stream())
     return y, context
 
 
@@ -985,6 +986,8 @@ def maxpool2d_backward(grad_y, context):
     """dx: each dy goes to its window's argmax; overlapping windows add in (oh, ow) order."""
     if not isinstance(context, NativePoolContext) or context.device_id != torch.cuda.current_device():
         raise ValueError("context must come from maxpool2d_forward on the current device")
+    if context.argmax is None:
+        raise ValueError("the forward ran without its argmax (with_argmax=False): no backward")
     grad_y = _device_f32(grad_y, "grad_y")
     if tuple(grad_y.shape) != tuple(context.output_shape):
         raise ValueError("grad_y does not have the pooled output's shape")

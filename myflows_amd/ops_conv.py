@@ -339,6 +339,8 @@ class MaxPool2d_Op(GradientOp):
     """Max pooling. ``padding`` pads with -inf (as torch.nn.MaxPool2d); the native kernels then see an
     unpadded input and the input gradient is cropped back."""
 
+    inference = False  # set by the inference rewrite: the window indices are not stored
+
     def __init__(self, x, kernel_size=2, stride=2, backend="auto", padding=0):
         super().__init__(x)
         self.backend = _backend_name(backend)
@@ -352,12 +354,19 @@ class MaxPool2d_Op(GradientOp):
         ph, pw = self.padding
         if ph or pw:
             x_val = torch.nn.functional.pad(x_val, (pw, pw, ph, ph), value=float("-inf"))
-        self.value, context = native.maxpool2d_forward(x_val, kernel_size=self.kernel_size, stride=self.stride)
-        self._context = context if self.requires_grad else None
+        # A pass no backward follows (no gradient needed, or an inference graph) does not store the
+        # window indices.
+        keep = self.requires_grad and not self.inference
+        self.value, context = native.maxpool2d_forward(x_val, kernel_size=self.kernel_size, stride=self.stride,
+                                                       with_argmax=keep)
+        self._context = context if keep else None
 
     def backward(self):
         if not hasattr(self, "actual_backend"):
             raise RuntimeError("forward must run before backward")
+        if self.inference:
+            raise RuntimeError("MaxPool2d_Op of an inference graph (apply_graph_optimizations(mode='inference')) "
+                               "keeps no window indices and has no backward")
         _resolve_backend(self.actual_backend, self.grad, self.parents[0].value)
         dx = native.maxpool2d_backward(self.grad, self._context)
         ph, pw = self.padding

@@ -68,3 +68,44 @@ def test_pool_rejects_bad_calls():
         native.maxpool2d_backward(torch.zeros((1, 1, 3, 3), device="cuda"), ctx)
     with pytest.raises(ValueError):
         native.maxpool2d_backward(y, object())
+
+
+@pytest.mark.parametrize("shape,kernel,stride", (((4, 8, 60, 80), (3, 3), (2, 2)), ((3, 5, 13, 16), (2, 2), (2, 2)),
+                                                 ((2, 3, 9, 9), (3, 3), (1, 1))), ids=str)
+def test_pool_forward_without_indices_gives_the_same_values_and_no_backward(shape, kernel, stride):
+    """A pass no backward follows (with_argmax=False: the inference graph's max-pools) writes the same
+    window maxima and no indices; its context refuses a backward."""
+    print("pool without indices", shape, kernel, stride, flush=True)
+    x = gpu(np.random.default_rng(9).integers(-3, 4, size=shape).astype(np.float32))
+    y, ctx = native.maxpool2d_forward(x, kernel_size=kernel, stride=stride)
+    y_plain, ctx_plain = native.maxpool2d_forward(x, kernel_size=kernel, stride=stride, with_argmax=False)
+    assert ctx_plain.argmax is None and ctx.argmax is not None
+    np.testing.assert_array_equal(host(y_plain), host(y))
+    with pytest.raises(ValueError):
+        native.maxpool2d_backward(torch.ones_like(y_plain), ctx_plain)
+
+
+def test_inference_graph_pools_keep_no_indices():
+    """apply_graph_optimizations(mode="inference") marks the max-pools: they store no window indices
+    and refuse a backward, while the pooled values are the training graph's."""
+    print("inference graph pool", flush=True)
+    x = mf.Variable(gpu(np.random.default_rng(11).standard_normal((2, 3, 16, 16)).astype(np.float32)),
+                    requires_grad=False)
+    conv = mf.Conv2D(3, 4, 3, padding=1, fuse_activation=False, backend="hip_native")
+    bn = mf.BatchNorm2d(4)
+    bn.eval()
+    out = mf.MaxPool2d(3, 2, backend="hip_native")(mf.ReLU(bn(conv(x))))
+    plain = mf.Graph(out)
+    plain.forward()
+    expected = host(out.value)
+    root, stats = mf.apply_graph_optimizations(out, mode="inference", fold_constants=False)
+    assert stats["bn_folds"] == 1
+    pool = root if isinstance(root, mf.MaxPool2d_Op) else next(
+        n for n in mf.Graph(root).nodes if isinstance(n, mf.MaxPool2d_Op))
+    assert pool.inference
+    mf.Graph(root, optimize=True).forward()
+    assert pool._context is None
+    np.testing.assert_allclose(host(pool.value), expected, rtol=1e-5, atol=1e-5)
+    pool.grad = torch.ones_like(pool.value)
+    with pytest.raises(RuntimeError):
+        pool.backward()
