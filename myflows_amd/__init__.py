@@ -12,8 +12,8 @@ from .device import cuda_available, get_device, set_device
 from .fusion import apply_graph_optimizations
 from .graph import GradientOp, Graph, Node, Variable
 from .init import make_initializer
-from .layers import Conv2D, Dense, Flatten, Layer, MaxPool2d
-from .ops_basic import LINEAR_BACKENDS, Add, LeakyReLU, Linear, MSELoss, ReLU
+from .layers import Conv2D, Dense, Dropout, Flatten, Layer, MaxPool2d
+from .ops_basic import LINEAR_BACKENDS, Add, ChannelNormalize_Op, Dropout_Op, LeakyReLU, Linear, MSELoss, ReLU
 from .ops_conv import (BACKENDS, NATIVE_BACKENDS, Conv2D_AddReLU_Op, Conv2D_LeakyReLU_Op, Conv2D_Op, Conv2D_ReLU_Op,
                        Flatten_Op, MaxPool2d_Op)
 from .ops_norm import BatchNorm2d_Op, BatchNormActivation, BatchNormReLUPool, GlobalAvgPool2d_Op
@@ -22,7 +22,7 @@ from .resnet import BasicBlock, BatchNorm2d, GlobalAvgPool2d, ResNet18
 
 __all__ = [
     "Adam", "Add", "BACKENDS", "BasicBlock", "BatchNorm2d", "BatchNorm2d_Op", "BatchNormActivation",
-    "BatchNormReLUPool", "CapturedStep", "Conv2D",
+    "BatchNormReLUPool", "CapturedStep", "ChannelNormalize_Op", "Conv2D", "Dropout", "Dropout_Op",
     "Conv2D_AddReLU_Op", "Conv2D_LeakyReLU_Op", "Conv2D_Op", "Conv2D_ReLU_Op", "Dense", "Flatten", "Flatten_Op",
     "GlobalAvgPool2d", "GlobalAvgPool2d_Op", "GradientOp", "Graph", "LINEAR_BACKENDS", "Layer", "LeakyReLU", "Linear", "MBGD",
     "MSELoss", "MaxPool2d", "MaxPool2d_Op", "NATIVE_BACKENDS", "Node", "Optimizer", "ParameterGroups",

@@ -1,17 +1,19 @@
-"""Layers with the reference's constructor arguments (``layers/layer.py:36-383``): ``Dense``,
+"""Layers with the reference's constructor arguments (``layers/layer.py:36-425``): ``Dense``,
 ``Conv2D``, ``MaxPool2d`` and ``Flatten``, each taking ``backend=`` ("hip_native", or "auto", which
-is hip_native on the GPU). Parameters are drawn by the seeded initialiser in float64 and cast to
+is hip_native on the GPU), and ``Dropout``. Parameters are drawn by the seeded initialiser in float64 and cast to
 float32 on the active device, so a seeded model holds the reference model's weights.
 """
 
 from __future__ import annotations
+
+import weakref
 
 import torch
 
 from .device import asarray
 from .graph import Variable
 from .init import make_initializer
-from .ops_basic import Linear, ReLU, _linear_backend
+from .ops_basic import Dropout_Op, Linear, ReLU, _linear_backend
 from .ops_conv import Conv2D_Op, Conv2D_ReLU_Op, Flatten_Op, MaxPool2d_Op, _backend_name, _int_pair
 
 
@@ -104,3 +106,30 @@ class MaxPool2d(Layer):
 class Flatten(Layer):
     def forward(self, input_node):
         return Flatten_Op(input_node)
+
+
+class Dropout(Layer):
+    """Inverted dropout (Dropout_Op): active in train mode, the identity in eval mode; ``train()`` /
+    ``eval()`` switch every operator the layer has built. The reference's ``layers/layer.py:391-416``."""
+
+    def __init__(self, p=0.5, seed=None, name=None):
+        super().__init__(name=name)
+        self.p = float(p)
+        if self.p < 0.0 or self.p >= 1.0:
+            raise ValueError("dropout p must be in [0, 1)")
+        self.seed = seed
+        self.training = True
+        self._built = weakref.WeakSet()
+
+    def forward(self, input_node):
+        op = Dropout_Op(input_node, p=self.p, training=self.training, seed=self.seed, name=self.name)
+        self._built.add(op)
+        return op
+
+    def train(self, mode=True):
+        self.training = bool(mode)
+        for op in self._built:
+            op.training = self.training
+
+    def eval(self):
+        self.train(False)

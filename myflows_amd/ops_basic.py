@@ -1,8 +1,10 @@
-"""Add, the fused Linear operator (y = x W + b), ReLU / LeakyReLU and MSELoss.
+"""Add, the fused Linear operator (y = x W + b), ReLU / LeakyReLU, MSELoss, the input channel
+normalisation and dropout.
 
 Operator API of the reference's ``ops/basic.py`` (``Add`` :5-35, ``Linear`` :76-164),
-``ops/activation.py`` (``ReLU`` :43-52, ``LeakyReLU`` :67-80) and ``ops/loss.py`` (``MSELoss``
-:94-113).
+``ops/activation.py`` (``ReLU`` :43-52, ``LeakyReLU`` :67-80), ``ops/loss.py`` (``MSELoss``
+:94-113), ``ops/pooling.py`` (``ChannelNormalize_Op`` :65-87) and ``ops/dropout.py``
+(``Dropout_Op`` :12-40); the last two are device tensor arithmetic, off the kernel path.
 
 * ``Linear`` on ``hip_native`` runs its three GEMMs on the MFMA engine: the forward with the bias
   in the epilogue, dX = g W^T and dW = x^T g reading the transposed operands in place;
@@ -17,6 +19,7 @@ Operator API of the reference's ``ops/basic.py`` (``Add`` :5-35, ``Linear`` :76-
 
 from __future__ import annotations
 
+import numpy as np
 import torch
 
 from . import fused, native
@@ -177,3 +180,72 @@ class MSELoss(GradientOp):
             return
         count = max(y_pred.value.numel(), 1)
         y_pred.accumulate_grad(self.grad * (2.0 * (y_pred.value - y_true.value) / count), owned=True)
+
+
+# ImageNet channel statistics of [0, 1] RGB inputs (torchvision's pretrained-weight convention).
+IMAGENET_MEAN = (0.485, 0.456, 0.406)
+IMAGENET_STD = (0.229, 0.224, 0.225)
+
+
+class ChannelNormalize_Op(GradientOp):
+    """y = (x - mean[c]) / std[c] over the channels of an NCHW tensor, in x's dtype (device tensor
+    arithmetic); the gradient is dy / std[c]. The reference's ``ops/pooling.py:65-87``."""
+
+    def __init__(self, x, mean=IMAGENET_MEAN, std=IMAGENET_STD, name=None):
+        super().__init__(x, name=name)
+        self.mean = tuple(float(v) for v in mean)
+        self.std = tuple(float(v) for v in std)
+        if len(self.mean) != len(self.std):
+            raise ValueError("mean and std must have one value per channel")
+        if any(v <= 0 for v in self.std):
+            raise ValueError("std must be positive")
+
+    def _channel(self, values, like):
+        return torch.tensor(values, dtype=like.dtype, device=like.device).reshape(1, -1, 1, 1)
+
+    def forward(self, x_val):
+        if x_val.ndim != 4 or x_val.shape[1] != len(self.mean):
+            raise ValueError(f"expected an NCHW tensor of {len(self.mean)} channels, got shape {tuple(x_val.shape)}")
+        self.value = (x_val - self._channel(self.mean, x_val)) / self._channel(self.std, x_val)
+
+    def backward(self):
+        x_node = self.parents[0]
+        if not getattr(x_node, "requires_grad", True):
+            return
+        x_node.accumulate_grad(self.grad / self._channel(self.std, self.grad), owned=True)
+
+
+class Dropout_Op(GradientOp):
+    """Inverted dropout: in training, y = x * mask with mask = (u < 1 - p) / (1 - p) in x's dtype,
+    u uniform on [0, 1) drawn per element by NumPy's generator from ``seed`` (the reference's masks
+    for a seed), or by torch's on x's device without one; identity when not training or p = 0.
+    The reference's ``ops/dropout.py:12-40``."""
+
+    def __init__(self, x, p=0.5, training=True, seed=None, name=None):
+        self.p = float(p)
+        if self.p < 0.0 or self.p >= 1.0:
+            raise ValueError("dropout p must be in [0, 1)")
+        self.training = bool(training)
+        self.seed = seed
+        self._rng = np.random.default_rng(int(seed)) if seed is not None else None
+        self._mask = None
+        super().__init__(x, name=name)
+
+    def _uniform(self, like):
+        if self._rng is not None:
+            return torch.as_tensor(self._rng.random(tuple(like.shape)), device=like.device)
+        return torch.rand(like.shape, dtype=torch.float64, device=like.device)
+
+    def forward(self, x):
+        if not self.training or self.p == 0.0:
+            self._mask = torch.ones_like(x) if self.requires_grad else None
+            self.value = x
+            return
+        keep = 1.0 - self.p
+        self._mask = (self._uniform(x) < keep).to(x.dtype) / keep
+        self.value = x * self._mask
+        if not self.requires_grad:
+            self._mask = None
+
+    def backward(self):
+        self.parents[0].accumulate_grad(self.grad * self._mask, owned=True)

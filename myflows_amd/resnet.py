@@ -1,6 +1,9 @@
-"""ResNet18 on the hip_native backend (``layers/resnet.py:32-360`` of the reference, the default
-``compat="myflows"`` form: convolutions with bias, biased running variance, stem max-pool 3x3/2
-without padding).
+"""ResNet18 on the hip_native backend (``layers/resnet.py:32-360`` of the reference). Two structures,
+as there: ``compat="myflows"`` (the default: convolutions with bias, biased running variance, stem
+max-pool 3x3/2 without padding) and ``compat="torchvision"`` (torchvision's resnet18 layer for
+layer: convolutions without bias, running variance from the unbiased batch variance, stem max-pool
+with padding 1), with an optional in-graph ImageNet input normalisation and dropout before the
+head.
 
 ``ResNet18(conv_backend="hip_native")`` runs every convolution and the stem max-pool on libmfhip, and
 its fc ``Linear`` on the MFMA engine too (``auto`` is that engine on the GPU; the reference's fc used
@@ -18,8 +21,8 @@ import torch
 from .device import torch_device
 from .graph import Variable
 from .init import make_initializer
-from .layers import Conv2D, Layer
-from .ops_basic import Add, Linear, ReLU
+from .layers import Conv2D, Dropout, Layer
+from .ops_basic import Add, ChannelNormalize_Op, Linear, ReLU
 from .ops_conv import MaxPool2d_Op, _backend_name
 from .ops_norm import BatchNorm2d_Op, GlobalAvgPool2d_Op
 
@@ -72,9 +75,12 @@ class GlobalAvgPool2d(Layer):
         return GlobalAvgPool2d_Op(input_node)
 
 
-def _conv(in_c, out_c, size, stride, initializer, backend):
+COMPAT_MODES = ("myflows", "torchvision")
+
+
+def _conv(in_c, out_c, size, stride, initializer, backend, bias=True):
     return Conv2D(in_c, out_c, kernel_size=size, stride=stride, padding=size // 2, fuse_activation=False,
-                  initializer=initializer, backend=backend)
+                  initializer=initializer, backend=backend, bias=bias)
 
 
 class BasicBlock(Layer):
@@ -83,17 +89,21 @@ class BasicBlock(Layer):
 
     expansion = 1
 
-    def __init__(self, in_channels, out_channels, stride=1, name=None, initializer=None, conv_backend="auto"):
+    def __init__(self, in_channels, out_channels, stride=1, name=None, initializer=None, conv_backend="auto",
+                 compat="myflows"):
         super().__init__(name=name)
-        self.conv1 = _conv(in_channels, out_channels, 3, stride, initializer, conv_backend)
-        self.bn1 = BatchNorm2d(out_channels)
-        self.conv2 = _conv(out_channels, out_channels, 3, 1, initializer, conv_backend)
-        self.bn2 = BatchNorm2d(out_channels)
+        if compat not in COMPAT_MODES:
+            raise ValueError(f"compat must be one of {COMPAT_MODES}")
+        bias, unbiased = compat != "torchvision", compat == "torchvision"
+        self.conv1 = _conv(in_channels, out_channels, 3, stride, initializer, conv_backend, bias)
+        self.bn1 = BatchNorm2d(out_channels, unbiased_running_var=unbiased)
+        self.conv2 = _conv(out_channels, out_channels, 3, 1, initializer, conv_backend, bias)
+        self.bn2 = BatchNorm2d(out_channels, unbiased_running_var=unbiased)
         self.sub_layers = [self.conv1, self.bn1, self.conv2, self.bn2]
         self.downsample = None
         if stride != 1 or in_channels != out_channels:
-            self.downsample_conv = _conv(in_channels, out_channels, 1, stride, initializer, conv_backend)
-            self.downsample_bn = BatchNorm2d(out_channels)
+            self.downsample_conv = _conv(in_channels, out_channels, 1, stride, initializer, conv_backend, bias)
+            self.downsample_bn = BatchNorm2d(out_channels, unbiased_running_var=unbiased)
             self.downsample = (self.downsample_conv, self.downsample_bn)
             self.sub_layers += [self.downsample_conv, self.downsample_bn]
         self.params = [p for layer in self.sub_layers for p in layer.params]
@@ -107,31 +117,48 @@ class BasicBlock(Layer):
 class ResNet18(Layer):
     """Stem (7x7/2 conv + BN + ReLU + 3x3/2 max-pool for ``stem="imagenet"``, 3x3/1 conv + BN + ReLU
     for ``"cifar"``), four stages of two BasicBlocks (widths base_width x 1, 2, 4, 8; strides 1, 2,
-    2, 2), global average pooling and a Linear head."""
+    2, 2), global average pooling, dropout (when ``dropout`` > 0) and a Linear head.
+    ``compat="torchvision"`` (imagenet stem, base width 64, 3 input channels) builds torchvision's
+    structure; ``input_norm="imagenet"`` normalises [0, 1] RGB inputs by ImageNet's channel mean and
+    std in the graph (ChannelNormalize_Op)."""
 
-    def __init__(self, in_channels=3, output_dim=2, stem="imagenet", base_width=64, name=None, initializer=None,
-                 conv_backend="auto", linear_backend="auto"):
+    def __init__(self, in_channels=3, output_dim=2, stem="imagenet", base_width=64, name=None, dropout=0.0,
+                 initializer=None, conv_backend="auto", dropout_seed=None, compat="myflows", input_norm=None,
+                 linear_backend="auto"):
         super().__init__(name=name)
         if stem not in ("imagenet", "cifar"):
             raise ValueError("stem must be 'imagenet' or 'cifar'")
+        if compat not in COMPAT_MODES:
+            raise ValueError(f"compat must be one of {COMPAT_MODES}")
+        if compat == "torchvision" and (stem != "imagenet" or int(base_width) != 64 or in_channels != 3):
+            raise ValueError("compat='torchvision' requires stem='imagenet', base_width=64 and 3 input channels")
+        if input_norm not in (None, "imagenet"):
+            raise ValueError("input_norm must be None or 'imagenet'")
         self.conv_backend = _backend_name(conv_backend)
         self.linear_backend = linear_backend
         self.stem_type = stem
+        self.compat = compat
+        self.input_norm = input_norm
         self.output_dim = int(output_dim)
+        bias, unbiased = compat != "torchvision", compat == "torchvision"
         self.widths = [base_width * f for f in (1, 2, 4, 8)]
         if stem == "imagenet":
-            self.stem_conv = _conv(in_channels, self.widths[0], 7, 2, initializer, self.conv_backend)
+            self.stem_conv = _conv(in_channels, self.widths[0], 7, 2, initializer, self.conv_backend, bias)
         else:
             self.stem_conv = _conv(in_channels, self.widths[0], 3, 1, initializer, self.conv_backend)
-        self.stem_bn = BatchNorm2d(self.widths[0])
+        self.stem_bn = BatchNorm2d(self.widths[0], unbiased_running_var=unbiased)
         in_c = self.widths[0]
         stages = []
         for width, stride in zip(self.widths, (1, 2, 2, 2)):
-            stages.append([BasicBlock(in_c, width, stride, initializer=initializer, conv_backend=self.conv_backend),
-                           BasicBlock(width, width, 1, initializer=initializer, conv_backend=self.conv_backend)])
+            stages.append([BasicBlock(in_c, width, stride, initializer=initializer, conv_backend=self.conv_backend,
+                                      compat=compat),
+                           BasicBlock(width, width, 1, initializer=initializer, conv_backend=self.conv_backend,
+                                      compat=compat)])
             in_c = width
         self.layer1, self.layer2, self.layer3, self.layer4 = stages
         self.avgpool = GlobalAvgPool2d()
+        self.dropout = (Dropout(float(dropout), seed=dropout_seed, name="resnet_dropout")
+                        if float(dropout or 0.0) > 0.0 else None)
         device = torch_device()
         draw = make_initializer(initializer)
         self.fc_W = Variable(torch.as_tensor(draw((self.widths[3], self.output_dim)), dtype=torch.float32,
@@ -144,20 +171,28 @@ class ResNet18(Layer):
         for block in self.blocks():
             self.params += block.params
         self.params += [self.fc_W, self.fc_b]
+        if self.dropout is not None:
+            self.sub_layers.append(self.dropout)
 
     def blocks(self):
         return [*self.layer1, *self.layer2, *self.layer3, *self.layer4]
 
     def spatial_features(self, input_node):
+        if self.input_norm == "imagenet":
+            input_node = ChannelNormalize_Op(input_node)
         x = ReLU(self.stem_bn(self.stem_conv(input_node)))
         if self.stem_type == "imagenet":
-            x = MaxPool2d_Op(x, kernel_size=3, stride=2, backend=self.conv_backend, padding=0)
+            # torchvision's stem pool pads by 1 (56 x 56 from a 224 x 224 input); the default does not.
+            x = MaxPool2d_Op(x, kernel_size=3, stride=2, backend=self.conv_backend,
+                             padding=1 if self.compat == "torchvision" else 0)
         for block in self.blocks():
             x = block(x)
         return x
 
     def forward(self, input_node):
         features = self.avgpool(self.spatial_features(input_node))
+        if self.dropout is not None:
+            features = self.dropout(features)
         return Linear(features, self.fc_W, self.fc_b, backend=self.linear_backend)
 
     def train(self, mode=True):

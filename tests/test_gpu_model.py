@@ -492,3 +492,60 @@ def test_batched_kernel_orders_and_in_place_dx_reproduce_the_per_call_path(monke
         runs.append([host(out.value)] + [host(p.grad) for p in model.params])
     for a, b in zip(*runs):
         np.testing.assert_array_equal(a, b)
+
+
+def _torch_resnet18_tv(model, P, x, dropout_mask):
+    """torchvision's resnet18 structure in float64 on the host (torch.nn.functional), with P(variable)
+    giving each model parameter's float64 leaf: ImageNet input normalisation, bias-free
+    convolutions, training-mode batch norm, the padded stem pool, dropout by the given mask, then
+    the Linear head."""
+    import torch.nn.functional as F
+    mean = torch.tensor([0.485, 0.456, 0.406], dtype=torch.float64).reshape(1, 3, 1, 1)
+    std = torch.tensor([0.229, 0.224, 0.225], dtype=torch.float64).reshape(1, 3, 1, 1)
+
+    def conv(layer, v, stride, padding):
+        return F.conv2d(v, P(layer.kernel), stride=stride, padding=padding)
+
+    def bn(layer, v):
+        return F.batch_norm(v, None, None, P(layer.gamma), P(layer.beta), training=True, eps=layer.eps)
+
+    v = (x - mean) / std
+    v = F.relu(bn(model.stem_bn, conv(model.stem_conv, v, 2, 3)))
+    v = F.max_pool2d(v, 3, 2, padding=1)
+    for block in model.blocks():
+        stride = block.conv1.stride
+        out = F.relu(bn(block.bn1, conv(block.conv1, v, stride, 1)))
+        out = bn(block.bn2, conv(block.conv2, out, 1, 1))
+        short = v if block.downsample is None else bn(block.downsample_bn, conv(block.downsample_conv, v, stride, 0))
+        v = F.relu(out + short)
+    features = v.mean(dim=(2, 3)) * dropout_mask
+    return features @ P(model.fc_W) + P(model.fc_b)
+
+
+def test_torchvision_compat_resnet18_step_against_torch_fp64():
+    """ResNet18(compat="torchvision", input_norm="imagenet", dropout=0.5) at batch 4, 3x64x64: the
+    loss, the output and every parameter gradient of one forward + backward on the GPU against the
+    same network in float64 (torch.nn.functional on the host, the dropout mask the seed draws),
+    normwise within 1e-4 (float32 arithmetic through 18 layers)."""
+    print("torchvision-compat resnet18 step", flush=True)
+    model = mf.ResNet18(output_dim=2, compat="torchvision", input_norm="imagenet", dropout=0.5, dropout_seed=5,
+                        initializer=mf.make_initializer(seed=3), conv_backend="hip_native")
+    rng = np.random.default_rng(4)
+    x_np = rng.random((4, 3, 64, 64)).astype(np.float32)
+    t_np = rng.uniform(-1, 1, (4, 2)).astype(np.float32)
+    x = mf.Variable(gpu(x_np), requires_grad=False, name="images")
+    out = model(x)
+    loss = mf.MSELoss(out, mf.Variable(gpu(t_np), requires_grad=False))
+    graph = mf.Graph(loss, optimize=True)
+    graph.forward()
+    graph.backward()
+    mask = torch.as_tensor((np.random.default_rng(5).random((4, 512)) < 0.5).astype(np.float64) / 0.5)
+    params = list(model.params)
+    leaves = {id(p): p.value.detach().double().cpu().requires_grad_(True) for p in params}
+    ref_out = _torch_resnet18_tv(model, lambda v: leaves[id(v)], torch.as_tensor(x_np, dtype=torch.float64), mask)
+    ref_loss = ((ref_out - torch.as_tensor(t_np, dtype=torch.float64)) ** 2).mean()
+    ref_loss.backward()
+    assert normwise(host(out.value), ref_out.detach().numpy()) < 1e-4
+    assert normwise(host(loss.value), ref_loss.detach().numpy()) < 1e-4
+    for p in params:
+        assert normwise(host(p.grad), leaves[id(p)].grad.numpy()) < 1e-3, p.name
