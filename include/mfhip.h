@@ -139,6 +139,15 @@ MFH_API int mfh_conv_backward(uint64_t weight, uint64_t dy, uint64_t y, uint64_t
                               int grid_x, int activation, float alpha, int dw_engine, int dx_engine,
                               uint64_t workspace, int64_t workspace_floats, uint64_t stream);
 
+/* mfh_conv_backward with one engine for the dW and the dX products (the same argument list with
+ * `engine` in place of dw_engine, dx_engine).
+ * Replaces mf_conv_backward, native_cublas.cpp:1523-1532. */
+MFH_API int mfh_conv_backward_single(uint64_t weight, uint64_t dy, uint64_t y, uint64_t cols, uint64_t dyT,
+                                     uint64_t dw, uint64_t grad_cols, uint64_t dx, uint64_t partial, uint64_t db,
+                                     int N, int CI, int H, int W, int CO, int KH, int KW, int OH, int OW, int SH,
+                                     int SW, int PH, int PW, int grid_x, int activation, float alpha, int engine,
+                                     uint64_t workspace, int64_t workspace_floats, uint64_t stream);
+
 /* Implicit-GEMM convolution forward: y (N,CO,OH,OW) = act(conv(x, weight) + bias [+ residual]) with the im2col
  * matrix gathered from x inside the GEMM's operand loads (no cols buffer). One GEMM
  * W (CO x K) . view (K x N*OH*OW) over every image, stored straight into NCHW with the bias and

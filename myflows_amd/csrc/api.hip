@@ -513,6 +513,17 @@ MFH_API int mfh_conv_backward(std::uint64_t weight, std::uint64_t dy, std::uint6
     return launch_col2im_t(as_ptr<const float>(grad_cols), as_ptr<float>(dx), g, per_image, false, s);
 }
 
+MFH_API int mfh_conv_backward_single(std::uint64_t weight, std::uint64_t dy, std::uint64_t y, std::uint64_t cols,
+                                     std::uint64_t dyT, std::uint64_t dw, std::uint64_t grad_cols, std::uint64_t dx,
+                                     std::uint64_t partial, std::uint64_t db, int N, int CI, int H, int W, int CO,
+                                     int KH, int KW, int OH, int OW, int SH, int SW, int PH, int PW, int grid_x,
+                                     int activation, float alpha, int engine, std::uint64_t workspace,
+                                     std::int64_t workspace_floats, std::uint64_t stream) {
+    return mfh_conv_backward(weight, dy, y, cols, dyT, dw, grad_cols, dx, partial, db, N, CI, H, W, CO, KH, KW, OH,
+                             OW, SH, SW, PH, PW, grid_x, activation, alpha, engine, engine, workspace,
+                             workspace_floats, stream);
+}
+
 MFH_API int mfh_conv_forward_implicit(std::uint64_t x, std::uint64_t weight, std::uint64_t wt, int prepared,
                                       std::uint64_t bias, std::uint64_t residual, std::uint64_t y, int N, int CI, int H, int W, int CO, int KH,
                                       int KW, int OH, int OW, int SH, int SW, int PH, int PW, int activation,

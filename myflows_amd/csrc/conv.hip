@@ -477,6 +477,72 @@ __global__ __launch_bounds__(256) void pool_forward_plane_kernel(const float* __
     }
 }
 
+// 2x2 windows at stride 2 that tile the planes exactly (H = 2*OH, W = 2*OW, W a multiple of 4): each
+// input pixel lies in one window, so no plane is staged. Thread q takes output row r = q / (W/4)
+// (over all planes: input rows 2r and 2r + 1) and the output pair (2j, 2j + 1), j = q % (W/4): two
+// float4 reads of columns 4j .. 4j + 3, the two windows scanned in window_max's (kh, kw) order with
+// its comparison, so the values and indices are the staged kernels' bits.
+__device__ __forceinline__ void window_take(float v, int at, float& value, int& best) {
+    if (v > value || v != v) {
+        value = v;
+        best = at;
+    }
+}
+
+__global__ __launch_bounds__(256) void pool_forward_2x2_kernel(const float4* __restrict__ x, float2* __restrict__ y,
+                                                               int2* __restrict__ argmax, int total, FastDiv div_quads,
+                                                               int quads) {
+    const int q = blockIdx.x * 256 + threadIdx.x;
+    if (q >= total) return;
+    const int r = div_quads.div(q);
+    const int top = q + r * quads;  // float4 index of columns 4j .. 4j+3 of input row 2r
+    const float4 a = x[top], b = x[top + quads];
+    const int at = 4 * top, below = 4 * (top + quads);
+    float v0 = a.x, v1 = a.z;
+    int i0 = at, i1 = at + 2;
+    window_take(a.x, at, v0, i0);
+    window_take(a.y, at + 1, v0, i0);
+    window_take(b.x, below, v0, i0);
+    window_take(b.y, below + 1, v0, i0);
+    window_take(a.z, at + 2, v1, i1);
+    window_take(a.w, at + 3, v1, i1);
+    window_take(b.z, below + 2, v1, i1);
+    window_take(b.w, below + 3, v1, i1);
+    y[q] = make_float2(v0, v1);
+    if (argmax) argmax[q] = make_int2(i0, i1);
+}
+
+// Its backward: every input pixel takes 0 + the dy of its window when the window's argmax is that
+// pixel (the one window pool_pixel_grad would visit for it), else 0.
+__global__ __launch_bounds__(256) void pool_backward_2x2_kernel(const float2* __restrict__ dy,
+                                                                const int2* __restrict__ argmax,
+                                                                float* __restrict__ dx, int total, FastDiv div_quads,
+                                                                int quads) {
+    const int q = blockIdx.x * 256 + threadIdx.x;
+    if (q >= total) return;
+    const int r = div_quads.div(q);
+    const int top = q + r * quads;
+    const float2 g = dy[q];
+    const int2 w = argmax[q];
+    const int at = 4 * top, below = 4 * (top + quads);
+    auto pick = [](int where, int target, float grad) { return where == target ? 0.0f + grad : 0.0f; };
+    store_streaming4(dx + at, pick(w.x, at, g.x), pick(w.x, at + 1, g.x), pick(w.y, at + 2, g.y),
+                     pick(w.y, at + 3, g.y));
+    store_streaming4(dx + below, pick(w.x, below, g.x), pick(w.x, below + 1, g.x), pick(w.y, below + 2, g.y),
+                     pick(w.y, below + 3, g.y));
+}
+
+// Whether a pool takes the 2x2 kernels above: the window shape and stride, planes they tile exactly,
+// and the alignment of their vector accesses.
+bool pool_tiles_2x2(const void* x, const void* y, const void* argmax, int H, int W, int OH, int OW, int KH, int KW,
+                    int SH, int SW) {
+    const auto aligned = [](const void* p, std::uintptr_t bytes) {
+        return (reinterpret_cast<std::uintptr_t>(p) & (bytes - 1)) == 0;
+    };
+    return KH == 2 && KW == 2 && SH == 2 && SW == 2 && H == 2 * OH && W == 2 * OW && W % 4 == 0 && aligned(x, 16) &&
+           aligned(y, 8) && aligned(argmax, 8);
+}
+
 // Max-pool backward over `per` consecutive planes per workgroup: the planes' dy and argmax are
 // staged in LDS, then every input pixel gathers the windows that cover it, in (oh, ow) order.
 // div_plane and div_row divide by the units of a plane and of a row: pixels (H*W, W), or under VEC4
@@ -637,6 +703,13 @@ int pool_planes_per_block(int plane_floats, int capacity) {
 int launch_pool_forward(const float* x, float* y, int* argmax, int N, int C, int H, int W, int OH, int OW, int KH,
                         int KW, int SH, int SW, hipStream_t stream) {
     const int total = N * C * OH * OW;
+    if (pool_tiles_2x2(x, y, argmax, H, W, OH, OW, KH, KW, SH, SW)) {
+        const int quads = W / 4;
+        launch(pool_forward_2x2_kernel, blocks_for(total / 2, 256), 256, 0, stream,
+               reinterpret_cast<const float4*>(x), reinterpret_cast<float2*>(y), reinterpret_cast<int2*>(argmax),
+               total / 2, FastDiv(quads), quads);
+        return MFH_CHECK_LAUNCH("pool_forward_2x2", stream);
+    }
     const int per = pool_planes_per_block(H * W, PLANE_FLOATS);
     if (per > 0) {
         const int planes = N * C;
@@ -653,6 +726,12 @@ int launch_pool_forward(const float* x, float* y, int* argmax, int N, int C, int
 int launch_pool_backward(const float* dy, const int* argmax, float* dx, int N, int C, int H, int W, int OH, int OW,
                          int KH, int KW, int SH, int SW, hipStream_t stream) {
     const int total = N * C * H * W;
+    if (pool_tiles_2x2(dx, dy, argmax, H, W, OH, OW, KH, KW, SH, SW)) {
+        const int quads = W / 4, pairs = N * C * OH * OW / 2;
+        launch(pool_backward_2x2_kernel, blocks_for(pairs, 256), 256, 0, stream, reinterpret_cast<const float2*>(dy),
+               reinterpret_cast<const int2*>(argmax), dx, pairs, FastDiv(quads), quads);
+        return MFH_CHECK_LAUNCH("pool_backward_2x2", stream);
+    }
     const int per = std::min(pool_planes_per_block(OH * OW, PLANE_FLOATS / 2),
                              pool_planes_per_block(H * W, 1 << 30));
     if (per > 0) {

@@ -96,6 +96,7 @@ _SIGNATURES = {
     "mfh_conv_col2im": ("i", "pp" + _CONV + "iip"),
     "mfh_conv_forward": ("i", "pppppp" + _CONV + "ifipqp"),
     "mfh_conv_backward": ("i", "pppppppppp" + _CONV + "iifiipqp"),
+    "mfh_conv_backward_single": ("i", "pppppppppp" + _CONV + "iifipqp"),
     "mfh_conv_forward_implicit": ("i", "pppippp" + _CONV + "ifipqp"),
     "mfh_conv_forward_implicit_deferred": ("i", "pppipp" + _CONV + "ipqPp"),
     "mfh_conv_weight_orders": ("i", "UUPip"),

@@ -245,6 +245,49 @@ def test_im2col_and_col2im_are_bit_exact(shape, kernel, stride, padding):
         np.testing.assert_array_equal(host(out), base + expected, err_msg=f"per_image={per_image} accumulate")
 
 
+@pytest.mark.parametrize("plan", ["mfma", ("64x64", 1)])
+def test_single_engine_backward_is_the_two_engine_call(plan):
+    """mfh_conv_backward_single (the reference's mf_conv_backward) gives the bits of mfh_conv_backward
+    with its engine for both products, through a ReLU gate, with dW, db and dX requested."""
+    print("single-engine backward", plan, flush=True)
+    rng = np.random.default_rng(11)
+    n, ci, h, w_, co = 2, 16, 12, 14, 8
+    x = rng.standard_normal((n, ci, h, w_)).astype(np.float32)
+    w = rng.standard_normal((co, ci, 3, 3)).astype(np.float32)
+    dy = rng.standard_normal((n, co, h, w_)).astype(np.float32)
+    gate = rng.standard_normal((n, co, h, w_)).astype(np.float32)
+    code = native.GEMM_ENGINES["mfma"] if plan == "mfma" else native._plan_code(*plan)
+    xg, wg, dyg, gateg = gpu(x), gpu(w), gpu(dy), gpu(gate)
+    cols = native.conv2d_im2col(xg, w.shape, stride=(1, 1), padding=(1, 1))
+    m, k = n * h * w_, ci * 9
+    tiles = native._grad_tiles(n, h * w_, co, 0)
+    workspace, floats = native._workspace((code, co, k, m))
+    lib = native._library()
+
+    def run(single):
+        outs = [torch.empty((m, co), device="cuda"), torch.empty((co, k), device="cuda"),
+                torch.empty(m * k, device="cuda"), torch.empty(x.shape, device="cuda"),
+                torch.empty(n * tiles * co, dtype=torch.float64, device="cuda"), torch.empty(co, device="cuda")]
+        head = (wg.data_ptr(), dyg.data_ptr(), gateg.data_ptr(), cols.data_ptr(), *(t.data_ptr() for t in outs),
+                n, ci, h, w_, co, 3, 3, h, w_, 1, 1, 1, 1, tiles, 1, 0.0)
+        tail = (workspace.data_ptr() if workspace is not None else 0, floats, native._stream())
+        if single:
+            status = lib.mfh_conv_backward_single(*head, code, *tail)
+        else:
+            status = lib.mfh_conv_backward(*head, code, code, *tail)
+        native._raise_for(status, lib)
+        return [host(t) for t in outs[1:]]
+
+    single, pair = run(True), run(False)
+    for name, a, b in zip(("dw", "grad_cols", "dx", "partial", "db"), single, pair):
+        np.testing.assert_array_equal(a, b, err_msg=name)
+    gated = np.where(gate > 0, dy, 0.0).astype(np.float64)
+    np.testing.assert_allclose(single[4], gated.sum(axis=(0, 2, 3)), rtol=EPS32, atol=EPS32)
+    dx_ref, dw_ref = naive.conv_backward(x.astype(np.float64), w.astype(np.float64), gated, (1, 1), (1, 1))
+    assert_near(single[0].reshape(w.shape), dw_ref, 1e-5, "dw")
+    assert_near(single[2], dx_ref, 1e-5, "dx")
+
+
 def test_native_errors_name_the_reason():
     lib = native._library()
     x = torch.zeros((1, 1, 4, 4), device="cuda")

@@ -26,7 +26,11 @@ def host(t):
 @pytest.mark.parametrize("shape,kernel,stride,padding", POOL_CASES + (
     ((4, 8, 60, 80), (3, 3), (2, 2), (0, 0)), ((2, 4, 30, 40), (2, 2), (2, 2), (0, 0)),
     ((2, 3, 9, 9), (3, 3), (1, 1), (1, 1)),
-    ((3, 5, 13, 16), (3, 3), (2, 2), (0, 0))))  # two-row backward blocks: odd H, nine planes per workgroup
+    ((3, 5, 13, 16), (3, 3), (2, 2), (0, 0)),  # two-row backward blocks: odd H, nine planes per workgroup
+    # 2x2 windows that tile the planes (the direct kernels), and beside them an odd H and a W that is
+    # not a multiple of four (the staged kernels)
+    ((3, 5, 14, 24), (2, 2), (2, 2), (0, 0)), ((1, 2, 2, 4), (2, 2), (2, 2), (0, 0)),
+    ((3, 5, 13, 24), (2, 2), (2, 2), (0, 0)), ((3, 5, 14, 22), (2, 2), (2, 2), (0, 0))))
 def test_pool_bit_exact_with_ties_padding_and_overlap(shape, kernel, stride, padding):
     print("pool", shape, kernel, stride, padding, flush=True)
     rng = np.random.default_rng(7)
@@ -57,6 +61,31 @@ def test_tie_nan_and_signed_zero():
         assert np.isnan(host(native.maxpool2d_forward(gpu(z))[0])).all()
     yz, cz = native.maxpool2d_forward(gpu(np.array([[[[-0.0, 0.0], [0.0, -0.0]]]], np.float32)))
     assert host(cz.argmax).item() == 0 and np.signbit(host(yz).item())
+
+
+def test_tiling_2x2_pool_nan_signed_zero_and_without_indices():
+    """The direct 2x2 kernels (windows tiling the planes) on NaNs at every window position, signed zeros
+    and ties, a -0 gradient (0 + -0 is +0, as the staged kernels' sums give), and a pass without
+    indices: bit-exact with the native semantics."""
+    rng = np.random.default_rng(5)
+    x = rng.integers(-1, 2, size=(2, 3, 8, 16)).astype(np.float32)
+    x[0, 0, 0, :8] = [np.nan, 1, 2, np.nan, 0, 0, 3, 3]
+    x[0, 0, 1, :8] = [0, np.nan, np.nan, 5, np.nan, 1, 3, np.nan]
+    x[1, 2, 2:4, 4:8] = [[-0.0, 0.0, 0.0, -0.0], [0.0, -0.0, -0.0, -0.0]]
+    y_ref, argmax_ref = rp.maxpool2d_native_forward(x, (2, 2), (2, 2))
+    dy = rng.standard_normal(y_ref.shape).astype(np.float32)
+    dy[0, 0, 0, :2] = -0.0
+    dx_ref = rp.maxpool2d_native_backward(dy, argmax_ref, x.shape)
+    y, ctx = native.maxpool2d_forward(gpu(x))
+    np.testing.assert_array_equal(host(y), y_ref)
+    np.testing.assert_array_equal(np.signbit(host(y)), np.signbit(y_ref))
+    np.testing.assert_array_equal(host(ctx.argmax), argmax_ref)
+    dx = host(native.maxpool2d_backward(gpu(dy), ctx))
+    np.testing.assert_array_equal(dx, dx_ref)
+    np.testing.assert_array_equal(np.signbit(dx), np.signbit(dx_ref))
+    y_plain, ctx_plain = native.maxpool2d_forward(gpu(x), with_argmax=False)
+    np.testing.assert_array_equal(host(y_plain), y_ref)
+    assert ctx_plain.argmax is None
 
 
 def test_pool_rejects_bad_calls():
