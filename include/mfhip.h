@@ -60,7 +60,10 @@ MFH_API void mfh_set_debug_sync(int enabled);
 
 /* Stream order: nothing issued on `waiting` after this call starts before all the work issued so
  * far on `signalling` has finished (an event recorded on one, waited for by the other; the host
- * does not block). Both are streams of the current device; the same stream twice is a no-op.
+ * does not block). Both are streams of the current device; the same stream twice is a no-op. The
+ * event carries no system-scope fence: it orders the device's streams (the memory the signalling
+ * stream's kernels wrote is visible to the waiting stream's), not the host, which synchronises
+ * through its own stream or device synchronisation.
  * No counterpart in the reference, whose operators run on one stream: for callers that issue work
  * on a second stream, such as the dW products of a backward pass beside its dX products. */
 MFH_API int mfh_stream_wait(uint64_t waiting, uint64_t signalling);
