@@ -34,10 +34,14 @@ constexpr int MIN_CHUNK = 256;    // smallest K slice the automatic planner make
 constexpr int NAMED_BASE = 16, NAMED_SLICES = 32, NAMED_COUNT = 5;
 constexpr int EXTENDED_BASE = 1024, EXTENDED_SLICES = 128;
 constexpr int NAMED_TILE_OF[NAMED_COUNT] = {0, 1, 4, 2, 5};
+// The engine's k pairing: the two terms of an MFMA are 8 apart in sub-stages of 16 k, for every
+// tile (the 32-deep stages of the 256x256 tile included), so that every one-group tile adds an
+// output's K terms in one order.
+constexpr int GEMM_PAIR = 8;
 
 template <int BM, int BN, int BK, int WM, int WN, bool TA, bool TB, bool VA, bool VB>
 __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void gemm_mfma_kernel(GemmParams p) {
-    using S = MfmaShape<BM, BN, BK, WM, WN, TA, TB>;
+    using S = MfmaShape<BM, BN, BK, WM, WN, TA, TB, 4, 4, GEMM_PAIR>;
     __shared__ __attribute__((aligned(16))) float smem[2 * S::STAGE];
 
     int tile_m, tile_n, z;
@@ -82,7 +86,7 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void gemm_mfma_kernel(G
 // reproducible run to run (a grouped tile sums in another order than the one-group tiles).
 template <int BM, int BN, int BK, int WM, int WN, int KG, bool TA, bool TB, bool VA, bool VB>
 __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64 * KG) void gemm_grouped_kernel(GemmParams p) {
-    using S = MfmaShape<BM, BN, BK, WM, WN, TA, TB>;
+    using S = MfmaShape<BM, BN, BK, WM, WN, TA, TB, 4, 4, GEMM_PAIR>;
     constexpr int PARTIAL = S::THREADS * 16 * S::TM * S::TN;  // floats of one group's accumulators
     static_assert((KG - 1) * PARTIAL <= KG * 2 * S::STAGE, "the group sums fit in the stage buffers");
     __shared__ __attribute__((aligned(16))) float smem[KG * 2 * S::STAGE];
@@ -326,9 +330,10 @@ struct KernelTable {
         fill_row<6>(fn[6]);
         fill_row<7>(fn[7]);
         fill_row<8>(fn[8]);
+        fill_row<9>(fn[9]);
     }
 };
-static_assert(NUM_TILES == 9, "KernelTable lists every tile");
+static_assert(NUM_TILES == 10, "KernelTable lists every tile");
 
 const KernelTable& kernel_table() {
     static const KernelTable table;
@@ -347,7 +352,7 @@ struct TileCost {
     int per_cu;
 };
 constexpr TileCost COST[NUM_TILES] = {
-    {1.063, 3}, {0.95, 3}, {0.85, 4}, {0.935, 6}, {0.60, 6}, {0.60, 6}, {1.02, 2}, {1.02, 2}, {0.93, 3},
+    {1.063, 3}, {0.95, 3}, {0.85, 4}, {0.935, 6}, {0.60, 6}, {0.60, 6}, {1.02, 2}, {1.02, 2}, {0.93, 3}, {1.054, 1},
 };
 constexpr double HIDING_HALF = 0.75;  // resident waves per SIMD at which half the latency is hidden
 constexpr int SPLITS[] = {1, 2, 3, 4, 6, 8, 12, 16, 24, 32, 48, 64, 96, 128};
@@ -408,10 +413,10 @@ bool gemm_engine_valid(int engine) {
            (engine >= EXTENDED_BASE && engine < EXTENDED_BASE + NUM_TILES * EXTENDED_SLICES);
 }
 
-int gemm_plan_from_engine(int engine, int M, int N, int K, GemmPlan* plan, int batch) {
+int gemm_plan_from_engine(int engine, int M, int N, int K, GemmPlan* plan, int batch, unsigned tiles) {
     if (!gemm_engine_valid(engine)) return MFH_FAIL(ERR_ARG, "unknown GEMM engine or plan code");
     if (engine == 1) {
-        *plan = gemm_auto_plan(M, N, K, batch);
+        *plan = gemm_auto_plan(M, N, K, batch, tiles);
         return OK;
     }
     const bool named = engine < EXTENDED_BASE;
@@ -427,6 +432,12 @@ int gemm_plan_from_engine(int engine, int M, int N, int K, GemmPlan* plan, int b
 
 std::int64_t gemm_workspace_floats(const GemmPlan& plan, int M, int N) {
     return plan.slices > 1 ? static_cast<std::int64_t>(plan.slices) * M * N : 0;
+}
+
+std::int64_t gemm_auto_workspace_floats(int M, int N, int K) {
+    // Enough for the automatic plan of every layout (they may differ by the 256x256 tile).
+    return std::max(gemm_workspace_floats(gemm_auto_plan(M, N, K, 1, ALL_TILES), M, N),
+                    gemm_workspace_floats(gemm_auto_plan(M, N, K, 1, TRANSPOSED_TILES), M, N));
 }
 
 namespace {
@@ -543,8 +554,11 @@ bool takes_skinny(int engine, int batch, int N, const GemmEpilogue& e) {
 
 }  // namespace
 
-std::int64_t gemm_launch_workspace(int engine, int M, int N, int K) {
+std::int64_t gemm_launch_workspace(int engine, int M, int N, int K, int layout) {
     if (takes_skinny(engine, 1, N, GemmEpilogue{})) return 0;
+    if (engine == 1)
+        return layout < 0 ? gemm_auto_workspace_floats(M, N, K)
+                          : gemm_workspace_floats(gemm_auto_plan(M, N, K, 1, auto_tiles(layout & 2, layout & 1)), M, N);
     GemmPlan plan;
     if (gemm_plan_from_engine(engine, M, N, K, &plan) != OK) return -1;
     return gemm_workspace_floats(plan, M, N);
@@ -566,7 +580,7 @@ int gemm_launch(int engine, hipStream_t stream, const GemmOperands& o, const Gem
         return MFH_CHECK_LAUNCH("gemm_skinny", stream);
     }
     GemmPlan plan;
-    MFH_TRY(gemm_plan_from_engine(engine, M, N, K, &plan, o.batch));
+    MFH_TRY(gemm_plan_from_engine(engine, M, N, K, &plan, o.batch, auto_tiles(o.trans_a, o.trans_b)));
     if (o.batch > 1 || (plan.slices > 1 && (!workspace || workspace_floats < gemm_workspace_floats(plan, M, N))))
         plan = GemmPlan{plan.tile, 1, K};
     const bool split = plan.slices > 1;

@@ -18,10 +18,12 @@
 // A[l % 32][l / 32]) by a 2x32 slice of B (lane l supplies B[l / 32][l % 32]) and accumulates the
 // 32x32 product; lane l holds output column l % 32, rows 8 * (r / 4) + 4 * (l / 32) + r % 4 in its
 // register r. Which k a lane half (l / 32) feeds at each step is free as long as A and B agree, so
-// half h consumes k = h * BK/2 + s for s = 0 .. BK/2 - 1: a k-contiguous operand then reads four
-// consecutive k of its row with one 16-byte LDS load. Every tile uses the same BK and the same k
-// mapping, so an unsplit product adds each output's K terms in the same order whatever the tile
-// (of one K group: a K-grouped tile, gemm.hip, adds its groups' runs of stages afterwards).
+// half h consumes k = h * BK/2 + s for s = 0 .. BK/2 - 1 (or, with a pairing span below BK/2, the
+// same within each sub-stage of MfmaShape::PAIR): a k-contiguous operand then reads four
+// consecutive k of its row with one 16-byte LDS load. Every tile of one kernel family uses the same
+// k mapping (the GEMM engine: pairs 8 apart in sub-stages of 16; the implicit products: stages of
+// 32), so an unsplit product adds each output's K terms in the same order whatever the tile (of one
+// K group: a K-grouped tile, gemm.hip, adds its groups' runs of stages afterwards).
 #pragma once
 
 #include <type_traits>
@@ -38,12 +40,19 @@ constexpr int XCDS = 8;     // accelerator complex dies of an MI355X
 // PAD_A / PAD_B: floats of padding after each LDS row. k-contiguous tiles need it (the float4
 // reads of consecutive rows at one k would otherwise share banks); an mn-contiguous tile is read
 // along its rows and can go without.
-template <int BM_, int BN_, int BK_, int WM_, int WN_, bool TA_, bool TB_, int PAD_A = 4, int PAD_B = 4>
+// PAIR: the k span between the two terms of one MFMA (lane half 1 reads k + PAIR where half 0
+// reads k). With PAIR = BK / 2 (the default) half h consumes k = h * BK/2 + s of each stage; with a
+// smaller PAIR the stage is consumed as BK / (2 * PAIR) sub-stages of depth 2 * PAIR in turn, each
+// in that order, so a tile with deeper stages adds each output's terms in the same order, and to the
+// same bits, as one whose stages are 2 * PAIR deep.
+template <int BM_, int BN_, int BK_, int WM_, int WN_, bool TA_, bool TB_, int PAD_A = 4, int PAD_B = 4,
+          int PAIR_ = BK_ / 2>
 struct MfmaShape {
     static constexpr int BM = BM_, BN = BN_, BK = BK_, WM = WM_, WN = WN_;
     static constexpr bool TA = TA_, TB = TB_;
     static constexpr int WGN = BN / WN, WAVES = (BM / WM) * WGN, THREADS = WAVES * 64;
-    static constexpr int TM = WM / 32, TN = WN / 32, HALF = BK / 2;
+    static constexpr int TM = WM / 32, TN = WN / 32, HALF = BK / 2, PAIR = PAIR_;
+    static_assert(PAIR % 4 == 0 && HALF % PAIR == 0, "a stage is whole sub-stages of groups of four k");
     static constexpr int LDA_S = TA ? BM + PAD_A : BK + PAD_A;  // LDS row lengths (floats)
     static constexpr int LDB_S = TB ? BK + PAD_B : BN + PAD_B;
     static constexpr int A_SIZE = TA ? BK * LDA_S : BM * LDA_S;
@@ -249,11 +258,11 @@ __device__ __forceinline__ void zero_acc(v16f (&acc)[S::TM][S::TN]) {
 template <class S, int KK0 = 0, int KK1 = S::HALF, bool RESTART = false>
 __device__ __forceinline__ void mfma_stage(const float* As, const float* Bs, v16f (&acc)[S::TM][S::TN], int wm0,
                                            int wn0, int lane) {
-    constexpr int HALF = S::HALF, LDA_S = S::LDA_S, LDB_S = S::LDB_S;
+    constexpr int PAIR = S::PAIR, LDA_S = S::LDA_S, LDB_S = S::LDB_S;
     const int lm = lane % 32, h = lane / 32;
 #pragma unroll
     for (int kk = KK0; kk < KK1; kk += 4) {
-        const int k = h * HALF + kk;
+        const int k = kk / PAIR * 2 * PAIR + h * PAIR + kk % PAIR;
         float4 a[S::TM], b[S::TN];
 #pragma unroll
         for (int i = 0; i < S::TM; ++i) {

@@ -58,7 +58,8 @@ def test_adam_table_layout_matches_the_header(tmp_path):
 
 def test_tile_catalogue_and_plan_codes():
     catalogue = native.tile_catalog()
-    assert catalogue["128x128"][0] == 0 and all(entry[-1] == 16 for entry in catalogue.values())
+    assert catalogue["128x128"][0] == 0
+    assert all(entry[-1] == (32 if name == "256x256" else 16) for name, entry in catalogue.items())
     # The reference's code arithmetic (native.py:298-309 there): its named tiles take
     # 16 + index * 32 + slices - 1 (run here on the tile of the same role), catalogue tiles
     # 1024 + index * 128 + slices - 1.

@@ -146,8 +146,8 @@ def test_split_reduce_is_the_fp64_loop_bit_for_bit(slices):
         np.testing.assert_array_equal(got.view(np.uint32)[~nan], expected.view(np.uint32)[~nan])
 
 
-@pytest.mark.parametrize("plan", (("128x128", 5), ("64x128", 11), ("64x64", 2), ("256x64", 3), ("64x64k2", 4)),
-                         ids=str)
+@pytest.mark.parametrize("plan", (("128x128", 5), ("64x128", 11), ("64x64", 2), ("256x64", 3), ("64x64k2", 4),
+                                  ("256x256", 3)), ids=str)
 def test_split_gemm_is_the_fp64_reduction_of_its_chunks(plan):
     tile, requested = plan
     rng = np.random.default_rng(32)
@@ -239,15 +239,35 @@ def test_teaching_kernel_bias_and_argument_checks():
         native.matmul(gpu(a).double(), gpu(b))
 
 
+def test_automatic_plans_per_layout_and_their_workspace():
+    """The 256x256 tile is in the automatic plans of NN products only (4096^3 NN takes it); the
+    workspace query covers the plan of every layout, and the launch of each layout runs its plan."""
+    assert native.gemm_plan(4096, 4096, 4096) == ("256x256", 1) == native.gemm_plan(4096, 4096, 4096, layout="NN")
+    for layout in ("NT", "TN", "TT"):
+        assert native.gemm_plan(4096, 4096, 4096, layout=layout)[0] != "256x256", layout
+    lib = native._library()
+    for m, n, k in ((4096, 4096, 4096), (2048, 2048, 2048), (1024, 1024, 1024), (576, 64, 38400), (300, 700, 20000)):
+        need = lib.mfh_gemm_workspace(m, n, k)
+        for layout in LAYOUTS:
+            _, slices = native.gemm_plan(m, n, k, layout=layout)
+            assert need >= (slices * m * n if slices > 1 else 0), (m, n, k, layout)
+    rng = np.random.default_rng(12)
+    a, b = gpu(rng.standard_normal((512, 1024)).astype(np.float32)), gpu(rng.standard_normal((1024, 512)).astype(np.float32))
+    assert torch.equal(native.gemm(a, b, plan=("256x256", 1)), native.gemm(a, b, plan=("256x128", 1)))
+    with pytest.raises(ValueError):
+        native.gemm_plan(64, 64, 64, layout="XN")
+
+
 @pytest.mark.parametrize("layout", LAYOUTS)
 def test_every_unsplit_tile_adds_in_the_same_order(layout):
-    """All one-group tiles use the same stage depth and k mapping, so one-pass products are
-    bit-identical whatever the tile (and the XCD tile order)."""
+    """All one-group tiles use the same k mapping (the two terms of an MFMA 8 apart in sub-stages of
+    16 k, the 256x256 tile's 32-deep stages included), so one-pass products are bit-identical
+    whatever the tile (and the XCD tile order); K = 1000 ends inside a stage of every tile."""
     trans_a, trans_b = LAYOUTS[layout]
     rng = np.random.default_rng(6)
     a, b, _, _ = operands(rng, 300, 260, 1000, trans_a, trans_b)
     tiles = [tile for tile in native.tile_catalog() if native.tile_groups(tile) == 1]
-    assert len(tiles) == 8
+    assert len(tiles) == 9 and "256x256" in tiles
     results = [native.gemm(gpu(a), gpu(b), trans_a=trans_a, trans_b=trans_b, plan=(tile, 1)) for tile in tiles]
     for other in results[1:]:
         assert torch.equal(results[0], other)
