@@ -319,18 +319,11 @@ MFH_API int mfh_gemm_tile_groups(int index);
  * 0 meant register double buffering and 2-4 a cp.async pipeline). */
 MFH_API int mfh_gemm_tile_stages(int index);
 
-/* Automatic tile and split-K slice count for C(M,N) over K, of a product with both operands in
- * their natural orientation (NN; products with a transposed operand leave out the 256x256 tile:
- * mfh_gemm_plan_layout).
+/* Automatic tile and split-K slice count for C(M,N) over K.
  * Replaces mf_gemm_plan, native_cublas.cpp:1635-1643. */
 MFH_API int mfh_gemm_plan(int M, int N, int K, int* tile, int* slices);
 
-/* mfh_gemm_plan for the layout of mfh_gemm's trans_a / trans_b: the plan its automatic engine uses.
- * No counterpart in the reference, whose planner does not depend on the layout. */
-MFH_API int mfh_gemm_plan_layout(int M, int N, int K, int trans_a, int trans_b, int* tile, int* slices);
-
-/* Workspace floats the automatic plan uses (0 when it does not split), -1 on error: enough for the
- * plan of every layout.
+/* Workspace floats the automatic plan uses (0 when it does not split), -1 on error.
  * Replaces mf_gemm_workspace, native_cublas.cpp:1659-1666. */
 MFH_API int64_t mfh_gemm_workspace(int M, int N, int K);
 

@@ -140,7 +140,7 @@ def measure(layout, m, n, k, repeats=3, rounds=3, seed=197):
     for row in rows:
         row["median_ms"] = statistics.median(row["times_ms"])
     best = min(rows, key=lambda row: row["median_ms"])
-    auto_tile, auto_slices = native.gemm_plan(m, n, k, layout=layout)
+    auto_tile, auto_slices = native.gemm_plan(m, n, k)
     _, identity = device_identity(torch.cuda.current_device())
     return {"identity": identity, "layout": layout, "shape": [m, n, k], "candidates": rows, "selected": best,
             "automatic": {"tile": auto_tile, "slices": auto_slices}, "seconds": time.monotonic() - began}

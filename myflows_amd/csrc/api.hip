@@ -745,23 +745,13 @@ MFH_API int mfh_gemm_plan(int M, int N, int K, int* tile, int* slices) {
     return OK;
 }
 
-MFH_API int mfh_gemm_plan_layout(int M, int N, int K, int trans_a, int trans_b, int* tile, int* slices) {
-    MFH_TRY(require_ready());
-    MFH_REQUIRE(M > 0 && N > 0 && K > 0, "GEMM dimensions must be positive");
-    MFH_REQUIRE(tile && slices, "mfh_gemm_plan_layout received a null output");
-    const GemmPlan plan = gemm_auto_plan(M, N, K, 1, auto_tiles(trans_a != 0, trans_b != 0));
-    *tile = plan.tile;
-    *slices = plan.slices;
-    return OK;
-}
-
 MFH_API std::int64_t mfh_gemm_workspace(int M, int N, int K) {
     if (require_ready() != OK) return -1;
     if (M <= 0 || N <= 0 || K <= 0) {
         MFH_FAIL(ERR_ARG, "GEMM dimensions must be positive");
         return -1;
     }
-    return gemm_auto_workspace_floats(M, N, K);
+    return gemm_workspace_floats(gemm_auto_plan(M, N, K), M, N);
 }
 
 MFH_API int mfh_split_reduce(std::uint64_t partial, std::uint64_t c, int slices, int M, int N, int ldc, int reference,
@@ -815,7 +805,7 @@ MFH_API int mfh_gemm_noalloc(int engine, int trans_a, int trans_b, std::uint64_t
     MFH_TRY(require_ready());
     MFH_TRY(validate_engine(engine));
     MFH_REQUIRE(M > 0 && N > 0 && K > 0, "GEMM dimensions must be positive");
-    const std::int64_t needed = gemm_launch_workspace(engine, M, N, K, (trans_a ? 2 : 0) + (trans_b ? 1 : 0));
+    const std::int64_t needed = gemm_launch_workspace(engine, M, N, K);
     if (needed < 0) return MFH_FAIL(ERR_ARG, "unknown GEMM engine or plan code");
     if (needed > MFH_GEMM_NOALLOC_SCRATCH_FLOATS)
         return MFH_FAIL(ERR_ARG, "mfh_gemm_noalloc: this plan's split-K workspace needs " + std::to_string(needed) +

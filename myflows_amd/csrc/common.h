@@ -113,14 +113,6 @@ inline constexpr GemmTile GEMM_TILES[] = {
 };
 constexpr int GEMM_TILE_COUNT = sizeof(GEMM_TILES) / sizeof(GEMM_TILES[0]);
 constexpr unsigned ALL_TILES = (1u << GEMM_TILE_COUNT) - 1;
-// The automatic plans of products whose operands are not both in their natural orientation (NT, TN,
-// TT) leave out the 256x256 tile: on MI355X its 4096^3 NN product is 3 % faster than the 256x128
-// tile's, its NT and TN products 1-8 % slower.
-constexpr int WIDE_TILE = 9;
-constexpr unsigned TRANSPOSED_TILES = ALL_TILES & ~(1u << WIDE_TILE);
-inline constexpr unsigned auto_tiles(bool trans_a, bool trans_b) {
-    return trans_a || trans_b ? TRANSPOSED_TILES : ALL_TILES;
-}
 constexpr GemmTile gemm_tile_constexpr(int index) { return GEMM_TILES[index]; }
 int gemm_tile_count();
 const GemmTile& gemm_tile(int index);
@@ -132,11 +124,9 @@ struct GemmPlan {
 // among the tiles whose bits are set in `tiles`.
 GemmPlan gemm_auto_plan(int M, int N, int K, int batch = 1, unsigned tiles = ALL_TILES);
 // Plan from an engine code: 1 = automatic, 16 + tile * 128 + (slices - 1) = explicit.
-int gemm_plan_from_engine(int engine, int M, int N, int K, GemmPlan* plan, int batch = 1, unsigned tiles = ALL_TILES);
+int gemm_plan_from_engine(int engine, int M, int N, int K, GemmPlan* plan, int batch = 1);
 bool gemm_engine_valid(int engine);
 std::int64_t gemm_workspace_floats(const GemmPlan& plan, int M, int N);
-// Workspace floats of the automatic plan of any layout of C(M,N) over K.
-std::int64_t gemm_auto_workspace_floats(int M, int N, int K);
 
 constexpr int BIAS_NONE = 0, BIAS_COLUMN = 1, BIAS_ROW = 2;
 
@@ -221,8 +211,7 @@ int gemm_launch(int engine, hipStream_t stream, const GemmOperands& operands, co
 // Workspace floats gemm_launch uses for one problem with a plain epilogue (bias per column at
 // most) when it is given all it asks for: the plan's slices * M * N, or 0 (no split, or an output
 // of at most 8 columns under the automatic plan, which takes the one-wave-per-row kernel).
-// layout: (trans_a ? 2 : 0) + (trans_b ? 1 : 0), or -1 for enough for any layout.
-std::int64_t gemm_launch_workspace(int engine, int M, int N, int K, int layout = -1);
+std::int64_t gemm_launch_workspace(int engine, int M, int N, int K);
 int split_reduce(const float* partial, float* c, int slices, int M, int N, int ldc, bool reference,
                  hipStream_t stream);
 // The FP64 slice-order reduction of split-K partials (slices x M x N, dense) followed by the

@@ -72,7 +72,11 @@ __global__ __launch_bounds__((BM / WM) * (BN / WN) * 64) void gemm_mfma_kernel(G
 
     v16f acc[S::TM][S::TN];
     zero_acc<S>(acc);
-    mfma_k_loop<S, STAGE_PRIORITY>(smem, k_begin, k_end, fetch, store, acc, wm0, wn0, lane);
+    // The 16-deep tiles run two or more workgroups per CU and gain from a raised priority over
+    // the MFMAs; the 32-deep 256x256 tile (one workgroup per CU) from an early store of the next
+    // stage.
+    constexpr int ORDER = BK >= 32 ? STAGE_EARLY_STORE : STAGE_PRIORITY;
+    mfma_k_loop<S, ORDER>(smem, k_begin, k_end, fetch, store, acc, wm0, wn0, lane);
     store_acc<S>(p, C, acc, m0, n0, wm0, wn0, lane);
 }
 
@@ -352,7 +356,7 @@ struct TileCost {
     int per_cu;
 };
 constexpr TileCost COST[NUM_TILES] = {
-    {1.063, 3}, {0.95, 3}, {0.85, 4}, {0.935, 6}, {0.60, 6}, {0.60, 6}, {1.02, 2}, {1.02, 2}, {0.93, 3}, {1.054, 1},
+    {1.063, 3}, {0.95, 3}, {0.85, 4}, {0.935, 6}, {0.60, 6}, {0.60, 6}, {1.02, 2}, {1.02, 2}, {0.93, 3}, {1.07, 1},
 };
 constexpr double HIDING_HALF = 0.75;  // resident waves per SIMD at which half the latency is hidden
 constexpr int SPLITS[] = {1, 2, 3, 4, 6, 8, 12, 16, 24, 32, 48, 64, 96, 128};
@@ -413,10 +417,10 @@ bool gemm_engine_valid(int engine) {
            (engine >= EXTENDED_BASE && engine < EXTENDED_BASE + NUM_TILES * EXTENDED_SLICES);
 }
 
-int gemm_plan_from_engine(int engine, int M, int N, int K, GemmPlan* plan, int batch, unsigned tiles) {
+int gemm_plan_from_engine(int engine, int M, int N, int K, GemmPlan* plan, int batch) {
     if (!gemm_engine_valid(engine)) return MFH_FAIL(ERR_ARG, "unknown GEMM engine or plan code");
     if (engine == 1) {
-        *plan = gemm_auto_plan(M, N, K, batch, tiles);
+        *plan = gemm_auto_plan(M, N, K, batch);
         return OK;
     }
     const bool named = engine < EXTENDED_BASE;
@@ -434,11 +438,6 @@ std::int64_t gemm_workspace_floats(const GemmPlan& plan, int M, int N) {
     return plan.slices > 1 ? static_cast<std::int64_t>(plan.slices) * M * N : 0;
 }
 
-std::int64_t gemm_auto_workspace_floats(int M, int N, int K) {
-    // Enough for the automatic plan of every layout (they may differ by the 256x256 tile).
-    return std::max(gemm_workspace_floats(gemm_auto_plan(M, N, K, 1, ALL_TILES), M, N),
-                    gemm_workspace_floats(gemm_auto_plan(M, N, K, 1, TRANSPOSED_TILES), M, N));
-}
 
 namespace {
 
@@ -554,11 +553,8 @@ bool takes_skinny(int engine, int batch, int N, const GemmEpilogue& e) {
 
 }  // namespace
 
-std::int64_t gemm_launch_workspace(int engine, int M, int N, int K, int layout) {
+std::int64_t gemm_launch_workspace(int engine, int M, int N, int K) {
     if (takes_skinny(engine, 1, N, GemmEpilogue{})) return 0;
-    if (engine == 1)
-        return layout < 0 ? gemm_auto_workspace_floats(M, N, K)
-                          : gemm_workspace_floats(gemm_auto_plan(M, N, K, 1, auto_tiles(layout & 2, layout & 1)), M, N);
     GemmPlan plan;
     if (gemm_plan_from_engine(engine, M, N, K, &plan) != OK) return -1;
     return gemm_workspace_floats(plan, M, N);
@@ -580,7 +576,7 @@ int gemm_launch(int engine, hipStream_t stream, const GemmOperands& o, const Gem
         return MFH_CHECK_LAUNCH("gemm_skinny", stream);
     }
     GemmPlan plan;
-    MFH_TRY(gemm_plan_from_engine(engine, M, N, K, &plan, o.batch, auto_tiles(o.trans_a, o.trans_b)));
+    MFH_TRY(gemm_plan_from_engine(engine, M, N, K, &plan, o.batch));
     if (o.batch > 1 || (plan.slices > 1 && (!workspace || workspace_floats < gemm_workspace_floats(plan, M, N))))
         plan = GemmPlan{plan.tile, 1, K};
     const bool split = plan.slices > 1;

@@ -302,8 +302,11 @@ __device__ __forceinline__ void mfma_stage(const float* As, const float* Bs, v16
 //                   its MFMAs to the barrier, so that waves in their MFMA phase issue first while
 //                   the others store and wait: 4 % on the dense 256x128 GEMM;
 //   STAGE_MID_STORE the LDS store of the next stage between the first and the second half of the
-//                   stage's MFMAs: 3-5 % on the dW products, whose stores carry gathered operands.
-enum StageOrder : int { STAGE_PLAIN = 0, STAGE_PRIORITY = 1, STAGE_MID_STORE = 2 };
+//                   stage's MFMAs: 3-5 % on the dW products, whose stores carry gathered operands;
+//   STAGE_EARLY_STORE the store after the first quarter of the stage's MFMAs (stages of at least
+//                   32 k, one-ahead loop only): 3 % on the 256x256 GEMM tile (one workgroup per CU,
+//                   where a raised priority only delays the other waves' stores).
+enum StageOrder : int { STAGE_PLAIN = 0, STAGE_PRIORITY = 1, STAGE_MID_STORE = 2, STAGE_EARLY_STORE = 3 };
 
 // What a K loop does with the accumulators after each stage's MFMAs: nothing (the FP32 chain runs
 // on over the whole K range), or StageSums below (restarts = whether each stage starts its
@@ -372,8 +375,8 @@ __device__ __forceinline__ void mfma_k_loop(float* smem, int k_begin, int k_end,
         const float* As = smem + (t & 1) * S::STAGE;
         float* next = smem + ((t + 1) & 1) * S::STAGE;
         constexpr bool RESTART = std::decay_t<Drain>::restarts;
-        if constexpr (ORDER == STAGE_MID_STORE && S::HALF >= 8) {
-            constexpr int MID = S::HALF / 8 * 4;
+        if constexpr ((ORDER == STAGE_MID_STORE && S::HALF >= 8) || (ORDER == STAGE_EARLY_STORE && S::HALF >= 16)) {
+            constexpr int MID = ORDER == STAGE_EARLY_STORE ? S::HALF / 16 * 4 : S::HALF / 8 * 4;
             mfma_stage<S, 0, MID, RESTART>(As, As + S::A_SIZE, acc, wm0, wn0, lane);
             if (more) store(next, next + S::A_SIZE);
             mfma_stage<S, MID, S::HALF>(As, As + S::A_SIZE, acc, wm0, wn0, lane);

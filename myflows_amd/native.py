@@ -112,7 +112,6 @@ _SIGNATURES = {
     "mfh_gemm_tile_stages": ("i", "i"),
     "mfh_gemm_tile_groups": ("i", "i"),
     "mfh_gemm_plan": ("i", "iiiPP"),
-    "mfh_gemm_plan_layout": ("i", "iiiiiPP"),
     "mfh_gemm_workspace": ("q", "iii"),
     "mfh_split_reduce": ("i", "pp" + "iiiii" + "p"),
     "mfh_gemm": ("i", "iiipppp" + "iiiiii" + "pqp"),
@@ -1048,8 +1047,7 @@ def matmul(a, b, bias=None, *, variant="shared", tile=32, accumulate="kahan", ou
 
 
 def gemm_plan(m, n, k, *, layout=None):
-    """(tile name, split-K slices) the MFMA engine picks for an m x n output over k: of an NN product,
-    or of `layout` ("NN", "NT", "TN", "TT"; the transposed ones leave out the 256x256 tile)."""
+    """(tile name, split-K slices) the MFMA engine picks for an m x n output over k."""
     if min(m, n, k) <= 0:
         raise ValueError("gemm dimensions must be positive")
     if layout is not None and os.environ.get("MFHIP_GEMM_AUTOTUNE") == "1":
@@ -1057,13 +1055,7 @@ def gemm_plan(m, n, k, *, layout=None):
         tile, requested = selected_plan(layout, m, n, k)
         return tile, _slices(k, requested, tile_catalog()[tile][-1])
     tile, slices = ctypes.c_int(), ctypes.c_int()
-    if layout is None:
-        _call("mfh_gemm_plan", m, n, k, ctypes.byref(tile), ctypes.byref(slices))
-    else:
-        if layout not in ("NN", "NT", "TN", "TT"):
-            raise ValueError(f"unknown layout {layout!r}")
-        _call("mfh_gemm_plan_layout", m, n, k, int(layout[0] == "T"), int(layout[1] == "T"), ctypes.byref(tile),
-              ctypes.byref(slices))
+    _call("mfh_gemm_plan", m, n, k, ctypes.byref(tile), ctypes.byref(slices))
     return list(tile_catalog())[tile.value], slices.value
 
 

@@ -239,23 +239,16 @@ def test_teaching_kernel_bias_and_argument_checks():
         native.matmul(gpu(a).double(), gpu(b))
 
 
-def test_automatic_plans_per_layout_and_their_workspace():
-    """The 256x256 tile is in the automatic plans of NN products only (4096^3 NN takes it); the
-    workspace query covers the plan of every layout, and the launch of each layout runs its plan."""
-    assert native.gemm_plan(4096, 4096, 4096) == ("256x256", 1) == native.gemm_plan(4096, 4096, 4096, layout="NN")
-    for layout in ("NT", "TN", "TT"):
-        assert native.gemm_plan(4096, 4096, 4096, layout=layout)[0] != "256x256", layout
-    lib = native._library()
-    for m, n, k in ((4096, 4096, 4096), (2048, 2048, 2048), (1024, 1024, 1024), (576, 64, 38400), (300, 700, 20000)):
-        need = lib.mfh_gemm_workspace(m, n, k)
-        for layout in LAYOUTS:
-            _, slices = native.gemm_plan(m, n, k, layout=layout)
-            assert need >= (slices * m * n if slices > 1 else 0), (m, n, k, layout)
+def test_large_products_take_the_256x256_tile():
+    """The automatic plan of a 4096^3 product is the 256x256 tile (one workgroup per CU), whose
+    32-deep stages give the 16-deep tiles' bits in every layout."""
+    assert native.gemm_plan(4096, 4096, 4096) == ("256x256", 1)
     rng = np.random.default_rng(12)
-    a, b = gpu(rng.standard_normal((512, 1024)).astype(np.float32)), gpu(rng.standard_normal((1024, 512)).astype(np.float32))
-    assert torch.equal(native.gemm(a, b, plan=("256x256", 1)), native.gemm(a, b, plan=("256x128", 1)))
-    with pytest.raises(ValueError):
-        native.gemm_plan(64, 64, 64, layout="XN")
+    for layout, (trans_a, trans_b) in LAYOUTS.items():
+        a, b, _, _ = operands(rng, 520, 300, 1000, trans_a, trans_b)
+        a, b = gpu(a), gpu(b)
+        wide = native.gemm(a, b, trans_a=trans_a, trans_b=trans_b, plan=("256x256", 1))
+        assert torch.equal(wide, native.gemm(a, b, trans_a=trans_a, trans_b=trans_b, plan=("256x128", 1))), layout
 
 
 @pytest.mark.parametrize("layout", LAYOUTS)
