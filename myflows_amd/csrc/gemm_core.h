@@ -304,8 +304,9 @@ __device__ __forceinline__ void mfma_stage(const float* As, const float* Bs, v16
 //   STAGE_MID_STORE the LDS store of the next stage between the first and the second half of the
 //                   stage's MFMAs: 3-5 % on the dW products, whose stores carry gathered operands;
 //   STAGE_EARLY_STORE the store after the first quarter of the stage's MFMAs (stages of at least
-//                   32 k, one-ahead loop only): 3 % on the 256x256 GEMM tile (one workgroup per CU,
-//                   where a raised priority only delays the other waves' stores).
+//                   32 k): 3 % on the 256x256 GEMM tile (one workgroup per CU, where a raised
+//                   priority only delays the other waves' stores) and 1 % on the batch-64 training
+//                   step through the forward / dX products, whose reads run two stages ahead.
 enum StageOrder : int { STAGE_PLAIN = 0, STAGE_PRIORITY = 1, STAGE_MID_STORE = 2, STAGE_EARLY_STORE = 3 };
 
 // What a K loop does with the accumulators after each stage's MFMAs: nothing (the FP32 chain runs
@@ -396,7 +397,7 @@ __device__ __forceinline__ void mfma_k_loop(float* smem, int k_begin, int k_end,
 // before they are stored to LDS (at the end of stage t + 1) instead of one. fetch(slot, kt) and
 // store(slot, a_lds, b_lds) take the slot as std::integral_constant<int, 0 or 1>: stage t uses slot
 // t % 2 and LDS buffer t % 2. The MFMAs, their operands and their order are mfma_k_loop's (with
-// ORDER STAGE_PLAIN or STAGE_MID_STORE), so the results are its bits. fetch is issued for every stage, also for the two past
+// ORDER STAGE_PLAIN, STAGE_MID_STORE or STAGE_EARLY_STORE), so the results are its bits. fetch is issued for every stage, also for the two past
 // the end (kt >= k_end), and store for every stage, also for the one past the end (into the LDS
 // buffer that no MFMA reads any more: every wave has passed the barrier after its last read), so
 // that the compiler sees the same loads in flight on every path and waits for exactly one stage's
@@ -427,8 +428,8 @@ __device__ __forceinline__ void mfma_k_loop_ahead(float* smem, int k_begin, int 
         if (t > 0) drain(acc);
         const float* As = smem + T * S::STAGE;
         float* next = smem + (1 - T) * S::STAGE;
-        if constexpr (ORDER == STAGE_MID_STORE && S::HALF >= 8) {
-            constexpr int MID = S::HALF / 8 * 4;
+        if constexpr ((ORDER == STAGE_MID_STORE && S::HALF >= 8) || (ORDER == STAGE_EARLY_STORE && S::HALF >= 16)) {
+            constexpr int MID = ORDER == STAGE_EARLY_STORE ? S::HALF / 16 * 4 : S::HALF / 8 * 4;
             mfma_stage<S, 0, MID, RESTART>(As, As + S::A_SIZE, acc, wm0, wn0, lane);
             store(Other{}, next, next + S::A_SIZE);
             mfma_stage<S, MID, S::HALF>(As, As + S::A_SIZE, acc, wm0, wn0, lane);

@@ -391,7 +391,9 @@ __device__ __forceinline__ void implicit_forward_tile(const GemmParams& p, const
             la[decltype(slot)::value].template store<S::LDA_S>(a_lds, tid);
             lb[decltype(slot)::value].template store<S::LDB_S>(b_lds, tid);
         };
-        mfma_k_loop_ahead<S>(smem, k_begin, k_end, fetch, store, acc, wm0, wn0, lane, sums);
+        // The next stage's operands are in registers when a stage starts (read two stages ahead),
+        // so they go to LDS after the first quarter of the stage's MFMAs.
+        mfma_k_loop_ahead<S, STAGE_EARLY_STORE>(smem, k_begin, k_end, fetch, store, acc, wm0, wn0, lane, sums);
     } else {
         auto fetch = [&](int kt) {
             la[0].load(p.A, p.lda, m0, p.M, kt, k_end, tid);
