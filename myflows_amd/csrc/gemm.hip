@@ -193,6 +193,7 @@ __device__ __forceinline__ void finish_row(const GemmParams& p, long long t) {
 // still run one at a time in slice order.
 __global__ __launch_bounds__(256) void split_reduce_kernel(const float* __restrict__ partial, float* __restrict__ C,
                                                            GemmParams p, int slices) {
+    raise_wave_priority();
     const long long i = blockIdx.x * 256LL + threadIdx.x, total = static_cast<long long>(p.M) * p.N;
     if (p.row_out) finish_row(p, i);
     if (i >= total) return;
@@ -213,6 +214,7 @@ __global__ __launch_bounds__(256) void split_reduce_kernel(const float* __restri
 // slice-order FP64 sums as split_reduce_kernel.
 __global__ __launch_bounds__(256) void split_reduce_vec4_kernel(const float* __restrict__ partial,
                                                                 float* __restrict__ C, GemmParams p, int slices) {
+    raise_wave_priority();
     const long long q = blockIdx.x * 256LL + threadIdx.x, total = static_cast<long long>(p.M) * p.N;
     if (p.row_out) finish_row(p, q);
     if (q * 4 >= total) return;

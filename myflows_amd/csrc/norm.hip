@@ -214,6 +214,7 @@ __device__ __forceinline__ void channel_partial(const PartialArgs& p, int c, int
 
 template <int MODE, int T, bool QUAD>
 __global__ __launch_bounds__(T) void norm_partials_kernel(PartialArgs p) {
+    raise_wave_priority();
     const int s = blockIdx.x, c = blockIdx.y, slices = gridDim.x;
     double sa, sb;
     channel_partial<MODE, T, QUAD>(p, c, s, sa, sb);
@@ -345,6 +346,7 @@ __device__ __forceinline__ float apply_value(const ApplyArgs& p, float x, float 
 template <int VEC>
 __global__ __launch_bounds__(APPLY_THREADS) void norm_apply_kernel(ApplyArgs p) {
 #pragma clang fp contract(off)
+    raise_wave_priority();
     __shared__ float coef[5][MAX_PLANES];
     const int e0 = blockIdx.x * APPLY_SPAN;
     int p0, p1;
@@ -450,6 +452,7 @@ __device__ __forceinline__ float dx_value(const DxArgs& p, float x, float dy, fl
 template <int VEC>
 __global__ __launch_bounds__(APPLY_THREADS) void norm_dx_kernel(DxArgs p) {
 #pragma clang fp contract(off)
+    raise_wave_priority();
     __shared__ float coef[5][MAX_PLANES];
     const int e0 = blockIdx.x * APPLY_SPAN;
     int p0, p1;
@@ -588,6 +591,7 @@ __device__ __forceinline__ void split_group(const SplitSource& src, int c, long 
 // SPLIT: x is formed from src first (and stored), then normalised as below, in one launch.
 template <int T, bool QUAD, bool SPLIT = false>
 __global__ __launch_bounds__(T) void norm_forward_channel_kernel(PartialArgs pa, ApplyArgs p, SplitSource src) {
+    raise_wave_priority();
     using S = ChannelSlots<T, QUAD>;
     constexpr int G = S::GROUPS, W = S::WIDTH;
     __shared__ float coef[3];
@@ -664,6 +668,7 @@ __global__ __launch_bounds__(T) void norm_forward_channel_kernel(PartialArgs pa,
 // is) and stored, then used as below, in one launch.
 template <int T, bool QUAD, bool SPLIT = false>
 __global__ __launch_bounds__(T) void norm_backward_channel_kernel(PartialArgs pa, DxArgs p, SplitSource src) {
+    raise_wave_priority();
     using S = ChannelSlots<T, QUAD>;
     constexpr int G = S::GROUPS, W = S::WIDTH;
     __shared__ float coef[3];
@@ -781,6 +786,7 @@ __device__ __forceinline__ void stage_pool_grads(const PoolGrad& g, int C, int c
 __global__ __launch_bounds__(APPLY_THREADS) void norm_apply_pool_kernel(ApplyArgs p, PoolShape q, float* __restrict__ pooled,
                                                                       int* __restrict__ argmax, int vec) {
 #pragma clang fp contract(off)
+    raise_wave_priority();
     extern __shared__ float plane_y[];  // H * W floats
     __shared__ float coef[3];
     const int pl = blockIdx.x;
@@ -860,6 +866,7 @@ __device__ __forceinline__ void pooled_quad(const float* grad, const int* where,
 // norm_partials<GRADS> (quads when QUAD).
 template <int T, bool QUAD>
 __global__ __launch_bounds__(T) void norm_partials_pool_kernel(PartialArgs p, PoolShape q, PoolGrad pg, int rows) {
+    raise_wave_priority();
     extern __shared__ float staged[];
     const int s = blockIdx.x, c = blockIdx.y, slices = gridDim.x;
     const int j0 = s * p.chunk, j1 = min(p.total, j0 + p.chunk);
@@ -934,6 +941,7 @@ __global__ __launch_bounds__(T) void norm_partials_pool_kernel(PartialArgs p, Po
 // Backward dx: one workgroup per plane pl = n * C + c, as norm_dx with the pooled gradient staged.
 __global__ __launch_bounds__(APPLY_THREADS) void norm_dx_pool_kernel(DxArgs p, PoolShape q, PoolGrad pg, int vec) {
 #pragma clang fp contract(off)
+    raise_wave_priority();
     extern __shared__ float staged[];
     __shared__ float coef[3];
     const int pl = blockIdx.x;
